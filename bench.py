@@ -1,0 +1,228 @@
+#!/usr/bin/env python3
+"""TESSA leaf-operator benchmark on one MI355X.
+
+Workload (C2): 4,096 leaves x 1,024 points x 768-d SQ8 codes quantized from a
+256-component unit-normalised Gaussian mixture (sigma 0.3, seed 1), all-pairs
+int8 dot products with int32 accumulation and per-row top-32 with the
+reference's tie rule; output (id, dist) candidate records.  A "step" is one
+pass of the leaf operator over all 4,096 leaves with inputs resident in HBM.
+
+Prints one JSON line.  `value` is the whole-job int8 throughput in TOPS over
+the K timed steps (algorithmic ops = 2*768*sum n(n-1)); `roofline.achieved`
+uses the average duration of the operator's launch measured with HIP events
+on the stream it runs on.  `cpu_baseline` times the CPU oracle (the repo's C
+restatement of the reference CPU semantics, OpenMP) on a bounded sample of
+the same leaves, and the same sample is checked bit for bit against the GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+LEAVES = 4096
+LEAF_ROWS = 1024
+DIM = 768
+K = 32
+COMPONENTS = 256
+SIGMA = 0.3
+SEED = 1
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--leaves", type=int, default=LEAVES)
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0,
+                    help="approximate seconds of CPU oracle work for cpu_baseline")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-json", default=None,
+                    help="profiles/*.json with measured HBM bytes per launch (rocprofv3 --pmc)")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (the TESSA operator has no multi-GPU path in this "
+              f"build; see DESIGN.md for how it would shard); got --gpus {args.gpus}, WORLD_SIZE {world}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from shear_amd import _native as N
+    from shear_amd import datagen
+    from shear_amd import tessa as T
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    N.load()
+    leaves = args.leaves
+    rows = leaves * LEAF_ROWS
+
+    t0 = time.time()
+    x = datagen.gmm_torch(rows, DIM, COMPONENTS, SIGMA, SEED, device=dev)
+    sq8 = T.quantize_sq_int8_matrix(x)
+    del x
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    log(f"generated + quantized {rows}x{DIM} in {time.time() - t0:.1f}s")
+
+    gids = torch.arange(rows, dtype=torch.int32, device=dev)
+    lay = T.LeafLayouts.contiguous(leaves, LEAF_ROWS, K, device=dev)
+    out_ids = torch.empty(lay.output_len, dtype=torch.int32, device=dev)
+    out_d = torch.empty(lay.output_len, dtype=torch.float32, device=dev)
+    ctr = torch.zeros(N.COUNTER_WORDS, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        T.leaf_topk(sq8, gids, lay, K, executor=N.EXEC_MFMA, out_ids=out_ids, out_dists=out_d, counters=ctr,
+                    stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    T.raise_on_overflow(ctr, "leaf top-k")
+    log(f"warmup {args.warmup} done")
+
+    ctr.zero_()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        step()
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    launch_ms = [a.elapsed_time(b) for a, b in evs]
+    T.raise_on_overflow(ctr, "leaf top-k")
+    c = ctr.cpu().numpy()
+    log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, launch median {np.median(launch_ms):.3f} ms")
+
+    pairs = leaves * LEAF_ROWS * (LEAF_ROWS - 1)
+    ops = 2.0 * DIM * pairs
+    value_tops = ops * args.steps / wall / 1e12
+    avg_launch_s = float(np.mean(launch_ms)) / 1e3
+    achieved = ops / avg_launch_s / 1e12
+    records_bytes = rows * K * 8
+    algo_bytes = rows * (DIM + 8) + records_bytes  # codes + scale/norm + (id, dist) records
+
+    traffic = None
+    if args.traffic_json and os.path.exists(args.traffic_json):
+        with open(args.traffic_json) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": "TESSA leaf int8 TOPS (% MFMA peak)",
+        "value": round(value_tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C2 TESSA leaf microbench: {leaves} leaves x {LEAF_ROWS} pts x {DIM}-d SQ8, k={K}, "
+                        f"{COMPONENTS}-comp GMM sigma={SIGMA} unit-norm, seed {SEED}",
+            "leaves": leaves, "leaf_rows": LEAF_ROWS, "padded_dim": DIM, "k": K,
+            "executor": "mfma (v_mfma_i32_32x32x32_i8)",
+        },
+        "pct_int8_mfma_peak": round(100.0 * value_tops / INT8_PEAK_TOPS, 2),
+        "pair_distances_per_s": pairs * args.steps / wall,
+        "records_gb_per_s": records_bytes * args.steps / wall / 1e9,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / INT8_PEAK_TOPS, 4),
+            "traffic": traffic,
+            "ops_per_launch": ops,
+            "algorithmic_hbm_bytes_per_launch": algo_bytes,
+            "launch_ms_median": round(float(np.median(launch_ms)), 4),
+            "launch_ms_min": round(float(np.min(launch_ms)), 4),
+            "launch_ms_max": round(float(np.max(launch_ms)), 4),
+        },
+        "counters": {
+            "rows_per_step": int(c[N.C_LEAF_ROWS]) // args.steps,
+            "exact_reruns_per_step": int(c[N.C_LEAF_FALLBACK_ROWS]) // args.steps,
+            "survivors_per_row": float(c[N.C_LEAF_SURVIVORS]) / max(1, int(c[N.C_LEAF_ROWS])),
+            "final_candidates_per_row": float(c[N.C_LEAF_FINAL_CANDIDATES]) / max(1, int(c[N.C_LEAF_ROWS])),
+            "refines_per_wave": float(c[N.C_LEAF_REFINES]) / max(1, int(c[N.C_LEAF_ROWS]) // 32),
+        },
+        "cpu_baseline": None,
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(sq8, out_ids, out_d, budget_s):
+    """Times the CPU oracle on a bounded leaf sample and checks the GPU output on it."""
+    from oracle import pyoracle as orc
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+
+    def run(first, count):
+        r0, r1 = first * LEAF_ROWS, (first + count) * LEAF_ROWS
+        codes = sq8.codes[r0:r1].cpu().numpy()
+        scales = sq8.scales[r0:r1].cpu().numpy()
+        norms = sq8.norms[r0:r1].cpu().numpy()
+        gids = np.arange(r0, r1, dtype=np.uint32)
+        members = np.arange(r1 - r0, dtype=np.uint32)
+        t = time.perf_counter()
+        ids, d = orc.leaf_topk(codes, scales, norms, gids, members, np.arange(count) * LEAF_ROWS,
+                               [LEAF_ROWS] * count, K, threads=threads)
+        return time.perf_counter() - t, ids, d
+
+    t1, _, _ = run(0, threads)  # calibration: one leaf per thread
+    count = threads * max(1, int(budget_s / max(t1, 1e-3)))
+    count = min(count, sq8.rows // LEAF_ROWS)
+    first = 0
+    secs, ids, d = run(first, count)
+    ops = 2.0 * DIM * count * LEAF_ROWS * (LEAF_ROWS - 1)
+    lo, hi = first * LEAF_ROWS * K, (first + count) * LEAF_ROWS * K
+    gpu_ids = out_ids[lo:hi].cpu().numpy().view(np.uint32)
+    gpu_d = out_d[lo:hi].cpu().numpy()
+    mism = int(np.count_nonzero((gpu_ids != ids) | (gpu_d.view(np.uint32) != d.view(np.uint32))))
+    log(f"cpu oracle: {count} leaves in {secs:.2f}s on {threads} threads; GPU mismatches {mism}")
+    base = {
+        "value": round(ops / secs / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{count} of {sq8.rows // LEAF_ROWS} leaves (1024 x 768, k=32), {secs:.1f}s, "
+                  f"dot kernel {['scalar', 'avx2', 'avx512-vnni'][orc.dot_kernel()]}",
+        "leaves_per_s": count / secs,
+    }
+    parity = {"leaves": count, "slots": int(hi - lo), "mismatched_slots": mism, "bit_exact": mism == 0}
+    return base, parity
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,231 @@
+/*
+ * tessa_hip.h -- C ABI of the MI355X (gfx950) TESSA construction operator.
+ *
+ * This is the drop-in boundary for SHEAR's CUDA operator path.  It is plain C:
+ * integers, floats and pointers; device pointers are `void*`/typed pointers
+ * into HIP device memory and `stream` is a hipStream_t passed as `void*`.
+ * Nothing here panics or throws across the boundary: every entry point returns
+ * a tessa_status whose `code` is 0 on success.
+ *
+ * Reference interfaces each entry point replaces (paths relative to
+ * shear-core/src/algorithm/pipnn/ in SHEAR):
+ *   tessa_query_caps             compute_backend.rs:3696-3702 validate_gpu_subtree_hardware
+ *                                / gpu_hardware_adaptation_profile
+ *   tessa_session_create/destroy compute_backend.rs:34648 TessaCudaReplaySession::new,
+ *                                :31510 CudaComputeBackend::new
+ *   tessa_session_upload_sq8     compute_backend.rs:26844 upload_quantized_resident_subtree
+ *                                (H2D of GpuSubtreeQuantizedInput :1871-1883)
+ *   tessa_leaf_topk              compute_backend.rs:16146-16334 gpu_persistent_subtree_topk_only
+ *                                (launched by TessaCudaReplaySession::run_mode :34841,
+ *                                layouts tessa_replay.rs:1021-1057)
+ *   tessa_assign_replay          compute_backend.rs:15729-15943 gpu_tessa_assignment_replay
+ *   tessa_sq8_quantize           dco_sq_int8.rs:1331-1467 quantize_sq_int8_matrix (its GPU
+ *                                twin compute_backend.rs:17955-18014 tree-reduces the norm;
+ *                                this one keeps the CPU's sequential sum, so bits match)
+ *   tessa_session_leaf_topk /    TessaCudaReplaySession::run_mode leaf / assignment legs
+ *   tessa_session_assign_replay  (tessa_replay.rs:190-200 TessaCudaModeResult)
+ *   tessa_overflow_labels        compute_backend.rs:2249-2296 gpu_persistent_overflow_labels
+ */
+#ifndef TESSA_HIP_H
+#define TESSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TESSA_ABI_VERSION 1u
+
+/* ---- status ----------------------------------------------------------- */
+enum tessa_code {
+    TESSA_OK = 0,
+    TESSA_ERR_INVALID_ARGUMENT = 1,
+    TESSA_ERR_HIP = 2,              /* a HIP runtime call failed */
+    TESSA_ERR_OVERFLOW = 3,         /* device set overflow_flags (see bits) */
+    TESSA_ERR_UNSUPPORTED = 4,      /* shape outside the kernels' limits */
+    TESSA_ERR_OUT_OF_MEMORY = 5,
+    TESSA_ERR_NO_DEVICE = 6
+};
+
+typedef struct tessa_status {
+    int32_t code;
+    uint32_t reserved;
+    uint64_t overflow_flags;  /* same bit meanings as the reference word */
+    char msg[512];            /* "overflow_flags=0x.. overflow_labels=..." tokens kept */
+} tessa_status;
+
+/* Overflow bits: identical to compute_backend.rs:4843-4860 / host :252-272. */
+#define TESSA_OVF_QUEUE_NODE               (1ull << 0)
+#define TESSA_OVF_QUEUE_ROW                (1ull << 1)
+#define TESSA_OVF_LEAF_DESC                (1ull << 2)
+#define TESSA_OVF_LEAF_ROW                 (1ull << 3)
+#define TESSA_OVF_LEADER                   (1ull << 4)
+#define TESSA_OVF_FANOUT_OVER_32           (1ull << 5)
+#define TESSA_OVF_NO_PROGRESS_SPLIT        (1ull << 7)
+#define TESSA_OVF_WORKSPACE_BUDGET         (1ull << 8)
+#define TESSA_OVF_OVERSIZED_TERMINAL_NODE  (1ull << 10)
+#define TESSA_OVF_WATCHDOG_STALLED         (1ull << 11)
+#define TESSA_OVF_ACTIVE_WORK_BUDGET       (1ull << 12)
+#define TESSA_OVF_INVALID_TOPK_ROW_ID      (1ull << 13)
+#define TESSA_OVF_INVALID_TOPK_COL_ID      (1ull << 14)
+#define TESSA_OVF_INVALID_ASSIGN_POINT_ID  (1ull << 15)
+#define TESSA_OVF_INVALID_ASSIGN_LEADER_ID (1ull << 16)
+#define TESSA_OVF_UNSUPPORTED_EXPLICIT_KERNEL (1ull << 18)
+
+/* ---- counters (u64 words, device-resident, accumulated by kernels) ----- */
+#define TESSA_COUNTER_WORDS 32
+enum tessa_counter {
+    TESSA_C_OVERFLOW_FLAGS = 0,
+    TESSA_C_LEAF_ROWS = 1,             /* rows whose top-k was written */
+    TESSA_C_LEAF_MFMA_TILES = 2,       /* 32x32 candidate tiles on the MFMA path */
+    TESSA_C_LEAF_EXACT_ROWS = 3,       /* rows evaluated by the exact scalar kernel */
+    TESSA_C_LEAF_FALLBACK_ROWS = 4,    /* MFMA rows re-run exactly (list overflow / gap) */
+    TESSA_C_LEAF_LIST_OVERFLOW_ROWS = 5,
+    TESSA_C_LEAF_GAP_FALLBACK_ROWS = 6,
+    TESSA_C_LEAF_REFINES = 7,          /* threshold refinements (wave-level) */
+    TESSA_C_LEAF_SURVIVORS = 8,        /* candidates that passed the running threshold */
+    TESSA_C_LEAF_FINAL_CANDIDATES = 9, /* entries fed to the final ordered insertion */
+    TESSA_C_ASSIGN_ROWS = 10,
+    TESSA_C_ASSIGN_PAIRS = 11,
+    TESSA_C_ASSIGN_TIE_EVENTS = 12     /* insertions decided by the eps tie key */
+};
+
+/* ---- executors (mirrors tessa_replay.rs:20-86 leaf_executor_code) ------ */
+#define TESSA_EXEC_EXACT 1u  /* scalar integer-dot kernel, reference "DP4A" role */
+#define TESSA_EXEC_MFMA  2u  /* int8 MFMA 32x32x32 kernel, reference "WMMA" role */
+
+/* ---- device capabilities ---------------------------------------------- */
+typedef struct tessa_caps {
+    int32_t device;
+    int32_t compute_units;
+    int32_t max_threads_per_block;
+    int32_t lds_bytes_per_block;
+    uint64_t hbm_bytes;
+    char arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int32_t supported;      /* 1 when the arch is gfx950 */
+    int32_t max_leaf_rows;  /* MFMA leaf path limit */
+    int32_t max_k;          /* 32 */
+    int32_t max_padded_dim; /* 1024 */
+} tessa_caps;
+
+tessa_status tessa_query_caps(int32_t device, tessa_caps *out);
+
+/* ---- SQ8 input (GpuSubtreeQuantizedInput, compute_backend.rs:1871-1883) --
+ * codes: rows x code_row_bytes int8 (DenseI8 layout, code_row_bytes ==
+ * padded_dim, padded_dim % 16 == 0); scales/norms: f32 per row; global_ids:
+ * u32 per row (ids written into candidate records). */
+typedef struct tessa_sq8_view {
+    const int8_t *codes;
+    const float *scales;
+    const float *norms;
+    const uint32_t *global_ids;
+    uint64_t rows;
+    uint32_t dim;
+    uint32_t padded_dim;
+} tessa_sq8_view;
+
+/* ---- leaf layouts (TessaLeafLayout, tessa_replay.rs:1041-1047) ---------
+ * members: local row ids (index into the SQ8 arrays), concatenated per leaf;
+ * member_offsets[l] / member_counts[l] / output_offsets[l]; output slot of
+ * (leaf l, member row r, rank q) is output_offsets[l] + r*k + q. */
+typedef struct tessa_leaf_batch {
+    const uint32_t *members;
+    const uint64_t *member_offsets;
+    const uint32_t *member_counts;
+    const uint64_t *output_offsets;
+    uint32_t leaf_count;
+    uint32_t max_leaf_rows;   /* upper bound of member_counts (checked on device) */
+    uint32_t k;               /* 1..32; per leaf k_eff = min(k, n-1) */
+    uint32_t executor;        /* TESSA_EXEC_MFMA or TESSA_EXEC_EXACT */
+    uint32_t debug_list_cap;  /* 0 = default; a small value forces the MFMA
+                                 path's per-row exact re-run (test knob) */
+    uint32_t reserved;
+} tessa_leaf_batch;
+
+/* Leaf all-pairs SQ8 evaluation + per-row top-k (candidate records).
+ * All pointers are device pointers; work is enqueued on `stream` (hipStream_t,
+ * NULL = default stream).  out_ids/out_dists receive (global id, f32 distance)
+ * per slot: bit-identical to the reference RowTopK order (eps 2e-5, ties by
+ * global id, columns in member order); unused slots are (0xffffffff, FLT_MAX).
+ * counters: TESSA_COUNTER_WORDS u64 (accumulated; caller zeroes), may be NULL.
+ * The call allocates its workspace on first use (grows, kept per device). */
+tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *leaves,
+                             uint32_t *out_ids, float *out_dists,
+                             uint64_t *counters, void *stream);
+
+/* ---- assignment tasks (TessaAssignmentLayout, tessa_replay.rs:1031-1039) -
+ * For member row m of task t, leaders of the task are visited in slot order;
+ * best r_h[t] <= 4 ranks are written at output_offsets[t] + m*r_h[t] + rank as
+ * (leader global id, f32 SQ8 distance). */
+typedef struct tessa_assign_batch {
+    const uint32_t *members;
+    const uint32_t *leaders;
+    const uint32_t *member_offsets;
+    const uint32_t *member_counts;
+    const uint32_t *leader_offsets;
+    const uint32_t *leader_counts;   /* each <= 128 */
+    const uint32_t *r_h;             /* each 1..4, <= leader count */
+    const uint64_t *output_offsets;
+    uint32_t task_count;
+    uint32_t max_members;            /* upper bound of member_counts */
+} tessa_assign_batch;
+
+tessa_status tessa_assign_replay(const tessa_sq8_view *sq8, const tessa_assign_batch *tasks,
+                                 uint32_t *out_ids, float *out_dists,
+                                 uint64_t *counters, void *stream);
+
+/* SQ8 quantizer on device: x is rows x dim f32 (device); codes rows x
+ * padded_dim int8, scales/norms f32.  Bit-identical to the reference CPU
+ * quantizer (sequential f32 norm, round half away from zero).  *bad_row_out
+ * (device u64, may be NULL) receives the first row holding a non-finite value
+ * or UINT64_MAX; such rows are left zero. */
+tessa_status tessa_sq8_quantize(const float *x, uint64_t rows, uint32_t dim,
+                                uint32_t padded_dim, uint32_t bits, int8_t *codes,
+                                float *scales, float *norms, uint64_t *bad_row_out,
+                                void *stream);
+
+/* ---- sessions (TessaCudaReplaySession / CudaComputeBackend role) --------
+ * A session owns one device, one stream and device copies of an SQ8 resident
+ * set.  Sessions are single-threaded: callers serialise, as the reference's
+ * Mutex<CudaGemmEngine> does. */
+typedef struct tessa_session tessa_session;
+
+typedef struct tessa_config {
+    int32_t device;
+    uint32_t reserved;
+} tessa_config;
+
+tessa_status tessa_session_create(const tessa_config *cfg, tessa_session **out);
+tessa_status tessa_session_destroy(tessa_session *session);
+/* H2D copy of a host SQ8 resident set into session-owned device buffers. */
+tessa_status tessa_session_upload_sq8(tessa_session *session, const tessa_sq8_view *host);
+
+/* Host-layout leaf replay: host arrays in, host arrays out; event_ms gets the
+ * kernel time measured with hipEvents on the session stream. */
+tessa_status tessa_session_leaf_topk(tessa_session *session,
+                                     const uint32_t *members, const uint64_t *member_offsets,
+                                     const uint32_t *member_counts,
+                                     const uint64_t *output_offsets, uint32_t leaf_count,
+                                     uint32_t k, uint32_t executor, uint32_t *out_ids,
+                                     float *out_dists, uint64_t *counters, float *event_ms);
+
+tessa_status tessa_session_assign_replay(tessa_session *session, const uint32_t *members,
+                                         const uint32_t *leaders,
+                                         const uint32_t *member_offsets,
+                                         const uint32_t *member_counts,
+                                         const uint32_t *leader_offsets,
+                                         const uint32_t *leader_counts, const uint32_t *r_h,
+                                         const uint64_t *output_offsets, uint32_t task_count,
+                                         uint32_t *out_ids, float *out_dists,
+                                         uint64_t *counters, float *event_ms);
+
+/* "QUEUE_NODE|LEAF_ROW|..." or "none" (same labels as the reference). */
+void tessa_overflow_labels(uint64_t flags, char *buf, size_t len);
+uint32_t tessa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,193 @@
+"""ctypes wrapper of oracle/libtessa_oracle.so -- TEST INFRASTRUCTURE ONLY.
+
+The CPU restatement of the reference semantics used as the parity checker and
+as bench.py's cpu_baseline.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py import this module; the product (shear_amd/)
+never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libtessa_oracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = C.CDLL(str(LIB))
+        P = C.c_void_p
+        _lib.orc_sq8_padded_dim.restype = C.c_size_t
+        _lib.orc_sq8_padded_dim.argtypes = [C.c_size_t, C.c_size_t]
+        _lib.orc_sq8_quantize.restype = C.c_int
+        _lib.orc_sq8_quantize.argtypes = [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_uint, P, P, P, P]
+        _lib.orc_sq8_dot_scalar.restype = C.c_int32
+        _lib.orc_sq8_dot_scalar.argtypes = [P, P, C.c_size_t]
+        _lib.orc_sq8_dot.restype = C.c_int32
+        _lib.orc_sq8_dot.argtypes = [P, P, C.c_size_t]
+        _lib.orc_sq8_dot_kernel.restype = C.c_int
+        _lib.orc_sq8_set_dot_kernel.restype = C.c_int
+        _lib.orc_sq8_set_dot_kernel.argtypes = [C.c_int]
+        _lib.orc_sq8_leaf_l2.restype = C.c_float
+        _lib.orc_sq8_leaf_l2.argtypes = [C.c_int32, C.c_float, C.c_float, C.c_float, C.c_float]
+        _lib.orc_sq8_assign_l2.restype = C.c_float
+        _lib.orc_sq8_assign_l2.argtypes = [C.c_int32, C.c_float, C.c_float, C.c_float, C.c_float]
+        _lib.orc_beats.restype = C.c_int
+        _lib.orc_beats.argtypes = [C.c_float, C.c_uint32, C.c_float, C.c_uint32]
+        _lib.orc_rowtopk_push.restype = None
+        _lib.orc_rowtopk_push.argtypes = [C.c_uint32, C.c_float, C.c_uint32, P, P, P]
+        _lib.orc_leaf_topk_batch.restype = C.c_int
+        _lib.orc_leaf_topk_batch.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, C.c_size_t,
+                                             C.c_uint32, P, P, C.c_int]
+        _lib.orc_hash64.restype = C.c_uint64
+        _lib.orc_hash64.argtypes = [C.c_uint64]
+        _lib.orc_assign_tie_key.restype = C.c_uint64
+        _lib.orc_assign_tie_key.argtypes = [C.c_uint32, C.c_uint32]
+        for name in ("orc_assign_replay", "orc_assign_strict"):
+            fn = getattr(_lib, name)
+            fn.restype = C.c_int
+            fn.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, P, P, P, P, C.c_size_t, P, P, C.c_int]
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def padded_dim(dim: int, k_align: int = 16) -> int:
+    return int(lib().orc_sq8_padded_dim(dim, k_align))
+
+
+def quantize(x: np.ndarray, k_align: int = 16, bits: int = 8):
+    """-> (codes int8 [rows, pd], scales f32, norms f32); ValueError on non-finite."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, dim = x.shape
+    pd = padded_dim(dim, k_align)
+    codes = np.zeros((rows, pd), dtype=np.int8)
+    scales = np.zeros(rows, dtype=np.float32)
+    norms = np.zeros(rows, dtype=np.float32)
+    bad = C.c_size_t(0)
+    rc = lib().orc_sq8_quantize(_p(x), rows, dim, pd, bits, _p(codes), _p(scales), _p(norms), C.byref(bad))
+    if rc == -1:
+        raise ValueError(f"SQ-int8 cannot quantize non-finite value (row {bad.value})")
+    if rc != 0:
+        raise ValueError(f"invalid quantize arguments (rc={rc})")
+    return codes, scales, norms
+
+
+def dot(a: np.ndarray, b: np.ndarray, scalar: bool = False) -> int:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    fn = lib().orc_sq8_dot_scalar if scalar else lib().orc_sq8_dot
+    return int(fn(_p(a), _p(b), a.size))
+
+
+def set_dot_kernel(k: int) -> int:
+    return int(lib().orc_sq8_set_dot_kernel(k))
+
+
+def dot_kernel() -> int:
+    return int(lib().orc_sq8_dot_kernel())
+
+
+def leaf_l2(dot_: int, rs: float, rn: float, cs: float, cn: float) -> np.float32:
+    return np.float32(lib().orc_sq8_leaf_l2(dot_, rs, rn, cs, cn))
+
+
+def assign_l2(dot_: int, ps: float, pn: float, ls: float, ln: float) -> np.float32:
+    return np.float32(lib().orc_sq8_assign_l2(dot_, ps, pn, ls, ln))
+
+
+def beats(dc: float, idc: int, ds: float, ids: int) -> bool:
+    return bool(lib().orc_beats(dc, idc, ds, ids))
+
+
+class RowTopK:
+    """leaf_build.rs:887-957 via the oracle's push."""
+
+    def __init__(self):
+        self.d = np.full(32, np.inf, dtype=np.float32)
+        self.ids = np.full(32, 0xFFFFFFFF, dtype=np.uint32)
+        self.len = C.c_uint32(0)
+
+    def push(self, k: int, dist: float, target: int):
+        lib().orc_rowtopk_push(k, dist, target, _p(self.d), _p(self.ids), C.byref(self.len))
+
+    def items(self):
+        n = self.len.value
+        return list(zip(self.ids[:n].tolist(), self.d[:n].tolist()))
+
+
+def leaf_topk(codes, scales, norms, global_ids, members, member_offsets, member_counts, k, threads=0):
+    """Leaf operator over replay layouts; returns (ids u32, dists f32) flat."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    norms = np.ascontiguousarray(norms, dtype=np.float32)
+    gids = np.ascontiguousarray(global_ids, dtype=np.uint32)
+    members = np.ascontiguousarray(members, dtype=np.uint32)
+    moff = np.ascontiguousarray(member_offsets, dtype=np.uint64)
+    mcnt = np.ascontiguousarray(member_counts, dtype=np.uint32)
+    ooff = np.zeros(len(mcnt), dtype=np.uint64)
+    if len(mcnt) > 1:
+        ooff[1:] = np.cumsum(mcnt[:-1].astype(np.uint64) * np.uint64(k))
+    total = int(mcnt.astype(np.int64).sum()) * k
+    out_ids = np.zeros(total, dtype=np.uint32)
+    out_d = np.zeros(total, dtype=np.float32)
+    rc = lib().orc_leaf_topk_batch(_p(codes), _p(scales), _p(norms), _p(gids), codes.shape[0], codes.shape[1],
+                                   _p(members), _p(moff), _p(mcnt), _p(ooff), len(mcnt), k, _p(out_ids),
+                                   _p(out_d), threads)
+    if rc != 0:
+        raise ValueError(f"oracle leaf_topk failed rc={rc}")
+    return out_ids, out_d
+
+
+def _assign(fn_name, codes, scales, norms, global_ids, members, leaders, member_offsets, member_counts,
+            leader_offsets, leader_counts, r_h, threads=0):
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    a32 = lambda x: np.ascontiguousarray(x, dtype=np.uint32)  # noqa: E731
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    norms = np.ascontiguousarray(norms, dtype=np.float32)
+    gids, mem, lead = a32(global_ids), a32(members), a32(leaders)
+    mo, mc, lo, lc, rh = a32(member_offsets), a32(member_counts), a32(leader_offsets), a32(leader_counts), a32(r_h)
+    oo = np.zeros(len(mc), dtype=np.uint64)
+    if len(mc) > 1:
+        oo[1:] = np.cumsum(mc[:-1].astype(np.uint64) * rh[:-1].astype(np.uint64))
+    total = int((mc.astype(np.int64) * rh.astype(np.int64)).sum())
+    out_ids = np.zeros(total, dtype=np.uint32)
+    out_d = np.zeros(total, dtype=np.float32)
+    rc = getattr(lib(), fn_name)(_p(codes), _p(scales), _p(norms), _p(gids), codes.shape[0], codes.shape[1],
+                                 _p(mem), _p(lead), _p(mo), _p(mc), _p(lo), _p(lc), _p(rh), _p(oo), len(mc),
+                                 _p(out_ids), _p(out_d), threads)
+    if rc != 0:
+        raise ValueError(f"oracle {fn_name} failed rc={rc}")
+    return out_ids, out_d
+
+
+def assign_replay(*args, **kw):
+    return _assign("orc_assign_replay", *args, **kw)
+
+
+def assign_strict(*args, **kw):
+    return _assign("orc_assign_strict", *args, **kw)
+
+
+def hash64(x: int) -> int:
+    return int(lib().orc_hash64(x))
+
+
+def assign_tie_key(point: int, leader: int) -> int:
+    return int(lib().orc_assign_tie_key(point, leader))

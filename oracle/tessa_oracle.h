@@ -1,0 +1,133 @@
+/*
+ * tessa_oracle.h -- CPU restatement of the reference TESSA operator semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * implementation in shear_amd/.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  The product path never calls it.
+ *
+ * Every function names the reference file:line whose behaviour it restates
+ * (paths are relative to shear-core/src/algorithm/pipnn/ in the reference).
+ *
+ * Pinning (what checks each function, besides retyping the formula):
+ *   orc_sq8_quantize      reference KATs dco_sq_int8.rs:3261-3299 (codes, scale
+ *                         bits, norm, zero row), round-half-away-from-zero and
+ *                         clamp cases, bit-width variants (4-bit KAT).
+ *   orc_sq8_dot*          brute-force int64 sum; VNNI/AVX2 == scalar on random
+ *                         and extreme (+-127) codes; KAT dco_sq_int8.rs:3301-3325.
+ *   orc_sq8_leaf_l2       KAT 127*64+64*127 dot; closed form evaluated in
+ *                         float64 then rounded step by step; d<=0 -> 0 clamp.
+ *   orc_rowtopk_push      brute force: with no eps-ties the result equals a
+ *                         stable sort by distance; tie KAT (smaller id wins
+ *                         within 2e-5); non-transitive chain example whose
+ *                         answer is worked by hand (order dependence).
+ *   orc_leaf_topk_batch   brute force on tiny leaves via an independent numpy
+ *                         restatement; invariants (self never listed, ids are
+ *                         members, k_eff = min(k, n-1)).
+ *   orc_assign_replay     hash64 == SplitMix64 finalizer known outputs; without
+ *                         near-ties equals the strict (dist, id) order of the
+ *                         CPU D0 path (orc_assign_strict).
+ */
+#ifndef TESSA_ORACLE_H
+#define TESSA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* mod.rs:74 STABLE_DISTANCE_TIE_EPS */
+#define ORC_TIE_EPS 2.0e-5f
+/* dco_sq_int8.rs:14 SQ_INT8_DEFAULT_K_ALIGN */
+#define ORC_SQ8_K_ALIGN 16u
+#define ORC_EMPTY_ID 0xffffffffu
+
+/* dco_sq_int8.rs:1216-1224 sq_int8_padded_dim (0 on dim == 0). */
+size_t orc_sq8_padded_dim(size_t dim, size_t k_align);
+
+/* dco_sq_int8.rs:1340-1375 + 1431-1467: per-vector symmetric quantizer.
+ * Returns 0, or -1 when a value is non-finite (its row in *bad_row), or -2 on
+ * bad arguments.  codes is rows*padded_dim, zero padded. */
+int orc_sq8_quantize(const float *x, size_t rows, size_t dim, size_t padded_dim,
+                     unsigned bits, int8_t *codes, float *scales, float *norms,
+                     size_t *bad_row);
+
+/* dco_sq_int8.rs:2685-2691 scalar dot; the dispatching version uses the best
+ * SIMD path present (dco_sq_int8.rs:2813-2948 analogue). */
+int32_t orc_sq8_dot_scalar(const int8_t *a, const int8_t *b, size_t n);
+int32_t orc_sq8_dot(const int8_t *a, const int8_t *b, size_t n);
+/* Which dot path orc_sq8_dot uses: 0 scalar, 1 avx2, 2 avx512-vnni. */
+int orc_sq8_dot_kernel(void);
+/* Force a path (for the SIMD == scalar tests); returns the previous one. */
+int orc_sq8_set_dot_kernel(int kernel);
+
+/* compute_backend.rs:8987-9002 (== dco_sq_int8.rs:2950-2965):
+ * (rn + cn) + (-2 * ((rs * cs) * (float)dot)), then d <= 0 -> 0. */
+float orc_sq8_leaf_l2(int32_t dot, float row_scale, float row_norm,
+                      float col_scale, float col_norm);
+
+/* rbc_partition.rs:17630-17639 (== compute_backend.rs:6400-6411 without
+ * contraction): (pn + ln) - ((2 * ps) * ls) * (float)dot, then d <= 0 -> 0. */
+float orc_sq8_assign_l2(int32_t dot, float point_scale, float point_norm,
+                        float leader_scale, float leader_norm);
+
+/* mod.rs:417-428 stable_distance_order(...).is_lt(): candidate c beats s. */
+int orc_beats(float dc, uint32_t idc, float ds, uint32_t ids);
+
+/* leaf_build.rs:887-957 RowTopK::push (k <= 32). */
+void orc_rowtopk_push(uint32_t k, float d, uint32_t id, float *best_d,
+                      uint32_t *best_id, uint32_t *len);
+
+/* Leaf operator over replay layouts (tessa_replay.rs:1021-1057 TessaLeafLayout,
+ * semantics leaf_build.rs:1566-1590 with the SQ8 distance): for every member
+ * row, every other member column in member order is pushed into RowTopK.
+ * Output slot [output_offset + row*k + rank] = (global id, distance); slots
+ * past k_eff = min(k, n-1) are (0xffffffff, FLT_MAX).
+ * threads <= 0 uses all OpenMP threads.  Returns 0 or a negative error. */
+int orc_leaf_topk_batch(const int8_t *codes, const float *scales,
+                        const float *norms, const uint32_t *global_ids,
+                        size_t resident_rows, size_t padded_dim,
+                        const uint32_t *members, const uint64_t *member_offsets,
+                        const uint32_t *member_counts,
+                        const uint64_t *output_offsets, size_t leaf_count,
+                        uint32_t k, uint32_t *out_ids, float *out_dists,
+                        int threads);
+
+/* compute_backend.rs:5983-5989 gpu_persistent_hash64 (SplitMix64 finalizer). */
+uint64_t orc_hash64(uint64_t x);
+/* compute_backend.rs:6513-6522 tie key. */
+uint64_t orc_assign_tie_key(uint32_t point, uint32_t leader);
+
+/* Assignment replay (compute_backend.rs:15729-15943 with best_slots4_no_dco
+ * :6618-6699 and insert :6524-6580): per member, leaders visited in slot
+ * order into 4 slots with the 2e-5 eps / hash tie key rule; output rank r of
+ * member row m at output_offset + m*r_h + r = (global id of leader, dist). */
+int orc_assign_replay(const int8_t *codes, const float *scales,
+                      const float *norms, const uint32_t *global_ids,
+                      size_t resident_rows, size_t padded_dim,
+                      const uint32_t *members, const uint32_t *leaders,
+                      const uint32_t *member_offsets,
+                      const uint32_t *member_counts,
+                      const uint32_t *leader_offsets,
+                      const uint32_t *leader_counts, const uint32_t *r_h,
+                      const uint64_t *output_offsets, size_t task_count,
+                      uint32_t *out_ids, float *out_dists, int threads);
+
+/* CPU D0 path (rbc_partition.rs:17453-17608, compare :17714-17733): strict
+ * (dist, leader global id) order, same output layout as orc_assign_replay. */
+int orc_assign_strict(const int8_t *codes, const float *scales,
+                      const float *norms, const uint32_t *global_ids,
+                      size_t resident_rows, size_t padded_dim,
+                      const uint32_t *members, const uint32_t *leaders,
+                      const uint32_t *member_offsets,
+                      const uint32_t *member_counts,
+                      const uint32_t *leader_offsets,
+                      const uint32_t *leader_counts, const uint32_t *r_h,
+                      const uint64_t *output_offsets, size_t task_count,
+                      uint32_t *out_ids, float *out_dists, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,178 @@
+"""ctypes binding of libtessa_hip.so (the C ABI in include/tessa_hip.h).
+
+The library is the product path: when it is missing or fails to load, every
+entry point raises -- there is no CPU fallback anywhere in this package.
+Device buffers are passed as raw device pointers (torch tensors on `cuda` are
+used only as allocations and streams).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtessa_hip.so"
+
+# enum tessa_counter / overflow bits (include/tessa_hip.h)
+COUNTER_WORDS = 32
+C_OVERFLOW_FLAGS = 0
+C_LEAF_ROWS = 1
+C_LEAF_MFMA_TILES = 2
+C_LEAF_EXACT_ROWS = 3
+C_LEAF_FALLBACK_ROWS = 4
+C_LEAF_LIST_OVERFLOW_ROWS = 5
+C_LEAF_GAP_FALLBACK_ROWS = 6
+C_LEAF_REFINES = 7
+C_LEAF_SURVIVORS = 8
+C_LEAF_FINAL_CANDIDATES = 9
+C_ASSIGN_ROWS = 10
+C_ASSIGN_PAIRS = 11
+C_ASSIGN_TIE_EVENTS = 12
+
+EXEC_EXACT = 1
+EXEC_MFMA = 2
+
+TESSA_OK = 0
+
+
+class TessaStatus(C.Structure):
+    _fields_ = [
+        ("code", C.c_int32),
+        ("reserved", C.c_uint32),
+        ("overflow_flags", C.c_uint64),
+        ("msg", C.c_char * 512),
+    ]
+
+
+class TessaCaps(C.Structure):
+    _fields_ = [
+        ("device", C.c_int32),
+        ("compute_units", C.c_int32),
+        ("max_threads_per_block", C.c_int32),
+        ("lds_bytes_per_block", C.c_int32),
+        ("hbm_bytes", C.c_uint64),
+        ("arch", C.c_char * 64),
+        ("supported", C.c_int32),
+        ("max_leaf_rows", C.c_int32),
+        ("max_k", C.c_int32),
+        ("max_padded_dim", C.c_int32),
+    ]
+
+
+class Sq8View(C.Structure):
+    _fields_ = [
+        ("codes", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("norms", C.c_void_p),
+        ("global_ids", C.c_void_p),
+        ("rows", C.c_uint64),
+        ("dim", C.c_uint32),
+        ("padded_dim", C.c_uint32),
+    ]
+
+
+class LeafBatch(C.Structure):
+    _fields_ = [
+        ("members", C.c_void_p),
+        ("member_offsets", C.c_void_p),
+        ("member_counts", C.c_void_p),
+        ("output_offsets", C.c_void_p),
+        ("leaf_count", C.c_uint32),
+        ("max_leaf_rows", C.c_uint32),
+        ("k", C.c_uint32),
+        ("executor", C.c_uint32),
+        ("debug_list_cap", C.c_uint32),
+        ("reserved", C.c_uint32),
+    ]
+
+
+class AssignBatch(C.Structure):
+    _fields_ = [
+        ("members", C.c_void_p),
+        ("leaders", C.c_void_p),
+        ("member_offsets", C.c_void_p),
+        ("member_counts", C.c_void_p),
+        ("leader_offsets", C.c_void_p),
+        ("leader_counts", C.c_void_p),
+        ("r_h", C.c_void_p),
+        ("output_offsets", C.c_void_p),
+        ("task_count", C.c_uint32),
+        ("max_members", C.c_uint32),
+    ]
+
+
+class TessaConfig(C.Structure):
+    _fields_ = [("device", C.c_int32), ("reserved", C.c_uint32)]
+
+
+# Every symbol include/tessa_hip.h declares, with its ctypes signature.
+_P = C.c_void_p
+_U32 = C.c_uint32
+_U64 = C.c_uint64
+SIGNATURES = {
+    "tessa_abi_version": (_U32, []),
+    "tessa_overflow_labels": (None, [_U64, C.c_char_p, C.c_size_t]),
+    "tessa_query_caps": (TessaStatus, [C.c_int32, C.POINTER(TessaCaps)]),
+    "tessa_leaf_topk": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P]),
+    "tessa_assign_replay": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(AssignBatch), _P, _P, _P, _P]),
+    "tessa_sq8_quantize": (TessaStatus, [_P, _U64, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
+    "tessa_session_create": (TessaStatus, [C.POINTER(TessaConfig), C.POINTER(_P)]),
+    "tessa_session_destroy": (TessaStatus, [_P]),
+    "tessa_session_upload_sq8": (TessaStatus, [_P, C.POINTER(Sq8View)]),
+    "tessa_session_leaf_topk": (
+        TessaStatus,
+        [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, C.POINTER(C.c_float)],
+    ),
+    "tessa_session_assign_replay": (
+        TessaStatus,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _P, _P, _P, C.POINTER(C.c_float)],
+    ),
+}
+
+_lib = None
+
+
+class TessaError(RuntimeError):
+    def __init__(self, status: TessaStatus, what: str):
+        self.code = int(status.code)
+        self.overflow_flags = int(status.overflow_flags)
+        self.message = status.msg.decode(errors="replace")
+        super().__init__(f"{what}: code={self.code} {self.message}")
+
+
+def load(path: Path | str | None = None):
+    """Load the HIP library once; raises if it is absent (no fallback)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} is missing: build it with `python -m shear_amd.build` "
+            "(the TESSA operator has no CPU fallback)"
+        )
+    lib = C.CDLL(str(p), mode=getattr(os, "RTLD_NOW", 2) | C.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(status: TessaStatus, what: str) -> None:
+    if status.code != TESSA_OK:
+        raise TessaError(status, what)
+
+
+def overflow_labels(flags: int) -> str:
+    buf = C.create_string_buffer(256)
+    load().tessa_overflow_labels(flags, buf, len(buf))
+    return buf.value.decode()
+
+
+def query_caps(device: int = 0) -> TessaCaps:
+    caps = TessaCaps()
+    check(load().tessa_query_caps(device, C.byref(caps)), "tessa_query_caps")
+    return caps

@@ -1,0 +1,139 @@
+// leaf_exact.hip -- exact scalar leaf top-k (the reference's DP4A role).
+//
+// One wavefront per (leaf, row).  Lanes compute 64 candidate distances at a
+// time with packed int8 dot4; lane 0 then pushes them, in member order, into
+// the row's 32-slot buffer with the reference insertion rule
+// (compute_backend.rs:7229-7259 / leaf_build.rs:887-957).  This kernel is the
+// semantic baseline on the GPU and re-runs rows the MFMA kernel flags.
+#include "leaf_kernels.h"
+#include "tessa_device.h"
+
+namespace tessa {
+
+namespace {
+
+constexpr int kExactThreads = 64;
+
+__device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row,
+                          float *cd, uint32_t *cg, float *bd, uint32_t *bid) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t n = p.member_counts[leaf];
+    if (row >= n) return;
+    const uint32_t *mem = p.members + p.member_offsets[leaf];
+    const uint32_t keff = (p.k < n - 1u) ? p.k : (n - 1u);
+    const uint32_t self = mem[row];
+    if (self >= p.rows) {
+        if (lane == 0) flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_ROW_ID);
+        return;
+    }
+    const int8_t *rc = p.codes + (uint64_t)self * p.padded_dim;
+    const float rs = p.scales[self];
+    const float rn = p.norms[self];
+    if (lane < kMaxK) {
+        bd[lane] = kEmptyDist;
+        bid[lane] = kEmptyId;
+    }
+    __syncthreads();
+    for (uint32_t base = 0; base < n; base += kExactThreads) {
+        const uint32_t c = base + lane;
+        float d = kEmptyDist;
+        uint32_t g = kEmptyId;
+        bool ok = c < n && c != row;
+        if (ok) {
+            const uint32_t cj = mem[c];
+            if (cj >= p.rows) {
+                flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+                ok = false;
+            } else {
+                int dot = dot_i8_rows(rc, p.codes + (uint64_t)cj * p.padded_dim, p.padded_dim);
+                d = leaf_l2(dot, rs, rn, p.scales[cj], p.norms[cj]);
+                g = p.gids[cj];
+            }
+        }
+        cd[lane] = ok ? d : -1.0f;  // -1 marks "no candidate"
+        cg[lane] = g;
+        __syncthreads();
+        if (lane == 0 && keff > 0) {
+            const uint32_t m = (n - base < (uint32_t)kExactThreads) ? (n - base) : kExactThreads;
+            for (uint32_t j = 0; j < m; ++j) {
+                const float dj = cd[j];
+                if (dj < 0.0f) continue;
+                const uint32_t gj = cg[j];
+                // compute_backend.rs:7229-7259 insertion (empty slots hold FLT_MAX).
+                if (!beats(dj, gj, bd[keff - 1], bid[keff - 1])) continue;
+                uint32_t pos = keff - 1;
+                while (pos > 0 && beats(dj, gj, bd[pos - 1], bid[pos - 1])) {
+                    bd[pos] = bd[pos - 1];
+                    bid[pos] = bid[pos - 1];
+                    --pos;
+                }
+                bd[pos] = dj;
+                bid[pos] = gj;
+            }
+        }
+        __syncthreads();
+    }
+    const uint64_t out = p.output_offsets[leaf] + (uint64_t)row * p.k;
+    if (lane < p.k) {
+        p.out_ids[out + lane] = lane < keff ? bid[lane] : kEmptyId;
+        p.out_dists[out + lane] = lane < keff ? bd[lane] : kEmptyDist;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kExactThreads) void leaf_exact_all_kernel(LeafParams p) {
+    __shared__ float cd[kExactThreads];
+    __shared__ uint32_t cg[kExactThreads];
+    __shared__ float bd[kMaxK];
+    __shared__ uint32_t bid[kMaxK];
+    const uint64_t total = (uint64_t)p.leaf_count * p.max_leaf_rows;
+    uint64_t done = 0;
+    for (uint64_t w = blockIdx.x; w < total; w += gridDim.x) {
+        const uint32_t leaf = (uint32_t)(w / p.max_leaf_rows);
+        const uint32_t row = (uint32_t)(w % p.max_leaf_rows);
+        if (row < p.member_counts[leaf]) {
+            exact_row(p, leaf, row, cd, cg, bd, bid);
+            ++done;
+        }
+    }
+    if (threadIdx.x == 0) {
+        counter_add(p.counters, TESSA_C_LEAF_EXACT_ROWS, done);
+        counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
+    }
+}
+
+__global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(LeafParams p) {
+    __shared__ float cd[kExactThreads];
+    __shared__ uint32_t cg[kExactThreads];
+    __shared__ float bd[kMaxK];
+    __shared__ uint32_t bid[kMaxK];
+    uint32_t count = *p.fallback_count;
+    if (count > p.fallback_capacity) count = p.fallback_capacity;
+    uint64_t done = 0;
+    for (uint32_t w = blockIdx.x; w < count; w += gridDim.x) {
+        exact_row(p, p.fallback[2 * w], p.fallback[2 * w + 1], cd, cg, bd, bid);
+        ++done;
+    }
+    if (threadIdx.x == 0) {
+        counter_add(p.counters, TESSA_C_LEAF_EXACT_ROWS, done);
+        counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
+    }
+}
+
+}  // namespace
+
+int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream) {
+    const uint64_t total = (uint64_t)p.leaf_count * p.max_leaf_rows;
+    if (total == 0) return 0;
+    const uint32_t grid = (uint32_t)(total < 65536 ? total : 65536);
+    hipLaunchKernelGGL(leaf_exact_all_kernel, dim3(grid), dim3(kExactThreads), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_leaf_exact_fallback(const LeafParams &p, hipStream_t stream) {
+    // Grid-stride over the device-side count: no host round trip.
+    hipLaunchKernelGGL(leaf_exact_fallback_kernel, dim3(2048), dim3(kExactThreads), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace tessa

@@ -1,0 +1,48 @@
+"""Seeded synthetic Gaussian-mixture vectors for the benchmark configurations.
+
+The reference builds on real datasets and ships no generator, so this one is
+ours (and unpinned by the reference).  Points are generated component by
+component, so rows [c*per, (c+1)*per) belong to component c: "sorted by
+component", and leaves cut from consecutive rows are spatially coherent.
+
+* ``gmm_numpy``  CPU, numpy PCG64 -- used by tests and small configs.
+* ``gmm_torch``  GPU, torch Philox on the device -- used for bench-size data
+                 (4M x 768 does not fit a host round trip inside a bench run).
+The two generators use different RNG streams; parity tests always feed the
+same generated arrays to both sides.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def gmm_numpy(n: int, dim: int, components: int, sigma: float, seed: int,
+              unit_norm: bool = True) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    centers = rng.standard_normal((components, dim)).astype(np.float64)
+    per = -(-n // components)
+    comp = np.minimum(np.arange(n) // per, components - 1)
+    x = centers[comp] + sigma * rng.standard_normal((n, dim))
+    if unit_norm:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+    return x.astype(np.float32)
+
+
+def gmm_torch(n: int, dim: int, components: int, sigma: float, seed: int, device="cuda",
+              unit_norm: bool = True, chunk_rows: int = 1 << 18):
+    """Same construction on the GPU, chunked to bound temporary memory."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    centers = torch.randn((components, dim), generator=g, device=device, dtype=torch.float32)
+    per = -(-n // components)
+    out = torch.empty((n, dim), dtype=torch.float32, device=device)
+    for start in range(0, n, chunk_rows):
+        end = min(n, start + chunk_rows)
+        comp = torch.clamp(torch.arange(start, end, device=device) // per, max=components - 1)
+        x = centers[comp] + sigma * torch.randn((end - start, dim), generator=g, device=device)
+        if unit_norm:
+            x = x / torch.linalg.vector_norm(x, dim=1, keepdim=True)
+        out[start:end] = x
+    return out
