@@ -168,6 +168,9 @@ def main() -> int:
         "counters": {
             "rows_per_step": int(c[N.C_LEAF_ROWS]) // args.steps,
             "exact_reruns_per_step": int(c[N.C_LEAF_FALLBACK_ROWS]) // args.steps,
+            "list_overflow_rows_per_step": int(c[N.C_LEAF_LIST_OVERFLOW_ROWS]) // args.steps,
+            "gap_fallback_rows_per_step": int(c[N.C_LEAF_GAP_FALLBACK_ROWS]) // args.steps,
+            "chain_rows_per_step": int(c[N.C_LEAF_CHAIN_ROWS]) // args.steps,
             "survivors_per_row": float(c[N.C_LEAF_SURVIVORS]) / max(1, int(c[N.C_LEAF_ROWS])),
             "final_candidates_per_row": float(c[N.C_LEAF_FINAL_CANDIDATES]) / max(1, int(c[N.C_LEAF_ROWS])),
             "refines_per_wave": float(c[N.C_LEAF_REFINES]) / max(1, int(c[N.C_LEAF_ROWS]) // 32),

@@ -89,7 +89,9 @@ enum tessa_counter {
     TESSA_C_LEAF_FINAL_CANDIDATES = 9, /* entries fed to the final ordered insertion */
     TESSA_C_ASSIGN_ROWS = 10,
     TESSA_C_ASSIGN_PAIRS = 11,
-    TESSA_C_ASSIGN_TIE_EVENTS = 12     /* insertions decided by the eps tie key */
+    TESSA_C_ASSIGN_TIE_EVENTS = 12,    /* insertions decided by the eps tie key */
+    TESSA_C_LEAF_CHAIN_ROWS = 13       /* MFMA rows whose eps-tie chains were replayed
+                                          in column order over their candidate set */
 };
 
 /* ---- executors (mirrors tessa_replay.rs:20-86 leaf_executor_code) ------ */
@@ -139,8 +141,9 @@ typedef struct tessa_leaf_batch {
     uint32_t max_leaf_rows;   /* upper bound of member_counts (checked on device) */
     uint32_t k;               /* 1..32; per leaf k_eff = min(k, n-1) */
     uint32_t executor;        /* TESSA_EXEC_MFMA or TESSA_EXEC_EXACT */
-    uint32_t debug_list_cap;  /* 0 = default; a small value forces the MFMA
-                                 path's per-row exact re-run (test knob) */
+    uint32_t debug_rerun_every; /* 0 = off; else rows whose leaf position is a
+                                   multiple of it take the exact re-run path
+                                   (test knob for the MFMA executor) */
     uint32_t reserved;
 } tessa_leaf_batch;
 

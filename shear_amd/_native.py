@@ -28,6 +28,7 @@ C_LEAF_FINAL_CANDIDATES = 9
 C_ASSIGN_ROWS = 10
 C_ASSIGN_PAIRS = 11
 C_ASSIGN_TIE_EVENTS = 12
+C_LEAF_CHAIN_ROWS = 13
 
 EXEC_EXACT = 1
 EXEC_MFMA = 2
@@ -81,7 +82,7 @@ class LeafBatch(C.Structure):
         ("max_leaf_rows", C.c_uint32),
         ("k", C.c_uint32),
         ("executor", C.c_uint32),
-        ("debug_list_cap", C.c_uint32),
+        ("debug_rerun_every", C.c_uint32),
         ("reserved", C.c_uint32),
     ]
 

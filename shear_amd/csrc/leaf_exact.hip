@@ -120,7 +120,106 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(Leaf
     }
 }
 
+// ---- chain replay -----------------------------------------------------------
+// For a row whose certified candidate set G (every candidate outside G is more
+// than 2e-5 above all of G) contains an eps-tie chain, the reference result is
+// the bounded insertion over G's members in column order; other candidates can
+// neither enter in front of G's nor stay in the buffer.  One lane per row:
+// sort G by column in LDS, then replay compute_backend.rs:7229-7259.
+constexpr int kChainMax = 64;
+constexpr int kChainLanes = 64;
+constexpr int kChainLdsBytes = kChainMax * kChainLanes * 12 + kMaxK * kChainLanes * 8;
+
+__global__ __launch_bounds__(kChainLanes) void leaf_chain_kernel(LeafParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    uint32_t *cc = reinterpret_cast<uint32_t *>(smem);  // column   [i * 64 + lane]
+    float *cd = reinterpret_cast<float *>(cc + kChainMax * kChainLanes);
+    uint32_t *cg = reinterpret_cast<uint32_t *>(cd + kChainMax * kChainLanes);
+    float *bd = reinterpret_cast<float *>(cg + kChainMax * kChainLanes);
+    uint32_t *bg = reinterpret_cast<uint32_t *>(bd + kMaxK * kChainLanes);
+    const uint32_t lane = threadIdx.x;
+    uint32_t count = *p.chain_count;
+    if (count > p.chain_capacity) count = p.chain_capacity;
+    uint64_t done = 0;
+    for (uint32_t w = blockIdx.x * kChainLanes + lane; w < count; w += gridDim.x * kChainLanes) {
+        const uint4 hdr = p.chain_rows[w];
+        const uint32_t leaf = hdr.x, r = hdr.y, off = hdr.z;
+        const uint32_t m = hdr.w < (uint32_t)kChainMax ? hdr.w : (uint32_t)kChainMax;
+        const uint32_t n = p.member_counts[leaf];
+        const uint32_t *mem = p.members + p.member_offsets[leaf];
+        const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
+        for (uint32_t i = 0; i < m; ++i) {
+            const uint2 e = p.chain_pool[off + i];
+            const uint32_t c = e.y;
+            const uint32_t mc = c < n ? mem[c] : 0u;
+            cc[i * kChainLanes + lane] = c;
+            cd[i * kChainLanes + lane] = __uint_as_float(e.x);
+            cg[i * kChainLanes + lane] = mc < p.rows ? p.gids[mc] : kEmptyId;
+        }
+        // insertion sort by column (member order)
+        for (uint32_t i = 1; i < m; ++i) {
+            const uint32_t kc = cc[i * kChainLanes + lane];
+            const float kd = cd[i * kChainLanes + lane];
+            const uint32_t kg = cg[i * kChainLanes + lane];
+            uint32_t j = i;
+            while (j > 0 && cc[(j - 1) * kChainLanes + lane] > kc) {
+                cc[j * kChainLanes + lane] = cc[(j - 1) * kChainLanes + lane];
+                cd[j * kChainLanes + lane] = cd[(j - 1) * kChainLanes + lane];
+                cg[j * kChainLanes + lane] = cg[(j - 1) * kChainLanes + lane];
+                --j;
+            }
+            cc[j * kChainLanes + lane] = kc;
+            cd[j * kChainLanes + lane] = kd;
+            cg[j * kChainLanes + lane] = kg;
+        }
+        // leaf_build.rs:913-951 bounded insertion over G in column order
+        uint32_t len = 0;
+        for (uint32_t i = 0; i < m && keff > 0u; ++i) {
+            const float d = cd[i * kChainLanes + lane];
+            const uint32_t g = cg[i * kChainLanes + lane];
+            uint32_t pos;
+            if (len < keff) {
+                pos = len++;
+            } else {
+                if (!beats(d, g, bd[(keff - 1) * kChainLanes + lane], bg[(keff - 1) * kChainLanes + lane]))
+                    continue;
+                pos = keff - 1;
+            }
+            while (pos > 0 &&
+                   beats(d, g, bd[(pos - 1) * kChainLanes + lane], bg[(pos - 1) * kChainLanes + lane])) {
+                bd[pos * kChainLanes + lane] = bd[(pos - 1) * kChainLanes + lane];
+                bg[pos * kChainLanes + lane] = bg[(pos - 1) * kChainLanes + lane];
+                --pos;
+            }
+            bd[pos * kChainLanes + lane] = d;
+            bg[pos * kChainLanes + lane] = g;
+        }
+        const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
+        for (uint32_t s = 0; s < p.k; ++s) {
+            const bool live = s < len;
+            p.out_ids[out + s] = live ? bg[s * kChainLanes + lane] : kEmptyId;
+            p.out_dists[out + s] = live ? bd[s * kChainLanes + lane] : kEmptyDist;
+        }
+        ++done;
+    }
+    // per-wave row count
+    for (int offs = 32; offs > 0; offs >>= 1) done += __shfl_xor(done, offs);
+    if (lane == 0) counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
+}
+
 }  // namespace
+
+int launch_leaf_chain(const LeafParams &p, hipStream_t stream) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void *)leaf_chain_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kChainLdsBytes) != hipSuccess)
+            return -1;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(leaf_chain_kernel, dim3(1024), dim3(kChainLanes), kChainLdsBytes, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream) {
     const uint64_t total = (uint64_t)p.leaf_count * p.max_leaf_rows;

@@ -28,15 +28,25 @@ struct LeafParams {
     uint32_t *fallback;
     uint32_t *fallback_count;
     uint32_t fallback_capacity;
-    // Debug/test knob: lowers the per-lane candidate list capacity so the
-    // overflow -> exact fallback path runs on ordinary inputs (0 = default).
-    uint32_t list_cap_override;
+    // Test knob: rows whose leaf position is a multiple of this value skip
+    // certification and are re-run by the exact kernel (0 = off).
+    uint32_t debug_rerun_every;
+    // Rows whose certified candidate set G holds an eps-tie chain: header
+    // (leaf, row, pool offset, |G|) plus |G| pool entries (f32 bits, column),
+    // replayed in column order by the chain kernel.
+    uint4 *chain_rows;
+    uint32_t *chain_count;
+    uint32_t chain_capacity;
+    uint2 *chain_pool;
+    uint32_t *chain_pool_used;
+    uint32_t chain_pool_capacity;
 };
 
 // Host-side launchers (leaf_exact.hip / leaf_mfma.hip).
 int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream);
 int launch_leaf_exact_fallback(const LeafParams &p, hipStream_t stream);
 int launch_leaf_mfma(const LeafParams &p, hipStream_t stream);
+int launch_leaf_chain(const LeafParams &p, hipStream_t stream);
 int leaf_mfma_supported(uint32_t padded_dim, uint32_t max_leaf_rows);
 
 }  // namespace tessa

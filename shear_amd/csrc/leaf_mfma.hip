@@ -7,27 +7,32 @@
 //
 // Work item = (leaf, block of 128 member rows); a workgroup is 4 waves, wave w
 // owns 32 rows.  The wave keeps its 32 rows' codes in VGPRs for the whole K
-// range and is the MFMA "B" operand (N = rows); 32-candidate column tiles are
-// staged in LDS and are the "A" operand (M = candidates).  With
-// v_mfma_i32_32x32x32_i8 the output lane l holds row l%32 and the 16
-// candidates 8*(v/4) + 4*(l/32) + v%4 of the tile, so each lane owns half of
-// one row's candidates and walks them in increasing column order.
+// range as the MFMA "B" operand (N = rows); 32-candidate column tiles are
+// staged in LDS as the "A" operand (M = candidates).  With
+// v_mfma_i32_32x32x32_i8 output lane l holds row l%32 and candidates
+// 8*(v/4) + 4*(l/32) + v%4 of the tile: each row is served by a lane pair
+// (l, l+32), each lane seeing half of the row's candidates.
 //
-// Selection is exact by construction:
-//  * each lane keeps every candidate with d <= F in a list (F is the running
-//    threshold of the row, shared by its two lanes, never increasing);
-//  * F is the larger of the two lanes' 16th-smallest distance seen so far, so
-//    at least 32 >= k candidates of the row are <= F at all times;
-//  * at the end, the row's listed candidates with d <= F are pushed in column
-//    order through the reference insertion rule.  Let M be the largest kept
-//    distance and theta the smallest value >= M with no candidate in
-//    (theta, theta + 2e-5].  Every candidate <= theta is listed (theta <= F is
-//    checked), every candidate above it is > theta + 2e-5 away from all of
-//    them, and for such a split the bounded insertion over the whole row and
-//    over the listed part give the same buffer (candidates more than eps
-//    above every kept one can never enter in front of them or stay).  Rows
-//    where the check fails, or whose list overflowed, are queued and re-run
-//    by the exact scalar kernel.
+// Selection (exact by construction, see the certificate below):
+//  * every lane keeps the 32 smallest distances it has seen, with their
+//    columns, sorted in registers; new candidates below the row threshold are
+//    staged in LDS and folded in 16 at a time with bitonic networks;
+//  * the row threshold F is the exact 32nd smallest distance of the pair's
+//    two top-32 lists (the row's running 32nd distance), widened by 3*eps;
+//  * every candidate a lane drops (filtered, or evicted from its top-32)
+//    lowers that lane's `disc` to the smallest dropped distance;
+//  * at the end the pair's lists are merged into the sorted known sequence
+//    s_0 <= s_1 <= ...  Consecutive elements within 2e-5 form tie clusters.
+//    G = s_0..s_q, the prefix closed at the cluster holding s_{k-1}.  The row
+//    is certified when the next distance after s_q, known or dropped, lies
+//    more than 2e-5 above s_q, and every cluster inside G spans <= 2e-5.
+//    Then every candidate outside G is more than eps above every one inside,
+//    so the reference's bounded insertion over the whole row keeps exactly G's
+//    k best (candidates eps-separated from all kept ones can never enter in
+//    front of them or stay); and inside G the tie relation is an equivalence,
+//    so the comparator is a total order there: distance order, clusters
+//    ordered by global id.  Uncertified rows are queued for the exact scalar
+//    kernel.
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
@@ -42,30 +47,37 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerBlock = kWaves * 32;
 constexpr int kTileCols = 32;
-constexpr int kCap = 56;       // per-lane candidate list capacity
-constexpr int kKeepPerLane = 16;
+constexpr int kTop = 32;        // per-lane sorted list (registers)
+constexpr int kStage = 32;      // per-lane staging capacity (LDS)
 constexpr uint32_t kMaxLeafRows = 4096;
+constexpr float kFilterMargin = 3.0f * kTieEps;
 
 template <int KS>
 struct Layout {
-    static constexpr int kTileStride = KS * 32 + 16;                 // bytes per LDS tile row
+    static constexpr int kTileStride = KS * 32 + 16;  // bytes per LDS tile row (16 B pad: no bank aliasing)
     static constexpr int kTileBytes = kTileCols * kTileStride;
-    // The tile area also stages the leaf's global ids for the final phase.
-    static constexpr int kTileRegion =
-        kTileBytes > (int)kMaxLeafRows * 4 ? kTileBytes : (int)kMaxLeafRows * 4;
-    static constexpr int kMetaOff = kTileRegion;                     // scales[32], norms[32]
-    static constexpr int kListDOff = kMetaOff + 2 * kTileCols * 4;
-    static constexpr int kListCOff = kListDOff + (kCap + 1) * kThreads * 4;
-    static constexpr int kFinDOff = kListCOff + (kCap + 1) * kThreads * 2;
-    static constexpr int kFinGOff = kFinDOff + kMaxK * kRowsPerBlock * 4;
-    static constexpr int kBytes = kFinGOff + kMaxK * kRowsPerBlock * 4;
-    static constexpr int kChunks = kTileCols * KS * 2;               // 16-byte chunks per tile
+    static constexpr int kMetaOff = kTileBytes;                   // scales[32], norms[32]
+    static constexpr int kMemOff = kMetaOff + 2 * kTileCols * 4;  // leaf member ids
+    static constexpr int kStageOff = kMemOff + (int)kMaxLeafRows * 4;
+    static constexpr int kBytes = kStageOff + kStage * kThreads * 8;
+    static constexpr int kChunks = kTileCols * KS * 2;            // 16-byte chunks per tile
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
     static_assert(kBytes <= 160 * 1024, "LDS budget");
 };
 
+// Compare-exchange on (key, payload) pairs; ascending when `up`.
+__device__ __forceinline__ void cex(float &a, uint32_t &pa, float &b, uint32_t &pb, bool up) {
+    const bool sw = up ? (b < a) : (a < b);
+    const float ta = a;
+    const uint32_t tpa = pa;
+    a = sw ? b : a;
+    pa = sw ? pb : pa;
+    b = sw ? ta : b;
+    pb = sw ? tpa : pb;
+}
+
 template <int N>
-__device__ __forceinline__ void bitonic_sort(float (&v)[N]) {
+__device__ __forceinline__ void bitonic_sort_kv(float (&v)[N], uint32_t (&p)[N]) {
 #pragma unroll
     for (int k = 2; k <= N; k <<= 1) {
 #pragma unroll
@@ -73,29 +85,20 @@ __device__ __forceinline__ void bitonic_sort(float (&v)[N]) {
 #pragma unroll
             for (int i = 0; i < N; ++i) {
                 const int l = i ^ j;
-                if (l > i) {
-                    const float a = v[i], b = v[l];
-                    const float lo = fminf(a, b), hi = fmaxf(a, b);
-                    if ((i & k) == 0) { v[i] = lo; v[l] = hi; }
-                    else { v[i] = hi; v[l] = lo; }
-                }
+                if (l > i) cex(v[i], p[i], v[l], p[l], (i & k) == 0);
             }
         }
     }
 }
 
 template <int N>
-__device__ __forceinline__ void bitonic_merge(float (&v)[N]) {
+__device__ __forceinline__ void bitonic_merge_kv(float (&v)[N], uint32_t (&p)[N]) {
 #pragma unroll
     for (int j = N >> 1; j > 0; j >>= 1) {
 #pragma unroll
         for (int i = 0; i < N; ++i) {
             const int l = i ^ j;
-            if (l > i) {
-                const float a = v[i], b = v[l];
-                v[i] = fminf(a, b);
-                v[l] = fmaxf(a, b);
-            }
+            if (l > i) cex(v[i], p[i], v[l], p[l], true);
         }
     }
 }
@@ -106,6 +109,47 @@ __device__ __forceinline__ int wave_max_i(int x) {
     return x;
 }
 
+// 32nd smallest of the union of two ascending 32-lists (own `a`, partner via
+// shuffle): min over i of max(a[i-1], b[31-i]).  Both lanes of a pair get the
+// same value.
+__device__ __forceinline__ float pair_kth32(const float (&a)[kTop]) {
+    float b[kTop];
+#pragma unroll
+    for (int m = 0; m < kTop; ++m) b[m] = __shfl_xor(a[m], 32);
+    float best = b[kTop - 1];
+#pragma unroll
+    for (int i = 1; i < kTop; ++i) best = fminf(best, fmaxf(a[i - 1], b[kTop - 1 - i]));
+    return fminf(best, a[kTop - 1]);
+}
+
+// Fold `staged` LDS entries of this lane into its sorted top-32.
+__device__ __forceinline__ void fold_staged(const uint2 *stage, uint32_t tid, int staged, float (&topd)[kTop],
+                                            uint32_t (&topc)[kTop], float &disc) {
+    const int chunks = (wave_max_i(staged) + 15) / 16;
+    for (int ch = 0; ch < chunks; ++ch) {
+        float v[16];
+        uint32_t c[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = ch * 16 + i;
+            const uint2 s = e < staged ? stage[e * kThreads + tid] : make_uint2(0x7f800000u, 0xffffu);
+            v[i] = __uint_as_float(s.x);
+            c[i] = s.y;
+        }
+        bitonic_sort_kv<16>(v, c);
+        // lower half of (top ascending) vs (chunk ascending, padded to 32, reversed)
+#pragma unroll
+        for (int i = 16; i < kTop; ++i) {
+            const float a = topd[i], b = v[kTop - 1 - i];
+            const bool sw = b < a;
+            disc = fminf(disc, sw ? a : b);  // the larger one leaves the list
+            topd[i] = sw ? b : a;
+            topc[i] = sw ? c[kTop - 1 - i] : topc[i];
+        }
+        bitonic_merge_kv<kTop>(topd, topc);
+    }
+}
+
 template <int KS>
 __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
                                                               uint32_t total_work, uint32_t padded_grid) {
@@ -114,11 +158,8 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
     float *meta_s = reinterpret_cast<float *>(smem + L::kMetaOff);
     float *meta_n = meta_s + kTileCols;
-    float *list_d = reinterpret_cast<float *>(smem + L::kListDOff);
-    uint16_t *list_c = reinterpret_cast<uint16_t *>(smem + L::kListCOff);
-    float *fin_d = reinterpret_cast<float *>(smem + L::kFinDOff);
-    uint32_t *fin_g = reinterpret_cast<uint32_t *>(smem + L::kFinGOff);
-    uint32_t *gid_lds = reinterpret_cast<uint32_t *>(smem);  // reuses the tile area at the end
+    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kMemOff);
+    uint2 *stage = reinterpret_cast<uint2 *>(smem + L::kStageOff);
 
     // XCD-aware order: blocks are dispatched round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of work items (the row blocks of one
@@ -137,22 +178,26 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     }
     const uint32_t *mem = p.members + p.member_offsets[leaf];
     const uint32_t pd = p.padded_dim;
-    const uint32_t cap = (p.list_cap_override != 0u && p.list_cap_override < (uint32_t)kCap)
-                             ? p.list_cap_override : (uint32_t)kCap;
-
     const uint32_t tid = threadIdx.x;
+
+    // Leaf member ids once in LDS (tile loads then need one global hop, not two).
+    for (uint32_t c = tid; c < n; c += kThreads) {
+        uint32_t mc = mem[c];
+        if (mc >= p.rows) {
+            flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+            mc = 0u;
+        }
+        mem_lds[c] = mc;
+    }
+    __syncthreads();
+
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
     const uint32_t j = lane & 31u;
     const uint32_t h = lane >> 5;
     const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
-    bool row_ok = r < n;
-    uint32_t mr = row_ok ? mem[r] : 0u;
-    if (row_ok && mr >= p.rows) {
-        flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_ROW_ID);
-        row_ok = false;
-        mr = 0u;
-    }
+    const bool row_ok = r < n;
+    const uint32_t mr = row_ok ? mem_lds[r] : 0u;
 
     // Row codes for the whole K range (B operand), zero past padded_dim.
     v4i bfrag[KS];
@@ -169,13 +214,16 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     const float rs = row_ok ? p.scales[mr] : 0.0f;
     const float rn = row_ok ? p.norms[mr] : 0.0f;
 
-    float top[kKeepPerLane];
+    float topd[kTop];
+    uint32_t topc[kTop];
 #pragma unroll
-    for (int i = 0; i < kKeepPerLane; ++i) top[i] = __builtin_inff();
-    float F = __builtin_inff();
-    int cnt = 0;
-    int merged = 0;      // list entries already folded into `top`
-    bool ovf = false;
+    for (int i = 0; i < kTop; ++i) {
+        topd[i] = __builtin_inff();
+        topc[i] = 0xffffu;
+    }
+    float F = __builtin_inff();   // filter threshold (running 32nd + margin)
+    float disc = __builtin_inff(); // smallest distance this lane dropped
+    int staged = 0;
     uint32_t survivors = 0, refines = 0;
 
     const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
@@ -191,10 +239,8 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
                 const uint32_t row = chunk / (KS * 2);
                 const uint32_t off = (chunk % (KS * 2)) * 16u;
                 const uint32_t c = t * kTileCols + row;
-                if (c < n && off < pd) {
-                    const uint32_t mc = mem[c];
-                    if (mc < p.rows) z = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mc * pd + off);
-                }
+                if (c < n && off < pd)
+                    z = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mem_lds[c] * pd + off);
             }
             pre[q] = z;
         }
@@ -202,11 +248,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
         if (tid < 2u * kTileCols) {
             const uint32_t c = t * kTileCols + (tid & 31u);
             float v = 0.0f;
-            if (c < n) {
-                const uint32_t mc = mem[c];
-                if (mc < p.rows) v = (tid < 32u) ? p.scales[mc] : p.norms[mc];
-                else flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
-            }
+            if (c < n) v = (tid < 32u) ? p.scales[mem_lds[c]] : p.norms[mem_lds[c]];
             pre_meta = v;
         }
     };
@@ -235,7 +277,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
         }
 
-        // Epilogue: exact distances, running-threshold filter, list append.
+        // Epilogue: exact distances, threshold filter, stage or drop.
         const uint32_t cbase = t * kTileCols;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -248,186 +290,213 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
                 const int v = 4 * q + e;
                 const uint32_t c = cbase + 8u * q + 4u * h + e;
                 const float d = leaf_l2(acc[v], rs, rn, csv[e], cnv[e]);
-                const bool cand = row_ok && c < n && c != r && d <= F;
-                const bool room = cnt < (int)cap;
-                ovf |= cand && !room;
-                const bool take = cand && room;
-                const int slot = take ? cnt : kCap;  // slot kCap is a scratch sink
-                list_d[slot * kThreads + tid] = d;
-                list_c[slot * kThreads + tid] = (uint16_t)c;
-                cnt += take ? 1 : 0;
-                survivors += take ? 1u : 0u;
+                const bool valid = row_ok && c < n && c != r;
+                const bool take = valid && d <= F;
+                if (take) {
+                    stage[staged * kThreads + tid] = make_uint2(__float_as_uint(d), c);
+                    ++staged;
+                    ++survivors;
+                }
+                disc = (valid && !take) ? fminf(disc, d) : disc;
             }
         }
 
-        // Refine before the next tile can overflow a list (up to 16 appends).
-        if (__any(cnt > (int)cap - 16)) {
+        // Fold staged candidates before the next tile could overflow staging.
+        if (__any(staged > kStage - 16)) {
             ++refines;
-            const int fresh = wave_max_i(cnt - merged);
-            for (int base = 0; base < fresh; base += 16) {
-                float v[16];
+            fold_staged(stage, tid, staged, topd, topc, disc);
+            staged = 0;
+            F = __fadd_rn(pair_kth32(topd), kFilterMargin);
+        }
+    }
+    // ---- final: merge the pair's lists, certify, order, write ---------------
+    if (__any(staged > 0)) fold_staged(stage, tid, staged, topd, topc, disc);
+
+    float sd[2 * kTop];
+    uint32_t sc[2 * kTop];
+    {
+        float bd[kTop];
+        uint32_t bc[kTop];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int e = merged + base + i;
-                    v[i] = (e < cnt) ? list_d[e * kThreads + tid] : __builtin_inff();
-                }
-                bitonic_sort<16>(v);
-                float m[16];
+        for (int m = 0; m < kTop; ++m) {
+            bd[m] = __shfl_xor(topd[m], 32);
+            bc[m] = __shfl_xor(topc[m], 32);
+        }
+        // (own ascending) x (partner ascending, reversed): lower halves hold the
+        // 32 smallest, upper halves the rest; both bitonic.
 #pragma unroll
-                for (int i = 0; i < 16; ++i) m[i] = fminf(top[i], v[15 - i]);
-                bitonic_merge<16>(m);
+        for (int i = 0; i < kTop; ++i) {
+            const float a = topd[i], b = bd[kTop - 1 - i];
+            const bool sw = b < a;
+            sd[i] = sw ? b : a;
+            sc[i] = sw ? bc[kTop - 1 - i] : topc[i];
+            sd[kTop + i] = sw ? a : b;
+            sc[kTop + i] = sw ? topc[i] : bc[kTop - 1 - i];
+        }
+    }
+    {
+        float lo[kTop], hi[kTop];
+        uint32_t plo[kTop], phi[kTop];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) top[i] = m[i];
+        for (int i = 0; i < kTop; ++i) {
+            lo[i] = sd[i];
+            plo[i] = sc[i];
+            hi[i] = sd[kTop + i];
+            phi[i] = sc[kTop + i];
+        }
+        bitonic_merge_kv<kTop>(lo, plo);
+        bitonic_merge_kv<kTop>(hi, phi);
+#pragma unroll
+        for (int i = 0; i < kTop; ++i) {
+            sd[i] = lo[i];
+            sc[i] = plo[i];
+            sd[kTop + i] = hi[i];
+            sc[kTop + i] = phi[i];
+        }
+    }
+    const float disc_all = fminf(disc, __shfl_xor(disc, 32));
+
+    const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
+    // Tie clusters over the sorted known sequence.
+    int q_end = (int)keff - 1;   // last index of G
+    bool extending = keff > 0u;
+    bool clique_bad = false;
+    float cstart = sd[0];
+    uint32_t cid[2 * kTop];
+    cid[0] = 0;
+#pragma unroll
+    for (int i = 1; i < 2 * kTop; ++i) {
+        const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
+        cid[i] = tie ? cid[i - 1] : (uint32_t)i;
+        const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
+        cstart = tie ? cstart : sd[i];
+        if (i >= (int)keff && extending) {
+            if (tie) q_end = i;
+            else extending = false;
+        }
+        clique_bad |= span_bad && (i <= q_end || (extending && i >= (int)keff));
+    }
+    // Gap certificate: the cluster holding s_{keff-1} closes inside the known
+    // 64 and the next distance after it -- known or dropped -- is > eps away.
+    bool gap_ok = keff == 0u || !extending;
+    if (keff > 0u && gap_ok) {
+        float theta = sd[0];
+        float next = disc_all;
+#pragma unroll
+        for (int i = 1; i < 2 * kTop; ++i) {
+            theta = (i == q_end) ? sd[i] : theta;  // static indices only: no scratch
+            next = (i == q_end + 1) ? fminf(next, sd[i]) : next;
+        }
+        gap_ok = next == __builtin_inff() || __fsub_rn(next, theta) > kTieEps;
+    }
+    // Test knob: re-run every `debug_rerun_every`-th row through the exact kernel.
+    if (p.debug_rerun_every != 0u && (r % p.debug_rerun_every) == 0u) gap_ok = false;
+    // Outcome: direct output (all clusters of G are cliques), chain queue (a
+    // cluster of G is an eps-chain: its order depends on arrival order, so G
+    // is replayed in column order by leaf_chain_kernel), or full exact re-run.
+    const bool direct = gap_ok && !clique_bad;
+    const bool chain = gap_ok && clique_bad;
+
+    // Global ids of G's positions, then order each cluster by global id.
+    uint32_t sg[2 * kTop];
+#pragma unroll
+    for (int i = 0; i < 2 * kTop; ++i)
+        sg[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? p.gids[mem_lds[sc[i]]] : kEmptyId;
+    bool need_sort = false;
+#pragma unroll
+    for (int i = 1; i < 2 * kTop; ++i) need_sort |= (i <= q_end) && (cid[i] == cid[i - 1]);
+    if (__any(row_ok && direct && need_sort)) {
+        // odd-even transposition sort by global id inside each cluster of G
+        // (sorted once an even and an odd phase in a row swap nothing)
+        for (int pass = 0; pass < 2 * kTop + 2; pass += 2) {
+            bool swapped = false;
+#pragma unroll
+            for (int i = 0; i + 1 < 2 * kTop; i += 2) {
+                const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
+                const uint32_t ga = sg[i], gb = sg[i + 1];
+                const float da = sd[i], db = sd[i + 1];
+                sg[i] = sw ? gb : ga;
+                sg[i + 1] = sw ? ga : gb;
+                sd[i] = sw ? db : da;
+                sd[i + 1] = sw ? da : db;
+                swapped |= sw;
             }
-            const float own = top[kKeepPerLane - 1];
-            F = fmaxf(own, __shfl_xor(own, 32));
-            const int cmax = wave_max_i(cnt);
-            int kept = 0;
-            for (int e = 0; e < cmax; ++e) {
-                if (e < cnt) {
-                    const float d = list_d[e * kThreads + tid];
-                    const uint16_t c = list_c[e * kThreads + tid];
-                    const bool keep = d <= F;
-                    const int slot = keep ? kept : kCap;
-                    list_d[slot * kThreads + tid] = d;
-                    list_c[slot * kThreads + tid] = c;
-                    kept += keep ? 1 : 0;
-                }
+#pragma unroll
+            for (int i = 1; i + 1 < 2 * kTop; i += 2) {
+                const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
+                const uint32_t ga = sg[i], gb = sg[i + 1];
+                const float da = sd[i], db = sd[i + 1];
+                sg[i] = sw ? gb : ga;
+                sg[i + 1] = sw ? ga : gb;
+                sd[i] = sw ? db : da;
+                sd[i + 1] = sw ? da : db;
+                swapped |= sw;
             }
-            cnt = kept;
-            merged = kept;
+            if (!__any(swapped)) break;
         }
     }
 
-    // ---- final ordered insertion -------------------------------------------
-    __syncthreads();  // tile area is free: stage the leaf's global ids
-    for (uint32_t c = tid; c < n; c += kThreads) {
-        const uint32_t mc = mem[c];
-        gid_lds[c] = mc < p.rows ? p.gids[mc] : kEmptyId;
-    }
-    __syncthreads();
-
-    const int cnt_b = __shfl_xor(cnt, 32);
-    const bool ovf_b = __shfl_xor((int)ovf, 32) != 0;
-    uint32_t final_cands = 0, fallbacks = 0, gap_fallbacks = 0, list_ovf = 0, done_rows = 0;
-    if (h == 0u && row_ok) {
-        const uint32_t keff = (p.k < n - 1u) ? p.k : (n - 1u);
-        const uint32_t slot_row = wave * 32u + j;
-        const uint32_t tid_b = tid + 32u;
-        bool ok = !(ovf || ovf_b);
-        if (!ok) ++list_ovf;
-        uint32_t len = 0;
-        if (ok && keff > 0u) {
-            int ia = 0, ib = 0;
-            while (ia < cnt || ib < cnt_b) {
-                float d;
-                uint32_t c;
-                const uint32_t ca = ia < cnt ? list_c[ia * kThreads + tid] : 0xffffu;
-                const uint32_t cb = ib < cnt_b ? list_c[ib * kThreads + tid_b] : 0xffffu;
-                if (ia < cnt && (ib >= cnt_b || ca < cb)) {
-                    d = list_d[ia * kThreads + tid];
-                    c = ca;
-                    ++ia;
-                } else {
-                    d = list_d[ib * kThreads + tid_b];
-                    c = cb;
-                    ++ib;
-                }
-                if (!(d <= F)) continue;
-                ++final_cands;
-                const uint32_t g = gid_lds[c];
-                // compute_backend.rs:7229-7259 insertion into keff slots.
-                if (len < keff) {
-                    uint32_t pos = len;
-                    while (pos > 0 && beats(d, g, fin_d[(pos - 1) * kRowsPerBlock + slot_row],
-                                            fin_g[(pos - 1) * kRowsPerBlock + slot_row])) {
-                        fin_d[pos * kRowsPerBlock + slot_row] = fin_d[(pos - 1) * kRowsPerBlock + slot_row];
-                        fin_g[pos * kRowsPerBlock + slot_row] = fin_g[(pos - 1) * kRowsPerBlock + slot_row];
-                        --pos;
-                    }
-                    fin_d[pos * kRowsPerBlock + slot_row] = d;
-                    fin_g[pos * kRowsPerBlock + slot_row] = g;
-                    ++len;
-                } else {
-                    const uint32_t last = keff - 1;
-                    if (!beats(d, g, fin_d[last * kRowsPerBlock + slot_row], fin_g[last * kRowsPerBlock + slot_row]))
-                        continue;
-                    uint32_t pos = last;
-                    while (pos > 0 && beats(d, g, fin_d[(pos - 1) * kRowsPerBlock + slot_row],
-                                            fin_g[(pos - 1) * kRowsPerBlock + slot_row])) {
-                        fin_d[pos * kRowsPerBlock + slot_row] = fin_d[(pos - 1) * kRowsPerBlock + slot_row];
-                        fin_g[pos * kRowsPerBlock + slot_row] = fin_g[(pos - 1) * kRowsPerBlock + slot_row];
-                        --pos;
-                    }
-                    fin_d[pos * kRowsPerBlock + slot_row] = d;
-                    fin_g[pos * kRowsPerBlock + slot_row] = g;
-                }
-            }
-            if (len < keff) ok = false;  // cannot happen when F is finite; be strict
-            if (ok) {
-                // Gap certificate: theta >= max kept distance, no candidate in
-                // (theta, theta + eps], and theta + eps < F (list completeness).
-                float theta = 0.0f;
-                for (uint32_t s = 0; s < keff; ++s) theta = fmaxf(theta, fin_d[s * kRowsPerBlock + slot_row]);
-                for (int guard = 0; guard < 2 * kCap + 2; ++guard) {
-                    float next = __builtin_inff();
-                    for (int e = 0; e < cnt; ++e) {
-                        const float d = list_d[e * kThreads + tid];
-                        if (d <= F && d > theta) next = fminf(next, d);
-                    }
-                    for (int e = 0; e < cnt_b; ++e) {
-                        const float d = list_d[e * kThreads + tid_b];
-                        if (d <= F && d > theta) next = fminf(next, d);
-                    }
-                    if (next == __builtin_inff()) {
-                        ok = __fsub_rn(F, theta) > kTieEps;
-                        break;
-                    }
-                    if (__fsub_rn(next, theta) > kTieEps) break;
-                    theta = next;
-                    if (guard == 2 * kCap + 1) ok = false;
-                }
-                if (!ok) ++gap_fallbacks;
-            }
-        }
-        if (ok) {
+    uint32_t fallbacks = 0, chains = 0, done_rows = 0, final_cands = 0;
+    if (row_ok) {
+        if (direct) {
             const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
-            for (uint32_t s = 0; s < p.k; ++s) {
-                const bool live = s < keff;
-                p.out_ids[out + s] = live ? fin_g[s * kRowsPerBlock + slot_row] : kEmptyId;
-                p.out_dists[out + s] = live ? fin_d[s * kRowsPerBlock + slot_row] : kEmptyDist;
+            // lane h writes slots [16h, 16h + 16)
+#pragma unroll
+            for (int i = 0; i < kTop; ++i) {
+                if ((uint32_t)i >= p.k) continue;
+                if ((i >> 4) != (int)h) continue;
+                const bool live = (uint32_t)i < keff;
+                p.out_ids[out + i] = live ? sg[i] : kEmptyId;
+                p.out_dists[out + i] = live ? sd[i] : kEmptyDist;
             }
-            ++done_rows;
-        } else {
-            ++fallbacks;
-            const uint32_t idx = atomicAdd(p.fallback_count, 1u);
-            if (idx < p.fallback_capacity) {
-                p.fallback[2 * idx] = leaf;
-                p.fallback[2 * idx + 1] = r;
-            } else {
-                flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+            done_rows = h == 0u ? 1u : 0u;
+        } else if (h == 0u) {
+            bool queued = false;
+            const uint32_t m = (uint32_t)q_end + 1u;
+            if (chain) {
+                const uint32_t off = atomicAdd(p.chain_pool_used, m);
+                if (off + m <= p.chain_pool_capacity) {
+                    const uint32_t idx = atomicAdd(p.chain_count, 1u);
+                    if (idx < p.chain_capacity) {
+#pragma unroll
+                        for (int i = 0; i < 2 * kTop; ++i)
+                            if ((uint32_t)i < m) p.chain_pool[off + i] = make_uint2(__float_as_uint(sd[i]), sc[i]);
+                        p.chain_rows[idx] = make_uint4(leaf, r, off, m);
+                        queued = true;
+                        chains = 1;
+                        final_cands = m;
+                    }
+                }
+            }
+            if (!queued) {
+                fallbacks = 1;
+                const uint32_t idx = atomicAdd(p.fallback_count, 1u);
+                if (idx < p.fallback_capacity) {
+                    p.fallback[2 * idx] = leaf;
+                    p.fallback[2 * idx + 1] = r;
+                } else {
+                    flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+                }
             }
         }
     }
 
     // One atomic per counter per wave.
-    uint64_t s_surv = survivors, s_fc = final_cands, s_fb = fallbacks, s_gap = gap_fallbacks,
-             s_lo = list_ovf, s_done = done_rows;
+    uint64_t s_surv = survivors, s_fb = fallbacks, s_done = done_rows, s_ch = chains, s_fc = final_cands;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         s_surv += __shfl_xor(s_surv, off);
-        s_fc += __shfl_xor(s_fc, off);
         s_fb += __shfl_xor(s_fb, off);
-        s_gap += __shfl_xor(s_gap, off);
-        s_lo += __shfl_xor(s_lo, off);
         s_done += __shfl_xor(s_done, off);
+        s_ch += __shfl_xor(s_ch, off);
+        s_fc += __shfl_xor(s_fc, off);
     }
     if (lane == 0) {
         counter_add(p.counters, TESSA_C_LEAF_SURVIVORS, s_surv);
-        counter_add(p.counters, TESSA_C_LEAF_FINAL_CANDIDATES, s_fc);
         counter_add(p.counters, TESSA_C_LEAF_FALLBACK_ROWS, s_fb);
-        counter_add(p.counters, TESSA_C_LEAF_GAP_FALLBACK_ROWS, s_gap);
-        counter_add(p.counters, TESSA_C_LEAF_LIST_OVERFLOW_ROWS, s_lo);
+        counter_add(p.counters, TESSA_C_LEAF_GAP_FALLBACK_ROWS, s_fb);
+        counter_add(p.counters, TESSA_C_LEAF_CHAIN_ROWS, s_ch);
+        counter_add(p.counters, TESSA_C_LEAF_FINAL_CANDIDATES, s_fc);
         counter_add(p.counters, TESSA_C_LEAF_ROWS, s_done);
         counter_add(p.counters, TESSA_C_LEAF_REFINES, refines);
         counter_add(p.counters, TESSA_C_LEAF_MFMA_TILES, ntiles);

@@ -52,39 +52,57 @@ __global__ void fill_u32_kernel(uint32_t *p, uint32_t n, uint32_t v) {
     if (i < n) p[i] = v;
 }
 
-// Per-device workspace for the MFMA leaf path's fallback queue.  It grows on
-// demand and lives until the process ends (or tessa_session_destroy of the
-// last session does not free it: other callers may share the device).
+// Per-device workspace of the MFMA leaf path: the exact re-run queue (pairs
+// (leaf, row)), the chain queue (headers + candidate pool) and their three
+// counters.  Grown on demand; kept until the process ends (other callers may
+// share the device).
 struct DeviceWorkspace {
-    uint32_t *fallback = nullptr;  // pairs (leaf, row)
-    uint32_t *fallback_count = nullptr;
-    uint64_t capacity = 0;
+    uint32_t *queue_counts = nullptr;  // [0] fallback, [1] chain rows, [2] chain pool used
+    uint32_t *fallback = nullptr;
+    uint64_t fallback_capacity = 0;
+    uint4 *chain_rows = nullptr;
+    uint64_t chain_capacity = 0;
+    uint2 *chain_pool = nullptr;
+    uint64_t pool_capacity = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
 
-tessa_status get_workspace(uint64_t need_pairs, DeviceWorkspace **out) {
+template <typename T>
+tessa_status grow(T **ptr, uint64_t *cap, uint64_t need, size_t elem_bytes, const char *what) {
+    if (*cap >= need) return ok_status();
+    if (*ptr) {
+        TESSA_HIP_TRY(hipDeviceSynchronize());
+        TESSA_HIP_TRY(hipFree(*ptr));
+        *ptr = nullptr;
+        *cap = 0;
+    }
+    const uint64_t n = need < 4096 ? 4096 : need;
+    if (hipMalloc((void **)ptr, n * elem_bytes) != hipSuccess)
+        return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
+                           "%s allocation of %llu entries failed overflow_flags=0x%llx "
+                           "overflow_labels=WORKSPACE_BUDGET",
+                           what, (unsigned long long)n, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+    *cap = n;
+    return ok_status();
+}
+
+tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     int dev = 0;
     TESSA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
     DeviceWorkspace &ws = g_ws[dev];
-    if (ws.fallback_count == nullptr) TESSA_HIP_TRY(hipMalloc(&ws.fallback_count, 64));
-    if (ws.capacity < need_pairs) {
-        if (ws.fallback) {
-            TESSA_HIP_TRY(hipDeviceSynchronize());
-            TESSA_HIP_TRY(hipFree(ws.fallback));
-            ws.fallback = nullptr;
-            ws.capacity = 0;
-        }
-        uint64_t cap = need_pairs < 4096 ? 4096 : need_pairs;
-        if (hipMalloc(&ws.fallback, cap * 2 * sizeof(uint32_t)) != hipSuccess)
-            return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
-                               "fallback queue allocation of %llu pairs failed overflow_flags=0x%llx "
-                               "overflow_labels=WORKSPACE_BUDGET",
-                               (unsigned long long)cap, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
-        ws.capacity = cap;
-    }
+    if (ws.queue_counts == nullptr) TESSA_HIP_TRY(hipMalloc(&ws.queue_counts, 64));
+    tessa_status st = grow(&ws.fallback, &ws.fallback_capacity, rows, 2 * sizeof(uint32_t), "re-run queue");
+    if (st.code) return st;
+    // Chain rows are a fraction of all rows; a row that finds the chain queue
+    // full takes the exact re-run instead, so these sizes bound speed, not
+    // correctness.
+    st = grow(&ws.chain_rows, &ws.chain_capacity, rows / 2 + 1, sizeof(uint4), "chain queue");
+    if (st.code) return st;
+    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint2), "chain pool");
+    if (st.code) return st;
     *out = &ws;
     return ok_status();
 }
@@ -207,7 +225,7 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
     p.out_ids = out_ids;
     p.out_dists = out_dists;
     p.counters = counters;
-    p.list_cap_override = lb->debug_list_cap;
+    p.debug_rerun_every = lb->debug_rerun_every;
     const uint32_t exec = lb->executor;
     if (exec == TESSA_EXEC_EXACT) {
         if (launch_leaf_exact_all(p, s) != 0)
@@ -225,12 +243,20 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
     DeviceWorkspace *ws = nullptr;
     st = get_workspace((uint64_t)lb->leaf_count * lb->max_leaf_rows, &ws);
     if (st.code) return st;
+    auto clamp32 = [](uint64_t v) { return (uint32_t)(v < 0xffffffffull ? v : 0xffffffffull); };
     p.fallback = ws->fallback;
-    p.fallback_count = ws->fallback_count;
-    p.fallback_capacity = (uint32_t)(ws->capacity < 0xffffffffull ? ws->capacity : 0xffffffffull);
-    // Zero the queue counter with a kernel (capture-safe, unlike a memset node).
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->fallback_count, 1u, 0u);
+    p.fallback_count = ws->queue_counts;
+    p.fallback_capacity = clamp32(ws->fallback_capacity);
+    p.chain_rows = ws->chain_rows;
+    p.chain_count = ws->queue_counts + 1;
+    p.chain_capacity = clamp32(ws->chain_capacity);
+    p.chain_pool = ws->chain_pool;
+    p.chain_pool_used = ws->queue_counts + 2;
+    p.chain_pool_capacity = clamp32(ws->pool_capacity);
+    // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->queue_counts, 3u, 0u);
     if (launch_leaf_mfma(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "MFMA leaf kernel launch failed");
+    if (launch_leaf_chain(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "leaf chain kernel launch failed");
     if (launch_leaf_exact_fallback(p, s) != 0)
         return make_status(TESSA_ERR_HIP, 0, "leaf fallback kernel launch failed");
     return ok_status();

@@ -152,7 +152,7 @@ class LeafLayouts:
 def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k: int,
               executor: int = N.EXEC_MFMA, out_ids: torch.Tensor | None = None,
               out_dists: torch.Tensor | None = None, counters: torch.Tensor | None = None,
-              stream: torch.cuda.Stream | None = None, debug_list_cap: int = 0):
+              stream: torch.cuda.Stream | None = None, debug_rerun_every: int = 0):
     """Enqueue the leaf operator; returns (ids int32 view of u32, dists f32, counters int64)."""
     dev = sq8.codes.device
     if out_ids is None:
@@ -164,7 +164,7 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
     view = sq8.view(global_ids)
     lb = N.LeafBatch(_ptr(layouts.members), _ptr(layouts.member_offsets), _ptr(layouts.member_counts),
                      _ptr(layouts.output_offsets), layouts.leaf_count, layouts.max_leaf_rows, k, executor,
-                     debug_list_cap, 0)
+                     debug_rerun_every, 0)
     N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                      _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
     return out_ids, out_dists, counters

@@ -28,10 +28,10 @@ def dev_u32(a) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to("cuda:0")
 
 
-def run_leaf(sq8: T.Sq8Matrix, gids: np.ndarray, members, offsets, counts, k, executor, debug_list_cap=0):
+def run_leaf(sq8: T.Sq8Matrix, gids: np.ndarray, members, offsets, counts, k, executor, debug_rerun_every=0):
     lay = T.LeafLayouts.from_host(np.asarray(members, np.uint32), np.asarray(offsets, np.int64),
                                   np.asarray(counts, np.int64), k)
-    ids, d, ctr = T.leaf_topk(sq8, dev_u32(gids), lay, k, executor=executor, debug_list_cap=debug_list_cap)
+    ids, d, ctr = T.leaf_topk(sq8, dev_u32(gids), lay, k, executor=executor, debug_rerun_every=debug_rerun_every)
     torch.cuda.synchronize()
     T.raise_on_overflow(ctr, "leaf top-k")
     return (ids.cpu().numpy().view(np.uint32), d.cpu().numpy(), ctr.cpu().numpy())

@@ -146,12 +146,14 @@ def test_session_leaf_and_assign_host_arrays(gpu, orc):
         assert_same(ids, d, want_ids, want_d, "session leaf")
         assert ms.value > 0 and ctr[N.C_LEAF_ROWS] == 3000
         lead = np.arange(0, 3000, 50, dtype=np.uint32)
-        one = lambda v: np.array([v], np.uint32)  # noqa: E731
+        # keep every host array alive for the duration of the call
+        zero, m_cnt, l_cnt, rh = (np.array([v], np.uint32) for v in (0, 3000, len(lead), 2))
+        o_off = np.array([0], np.uint64)
         aids = np.zeros(3000 * 2, np.uint32)
         ad = np.zeros(3000 * 2, np.float32)
-        N.check(lib.tessa_session_assign_replay(h, p(members), p(lead), p(one(0)), p(one(3000)), p(one(0)),
-                                                p(one(len(lead))), p(one(2)), p(np.array([0], np.uint64)), 1,
-                                                p(aids), p(ad), p(ctr), C.byref(ms)), "session assign")
+        N.check(lib.tessa_session_assign_replay(h, p(members), p(lead), p(zero), p(m_cnt), p(zero), p(l_cnt),
+                                                p(rh), p(o_off), 1, p(aids), p(ad), p(ctr), C.byref(ms)),
+                "session assign")
         w_ids, w_d = orc.assign_replay(codes, scales, norms, gids, members, lead, [0], [3000], [0], [len(lead)], [2])
         assert_same(aids, ad, w_ids, w_d, "session assign")
         # invalid member ids are rejected with the reference's message tokens

@@ -85,7 +85,7 @@ def test_large_leaves_and_k_match_oracle(gpu, orc):
 
 
 def test_forced_exact_rerun_path_matches_oracle(gpu, orc):
-    # A tiny list capacity overflows every row: all rows take the exact re-run.
+    # The test knob sends every 4th / 20th row through the exact re-run kernel.
     sizes = [200, 513]
     n = sum(sizes)
     codes, scales, norms, gids = _gmm_case(orc, n, 64, seed=9)
@@ -94,7 +94,7 @@ def test_forced_exact_rerun_path_matches_oracle(gpu, orc):
     sq8 = to_dev_sq8(codes, scales, norms, 64)
     want_ids, want_d = orc.leaf_topk(codes, scales, norms, gids, members, offs, sizes, 32)
     for cap in (4, 20):
-        ids, d, ctr = run_leaf(sq8, gids, members, offs, sizes, 32, N.EXEC_MFMA, debug_list_cap=cap)
+        ids, d, ctr = run_leaf(sq8, gids, members, offs, sizes, 32, N.EXEC_MFMA, debug_rerun_every=cap)
         assert_same(ids, d, want_ids, want_d, f"cap={cap}")
         assert ctr[N.C_LEAF_FALLBACK_ROWS] > 0
         assert ctr[N.C_LEAF_ROWS] == n
