@@ -33,6 +33,8 @@
 //    so the comparator is a total order there: distance order, clusters
 //    ordered by global id.  Uncertified rows are queued for the exact scalar
 //    kernel.
+#include <type_traits>
+
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
@@ -48,7 +50,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerBlock = kWaves * 32;
 constexpr int kTileCols = 32;
 constexpr int kTop = 32;        // per-lane sorted list (registers)
-constexpr int kStage = 32;      // per-lane staging capacity (LDS)
+constexpr int kStageMax = 64;   // per-lane staging capacity limit (LDS)
 constexpr uint32_t kMaxLeafRows = 4096;
 constexpr float kFilterMargin = 3.0f * kTieEps;
 
@@ -56,14 +58,25 @@ template <int KS>
 struct Layout {
     static constexpr int kTileStride = KS * 32 + 16;  // bytes per LDS tile row (16 B pad: no bank aliasing)
     static constexpr int kTileBytes = kTileCols * kTileStride;
-    static constexpr int kMetaOff = kTileBytes;                   // scales[32], norms[32]
-    static constexpr int kMemOff = kMetaOff + 2 * kTileCols * 4;  // leaf member ids
-    static constexpr int kStageOff = kMemOff + (int)kMaxLeafRows * 4;
-    static constexpr int kBytes = kStageOff + kStage * kThreads * 8;
     static constexpr int kChunks = kTileCols * KS * 2;            // 16-byte chunks per tile
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
-    static_assert(kBytes <= 160 * 1024, "LDS budget");
 };
+
+constexpr uint32_t kLdsBudget = 160u * 1024u;
+
+// Staging entries per lane that fit next to the tile and the leaf-wide
+// member/scale/norm arrays (one slot is the sink for rejected candidates).
+__host__ __device__ constexpr uint32_t stage_capacity(uint32_t tile_bytes, uint32_t cols_cap) {
+    const uint32_t fixed = tile_bytes + cols_cap * 12u + 64u;
+    const uint32_t per = kThreads * 8u;
+    const uint32_t slots = fixed < kLdsBudget ? (kLdsBudget - fixed) / per : 0u;
+    const uint32_t cap = slots > 0u ? slots - 1u : 0u;
+    return cap > (uint32_t)kStageMax ? (uint32_t)kStageMax : cap;
+}
+
+__host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
+    return tile_bytes + cols_cap * 12u + 64u + (stage_capacity(tile_bytes, cols_cap) + 1u) * kThreads * 8u;
+}
 
 // Compare-exchange on (key, payload) pairs; ascending when `up`.
 __device__ __forceinline__ void cex(float &a, uint32_t &pa, float &b, uint32_t &pb, bool up) {
@@ -122,8 +135,10 @@ __device__ __forceinline__ float pair_kth32(const float (&a)[kTop]) {
     return fminf(best, a[kTop - 1]);
 }
 
-// Fold `staged` LDS entries of this lane into its sorted top-32.
-__device__ __forceinline__ void fold_staged(const uint2 *stage, uint32_t tid, int staged, float (&topd)[kTop],
+// Fold `staged` LDS entries (raw dot, column) of this lane into its sorted
+// top-32: exact distances are computed here, for staged candidates only.
+__device__ __forceinline__ void fold_staged(const uint2 *stage, const float *cs, const float *cn, uint32_t tid,
+                                            int staged, float rs, float rn, float (&topd)[kTop],
                                             uint32_t (&topc)[kTop], float &disc) {
     const int chunks = (wave_max_i(staged) + 15) / 16;
     for (int ch = 0; ch < chunks; ++ch) {
@@ -132,9 +147,15 @@ __device__ __forceinline__ void fold_staged(const uint2 *stage, uint32_t tid, in
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int e = ch * 16 + i;
-            const uint2 s = e < staged ? stage[e * kThreads + tid] : make_uint2(0x7f800000u, 0xffffu);
-            v[i] = __uint_as_float(s.x);
-            c[i] = s.y;
+            float d = __builtin_inff();
+            uint32_t col = 0xffffu;
+            if (e < staged) {
+                const uint2 s = stage[e * kThreads + tid];
+                col = s.y;
+                d = leaf_l2((int)s.x, rs, rn, cs[col], cn[col]);
+            }
+            v[i] = d;
+            c[i] = col;
         }
         bitonic_sort_kv<16>(v, c);
         // lower half of (top ascending) vs (chunk ascending, padded to 32, reversed)
@@ -150,16 +171,30 @@ __device__ __forceinline__ void fold_staged(const uint2 *stage, uint32_t tid, in
     }
 }
 
+// Necessary condition for a candidate to pass d <= F, as a bound on cs * dot:
+// d <= F implies 2*rs*cs*dot >= rn + cn - F - err >= rn + cn_min - F - err,
+// with err covering the f32 roundings of d (computed in double, lowered).
+__device__ __forceinline__ float filter_bound(float F, float rs, float rn, float cn_min, float cn_max) {
+    if (!(F < __builtin_inff())) return -__builtin_inff();
+    const double err = 1.0e-6 * ((double)fabsf(rn) + (double)cn_max + (double)F) + 1.0e-30;
+    const double tau = ((double)rn + (double)cn_min - (double)F - err) / (2.0 * (double)rs);
+    return (float)(tau - fabs(tau) * 2.0e-6 - 1.0e-30);
+}
+
 template <int KS>
 __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
                                                               uint32_t total_work, uint32_t padded_grid) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    // Runtime layout: tile | members | scales | norms | misc | staging.
+    const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
+    const int stage_cap = (int)stage_capacity(L::kTileBytes, cols_cap);
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
-    float *meta_s = reinterpret_cast<float *>(smem + L::kMetaOff);
-    float *meta_n = meta_s + kTileCols;
-    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kMemOff);
-    uint2 *stage = reinterpret_cast<uint2 *>(smem + L::kStageOff);
+    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kTileBytes);
+    float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
+    float *cn_lds = cs_lds + cols_cap;
+    uint32_t *misc = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);
+    uint2 *stage = reinterpret_cast<uint2 *>(misc + 16);
 
     // XCD-aware order: blocks are dispatched round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of work items (the row blocks of one
@@ -180,16 +215,34 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     const uint32_t pd = p.padded_dim;
     const uint32_t tid = threadIdx.x;
 
-    // Leaf member ids once in LDS (tile loads then need one global hop, not two).
-    for (uint32_t c = tid; c < n; c += kThreads) {
-        uint32_t mc = mem[c];
-        if (mc >= p.rows) {
-            flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
-            mc = 0u;
-        }
-        mem_lds[c] = mc;
+    // Leaf member ids, scales and norms once in LDS; min/max norm of the leaf.
+    if (tid == 0) {
+        misc[0] = 0x7f800000u;  // +inf bits: min norm
+        misc[1] = 0u;           // max norm
     }
     __syncthreads();
+    {
+        float lo = __builtin_inff(), hi = 0.0f;
+        for (uint32_t c = tid; c < n; c += kThreads) {
+            uint32_t mc = mem[c];
+            if (mc >= p.rows) {
+                flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+                mc = 0u;
+            }
+            mem_lds[c] = mc;
+            const float cn = p.norms[mc];
+            cs_lds[c] = p.scales[mc];
+            cn_lds[c] = cn;
+            lo = fminf(lo, cn);
+            hi = fmaxf(hi, cn);
+        }
+        // norms are sums of squares (>= 0): their bit patterns order like the values
+        atomicMin(&misc[0], __float_as_uint(lo));
+        atomicMax(&misc[1], __float_as_uint(hi));
+    }
+    __syncthreads();
+    const float cn_min = __uint_as_float(misc[0]);
+    const float cn_max = __uint_as_float(misc[1]);
 
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
@@ -197,6 +250,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     const uint32_t h = lane >> 5;
     const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
     const bool row_ok = r < n;
+    const bool wave_rows_full = row_base + wave * 32u + 32u <= n;
     const uint32_t mr = row_ok ? mem_lds[r] : 0u;
 
     // Row codes for the whole K range (B operand), zero past padded_dim.
@@ -211,8 +265,8 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
             bfrag[s] = z;
         }
     }
-    const float rs = row_ok ? p.scales[mr] : 0.0f;
-    const float rn = row_ok ? p.norms[mr] : 0.0f;
+    const float rs = row_ok ? cs_lds[r] : 1.0f;
+    const float rn = row_ok ? cn_lds[r] : 0.0f;
 
     float topd[kTop];
     uint32_t topc[kTop];
@@ -221,14 +275,15 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
         topd[i] = __builtin_inff();
         topc[i] = 0xffffu;
     }
-    float F = __builtin_inff();   // filter threshold (running 32nd + margin)
-    float disc = __builtin_inff(); // smallest distance this lane dropped
+    float F = __builtin_inff();      // filter threshold (running pair 32nd + margin)
+    float tau = -__builtin_inff();   // cs * dot bound implied by F
+    float disc = __builtin_inff();   // smallest distance evicted from this lane's list
     int staged = 0;
     uint32_t survivors = 0, refines = 0;
 
     const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
+    const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
     v4i pre[L::kChunksPerThread];
-    float pre_meta = 0.0f;
 
     auto load_tile = [&](uint32_t t) {
 #pragma unroll
@@ -244,13 +299,6 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
             }
             pre[q] = z;
         }
-        // threads 0..31 carry scales, 32..63 norms of the tile's columns
-        if (tid < 2u * kTileCols) {
-            const uint32_t c = t * kTileCols + (tid & 31u);
-            float v = 0.0f;
-            if (c < n) v = (tid < 32u) ? p.scales[mem_lds[c]] : p.norms[mem_lds[c]];
-            pre_meta = v;
-        }
     };
 
     load_tile(0);
@@ -265,7 +313,6 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
                 *reinterpret_cast<v4i *>(tile + row * L::kTileStride + off) = pre[q];
             }
         }
-        if (tid < 2u * kTileCols) meta_s[tid] = pre_meta;  // meta_n follows meta_s
         __syncthreads();
         if (t + 1 < ntiles) load_tile(t + 1);
 
@@ -277,84 +324,109 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
         }
 
-        // Epilogue: exact distances, threshold filter, stage or drop.
+        // Epilogue: necessary-condition filter cs*dot >= tau, stage (dot, col)
+        // branch-free (a rejected candidate goes to the sink slot).  Only the
+        // diagonal tile (self columns), the last tile (columns past n) and
+        // partially filled row groups need per-candidate validity checks; the
+        // choice is wave-uniform.
         const uint32_t cbase = t * kTileCols;
+        const bool checked =
+            __builtin_amdgcn_readfirstlane((t == diag_tile || cbase + kTileCols > n || !wave_rows_full) ? 1 : 0);
+        auto epilogue = [&](auto check_tag) {
+            constexpr bool kCheck = decltype(check_tag)::value;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 cs4 = *reinterpret_cast<const float4 *>(meta_s + 8 * q + 4 * h);
-            const float4 cn4 = *reinterpret_cast<const float4 *>(meta_n + 8 * q + 4 * h);
-            const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-            const float cnv[4] = {cn4.x, cn4.y, cn4.z, cn4.w};
+            for (int q = 0; q < 4; ++q) {
+                const float4 cs4 = *reinterpret_cast<const float4 *>(cs_lds + cbase + 8 * q + 4 * h);
+                const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int v = 4 * q + e;
-                const uint32_t c = cbase + 8u * q + 4u * h + e;
-                const float d = leaf_l2(acc[v], rs, rn, csv[e], cnv[e]);
-                const bool valid = row_ok && c < n && c != r;
-                const bool take = valid && d <= F;
-                if (take) {
-                    stage[staged * kThreads + tid] = make_uint2(__float_as_uint(d), c);
-                    ++staged;
-                    ++survivors;
+                for (int e = 0; e < 4; ++e) {
+                    const int v = 4 * q + e;
+                    const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
+                    bool take = __fmul_rn((float)acc[v], csv[e]) >= tau;
+                    if (kCheck) take = take && row_ok && c < n && c != r;
+                    const int slot = take ? staged : stage_cap;
+                    stage[slot * kThreads + tid] = make_uint2((uint32_t)acc[v], c);
+                    staged += take ? 1 : 0;
                 }
-                disc = (valid && !take) ? fminf(disc, d) : disc;
             }
-        }
+        };
+        if (checked) epilogue(std::true_type{});
+        else epilogue(std::false_type{});
 
         // Fold staged candidates before the next tile could overflow staging.
-        if (__any(staged > kStage - 16)) {
+        if (__any(staged > stage_cap - 16)) {
             ++refines;
-            fold_staged(stage, tid, staged, topd, topc, disc);
+            survivors += (uint32_t)staged;
+            fold_staged(stage, cs_lds, cn_lds, tid, staged, rs, rn, topd, topc, disc);
             staged = 0;
             F = __fadd_rn(pair_kth32(topd), kFilterMargin);
+            tau = row_ok ? filter_bound(F, rs, rn, cn_min, cn_max) : __builtin_inff();
         }
     }
     // ---- final: merge the pair's lists, certify, order, write ---------------
-    if (__any(staged > 0)) fold_staged(stage, tid, staged, topd, topc, disc);
+    survivors += (uint32_t)staged;
+    if (__any(staged > 0)) fold_staged(stage, cs_lds, cn_lds, tid, staged, rs, rn, topd, topc, disc);
 
-    float sd[2 * kTop];
-    uint32_t sc[2 * kTop];
+    // Known sequence: the pair's 32 smallest sorted (positions 0..31) and the
+    // 8 smallest of the rest (32..39).  Everything not known is > min(disc, F).
+    constexpr int kSeq = kTop + 8;
+    float sd[kSeq];
+    uint32_t sc[kSeq];
     {
-        float bd[kTop];
-        uint32_t bc[kTop];
+        float hi[kTop];
+        uint32_t phi[kTop];
+        {
+            float bd[kTop];
+            uint32_t bc[kTop];
 #pragma unroll
-        for (int m = 0; m < kTop; ++m) {
-            bd[m] = __shfl_xor(topd[m], 32);
-            bc[m] = __shfl_xor(topc[m], 32);
-        }
-        // (own ascending) x (partner ascending, reversed): lower halves hold the
-        // 32 smallest, upper halves the rest; both bitonic.
+            for (int m = 0; m < kTop; ++m) {
+                bd[m] = __shfl_xor(topd[m], 32);
+                bc[m] = __shfl_xor(topc[m], 32);
+            }
 #pragma unroll
-        for (int i = 0; i < kTop; ++i) {
-            const float a = topd[i], b = bd[kTop - 1 - i];
-            const bool sw = b < a;
-            sd[i] = sw ? b : a;
-            sc[i] = sw ? bc[kTop - 1 - i] : topc[i];
-            sd[kTop + i] = sw ? a : b;
-            sc[kTop + i] = sw ? topc[i] : bc[kTop - 1 - i];
+            for (int i = 0; i < kTop; ++i) {
+                const float a = topd[i], b = bd[kTop - 1 - i];
+                const bool sw = b < a;
+                sd[i] = sw ? b : a;
+                sc[i] = sw ? bc[kTop - 1 - i] : topc[i];
+                hi[i] = sw ? a : b;
+                phi[i] = sw ? topc[i] : bc[kTop - 1 - i];
+            }
         }
-    }
-    {
-        float lo[kTop], hi[kTop];
-        uint32_t plo[kTop], phi[kTop];
+        float lo[kTop];
+        uint32_t plo[kTop];
 #pragma unroll
         for (int i = 0; i < kTop; ++i) {
             lo[i] = sd[i];
             plo[i] = sc[i];
-            hi[i] = sd[kTop + i];
-            phi[i] = sc[kTop + i];
         }
         bitonic_merge_kv<kTop>(lo, plo);
-        bitonic_merge_kv<kTop>(hi, phi);
 #pragma unroll
         for (int i = 0; i < kTop; ++i) {
             sd[i] = lo[i];
             sc[i] = plo[i];
+        }
+        // half-cleaners keep the lower half of a bitonic sequence: 32 -> 16 -> 8,
+        // then a bitonic merge sorts those 8
+#pragma unroll
+        for (int w = 16; w >= 8; w >>= 1) {
+#pragma unroll
+            for (int i = 0; i < w; ++i) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
+        }
+#pragma unroll
+        for (int w = 4; w >= 1; w >>= 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if ((i & w) == 0) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
             sd[kTop + i] = hi[i];
             sc[kTop + i] = phi[i];
         }
     }
-    const float disc_all = fminf(disc, __shfl_xor(disc, 32));
+    // dropped on arrival: d > F (F never increases); evicted: >= disc
+    const float disc_all = fminf(fminf(disc, __shfl_xor(disc, 32)), F);
 
     const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
     // Tie clusters over the sorted known sequence.
@@ -362,10 +434,10 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     bool extending = keff > 0u;
     bool clique_bad = false;
     float cstart = sd[0];
-    uint32_t cid[2 * kTop];
+    uint32_t cid[kSeq];
     cid[0] = 0;
 #pragma unroll
-    for (int i = 1; i < 2 * kTop; ++i) {
+    for (int i = 1; i < kSeq; ++i) {
         const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
         cid[i] = tie ? cid[i - 1] : (uint32_t)i;
         const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
@@ -383,7 +455,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
         float theta = sd[0];
         float next = disc_all;
 #pragma unroll
-        for (int i = 1; i < 2 * kTop; ++i) {
+        for (int i = 1; i < kSeq; ++i) {
             theta = (i == q_end) ? sd[i] : theta;  // static indices only: no scratch
             next = (i == q_end + 1) ? fminf(next, sd[i]) : next;
         }
@@ -398,20 +470,20 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
     const bool chain = gap_ok && clique_bad;
 
     // Global ids of G's positions, then order each cluster by global id.
-    uint32_t sg[2 * kTop];
+    uint32_t sg[kSeq];
 #pragma unroll
-    for (int i = 0; i < 2 * kTop; ++i)
+    for (int i = 0; i < kSeq; ++i)
         sg[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? p.gids[mem_lds[sc[i]]] : kEmptyId;
     bool need_sort = false;
 #pragma unroll
-    for (int i = 1; i < 2 * kTop; ++i) need_sort |= (i <= q_end) && (cid[i] == cid[i - 1]);
+    for (int i = 1; i < kSeq; ++i) need_sort |= (i <= q_end) && (cid[i] == cid[i - 1]);
     if (__any(row_ok && direct && need_sort)) {
         // odd-even transposition sort by global id inside each cluster of G
         // (sorted once an even and an odd phase in a row swap nothing)
-        for (int pass = 0; pass < 2 * kTop + 2; pass += 2) {
+        for (int pass = 0; pass < kSeq + 2; pass += 2) {
             bool swapped = false;
 #pragma unroll
-            for (int i = 0; i + 1 < 2 * kTop; i += 2) {
+            for (int i = 0; i + 1 < kSeq; i += 2) {
                 const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
                 const uint32_t ga = sg[i], gb = sg[i + 1];
                 const float da = sd[i], db = sd[i + 1];
@@ -422,7 +494,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
                 swapped |= sw;
             }
 #pragma unroll
-            for (int i = 1; i + 1 < 2 * kTop; i += 2) {
+            for (int i = 1; i + 1 < kSeq; i += 2) {
                 const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
                 const uint32_t ga = sg[i], gb = sg[i + 1];
                 const float da = sd[i], db = sd[i + 1];
@@ -459,7 +531,7 @@ __global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, ui
                     const uint32_t idx = atomicAdd(p.chain_count, 1u);
                     if (idx < p.chain_capacity) {
 #pragma unroll
-                        for (int i = 0; i < 2 * kTop; ++i)
+                        for (int i = 0; i < kSeq; ++i)
                             if ((uint32_t)i < m) p.chain_pool[off + i] = make_uint2(__float_as_uint(sd[i]), sc[i]);
                         p.chain_rows[idx] = make_uint4(leaf, r, off, m);
                         queued = true;
@@ -508,18 +580,20 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     using L = Layout<KS>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes) != hipSuccess)
+        if (hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kLdsBudget) != hipSuccess)
             return -1;
         attr_set = true;
     }
+    const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
+    if (stage_capacity(L::kTileBytes, cols_cap) < 32u) return -4;  // leaf too large for this dim
     const uint32_t blocks_per_leaf = (p.max_leaf_rows + kRowsPerBlock - 1) / kRowsPerBlock;
     const uint64_t total = (uint64_t)blocks_per_leaf * p.leaf_count;
     if (total == 0) return 0;
     if (total > 0x7fffff00ull) return -2;
     const uint32_t padded = (uint32_t)((total + 7) / 8 * 8);
-    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(padded), dim3(kThreads), L::kBytes, stream, p,
-                       blocks_per_leaf, (uint32_t)total, padded);
+    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(padded), dim3(kThreads), lds_bytes(L::kTileBytes, cols_cap),
+                       stream, p, blocks_per_leaf, (uint32_t)total, padded);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
