@@ -224,6 +224,127 @@ tessa_status tessa_session_assign_replay(tessa_session *session, const uint32_t 
                                          uint32_t *out_ids, float *out_dists,
                                          uint64_t *counters, float *event_ms);
 
+/* ---- resident subtree: recursive partition + leaf top-k -----------------
+ * Replaces PiPNNComputeBackend::process_quantized_subtree_l2_compact_topk
+ * (compute_backend.rs:3794-3805; request GpuSubtreePartitionRequest
+ * :1818-1826, result GpuSubtreeTopKResult :1945-1951) as executed by
+ * gpu_persistent_subtree_topk (:16336-17380) after plan_gpu_persistent_subtree
+ * (:1309-1488).  The session's uploaded SQ8 rows are the resident subtree
+ * (local row r = upload row r, global id = global_ids[r]). */
+
+/* Counter words of a subtree run, at the reference's indices
+ * (compute_backend.rs:5028-5187).  Words with no counterpart in this
+ * implementation (queue heads, polls, locks, clocks) stay 0. */
+#define TESSA_SUBTREE_COUNTER_WORDS 159
+enum tessa_subtree_counter {
+    TESSA_P_OVERFLOW_FLAGS = 7,
+    TESSA_P_PARTITION_POPS = 8,
+    TESSA_P_OUTPUT_ROWS = 12,
+    TESSA_P_OUTPUT_LEAF_COUNT = 13,
+    TESSA_P_ASSIGNMENT_PASSES = 14,
+    TESSA_P_MAX_ACTIVE = 15,
+    TESSA_P_EFFECTIVE_ROOT_FANOUT = 17,
+    TESSA_P_EFFECTIVE_DEEPER_FANOUT = 18,
+    TESSA_P_FANOUT_ASSIGNMENT_SLOTS = 19,
+    TESSA_P_REPLICATED_ROWS = 20,
+    TESSA_P_UNIQUE_RESIDENT_ROWS = 21,
+    TESSA_P_LARGE_NODE_CLAIMS = 27,
+    TESSA_P_LARGE_NODE_SPLITS = 28,
+    TESSA_P_LARGE_NODE_ROWS = 29,
+    TESSA_P_LARGE_NODE_MAX_ROWS = 30,
+    TESSA_P_LEAF_SIZE_MIN = 33,
+    TESSA_P_LEAF_SIZE_MAX = 34,
+    TESSA_P_LEAF_SIZE_SUM = 35,
+    TESSA_P_LEAF_SIZE_COUNT = 36,
+    TESSA_P_PARTITION_LEVEL_ROUNDS = 119,
+    TESSA_P_LARGE_SPLIT_RETRIES = 130,
+    TESSA_P_LARGE_BALANCED_FALLBACKS = 131,
+    TESSA_P_LARGE_PHYSICAL_TILES = 145,
+    TESSA_P_LEAF_SQ8_WMMA_TILES = 158
+};
+
+/* plan_gpu_persistent_subtree (compute_backend.rs:1309-1488): capacities and
+ * admission.  required_bytes is this implementation's device workspace plus
+ * outputs; the fallback reasons keep the reference's bits. */
+/* GPU_PERSISTENT_FALLBACK_REASON_* (compute_backend.rs:375-383) */
+#define TESSA_PLAN_FALLBACK_UNSUPPORTED_K       (1u << 2)
+#define TESSA_PLAN_FALLBACK_UNSUPPORTED_FANOUT  (1u << 3)
+#define TESSA_PLAN_FALLBACK_UNSUPPORTED_LEADERS (1u << 4)
+#define TESSA_PLAN_FALLBACK_WORKSPACE           (1u << 5)
+typedef struct tessa_subtree_plan {
+    int32_t supported;
+    uint32_t fallback_reason_flags;
+    uint64_t overflow_flags;
+    uint32_t leaf_min;            /* 64 (GPU_PERSISTENT_LEAF_MIN) */
+    uint32_t leaf_target;         /* 128 */
+    uint32_t leaf_max;            /* max(256, c_max) */
+    uint32_t small_node_limit;    /* 4096 */
+    uint32_t effective_root_fanout;
+    uint32_t effective_deeper_fanout;
+    uint32_t fanout_amplification;
+    uint32_t large_child_slots;   /* 128 */
+    uint64_t max_queue_nodes;
+    uint64_t max_leaf_count;      /* capacity of leaf_starts / leaf_sizes */
+    uint64_t max_leaf_rows;       /* capacity of leaf_row_ids; top-k rows */
+    uint64_t large_scratch_rows;
+    uint64_t required_bytes;
+    uint64_t budget_bytes;
+} tessa_subtree_plan;
+
+tessa_status tessa_plan_subtree(uint64_t resident_rows, uint32_t leaf_knn,
+                                uint32_t max_leaders_per_node, uint32_t max_fanout,
+                                uint64_t budget_bytes /* 0 = unlimited */, uint32_t c_max,
+                                tessa_subtree_plan *plan);
+
+/* gpu_queue_root_seed (compute_backend.rs:1597-1603). */
+uint64_t tessa_subtree_root_seed(uint64_t random_seed, uint64_t depth, uint64_t point_count,
+                                 uint64_t parent_points, uint64_t min_recurse_size);
+
+typedef struct tessa_subtree_request {
+    const uint32_t *root_leaders;  /* host array of resident row ids, or NULL */
+    uint32_t root_leader_count;    /* <= min(max_leaders, 128) */
+    uint32_t root_depth;           /* request.depth */
+    uint64_t seed;                 /* tessa_subtree_root_seed(...) */
+    uint32_t leaf_knn;             /* 1..32 (k = min(leaf_knn, rows-1)) */
+    uint32_t fanout_second;        /* 1..4, root-level replication */
+    uint32_t max_depth;
+    uint32_t max_leaders;          /* params.max_leaders */
+    uint32_t leaf_min;             /* plan.leaf_min */
+    uint32_t leaf_max;             /* plan.leaf_max (<= 4096 for the top-k) */
+    uint32_t small_node_limit;     /* plan.small_node_limit */
+    float psamp_fraction;          /* params.psamp_fraction as f32 */
+    uint32_t executor;             /* TESSA_EXEC_MFMA or TESSA_EXEC_EXACT */
+    uint32_t partition_only;       /* 1: leaves only, no top-k */
+    uint64_t max_leaf_count;       /* output capacities (plan values) */
+    uint64_t max_leaf_rows;
+} tessa_subtree_request;
+
+/* Device output buffers (caller-owned, sized from the plan) and results.
+ * Leaf l holds leaf_row_ids[leaf_starts[l] .. + leaf_sizes[l]] (resident row
+ * ids); the top-k of its member row r is at (leaf_starts[l] + r) * k + rank,
+ * k = min(leaf_knn, rows - 1), unused slots (0xffffffff, FLT_MAX).  Leaves
+ * are numbered level by level, each node's children in leader-slot order,
+ * and the rows of every leaf are ascending (one legal order of the
+ * reference's concurrent walk, which has none fixed). */
+typedef struct tessa_subtree_output {
+    uint32_t *leaf_row_ids;        /* device, max_leaf_rows */
+    uint64_t *leaf_starts;         /* device, max_leaf_count */
+    uint64_t *leaf_sizes;          /* device, max_leaf_count */
+    uint32_t *topk_ids;            /* device, max_leaf_rows * k (unused if partition_only) */
+    float *topk_dists;
+    uint64_t *counters;            /* host, TESSA_SUBTREE_COUNTER_WORDS, may be NULL */
+    uint64_t *leaf_counters;       /* host, TESSA_COUNTER_WORDS, may be NULL */
+    uint64_t leaf_count;           /* out */
+    uint64_t leaf_rows;            /* out */
+    uint32_t k;                    /* out: top-k row stride */
+    uint32_t levels;               /* out: partition levels walked */
+    float partition_ms;            /* out: hipEvent time of the partition */
+    float leaf_ms;                 /* out: hipEvent time of the leaf top-k */
+} tessa_subtree_output;
+
+tessa_status tessa_session_run_subtree(tessa_session *session, const tessa_subtree_request *req,
+                                       tessa_subtree_output *out);
+
 /* "QUEUE_NODE|LEAF_ROW|..." or "none" (same labels as the reference). */
 void tessa_overflow_labels(uint64_t flags, char *buf, size_t len);
 uint32_t tessa_abi_version(void);

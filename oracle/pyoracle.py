@@ -61,7 +61,45 @@ def lib():
             fn = getattr(_lib, name)
             fn.restype = C.c_int
             fn.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, P, P, P, P, C.c_size_t, P, P, C.c_int]
+        _lib.orc_assign_before.restype = C.c_int
+        _lib.orc_assign_before.argtypes = [C.c_float, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]
+        _lib.orc_adaptive_psamp.restype = C.c_float
+        _lib.orc_adaptive_psamp.argtypes = [C.c_float, C.c_uint32, C.c_uint32]
+        _lib.orc_meaningful_split.restype = C.c_int
+        _lib.orc_meaningful_split.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
+        _lib.orc_sort_unique.restype = None
+        _lib.orc_sort_unique.argtypes = [P, P]
+        _lib.orc_sample_retry_leaders.restype = None
+        _lib.orc_sample_retry_leaders.argtypes = [P, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint32, P]
+        _lib.orc_hash_rank_leaders.restype = None
+        _lib.orc_hash_rank_leaders.argtypes = [P, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint32, C.c_uint32, P]
+        _lib.orc_subtree_root_seed.restype = C.c_uint64
+        _lib.orc_subtree_root_seed.argtypes = [C.c_uint64] * 5
+        _lib.orc_subtree_partition.restype = C.c_int
+        _lib.orc_subtree_partition.argtypes = [P, P, P, C.c_size_t, C.c_size_t, C.POINTER(SubtreeCfg), P, P, P,
+                                               P, P, P]
     return _lib
+
+
+class SubtreeCfg(C.Structure):
+    """orc_subtree_cfg (tessa_oracle.h)."""
+
+    _fields_ = [
+        ("root_leaders", C.c_void_p),
+        ("root_leader_count", C.c_uint32),
+        ("root_depth", C.c_uint32),
+        ("max_depth", C.c_uint32),
+        ("max_leaders", C.c_uint32),
+        ("fanout_second", C.c_uint32),
+        ("leaf_min", C.c_uint32),
+        ("leaf_max", C.c_uint32),
+        ("small_node_limit", C.c_uint32),
+        ("large_scratch_rows", C.c_uint64),
+        ("max_leaf_count", C.c_uint64),
+        ("max_leaf_rows", C.c_uint64),
+        ("psamp_fraction", C.c_float),
+        ("seed", C.c_uint64),
+    ]
 
 
 def _p(a: np.ndarray):
@@ -191,3 +229,79 @@ def hash64(x: int) -> int:
 
 def assign_tie_key(point: int, leader: int) -> int:
     return int(lib().orc_assign_tie_key(point, leader))
+
+
+def assign_before(d: float, point: int, leader: int, od: float, oleader: int) -> bool:
+    return bool(lib().orc_assign_before(d, point, leader, od, oleader))
+
+
+def adaptive_psamp(base: float, n: int, depth: int) -> np.float32:
+    return np.float32(lib().orc_adaptive_psamp(base, n, depth))
+
+
+def meaningful_split(parent: int, max_child: int, terminal: int) -> bool:
+    return bool(lib().orc_meaningful_split(parent, max_child, terminal))
+
+
+def sort_unique(v) -> np.ndarray:
+    a = np.ascontiguousarray(v, np.uint32).copy()
+    n = C.c_uint32(len(a))
+    lib().orc_sort_unique(_p(a), C.byref(n))
+    return a[: n.value]
+
+
+def sample_retry_leaders(rows, num_leaders: int, seed: int, attempt: int) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, np.uint32)
+    out = np.zeros(num_leaders, np.uint32)
+    lib().orc_sample_retry_leaders(_p(rows), len(rows), num_leaders, seed, attempt, _p(out))
+    return out
+
+
+def hash_rank_leaders(pts, num_leaders: int, seed: int, attempt: int, depth: int) -> np.ndarray:
+    pts = np.ascontiguousarray(pts, np.uint32)
+    out = np.zeros(num_leaders, np.uint32)
+    lib().orc_hash_rank_leaders(_p(pts), len(pts), num_leaders, seed, attempt, depth, _p(out))
+    return out
+
+
+def subtree_root_seed(random_seed: int, depth: int, point_count: int, parent_points: int,
+                      min_recurse_size: int) -> int:
+    return int(lib().orc_subtree_root_seed(random_seed, depth, point_count, parent_points, min_recurse_size))
+
+
+COUNTER_WORDS = 159
+
+
+def subtree_partition(codes, scales, norms, *, seed: int, root_depth: int = 0, max_depth: int = 10,
+                      max_leaders: int = 128, fanout_second: int = 1, leaf_min: int = 64, leaf_max: int = 256,
+                      small_node_limit: int = 4096, psamp_fraction: float = 0.001, root_leaders=None,
+                      large_scratch_rows: int | None = None, max_leaf_count: int | None = None,
+                      max_leaf_rows: int | None = None):
+    """-> (leaves: list of u32 arrays (resident rows, in order), counters u64[159])."""
+    codes = np.ascontiguousarray(codes, np.int8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    norms = np.ascontiguousarray(norms, np.float32)
+    rows, pd = codes.shape
+    famp = max(1, min(fanout_second, 4))
+    roots = np.zeros(0, np.uint32) if root_leaders is None else np.ascontiguousarray(root_leaders, np.uint32)
+    mlr = max_leaf_rows if max_leaf_rows is not None else max(rows * famp, 1)
+    mlc = max_leaf_count if max_leaf_count is not None else max(rows * famp, 1)
+    cfg = SubtreeCfg(roots.ctypes.data if len(roots) else None, len(roots), root_depth, max_depth, max_leaders,
+                     fanout_second, leaf_min, leaf_max, small_node_limit,
+                     large_scratch_rows if large_scratch_rows is not None else max(rows, 1) * famp,
+                     mlc, mlr, np.float32(psamp_fraction).item(), seed & (2**64 - 1))
+    leaf_rows = np.zeros(max(mlr, 1), np.uint32)
+    starts = np.zeros(max(mlc, 1), np.uint64)
+    sizes = np.zeros(max(mlc, 1), np.uint64)
+    ctr = np.zeros(COUNTER_WORDS, np.uint64)
+    lc = C.c_uint64(0)
+    lr = C.c_uint64(0)
+    rc = lib().orc_subtree_partition(_p(codes), _p(scales), _p(norms), rows, pd, C.byref(cfg), _p(leaf_rows),
+                                     _p(starts), _p(sizes), _p(ctr), C.byref(lc), C.byref(lr))
+    if rc != 0:
+        raise ValueError(f"orc_subtree_partition failed: {rc}")
+    n_leaves = min(lc.value, mlc)
+    if ctr[7] != 0:
+        return None, ctr
+    leaves = [leaf_rows[int(starts[i]): int(starts[i]) + int(sizes[i])].copy() for i in range(n_leaves)]
+    return leaves, ctr

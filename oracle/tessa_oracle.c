@@ -305,7 +305,7 @@ uint64_t orc_assign_tie_key(uint32_t point, uint32_t leader) {
     return orc_hash64((((uint64_t)point) << 32) ^ (uint64_t)leader ^ 0x9e3779b97f4a7c15ull);
 }
 
-static int assign_before(float d, uint32_t point, uint32_t leader, float od,
+int orc_assign_before(float d, uint32_t point, uint32_t leader, float od,
                          uint32_t oleader) {
     /* compute_backend.rs:6541-6568: eps tie -> (tie key, leader) order */
     if (fabsf(d - od) <= ORC_TIE_EPS) {
@@ -364,9 +364,9 @@ int orc_assign_replay(const int8_t *codes, const float *scales,
                 int32_t dot = orc_sq8_dot(codes + (size_t)p * padded_dim,
                                           codes + (size_t)l * padded_dim, padded_dim);
                 float d = orc_sq8_assign_l2(dot, scales[p], norms[p], scales[l], norms[l]);
-                if (!assign_before(d, p, l, bd[3], bl[3])) continue;
+                if (!orc_assign_before(d, p, l, bd[3], bl[3])) continue;
                 uint32_t pos = 3;
-                while (pos > 0 && assign_before(d, p, l, bd[pos - 1], bl[pos - 1])) {
+                while (pos > 0 && orc_assign_before(d, p, l, bd[pos - 1], bl[pos - 1])) {
                     bd[pos] = bd[pos - 1];
                     bs[pos] = bs[pos - 1];
                     bl[pos] = bl[pos - 1];

@@ -127,6 +127,95 @@ int orc_assign_strict(const int8_t *codes, const float *scales,
                       const uint64_t *output_offsets, size_t task_count,
                       uint32_t *out_ids, float *out_dists, int threads);
 
+/* compute_backend.rs:6541-6568: does (d, leader) go before (od, oleader)
+ * for this point?  Within 2e-5 the SplitMix64 tie key, then leader id. */
+int orc_assign_before(float d, uint32_t point, uint32_t leader, float od, uint32_t oleader);
+
+/* ---- subtree partition (tessa_partition.c) ------------------------------ */
+
+/* Overflow bits, compute_backend.rs:4843-4860 */
+#define ORC_OVF_QUEUE_NODE              (1ull << 0)
+#define ORC_OVF_QUEUE_ROW               (1ull << 1)
+#define ORC_OVF_LEAF_DESC               (1ull << 2)
+#define ORC_OVF_LEAF_ROW                (1ull << 3)
+#define ORC_OVF_LEADER                  (1ull << 4)
+#define ORC_OVF_FANOUT_OVER_32          (1ull << 5)
+#define ORC_OVF_NO_PROGRESS_SPLIT       (1ull << 7)
+#define ORC_OVF_OVERSIZED_TERMINAL_NODE (1ull << 10)
+
+/* Counter words used by the partition, at the reference's indices
+ * (compute_backend.rs:5028-5187, 159 words). */
+#define ORC_P_COUNTER_WORDS 159
+enum {
+    ORC_P_LEAF_PUSHES = 9,
+    ORC_P_OVERFLOW_FLAGS = 7,
+    ORC_P_PARTITION_POPS = 8,
+    ORC_P_OUTPUT_ROWS = 12,
+    ORC_P_OUTPUT_LEAF_COUNT = 13,
+    ORC_P_ASSIGNMENT_PASSES = 14,
+    ORC_P_MAX_ACTIVE = 15,
+    ORC_P_EFFECTIVE_ROOT_FANOUT = 17,
+    ORC_P_EFFECTIVE_DEEPER_FANOUT = 18,
+    ORC_P_FANOUT_ASSIGNMENT_SLOTS = 19,
+    ORC_P_REPLICATED_ROWS = 20,
+    ORC_P_UNIQUE_RESIDENT_ROWS = 21,
+    ORC_P_LARGE_NODE_CLAIMS = 27,
+    ORC_P_LARGE_NODE_SPLITS = 28,
+    ORC_P_LARGE_NODE_ROWS = 29,
+    ORC_P_LARGE_NODE_MAX_ROWS = 30,
+    ORC_P_LEAF_SIZE_MIN = 33,
+    ORC_P_LEAF_SIZE_MAX = 34,
+    ORC_P_LEAF_SIZE_SUM = 35,
+    ORC_P_LEAF_SIZE_COUNT = 36,
+    ORC_P_PARTITION_LEVEL_ROUNDS = 119,
+    ORC_P_LARGE_SPLIT_RETRIES = 130,
+    ORC_P_LARGE_BALANCED_FALLBACKS = 131,
+    ORC_P_LARGE_PHYSICAL_TILES = 145
+};
+
+typedef struct orc_subtree_cfg {
+    const uint32_t *root_leaders; /* resident row ids; NULL when count == 0 */
+    uint32_t root_leader_count;
+    uint32_t root_depth;          /* request.depth */
+    uint32_t max_depth;           /* params.max_depth */
+    uint32_t max_leaders;         /* params.max_leaders */
+    uint32_t fanout_second;       /* params.fanout_second (1..4) */
+    uint32_t leaf_min;            /* plan leaf_min (merge threshold) */
+    uint32_t leaf_max;            /* plan leaf_max = max(256, c_max) */
+    uint32_t small_node_limit;    /* plan small_node_limit (4096) */
+    uint64_t large_scratch_rows;  /* plan large_scratch_rows */
+    uint64_t max_leaf_count;
+    uint64_t max_leaf_rows;
+    float psamp_fraction;         /* params.psamp_fraction as f32 */
+    uint64_t seed;                /* orc_subtree_root_seed(...) */
+} orc_subtree_cfg;
+
+/* compute_backend.rs:7044-7075, 7082-7101, 7103-7121 */
+float orc_adaptive_psamp(float base, uint32_t cluster_size, uint32_t depth);
+int orc_meaningful_split(uint32_t parent_rows, uint32_t max_child_rows, uint32_t terminal_limit);
+void orc_sort_unique(uint32_t *v, uint32_t *len);
+/* compute_backend.rs:5991-6019 */
+void orc_sample_retry_leaders(const uint32_t *rows, uint32_t row_count, uint32_t num_leaders,
+                              uint64_t seed, uint32_t attempt, uint32_t *leaders);
+/* compute_backend.rs:12770-12800 hash-ranked leaders of a small node. */
+void orc_hash_rank_leaders(const uint32_t *pts, uint32_t n, uint32_t num_leaders, uint64_t seed,
+                           uint32_t attempt, uint32_t depth, uint32_t *leaders);
+/* compute_backend.rs:1597-1603 */
+uint64_t orc_subtree_root_seed(uint64_t random_seed, uint64_t depth, uint64_t point_count,
+                               uint64_t parent_points, uint64_t min_recurse_size);
+
+/* Recursive partition of resident rows 0..resident_rows-1 into leaves
+ * (leaf_row_ids / leaf_starts / leaf_sizes, compute_backend.rs:11735-11839
+ * layout), in the level / slot / parent-row order described in
+ * tessa_partition.c.  Overflow bits land in counters[ORC_P_OVERFLOW_FLAGS]
+ * and stop the walk after the level that raised them.  Returns 0, or a
+ * negative value on bad arguments (-2), bad root leaders (-3), or when out
+ * of host memory (-4). */
+int orc_subtree_partition(const int8_t *codes, const float *scales, const float *norms,
+                          size_t resident_rows, size_t padded_dim, const orc_subtree_cfg *cfg,
+                          uint32_t *leaf_row_ids, uint64_t *leaf_starts, uint64_t *leaf_sizes,
+                          uint64_t *counters, uint64_t *leaf_count, uint64_t *leaf_rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,6 +106,100 @@ class TessaConfig(C.Structure):
     _fields_ = [("device", C.c_int32), ("reserved", C.c_uint32)]
 
 
+# Subtree counters at the reference's indices (enum tessa_subtree_counter).
+SUBTREE_COUNTER_WORDS = 159
+P_OVERFLOW_FLAGS = 7
+P_PARTITION_POPS = 8
+P_OUTPUT_ROWS = 12
+P_OUTPUT_LEAF_COUNT = 13
+P_ASSIGNMENT_PASSES = 14
+P_MAX_ACTIVE = 15
+P_EFFECTIVE_ROOT_FANOUT = 17
+P_EFFECTIVE_DEEPER_FANOUT = 18
+P_FANOUT_ASSIGNMENT_SLOTS = 19
+P_REPLICATED_ROWS = 20
+P_UNIQUE_RESIDENT_ROWS = 21
+P_LARGE_NODE_CLAIMS = 27
+P_LARGE_NODE_SPLITS = 28
+P_LARGE_NODE_ROWS = 29
+P_LARGE_NODE_MAX_ROWS = 30
+P_LEAF_SIZE_MIN = 33
+P_LEAF_SIZE_MAX = 34
+P_LEAF_SIZE_SUM = 35
+P_LEAF_SIZE_COUNT = 36
+P_PARTITION_LEVEL_ROUNDS = 119
+P_LARGE_SPLIT_RETRIES = 130
+P_LARGE_BALANCED_FALLBACKS = 131
+P_LARGE_PHYSICAL_TILES = 145
+P_LEAF_SQ8_WMMA_TILES = 158
+
+PLAN_FALLBACK_UNSUPPORTED_K = 1 << 2
+PLAN_FALLBACK_UNSUPPORTED_FANOUT = 1 << 3
+PLAN_FALLBACK_UNSUPPORTED_LEADERS = 1 << 4
+PLAN_FALLBACK_WORKSPACE = 1 << 5
+
+
+class SubtreePlan(C.Structure):
+    _fields_ = [
+        ("supported", C.c_int32),
+        ("fallback_reason_flags", C.c_uint32),
+        ("overflow_flags", C.c_uint64),
+        ("leaf_min", C.c_uint32),
+        ("leaf_target", C.c_uint32),
+        ("leaf_max", C.c_uint32),
+        ("small_node_limit", C.c_uint32),
+        ("effective_root_fanout", C.c_uint32),
+        ("effective_deeper_fanout", C.c_uint32),
+        ("fanout_amplification", C.c_uint32),
+        ("large_child_slots", C.c_uint32),
+        ("max_queue_nodes", C.c_uint64),
+        ("max_leaf_count", C.c_uint64),
+        ("max_leaf_rows", C.c_uint64),
+        ("large_scratch_rows", C.c_uint64),
+        ("required_bytes", C.c_uint64),
+        ("budget_bytes", C.c_uint64),
+    ]
+
+
+class SubtreeRequest(C.Structure):
+    _fields_ = [
+        ("root_leaders", C.c_void_p),
+        ("root_leader_count", C.c_uint32),
+        ("root_depth", C.c_uint32),
+        ("seed", C.c_uint64),
+        ("leaf_knn", C.c_uint32),
+        ("fanout_second", C.c_uint32),
+        ("max_depth", C.c_uint32),
+        ("max_leaders", C.c_uint32),
+        ("leaf_min", C.c_uint32),
+        ("leaf_max", C.c_uint32),
+        ("small_node_limit", C.c_uint32),
+        ("psamp_fraction", C.c_float),
+        ("executor", C.c_uint32),
+        ("partition_only", C.c_uint32),
+        ("max_leaf_count", C.c_uint64),
+        ("max_leaf_rows", C.c_uint64),
+    ]
+
+
+class SubtreeOutput(C.Structure):
+    _fields_ = [
+        ("leaf_row_ids", C.c_void_p),
+        ("leaf_starts", C.c_void_p),
+        ("leaf_sizes", C.c_void_p),
+        ("topk_ids", C.c_void_p),
+        ("topk_dists", C.c_void_p),
+        ("counters", C.c_void_p),
+        ("leaf_counters", C.c_void_p),
+        ("leaf_count", C.c_uint64),
+        ("leaf_rows", C.c_uint64),
+        ("k", C.c_uint32),
+        ("levels", C.c_uint32),
+        ("partition_ms", C.c_float),
+        ("leaf_ms", C.c_float),
+    ]
+
+
 # Every symbol include/tessa_hip.h declares, with its ctypes signature.
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -127,6 +221,12 @@ SIGNATURES = {
     "tessa_session_assign_replay": (
         TessaStatus,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _P, _P, _P, C.POINTER(C.c_float)],
+    ),
+    "tessa_plan_subtree": (TessaStatus, [_U64, _U32, _U32, _U32, _U64, _U32, C.POINTER(SubtreePlan)]),
+    "tessa_subtree_root_seed": (_U64, [_U64, _U64, _U64, _U64, _U64]),
+    "tessa_session_run_subtree": (
+        TessaStatus,
+        [_P, C.POINTER(SubtreeRequest), C.POINTER(SubtreeOutput)],
     ),
 }
 

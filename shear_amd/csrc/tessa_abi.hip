@@ -17,6 +17,7 @@
 #include "../../include/tessa_hip.h"
 #include "assign_kernels.h"
 #include "leaf_kernels.h"
+#include "partition.h"
 #include "tessa_device.h"
 
 
@@ -195,8 +196,14 @@ tessa_status tessa_query_caps(int32_t device, tessa_caps *out) {
     return ok_status();
 }
 
-tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint32_t *out_ids,
-                             float *out_dists, uint64_t *counters, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// Leaf top-k over device layouts; `rows_bound` bounds the member rows and
+// sizes the re-run / chain queues.
+tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint64_t rows_bound,
+                            uint32_t *out_ids, float *out_dists, uint64_t *counters, void *stream) {
     tessa_status st = check_view(sq8);
     if (st.code) return st;
     if (!lb || !lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets || !out_ids ||
@@ -241,7 +248,7 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
                            "MFMA leaf path needs padded_dim <= 1024 and max_leaf_rows <= 4096 (got %u, %u)",
                            sq8->padded_dim, lb->max_leaf_rows);
     DeviceWorkspace *ws = nullptr;
-    st = get_workspace((uint64_t)lb->leaf_count * lb->max_leaf_rows, &ws);
+    st = get_workspace(rows_bound, &ws);
     if (st.code) return st;
     auto clamp32 = [](uint64_t v) { return (uint32_t)(v < 0xffffffffull ? v : 0xffffffffull); };
     p.fallback = ws->fallback;
@@ -260,6 +267,17 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
     if (launch_leaf_exact_fallback(p, s) != 0)
         return make_status(TESSA_ERR_HIP, 0, "leaf fallback kernel launch failed");
     return ok_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint32_t *out_ids,
+                             float *out_dists, uint64_t *counters, void *stream) {
+    if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
+    return leaf_topk_impl(sq8, lb, (uint64_t)lb->leaf_count * lb->max_leaf_rows, out_ids, out_dists, counters,
+                          stream);
 }
 
 tessa_status tessa_assign_replay(const tessa_sq8_view *sq8, const tessa_assign_batch *tb, uint32_t *out_ids,
@@ -329,6 +347,13 @@ struct tessa_session {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     uint64_t *counters = nullptr;
+    // subtree partition workspace (one device block carved into arrays)
+    void *part = nullptr;
+    size_t part_bytes = 0;
+    uint64_t *part_counters = nullptr;  // TESSA_SUBTREE_COUNTER_WORDS
+    tessa::LevelHeader *part_hdr = nullptr;
+    tessa::LevelHeader *part_hdr_host = nullptr;  // pinned
+    hipEvent_t ev2 = nullptr;
 };
 
 namespace {
@@ -396,7 +421,11 @@ tessa_status tessa_session_create(const tessa_config *cfg, tessa_session **out) 
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&s->ev0);
     if (e == hipSuccess) e = hipEventCreate(&s->ev1);
+    if (e == hipSuccess) e = hipEventCreate(&s->ev2);
     if (e == hipSuccess) e = hipMalloc(&s->counters, TESSA_COUNTER_WORDS * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc(&s->part_counters, TESSA_SUBTREE_COUNTER_WORDS * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc(&s->part_hdr, sizeof(tessa::LevelHeader));
+    if (e == hipSuccess) e = hipHostMalloc(&s->part_hdr_host, sizeof(tessa::LevelHeader), hipHostMallocDefault);
     if (e != hipSuccess) {
         tessa_session_destroy(s);
         return make_status(TESSA_ERR_HIP, 0, "session setup failed: %s", hipGetErrorString(e));
@@ -412,6 +441,11 @@ tessa_status tessa_session_destroy(tessa_session *s) {
     free_sq8(s);
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->counters) (void)hipFree(s->counters);
+    if (s->part) (void)hipFree(s->part);
+    if (s->part_counters) (void)hipFree(s->part_counters);
+    if (s->part_hdr) (void)hipFree(s->part_hdr);
+    if (s->part_hdr_host) (void)hipHostFree(s->part_hdr_host);
+    if (s->ev2) (void)hipEventDestroy(s->ev2);
     if (s->ev0) (void)hipEventDestroy(s->ev0);
     if (s->ev1) (void)hipEventDestroy(s->ev1);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -584,6 +618,306 @@ tessa_status tessa_session_assign_replay(tessa_session *s, const uint32_t *membe
         *event_ms = ms;
     }
     return st;
+}
+
+}  // extern "C"
+
+// ---- resident subtree ------------------------------------------------------
+
+namespace {
+
+constexpr uint32_t kLeafMin = 64;          // GPU_PERSISTENT_LEAF_MIN compute_backend.rs:385
+constexpr uint32_t kLeafTarget = 128;      // :387
+constexpr uint32_t kLeafMaxFloor = 256;    // :389
+constexpr uint32_t kSmallNodeLimit = 4096; // plan small_node_limit :1341
+constexpr uint32_t kLeaderStride = 128;    // GPU_QUEUE_LEADER_STRIDE :371
+
+uint64_t div_ceil(uint64_t a, uint64_t b) { return b ? (a + b - 1) / b : 0; }
+
+// Byte layout of the partition workspace for the given capacities.
+struct PartLayout {
+    uint64_t arena_cap = 0, item_cap = 0, leaf_cap = 0;
+    uint32_t node_cap = 0;
+    size_t off_arena[2] = {0, 0}, off_nodes[2] = {0, 0}, off_leaders = 0, off_ccount = 0, off_cidx = 0,
+           off_crel = 0, off_slots = 0, off_items = 0, off_sizes32 = 0, off_outoff = 0, bytes = 0;
+};
+
+PartLayout part_layout(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_t leaf_cap) {
+    PartLayout L;
+    partition_capacity(rows, famp, leaf_max, &L.arena_cap, &L.node_cap, &L.item_cap);
+    L.leaf_cap = leaf_cap ? leaf_cap : 1;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o += align256(bytes);
+        return at;
+    };
+    const uint64_t nc = L.node_cap;
+    L.off_arena[0] = take(L.arena_cap * 4);
+    L.off_arena[1] = take(L.arena_cap * 4);
+    L.off_nodes[0] = take(nc * sizeof(NodeDesc));
+    L.off_nodes[1] = take(nc * sizeof(NodeDesc));
+    L.off_leaders = take(nc * kPartMaxLeaders * 4);
+    L.off_ccount = take(nc * kPartMaxLeaders * 4);
+    L.off_cidx = take(nc * kPartMaxLeaders * 4);
+    L.off_crel = take(nc * kPartMaxLeaders * 4);
+    L.off_slots = take(L.arena_cap * 4);
+    L.off_items = take(L.item_cap * kPartMaxLeaders * 4);
+    L.off_sizes32 = take(L.leaf_cap * 4);
+    L.off_outoff = take(L.leaf_cap * 8);
+    L.bytes = o + kLeaderStride * 4;  // root leaders
+    return L;
+}
+
+// Re-run / chain queues of the MFMA leaf path for `rows` leaf rows.
+uint64_t leaf_workspace_bytes(uint64_t rows) {
+    return rows * 8 + (rows / 2 + 1) * 16 + (rows / 2 + 1) * 40 * 8;
+}
+
+tessa_status subtree_overflow(const tessa_session *s, const uint64_t *c, float ms) {
+    char labels[256];
+    const uint64_t f = c[TESSA_P_OVERFLOW_FLAGS];
+    tessa_overflow_labels(f, labels, sizeof(labels));
+    // "CUDA persistent subtree overflow" is the token rbc_partition.rs:2982-2998
+    // classifies as a capacity error; it is kept verbatim for that caller.
+    return make_status(TESSA_ERR_OVERFLOW, f,
+                       "CUDA persistent subtree overflow: resident_rows=%llu overflow_flags=0x%llx "
+                       "overflow_labels=%s leaf_rows=%llu leaf_count=%llu partition_pops=%llu "
+                       "assignment_passes=%llu max_active_points=%llu persistent_kernel_event_ms=%.3f "
+                       "partition_level_rounds=%llu (HIP gfx950 level-synchronous partition)",
+                       (unsigned long long)s->rows, (unsigned long long)f, labels,
+                       (unsigned long long)c[TESSA_P_OUTPUT_ROWS], (unsigned long long)c[TESSA_P_OUTPUT_LEAF_COUNT],
+                       (unsigned long long)c[TESSA_P_PARTITION_POPS],
+                       (unsigned long long)c[TESSA_P_ASSIGNMENT_PASSES], (unsigned long long)c[TESSA_P_MAX_ACTIVE],
+                       ms, (unsigned long long)c[TESSA_P_PARTITION_LEVEL_ROUNDS]);
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t tessa_subtree_root_seed(uint64_t random_seed, uint64_t depth, uint64_t point_count, uint64_t parent_points,
+                                 uint64_t min_recurse_size) {
+    auto rotl = [](uint64_t x, int r) { return (x << r) | (x >> (64 - r)); };
+    return random_seed ^ (depth * 0x9e3779b97f4a7c15ull) ^ rotl(point_count, 17) ^ rotl(parent_points, 7) ^
+           rotl(min_recurse_size, 29);
+}
+
+tessa_status tessa_plan_subtree(uint64_t resident_rows, uint32_t leaf_knn, uint32_t max_leaders_per_node,
+                                uint32_t max_fanout, uint64_t budget_bytes, uint32_t c_max,
+                                tessa_subtree_plan *plan) {
+    if (!plan) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "plan output is null");
+    tessa_subtree_plan p;
+    std::memset(&p, 0, sizeof(p));
+    const uint64_t r1 = resident_rows ? resident_rows : 1;
+    const uint32_t persistent_fanout = max_fanout ? max_fanout : 1;
+    const uint32_t famp = persistent_fanout < 4 ? persistent_fanout : 4;
+    p.leaf_min = kLeafMin;
+    p.leaf_target = kLeafTarget;
+    p.leaf_max = (c_max ? c_max : 1) > kLeafMaxFloor ? (c_max ? c_max : 1) : kLeafMaxFloor;
+    p.small_node_limit = kSmallNodeLimit;
+    p.effective_root_fanout = famp;
+    p.effective_deeper_fanout = 1;
+    p.fanout_amplification = famp;
+    p.large_child_slots = kLeaderStride;
+    // compute_backend.rs:1351-1380
+    p.max_queue_nodes = r1 * famp + div_ceil(r1, p.leaf_min);
+    p.max_leaf_rows = resident_rows * famp;
+    const uint64_t semantic_leaf_count = div_ceil(p.max_leaf_rows ? p.max_leaf_rows : 1, p.leaf_min) * 8;
+    p.max_leaf_count = semantic_leaf_count ? semantic_leaf_count : 1;
+    p.large_scratch_rows = r1 * famp;
+    const uint32_t k = leaf_knn < 32 ? leaf_knn : 32;
+    const PartLayout L = part_layout(resident_rows, famp, p.leaf_max, p.max_leaf_count);
+    p.required_bytes = L.bytes + TESSA_SUBTREE_COUNTER_WORDS * 8 + p.max_leaf_rows * 4 + p.max_leaf_count * 16 +
+                       p.max_leaf_rows * (uint64_t)k * 8 + leaf_workspace_bytes(p.max_leaf_rows);
+    p.budget_bytes = budget_bytes ? budget_bytes : UINT64_MAX;
+    if (resident_rows != 0 && budget_bytes != 0 && p.required_bytes > budget_bytes) {
+        p.fallback_reason_flags |= TESSA_PLAN_FALLBACK_WORKSPACE;
+        p.overflow_flags |= TESSA_OVF_WORKSPACE_BUDGET;
+    }
+    if (leaf_knn > 32) {
+        p.fallback_reason_flags |= TESSA_PLAN_FALLBACK_UNSUPPORTED_K;
+        p.overflow_flags |= TESSA_OVF_LEAF_DESC;
+    }
+    if (persistent_fanout > 4) {
+        p.fallback_reason_flags |= TESSA_PLAN_FALLBACK_UNSUPPORTED_FANOUT;
+        p.overflow_flags |= TESSA_OVF_FANOUT_OVER_32;
+    }
+    if (max_leaders_per_node > kLeaderStride) {
+        p.fallback_reason_flags |= TESSA_PLAN_FALLBACK_UNSUPPORTED_LEADERS;
+        p.overflow_flags |= TESSA_OVF_LEADER;
+    }
+    p.supported = p.fallback_reason_flags == 0;
+    *plan = p;
+    return ok_status();
+}
+
+tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_request *rq,
+                                       tessa_subtree_output *out) {
+    if (!s || !s->codes) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session has no SQ8 upload");
+    if (!rq || !out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "subtree request/output is null");
+    const uint64_t rows = s->rows;
+    out->leaf_count = out->leaf_rows = 0;
+    out->k = 0;
+    out->levels = 0;
+    out->partition_ms = out->leaf_ms = 0.0f;
+    const bool partition_only = rq->partition_only != 0;
+    if (!partition_only && (rq->leaf_knn == 0 || rq->leaf_knn > (uint32_t)kMaxK))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, TESSA_OVF_LEAF_DESC,
+                           "CUDA persistent strict error: unsupported subtree leaf_knn=%u (1..32) "
+                           "fallback_reason_flags=0x%x",
+                           rq->leaf_knn, TESSA_PLAN_FALLBACK_UNSUPPORTED_K);
+    if (rq->fanout_second == 0 || rq->fanout_second > 4)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, TESSA_OVF_FANOUT_OVER_32,
+                           "CUDA persistent strict error: unsupported subtree fanout_second=%u (1..4) "
+                           "fallback_reason_flags=0x%x",
+                           rq->fanout_second, TESSA_PLAN_FALLBACK_UNSUPPORTED_FANOUT);
+    if (rq->max_leaders == 0 || rq->leaf_min == 0 || rq->leaf_max == 0 || rq->small_node_limit == 0 ||
+        rq->small_node_limit > kSmallNodeLimit)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "subtree request needs max_leaders, leaf_min, leaf_max >= 1 and "
+                           "small_node_limit in [1, 4096]");
+    if (!partition_only && rq->executor == TESSA_EXEC_MFMA && rq->leaf_max > 4096)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "MFMA leaf path needs leaf_max <= 4096 (got %u)", rq->leaf_max);
+    if (s->padded_dim > 1024)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "subtree path needs padded_dim <= 1024 (got %u)", s->padded_dim);
+    const uint32_t leader_cap = rq->max_leaders < kLeaderStride ? rq->max_leaders : kLeaderStride;
+    if (rq->root_leader_count > leader_cap)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "CUDA persistent root leader override has %u leaders, exceeding per-node limit %u",
+                           rq->root_leader_count, leader_cap);
+    if (rq->root_leader_count > 0 && !rq->root_leaders)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "root leader count without root leader ids");
+    for (uint32_t i = 0; i < rq->root_leader_count; ++i)
+        if (rq->root_leaders[i] >= rows)
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                               "CUDA persistent root leader override row %u exceeds resident rows %llu",
+                               rq->root_leaders[i], (unsigned long long)rows);
+    const uint32_t famp = rq->fanout_second;
+    if (rows * famp > 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "resident rows x fanout must stay below 2^32");
+    if (!out->leaf_row_ids || !out->leaf_starts || !out->leaf_sizes ||
+        (!partition_only && (!out->topk_ids || !out->topk_dists)))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "subtree output has a null device pointer");
+    if (rq->max_leaf_count == 0 || rq->max_leaf_rows == 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "subtree output capacities must be positive");
+    TESSA_HIP_TRY(hipSetDevice(s->device));
+
+    const PartLayout L = part_layout(rows, famp, rq->leaf_max, rq->max_leaf_count);
+    if (s->part_bytes < L.bytes) {
+        TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+        if (s->part) (void)hipFree(s->part);
+        s->part = nullptr;
+        s->part_bytes = 0;
+        if (hipMalloc(&s->part, L.bytes) != hipSuccess)
+            return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
+                               "Failed to allocate CUDA GPU persistent subtree workspace (HIP, %zu bytes) "
+                               "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                               L.bytes, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+        s->part_bytes = L.bytes;
+    }
+    char *base = static_cast<char *>(s->part);
+    PartArgs a{};
+    a.codes = s->codes;
+    a.scales = s->scales;
+    a.norms = s->norms;
+    a.rows = (uint32_t)rows;
+    a.padded_dim = s->padded_dim;
+    uint32_t *d_root = reinterpret_cast<uint32_t *>(base + L.bytes - kLeaderStride * 4);
+    if (rq->root_leader_count)
+        TESSA_HIP_TRY(hipMemcpyAsync(d_root, rq->root_leaders, rq->root_leader_count * 4ull,
+                                     hipMemcpyHostToDevice, s->stream));
+    a.root_leaders = d_root;
+    a.root_leader_count = rq->root_leader_count;
+    a.root_depth = rq->root_depth;
+    a.max_depth = rq->max_depth;
+    a.max_leaders = rq->max_leaders;
+    a.fanout_second = rq->fanout_second;
+    a.leaf_min = rq->leaf_min;
+    a.leaf_max = rq->leaf_max;
+    a.small_node_limit = rq->small_node_limit;
+    const uint32_t k = partition_only ? 0u
+                                      : (uint32_t)(rq->leaf_knn < rows - 1 ? rq->leaf_knn : (rows ? rows - 1 : 0));
+    a.k = k;
+    a.psamp = rq->psamp_fraction;
+    a.seed = rq->seed;
+    a.large_scratch_rows = rows * famp;
+    a.max_leaf_count = rq->max_leaf_count;
+    a.max_leaf_rows = rq->max_leaf_rows;
+    a.leaf_row_ids = out->leaf_row_ids;
+    a.leaf_starts = out->leaf_starts;
+    a.leaf_sizes = out->leaf_sizes;
+    a.leaf_sizes32 = reinterpret_cast<uint32_t *>(base + L.off_sizes32);
+    a.leaf_out_offsets = reinterpret_cast<uint64_t *>(base + L.off_outoff);
+    a.counters = s->part_counters;
+    a.hdr = s->part_hdr;
+    for (int i = 0; i < 2; ++i) {
+        a.arena[i] = reinterpret_cast<uint32_t *>(base + L.off_arena[i]);
+        a.nodes[i] = reinterpret_cast<NodeDesc *>(base + L.off_nodes[i]);
+    }
+    a.leaders = reinterpret_cast<uint32_t *>(base + L.off_leaders);
+    a.child_counts = reinterpret_cast<uint32_t *>(base + L.off_ccount);
+    a.child_idx = reinterpret_cast<uint32_t *>(base + L.off_cidx);
+    a.child_rel = reinterpret_cast<uint32_t *>(base + L.off_crel);
+    a.slots = reinterpret_cast<uint32_t *>(base + L.off_slots);
+    a.item_counts = reinterpret_cast<uint32_t *>(base + L.off_items);
+    a.arena_cap = L.arena_cap;
+    a.item_cap = L.item_cap;
+    a.node_cap = L.node_cap;
+
+    TESSA_HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    PartResult pr{};
+    const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr);
+    if (rc != 0)
+        return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
+                           rc == -2 ? "level/attempt bound exceeded"
+                                    : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+    TESSA_HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    uint64_t c[TESSA_SUBTREE_COUNTER_WORDS];
+    TESSA_HIP_TRY(hipMemcpyAsync(c, s->part_counters, sizeof(c), hipMemcpyDeviceToHost, s->stream));
+    TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+    float part_ms = 0.0f;
+    (void)hipEventElapsedTime(&part_ms, s->ev0, s->ev1);
+    out->partition_ms = part_ms;
+    out->levels = pr.levels;
+    out->leaf_count = pr.leaf_count;
+    out->leaf_rows = pr.leaf_rows;
+    out->k = k;
+    if (out->counters) std::memcpy(out->counters, c, sizeof(c));
+    if (c[TESSA_P_OVERFLOW_FLAGS] != 0) return subtree_overflow(s, c, part_ms);
+    if (partition_only || k == 0 || pr.leaf_count == 0) return ok_status();
+
+    // Leaf top-k over the published leaves (the top-k CTAs' role,
+    // compute_backend.rs:17113-17370).
+    if (pr.leaf_count > 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaves");
+    const uint32_t max_rows = (uint32_t)c[TESSA_P_LEAF_SIZE_MAX];
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((TESSA_COUNTER_WORDS * 2 + 63) / 64), dim3(64), 0, s->stream,
+                       reinterpret_cast<uint32_t *>(s->counters), (uint32_t)(TESSA_COUNTER_WORDS * 2), 0u);
+    tessa_sq8_view view{s->codes, s->scales, s->norms, s->gids, s->rows, s->dim, s->padded_dim};
+    tessa_leaf_batch lb{out->leaf_row_ids, out->leaf_starts, a.leaf_sizes32, a.leaf_out_offsets,
+                        (uint32_t)pr.leaf_count, max_rows, k, rq->executor, 0u, 0u};
+    tessa_status st = leaf_topk_impl(&view, &lb, pr.leaf_rows, out->topk_ids, out->topk_dists, s->counters,
+                                     s->stream);
+    if (st.code) return st;
+    TESSA_HIP_TRY(hipEventRecord(s->ev2, s->stream));
+    uint64_t lc[TESSA_COUNTER_WORDS];
+    TESSA_HIP_TRY(hipMemcpyAsync(lc, s->counters, sizeof(lc), hipMemcpyDeviceToHost, s->stream));
+    TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+    float leaf_ms = 0.0f;
+    (void)hipEventElapsedTime(&leaf_ms, s->ev1, s->ev2);
+    out->leaf_ms = leaf_ms;
+    if (out->leaf_counters) std::memcpy(out->leaf_counters, lc, sizeof(lc));
+    if (out->counters) out->counters[TESSA_P_LEAF_SQ8_WMMA_TILES] = lc[TESSA_C_LEAF_MFMA_TILES];
+    if (lc[TESSA_C_OVERFLOW_FLAGS] != 0) {
+        char labels[256];
+        tessa_overflow_labels(lc[TESSA_C_OVERFLOW_FLAGS], labels, sizeof(labels));
+        return make_status(TESSA_ERR_OVERFLOW, lc[TESSA_C_OVERFLOW_FLAGS],
+                           "CUDA persistent subtree overflow: resident_rows=%llu overflow_flags=0x%llx "
+                           "overflow_labels=%s (leaf top-k)",
+                           (unsigned long long)rows, (unsigned long long)lc[TESSA_C_OVERFLOW_FLAGS], labels);
+    }
+    return ok_status();
 }
 
 }  // extern "C"

@@ -1,0 +1,201 @@
+"""Resident-subtree operator: recursive partition + leaf top-k over the HIP C ABI.
+
+Mirrors (paths relative to shear-core/src/algorithm/pipnn/ in the reference):
+
+* ``PiPNNSubtreeParams``          the PiPNNParams fields the path reads
+                                  (params.rs:3362-3372 defaults)
+* ``GpuSubtreePartitionRequest``  compute_backend.rs:1818-1826
+* ``plan_subtree``                plan_gpu_persistent_subtree :1309-1488
+* ``subtree_root_seed``           gpu_queue_root_seed :1597-1603
+* ``SubtreeSession.process_quantized_subtree_l2_compact_topk``
+                                  PiPNNComputeBackend::process_quantized_subtree_l2_compact_topk
+                                  :3794-3805 -> GpuSubtreeTopKResult :1945-1951,
+                                  batches from compact_batches_from_persistent_slices
+                                  :32243-32339
+
+All work runs in libtessa_hip.so; torch tensors only hold device memory.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .tessa import CompactTopKBatch, compact_batches_from_slices
+
+GPU_QUEUE_LEADER_STRIDE = 128  # compute_backend.rs:371
+
+
+@dataclass
+class PiPNNSubtreeParams:
+    leaf_knn: int = 2
+    c_min: int = 256
+    c_max: int = 2048
+    psamp_fraction: float = 0.001
+    max_leaders: int = 1000
+    max_depth: int = 10
+    fanout_second: int = 3
+    random_seed: int = 42
+    gpu_workspace_budget_bytes: int = 0  # 0 = unlimited
+    executor: int = N.EXEC_MFMA
+
+
+@dataclass
+class GpuSubtreePartitionRequest:
+    point_ids: np.ndarray                 # u32 global ids of the resident rows
+    root_leader_ids: np.ndarray | None = None  # resident row ids
+    depth: int = 0
+    parent_points: int = 0
+    adaptive_c_max: int = 0
+    min_recurse_size: int = 0
+    memory_budget_bytes: int | None = None
+
+
+@dataclass
+class GpuSubtreeTopKResult:
+    compact_batches: list[CompactTopKBatch]
+    assignment_passes: int
+    leaf_count: int
+    max_active_points: int
+    profile: dict = field(default_factory=dict)
+
+
+def subtree_root_seed(random_seed: int, depth: int, point_count: int, parent_points: int,
+                      min_recurse_size: int) -> int:
+    return int(N.load().tessa_subtree_root_seed(random_seed & (2**64 - 1), depth, point_count, parent_points,
+                                                min_recurse_size))
+
+
+def plan_subtree(resident_rows: int, leaf_knn: int, max_leaders_per_node: int, max_fanout: int,
+                 budget_bytes: int | None, c_max: int) -> N.SubtreePlan:
+    plan = N.SubtreePlan()
+    N.check(N.load().tessa_plan_subtree(resident_rows, leaf_knn, max_leaders_per_node, max_fanout,
+                                        budget_bytes or 0, c_max, C.byref(plan)), "tessa_plan_subtree")
+    return plan
+
+
+@dataclass
+class SubtreeDeviceOutput:
+    """Device-resident result of one run (before any host copy)."""
+
+    leaf_row_ids: torch.Tensor  # int32 view of u32
+    leaf_starts: torch.Tensor   # int64
+    leaf_sizes: torch.Tensor    # int64
+    topk_ids: torch.Tensor      # int32 view of u32
+    topk_dists: torch.Tensor    # f32
+    counters: np.ndarray        # u64[159], reference layout
+    leaf_counters: np.ndarray   # u64[32]
+    leaf_count: int
+    leaf_rows: int
+    k: int
+    levels: int
+    partition_ms: float
+    leaf_ms: float
+
+
+class SubtreeSession:
+    """One device, one stream, one uploaded resident subtree (the reference's
+    CudaComputeBackend with its resident subtree workspace)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = N.load()
+        h = C.c_void_p()
+        N.check(self._lib.tessa_session_create(C.byref(N.TessaConfig(device, 0)), C.byref(h)), "session create")
+        self._h = h
+        self.device = device
+        self.rows = 0
+        self._keep = ()
+
+    def close(self):
+        if self._h:
+            N.check(self._lib.tessa_session_destroy(self._h), "session destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def upload(self, codes: np.ndarray, scales: np.ndarray, norms: np.ndarray, global_ids: np.ndarray, dim: int):
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        norms = np.ascontiguousarray(norms, np.float32)
+        gids = np.ascontiguousarray(global_ids, np.uint32)
+        view = N.Sq8View(codes.ctypes.data, scales.ctypes.data, norms.ctypes.data, gids.ctypes.data,
+                         codes.shape[0], dim, codes.shape[1])
+        N.check(self._lib.tessa_session_upload_sq8(self._h, C.byref(view)), "session upload")
+        self.rows = codes.shape[0]
+        self.global_ids = gids
+
+    def run(self, request: GpuSubtreePartitionRequest, params: PiPNNSubtreeParams,
+            partition_only: bool = False) -> SubtreeDeviceOutput:
+        rows = self.rows
+        famp = max(params.fanout_second, 1)
+        max_leaders = min(max(params.max_leaders, 1), GPU_QUEUE_LEADER_STRIDE)
+        plan = plan_subtree(rows, params.leaf_knn, max_leaders, famp, request.memory_budget_bytes,
+                            params.c_max)
+        if not plan.supported:
+            raise N.TessaError(_status(4, plan.overflow_flags,
+                                       f"CUDA persistent strict error: unsupported subtree "
+                                       f"fallback_reason_flags=0x{plan.fallback_reason_flags:x}"), "plan")
+        seed = subtree_root_seed(params.random_seed, request.depth, len(request.point_ids),
+                                 request.parent_points, request.min_recurse_size)
+        k = 0 if partition_only else min(params.leaf_knn, max(rows - 1, 0))
+        dev = torch.device("cuda", self.device)
+        max_rows = max(int(plan.max_leaf_rows), 1)
+        max_leaves = max(int(plan.max_leaf_count), 1)
+        out_rows = torch.empty(max_rows, dtype=torch.int32, device=dev)
+        out_starts = torch.empty(max_leaves, dtype=torch.int64, device=dev)
+        out_sizes = torch.empty(max_leaves, dtype=torch.int64, device=dev)
+        out_ids = torch.empty(max(max_rows * k, 1), dtype=torch.int32, device=dev)
+        out_d = torch.empty(max(max_rows * k, 1), dtype=torch.float32, device=dev)
+        counters = np.zeros(N.SUBTREE_COUNTER_WORDS, np.uint64)
+        leaf_counters = np.zeros(N.COUNTER_WORDS, np.uint64)
+        roots = (np.zeros(0, np.uint32) if request.root_leader_ids is None
+                 else np.ascontiguousarray(request.root_leader_ids, np.uint32))
+        rq = N.SubtreeRequest(
+            roots.ctypes.data if len(roots) else None, len(roots), request.depth, seed,
+            max(params.leaf_knn, 1), famp, params.max_depth, max_leaders, plan.leaf_min, plan.leaf_max,
+            plan.small_node_limit, np.float32(params.psamp_fraction).item(), params.executor,
+            1 if partition_only else 0, plan.max_leaf_count, plan.max_leaf_rows)
+        out = N.SubtreeOutput(out_rows.data_ptr(), out_starts.data_ptr(), out_sizes.data_ptr(),
+                              out_ids.data_ptr(), out_d.data_ptr(), counters.ctypes.data,
+                              leaf_counters.ctypes.data, 0, 0, 0, 0, 0.0, 0.0)
+        torch.cuda.synchronize(dev)  # outputs allocated on torch's stream
+        st = self._lib.tessa_session_run_subtree(self._h, C.byref(rq), C.byref(out))
+        N.check(st, "tessa_session_run_subtree")
+        return SubtreeDeviceOutput(out_rows, out_starts, out_sizes, out_ids, out_d, counters, leaf_counters,
+                                   int(out.leaf_count), int(out.leaf_rows), int(out.k), int(out.levels),
+                                   float(out.partition_ms), float(out.leaf_ms))
+
+    def process_quantized_subtree_l2_compact_topk(self, request: GpuSubtreePartitionRequest,
+                                                  params: PiPNNSubtreeParams) -> GpuSubtreeTopKResult:
+        r = self.run(request, params)
+        lc, lr = r.leaf_count, r.leaf_rows
+        leaf_row_ids = r.leaf_row_ids[:lr].cpu().numpy().view(np.uint32)
+        starts = r.leaf_starts[:lc].cpu().numpy().astype(np.int64)
+        sizes = r.leaf_sizes[:lc].cpu().numpy().astype(np.int64)
+        ids = r.topk_ids[: lr * r.k].cpu().numpy().view(np.uint32)
+        d = r.topk_dists[: lr * r.k].cpu().numpy()
+        batches = compact_batches_from_slices(np.asarray(request.point_ids, np.uint32), leaf_row_ids, starts,
+                                              sizes, ids, d, r.k, params.leaf_knn)
+        return GpuSubtreeTopKResult(
+            compact_batches=batches,
+            assignment_passes=int(r.counters[N.P_ASSIGNMENT_PASSES]),
+            leaf_count=lc,
+            max_active_points=int(r.counters[N.P_MAX_ACTIVE]),
+            profile={"counters": r.counters, "leaf_counters": r.leaf_counters, "levels": r.levels,
+                     "partition_ms": r.partition_ms, "leaf_ms": r.leaf_ms},
+        )
+
+
+def _status(code: int, flags: int, msg: str) -> N.TessaStatus:
+    s = N.TessaStatus()
+    s.code = code
+    s.overflow_flags = flags
+    s.msg = msg.encode()[:511]
+    return s

@@ -109,3 +109,191 @@ def hash64(v: int) -> int:
     v ^= v >> 27
     v = (v * 0x94D049BB133111EB) & m
     return v ^ (v >> 31)
+
+
+# ---- subtree partition ---------------------------------------------------------
+
+M64 = (1 << 64) - 1
+
+
+def tie_key(point: int, leader: int) -> int:
+    return hash64(((point << 32) ^ leader ^ 0x9E3779B97F4A7C15) & M64)
+
+
+def assign_before(d, p, l, od, ol) -> bool:
+    """compute_backend.rs:6541-6568."""
+    if abs(F32(F32(d) - F32(od))) <= EPS:
+        a, b = tie_key(p, l), tie_key(p, ol)
+        return a < b or (a == b and l < ol)
+    return F32(d) < F32(od)
+
+
+def adaptive_psamp(base, n: int, depth: int) -> np.float32:
+    f = F32(base)
+    for lim, m in ((20_000_000, 0.05), (10_000_000, 0.1), (5_000_000, 0.2), (1_000_000, 0.4), (100_000, 0.7)):
+        if n >= lim:
+            f = F32(f * F32(m))
+            break
+    if depth > 4:
+        f = F32(f * F32(0.35))
+    elif depth > 2:
+        f = F32(f * F32(0.5))
+    elif depth > 0:
+        f = F32(f * F32(0.8))
+    return min(max(f, F32(0.00005)), F32(0.1))
+
+
+def meaningful(parent: int, max_child: int, terminal: int) -> bool:
+    if parent <= terminal or max_child <= terminal:
+        return True
+    if max_child >= parent:
+        return False
+    shrink = max(parent >> 5, 32)
+    if shrink >= parent:
+        shrink = 1
+    return max_child + shrink <= parent
+
+
+def partition(codes, scales, norms, *, seed, root_depth=0, max_depth=10, max_leaders=128, fanout_second=1,
+              leaf_min=64, leaf_max=256, small_node_limit=4096, psamp=0.001, root_leaders=None):
+    """Level-order RBC split (compute_backend.rs:12456-13078, 15047-15727):
+    -> (leaves as lists of row ids, flags).  Children keep the parent's row
+    order; nodes of a level are processed in publication order."""
+    R = len(codes)
+    c64 = codes.astype(np.int64)
+    roots = [] if root_leaders is None else [int(x) for x in root_leaders]
+
+    def best(p, leaders, F):
+        bd = [F32(np.finfo(np.float32).max)] * F
+        bs = [None] * F
+        bl = [0xFFFFFFFF] * F
+        dots = c64[leaders] @ c64[p]
+        for s, l in enumerate(leaders):
+            d = assign_dist(int(dots[s]), scales[p], norms[p], scales[l], norms[l])
+            if not assign_before(d, p, l, bd[F - 1], bl[F - 1]):
+                continue
+            pos = F - 1
+            while pos > 0 and assign_before(d, p, l, bd[pos - 1], bl[pos - 1]):
+                bd[pos], bs[pos], bl[pos] = bd[pos - 1], bs[pos - 1], bl[pos - 1]
+                pos -= 1
+            bd[pos], bs[pos], bl[pos] = d, s, l
+        return bs
+
+    def base_count(n, depth, cap):
+        b = int(F32(F32(adaptive_psamp(psamp, n, depth) * F32(n)) + F32(0.5)))
+        return min(max(b, 2), cap)
+
+    leaves, flags = [], 0
+    level = [(list(range(R)), root_depth, seed & M64)] if R else []
+    while level and not flags:
+        nxt = []
+        for rows, depth, nseed in level:
+            n = len(rows)
+            rel = max(depth - root_depth, 0)
+            probe = rel == 0 and fanout_second > 1 and n > 1
+            if n > leaf_max or (probe and n * fanout_second > small_node_limit):
+                # ---- large node
+                if depth >= max_depth:
+                    flags |= 1 << 10
+                    continue
+                max_l = max(2, min(max_leaders, min(max(n, 2), 128)))
+                use_root = rel == 0 and len(roots) > 0
+                L = min(len(roots) if use_root else base_count(n, depth, max_l), max_l)
+                F = min(max(fanout_second if rel == 0 else 1, 1), L)
+                leaders = roots[:L] if use_root else [rows[min(s * n // L, n - 1)] for s in range(L)]
+                attempt = 0
+                while True:
+                    slots = [best(p, leaders, F) for p in rows]
+                    counts = [0] * L
+                    for sl in slots:
+                        for s in sl:
+                            counts[s] += 1
+                    nonempty = sum(1 for c in counts if c)
+                    if nonempty > 1 and meaningful(n, max(counts), leaf_max):
+                        children = [[p for p, sl in zip(rows, slots) if s in sl] for s in range(L)]
+                        break
+                    if not use_root and (attempt == 0 or L < max_l):
+                        nl = L if attempt == 0 else (2 * L if 2 * L < max_l else max_l)
+                        attempt += 1
+                        new = []
+                        for s in range(nl):
+                            b, e = s * n // nl, (s + 1) * n // nl
+                            e = max(e, b + 1)
+                            key = hash64((nseed ^ ((attempt * 0xD6E8FEB86659FD93) & M64)
+                                          ^ ((s * 0x9E3779B97F4A7C15) & M64)) & M64)
+                            new.append(rows[b + key % (e - b)])
+                        leaders, L = new, nl
+                        continue
+                    children = [rows[0::2], rows[1::2]]
+                    break
+                for s, ch in enumerate(children):
+                    if not ch:
+                        continue
+                    if len(ch) <= leaf_max:
+                        leaves.append(ch)
+                    elif depth + 1 >= max_depth:
+                        flags |= 1 << 10
+                        break
+                    else:
+                        cs = nseed ^ ((s * 0x94D049BB133111EB) & M64) ^ ((len(ch) << 23) & M64)
+                        nxt.append((ch, depth + 1, cs))
+            else:
+                # ---- small node (process_node)
+                pts = sorted(set(rows))
+                n = len(pts)
+                if n <= leaf_max and not probe:
+                    leaves.append(pts)
+                    continue
+                if depth >= max_depth:
+                    flags |= 1 << 10
+                    continue
+                max_l = max(min(max_leaders, n), 2)
+                if max_l > 128:
+                    flags |= 1 << 4
+                    continue
+                base = base_count(n, depth, max_l)
+                use_root = rel == 0 and len(roots) > 0
+                ok, kids = False, []
+                for attempt in range(1 if use_root else 6):
+                    L = min(len(roots) if use_root else base << attempt, max_l)
+                    if use_root:
+                        leaders = roots[:L]
+                    else:
+                        keyed = sorted((hash64((nseed ^ ((attempt * 0xBF58476D1CE4E5B9) & M64) ^ (depth << 19)
+                                                ^ (i << 7) ^ ((p << 31) & M64)) & M64), p)
+                                       for i, p in enumerate(pts))
+                        leaders = [p for _, p in keyed[:L]]
+                    F = min(max(fanout_second if rel == 0 else 1, 1), L)
+                    slots = [best(p, leaders, F) for p in pts]
+                    kids, small, maxc = [], [], 0
+                    for s in range(L):
+                        ch = sorted({p for p, sl in zip(pts, slots) if s in sl})
+                        if not ch:
+                            continue
+                        if len(ch) < leaf_min:
+                            small = sorted(set(small) | set(ch))
+                            if len(small) >= leaf_min:
+                                kids.append(small)
+                                maxc = max(maxc, len(small))
+                                small = []
+                        else:
+                            kids.append(ch)
+                            maxc = max(maxc, len(ch))
+                    if small:
+                        if kids and len(kids[-1]) + len(small) <= leaf_max:
+                            kids[-1] = sorted(set(kids[-1]) | set(small))
+                            maxc = max(maxc, len(kids[-1]))
+                        else:
+                            kids.append(small)
+                            maxc = max(maxc, len(small))
+                    if len(kids) > 1 and meaningful(n, maxc, leaf_max):
+                        ok = True
+                        break
+                    if L >= max_l:
+                        break
+                if not ok:
+                    leaves.append(pts)
+                else:
+                    leaves.extend(kids)
+        level = nxt
+    return leaves, flags
