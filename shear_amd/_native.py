@@ -209,6 +209,10 @@ SIGNATURES = {
     "tessa_overflow_labels": (None, [_U64, C.c_char_p, C.c_size_t]),
     "tessa_query_caps": (TessaStatus, [C.c_int32, C.POINTER(TessaCaps)]),
     "tessa_leaf_topk": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P]),
+    "tessa_leaf_topk_profiled": (
+        TessaStatus,
+        [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P, C.POINTER(C.c_float)],
+    ),
     "tessa_assign_replay": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(AssignBatch), _P, _P, _P, _P]),
     "tessa_sq8_quantize": (TessaStatus, [_P, _U64, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "tessa_session_create": (TessaStatus, [C.POINTER(TessaConfig), C.POINTER(_P)]),

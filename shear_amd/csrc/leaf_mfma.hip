@@ -62,7 +62,14 @@ struct Layout {
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
 };
 
-constexpr uint32_t kLdsBudget = 160u * 1024u;
+// LDS per workgroup; 160 KiB = one workgroup per CU.
+#ifndef TESSA_LEAF_LDS_KB
+#define TESSA_LEAF_LDS_KB 160
+#endif
+#ifndef TESSA_LEAF_MIN_BLOCKS
+#define TESSA_LEAF_MIN_BLOCKS 1
+#endif
+constexpr uint32_t kLdsBudget = TESSA_LEAF_LDS_KB * 1024u;
 
 // Staging entries per lane that fit next to the tile and the leaf-wide
 // member/scale/norm arrays (one slot is the sink for rejected candidates).
@@ -182,7 +189,7 @@ __device__ __forceinline__ float filter_bound(float F, float rs, float rn, float
 }
 
 template <int KS>
-__global__ __launch_bounds__(kThreads, 1) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
+__global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
                                                               uint32_t total_work, uint32_t padded_grid) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -586,7 +593,7 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
         attr_set = true;
     }
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
-    if (stage_capacity(L::kTileBytes, cols_cap) < 32u) return -4;  // leaf too large for this dim
+    if (stage_capacity(L::kTileBytes, cols_cap) < 17u) return -4;  // a tile adds up to 16 per lane
     const uint32_t blocks_per_leaf = (p.max_leaf_rows + kRowsPerBlock - 1) / kRowsPerBlock;
     const uint64_t total = (uint64_t)blocks_per_leaf * p.leaf_count;
     if (total == 0) return 0;

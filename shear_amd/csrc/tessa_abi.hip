@@ -200,10 +200,31 @@ tessa_status tessa_query_caps(int32_t device, tessa_caps *out) {
 
 namespace {
 
+// Events bracketing the three leaf kernels (MFMA, chain replay, exact
+// re-run), one set per device, created on first use.
+struct PhaseEvents {
+    hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+};
+std::mutex g_ev_mutex;
+std::vector<PhaseEvents> g_events;
+
+tessa_status phase_events(PhaseEvents **out) {
+    int dev = 0;
+    TESSA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ev_mutex);
+    if ((int)g_events.size() <= dev) g_events.resize(dev + 1);
+    PhaseEvents &pe = g_events[dev];
+    for (int i = 0; i < 4; ++i)
+        if (!pe.e[i]) TESSA_HIP_TRY(hipEventCreate(&pe.e[i]));
+    *out = &pe;
+    return ok_status();
+}
+
 // Leaf top-k over device layouts; `rows_bound` bounds the member rows and
-// sizes the re-run / chain queues.
+// sizes the re-run / chain queues.  `ev` (optional) brackets the kernels.
 tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint64_t rows_bound,
-                            uint32_t *out_ids, float *out_dists, uint64_t *counters, void *stream) {
+                            uint32_t *out_ids, float *out_dists, uint64_t *counters, void *stream,
+                            PhaseEvents *ev) {
     tessa_status st = check_view(sq8);
     if (st.code) return st;
     if (!lb || !lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets || !out_ids ||
@@ -262,10 +283,14 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.chain_pool_capacity = clamp32(ws->pool_capacity);
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
     hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->queue_counts, 3u, 0u);
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[0], s));
     if (launch_leaf_mfma(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "MFMA leaf kernel launch failed");
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[1], s));
     if (launch_leaf_chain(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "leaf chain kernel launch failed");
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[2], s));
     if (launch_leaf_exact_fallback(p, s) != 0)
         return make_status(TESSA_ERR_HIP, 0, "leaf fallback kernel launch failed");
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3], s));
     return ok_status();
 }
 
@@ -277,7 +302,26 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
                              float *out_dists, uint64_t *counters, void *stream) {
     if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
     return leaf_topk_impl(sq8, lb, (uint64_t)lb->leaf_count * lb->max_leaf_rows, out_ids, out_dists, counters,
-                          stream);
+                          stream, nullptr);
+}
+
+tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint32_t *out_ids,
+                                      float *out_dists, uint64_t *counters, void *stream, float *phase_ms) {
+    if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
+    if (!phase_ms) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "phase_ms is null");
+    PhaseEvents *ev = nullptr;
+    tessa_status st = phase_events(&ev);
+    if (st.code) return st;
+    st = leaf_topk_impl(sq8, lb, (uint64_t)lb->leaf_count * lb->max_leaf_rows, out_ids, out_dists, counters, stream,
+                        ev);
+    if (st.code) return st;
+    TESSA_HIP_TRY(hipEventSynchronize(ev->e[3]));
+    for (int i = 0; i < 3; ++i) {
+        float ms = 0.0f;
+        TESSA_HIP_TRY(hipEventElapsedTime(&ms, ev->e[i], ev->e[i + 1]));
+        phase_ms[i] = ms;
+    }
+    return ok_status();
 }
 
 tessa_status tessa_assign_replay(const tessa_sq8_view *sq8, const tessa_assign_batch *tb, uint32_t *out_ids,
@@ -898,7 +942,7 @@ tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_req
     tessa_leaf_batch lb{out->leaf_row_ids, out->leaf_starts, a.leaf_sizes32, a.leaf_out_offsets,
                         (uint32_t)pr.leaf_count, max_rows, k, rq->executor, 0u, 0u};
     tessa_status st = leaf_topk_impl(&view, &lb, pr.leaf_rows, out->topk_ids, out->topk_dists, s->counters,
-                                     s->stream);
+                                     s->stream, nullptr);
     if (st.code) return st;
     TESSA_HIP_TRY(hipEventRecord(s->ev2, s->stream));
     uint64_t lc[TESSA_COUNTER_WORDS];

@@ -152,8 +152,12 @@ class LeafLayouts:
 def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k: int,
               executor: int = N.EXEC_MFMA, out_ids: torch.Tensor | None = None,
               out_dists: torch.Tensor | None = None, counters: torch.Tensor | None = None,
-              stream: torch.cuda.Stream | None = None, debug_rerun_every: int = 0):
-    """Enqueue the leaf operator; returns (ids int32 view of u32, dists f32, counters int64)."""
+              stream: torch.cuda.Stream | None = None, debug_rerun_every: int = 0,
+              phase_ms: list | None = None):
+    """Enqueue the leaf operator; returns (ids int32 view of u32, dists f32, counters int64).
+
+    With ``phase_ms`` (a list) the call synchronises and appends the hipEvent
+    times of its three kernels (MFMA, chain replay, exact re-run) in ms."""
     dev = sq8.codes.device
     if out_ids is None:
         out_ids = torch.empty(layouts.output_len, dtype=torch.int32, device=dev)
@@ -165,8 +169,15 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
     lb = N.LeafBatch(_ptr(layouts.members), _ptr(layouts.member_offsets), _ptr(layouts.member_counts),
                      _ptr(layouts.output_offsets), layouts.leaf_count, layouts.max_leaf_rows, k, executor,
                      debug_rerun_every, 0)
-    N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
-                                     _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
+    if phase_ms is None:
+        N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
+                                         _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
+    else:
+        ph = (C.c_float * 3)()
+        N.check(N.load().tessa_leaf_topk_profiled(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
+                                                  _ptr(counters), _stream_ptr(stream), ph),
+                "tessa_leaf_topk_profiled")
+        phase_ms.append([float(ph[0]), float(ph[1]), float(ph[2])])
     return out_ids, out_dists, counters
 
 
