@@ -124,100 +124,103 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(Leaf
 // For a row whose certified candidate set G (every candidate outside G is more
 // than 2e-5 above all of G) contains an eps-tie chain, the reference result is
 // the bounded insertion over G's members in column order; other candidates can
-// neither enter in front of G's nor stay in the buffer.  One lane per row:
-// sort G by column in LDS, then replay compute_backend.rs:7229-7259.
+// neither enter in front of G's nor stay in the buffer.
+//
+// One wave per queued row.  Lane i holds G's i-th entry; a bitonic sort across
+// lanes orders G by column.  The bounded insertion (leaf_build.rs:913-951)
+// then runs with the k slots spread over lanes 0..k-1: for a candidate c each
+// lane evaluates "c beats slot j"; the reference scan from the tail stops at
+// the highest slot c does not beat, so the insertion position is one past it
+// (a ballot), and the slots from there up shift by one (a lane shuffle).
 constexpr int kChainMax = 64;
-constexpr int kChainLanes = 64;
-constexpr int kChainLdsBytes = kChainMax * kChainLanes * 12 + kMaxK * kChainLanes * 8;
+constexpr int kChainWaves = 4;
 
-__global__ __launch_bounds__(kChainLanes) void leaf_chain_kernel(LeafParams p) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    uint32_t *cc = reinterpret_cast<uint32_t *>(smem);  // column   [i * 64 + lane]
-    float *cd = reinterpret_cast<float *>(cc + kChainMax * kChainLanes);
-    uint32_t *cg = reinterpret_cast<uint32_t *>(cd + kChainMax * kChainLanes);
-    float *bd = reinterpret_cast<float *>(cg + kChainMax * kChainLanes);
-    uint32_t *bg = reinterpret_cast<uint32_t *>(bd + kMaxK * kChainLanes);
-    const uint32_t lane = threadIdx.x;
+__global__ __launch_bounds__(kChainWaves * 64) void leaf_chain_kernel(LeafParams p) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
     uint32_t count = *p.chain_count;
     if (count > p.chain_capacity) count = p.chain_capacity;
     uint64_t done = 0;
-    for (uint32_t w = blockIdx.x * kChainLanes + lane; w < count; w += gridDim.x * kChainLanes) {
+    for (uint32_t w = blockIdx.x * kChainWaves + wave; w < count; w += gridDim.x * kChainWaves) {
         const uint4 hdr = p.chain_rows[w];
         const uint32_t leaf = hdr.x, r = hdr.y, off = hdr.z;
         const uint32_t m = hdr.w < (uint32_t)kChainMax ? hdr.w : (uint32_t)kChainMax;
         const uint32_t n = p.member_counts[leaf];
         const uint32_t *mem = p.members + p.member_offsets[leaf];
         const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
-        for (uint32_t i = 0; i < m; ++i) {
-            const uint2 e = p.chain_pool[off + i];
-            const uint32_t c = e.y;
-            const uint32_t mc = c < n ? mem[c] : 0u;
-            cc[i * kChainLanes + lane] = c;
-            cd[i * kChainLanes + lane] = __uint_as_float(e.x);
-            cg[i * kChainLanes + lane] = mc < p.rows ? p.gids[mc] : kEmptyId;
+        uint32_t col = 0xffffffffu;
+        float d = kEmptyDist;
+        uint32_t g = kEmptyId;
+        if (lane < m) {
+            const uint2 e = p.chain_pool[off + lane];
+            col = e.y;
+            d = __uint_as_float(e.x);
+            const uint32_t mc = col < n ? mem[col] : 0u;
+            g = mc < p.rows ? p.gids[mc] : kEmptyId;
         }
-        // insertion sort by column (member order)
-        for (uint32_t i = 1; i < m; ++i) {
-            const uint32_t kc = cc[i * kChainLanes + lane];
-            const float kd = cd[i * kChainLanes + lane];
-            const uint32_t kg = cg[i * kChainLanes + lane];
-            uint32_t j = i;
-            while (j > 0 && cc[(j - 1) * kChainLanes + lane] > kc) {
-                cc[j * kChainLanes + lane] = cc[(j - 1) * kChainLanes + lane];
-                cd[j * kChainLanes + lane] = cd[(j - 1) * kChainLanes + lane];
-                cg[j * kChainLanes + lane] = cg[(j - 1) * kChainLanes + lane];
-                --j;
+        // bitonic sort of the 64 lanes by column (padding lanes sort last)
+#pragma unroll
+        for (uint32_t kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+            for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
+                const uint32_t oc = __shfl_xor(col, j);
+                const float od = __shfl_xor(d, j);
+                const uint32_t og = __shfl_xor(g, j);
+                const bool up = (lane & kk) == 0u;
+                const bool lower = (lane & j) == 0u;
+                const bool take = (up == lower) ? (oc < col) : (oc > col);
+                col = take ? oc : col;
+                d = take ? od : d;
+                g = take ? og : g;
             }
-            cc[j * kChainLanes + lane] = kc;
-            cd[j * kChainLanes + lane] = kd;
-            cg[j * kChainLanes + lane] = kg;
         }
-        // leaf_build.rs:913-951 bounded insertion over G in column order
+        // bounded insertion over G in column order; slot j lives in lane j
+        float bd = kEmptyDist;
+        uint32_t bg = kEmptyId;
         uint32_t len = 0;
         for (uint32_t i = 0; i < m && keff > 0u; ++i) {
-            const float d = cd[i * kChainLanes + lane];
-            const uint32_t g = cg[i * kChainLanes + lane];
-            uint32_t pos;
+            const float cd = __shfl(d, (int)i);
+            const uint32_t cg = __shfl(g, (int)i);
+            const bool b = lane < len && beats(cd, cg, bd, bg);
+            uint32_t new_len = len;
+            uint64_t stop;
             if (len < keff) {
-                pos = len++;
+                new_len = len + 1u;
+                stop = __ballot(lane < len && !b);
             } else {
-                if (!beats(d, g, bd[(keff - 1) * kChainLanes + lane], bg[(keff - 1) * kChainLanes + lane]))
-                    continue;
-                pos = keff - 1;
+                const uint64_t bm = __ballot(b);
+                if (((bm >> (keff - 1u)) & 1ull) == 0ull) continue;  // does not beat the tail
+                stop = __ballot(lane + 1u < keff && !b);
             }
-            while (pos > 0 &&
-                   beats(d, g, bd[(pos - 1) * kChainLanes + lane], bg[(pos - 1) * kChainLanes + lane])) {
-                bd[pos * kChainLanes + lane] = bd[(pos - 1) * kChainLanes + lane];
-                bg[pos * kChainLanes + lane] = bg[(pos - 1) * kChainLanes + lane];
-                --pos;
+            const uint32_t pos = stop ? (uint32_t)(64 - __clzll((long long)stop)) : 0u;
+            const float ud = __shfl(bd, (int)((lane + 63u) & 63u));
+            const uint32_t ug = __shfl(bg, (int)((lane + 63u) & 63u));
+            if (lane > pos && lane < new_len) {
+                bd = ud;
+                bg = ug;
             }
-            bd[pos * kChainLanes + lane] = d;
-            bg[pos * kChainLanes + lane] = g;
+            if (lane == pos) {
+                bd = cd;
+                bg = cg;
+            }
+            len = new_len;
         }
         const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
-        for (uint32_t s = 0; s < p.k; ++s) {
-            const bool live = s < len;
-            p.out_ids[out + s] = live ? bg[s * kChainLanes + lane] : kEmptyId;
-            p.out_dists[out + s] = live ? bd[s * kChainLanes + lane] : kEmptyDist;
+        if (lane < p.k) {
+            const bool live = lane < len;
+            p.out_ids[out + lane] = live ? bg : kEmptyId;
+            p.out_dists[out + lane] = live ? bd : kEmptyDist;
         }
-        ++done;
+        done += lane == 0u ? 1u : 0u;
     }
-    // per-wave row count
-    for (int offs = 32; offs > 0; offs >>= 1) done += __shfl_xor(done, offs);
     if (lane == 0) counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
 }
 
 }  // namespace
 
 int launch_leaf_chain(const LeafParams &p, hipStream_t stream) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)leaf_chain_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kChainLdsBytes) != hipSuccess)
-            return -1;
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(leaf_chain_kernel, dim3(1024), dim3(kChainLanes), kChainLdsBytes, stream, p);
+    // grid-stride over the device-side queue count: no host round trip
+    hipLaunchKernelGGL(leaf_chain_kernel, dim3(2048), dim3(kChainWaves * 64), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
