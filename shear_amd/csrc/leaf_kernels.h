@@ -40,7 +40,15 @@ struct LeafParams {
     uint2 *chain_pool;
     uint32_t *chain_pool_used;
     uint32_t chain_pool_capacity;
+    // MFMA kernel survivor log: one slot per persistent workgroup, holding
+    // log_capacity (raw dot, column) entries per thread.
+    uint2 *survivor_log;
+    uint32_t log_capacity;
+    uint32_t log_slots;
 };
+
+constexpr uint32_t kLeafLogCapacity = 128;
+constexpr uint32_t kLeafLogSlots = 2048;
 
 // Host-side launchers (leaf_exact.hip / leaf_mfma.hip).
 int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream);

@@ -50,7 +50,6 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerBlock = kWaves * 32;
 constexpr int kTileCols = 32;
 constexpr int kTop = 32;        // per-lane sorted list (registers)
-constexpr int kStageMax = 64;   // per-lane staging capacity limit (LDS)
 constexpr uint32_t kMaxLeafRows = 4096;
 constexpr float kFilterMargin = 3.0f * kTieEps;
 
@@ -62,27 +61,16 @@ struct Layout {
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
 };
 
-// LDS per workgroup; 160 KiB = one workgroup per CU.
-#ifndef TESSA_LEAF_LDS_KB
-#define TESSA_LEAF_LDS_KB 160
-#endif
+// Dynamic LDS limit (the whole CU); a C2-shaped leaf uses ~37 KiB, so two
+// workgroups share a CU, and registers are capped for two waves per SIMD.
 #ifndef TESSA_LEAF_MIN_BLOCKS
-#define TESSA_LEAF_MIN_BLOCKS 1
+#define TESSA_LEAF_MIN_BLOCKS 2
 #endif
-constexpr uint32_t kLdsBudget = TESSA_LEAF_LDS_KB * 1024u;
+constexpr uint32_t kLdsBudget = 160u * 1024u;
 
-// Staging entries per lane that fit next to the tile and the leaf-wide
-// member/scale/norm arrays (one slot is the sink for rejected candidates).
-__host__ __device__ constexpr uint32_t stage_capacity(uint32_t tile_bytes, uint32_t cols_cap) {
-    const uint32_t fixed = tile_bytes + cols_cap * 12u + 64u;
-    const uint32_t per = kThreads * 8u;
-    const uint32_t slots = fixed < kLdsBudget ? (kLdsBudget - fixed) / per : 0u;
-    const uint32_t cap = slots > 0u ? slots - 1u : 0u;
-    return cap > (uint32_t)kStageMax ? (uint32_t)kStageMax : cap;
-}
-
+// LDS: one column tile plus the leaf's member ids, scales and norms.
 __host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
-    return tile_bytes + cols_cap * 12u + 64u + (stage_capacity(tile_bytes, cols_cap) + 1u) * kThreads * 8u;
+    return tile_bytes + cols_cap * 12u + 64u;
 }
 
 // Compare-exchange on (key, payload) pairs; ascending when `up`.
@@ -142,9 +130,11 @@ __device__ __forceinline__ float pair_kth32(const float (&a)[kTop]) {
     return fminf(best, a[kTop - 1]);
 }
 
-// Fold `staged` LDS entries (raw dot, column) of this lane into its sorted
-// top-32: exact distances are computed here, for staged candidates only.
-__device__ __forceinline__ void fold_staged(const uint2 *stage, const float *cs, const float *cn, uint32_t tid,
+// Fold this thread's `staged` survivor-log entries (raw dot, column) into its
+// sorted top-32: exact distances are computed here, for survivors only.  The
+// loads are unconditional (entries past `staged` lie inside the thread's log
+// slot and are masked afterwards), so no per-entry branches are needed.
+__device__ __forceinline__ void fold_staged(const uint2 *stage, const float *cs, const float *cn, uint32_t ncols,
                                             int staged, float rs, float rn, float (&topd)[kTop],
                                             uint32_t (&topc)[kTop], float &disc) {
     const int chunks = (wave_max_i(staged) + 15) / 16;
@@ -154,15 +144,11 @@ __device__ __forceinline__ void fold_staged(const uint2 *stage, const float *cs,
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int e = ch * 16 + i;
-            float d = __builtin_inff();
-            uint32_t col = 0xffffu;
-            if (e < staged) {
-                const uint2 s = stage[e * kThreads + tid];
-                col = s.y;
-                d = leaf_l2((int)s.x, rs, rn, cs[col], cn[col]);
-            }
-            v[i] = d;
-            c[i] = col;
+            const uint2 s = stage[e];
+            const bool valid = e < staged;
+            const uint32_t col = (valid && s.y < ncols) ? s.y : 0u;
+            v[i] = valid ? leaf_l2((int)s.x, rs, rn, cs[col], cn[col]) : __builtin_inff();
+            c[i] = valid ? s.y : 0xffffu;
         }
         bitonic_sort_kv<16>(v, c);
         // lower half of (top ascending) vs (chunk ascending, padded to 32, reversed)
@@ -188,397 +174,500 @@ __device__ __forceinline__ float filter_bound(float F, float rs, float rn, float
     return (float)(tau - fabs(tau) * 2.0e-6 - 1.0e-30);
 }
 
+
+// Values-only compare-exchange (ascending).
+__device__ __forceinline__ void cexv(float &a, float &b) {
+    const float lo = fminf(a, b), hi = fmaxf(a, b);
+    a = lo;
+    b = hi;
+}
+
+template <int N>
+__device__ __forceinline__ void bitonic_sort_v(float (&v)[N]) {
+#pragma unroll
+    for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    if ((i & k) == 0) cexv(v[i], v[l]);
+                    else cexv(v[l], v[i]);
+                }
+            }
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void bitonic_merge_v(float (&v)[N]) {
+#pragma unroll
+    for (int j = N >> 1; j > 0; j >>= 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int l = i ^ j;
+            if (l > i) cexv(v[i], v[l]);
+        }
+    }
+}
+
+// rsel-th smallest (1-based, rsel <= 2N) of the union of this lane's and its
+// partner's ascending N-lists: ascending ++ descending is bitonic, one merge
+// sorts it, and a static select picks the element.
+template <int N>
+__device__ __forceinline__ float pair_kth(const float (&a)[N], int rsel) {
+    float m[2 * N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        m[i] = a[i];
+        m[2 * N - 1 - i] = __shfl_xor(a[i], 32);
+    }
+    bitonic_merge_v<2 * N>(m);
+    float res = __builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 2 * N; ++i) res = (i == rsel - 1) ? m[i] : res;
+    return res;
+}
+
 template <int KS>
 __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
-                                                              uint32_t total_work, uint32_t padded_grid) {
+                                                              uint32_t total_work, uint32_t per_xcd) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // Runtime layout: tile | members | scales | norms | misc | staging.
+    // Runtime layout: tile | members | scales | norms | misc.
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
-    const int stage_cap = (int)stage_capacity(L::kTileBytes, cols_cap);
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
     uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kTileBytes);
     float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
     float *cn_lds = cs_lds + cols_cap;
     uint32_t *misc = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);
-    uint2 *stage = reinterpret_cast<uint2 *>(misc + 16);
 
-    // XCD-aware order: blocks are dispatched round-robin over the 8 XCDs, so
-    // give each XCD a contiguous range of work items (the row blocks of one
-    // leaf then share that XCD's L2).
-    const uint32_t per_xcd = padded_grid / 8u;
-    const uint32_t work = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
-    if (work >= total_work) return;
-    const uint32_t leaf = work / blocks_per_leaf;
-    const uint32_t blk = work % blocks_per_leaf;
-    const uint32_t n = p.member_counts[leaf];
-    const uint32_t row_base = blk * kRowsPerBlock;
-    if (row_base >= n) return;
-    if (n > p.max_leaf_rows || n > kMaxLeafRows) {
-        if (threadIdx.x == 0) flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
-        return;
-    }
-    const uint32_t *mem = p.members + p.member_offsets[leaf];
-    const uint32_t pd = p.padded_dim;
     const uint32_t tid = threadIdx.x;
-
-    // Leaf member ids, scales and norms once in LDS; min/max norm of the leaf.
-    if (tid == 0) {
-        misc[0] = 0x7f800000u;  // +inf bits: min norm
-        misc[1] = 0u;           // max norm
-    }
-    __syncthreads();
-    {
-        float lo = __builtin_inff(), hi = 0.0f;
-        for (uint32_t c = tid; c < n; c += kThreads) {
-            uint32_t mc = mem[c];
-            if (mc >= p.rows) {
-                flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
-                mc = 0u;
-            }
-            mem_lds[c] = mc;
-            const float cn = p.norms[mc];
-            cs_lds[c] = p.scales[mc];
-            cn_lds[c] = cn;
-            lo = fminf(lo, cn);
-            hi = fmaxf(hi, cn);
-        }
-        // norms are sums of squares (>= 0): their bit patterns order like the values
-        atomicMin(&misc[0], __float_as_uint(lo));
-        atomicMax(&misc[1], __float_as_uint(hi));
-    }
-    __syncthreads();
-    const float cn_min = __uint_as_float(misc[0]);
-    const float cn_max = __uint_as_float(misc[1]);
-
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
     const uint32_t j = lane & 31u;
     const uint32_t h = lane >> 5;
-    const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
-    const bool row_ok = r < n;
-    const bool wave_rows_full = row_base + wave * 32u + 32u <= n;
-    const uint32_t mr = row_ok ? mem_lds[r] : 0u;
+    const uint32_t pd = p.padded_dim;
+    const uint32_t cap = p.log_capacity;
+        // This thread's entries are contiguous, so the final fold reads 16 of
+    // them with immediate offsets from one address.
+    uint2 *slog = p.survivor_log + ((uint64_t)blockIdx.x * kThreads + tid) * cap;
 
-    // Row codes for the whole K range (B operand), zero past padded_dim.
-    v4i bfrag[KS];
-    {
-        const int8_t *rc = p.codes + (uint64_t)mr * pd;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const uint32_t off = 32u * s + 16u * h;
-            v4i z = {0, 0, 0, 0};
-            if (row_ok && off < pd) z = *reinterpret_cast<const v4i *>(rc + off);
-            bfrag[s] = z;
+    // Work items are (leaf, 128-row block).  Blocks are dispatched round-robin
+    // over the 8 XCDs: XCD x walks its own contiguous item range, so the row
+    // blocks of a leaf share that XCD's L2.
+    const uint32_t xcd = blockIdx.x % 8u;
+    const uint32_t lane_in_xcd = blockIdx.x / 8u;
+    const uint32_t wgs_per_xcd = gridDim.x / 8u;
+    uint32_t s_surv = 0, s_fb = 0, s_done = 0, s_ch = 0, s_fc = 0, s_tiles = 0, s_ovf = 0;
+
+    for (uint32_t it = lane_in_xcd; it < per_xcd; it += wgs_per_xcd) {
+        const uint32_t work = xcd * per_xcd + it;
+        if (work >= total_work) break;
+        const uint32_t leaf = work / blocks_per_leaf;
+        const uint32_t blk = work % blocks_per_leaf;
+        const uint32_t n = p.member_counts[leaf];
+        const uint32_t row_base = blk * kRowsPerBlock;
+        if (row_base >= n) continue;
+        if (n > p.max_leaf_rows || n > kMaxLeafRows) {
+            if (tid == 0) flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+            continue;
         }
-    }
-    const float rs = row_ok ? cs_lds[r] : 1.0f;
-    const float rn = row_ok ? cn_lds[r] : 0.0f;
+        const uint32_t *mem = p.members + p.member_offsets[leaf];
 
-    float topd[kTop];
-    uint32_t topc[kTop];
-#pragma unroll
-    for (int i = 0; i < kTop; ++i) {
-        topd[i] = __builtin_inff();
-        topc[i] = 0xffffu;
-    }
-    float F = __builtin_inff();      // filter threshold (running pair 32nd + margin)
-    float tau = -__builtin_inff();   // cs * dot bound implied by F
-    float disc = __builtin_inff();   // smallest distance evicted from this lane's list
-    int staged = 0;
-    uint32_t survivors = 0, refines = 0;
-
-    const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
-    const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
-    v4i pre[L::kChunksPerThread];
-
-    auto load_tile = [&](uint32_t t) {
-#pragma unroll
-        for (int q = 0; q < L::kChunksPerThread; ++q) {
-            const uint32_t chunk = tid + q * kThreads;
-            v4i z = {0, 0, 0, 0};
-            if (chunk < (uint32_t)L::kChunks) {
-                const uint32_t row = chunk / (KS * 2);
-                const uint32_t off = (chunk % (KS * 2)) * 16u;
-                const uint32_t c = t * kTileCols + row;
-                if (c < n && off < pd)
-                    z = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mem_lds[c] * pd + off);
-            }
-            pre[q] = z;
-        }
-    };
-
-    load_tile(0);
-    for (uint32_t t = 0; t < ntiles; ++t) {
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < L::kChunksPerThread; ++q) {
-            const uint32_t chunk = tid + q * kThreads;
-            if (chunk < (uint32_t)L::kChunks) {
-                const uint32_t row = chunk / (KS * 2);
-                const uint32_t off = (chunk % (KS * 2)) * 16u;
-                *reinterpret_cast<v4i *>(tile + row * L::kTileStride + off) = pre[q];
-            }
+        __syncthreads();  // previous item's readers of the LDS arrays are done
+        if (tid == 0) {
+            misc[0] = 0x7f800000u;  // +inf bits: min norm
+            misc[1] = 0u;           // max norm
         }
         __syncthreads();
-        if (t + 1 < ntiles) load_tile(t + 1);
-
-        v16i acc = {};
-        const int8_t *arow = tile + j * L::kTileStride + 16u * h;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const v4i a = *reinterpret_cast<const v4i *>(arow + 32 * s);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
+        {
+            float lo = __builtin_inff(), hi = 0.0f;
+            for (uint32_t c = tid; c < n; c += kThreads) {
+                uint32_t mc = mem[c];
+                if (mc >= p.rows) {
+                    flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+                    mc = 0u;
+                }
+                mem_lds[c] = mc;
+                const float cn = p.norms[mc];
+                cs_lds[c] = p.scales[mc];
+                cn_lds[c] = cn;
+                lo = fminf(lo, cn);
+                hi = fmaxf(hi, cn);
+            }
+            // norms are sums of squares (>= 0): their bit patterns order like the values
+            atomicMin(&misc[0], __float_as_uint(lo));
+            atomicMax(&misc[1], __float_as_uint(hi));
         }
+        __syncthreads();
+        const float cn_min = __uint_as_float(misc[0]);
+        const float cn_max = __uint_as_float(misc[1]);
 
-        // Epilogue: necessary-condition filter cs*dot >= tau, stage (dot, col)
-        // branch-free (a rejected candidate goes to the sink slot).  Only the
-        // diagonal tile (self columns), the last tile (columns past n) and
-        // partially filled row groups need per-candidate validity checks; the
-        // choice is wave-uniform.
-        const uint32_t cbase = t * kTileCols;
-        const bool checked =
-            __builtin_amdgcn_readfirstlane((t == diag_tile || cbase + kTileCols > n || !wave_rows_full) ? 1 : 0);
-        auto epilogue = [&](auto check_tag) {
-            constexpr bool kCheck = decltype(check_tag)::value;
+        const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
+        const bool row_ok = r < n;
+        const bool wave_rows_full = row_base + wave * 32u + 32u <= n;
+        const uint32_t mr = row_ok ? mem_lds[r] : 0u;
+        const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
+
+        // Row codes for the whole K range (B operand), zero past padded_dim.
+        v4i bfrag[KS];
+        {
+            const int8_t *rc = p.codes + (uint64_t)mr * pd;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 cs4 = *reinterpret_cast<const float4 *>(cs_lds + cbase + 8 * q + 4 * h);
-                const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+            for (int s = 0; s < KS; ++s) {
+                const uint32_t off = 32u * s + 16u * h;
+                v4i z = {0, 0, 0, 0};
+                if (row_ok && off < pd) z = *reinterpret_cast<const v4i *>(rc + off);
+                bfrag[s] = z;
+            }
+        }
+        const float rs = row_ok ? cs_lds[r] : 1.0f;
+        const float rn = row_ok ? cn_lds[r] : 0.0f;
+
+        const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
+        const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
+        v4i pre[L::kChunksPerThread];
+
+        auto load_tile = [&](uint32_t t) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int v = 4 * q + e;
-                    const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
-                    bool take = __fmul_rn((float)acc[v], csv[e]) >= tau;
-                    if (kCheck) take = take && row_ok && c < n && c != r;
-                    const int slot = take ? staged : stage_cap;
-                    stage[slot * kThreads + tid] = make_uint2((uint32_t)acc[v], c);
-                    staged += take ? 1 : 0;
+            for (int q = 0; q < L::kChunksPerThread; ++q) {
+                const uint32_t chunk = tid + q * kThreads;
+                v4i z = {0, 0, 0, 0};
+                if (chunk < (uint32_t)L::kChunks) {
+                    const uint32_t row = chunk / (KS * 2);
+                    const uint32_t off = (chunk % (KS * 2)) * 16u;
+                    const uint32_t c = t * kTileCols + row;
+                    if (c < n && off < pd)
+                        z = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mem_lds[c] * pd + off);
+                }
+                pre[q] = z;
+            }
+        };
+        auto store_tile = [&]() {
+#pragma unroll
+            for (int q = 0; q < L::kChunksPerThread; ++q) {
+                const uint32_t chunk = tid + q * kThreads;
+                if (chunk < (uint32_t)L::kChunks) {
+                    const uint32_t row = chunk / (KS * 2);
+                    const uint32_t off = (chunk % (KS * 2)) * 16u;
+                    *reinterpret_cast<v4i *>(tile + row * L::kTileStride + off) = pre[q];
                 }
             }
         };
-        if (checked) epilogue(std::true_type{});
-        else epilogue(std::false_type{});
-
-        // Fold staged candidates before the next tile could overflow staging.
-        if (__any(staged > stage_cap - 16)) {
-            ++refines;
-            survivors += (uint32_t)staged;
-            fold_staged(stage, cs_lds, cn_lds, tid, staged, rs, rn, topd, topc, disc);
-            staged = 0;
-            F = __fadd_rn(pair_kth32(topd), kFilterMargin);
-            tau = row_ok ? filter_bound(F, rs, rn, cn_min, cn_max) : __builtin_inff();
-        }
-    }
-    // ---- final: merge the pair's lists, certify, order, write ---------------
-    survivors += (uint32_t)staged;
-    if (__any(staged > 0)) fold_staged(stage, cs_lds, cn_lds, tid, staged, rs, rn, topd, topc, disc);
-
-    // Known sequence: the pair's 32 smallest sorted (positions 0..31) and the
-    // 8 smallest of the rest (32..39).  Everything not known is > min(disc, F).
-    constexpr int kSeq = kTop + 8;
-    float sd[kSeq];
-    uint32_t sc[kSeq];
-    {
-        float hi[kTop];
-        uint32_t phi[kTop];
-        {
-            float bd[kTop];
-            uint32_t bc[kTop];
+        auto mfma_tile = [&]() {
+            v16i acc = {};
+            const int8_t *arow = tile + j * L::kTileStride + 16u * h;
 #pragma unroll
-            for (int m = 0; m < kTop; ++m) {
-                bd[m] = __shfl_xor(topd[m], 32);
-                bc[m] = __shfl_xor(topc[m], 32);
+            for (int s = 0; s < KS; ++s) {
+                const v4i a = *reinterpret_cast<const v4i *>(arow + 32 * s);
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < kTop; ++i) {
-                const float a = topd[i], b = bd[kTop - 1 - i];
-                const bool sw = b < a;
-                sd[i] = sw ? b : a;
-                sc[i] = sw ? bc[kTop - 1 - i] : topc[i];
-                hi[i] = sw ? a : b;
-                phi[i] = sw ? topc[i] : bc[kTop - 1 - i];
-            }
-        }
-        float lo[kTop];
-        uint32_t plo[kTop];
-#pragma unroll
-        for (int i = 0; i < kTop; ++i) {
-            lo[i] = sd[i];
-            plo[i] = sc[i];
-        }
-        bitonic_merge_kv<kTop>(lo, plo);
-#pragma unroll
-        for (int i = 0; i < kTop; ++i) {
-            sd[i] = lo[i];
-            sc[i] = plo[i];
-        }
-        // half-cleaners keep the lower half of a bitonic sequence: 32 -> 16 -> 8,
-        // then a bitonic merge sorts those 8
-#pragma unroll
-        for (int w = 16; w >= 8; w >>= 1) {
-#pragma unroll
-            for (int i = 0; i < w; ++i) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
-        }
-#pragma unroll
-        for (int w = 4; w >= 1; w >>= 1) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if ((i & w) == 0) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            sd[kTop + i] = hi[i];
-            sc[kTop + i] = phi[i];
-        }
-    }
-    // dropped on arrival: d > F (F never increases); evicted: >= disc
-    const float disc_all = fminf(fminf(disc, __shfl_xor(disc, 32)), F);
+            return acc;
+        };
 
-    const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
-    // Tie clusters over the sorted known sequence.
-    int q_end = (int)keff - 1;   // last index of G
-    bool extending = keff > 0u;
-    bool clique_bad = false;
-    float cstart = sd[0];
-    uint32_t cid[kSeq];
-    cid[0] = 0;
+        // ---- phase A: row threshold from every 4th column tile ---------------
+        // Each lane keeps the 16 smallest exact distances it sees (values only);
+        // F is the pair's kSel-th smallest sample distance plus 3 eps, so at
+        // least kSel candidates lie at or below F.
+        constexpr int kSample = 16;
+        const int rsel = (int)(keff < 24u ? keff : 24u);
+        float samp[kSample];
 #pragma unroll
-    for (int i = 1; i < kSeq; ++i) {
-        const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
-        cid[i] = tie ? cid[i - 1] : (uint32_t)i;
-        const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
-        cstart = tie ? cstart : sd[i];
-        if (i >= (int)keff && extending) {
-            if (tie) q_end = i;
-            else extending = false;
-        }
-        clique_bad |= span_bad && (i <= q_end || (extending && i >= (int)keff));
-    }
-    // Gap certificate: the cluster holding s_{keff-1} closes inside the known
-    // 64 and the next distance after it -- known or dropped -- is > eps away.
-    bool gap_ok = keff == 0u || !extending;
-    if (keff > 0u && gap_ok) {
-        float theta = sd[0];
-        float next = disc_all;
+        for (int i = 0; i < kSample; ++i) samp[i] = __builtin_inff();
+        for (uint32_t t = 0; t < ntiles; t += 4) {
+            load_tile(t);
+            __syncthreads();
+            store_tile();
+            __syncthreads();
+            const v16i acc = mfma_tile();
+            const uint32_t cbase = t * kTileCols;
+            float v[16];
 #pragma unroll
-        for (int i = 1; i < kSeq; ++i) {
-            theta = (i == q_end) ? sd[i] : theta;  // static indices only: no scratch
-            next = (i == q_end + 1) ? fminf(next, sd[i]) : next;
-        }
-        gap_ok = next == __builtin_inff() || __fsub_rn(next, theta) > kTieEps;
-    }
-    // Test knob: re-run every `debug_rerun_every`-th row through the exact kernel.
-    if (p.debug_rerun_every != 0u && (r % p.debug_rerun_every) == 0u) gap_ok = false;
-    // Outcome: direct output (all clusters of G are cliques), chain queue (a
-    // cluster of G is an eps-chain: its order depends on arrival order, so G
-    // is replayed in column order by leaf_chain_kernel), or full exact re-run.
-    const bool direct = gap_ok && !clique_bad;
-    const bool chain = gap_ok && clique_bad;
-
-    // Global ids of G's positions, then order each cluster by global id.
-    uint32_t sg[kSeq];
+            for (int q = 0; q < 4; ++q) {
 #pragma unroll
-    for (int i = 0; i < kSeq; ++i)
-        sg[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? p.gids[mem_lds[sc[i]]] : kEmptyId;
-    bool need_sort = false;
-#pragma unroll
-    for (int i = 1; i < kSeq; ++i) need_sort |= (i <= q_end) && (cid[i] == cid[i - 1]);
-    if (__any(row_ok && direct && need_sort)) {
-        // odd-even transposition sort by global id inside each cluster of G
-        // (sorted once an even and an odd phase in a row swap nothing)
-        for (int pass = 0; pass < kSeq + 2; pass += 2) {
-            bool swapped = false;
-#pragma unroll
-            for (int i = 0; i + 1 < kSeq; i += 2) {
-                const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
-                const uint32_t ga = sg[i], gb = sg[i + 1];
-                const float da = sd[i], db = sd[i + 1];
-                sg[i] = sw ? gb : ga;
-                sg[i + 1] = sw ? ga : gb;
-                sd[i] = sw ? db : da;
-                sd[i + 1] = sw ? da : db;
-                swapped |= sw;
-            }
-#pragma unroll
-            for (int i = 1; i + 1 < kSeq; i += 2) {
-                const bool sw = (i + 1) <= q_end && cid[i] == cid[i + 1] && sg[i] > sg[i + 1];
-                const uint32_t ga = sg[i], gb = sg[i + 1];
-                const float da = sd[i], db = sd[i + 1];
-                sg[i] = sw ? gb : ga;
-                sg[i + 1] = sw ? ga : gb;
-                sd[i] = sw ? db : da;
-                sd[i + 1] = sw ? da : db;
-                swapped |= sw;
-            }
-            if (!__any(swapped)) break;
-        }
-    }
-
-    uint32_t fallbacks = 0, chains = 0, done_rows = 0, final_cands = 0;
-    if (row_ok) {
-        if (direct) {
-            const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
-            // lane h writes slots [16h, 16h + 16)
-#pragma unroll
-            for (int i = 0; i < kTop; ++i) {
-                if ((uint32_t)i >= p.k) continue;
-                if ((i >> 4) != (int)h) continue;
-                const bool live = (uint32_t)i < keff;
-                p.out_ids[out + i] = live ? sg[i] : kEmptyId;
-                p.out_dists[out + i] = live ? sd[i] : kEmptyDist;
-            }
-            done_rows = h == 0u ? 1u : 0u;
-        } else if (h == 0u) {
-            bool queued = false;
-            const uint32_t m = (uint32_t)q_end + 1u;
-            if (chain) {
-                const uint32_t off = atomicAdd(p.chain_pool_used, m);
-                if (off + m <= p.chain_pool_capacity) {
-                    const uint32_t idx = atomicAdd(p.chain_count, 1u);
-                    if (idx < p.chain_capacity) {
-#pragma unroll
-                        for (int i = 0; i < kSeq; ++i)
-                            if ((uint32_t)i < m) p.chain_pool[off + i] = make_uint2(__float_as_uint(sd[i]), sc[i]);
-                        p.chain_rows[idx] = make_uint4(leaf, r, off, m);
-                        queued = true;
-                        chains = 1;
-                        final_cands = m;
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const int vi = 4 * q + e;
+                    const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
+                    const bool ok = row_ok && c < n && c != r;
+                    v[vi] = ok ? leaf_l2(acc[vi], rs, rn, cs_lds[c < n ? c : 0], cn_lds[c < n ? c : 0])
+                               : __builtin_inff();
                 }
             }
-            if (!queued) {
-                fallbacks = 1;
-                const uint32_t idx = atomicAdd(p.fallback_count, 1u);
-                if (idx < p.fallback_capacity) {
-                    p.fallback[2 * idx] = leaf;
-                    p.fallback[2 * idx + 1] = r;
-                } else {
-                    flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+            bitonic_sort_v<16>(v);
+#pragma unroll
+            for (int i = 0; i < kSample; ++i) samp[i] = fminf(samp[i], v[kSample - 1 - i]);
+            bitonic_merge_v<kSample>(samp);
+        }
+        float F = -__builtin_inff();
+        if (rsel > 0) F = __fadd_rn(pair_kth<kSample>(samp, rsel), kFilterMargin);
+        // tau: necessary condition on cs * dot for d <= F
+        const float tau = !row_ok ? __builtin_inff()
+                          : (F == -__builtin_inff() ? __builtin_inff() : filter_bound(F, rs, rn, cn_min, cn_max));
+
+        // ---- phase B: every tile, survivors (cs*dot >= tau) to the log ------------
+        uint32_t cnt = 0;
+        __syncthreads();
+        load_tile(0);
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            __syncthreads();
+            store_tile();
+            __syncthreads();
+            if (t + 1 < ntiles) load_tile(t + 1);
+            const v16i acc = mfma_tile();
+            const uint32_t cbase = t * kTileCols;
+            const bool checked =
+                __builtin_amdgcn_readfirstlane((t == diag_tile || cbase + kTileCols > n || !wave_rows_full) ? 1 : 0);
+            auto epilogue = [&](auto check_tag) {
+                constexpr bool kCheck = decltype(check_tag)::value;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 cs4 = *reinterpret_cast<const float4 *>(cs_lds + cbase + 8 * q + 4 * h);
+                    const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int vi = 4 * q + e;
+                        const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
+                        bool take = __fmul_rn((float)acc[vi], csv[e]) >= tau;
+                        if (kCheck) take = take && row_ok && c < n && c != r;
+                        if (take) {
+                            if (cnt < cap) slog[cnt] = make_uint2((uint32_t)acc[vi], c);
+                            ++cnt;
+                        }
+                    }
+                }
+            };
+            if (checked) epilogue(std::true_type{});
+            else epilogue(std::false_type{});
+        }
+        s_tiles += ntiles + (ntiles + 3u) / 4u;
+
+        // ---- final: fold the log, merge the pair, certify, order, write -----------
+        // The log entries were written by this thread's global stores above; the
+        // fence waits for them and drops stale cached lines before they are read.
+        __threadfence();
+        float topd[kTop];
+        uint32_t topc[kTop];
+#pragma unroll
+        for (int i = 0; i < kTop; ++i) {
+            topd[i] = __builtin_inff();
+            topc[i] = 0xffffu;
+        }
+        float disc = __builtin_inff();
+        const bool lane_ovf = cnt > cap;
+        const int logged = (int)(cnt < cap ? cnt : cap);
+        fold_staged(slog, cs_lds, cn_lds, n, logged, rs, rn, topd, topc, disc);
+        s_surv += logged;
+        s_ovf += lane_ovf ? 1u : 0u;
+        // pair flag through a ballot (a lane-mask value, not a shuffled register)
+        const uint64_t ovf_mask = __ballot(lane_ovf);
+        const bool pair_ovf = ((ovf_mask >> lane) & 1ull) != 0ull || ((ovf_mask >> (lane ^ 32u)) & 1ull) != 0ull;
+
+        // Known sequence: the pair's 32 smallest sorted (positions 0..31) and the
+        // 8 smallest of the rest (32..39).  Everything not known is > min(disc, F).
+        constexpr int kSeq = kTop + 8;
+        float sd[kSeq];
+        uint32_t sc[kSeq];
+        {
+            // Lower / upper halves of (own ascending) vs (partner descending):
+            // positions i and 31-i are handled together so the partner's
+            // entries are read (by shuffle) before either is overwritten.
+            float hi[kTop];
+            uint32_t phi[kTop];
+#pragma unroll
+            for (int i = 0; i < kTop / 2; ++i) {
+                const int i2 = kTop - 1 - i;
+                const float b0 = __shfl_xor(topd[i2], 32);
+                const uint32_t bc0 = __shfl_xor(topc[i2], 32);
+                const float b1 = __shfl_xor(topd[i], 32);
+                const uint32_t bc1 = __shfl_xor(topc[i], 32);
+                const float a0 = topd[i], a1 = topd[i2];
+                const uint32_t c0 = topc[i], c1 = topc[i2];
+                const bool sw0 = b0 < a0, sw1 = b1 < a1;
+                topd[i] = sw0 ? b0 : a0;
+                topc[i] = sw0 ? bc0 : c0;
+                hi[i] = sw0 ? a0 : b0;
+                phi[i] = sw0 ? c0 : bc0;
+                topd[i2] = sw1 ? b1 : a1;
+                topc[i2] = sw1 ? bc1 : c1;
+                hi[i2] = sw1 ? a1 : b1;
+                phi[i2] = sw1 ? c1 : bc1;
+            }
+            bitonic_merge_kv<kTop>(topd, topc);
+            // half-cleaners keep the lower half of a bitonic sequence: 32 -> 16 -> 8,
+            // then a bitonic merge sorts those 8
+#pragma unroll
+            for (int w = 16; w >= 8; w >>= 1) {
+#pragma unroll
+                for (int i = 0; i < w; ++i) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
+            }
+#pragma unroll
+            for (int w = 4; w >= 1; w >>= 1) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if ((i & w) == 0) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
+            }
+#pragma unroll
+            for (int i = 0; i < kTop; ++i) {
+                sd[i] = topd[i];
+                sc[i] = topc[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sd[kTop + i] = hi[i];
+                sc[kTop + i] = phi[i];
+            }
+        }
+        // not known: filtered (d > F) or evicted from a lane's list (>= disc)
+        const float disc_all = fminf(fminf(disc, __shfl_xor(disc, 32)), F);
+
+        // Tie clusters over the sorted known sequence; bit i of `same` says
+        // positions i and i+1 are in one cluster (swaps below stay inside
+        // clusters, so the bits keep their meaning).
+        int q_end = (int)keff - 1;   // last index of G
+        bool extending = keff > 0u;
+        bool clique_bad = false;
+        float cstart = sd[0];
+        uint64_t same = 0ull;
+#pragma unroll
+        for (int i = 1; i < kSeq; ++i) {
+            const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
+            same |= tie ? (1ull << (i - 1)) : 0ull;
+            const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
+            cstart = tie ? cstart : sd[i];
+            if (i >= (int)keff && extending) {
+                if (tie) q_end = i;
+                else extending = false;
+            }
+            clique_bad |= span_bad && (i <= q_end || (extending && i >= (int)keff));
+        }
+        // Gap certificate: the cluster holding s_{keff-1} closes inside the known
+        // sequence and the next distance after it -- known or not -- is > eps away.
+        bool gap_ok = (keff == 0u || !extending) && !pair_ovf;
+        if (keff > 0u && gap_ok) {
+            float theta = sd[0];
+            float next = disc_all;
+#pragma unroll
+            for (int i = 1; i < kSeq; ++i) {
+                theta = (i == q_end) ? sd[i] : theta;  // static indices only: no scratch
+                next = (i == q_end + 1) ? fminf(next, sd[i]) : next;
+            }
+            gap_ok = next == __builtin_inff() || __fsub_rn(next, theta) > kTieEps;
+        }
+        // Test knob: re-run every `debug_rerun_every`-th row through the exact kernel.
+        if (p.debug_rerun_every != 0u && (r % p.debug_rerun_every) == 0u) gap_ok = false;
+        // Outcome: direct output (all clusters of G are cliques), chain queue (a
+        // cluster of G is an eps-chain: its order depends on arrival order, so G
+        // is replayed in column order by leaf_chain_kernel), or full exact re-run.
+        const bool direct = gap_ok && !clique_bad;
+        const bool chain = gap_ok && clique_bad;
+
+        // Direct rows: global ids of G's positions (then each cluster is ordered
+        // by global id).  Other rows keep the columns for the chain queue.
+#pragma unroll
+        for (int i = 0; i < kSeq; ++i)
+            sc[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? p.gids[mem_lds[sc[i]]] : sc[i];
+        const uint64_t in_g = q_end >= 1 ? ((q_end >= 64 ? ~0ull : ((1ull << q_end) - 1ull))) : 0ull;
+        const bool need_sort = (same & in_g) != 0ull;
+        if (__any(row_ok && direct && need_sort)) {
+            // odd-even transposition sort by global id inside each cluster of G
+            // (sorted once an even and an odd phase in a row swap nothing)
+            const uint64_t mask = (row_ok && direct) ? (same & in_g) : 0ull;
+            for (int pass = 0; pass < kSeq + 2; pass += 2) {
+                bool swapped = false;
+#pragma unroll
+                for (int i = 0; i + 1 < kSeq; i += 2) {
+                    const bool sw = ((mask >> i) & 1ull) && sc[i] > sc[i + 1];
+                    const uint32_t ga = sc[i], gb = sc[i + 1];
+                    const float da = sd[i], db = sd[i + 1];
+                    sc[i] = sw ? gb : ga;
+                    sc[i + 1] = sw ? ga : gb;
+                    sd[i] = sw ? db : da;
+                    sd[i + 1] = sw ? da : db;
+                    swapped |= sw;
+                }
+#pragma unroll
+                for (int i = 1; i + 1 < kSeq; i += 2) {
+                    const bool sw = ((mask >> i) & 1ull) && sc[i] > sc[i + 1];
+                    const uint32_t ga = sc[i], gb = sc[i + 1];
+                    const float da = sd[i], db = sd[i + 1];
+                    sc[i] = sw ? gb : ga;
+                    sc[i + 1] = sw ? ga : gb;
+                    sd[i] = sw ? db : da;
+                    sd[i + 1] = sw ? da : db;
+                    swapped |= sw;
+                }
+                if (!__any(swapped)) break;
+            }
+        }
+
+        if (row_ok) {
+            if (direct) {
+                const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
+                // lane h writes slots [16h, 16h + 16)
+#pragma unroll
+                for (int i = 0; i < kTop; ++i) {
+                    if ((uint32_t)i >= p.k) continue;
+                    if ((i >> 4) != (int)h) continue;
+                    const bool live = (uint32_t)i < keff;
+                    p.out_ids[out + i] = live ? sc[i] : kEmptyId;
+                    p.out_dists[out + i] = live ? sd[i] : kEmptyDist;
+                }
+                s_done += h == 0u ? 1u : 0u;
+            } else if (h == 0u) {
+                bool queued = false;
+                const uint32_t m = (uint32_t)q_end + 1u;
+                if (chain) {
+                    const uint32_t off = atomicAdd(p.chain_pool_used, m);
+                    if (off + m <= p.chain_pool_capacity) {
+                        const uint32_t idx = atomicAdd(p.chain_count, 1u);
+                        if (idx < p.chain_capacity) {
+#pragma unroll
+                            for (int i = 0; i < kSeq; ++i)
+                                if ((uint32_t)i < m)
+                                    p.chain_pool[off + i] = make_uint2(__float_as_uint(sd[i]), sc[i]);
+                            p.chain_rows[idx] = make_uint4(leaf, r, off, m);
+                            queued = true;
+                            s_ch += 1;
+                            s_fc += m;
+                        }
+                    }
+                }
+                if (!queued) {
+                    s_fb += 1;
+                    const uint32_t idx = atomicAdd(p.fallback_count, 1u);
+                    if (idx < p.fallback_capacity) {
+                        p.fallback[2 * idx] = leaf;
+                        p.fallback[2 * idx + 1] = r;
+                    } else {
+                        flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+                    }
                 }
             }
         }
     }
 
     // One atomic per counter per wave.
-    uint64_t s_surv = survivors, s_fb = fallbacks, s_done = done_rows, s_ch = chains, s_fc = final_cands;
+    uint64_t a_surv = s_surv, a_fb = s_fb, a_done = s_done, a_ch = s_ch, a_fc = s_fc, a_ovf = s_ovf;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        s_surv += __shfl_xor(s_surv, off);
-        s_fb += __shfl_xor(s_fb, off);
-        s_done += __shfl_xor(s_done, off);
-        s_ch += __shfl_xor(s_ch, off);
-        s_fc += __shfl_xor(s_fc, off);
+        a_surv += __shfl_xor(a_surv, off);
+        a_fb += __shfl_xor(a_fb, off);
+        a_done += __shfl_xor(a_done, off);
+        a_ch += __shfl_xor(a_ch, off);
+        a_fc += __shfl_xor(a_fc, off);
+        a_ovf += __shfl_xor(a_ovf, off);
     }
     if (lane == 0) {
-        counter_add(p.counters, TESSA_C_LEAF_SURVIVORS, s_surv);
-        counter_add(p.counters, TESSA_C_LEAF_FALLBACK_ROWS, s_fb);
-        counter_add(p.counters, TESSA_C_LEAF_GAP_FALLBACK_ROWS, s_fb);
-        counter_add(p.counters, TESSA_C_LEAF_CHAIN_ROWS, s_ch);
-        counter_add(p.counters, TESSA_C_LEAF_FINAL_CANDIDATES, s_fc);
-        counter_add(p.counters, TESSA_C_LEAF_ROWS, s_done);
-        counter_add(p.counters, TESSA_C_LEAF_REFINES, refines);
-        counter_add(p.counters, TESSA_C_LEAF_MFMA_TILES, ntiles);
+        counter_add(p.counters, TESSA_C_LEAF_SURVIVORS, a_surv);
+        counter_add(p.counters, TESSA_C_LEAF_FALLBACK_ROWS, a_fb);
+        counter_add(p.counters, TESSA_C_LEAF_GAP_FALLBACK_ROWS, a_fb);
+        counter_add(p.counters, TESSA_C_LEAF_CHAIN_ROWS, a_ch);
+        counter_add(p.counters, TESSA_C_LEAF_FINAL_CANDIDATES, a_fc);
+        counter_add(p.counters, TESSA_C_LEAF_ROWS, a_done);
+        counter_add(p.counters, TESSA_C_LEAF_LIST_OVERFLOW_ROWS, a_ovf);
+        if (wave == 0) counter_add(p.counters, TESSA_C_LEAF_MFMA_TILES, s_tiles);
     }
 }
 
@@ -593,14 +682,21 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
         attr_set = true;
     }
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
-    if (stage_capacity(L::kTileBytes, cols_cap) < 17u) return -4;  // a tile adds up to 16 per lane
+    const uint32_t lds = lds_bytes(L::kTileBytes, cols_cap);
+    if (lds > kLdsBudget) return -4;
     const uint32_t blocks_per_leaf = (p.max_leaf_rows + kRowsPerBlock - 1) / kRowsPerBlock;
     const uint64_t total = (uint64_t)blocks_per_leaf * p.leaf_count;
     if (total == 0) return 0;
     if (total > 0x7fffff00ull) return -2;
-    const uint32_t padded = (uint32_t)((total + 7) / 8 * 8);
-    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(padded), dim3(kThreads), lds_bytes(L::kTileBytes, cols_cap),
-                       stream, p, blocks_per_leaf, (uint32_t)total, padded);
+    const uint32_t per_xcd = (uint32_t)((total + 7) / 8);
+    // persistent grid: each workgroup owns one survivor-log slot for its lifetime
+    uint32_t grid = p.log_slots;
+    const uint64_t need = (uint64_t)per_xcd * 8u;
+    if (need < grid) grid = (uint32_t)need;
+    grid = grid / 8u * 8u;
+    if (grid == 0) return -5;
+    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(grid), dim3(kThreads), lds, stream, p, blocks_per_leaf,
+                       (uint32_t)total, per_xcd);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -65,6 +65,8 @@ struct DeviceWorkspace {
     uint64_t chain_capacity = 0;
     uint2 *chain_pool = nullptr;
     uint64_t pool_capacity = 0;
+    uint2 *survivor_log = nullptr;  // slots x 256 threads x kLeafLogCapacity entries
+    uint64_t log_entries = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
@@ -103,6 +105,12 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     st = grow(&ws.chain_rows, &ws.chain_capacity, rows / 2 + 1, sizeof(uint4), "chain queue");
     if (st.code) return st;
     st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint2), "chain pool");
+    if (st.code) return st;
+    // one log slot per persistent MFMA workgroup: enough for every 128-row block
+    // of this batch, at most kLeafLogSlots
+    const uint64_t blocks = (rows + 127) / 128;
+    const uint64_t slots = ((blocks < kLeafLogSlots ? blocks : kLeafLogSlots) + 7) / 8 * 8;
+    st = grow(&ws.survivor_log, &ws.log_entries, slots * 256 * kLeafLogCapacity, sizeof(uint2), "survivor log");
     if (st.code) return st;
     *out = &ws;
     return ok_status();
@@ -281,6 +289,12 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.chain_pool = ws->chain_pool;
     p.chain_pool_used = ws->queue_counts + 2;
     p.chain_pool_capacity = clamp32(ws->pool_capacity);
+    p.survivor_log = ws->survivor_log;
+    p.log_capacity = kLeafLogCapacity;
+    {
+        const uint64_t slots = ws->log_entries / (256ull * kLeafLogCapacity);
+        p.log_slots = (uint32_t)(slots < kLeafLogSlots ? slots : kLeafLogSlots);
+    }
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
     hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->queue_counts, 3u, 0u);
     if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[0], s));
