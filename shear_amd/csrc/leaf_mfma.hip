@@ -444,9 +444,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         s_tiles += ntiles + (ntiles + 3u) / 4u;
 
         // ---- final: fold the log, merge the pair, certify, order, write -----------
-        // The log entries were written by this thread's global stores above; the
-        // fence waits for them and drops stale cached lines before they are read.
-        __threadfence();
+        // The log entries were written by this thread's global stores above.  A
+        // workgroup-scope fence waits for them; the workgroup's L1 serves all its
+        // waves, so no cache write-back or invalidation is needed (an agent-scope
+        // fence would write back L2 and costs more than the fold itself).
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
         float topd[kTop];
         uint32_t topc[kTop];
 #pragma unroll
