@@ -1,10 +1,15 @@
 // leaf_exact.hip -- exact scalar leaf top-k (the reference's DP4A role).
 //
 // One wavefront per (leaf, row).  Lanes compute 64 candidate distances at a
-// time with packed int8 dot4; lane 0 then pushes them, in member order, into
-// the row's 32-slot buffer with the reference insertion rule
-// (compute_backend.rs:7229-7259 / leaf_build.rs:887-957).  This kernel is the
-// semantic baseline on the GPU and re-runs rows the MFMA kernel flags.
+// time with packed int8 dot4; the candidates are then inserted, in member
+// order, into the row's k-slot buffer with the reference rule
+// (compute_backend.rs:7229-7259 / leaf_build.rs:887-957).  The buffer lives
+// in lanes 0..k-1 (slot j in lane j).  A candidate that does not beat the
+// buffer's tail is dropped, so one ballot finds the next candidate that can
+// enter; its insertion position is one past the highest slot it does not beat
+// (the reference's scan from the tail stops there) and the slots above shift
+// up by one lane.  This kernel is the semantic baseline on the GPU and
+// re-runs the rows the MFMA kernel cannot certify.
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
@@ -14,9 +19,38 @@ namespace {
 
 constexpr int kExactThreads = 64;
 
-__device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row,
-                          float *cd, uint32_t *cg, float *bd, uint32_t *bid) {
-    const uint32_t lane = threadIdx.x;
+// Insert candidate (cd, cg) into the lane-distributed buffer (bd, bg) of
+// length `len` <= keff; returns the new length.  Wave-uniform arguments.
+__device__ __forceinline__ uint32_t wave_insert(float cd, uint32_t cg, float &bd, uint32_t &bg, uint32_t len,
+                                                uint32_t keff) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const bool b = lane < len && beats(cd, cg, bd, bg);
+    uint32_t new_len = len;
+    uint64_t stop;
+    if (len < keff) {
+        new_len = len + 1u;
+        stop = __ballot(lane < len && !b);
+    } else {
+        const uint64_t bm = __ballot(b);
+        if (((bm >> (keff - 1u)) & 1ull) == 0ull) return len;  // does not beat the tail
+        stop = __ballot(lane + 1u < keff && !b);
+    }
+    const uint32_t pos = stop ? (uint32_t)(64 - __clzll((long long)stop)) : 0u;
+    const float ud = __shfl(bd, (int)((lane + 63u) & 63u));
+    const uint32_t ug = __shfl(bg, (int)((lane + 63u) & 63u));
+    if (lane > pos && lane < new_len) {
+        bd = ud;
+        bg = ug;
+    }
+    if (lane == pos) {
+        bd = cd;
+        bg = cg;
+    }
+    return new_len;
+}
+
+__device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row) {
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n = p.member_counts[leaf];
     if (row >= n) return;
     const uint32_t *mem = p.members + p.member_offsets[leaf];
@@ -29,12 +63,10 @@ __device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row,
     const int8_t *rc = p.codes + (uint64_t)self * p.padded_dim;
     const float rs = p.scales[self];
     const float rn = p.norms[self];
-    if (lane < kMaxK) {
-        bd[lane] = kEmptyDist;
-        bid[lane] = kEmptyId;
-    }
-    __syncthreads();
-    for (uint32_t base = 0; base < n; base += kExactThreads) {
+    float bd = kEmptyDist;
+    uint32_t bg = kEmptyId;
+    uint32_t len = 0;
+    for (uint32_t base = 0; base < n && keff > 0u; base += kExactThreads) {
         const uint32_t c = base + lane;
         float d = kEmptyDist;
         uint32_t g = kEmptyId;
@@ -45,54 +77,42 @@ __device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row,
                 flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
                 ok = false;
             } else {
-                int dot = dot_i8_rows(rc, p.codes + (uint64_t)cj * p.padded_dim, p.padded_dim);
+                const int dot = dot_i8_rows(rc, p.codes + (uint64_t)cj * p.padded_dim, p.padded_dim);
                 d = leaf_l2(dot, rs, rn, p.scales[cj], p.norms[cj]);
                 g = p.gids[cj];
             }
         }
-        cd[lane] = ok ? d : -1.0f;  // -1 marks "no candidate"
-        cg[lane] = g;
-        __syncthreads();
-        if (lane == 0 && keff > 0) {
-            const uint32_t m = (n - base < (uint32_t)kExactThreads) ? (n - base) : kExactThreads;
-            for (uint32_t j = 0; j < m; ++j) {
-                const float dj = cd[j];
-                if (dj < 0.0f) continue;
-                const uint32_t gj = cg[j];
-                // compute_backend.rs:7229-7259 insertion (empty slots hold FLT_MAX).
-                if (!beats(dj, gj, bd[keff - 1], bid[keff - 1])) continue;
-                uint32_t pos = keff - 1;
-                while (pos > 0 && beats(dj, gj, bd[pos - 1], bid[pos - 1])) {
-                    bd[pos] = bd[pos - 1];
-                    bid[pos] = bid[pos - 1];
-                    --pos;
-                }
-                bd[pos] = dj;
-                bid[pos] = gj;
+        // candidates in member order; skip those that cannot enter the full buffer
+        uint32_t next = 0;
+        while (true) {
+            bool cand = ok && lane >= next;
+            if (len == keff) {
+                const float td = __shfl(bd, (int)(keff - 1u));
+                const uint32_t tg = __shfl(bg, (int)(keff - 1u));
+                cand = cand && beats(d, g, td, tg);
             }
+            const uint64_t m = __ballot(cand);
+            if (m == 0ull) break;
+            const uint32_t i = (uint32_t)(__ffsll((long long)m) - 1);
+            len = wave_insert(__shfl(d, (int)i), __shfl(g, (int)i), bd, bg, len, keff);
+            next = i + 1u;
         }
-        __syncthreads();
     }
     const uint64_t out = p.output_offsets[leaf] + (uint64_t)row * p.k;
     if (lane < p.k) {
-        p.out_ids[out + lane] = lane < keff ? bid[lane] : kEmptyId;
-        p.out_dists[out + lane] = lane < keff ? bd[lane] : kEmptyDist;
+        p.out_ids[out + lane] = lane < len ? bg : kEmptyId;
+        p.out_dists[out + lane] = lane < len ? bd : kEmptyDist;
     }
-    __syncthreads();
 }
 
 __global__ __launch_bounds__(kExactThreads) void leaf_exact_all_kernel(LeafParams p) {
-    __shared__ float cd[kExactThreads];
-    __shared__ uint32_t cg[kExactThreads];
-    __shared__ float bd[kMaxK];
-    __shared__ uint32_t bid[kMaxK];
     const uint64_t total = (uint64_t)p.leaf_count * p.max_leaf_rows;
     uint64_t done = 0;
     for (uint64_t w = blockIdx.x; w < total; w += gridDim.x) {
         const uint32_t leaf = (uint32_t)(w / p.max_leaf_rows);
         const uint32_t row = (uint32_t)(w % p.max_leaf_rows);
         if (row < p.member_counts[leaf]) {
-            exact_row(p, leaf, row, cd, cg, bd, bid);
+            exact_row(p, leaf, row);
             ++done;
         }
     }
@@ -103,15 +123,11 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_all_kernel(LeafParam
 }
 
 __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(LeafParams p) {
-    __shared__ float cd[kExactThreads];
-    __shared__ uint32_t cg[kExactThreads];
-    __shared__ float bd[kMaxK];
-    __shared__ uint32_t bid[kMaxK];
     uint32_t count = *p.fallback_count;
     if (count > p.fallback_capacity) count = p.fallback_capacity;
     uint64_t done = 0;
     for (uint32_t w = blockIdx.x; w < count; w += gridDim.x) {
-        exact_row(p, p.fallback[2 * w], p.fallback[2 * w + 1], cd, cg, bd, bid);
+        exact_row(p, p.fallback[2 * w], p.fallback[2 * w + 1]);
         ++done;
     }
     if (threadIdx.x == 0) {
@@ -127,11 +143,8 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(Leaf
 // neither enter in front of G's nor stay in the buffer.
 //
 // One wave per queued row.  Lane i holds G's i-th entry; a bitonic sort across
-// lanes orders G by column.  The bounded insertion (leaf_build.rs:913-951)
-// then runs with the k slots spread over lanes 0..k-1: for a candidate c each
-// lane evaluates "c beats slot j"; the reference scan from the tail stops at
-// the highest slot c does not beat, so the insertion position is one past it
-// (a ballot), and the slots from there up shift by one (a lane shuffle).
+// lanes orders G by column; then G is replayed through wave_insert (the
+// bounded insertion of leaf_build.rs:913-951 with slots in lanes).
 constexpr int kChainMax = 64;
 constexpr int kChainWaves = 4;
 
@@ -178,33 +191,8 @@ __global__ __launch_bounds__(kChainWaves * 64) void leaf_chain_kernel(LeafParams
         float bd = kEmptyDist;
         uint32_t bg = kEmptyId;
         uint32_t len = 0;
-        for (uint32_t i = 0; i < m && keff > 0u; ++i) {
-            const float cd = __shfl(d, (int)i);
-            const uint32_t cg = __shfl(g, (int)i);
-            const bool b = lane < len && beats(cd, cg, bd, bg);
-            uint32_t new_len = len;
-            uint64_t stop;
-            if (len < keff) {
-                new_len = len + 1u;
-                stop = __ballot(lane < len && !b);
-            } else {
-                const uint64_t bm = __ballot(b);
-                if (((bm >> (keff - 1u)) & 1ull) == 0ull) continue;  // does not beat the tail
-                stop = __ballot(lane + 1u < keff && !b);
-            }
-            const uint32_t pos = stop ? (uint32_t)(64 - __clzll((long long)stop)) : 0u;
-            const float ud = __shfl(bd, (int)((lane + 63u) & 63u));
-            const uint32_t ug = __shfl(bg, (int)((lane + 63u) & 63u));
-            if (lane > pos && lane < new_len) {
-                bd = ud;
-                bg = ug;
-            }
-            if (lane == pos) {
-                bd = cd;
-                bg = cg;
-            }
-            len = new_len;
-        }
+        for (uint32_t i = 0; i < m && keff > 0u; ++i)
+            len = wave_insert(__shfl(d, (int)i), __shfl(g, (int)i), bd, bg, len, keff);
         const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
         if (lane < p.k) {
             const bool live = lane < len;
