@@ -19,6 +19,21 @@ namespace {
 
 constexpr int kExactThreads = 64;
 
+// Lane i receives lane i-1's value (DPP wave shift; lane 0 keeps its own).
+__device__ __forceinline__ uint32_t wave_shr1(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float wave_shr1(float v) {
+    return __uint_as_float(wave_shr1(__float_as_uint(v)));
+}
+// Broadcast of lane `i` (wave-uniform index).
+__device__ __forceinline__ uint32_t lane_bcast(uint32_t v, uint32_t i) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)i);
+}
+__device__ __forceinline__ float lane_bcast(float v, uint32_t i) {
+    return __uint_as_float(lane_bcast(__float_as_uint(v), i));
+}
+
 // Insert candidate (cd, cg) into the lane-distributed buffer (bd, bg) of
 // length `len` <= keff; returns the new length.  Wave-uniform arguments.
 __device__ __forceinline__ uint32_t wave_insert(float cd, uint32_t cg, float &bd, uint32_t &bg, uint32_t len,
@@ -36,8 +51,8 @@ __device__ __forceinline__ uint32_t wave_insert(float cd, uint32_t cg, float &bd
         stop = __ballot(lane + 1u < keff && !b);
     }
     const uint32_t pos = stop ? (uint32_t)(64 - __clzll((long long)stop)) : 0u;
-    const float ud = __shfl(bd, (int)((lane + 63u) & 63u));
-    const uint32_t ug = __shfl(bg, (int)((lane + 63u) & 63u));
+    const float ud = wave_shr1(bd);
+    const uint32_t ug = wave_shr1(bg);
     if (lane > pos && lane < new_len) {
         bd = ud;
         bg = ug;
@@ -87,14 +102,14 @@ __device__ void exact_row(const LeafParams &p, uint32_t leaf, uint32_t row) {
         while (true) {
             bool cand = ok && lane >= next;
             if (len == keff) {
-                const float td = __shfl(bd, (int)(keff - 1u));
-                const uint32_t tg = __shfl(bg, (int)(keff - 1u));
+                const float td = lane_bcast(bd, keff - 1u);
+                const uint32_t tg = lane_bcast(bg, keff - 1u);
                 cand = cand && beats(d, g, td, tg);
             }
             const uint64_t m = __ballot(cand);
             if (m == 0ull) break;
             const uint32_t i = (uint32_t)(__ffsll((long long)m) - 1);
-            len = wave_insert(__shfl(d, (int)i), __shfl(g, (int)i), bd, bg, len, keff);
+            len = wave_insert(lane_bcast(d, i), lane_bcast(g, i), bd, bg, len, keff);
             next = i + 1u;
         }
     }
@@ -153,24 +168,24 @@ __global__ __launch_bounds__(kChainWaves * 64) void leaf_chain_kernel(LeafParams
     const uint32_t wave = threadIdx.x >> 6;
     uint32_t count = *p.chain_count;
     if (count > p.chain_capacity) count = p.chain_capacity;
+    const uint32_t stride = gridDim.x * kChainWaves;
     uint64_t done = 0;
-    for (uint32_t w = blockIdx.x * kChainWaves + wave; w < count; w += gridDim.x * kChainWaves) {
-        const uint4 hdr = p.chain_rows[w];
-        const uint32_t leaf = hdr.x, r = hdr.y, off = hdr.z;
-        const uint32_t m = hdr.w < (uint32_t)kChainMax ? hdr.w : (uint32_t)kChainMax;
-        const uint32_t n = p.member_counts[leaf];
-        const uint32_t *mem = p.members + p.member_offsets[leaf];
-        const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
-        uint32_t col = 0xffffffffu;
-        float d = kEmptyDist;
-        uint32_t g = kEmptyId;
-        if (lane < m) {
-            const uint2 e = p.chain_pool[off + lane];
-            col = e.y;
-            d = __uint_as_float(e.x);
-            const uint32_t mc = col < n ? mem[col] : 0u;
-            g = mc < p.rows ? p.gids[mc] : kEmptyId;
-        }
+    uint32_t w = blockIdx.x * kChainWaves + wave;
+    // software pipeline: the next row's header and pool entry load while the
+    // current row is sorted and replayed
+    uint4 hdr = w < count ? p.chain_rows[w] : make_uint4(0u, 0u, 0u, 0u);
+    uint4 e = make_uint4(__float_as_uint(kEmptyDist), 0xffffffffu, kEmptyId, 0u);
+    if (w < count && lane < (hdr.w & 0xffu)) e = p.chain_pool[hdr.z + lane];
+    while (w < count) {
+        const uint32_t wn = w + stride;
+        const uint4 hdr_n = wn < count ? p.chain_rows[wn] : make_uint4(0u, 0u, 0u, 0u);
+        const uint64_t out = (uint64_t)hdr.x | ((uint64_t)hdr.y << 32);
+        uint32_t m = hdr.w & 0xffu;
+        m = m < (uint32_t)kChainMax ? m : (uint32_t)kChainMax;
+        const uint32_t keff = (hdr.w >> 8) & 0xffu;
+        uint32_t col = lane < m ? e.y : 0xffffffffu;
+        float d = lane < m ? __uint_as_float(e.x) : kEmptyDist;
+        uint32_t g = lane < m ? e.z : kEmptyId;
         // bitonic sort of the 64 lanes by column (padding lanes sort last)
 #pragma unroll
         for (uint32_t kk = 2; kk <= 64; kk <<= 1) {
@@ -187,19 +202,21 @@ __global__ __launch_bounds__(kChainWaves * 64) void leaf_chain_kernel(LeafParams
                 g = take ? og : g;
             }
         }
+        if (wn < count && lane < (hdr_n.w & 0xffu)) e = p.chain_pool[hdr_n.z + lane];
         // bounded insertion over G in column order; slot j lives in lane j
         float bd = kEmptyDist;
         uint32_t bg = kEmptyId;
         uint32_t len = 0;
         for (uint32_t i = 0; i < m && keff > 0u; ++i)
-            len = wave_insert(__shfl(d, (int)i), __shfl(g, (int)i), bd, bg, len, keff);
-        const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
+            len = wave_insert(lane_bcast(d, i), lane_bcast(g, i), bd, bg, len, keff);
         if (lane < p.k) {
             const bool live = lane < len;
             p.out_ids[out + lane] = live ? bg : kEmptyId;
             p.out_dists[out + lane] = live ? bd : kEmptyDist;
         }
         done += lane == 0u ? 1u : 0u;
+        hdr = hdr_n;
+        w = wn;
     }
     if (lane == 0) counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
 }

@@ -32,12 +32,13 @@ struct LeafParams {
     // certification and are re-run by the exact kernel (0 = off).
     uint32_t debug_rerun_every;
     // Rows whose certified candidate set G holds an eps-tie chain: header
-    // (leaf, row, pool offset, |G|) plus |G| pool entries (f32 bits, column),
-    // replayed in column order by the chain kernel.
+    // (output offset lo/hi, pool offset, |G| | k_eff << 8) plus |G| pool
+    // entries (f32 bits, column, global id, 0), replayed in column order by
+    // the chain kernel.
     uint4 *chain_rows;
     uint32_t *chain_count;
     uint32_t chain_capacity;
-    uint2 *chain_pool;
+    uint4 *chain_pool;
     uint32_t *chain_pool_used;
     uint32_t chain_pool_capacity;
     // MFMA kernel survivor log: one slot per persistent workgroup, holding

@@ -625,11 +625,15 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                     if (off + m <= p.chain_pool_capacity) {
                         const uint32_t idx = atomicAdd(p.chain_count, 1u);
                         if (idx < p.chain_capacity) {
+                            // pool entry: (distance bits, column, global id); header:
+                            // (output offset, pool offset, m | keff << 8)
 #pragma unroll
                             for (int i = 0; i < kSeq; ++i)
                                 if ((uint32_t)i < m)
-                                    p.chain_pool[off + i] = make_uint2(__float_as_uint(sd[i]), sc[i]);
-                            p.chain_rows[idx] = make_uint4(leaf, r, off, m);
+                                    p.chain_pool[off + i] = make_uint4(__float_as_uint(sd[i]), sc[i],
+                                                                       p.gids[mem_lds[sc[i] < n ? sc[i] : 0u]], 0u);
+                            const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
+                            p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), off, m | (keff << 8));
                             queued = true;
                             s_ch += 1;
                             s_fc += m;

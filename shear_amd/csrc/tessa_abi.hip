@@ -63,7 +63,7 @@ struct DeviceWorkspace {
     uint64_t fallback_capacity = 0;
     uint4 *chain_rows = nullptr;
     uint64_t chain_capacity = 0;
-    uint2 *chain_pool = nullptr;
+    uint4 *chain_pool = nullptr;
     uint64_t pool_capacity = 0;
     uint2 *survivor_log = nullptr;  // slots x 256 threads x kLeafLogCapacity entries
     uint64_t log_entries = 0;
@@ -104,7 +104,7 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     // correctness.
     st = grow(&ws.chain_rows, &ws.chain_capacity, rows / 2 + 1, sizeof(uint4), "chain queue");
     if (st.code) return st;
-    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint2), "chain pool");
+    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint4), "chain pool");
     if (st.code) return st;
     // one log slot per persistent MFMA workgroup: enough for every 128-row block
     // of this batch, at most kLeafLogSlots
