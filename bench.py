@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-json", default=None,
                     help="profiles/*.json with measured HBM bytes per launch (rocprofv3 --pmc)")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the timed steps, run one int32 elementwise copy kernel of this many MiB "
+                         "(read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE can be scaled")
     return ap.parse_args()
 
 
@@ -120,6 +123,16 @@ def main() -> int:
     T.raise_on_overflow(ctr, "leaf top-k")
     c = ctr.cpu().numpy()
     log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, launch median {np.median(launch_ms):.3f} ms")
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 18
+        src = torch.ones(n, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.add(src, 1, out=dst)  # one plain elementwise kernel: n*4 B read, n*4 B written
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n * 4} B read, {n * 4} B written")
+        del src, dst
 
     pairs = leaves * LEAF_ROWS * (LEAF_ROWS - 1)
     ops = 2.0 * DIM * pairs

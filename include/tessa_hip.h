@@ -25,6 +25,8 @@
  *   tessa_session_leaf_topk /    TessaCudaReplaySession::run_mode leaf / assignment legs
  *   tessa_session_assign_replay  (tessa_replay.rs:190-200 TessaCudaModeResult)
  *   tessa_overflow_labels        compute_backend.rs:2249-2296 gpu_persistent_overflow_labels
+ *   tessa_emit_edge_records      leaf_build.rs:1679-1829 flush_compact_topk_batch_into_edges
+ *                                (records: spill_hashprune.rs:137-145 SpillRecord16)
  */
 #ifndef TESSA_HIP_H
 #define TESSA_HIP_H
@@ -352,6 +354,55 @@ typedef struct tessa_subtree_output {
 
 tessa_status tessa_session_run_subtree(tessa_session *session, const tessa_subtree_request *req,
                                        tessa_subtree_output *out);
+
+/* ---- candidate records -> HashPrune edge records ------------------------
+ * Replaces the host conversion flush_compact_topk_batch_into_edges
+ * (leaf_build.rs:1679-1829) that SHEAR runs on every CompactTopKBatch the
+ * subtree operator returns (compute_backend.rs:32243-32339 builds one per
+ * leaf: leaf_id = leaf index, point_ids = global ids of the leaf's rows,
+ * k = min(leaf_knn, rows - 1)).  Each slot (j, d) of member row i with
+ * j != 0xffffffff and finite d yields two records, in the reference's order
+ * (leaf, row, rank; forward then reverse):
+ *   {src i, dst j, hash compute_hash(s_i, s_j), flags 0, d}
+ *   {src j, dst i, hash compute_hash(s_j, s_i), flags 0, d}
+ * compute_hash (hash_prune.rs:2239-2251): bit b = (s_c[b] - s_p[b] >= 0),
+ * b < m_bits.  Records use the SpillRecord16 layout
+ * (spill_hashprune.rs:137-145).  flags is 0: HashPrune evidence annotation and
+ * compact lune pruning (reference options, off by default) are not offered. */
+typedef struct tessa_edge_record {
+    uint32_t src;    /* PendingEdge.p */
+    uint32_t dst;    /* PendingEdge.c */
+    uint16_t hash;
+    uint16_t flags;  /* HashPruneMeta spill flags */
+    float dist;
+} tessa_edge_record;
+
+/* SketchAccessor rows (hash_prune.rs:21-36, SketchStore :60-72) on device:
+ * sketch_rows x width f32, row = global point id; m_bits = params.m_hash_bits
+ * (1..16, <= width). */
+typedef struct tessa_sketch_view {
+    const float *rows;
+    uint64_t sketch_rows;
+    uint32_t width;
+    uint32_t m_bits;
+} tessa_sketch_view;
+
+/* Device arrays in, device records out; leaves/topk as written by
+ * tessa_leaf_topk (output slot of (leaf l, row r, rank q) =
+ * output_offsets[l] + r*k + q; per leaf k = min(k, n-1); max_leaf_rows <=
+ * 4096), global_ids[resident_rows] maps member rows to point ids.  out holds
+ * out_capacity records; leaf_record_offsets (device, leaf_count + 1, may be
+ * NULL) receives each leaf's first record index and, last, the total.
+ * Synchronises `stream`; *record_count = records written.  Errors: a top-k id
+ * outside its leaf ("Compact top-k batch references point J outside leaf L",
+ * leaf_build.rs:1796-1801), a point without a sketch row, out_capacity below
+ * the record count (nothing written). */
+tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t resident_rows,
+                                     const tessa_leaf_batch *leaves, const uint32_t *topk_ids,
+                                     const float *topk_dists, const tessa_sketch_view *sketches,
+                                     tessa_edge_record *out, uint64_t out_capacity,
+                                     uint64_t *leaf_record_offsets, uint64_t *record_count,
+                                     void *stream);
 
 /* "QUEUE_NODE|LEAF_ROW|..." or "none" (same labels as the reference). */
 void tessa_overflow_labels(uint64_t flags, char *buf, size_t len);

@@ -78,6 +78,11 @@ def lib():
         _lib.orc_subtree_partition.restype = C.c_int
         _lib.orc_subtree_partition.argtypes = [P, P, P, C.c_size_t, C.c_size_t, C.POINTER(SubtreeCfg), P, P, P,
                                                P, P, P]
+        _lib.orc_compute_hash.restype = C.c_uint16
+        _lib.orc_compute_hash.argtypes = [P, P, C.c_uint]
+        _lib.orc_flush_compact_topk_into_edges.restype = C.c_longlong
+        _lib.orc_flush_compact_topk_into_edges.argtypes = [P, C.c_size_t, C.c_size_t, P, P, P, C.c_size_t,
+                                                           C.c_size_t, C.c_uint, P, C.c_size_t, P]
     return _lib
 
 
@@ -305,3 +310,37 @@ def subtree_partition(codes, scales, norms, *, seed: int, root_depth: int = 0, m
         return None, ctr
     leaves = [leaf_rows[int(starts[i]): int(starts[i]) + int(sizes[i])].copy() for i in range(n_leaves)]
     return leaves, ctr
+
+
+# spill_hashprune.rs:137-145 SpillRecord16 (little-endian, 16 bytes)
+EDGE_DTYPE = np.dtype([("src", "<u4"), ("dst", "<u4"), ("hash", "<u2"), ("flags", "<u2"), ("dist", "<f4")])
+
+
+def compute_hash(sketch_p, sketch_c, m_bits: int) -> int:
+    sp = np.ascontiguousarray(sketch_p, np.float32)
+    sc = np.ascontiguousarray(sketch_c, np.float32)
+    return int(lib().orc_compute_hash(_p(sp), _p(sc), m_bits))
+
+
+class EdgeError(ValueError):
+    def __init__(self, code: int, point: int):
+        super().__init__(f"orc_flush_compact_topk_into_edges: {code} (point {point})")
+        self.code = code
+        self.point = point
+
+
+def flush_compact_topk_into_edges(point_ids, k: int, topk_ids, topk_dists, sketches, m_bits: int):
+    """One CompactTopKBatch -> SpillRecord16 records (EDGE_DTYPE array).
+    sketches: [sketch_rows, width] f32, row = global point id."""
+    pids = np.ascontiguousarray(point_ids, np.uint32)
+    ids = np.ascontiguousarray(topk_ids, np.uint32)
+    d = np.ascontiguousarray(topk_dists, np.float32)
+    sk = np.ascontiguousarray(sketches, np.float32)
+    rows = len(pids)
+    out = np.zeros(max(2 * rows * k, 1), EDGE_DTYPE)
+    bad = C.c_uint32(0)
+    n = lib().orc_flush_compact_topk_into_edges(_p(pids), rows, k, _p(ids), _p(d), _p(sk), sk.shape[0],
+                                                sk.shape[1], m_bits, _p(out), len(out), C.byref(bad))
+    if n < 0:
+        raise EdgeError(int(n), bad.value)
+    return out[:n]

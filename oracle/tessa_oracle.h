@@ -26,6 +26,10 @@
  *   orc_assign_replay     hash64 == SplitMix64 finalizer known outputs; without
  *                         near-ties equals the strict (dist, id) order of the
  *                         CPU D0 path (orc_assign_strict).
+ *   orc_compute_hash /    the reference's own fixture batch (leaf_build.rs:3126-3137
+ *   orc_flush_compact_    with build_test_sketches :2900-2908), whose edges follow
+ *   topk_into_edges       in closed form; an independent numpy restatement on random
+ *                         batches; the empty-slot, non-finite and outside-leaf cases.
  */
 #ifndef TESSA_ORACLE_H
 #define TESSA_ORACLE_H
@@ -215,6 +219,35 @@ int orc_subtree_partition(const int8_t *codes, const float *scales, const float 
                           size_t resident_rows, size_t padded_dim, const orc_subtree_cfg *cfg,
                           uint32_t *leaf_row_ids, uint64_t *leaf_starts, uint64_t *leaf_sizes,
                           uint64_t *counters, uint64_t *leaf_count, uint64_t *leaf_rows);
+
+/* ---- candidate records -> HashPrune edges ------------------------------ */
+
+/* spill_hashprune.rs:137-145 SpillRecord16, the 16-byte form of PendingEdge
+ * (leaf_build.rs:59-65; flags = HashPruneMeta spill flags). */
+typedef struct orc_edge_record {
+    uint32_t src;
+    uint32_t dst;
+    uint16_t hash;
+    uint16_t flags;
+    float dist;
+} orc_edge_record;
+
+/* hash_prune.rs:2239-2251 compute_hash: bit i = (sketch_c[i] - sketch_p[i] >= 0). */
+uint16_t orc_compute_hash(const float *sketch_p, const float *sketch_c, unsigned m_bits);
+
+/* leaf_build.rs:1679-1829 flush_compact_topk_batch_into_edges for one
+ * CompactTopKBatch (leaf_build.rs:271-282), evidence annotation and compact
+ * lune pruning off (their defaults).  Sketch rows are indexed by global point
+ * id (LeafSketchCache::prefetch over batch.point_ids).  Appends 2 records per
+ * valid slot to out[0..capacity).  Returns the number written, or
+ *   -1  a top-k id is not a member of the batch (*bad_point = that id),
+ *   -2  m_bits > 16 or > width, or capacity too small,
+ *   -3  a point id has no sketch row (*bad_point = that id). */
+long long orc_flush_compact_topk_into_edges(const uint32_t *point_ids, size_t rows, size_t k,
+                                            const uint32_t *topk_ids, const float *topk_dists,
+                                            const float *sketches, size_t sketch_rows, size_t width,
+                                            unsigned m_bits, orc_edge_record *out, size_t capacity,
+                                            uint32_t *bad_point);
 
 #ifdef __cplusplus
 }

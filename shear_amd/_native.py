@@ -200,6 +200,27 @@ class SubtreeOutput(C.Structure):
     ]
 
 
+class EdgeRecord(C.Structure):
+    """tessa_edge_record: SpillRecord16 (spill_hashprune.rs:137-145)."""
+
+    _fields_ = [
+        ("src", C.c_uint32),
+        ("dst", C.c_uint32),
+        ("hash", C.c_uint16),
+        ("flags", C.c_uint16),
+        ("dist", C.c_float),
+    ]
+
+
+class SketchView(C.Structure):
+    _fields_ = [
+        ("rows", C.c_void_p),
+        ("sketch_rows", C.c_uint64),
+        ("width", C.c_uint32),
+        ("m_bits", C.c_uint32),
+    ]
+
+
 # Every symbol include/tessa_hip.h declares, with its ctypes signature.
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -231,6 +252,10 @@ SIGNATURES = {
     "tessa_session_run_subtree": (
         TessaStatus,
         [_P, C.POINTER(SubtreeRequest), C.POINTER(SubtreeOutput)],
+    ),
+    "tessa_emit_edge_records": (
+        TessaStatus,
+        [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, C.POINTER(_U64), _P],
     ),
 }
 

@@ -16,6 +16,7 @@
 
 #include "../../include/tessa_hip.h"
 #include "assign_kernels.h"
+#include "edge_kernels.h"
 #include "leaf_kernels.h"
 #include "partition.h"
 #include "tessa_device.h"
@@ -67,6 +68,13 @@ struct DeviceWorkspace {
     uint64_t pool_capacity = 0;
     uint2 *survivor_log = nullptr;  // slots x 256 threads x kLeafLogCapacity entries
     uint64_t log_entries = 0;
+    // edge-record kernels: per-leaf totals, leaf record offsets, status words
+    uint32_t *edge_totals = nullptr;
+    uint64_t edge_totals_capacity = 0;
+    uint64_t *edge_base = nullptr;
+    uint64_t edge_base_capacity = 0;
+    uint64_t *edge_status = nullptr;
+    uint64_t edge_status_capacity = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
@@ -113,6 +121,15 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     st = grow(&ws.survivor_log, &ws.log_entries, slots * 256 * kLeafLogCapacity, sizeof(uint2), "survivor log");
     if (st.code) return st;
     *out = &ws;
+    return ok_status();
+}
+
+tessa_status device_workspace(DeviceWorkspace **out) {
+    int dev = 0;
+    TESSA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    *out = &g_ws[dev];
     return ok_status();
 }
 
@@ -975,6 +992,112 @@ tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_req
                            "overflow_labels=%s (leaf top-k)",
                            (unsigned long long)rows, (unsigned long long)lc[TESSA_C_OVERFLOW_FLAGS], labels);
     }
+    return ok_status();
+}
+
+}  // extern "C"
+
+// ---- candidate records -> edge records -----------------------------------------
+
+extern "C" {
+
+tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t resident_rows, const tessa_leaf_batch *lb,
+                                     const uint32_t *topk_ids, const float *topk_dists,
+                                     const tessa_sketch_view *sk, tessa_edge_record *out, uint64_t out_capacity,
+                                     uint64_t *leaf_record_offsets, uint64_t *record_count, void *stream) {
+    static_assert(sizeof(tessa_edge_record) == 16, "SpillRecord16 is 16 bytes");
+    if (record_count) *record_count = 0;
+    if (!global_ids || !lb || !topk_ids || !topk_dists || !sk || !sk->rows || !record_count)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge records: null argument");
+    if (!lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
+    if (lb->k == 0 || lb->k > (uint32_t)kMaxK)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf k=%u outside [1, 32]", lb->k);
+    if (sk->m_bits == 0 || sk->m_bits > 16 || sk->m_bits > sk->width)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "m_hash_bits=%u must be in [1, min(16, width=%u)]",
+                           sk->m_bits, sk->width);
+    if (lb->max_leaf_rows > kEdgeMaxLeafRows)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "edge records: max_leaf_rows=%u above %u", lb->max_leaf_rows,
+                           kEdgeMaxLeafRows);
+    if (lb->leaf_count > 0 && !out && out_capacity > 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge records: null output with capacity %llu",
+                           (unsigned long long)out_capacity);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    DeviceWorkspace *ws = nullptr;
+    tessa_status st = device_workspace(&ws);
+    if (st.code) return st;
+    const uint64_t leaves = lb->leaf_count;
+    st = grow(&ws->edge_totals, &ws->edge_totals_capacity, leaves + 1, sizeof(uint32_t), "edge leaf totals");
+    if (st.code) return st;
+    st = grow(&ws->edge_status, &ws->edge_status_capacity, kEdgeStatusWords, sizeof(uint64_t), "edge status");
+    if (st.code) return st;
+    if (!leaf_record_offsets) {
+        st = grow(&ws->edge_base, &ws->edge_base_capacity, leaves + 1, sizeof(uint64_t), "edge leaf offsets");
+        if (st.code) return st;
+    }
+    EdgeParams p{};
+    p.gids = global_ids;
+    p.resident_rows = resident_rows;
+    p.members = lb->members;
+    p.member_offsets = lb->member_offsets;
+    p.member_counts = lb->member_counts;
+    p.output_offsets = lb->output_offsets;
+    p.leaf_count = lb->leaf_count;
+    p.k = lb->k;
+    p.topk_ids = topk_ids;
+    p.topk_dists = topk_dists;
+    p.sketches = sk->rows;
+    p.sketch_rows = sk->sketch_rows;
+    p.width = sk->width;
+    p.m_bits = sk->m_bits;
+    p.out = reinterpret_cast<uint4 *>(out);
+    p.out_capacity = out ? out_capacity : 0;
+    p.leaf_totals = ws->edge_totals;
+    p.leaf_base = leaf_record_offsets ? leaf_record_offsets : ws->edge_base;
+    p.status = ws->edge_status;
+    if (launch_edge_records(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "edge record kernel launch failed");
+    uint64_t w[kEdgeStatusWords];
+    TESSA_HIP_TRY(hipMemcpyAsync(w, p.status, sizeof(w), hipMemcpyDeviceToHost, s));
+    TESSA_HIP_TRY(hipStreamSynchronize(s));
+    if (w[kEdgeLeafTooLarge])
+        return make_status(TESSA_ERR_OVERFLOW, TESSA_OVF_LEAF_ROW,
+                           "edge records: a leaf of %llu rows exceeds %u overflow_flags=0x%llx overflow_labels=LEAF_ROW",
+                           (unsigned long long)(w[kEdgeLeafTooLarge] - 1), kEdgeMaxLeafRows,
+                           (unsigned long long)TESSA_OVF_LEAF_ROW);
+    if (w[kEdgeFirstError] != ~0ull) {
+        const uint64_t key = w[kEdgeFirstError];
+        const uint64_t leaf = key >> 20;
+        const uint64_t kind = (key >> 19) & 1u;
+        const uint32_t row = (uint32_t)((key >> 6) & 0x1fffu);
+        const uint32_t rank = (uint32_t)(key & 63u);
+        if (kind == kEdgeErrOutside) {
+            uint64_t out0 = 0;
+            uint32_t j = 0;
+            TESSA_HIP_TRY(hipMemcpy(&out0, lb->output_offsets + leaf, sizeof(out0), hipMemcpyDeviceToHost));
+            TESSA_HIP_TRY(hipMemcpy(&j, topk_ids + out0 + (uint64_t)row * lb->k + rank, sizeof(j),
+                                    hipMemcpyDeviceToHost));
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                               "Compact top-k batch references point %u outside leaf %llu", j,
+                               (unsigned long long)leaf);
+        }
+        uint64_t moff = 0;
+        uint32_t mr = 0, g = 0xffffffffu;
+        TESSA_HIP_TRY(hipMemcpy(&moff, lb->member_offsets + leaf, sizeof(moff), hipMemcpyDeviceToHost));
+        TESSA_HIP_TRY(hipMemcpy(&mr, lb->members + moff + row, sizeof(mr), hipMemcpyDeviceToHost));
+        if (mr < resident_rows) TESSA_HIP_TRY(hipMemcpy(&g, global_ids + mr, sizeof(g), hipMemcpyDeviceToHost));
+        if (mr >= resident_rows)
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, TESSA_OVF_INVALID_TOPK_ROW_ID,
+                               "leaf %llu row %u: resident row %u outside %llu rows overflow_flags=0x%llx "
+                               "overflow_labels=INVALID_TOPK_ROW_ID",
+                               (unsigned long long)leaf, row, mr, (unsigned long long)resident_rows,
+                               (unsigned long long)TESSA_OVF_INVALID_TOPK_ROW_ID);
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf %llu point %u has no sketch row (sketch rows %llu)",
+                           (unsigned long long)leaf, g, (unsigned long long)sk->sketch_rows);
+    }
+    if (w[kEdgeCapacityHit])
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge record capacity %llu below the %llu records needed",
+                           (unsigned long long)p.out_capacity, (unsigned long long)w[kEdgeRecordCount]);
+    *record_count = w[kEdgeRecordCount];
     return ok_status();
 }
 

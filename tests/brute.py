@@ -297,3 +297,32 @@ def partition(codes, scales, norms, *, seed, root_depth=0, max_depth=10, max_lea
                     leaves.extend(kids)
         level = nxt
     return leaves, flags
+
+
+# ---- candidate records -> edges (leaf_build.rs:1679-1829) ---------------------------
+
+def compute_hash(sp, sc, m_bits: int) -> int:
+    """hash_prune.rs:2239-2251, vectorised over the bits."""
+    diff = np.asarray(sc, np.float32)[:m_bits] - np.asarray(sp, np.float32)[:m_bits]
+    bits = (diff >= np.float32(0)).astype(np.uint32)
+    return int((bits << np.arange(m_bits, dtype=np.uint32)).sum())
+
+
+def flush_edges(point_ids, k, topk_ids, topk_dists, sketches, m_bits):
+    """List of (src, dst, hash, flags, dist bits) in the reference's push order."""
+    pids = np.asarray(point_ids, np.uint32)
+    members = set(int(p) for p in pids)
+    ids = np.asarray(topk_ids, np.uint32).reshape(len(pids), k) if k else np.zeros((len(pids), 0), np.uint32)
+    ds = np.asarray(topk_dists, np.float32).reshape(len(pids), k) if k else np.zeros((len(pids), 0), np.float32)
+    out = []
+    for i, gi in enumerate(pids.tolist()):
+        for q in range(k):
+            j, d = int(ids[i, q]), ds[i, q]
+            if j == 0xFFFFFFFF or not np.isfinite(d):
+                continue
+            if j not in members:
+                raise KeyError(j)
+            dbits = int(np.float32(d).view(np.uint32))
+            out.append((gi, j, compute_hash(sketches[gi], sketches[j], m_bits), 0, dbits))
+            out.append((j, gi, compute_hash(sketches[j], sketches[gi], m_bits), 0, dbits))
+    return out

@@ -46,6 +46,8 @@ def test_struct_layouts_match_header_sizes():
     assert C.sizeof(N.TessaStatus) == 8 + 8 + 512
     assert C.sizeof(N.LeafBatch) == 4 * 8 + 6 * 4
     assert C.sizeof(N.Sq8View) == 4 * 8 + 8 + 4 + 4
+    assert C.sizeof(N.EdgeRecord) == 16  # SpillRecord16
+    assert C.sizeof(N.SketchView) == 8 + 8 + 4 + 4
 
 
 def test_missing_library_fails_loudly(tmp_path):
