@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-json", default=None,
                     help="profiles/*.json with measured HBM bytes per launch (rocprofv3 --pmc)")
+    ap.add_argument("--no-edges", action="store_true",
+                    help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the timed steps, run one int32 elementwise copy kernel of this many MiB "
                          "(read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE can be scaled")
@@ -200,10 +202,54 @@ def main() -> int:
         "cpu_baseline": None,
     }
 
+    if not args.no_edges:
+        result["record_emission"] = edge_leg(gids, lay, out_ids, out_d, stream, args.steps, args.warmup)
+
     if not args.no_cpu_baseline:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def edge_leg(gids, lay, out_ids, out_d, stream, steps, warmup):
+    """Record emission over the step's top-k output: every slot -> the two
+    SpillRecord16 edge records of flush_compact_topk_batch_into_edges, with
+    12-bit hashes from random 12-wide sketches (row = global id)."""
+    import torch
+
+    from shear_amd import edges as E
+
+    dev = out_ids.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    sketches = torch.randn((gids.numel(), 12), generator=gen, device=dev, dtype=torch.float32)
+    rec = torch.empty((2 * lay.output_len, 4), dtype=torch.int32, device=dev)
+    ms = []
+    count = 0
+    for i in range(warmup + steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        _, count = E.emit_edge_records(gids, lay, K, out_ids, out_d, sketches, 12, out=rec, stream=stream)
+        b.record(stream)
+        b.synchronize()
+        if i >= warmup:
+            ms.append(a.elapsed_time(b))
+    t = float(np.mean(ms)) / 1e3
+    slots = lay.output_len
+    log(f"record emission: {count} records, {np.mean(ms):.3f} ms")
+    del rec, sketches
+    return {
+        "kernels": "edge_count_kernel + edge_scan_kernel + edge_emit_kernel",
+        "records": count,
+        "ms_mean": round(float(np.mean(ms)), 4),
+        "ms_min": round(float(np.min(ms)), 4),
+        "slot_gb_per_s": round(slots * 8 / t / 1e9, 2),        # rows*k*8 / t
+        "record_write_gb_per_s": round(count * 16 / t / 1e9, 2),
+        # slots read once, records written once, one sketch row per point
+        "hbm_bytes_algorithmic": slots * 8 + count * 16 + gids.numel() * 48,
+        "hbm_gb_per_s_algorithmic": round((slots * 8 + count * 16 + gids.numel() * 48) / t / 1e9, 2),
+        "peak_gb_per_s": HBM_PEAK_GBS,
+    }
 
 
 def cpu_baseline(sq8, out_ids, out_d, budget_s):

@@ -7,7 +7,8 @@
 
 namespace tessa {
 
-// Largest leaf the edge kernels take (LDS membership table of 2x that size).
+// Largest leaf the edge kernels take (LDS: row counts, member ids and a
+// membership table of 2x that size, 64 KB at this bound).
 constexpr uint32_t kEdgeMaxLeafRows = 4096;
 
 // Status words written by the edge kernels (device u64[4]).
@@ -15,7 +16,7 @@ enum EdgeStatusWord : uint32_t {
     kEdgeRecordCount = 0,  // records the batch needs (2 per valid slot)
     kEdgeFirstError = 1,   // smallest error key, UINT64_MAX when none (see edge_error_key)
     kEdgeCapacityHit = 2,  // 1 when out_capacity was too small (nothing written)
-    kEdgeLeafTooLarge = 3, // 1 + largest leaf above kEdgeMaxLeafRows (such leaves emit nothing)
+    kEdgeLeafTooLarge = 3, // 1 + largest leaf above max_leaf_rows (such leaves emit nothing)
     kEdgeStatusWords = 4
 };
 
@@ -36,6 +37,8 @@ struct EdgeParams {
     const uint32_t *member_counts;
     const uint64_t *output_offsets;  // slot of (leaf, row 0, rank 0)
     uint32_t leaf_count;
+    uint32_t max_leaf_rows;          // <= kEdgeMaxLeafRows; larger leaves are reported, not emitted
+    uint32_t table_bits;             // edge_table_bits(max_leaf_rows)
     uint32_t k;                      // slot stride; per leaf k = min(k, n - 1)
     const uint32_t *topk_ids;
     const float *topk_dists;
@@ -50,6 +53,8 @@ struct EdgeParams {
     uint64_t *status;                // kEdgeStatusWords
 };
 
+// log2 of the LDS membership table size: >= 2 x max_leaf_rows, >= 64.
+uint32_t edge_table_bits(uint32_t max_leaf_rows);
 int launch_edge_records(const EdgeParams &p, hipStream_t stream);
 
 }  // namespace tessa

@@ -28,44 +28,84 @@
 namespace tessa {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr uint32_t kTableBits = 13;  // 8192 slots >= 2 x kEdgeMaxLeafRows
-constexpr uint32_t kTableSize = 1u << kTableBits;
+constexpr int kCountUnroll = 4;  // rows per half-wave in flight (count pass)
+constexpr int kEmitUnroll = 4;   // rows per half-wave in flight (emit pass)
 constexpr uint32_t kNoKey = 0xffffffffu;
+constexpr uint32_t kLeafRegular = 0x80000000u;  // leaf_totals flag: every row has k_eff valid slots
+constexpr size_t kEmitLdsBudget = 80 * 1024;  // two 512-thread workgroups per CU
 
 __device__ __forceinline__ bool slot_valid(uint32_t id, float d) {
     // j != u32::MAX && d.is_finite()
     return id != 0xffffffffu && (__float_as_uint(d) & 0x7f800000u) != 0x7f800000u;
 }
 
-__device__ __forceinline__ uint32_t table_hash(uint32_t g) { return (g * 0x9E3779B1u) >> (32 - kTableBits); }
+// Records are written once and never read back by these kernels: stream them
+// past the caches (nontemporal stores).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_record(uint4 *out, uint64_t i, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    u32x4 v = {a, b, c, d};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + i));
+}
+
+__device__ __forceinline__ uint32_t table_hash(uint32_t g, uint32_t bits) { return (g * 0x9E3779B1u) >> (32 - bits); }
 
 __device__ __forceinline__ uint32_t leaf_k(const EdgeParams &p, uint32_t n) {
     return n > 1u ? (p.k < n - 1u ? p.k : n - 1u) : 0u;
 }
 
+// Rows of a leaf, 1 + largest-leaf flag when a leaf exceeds max_leaf_rows
+// (its records are not emitted; the host reports LEAF_ROW).
+__device__ __forceinline__ uint32_t leaf_rows(const EdgeParams &p, uint32_t leaf, bool report) {
+    const uint32_t n = p.member_counts[leaf];
+    if (n <= p.max_leaf_rows) return n;
+    if (report && threadIdx.x == 0) atomicMax((unsigned long long *)&p.status[kEdgeLeafTooLarge], 1ull + n);
+    return 0u;
+}
+
 // Valid-slot count of every row of leaf `leaf` into cnt[0..n), then an
-// exclusive scan in place; returns the leaf total.  All threads call it.
+// exclusive scan in place; returns the leaf total and whether every row has
+// all of its k_eff slots valid (then row r's records start at 2*r*k_eff).
+// All threads call it.
+// Each half-wave owns a row (lane q = rank); kCountUnroll rows per half-wave
+// have their loads in flight together.
 __device__ uint32_t row_counts_scan(const EdgeParams &p, uint32_t leaf, uint32_t n, uint32_t kl, uint32_t *cnt,
-                                    uint32_t *wsum) {
+                                    uint32_t *wsum, bool &regular) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
     const uint32_t q = lane & 31u;
     const uint32_t h = lane >> 5;
     const uint64_t out0 = p.output_offsets[leaf];
-    for (uint32_t r0 = 2u * wave; r0 < n; r0 += 2u * kWaves) {
-        const uint32_t r = r0 + h;
-        bool valid = false;
-        if (r < n && q < kl) {
-            const uint64_t s = out0 + (uint64_t)r * p.k + q;
-            valid = slot_valid(p.topk_ids[s], p.topk_dists[s]);
+    constexpr uint32_t kStep = 2u * kWaves;
+    int irregular = 0;
+    for (uint32_t r0 = 2u * wave + h; r0 < n + h; r0 += kStep * kCountUnroll) {
+        uint32_t id[kCountUnroll];
+        float d[kCountUnroll];
+#pragma unroll
+        for (int u = 0; u < kCountUnroll; ++u) {
+            const uint32_t r = r0 + u * kStep;
+            id[u] = kNoKey;
+            d[u] = 0.0f;
+            if (r < n && q < kl) {
+                const uint64_t s = out0 + (uint64_t)r * p.k + q;
+                id[u] = p.topk_ids[s];
+                d[u] = p.topk_dists[s];
+            }
         }
-        const uint64_t m = __ballot(valid);
-        if (r < n && q == 0u) cnt[r] = __popcll(h ? (m >> 32) : (m & 0xffffffffull));
+#pragma unroll
+        for (int u = 0; u < kCountUnroll; ++u) {
+            const uint32_t r = r0 + u * kStep;
+            const uint64_t m = __ballot(slot_valid(id[u], d[u]));
+            const uint32_t c = __popcll(h ? (m >> 32) : (m & 0xffffffffull));
+            if (r < n && q == 0u) {
+                cnt[r] = c;
+                irregular |= c != kl ? 1 : 0;
+            }
+        }
     }
-    __syncthreads();
+    regular = __syncthreads_or(irregular) == 0;
     const uint32_t per = (n + kThreads - 1) / kThreads;
     const uint32_t b = tid * per;
     const uint32_t e = b + per < n ? b + per : n;
@@ -96,16 +136,15 @@ __device__ uint32_t row_counts_scan(const EdgeParams &p, uint32_t leaf, uint32_t
 }
 
 __global__ __launch_bounds__(kThreads) void edge_count_kernel(EdgeParams p) {
-    __shared__ uint32_t cnt[kEdgeMaxLeafRows];
-    __shared__ uint32_t wsum[kWaves];
+    extern __shared__ uint32_t lds[];
+    uint32_t *wsum = lds;
+    uint32_t *cnt = lds + kWaves;
     for (uint32_t leaf = blockIdx.x; leaf < p.leaf_count; leaf += gridDim.x) {
-        uint32_t n = p.member_counts[leaf];
-        if (n > kEdgeMaxLeafRows) {
-            if (threadIdx.x == 0) atomicMax((unsigned long long *)&p.status[kEdgeLeafTooLarge], 1ull + n);
-            n = 0;
-        }
-        const uint32_t total = row_counts_scan(p, leaf, n, leaf_k(p, n), cnt, wsum);
-        if (threadIdx.x == 0) p.leaf_totals[leaf] = total;
+        const uint32_t n = leaf_rows(p, leaf, true);
+        bool regular;
+        const uint32_t total = row_counts_scan(p, leaf, n, leaf_k(p, n), cnt, wsum, regular);
+        // total <= 4096 * 32: bit 31 is free for the regular-leaf flag
+        if (threadIdx.x == 0) p.leaf_totals[leaf] = total | (regular ? kLeafRegular : 0u);
     }
 }
 
@@ -117,7 +156,7 @@ __global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
     uint64_t carry = 0;
     for (uint32_t base = 0; base < p.leaf_count; base += 1024u) {
         const uint32_t i = base + tid;
-        const uint64_t v = i < p.leaf_count ? p.leaf_totals[i] : 0ull;
+        const uint64_t v = i < p.leaf_count ? (p.leaf_totals[i] & ~kLeafRegular) : 0ull;
         uint64_t x = v;
 #pragma unroll
         for (uint32_t off = 1; off < 64; off <<= 1) {
@@ -141,10 +180,66 @@ __global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
     }
 }
 
+// compute_hash(s_i, s_j) and compute_hash(s_j, s_i) over m_bits coordinates.
+// kVec4: both rows are 16-byte aligned with at least ceil(m_bits/4)*4 floats.
+template <bool kVec4>
+__device__ __forceinline__ void pair_hashes(const float *si, const float *sj, uint32_t m_bits, uint32_t &hf,
+                                            uint32_t &hr) {
+    hf = 0u;
+    hr = 0u;
+    if (kVec4) {
+        const float4 *a4 = reinterpret_cast<const float4 *>(si);
+        const float4 *c4 = reinterpret_cast<const float4 *>(sj);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            if (4u * v >= m_bits) break;
+            const float4 a = a4[v], c = c4[v];
+            const float av[4] = {a.x, a.y, a.z, a.w};
+            const float cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t bit = 4u * v + e;
+                if (bit < m_bits) {
+                    hf |= (cv[e] - av[e] >= 0.0f ? 1u : 0u) << bit;
+                    hr |= (av[e] - cv[e] >= 0.0f ? 1u : 0u) << bit;
+                }
+            }
+        }
+    } else {
+        for (uint32_t bit = 0; bit < m_bits; ++bit) {
+            const float a = si[bit], c = sj[bit];
+            hf |= (c - a >= 0.0f ? 1u : 0u) << bit;
+            hr |= (a - c >= 0.0f ? 1u : 0u) << bit;
+        }
+    }
+}
+
+// Sketch access modes of the emit kernel.
+enum SketchMode : int {
+    kSketchGlobal = 0,    // scalar loads from the sketch rows in HBM
+    kSketchGlobalV4 = 1,  // float4 loads (width % 4 == 0, 16-byte aligned base)
+    kSketchLds = 2        // the leaf's sketch rows staged in LDS (float4 reads)
+};
+
+// LDS words of the emit kernel: wave sums | row counts | member ids | table
+// keys | table values (u16) | (16-byte aligned) staged sketches.
+__host__ __device__ inline uint32_t emit_sketch_offset(uint32_t max_rows, uint32_t table_bits) {
+    const uint32_t words = kWaves + 2u * max_rows + (1u << table_bits) + (1u << table_bits) / 2u;
+    return (words + 3u) & ~3u;
+}
+
+template <int kMode>
 __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
-    __shared__ uint32_t cnt[kEdgeMaxLeafRows];
-    __shared__ uint32_t table[kTableSize];
-    __shared__ uint32_t wsum[kWaves];
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const uint32_t tbits = p.table_bits;
+    const uint32_t tmask = (1u << tbits) - 1u;
+    uint32_t *wsum = lds;
+    uint32_t *cnt = lds + kWaves;
+    uint32_t *gid = cnt + p.max_leaf_rows;
+    uint32_t *tkey = gid + p.max_leaf_rows;
+    uint16_t *tval = reinterpret_cast<uint16_t *>(tkey + (1u << tbits));
+    float *sk_lds = reinterpret_cast<float *>(lds + emit_sketch_offset(p.max_leaf_rows, tbits));
+    const uint32_t mw = (p.m_bits + 3u) & ~3u;  // staged row stride (floats)
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
@@ -155,77 +250,141 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
         return;  // uniform over the grid: nothing is written
     }
     for (uint32_t leaf = blockIdx.x; leaf < p.leaf_count; leaf += gridDim.x) {
-        uint32_t n = p.member_counts[leaf];
-        n = n <= kEdgeMaxLeafRows ? n : 0u;  // reported by the count kernel
+        const uint32_t n = leaf_rows(p, leaf, false);
         const uint32_t kl = leaf_k(p, n);
         const uint32_t *mem = p.members + p.member_offsets[leaf];
-        for (uint32_t i = tid; i < kTableSize; i += kThreads) table[i] = kNoKey;
-        row_counts_scan(p, leaf, n, kl, cnt, wsum);  // ends with a barrier (table cleared)
-        // Membership table of the leaf's global ids.  A point without a
+        for (uint32_t i = tid; i <= tmask; i += kThreads) tkey[i] = kNoKey;
+        // Row record offsets: r * k_eff for a regular leaf (every slot valid),
+        // else counted again and scanned into cnt.
+        const bool regular = (p.leaf_totals[leaf] & kLeafRegular) != 0u;
+        if (regular) {
+            __syncthreads();
+        } else {
+            bool unused;
+            row_counts_scan(p, leaf, n, kl, cnt, wsum, unused);  // ends with a barrier
+        }
+        // Member ids, the membership table (global id -> member position) and,
+        // in LDS mode, the m_bits leading coordinates of every member's sketch
+        // row (independent loads, all in flight together).  A point without a
         // resident row or sketch row is an error (the reference's sketch
-        // prefetch of the batch, leaf_build.rs:1758-1763) and is left out.
+        // prefetch of the batch, leaf_build.rs:1758-1763) and is left out of
+        // the table.
         for (uint32_t c = tid; c < n; c += kThreads) {
             const uint32_t mr = mem[c];
             const uint32_t g = mr < p.resident_rows ? p.gids[mr] : kNoKey;
-            if (mr >= p.resident_rows || g >= p.sketch_rows) {
+            const bool ok = mr < p.resident_rows && g < p.sketch_rows;
+            gid[c] = ok ? g : kNoKey;
+            if (kMode == kSketchLds) {
+                float v[16];
+                const float *row = p.sketches + (uint64_t)(ok ? g : 0u) * p.width;
+#pragma unroll
+                for (uint32_t bit = 0; bit < 16u; ++bit) v[bit] = (ok && bit < p.m_bits) ? row[bit] : 0.0f;
+#pragma unroll
+                for (uint32_t bit = 0; bit < 16u; ++bit)
+                    if (bit < mw) sk_lds[c * mw + bit] = v[bit];
+            }
+            if (!ok) {
                 atomicMin((unsigned long long *)&p.status[kEdgeFirstError],
                           (unsigned long long)edge_error_key(leaf, kEdgeErrSketch, c, 0));
                 continue;
             }
-            uint32_t slot = table_hash(g);
+            uint32_t slot = table_hash(g, tbits);
             while (true) {
-                const uint32_t prev = atomicCAS(&table[slot], kNoKey, g);
-                if (prev == kNoKey || prev == g) break;
-                slot = (slot + 1u) & (kTableSize - 1u);
+                const uint32_t prev = atomicCAS(&tkey[slot], kNoKey, g);
+                if (prev == kNoKey) {
+                    tval[slot] = (uint16_t)c;
+                    break;
+                }
+                if (prev == g) break;  // repeated id: the first position holds it
+                slot = (slot + 1u) & tmask;
             }
         }
         __syncthreads();
         const uint64_t out0 = p.output_offsets[leaf];
         const uint64_t rec0 = p.leaf_base[leaf];
-        for (uint32_t r0 = 2u * wave; r0 < n; r0 += 2u * kWaves) {
-            const uint32_t r = r0 + h;
-            bool valid = false;
-            uint32_t j = kNoKey;
-            float d = 0.0f;
-            if (r < n && q < kl) {
-                const uint64_t s = out0 + (uint64_t)r * p.k + q;
-                j = p.topk_ids[s];
-                d = p.topk_dists[s];
-                valid = slot_valid(j, d);
-            }
-            const uint64_t m = __ballot(valid);
-            if (!valid) continue;
-            const uint32_t half = (uint32_t)(h ? (m >> 32) : m);
-            const uint64_t pos = rec0 + 2ull * (cnt[r] + (uint32_t)__popc(half & ((1u << q) - 1u)));
-            const uint32_t mr = mem[r];
-            const uint32_t gi = mr < p.resident_rows ? p.gids[mr] : kNoKey;
-            // membership of j (leaf_build.rs:1783-1801)
-            bool member = false;
-            for (uint32_t slot = table_hash(j);; slot = (slot + 1u) & (kTableSize - 1u)) {
-                const uint32_t t = table[slot];
-                if (t == j) {
-                    member = true;
-                    break;
+        constexpr uint32_t kStep = 2u * kWaves;
+        for (uint32_t r0 = 2u * wave + h; r0 < n + h; r0 += kStep * kEmitUnroll) {
+            uint32_t j[kEmitUnroll];
+            float d[kEmitUnroll];
+#pragma unroll
+            for (int u = 0; u < kEmitUnroll; ++u) {
+                const uint32_t r = r0 + u * kStep;
+                j[u] = kNoKey;
+                d[u] = 0.0f;
+                if (r < n && q < kl) {
+                    const uint64_t s = out0 + (uint64_t)r * p.k + q;
+                    j[u] = p.topk_ids[s];
+                    d[u] = p.topk_dists[s];
                 }
-                if (t == kNoKey) break;
             }
-            if (!member) {
-                atomicMin((unsigned long long *)&p.status[kEdgeFirstError],
-                          (unsigned long long)edge_error_key(leaf, kEdgeErrOutside, r, q));
-                continue;
+#pragma unroll
+            for (int u = 0; u < kEmitUnroll; ++u) {
+                const uint32_t r = r0 + u * kStep;
+                const bool valid = slot_valid(j[u], d[u]);
+                const uint64_t m = __ballot(valid);
+                const uint32_t half = (uint32_t)(h ? (m >> 32) : m);
+                const uint32_t gi = r < n ? gid[r] : kNoKey;
+                // valid slots of the leaf before row r
+                const uint32_t row_rec = r < n ? (regular ? r * kl : cnt[r]) : 0u;
+                uint32_t hf = 0, hr = 0;
+                bool ok = false;
+                if (valid) {
+                    // membership of j (leaf_build.rs:1783-1801)
+                    uint32_t cj = kNoKey;
+                    for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask) {
+                        const uint32_t t = tkey[slot];
+                        if (t == j[u]) {
+                            cj = tval[slot];
+                            break;
+                        }
+                        if (t == kNoKey) break;
+                    }
+                    if (cj == kNoKey)
+                        atomicMin((unsigned long long *)&p.status[kEdgeFirstError],
+                                  (unsigned long long)edge_error_key(leaf, kEdgeErrOutside, r, q));
+                    ok = cj != kNoKey && gi != kNoKey;  // a missing sketch row is reported by the table build
+                    if (ok) {
+                        if (kMode == kSketchLds)
+                            pair_hashes<true>(sk_lds + r * mw, sk_lds + cj * mw, p.m_bits, hf, hr);
+                        else
+                            pair_hashes<kMode == kSketchGlobalV4>(p.sketches + (uint64_t)gi * p.width,
+                                                                  p.sketches + (uint64_t)j[u] * p.width, p.m_bits,
+                                                                  hf, hr);
+                    }
+                }
+                const uint32_t db = __float_as_uint(d[u]);
+                // Records of row r: 2 per valid slot, forward then reverse, from
+                // record rec0 + 2*row_rec.  When every row of the wave has its
+                // valid slots as a prefix of its ranks (always, for leaf top-k
+                // output), lane q of a half writes records q and 32 + q of its
+                // row, taking the slot's values by shuffle: 16-byte stores from
+                // consecutive lanes to consecutive addresses.
+                const uint64_t ok_mask = __ballot(ok);
+                if (__ballot((half & (half + 1u)) != 0u) == 0ull) {
+                    const uint32_t row_slots = (uint32_t)__popc(half);
+                    const uint64_t base = rec0 + 2ull * row_rec;
+#pragma unroll
+                    for (uint32_t pass = 0; pass < 2u; ++pass) {
+                        const uint32_t sidx = 16u * pass + (q >> 1);
+                        const uint32_t src = (h << 5) + sidx;
+                        const uint32_t js = __shfl(j[u], (int)src);
+                        const uint32_t ds = __shfl(db, (int)src);
+                        const uint32_t hfs = __shfl(hf, (int)src);
+                        const uint32_t hrs = __shfl(hr, (int)src);
+                        const bool oks = ((ok_mask >> src) & 1ull) != 0ull;
+                        if (sidx < row_slots && oks) {
+                            if (q & 1u)
+                                store_record(p.out, base + 32u * pass + q, js, gi, hrs, ds);
+                            else
+                                store_record(p.out, base + 32u * pass + q, gi, js, hfs, ds);
+                        }
+                    }
+                } else if (ok) {
+                    const uint64_t pos = rec0 + 2ull * (row_rec + (uint32_t)__popc(half & ((1u << q) - 1u)));
+                    store_record(p.out, pos, gi, j[u], hf, db);  // flags 0: evidence annotation off
+                    store_record(p.out, pos + 1, j[u], gi, hr, db);
+                }
             }
-            if (gi >= p.sketch_rows) continue;  // reported by the table build
-            const float *si = p.sketches + (uint64_t)gi * p.width;
-            const float *sj = p.sketches + (uint64_t)j * p.width;
-            uint32_t hf = 0, hr = 0;
-            for (uint32_t bit = 0; bit < p.m_bits; ++bit) {
-                const float a = si[bit], c = sj[bit];
-                hf |= (c - a >= 0.0f ? 1u : 0u) << bit;  // compute_hash(s_i, s_j)
-                hr |= (a - c >= 0.0f ? 1u : 0u) << bit;  // compute_hash(s_j, s_i)
-            }
-            const uint32_t db = __float_as_uint(d);
-            p.out[pos] = make_uint4(gi, j, hf, db);  // flags 0: evidence annotation off
-            p.out[pos + 1] = make_uint4(j, gi, hr, db);
         }
         __syncthreads();  // the next leaf clears the table
     }
@@ -237,13 +396,30 @@ __global__ void edge_status_init_kernel(uint64_t *status) {
 
 }  // namespace
 
+uint32_t edge_table_bits(uint32_t max_leaf_rows) {
+    uint32_t bits = 6;
+    while ((1u << bits) < 2u * max_leaf_rows) ++bits;
+    return bits;
+}
+
 int launch_edge_records(const EdgeParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(edge_status_init_kernel, dim3(1), dim3(64), 0, stream, p.status);
     if (p.leaf_count == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
-    const uint32_t grid = p.leaf_count < 4096u ? p.leaf_count : 4096u;
-    hipLaunchKernelGGL(edge_count_kernel, dim3(grid), dim3(kThreads), 0, stream, p);
+    const uint32_t grid = p.leaf_count < 8192u ? p.leaf_count : 8192u;
+    const size_t count_lds = (kWaves + (size_t)p.max_leaf_rows) * sizeof(uint32_t);
+    hipLaunchKernelGGL(edge_count_kernel, dim3(grid), dim3(kThreads), count_lds, stream, p);
     hipLaunchKernelGGL(edge_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
-    hipLaunchKernelGGL(edge_emit_kernel, dim3(grid), dim3(kThreads), 0, stream, p);
+    // Stage the leaf's sketch rows in LDS when that keeps two workgroups per
+    // CU; else read them from HBM (float4 loads when rows are 16-byte aligned).
+    const size_t base_lds = (size_t)emit_sketch_offset(p.max_leaf_rows, p.table_bits) * sizeof(uint32_t);
+    const size_t staged = (size_t)p.max_leaf_rows * ((p.m_bits + 3u) & ~3u) * sizeof(float);
+    const bool vec4 = p.width % 4u == 0u && (reinterpret_cast<uintptr_t>(p.sketches) & 15u) == 0u;
+    if (base_lds + staged <= kEmitLdsBudget)
+        hipLaunchKernelGGL(edge_emit_kernel<kSketchLds>, dim3(grid), dim3(kThreads), base_lds + staged, stream, p);
+    else if (vec4)
+        hipLaunchKernelGGL(edge_emit_kernel<kSketchGlobalV4>, dim3(grid), dim3(kThreads), base_lds, stream, p);
+    else
+        hipLaunchKernelGGL(edge_emit_kernel<kSketchGlobal>, dim3(grid), dim3(kThreads), base_lds, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -1043,6 +1043,8 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
     p.member_counts = lb->member_counts;
     p.output_offsets = lb->output_offsets;
     p.leaf_count = lb->leaf_count;
+    p.max_leaf_rows = lb->max_leaf_rows;
+    p.table_bits = edge_table_bits(lb->max_leaf_rows);
     p.k = lb->k;
     p.topk_ids = topk_ids;
     p.topk_dists = topk_dists;
@@ -1061,8 +1063,9 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
     TESSA_HIP_TRY(hipStreamSynchronize(s));
     if (w[kEdgeLeafTooLarge])
         return make_status(TESSA_ERR_OVERFLOW, TESSA_OVF_LEAF_ROW,
-                           "edge records: a leaf of %llu rows exceeds %u overflow_flags=0x%llx overflow_labels=LEAF_ROW",
-                           (unsigned long long)(w[kEdgeLeafTooLarge] - 1), kEdgeMaxLeafRows,
+                           "edge records: a leaf of %llu rows exceeds max_leaf_rows=%u overflow_flags=0x%llx "
+                           "overflow_labels=LEAF_ROW",
+                           (unsigned long long)(w[kEdgeLeafTooLarge] - 1), lb->max_leaf_rows,
                            (unsigned long long)TESSA_OVF_LEAF_ROW);
     if (w[kEdgeFirstError] != ~0ull) {
         const uint64_t key = w[kEdgeFirstError];

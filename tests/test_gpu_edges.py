@@ -75,14 +75,19 @@ def _batches(gids, members, offs, sizes, ids, d, k):
                                          ids.cpu().numpy().view(np.uint32), d.cpu().numpy(), k, k)
 
 
-@pytest.mark.parametrize("sizes,dim,k,m_bits", [
-    ([1, 2, 3, 33, 100, 257, 1024], 48, 32, 12),
-    ([64] * 20 + [5, 1, 700], 32, 8, 16),
-    ([4096, 900], 16, 32, 12),
-    ([300, 2, 2, 41], 96, 1, 1),
+# sketch access: rows staged in LDS for small leaves; float4 (width % 4 == 0)
+# or scalar loads from HBM when a 4096-row leaf does not fit the LDS budget
+@pytest.mark.parametrize("sizes,dim,k,m_bits,width", [
+    ([1, 2, 3, 33, 100, 257, 1024], 48, 32, 12, 16),
+    ([64] * 20 + [5, 1, 700], 32, 8, 16, 16),
+    ([4096, 900], 16, 32, 12, 16),
+    ([4096, 20], 16, 16, 13, 13),
+    ([300, 2, 2, 41], 96, 1, 1, 16),
+    ([500, 77], 24, 32, 7, 9),
 ])
-def test_leaf_output_records_match_oracle(gpu, orc, sizes, dim, k, m_bits):
-    gids, sk, members, offs, sizes, lay, g, ids, d = _leaf_case(orc, sizes, dim, k, len(sizes) + dim, m_bits)
+def test_leaf_output_records_match_oracle(gpu, orc, sizes, dim, k, m_bits, width):
+    gids, sk, members, offs, sizes, lay, g, ids, d = _leaf_case(orc, sizes, dim, k, len(sizes) + dim, m_bits,
+                                                                width)
     dsk = torch.from_numpy(sk).to(gpu)
     offsets = torch.empty(lay.leaf_count + 1, dtype=torch.int64, device=gpu)
     rec, n = E.emit_edge_records(g, lay, k, ids, d, dsk, m_bits, leaf_record_offsets=offsets)
