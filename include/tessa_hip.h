@@ -25,6 +25,8 @@
  *   tessa_session_leaf_topk /    TessaCudaReplaySession::run_mode leaf / assignment legs
  *   tessa_session_assign_replay  (tessa_replay.rs:190-200 TessaCudaModeResult)
  *   tessa_overflow_labels        compute_backend.rs:2249-2296 gpu_persistent_overflow_labels
+ *   tessa_session_submit_subtree compute_backend.rs:3807-3815 submit_owned_quantized_subtree_l2_compact_topk
+ *   / _wait / _release           (Deferred result, pinned slot ring :31432-31497)
  *   tessa_emit_edge_records      leaf_build.rs:1679-1829 flush_compact_topk_batch_into_edges
  *                                (records: spill_hashprune.rs:137-145 SpillRecord16)
  */
@@ -403,6 +405,41 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
                                      tessa_edge_record *out, uint64_t out_capacity,
                                      uint64_t *leaf_record_offsets, uint64_t *record_count,
                                      void *stream);
+
+/* ---- asynchronous subtree submissions ----------------------------------
+ * Replaces submit_owned_quantized_subtree_l2_compact_topk
+ * (compute_backend.rs:3807-3815) with its Deferred result and pinned host-slot
+ * ring (CudaDeferredPinnedQuantizedScatter, :31432-31497): the device work of
+ * one task overlaps the caller's host-side use of the previous result.
+ * A session runs submissions in order on a worker thread of its own and holds
+ * two pinned host result slots.  submit copies the request (and its root
+ * leader ids); `host_sq8` (may be NULL: keep the current upload) is uploaded
+ * by the job, so its arrays must stay valid until tessa_session_wait returns.
+ * submit fails when both slots hold unreleased results.  The request's
+ * output capacities (max_leaf_count, max_leaf_rows) size the session's device
+ * outputs.  wait blocks until the job is done and returns its status; the
+ * result arrays stay valid until tessa_session_release(seq).  Other session
+ * calls wait for a running job. */
+typedef struct tessa_subtree_host_result {
+    const uint32_t *leaf_row_ids;   /* pinned host, leaf_rows (resident rows) */
+    const uint64_t *leaf_starts;    /* leaf_count */
+    const uint64_t *leaf_sizes;     /* leaf_count */
+    const uint32_t *topk_ids;       /* leaf_rows * k, global ids */
+    const float *topk_dists;        /* leaf_rows * k */
+    const uint64_t *counters;       /* TESSA_SUBTREE_COUNTER_WORDS */
+    const uint64_t *leaf_counters;  /* TESSA_COUNTER_WORDS */
+    uint64_t leaf_count;
+    uint64_t leaf_rows;
+    uint32_t k;
+    uint32_t levels;
+    float partition_ms;
+    float leaf_ms;
+} tessa_subtree_host_result;
+
+tessa_status tessa_session_submit_subtree(tessa_session *session, const tessa_sq8_view *host_sq8,
+                                          const tessa_subtree_request *req, uint64_t *seq);
+tessa_status tessa_session_wait(tessa_session *session, uint64_t seq, tessa_subtree_host_result *out);
+tessa_status tessa_session_release(tessa_session *session, uint64_t seq);
 
 /* "QUEUE_NODE|LEAF_ROW|..." or "none" (same labels as the reference). */
 void tessa_overflow_labels(uint64_t flags, char *buf, size_t len);

@@ -200,6 +200,24 @@ class SubtreeOutput(C.Structure):
     ]
 
 
+class SubtreeHostResult(C.Structure):
+    _fields_ = [
+        ("leaf_row_ids", C.c_void_p),
+        ("leaf_starts", C.c_void_p),
+        ("leaf_sizes", C.c_void_p),
+        ("topk_ids", C.c_void_p),
+        ("topk_dists", C.c_void_p),
+        ("counters", C.c_void_p),
+        ("leaf_counters", C.c_void_p),
+        ("leaf_count", C.c_uint64),
+        ("leaf_rows", C.c_uint64),
+        ("k", C.c_uint32),
+        ("levels", C.c_uint32),
+        ("partition_ms", C.c_float),
+        ("leaf_ms", C.c_float),
+    ]
+
+
 class EdgeRecord(C.Structure):
     """tessa_edge_record: SpillRecord16 (spill_hashprune.rs:137-145)."""
 
@@ -253,6 +271,12 @@ SIGNATURES = {
         TessaStatus,
         [_P, C.POINTER(SubtreeRequest), C.POINTER(SubtreeOutput)],
     ),
+    "tessa_session_submit_subtree": (
+        TessaStatus,
+        [_P, C.POINTER(Sq8View), C.POINTER(SubtreeRequest), C.POINTER(_U64)],
+    ),
+    "tessa_session_wait": (TessaStatus, [_P, _U64, C.POINTER(SubtreeHostResult)]),
+    "tessa_session_release": (TessaStatus, [_P, _U64]),
     "tessa_emit_edge_records": (
         TessaStatus,
         [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, C.POINTER(_U64), _P],

@@ -7,11 +7,14 @@
 // by substring (rbc_partition.rs:2982-2998).
 #include <hip/hip_runtime.h>
 
+#include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <mutex>
 #include <new>
+#include <thread>
 #include <vector>
 
 #include "../../include/tessa_hip.h"
@@ -429,9 +432,50 @@ struct tessa_session {
     tessa::LevelHeader *part_hdr = nullptr;
     tessa::LevelHeader *part_hdr_host = nullptr;  // pinned
     hipEvent_t ev2 = nullptr;
+    // Held by every call (and by the async worker for a whole job) that uses
+    // the stream, the uploaded rows or the workspaces above.
+    std::mutex exec_mu;
+    // ---- asynchronous submissions (tessa_session_submit_subtree) ----
+    struct AsyncSlot {
+        int state = 0;  // 0 free, 1 queued or running, 2 result ready
+        uint64_t seq = 0;
+        bool upload = false;
+        tessa_sq8_view host{};
+        tessa_subtree_request req{};
+        std::vector<uint32_t> roots;
+        tessa_status status{};
+        // results, in pinned host memory grown to the largest result seen
+        uint32_t *rows_h = nullptr;
+        uint64_t *starts_h = nullptr, *sizes_h = nullptr;
+        uint32_t *ids_h = nullptr;
+        float *dists_h = nullptr;
+        uint64_t rows_cap = 0, starts_cap = 0, sizes_cap = 0, ids_cap = 0, dists_cap = 0;
+        uint64_t counters[TESSA_SUBTREE_COUNTER_WORDS] = {};
+        uint64_t leaf_counters[TESSA_COUNTER_WORDS] = {};
+        uint64_t leaf_count = 0, leaf_rows = 0;
+        uint32_t k = 0, levels = 0;
+        float partition_ms = 0.0f, leaf_ms = 0.0f;
+    };
+    static constexpr int kAsyncSlots = 2;
+    AsyncSlot slots[kAsyncSlots];
+    std::mutex q_mu;
+    std::condition_variable q_cv;
+    std::deque<int> queue;
+    std::thread worker;
+    bool worker_started = false;
+    bool stop = false;
+    uint64_t next_seq = 1;
+    // device outputs of async jobs (one job runs at a time)
+    uint32_t *a_rows = nullptr;
+    uint64_t *a_starts = nullptr, *a_sizes = nullptr;
+    uint32_t *a_ids = nullptr;
+    float *a_dists = nullptr;
+    uint64_t a_rows_cap = 0, a_starts_cap = 0, a_sizes_cap = 0, a_ids_cap = 0, a_dists_cap = 0;
 };
 
 namespace {
+
+void stop_async(tessa_session *s);  // asynchronous submissions, below
 
 void free_sq8(tessa_session *s) {
     if (s->codes) (void)hipFree(s->codes);
@@ -512,6 +556,7 @@ tessa_status tessa_session_create(const tessa_config *cfg, tessa_session **out) 
 tessa_status tessa_session_destroy(tessa_session *s) {
     if (!s) return ok_status();
     (void)hipSetDevice(s->device);
+    stop_async(s);  // finishes the queued jobs, joins the worker, frees the result slots
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     free_sq8(s);
     if (s->scratch) (void)hipFree(s->scratch);
@@ -528,7 +573,7 @@ tessa_status tessa_session_destroy(tessa_session *s) {
     return ok_status();
 }
 
-tessa_status tessa_session_upload_sq8(tessa_session *s, const tessa_sq8_view *host) {
+static tessa_status tessa_session_upload_sq8_locked(tessa_session *s, const tessa_sq8_view *host) {
     if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
     tessa_status st = check_view(host);
     if (st.code) return st;
@@ -555,7 +600,13 @@ tessa_status tessa_session_upload_sq8(tessa_session *s, const tessa_sq8_view *ho
     return ok_status();
 }
 
-tessa_status tessa_session_leaf_topk(tessa_session *s, const uint32_t *members, const uint64_t *member_offsets,
+tessa_status tessa_session_upload_sq8(tessa_session *s, const tessa_sq8_view *host) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    return tessa_session_upload_sq8_locked(s, host);
+}
+
+static tessa_status tessa_session_leaf_topk_locked(tessa_session *s, const uint32_t *members, const uint64_t *member_offsets,
                                      const uint32_t *member_counts, const uint64_t *output_offsets,
                                      uint32_t leaf_count, uint32_t k, uint32_t executor, uint32_t *out_ids,
                                      float *out_dists, uint64_t *counters, float *event_ms) {
@@ -615,7 +666,17 @@ tessa_status tessa_session_leaf_topk(tessa_session *s, const uint32_t *members, 
     return st;
 }
 
-tessa_status tessa_session_assign_replay(tessa_session *s, const uint32_t *members, const uint32_t *leaders,
+tessa_status tessa_session_leaf_topk(tessa_session *s, const uint32_t *members, const uint64_t *member_offsets,
+                                     const uint32_t *member_counts, const uint64_t *output_offsets,
+                                     uint32_t leaf_count, uint32_t k, uint32_t executor, uint32_t *out_ids,
+                                     float *out_dists, uint64_t *counters, float *event_ms) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    return tessa_session_leaf_topk_locked(s, members, member_offsets, member_counts, output_offsets, leaf_count, k,
+                                          executor, out_ids, out_dists, counters, event_ms);
+}
+
+static tessa_status tessa_session_assign_replay_locked(tessa_session *s, const uint32_t *members, const uint32_t *leaders,
                                          const uint32_t *member_offsets, const uint32_t *member_counts,
                                          const uint32_t *leader_offsets, const uint32_t *leader_counts,
                                          const uint32_t *r_h, const uint64_t *output_offsets, uint32_t task_count,
@@ -693,6 +754,18 @@ tessa_status tessa_session_assign_replay(tessa_session *s, const uint32_t *membe
         *event_ms = ms;
     }
     return st;
+}
+
+tessa_status tessa_session_assign_replay(tessa_session *s, const uint32_t *members, const uint32_t *leaders,
+                                         const uint32_t *member_offsets, const uint32_t *member_counts,
+                                         const uint32_t *leader_offsets, const uint32_t *leader_counts,
+                                         const uint32_t *r_h, const uint64_t *output_offsets, uint32_t task_count,
+                                         uint32_t *out_ids, float *out_dists, uint64_t *counters, float *event_ms) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    return tessa_session_assign_replay_locked(s, members, leaders, member_offsets, member_counts, leader_offsets,
+                                             leader_counts, r_h, output_offsets, task_count, out_ids, out_dists,
+                                             counters, event_ms);
 }
 
 }  // extern "C"
@@ -827,7 +900,7 @@ tessa_status tessa_plan_subtree(uint64_t resident_rows, uint32_t leaf_knn, uint3
     return ok_status();
 }
 
-tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_request *rq,
+static tessa_status tessa_session_run_subtree_locked(tessa_session *s, const tessa_subtree_request *rq,
                                        tessa_subtree_output *out) {
     if (!s || !s->codes) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session has no SQ8 upload");
     if (!rq || !out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "subtree request/output is null");
@@ -993,6 +1066,255 @@ tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_req
                            (unsigned long long)rows, (unsigned long long)lc[TESSA_C_OVERFLOW_FLAGS], labels);
     }
     return ok_status();
+}
+
+tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_request *rq, tessa_subtree_output *out) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    return tessa_session_run_subtree_locked(s, rq, out);
+}
+
+}  // extern "C"
+
+// ---- asynchronous subtree submissions --------------------------------------
+//
+// The reference's submit_owned_quantized_subtree_l2_compact_topk
+// (compute_backend.rs:3807-3815) returns a Deferred result whose finish()
+// waits for the device work and the D2H copy into a pinned host slot taken
+// from a small ring (CudaDeferredPinnedQuantizedScatter, :31432-31497), so the
+// caller's host-side scatter of one task overlaps the device work of the next.
+// Here a session owns one worker thread and two pinned result slots: submit
+// queues a job (upload of the task's SQ8 rows, partition, leaf top-k, D2H of
+// the leaf layout and top-k into the slot) and returns its sequence number;
+// wait blocks until that job is done and hands out the slot's host arrays;
+// release returns the slot to the ring.
+
+namespace {
+
+template <typename T>
+tessa_status grow_pinned(T **p, uint64_t *cap, uint64_t need) {
+    if (*cap >= need) return ok_status();
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    const uint64_t n = need < 1024 ? 1024 : need;
+    if (hipHostMalloc((void **)p, n * sizeof(T), hipHostMallocDefault) != hipSuccess)
+        return make_status(TESSA_ERR_OUT_OF_MEMORY, 0, "pinned host result slot of %llu entries failed",
+                           (unsigned long long)n);
+    *cap = n;
+    return ok_status();
+}
+
+template <typename T>
+tessa_status grow_device(T **p, uint64_t *cap, uint64_t need) {
+    if (*cap >= need) return ok_status();
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    const uint64_t n = need < 1024 ? 1024 : need;
+    if (hipMalloc((void **)p, n * sizeof(T)) != hipSuccess)
+        return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
+                           "Failed to allocate CUDA GPU persistent subtree output (HIP, %llu entries) "
+                           "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                           (unsigned long long)n, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+    *cap = n;
+    return ok_status();
+}
+
+// One queued job, run by the worker with exec_mu held.
+tessa_status run_async_job(tessa_session *s, tessa_session::AsyncSlot &slot) {
+    if (slot.upload) {
+        tessa_status st = tessa_session_upload_sq8_locked(s, &slot.host);
+        if (st.code) return st;
+    }
+    const tessa_subtree_request &rq = slot.req;
+    const uint64_t k_cap = rq.partition_only ? 1 : (rq.leaf_knn ? rq.leaf_knn : 1);
+    tessa_status st = grow_device(&s->a_rows, &s->a_rows_cap, rq.max_leaf_rows);
+    if (!st.code) st = grow_device(&s->a_starts, &s->a_starts_cap, rq.max_leaf_count);
+    if (!st.code) st = grow_device(&s->a_sizes, &s->a_sizes_cap, rq.max_leaf_count);
+    if (!st.code) st = grow_device(&s->a_ids, &s->a_ids_cap, rq.max_leaf_rows * k_cap);
+    if (!st.code) st = grow_device(&s->a_dists, &s->a_dists_cap, rq.max_leaf_rows * k_cap);
+    if (st.code) return st;
+    tessa_subtree_request req = rq;
+    req.root_leaders = slot.roots.empty() ? nullptr : slot.roots.data();
+    tessa_subtree_output out{};
+    out.leaf_row_ids = s->a_rows;
+    out.leaf_starts = s->a_starts;
+    out.leaf_sizes = s->a_sizes;
+    out.topk_ids = s->a_ids;
+    out.topk_dists = s->a_dists;
+    out.counters = slot.counters;
+    out.leaf_counters = slot.leaf_counters;
+    std::memset(slot.counters, 0, sizeof(slot.counters));
+    std::memset(slot.leaf_counters, 0, sizeof(slot.leaf_counters));
+    st = tessa_session_run_subtree_locked(s, &req, &out);
+    slot.leaf_count = out.leaf_count;
+    slot.leaf_rows = out.leaf_rows;
+    slot.k = out.k;
+    slot.levels = out.levels;
+    slot.partition_ms = out.partition_ms;
+    slot.leaf_ms = out.leaf_ms;
+    if (st.code) return st;
+    const uint64_t nslots = out.leaf_rows * out.k;
+    st = grow_pinned(&slot.rows_h, &slot.rows_cap, out.leaf_rows);
+    if (!st.code) st = grow_pinned(&slot.starts_h, &slot.starts_cap, out.leaf_count);
+    if (!st.code) st = grow_pinned(&slot.sizes_h, &slot.sizes_cap, out.leaf_count);
+    if (!st.code) st = grow_pinned(&slot.ids_h, &slot.ids_cap, nslots);
+    if (!st.code) st = grow_pinned(&slot.dists_h, &slot.dists_cap, nslots);
+    if (st.code) return st;
+    hipStream_t q = s->stream;
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.rows_h, s->a_rows, out.leaf_rows * 4, hipMemcpyDeviceToHost, q));
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.starts_h, s->a_starts, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.sizes_h, s->a_sizes, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
+    if (nslots) {
+        TESSA_HIP_TRY(hipMemcpyAsync(slot.ids_h, s->a_ids, nslots * 4, hipMemcpyDeviceToHost, q));
+        TESSA_HIP_TRY(hipMemcpyAsync(slot.dists_h, s->a_dists, nslots * 4, hipMemcpyDeviceToHost, q));
+    }
+    TESSA_HIP_TRY(hipStreamSynchronize(q));
+    return ok_status();
+}
+
+void async_worker(tessa_session *s) {
+    (void)hipSetDevice(s->device);
+    while (true) {
+        int idx = -1;
+        {
+            std::unique_lock<std::mutex> lk(s->q_mu);
+            s->q_cv.wait(lk, [s] { return s->stop || !s->queue.empty(); });
+            if (s->queue.empty()) return;  // stop requested and nothing left
+            idx = s->queue.front();
+            s->queue.pop_front();
+        }
+        tessa_session::AsyncSlot &slot = s->slots[idx];
+        tessa_status st;
+        {
+            std::lock_guard<std::mutex> lock(s->exec_mu);
+            st = run_async_job(s, slot);
+        }
+        {
+            std::lock_guard<std::mutex> lk(s->q_mu);
+            slot.status = st;
+            slot.state = 2;
+        }
+        s->q_cv.notify_all();
+    }
+}
+
+void stop_async(tessa_session *s) {
+    {
+        std::lock_guard<std::mutex> lk(s->q_mu);
+        s->stop = true;
+    }
+    s->q_cv.notify_all();
+    if (s->worker_started && s->worker.joinable()) s->worker.join();
+    s->worker_started = false;
+    for (auto &slot : s->slots) {
+        if (slot.rows_h) (void)hipHostFree(slot.rows_h);
+        if (slot.starts_h) (void)hipHostFree(slot.starts_h);
+        if (slot.sizes_h) (void)hipHostFree(slot.sizes_h);
+        if (slot.ids_h) (void)hipHostFree(slot.ids_h);
+        if (slot.dists_h) (void)hipHostFree(slot.dists_h);
+        slot = tessa_session::AsyncSlot{};
+    }
+    if (s->a_rows) (void)hipFree(s->a_rows);
+    if (s->a_starts) (void)hipFree(s->a_starts);
+    if (s->a_sizes) (void)hipFree(s->a_sizes);
+    if (s->a_ids) (void)hipFree(s->a_ids);
+    if (s->a_dists) (void)hipFree(s->a_dists);
+    s->a_rows = s->a_ids = nullptr;
+    s->a_starts = s->a_sizes = nullptr;
+    s->a_dists = nullptr;
+    s->a_rows_cap = s->a_starts_cap = s->a_sizes_cap = s->a_ids_cap = s->a_dists_cap = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+tessa_status tessa_session_submit_subtree(tessa_session *s, const tessa_sq8_view *host_sq8,
+                                          const tessa_subtree_request *req, uint64_t *seq) {
+    if (!s || !req || !seq) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "submit: null argument");
+    *seq = 0;
+    if (host_sq8) {
+        tessa_status st = check_view(host_sq8);
+        if (st.code) return st;
+    }
+    if (req->root_leader_count > kLeaderStride)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "CUDA persistent root leader override has %u leaders, exceeding per-node limit %u",
+                           req->root_leader_count, kLeaderStride);
+    if (req->root_leader_count > 0 && !req->root_leaders)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "root leader count without root leader ids");
+    std::lock_guard<std::mutex> lk(s->q_mu);
+    int idx = -1;
+    for (int i = 0; i < tessa_session::kAsyncSlots; ++i)
+        if (s->slots[i].state == 0) {
+            idx = i;
+            break;
+        }
+    if (idx < 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "both pinned host result slots are held: wait for and release a submission first");
+    tessa_session::AsyncSlot &slot = s->slots[idx];
+    slot.state = 1;
+    slot.seq = s->next_seq++;
+    slot.upload = host_sq8 != nullptr;
+    if (host_sq8) slot.host = *host_sq8;
+    slot.req = *req;
+    slot.roots.assign(req->root_leaders, req->root_leaders + req->root_leader_count);
+    slot.req.root_leaders = nullptr;
+    slot.status = ok_status();
+    if (!s->worker_started) {
+        s->stop = false;
+        s->worker = std::thread(async_worker, s);
+        s->worker_started = true;
+    }
+    s->queue.push_back(idx);
+    *seq = slot.seq;
+    s->q_cv.notify_all();
+    return ok_status();
+}
+
+tessa_status tessa_session_wait(tessa_session *s, uint64_t seq, tessa_subtree_host_result *out) {
+    if (!s || !out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "wait: null argument");
+    std::memset(out, 0, sizeof(*out));
+    std::unique_lock<std::mutex> lk(s->q_mu);
+    int idx = -1;
+    for (int i = 0; i < tessa_session::kAsyncSlots; ++i)
+        if (s->slots[i].state != 0 && s->slots[i].seq == seq) idx = i;
+    if (idx < 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "no pending or unreleased submission %llu",
+                           (unsigned long long)seq);
+    tessa_session::AsyncSlot &slot = s->slots[idx];
+    s->q_cv.wait(lk, [&slot] { return slot.state == 2; });
+    out->leaf_row_ids = slot.rows_h;
+    out->leaf_starts = slot.starts_h;
+    out->leaf_sizes = slot.sizes_h;
+    out->topk_ids = slot.ids_h;
+    out->topk_dists = slot.dists_h;
+    out->counters = slot.counters;
+    out->leaf_counters = slot.leaf_counters;
+    out->leaf_count = slot.leaf_count;
+    out->leaf_rows = slot.leaf_rows;
+    out->k = slot.k;
+    out->levels = slot.levels;
+    out->partition_ms = slot.partition_ms;
+    out->leaf_ms = slot.leaf_ms;
+    return slot.status;
+}
+
+tessa_status tessa_session_release(tessa_session *s, uint64_t seq) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lk(s->q_mu);
+    for (auto &slot : s->slots)
+        if (slot.state != 0 && slot.seq == seq) {
+            if (slot.state != 2)
+                return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "submission %llu is still running: wait first",
+                                   (unsigned long long)seq);
+            slot.state = 0;
+            return ok_status();
+        }
+    return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "no unreleased submission %llu", (unsigned long long)seq);
 }
 
 }  // extern "C"

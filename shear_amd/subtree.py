@@ -131,9 +131,9 @@ class SubtreeSession:
         self.rows = codes.shape[0]
         self.global_ids = gids
 
-    def run(self, request: GpuSubtreePartitionRequest, params: PiPNNSubtreeParams,
-            partition_only: bool = False) -> SubtreeDeviceOutput:
-        rows = self.rows
+    def _request(self, rows: int, request: GpuSubtreePartitionRequest, params: PiPNNSubtreeParams,
+                 partition_only: bool):
+        """-> (tessa_subtree_request, plan, k, root leader array kept alive by the caller)."""
         famp = max(params.fanout_second, 1)
         max_leaders = min(max(params.max_leaders, 1), GPU_QUEUE_LEADER_STRIDE)
         plan = plan_subtree(rows, params.leaf_knn, max_leaders, famp, request.memory_budget_bytes,
@@ -145,6 +145,42 @@ class SubtreeSession:
         seed = subtree_root_seed(params.random_seed, request.depth, len(request.point_ids),
                                  request.parent_points, request.min_recurse_size)
         k = 0 if partition_only else min(params.leaf_knn, max(rows - 1, 0))
+        roots = (np.zeros(0, np.uint32) if request.root_leader_ids is None
+                 else np.ascontiguousarray(request.root_leader_ids, np.uint32))
+        rq = N.SubtreeRequest(
+            roots.ctypes.data if len(roots) else None, len(roots), request.depth, seed,
+            max(params.leaf_knn, 1), famp, params.max_depth, max_leaders, plan.leaf_min, plan.leaf_max,
+            plan.small_node_limit, np.float32(params.psamp_fraction).item(), params.executor,
+            1 if partition_only else 0, plan.max_leaf_count, plan.max_leaf_rows)
+        return rq, plan, k, roots
+
+    def submit_owned_quantized_subtree_l2_compact_topk(
+            self, request: GpuSubtreePartitionRequest, codes: np.ndarray, scales: np.ndarray, norms: np.ndarray,
+            global_ids: np.ndarray, dim: int, params: PiPNNSubtreeParams) -> "DeferredGpuSubtreeTopK":
+        """compute_backend.rs:3807-3815: queue one task (its own SQ8 rows) on the
+        session's worker; returns at once.  ``finish()`` of the result waits for
+        the device work and the D2H into a pinned slot, builds the compact
+        batches and releases the slot (CudaDeferredPinnedQuantizedScatter,
+        compute_backend.rs:31432-31497)."""
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        norms = np.ascontiguousarray(norms, np.float32)
+        gids = np.ascontiguousarray(global_ids, np.uint32)
+        view = N.Sq8View(codes.ctypes.data, scales.ctypes.data, norms.ctypes.data, gids.ctypes.data,
+                         codes.shape[0], dim, codes.shape[1])
+        rq, plan, k, roots = self._request(codes.shape[0], request, params, False)
+        seq = C.c_uint64(0)
+        N.check(self._lib.tessa_session_submit_subtree(self._h, C.byref(view), C.byref(rq), C.byref(seq)),
+                "tessa_session_submit_subtree")
+        self.rows = codes.shape[0]
+        self.global_ids = gids
+        owned = (codes, scales, norms, gids, roots)  # the job reads these until it is waited for
+        est = int(plan.max_leaf_rows) * (4 + k * 8) + int(plan.max_leaf_count) * 16
+        return DeferredGpuSubtreeTopK(est, _PinnedScatter(self, int(seq.value), gids, params, owned))
+
+    def run(self, request: GpuSubtreePartitionRequest, params: PiPNNSubtreeParams,
+            partition_only: bool = False) -> SubtreeDeviceOutput:
+        rq, plan, k, roots = self._request(self.rows, request, params, partition_only)
         dev = torch.device("cuda", self.device)
         max_rows = max(int(plan.max_leaf_rows), 1)
         max_leaves = max(int(plan.max_leaf_count), 1)
@@ -155,13 +191,6 @@ class SubtreeSession:
         out_d = torch.empty(max(max_rows * k, 1), dtype=torch.float32, device=dev)
         counters = np.zeros(N.SUBTREE_COUNTER_WORDS, np.uint64)
         leaf_counters = np.zeros(N.COUNTER_WORDS, np.uint64)
-        roots = (np.zeros(0, np.uint32) if request.root_leader_ids is None
-                 else np.ascontiguousarray(request.root_leader_ids, np.uint32))
-        rq = N.SubtreeRequest(
-            roots.ctypes.data if len(roots) else None, len(roots), request.depth, seed,
-            max(params.leaf_knn, 1), famp, params.max_depth, max_leaders, plan.leaf_min, plan.leaf_max,
-            plan.small_node_limit, np.float32(params.psamp_fraction).item(), params.executor,
-            1 if partition_only else 0, plan.max_leaf_count, plan.max_leaf_rows)
         out = N.SubtreeOutput(out_rows.data_ptr(), out_starts.data_ptr(), out_sizes.data_ptr(),
                               out_ids.data_ptr(), out_d.data_ptr(), counters.ctypes.data,
                               leaf_counters.ctypes.data, 0, 0, 0, 0, 0.0, 0.0)
@@ -191,6 +220,58 @@ class SubtreeSession:
             profile={"counters": r.counters, "leaf_counters": r.leaf_counters, "levels": r.levels,
                      "partition_ms": r.partition_ms, "leaf_ms": r.leaf_ms},
         )
+
+
+class _PinnedScatter:
+    """DeferredGpuSubtreeScatter of one submission (compute_backend.rs:1958-1960)."""
+
+    def __init__(self, session: SubtreeSession, seq: int, global_ids: np.ndarray, params: PiPNNSubtreeParams,
+                 owned):
+        self._session, self._seq, self._gids, self._params, self._owned = session, seq, global_ids, params, owned
+
+    def finish(self) -> GpuSubtreeTopKResult:
+        lib, h = self._session._lib, self._session._h
+        r = N.SubtreeHostResult()
+        st = lib.tessa_session_wait(h, self._seq, C.byref(r))
+        try:
+            N.check(st, "tessa_session_wait")
+            lc, lr, k = int(r.leaf_count), int(r.leaf_rows), int(r.k)
+
+            def arr(ptr, n, ctype, dt):
+                if n == 0:
+                    return np.zeros(0, dt)
+                return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ctype)), shape=(n,)).astype(dt, copy=True)
+
+            rows = arr(r.leaf_row_ids, lr, C.c_uint32, np.uint32)
+            starts = arr(r.leaf_starts, lc, C.c_uint64, np.int64)
+            sizes = arr(r.leaf_sizes, lc, C.c_uint64, np.int64)
+            ids = arr(r.topk_ids, lr * k, C.c_uint32, np.uint32)
+            d = arr(r.topk_dists, lr * k, C.c_float, np.float32)
+            counters = arr(r.counters, N.SUBTREE_COUNTER_WORDS, C.c_uint64, np.uint64)
+            leaf_counters = arr(r.leaf_counters, N.COUNTER_WORDS, C.c_uint64, np.uint64)
+        finally:
+            lib.tessa_session_release(h, self._seq)
+            self._owned = None
+        batches = compact_batches_from_slices(self._gids, rows, starts, sizes, ids, d, k, self._params.leaf_knn)
+        return GpuSubtreeTopKResult(
+            compact_batches=batches,
+            assignment_passes=int(counters[N.P_ASSIGNMENT_PASSES]),
+            leaf_count=lc,
+            max_active_points=int(counters[N.P_MAX_ACTIVE]),
+            profile={"counters": counters, "leaf_counters": leaf_counters, "levels": int(r.levels),
+                     "partition_ms": float(r.partition_ms), "leaf_ms": float(r.leaf_ms)},
+        )
+
+
+@dataclass
+class DeferredGpuSubtreeTopK:
+    """compute_backend.rs:1958-1961."""
+
+    estimated_host_bytes: int
+    scatter: _PinnedScatter
+
+    def finish(self) -> GpuSubtreeTopKResult:
+        return self.scatter.finish()
 
 
 def _status(code: int, flags: int, msg: str) -> N.TessaStatus:
