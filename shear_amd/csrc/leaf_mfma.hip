@@ -45,7 +45,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
+#ifndef TESSA_LEAF_WAVES
+#define TESSA_LEAF_WAVES 8
+#endif
+constexpr int kWaves = TESSA_LEAF_WAVES;  // waves per workgroup, 32 rows each
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerBlock = kWaves * 32;
 constexpr int kTileCols = 32;
@@ -61,10 +64,11 @@ struct Layout {
     static constexpr int kChunksPerThread = (kChunks + kThreads - 1) / kThreads;
 };
 
-// Dynamic LDS limit (the whole CU); a C2-shaped leaf uses ~37 KiB, so two
-// workgroups share a CU, and registers are capped for two waves per SIMD.
+// Dynamic LDS limit (the whole CU).  One 8-wave workgroup per CU gives two
+// waves per SIMD (256 VGPRs each); its 256 rows share every LDS column tile,
+// so a leaf's tiles cross L2 -> LDS n/256 times.
 #ifndef TESSA_LEAF_MIN_BLOCKS
-#define TESSA_LEAF_MIN_BLOCKS 2
+#define TESSA_LEAF_MIN_BLOCKS 1
 #endif
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
@@ -695,8 +699,9 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     if (total == 0) return 0;
     if (total > 0x7fffff00ull) return -2;
     const uint32_t per_xcd = (uint32_t)((total + 7) / 8);
-    // persistent grid: each workgroup owns one survivor-log slot for its lifetime
-    uint32_t grid = p.log_slots;
+    // persistent grid: each workgroup owns kThreads / 256 survivor-log slots
+    // (a slot holds 256 threads' logs) for its lifetime
+    uint32_t grid = (uint32_t)((uint64_t)p.log_slots * 256u / kThreads);
     const uint64_t need = (uint64_t)per_xcd * 8u;
     if (need < grid) grid = (uint32_t)need;
     grid = grid / 8u * 8u;
