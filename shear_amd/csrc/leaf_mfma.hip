@@ -5,24 +5,31 @@
 // result must equal RowTopK insertion over the columns in member order
 // (leaf_build.rs:887-957 with dco_sq_int8.rs:2950-2965 distances).
 //
-// Work item = (leaf, block of 128 member rows); a workgroup is 4 waves, wave w
-// owns 32 rows.  The wave keeps its 32 rows' codes in VGPRs for the whole K
-// range as the MFMA "B" operand (N = rows); 32-candidate column tiles are
-// staged in LDS as the "A" operand (M = candidates).  With
-// v_mfma_i32_32x32x32_i8 output lane l holds row l%32 and candidates
-// 8*(v/4) + 4*(l/32) + v%4 of the tile: each row is served by a lane pair
-// (l, l+32), each lane seeing half of the row's candidates.
+// Work item = (leaf, block of 256 member rows); a workgroup is 8 waves (one
+// workgroup per CU, two waves per SIMD), wave w owns 32 rows.  The wave keeps
+// its 32 rows' codes in VGPRs for the whole K range as the MFMA "B" operand
+// (N = rows); 32-candidate column tiles are staged in LDS as the "A" operand
+// (M = candidates) and shared by the 8 waves.  With v_mfma_i32_32x32x32_i8
+// output lane l holds row l%32 and candidates 8*(v/4) + 4*(l/32) + v%4 of the
+// tile: each row is served by a lane pair (l, l+32), each lane seeing half of
+// the row's candidates.  The grid is persistent; the 8 XCDs each walk a
+// contiguous range of work items, so a leaf's row blocks share one L2.
 //
 // Selection (exact by construction, see the certificate below):
-//  * every lane keeps the 32 smallest distances it has seen, with their
-//    columns, sorted in registers; new candidates below the row threshold are
-//    staged in LDS and folded in 16 at a time with bitonic networks;
-//  * the row threshold F is the exact 32nd smallest distance of the pair's
-//    two top-32 lists (the row's running 32nd distance), widened by 3*eps;
-//  * every candidate a lane drops (filtered, or evicted from its top-32)
-//    lowers that lane's `disc` to the smallest dropped distance;
-//  * at the end the pair's lists are merged into the sorted known sequence
-//    s_0 <= s_1 <= ...  Consecutive elements within 2e-5 form tie clusters.
+//  * phase A: every kSampleStride-th column tile is evaluated and each lane
+//    keeps its 16 smallest exact distances (values only); the row threshold F
+//    is the pair's kSampleRank-th smallest sampled distance plus 3*eps, so at
+//    least that many candidates lie at or below F;
+//  * phase B: every column tile; a candidate passes when cs*dot meets the
+//    bound tau derived from F (a necessary condition for d <= F, evaluated in
+//    double with a rounding margin) and is appended (raw dot, column) to the
+//    lane's survivor log in global memory (128 entries per lane; a lane whose
+//    log overflows has its row re-run exactly);
+//  * final: the log is folded 16 entries at a time (exact distances, bitonic
+//    sort, merge into a sorted top-32 per lane); `disc` tracks the smallest
+//    distance a lane dropped; the pair's lists are merged into the sorted
+//    known sequence s_0 <= s_1 <= ...  Everything not known is > min(disc, F).
+//    Consecutive elements within 2e-5 form tie clusters.
 //    G = s_0..s_q, the prefix closed at the cluster holding s_{k-1}.  The row
 //    is certified when the next distance after s_q, known or dropped, lies
 //    more than 2e-5 above s_q, and every cluster inside G spans <= 2e-5.
@@ -31,8 +38,9 @@
 //    k best (candidates eps-separated from all kept ones can never enter in
 //    front of them or stay); and inside G the tie relation is an equivalence,
 //    so the comparator is a total order there: distance order, clusters
-//    ordered by global id.  Uncertified rows are queued for the exact scalar
-//    kernel.
+//    ordered by global id.  A row whose G holds a chain (a cluster wider than
+//    2e-5) is queued, with G, for the chain replay kernel; uncertified rows are
+//    queued for the exact scalar kernel.
 #include <type_traits>
 
 #include "leaf_kernels.h"
@@ -55,6 +63,17 @@ constexpr int kTileCols = 32;
 constexpr int kTop = 32;        // per-lane sorted list (registers)
 constexpr uint32_t kMaxLeafRows = 4096;
 constexpr float kFilterMargin = 3.0f * kTieEps;
+// Phase A samples every kSampleStride-th column tile; F is the pair's
+// kSampleRank-th smallest sampled distance plus the margin.  Every third
+// tile with rank 24 leaves ~73 survivors per 1024-row leaf row (C2).
+#ifndef TESSA_LEAF_SAMPLE_STRIDE
+#define TESSA_LEAF_SAMPLE_STRIDE 3
+#endif
+#ifndef TESSA_LEAF_SAMPLE_RANK
+#define TESSA_LEAF_SAMPLE_RANK 24
+#endif
+constexpr uint32_t kSampleStride = TESSA_LEAF_SAMPLE_STRIDE;
+constexpr int kSampleRank = TESSA_LEAF_SAMPLE_RANK;
 
 template <int KS>
 struct Layout {
@@ -258,7 +277,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     // them with immediate offsets from one address.
     uint2 *slog = p.survivor_log + ((uint64_t)blockIdx.x * kThreads + tid) * cap;
 
-    // Work items are (leaf, 128-row block).  Blocks are dispatched round-robin
+    // Work items are (leaf, 256-row block).  Blocks are dispatched round-robin
     // over the 8 XCDs: XCD x walks its own contiguous item range, so the row
     // blocks of a leaf share that XCD's L2.
     const uint32_t xcd = blockIdx.x % 8u;
@@ -371,16 +390,16 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             return acc;
         };
 
-        // ---- phase A: row threshold from every 4th column tile ---------------
+        // ---- phase A: row threshold from every kSampleStride-th column tile ----
         // Each lane keeps the 16 smallest exact distances it sees (values only);
         // F is the pair's kSel-th smallest sample distance plus 3 eps, so at
         // least kSel candidates lie at or below F.
         constexpr int kSample = 16;
-        const int rsel = (int)(keff < 24u ? keff : 24u);
+        const int rsel = (int)(keff < (uint32_t)kSampleRank ? keff : (uint32_t)kSampleRank);
         float samp[kSample];
 #pragma unroll
         for (int i = 0; i < kSample; ++i) samp[i] = __builtin_inff();
-        for (uint32_t t = 0; t < ntiles; t += 4) {
+        for (uint32_t t = 0; t < ntiles; t += kSampleStride) {
             load_tile(t);
             __syncthreads();
             store_tile();
@@ -445,7 +464,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             if (checked) epilogue(std::true_type{});
             else epilogue(std::false_type{});
         }
-        s_tiles += ntiles + (ntiles + 3u) / 4u;
+        s_tiles += ntiles + (ntiles + kSampleStride - 1u) / kSampleStride;
 
         // ---- final: fold the log, merge the pair, certify, order, write -----------
         // The log entries were written by this thread's global stores above.  A
