@@ -32,6 +32,7 @@ K = 32
 COMPONENTS = 256
 SIGMA = 0.3
 SEED = 1
+HERE = os.path.dirname(os.path.abspath(__file__))
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0
 
@@ -45,8 +46,9 @@ def parse():
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate seconds of CPU oracle work for cpu_baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--traffic-json", default=None,
-                    help="profiles/*.json with measured HBM bytes per launch (rocprofv3 --pmc)")
+    ap.add_argument("--traffic-json", default=os.path.join(HERE, "profiles", "leaf_mfma_c2_traffic.json"),
+                    help="measured HBM bytes per launch of leaf_mfma_kernel (rocprofv3 --pmc FETCH_SIZE and "
+                         "WRITE_SIZE, scaled by a copy kernel; see profiles/leaf_mfma_c2_traffic.md)")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -146,9 +148,9 @@ def main() -> int:
     algo_bytes = rows * (DIM + 8) + records_bytes  # codes + scale/norm + (id, dist) records
 
     traffic = None
-    if args.traffic_json and os.path.exists(args.traffic_json):
+    if args.traffic_json and os.path.exists(args.traffic_json) and leaves == LEAVES:
         with open(args.traffic_json) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            traffic = json.load(f).get("hbm_bytes_per_launch")  # measured on this same C2 workload
 
     result = {
         "metric": "TESSA leaf int8 TOPS (% MFMA peak)",
@@ -179,6 +181,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / INT8_PEAK_TOPS, 4),
             "traffic": traffic,
+            "traffic_source": os.path.relpath(args.traffic_json, HERE) if traffic is not None else None,
             "kernel": "leaf_mfma_kernel",
             "ops_per_launch": ops,
             "algorithmic_hbm_bytes_per_launch": algo_bytes,
