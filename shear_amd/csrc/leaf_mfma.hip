@@ -91,9 +91,10 @@ struct Layout {
 #endif
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
-// LDS: one column tile plus the leaf's member ids, scales and norms.
+// LDS: one column tile plus the leaf's member ids, scales, norms and global
+// ids, 64 bytes of scalars and each wave's output staging (32 rows x 32 slots).
 __host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
-    return tile_bytes + cols_cap * 12u + 64u;
+    return tile_bytes + cols_cap * 16u + 64u + kWaves * 2u * 32u * kTop * 4u;
 }
 
 // Compare-exchange on (key, payload) pairs; ascending when `up`.
@@ -258,13 +259,15 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                                                               uint32_t total_work, uint32_t per_xcd) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // Runtime layout: tile | members | scales | norms | misc.
+    // Runtime layout: tile | members | scales | norms | global ids | misc | stage.
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
     uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kTileBytes);
     float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
     float *cn_lds = cs_lds + cols_cap;
-    uint32_t *misc = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);
+    uint32_t *gid_lds = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);  // global id per member
+    uint32_t *misc = gid_lds + cols_cap;
+    uint32_t *stage = misc + 16;  // per wave: 32 rows x k output ids, then distances
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
@@ -314,6 +317,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                     mc = 0u;
                 }
                 mem_lds[c] = mc;
+                gid_lds[c] = p.gids[mc];
                 const float cn = p.norms[mc];
                 cs_lds[c] = p.scales[mc];
                 cn_lds[c] = cn;
@@ -592,7 +596,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         // by global id).  Other rows keep the columns for the chain queue.
 #pragma unroll
         for (int i = 0; i < kSeq; ++i)
-            sc[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? p.gids[mem_lds[sc[i]]] : sc[i];
+            sc[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? gid_lds[sc[i]] : sc[i];
         const uint64_t in_g = q_end >= 1 ? ((q_end >= 64 ? ~0ull : ((1ull << q_end) - 1ull))) : 0ull;
         const bool need_sort = (same & in_g) != 0ull;
         if (__any(row_ok && direct && need_sort)) {
@@ -627,18 +631,33 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             }
         }
 
+        // Output: the wave's 32 rows are consecutive, so their slots form one
+        // block of rows*k records.  Lanes stage their row's slots in the
+        // wave's LDS area, then the wave writes the block with consecutive
+        // lanes on consecutive addresses.  Rows that are not direct stage
+        // placeholders: the chain and exact kernels, which run after this one,
+        // overwrite their slots.
+        {
+            uint32_t *st_ids = stage + wave * (2u * 32u * (uint32_t)kTop);
+            float *st_d = reinterpret_cast<float *>(st_ids + 32u * kTop);
+#pragma unroll
+            for (int i = 0; i < kTop; ++i) {
+                if ((i >> 4) != (int)h || (uint32_t)i >= p.k) continue;
+                const bool live = (uint32_t)i < keff;
+                st_ids[j * p.k + i] = live ? sc[i] : kEmptyId;
+                st_d[j * p.k + i] = live ? sd[i] : kEmptyDist;
+            }
+            const uint32_t wrow0 = row_base + wave * 32u;
+            const uint32_t wrows = wrow0 < n ? (n - wrow0 < 32u ? n - wrow0 : 32u) : 0u;
+            const uint32_t total = wrows * p.k;
+            const uint64_t base = p.output_offsets[leaf] + (uint64_t)wrow0 * p.k;
+            for (uint32_t e = lane; e < total; e += 64u) {
+                p.out_ids[base + e] = st_ids[e];
+                p.out_dists[base + e] = st_d[e];
+            }
+        }
         if (row_ok) {
             if (direct) {
-                const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
-                // lane h writes slots [16h, 16h + 16)
-#pragma unroll
-                for (int i = 0; i < kTop; ++i) {
-                    if ((uint32_t)i >= p.k) continue;
-                    if ((i >> 4) != (int)h) continue;
-                    const bool live = (uint32_t)i < keff;
-                    p.out_ids[out + i] = live ? sc[i] : kEmptyId;
-                    p.out_dists[out + i] = live ? sd[i] : kEmptyDist;
-                }
                 s_done += h == 0u ? 1u : 0u;
             } else if (h == 0u) {
                 bool queued = false;
@@ -654,7 +673,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                             for (int i = 0; i < kSeq; ++i)
                                 if ((uint32_t)i < m)
                                     p.chain_pool[off + i] = make_uint4(__float_as_uint(sd[i]), sc[i],
-                                                                       p.gids[mem_lds[sc[i] < n ? sc[i] : 0u]], 0u);
+                                                                       gid_lds[sc[i] < n ? sc[i] : 0u], 0u);
                             const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
                             p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), off, m | (keff << 8));
                             queued = true;
