@@ -157,75 +157,125 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(Leaf
 // the bounded insertion over G's members in column order; other candidates can
 // neither enter in front of G's nor stay in the buffer.
 //
-// One wave per queued row.  Lane i holds G's i-th entry; a bitonic sort across
-// lanes orders G by column; then G is replayed through wave_insert (the
-// bounded insertion of leaf_build.rs:913-951 with slots in lanes).
-constexpr int kChainMax = 64;
-constexpr int kChainWaves = 4;
+// One lane per queued row (|G| <= 40).  The lane sorts (column, index) keys of
+// G in registers, keeps G's (distance, global id) in LDS for lookups by index,
+// and replays the bounded insertion of leaf_build.rs:913-951 over a 32-slot
+// list in registers: slot s is visited from the back, and a candidate moves
+// forward while it beats the slot before it.  Blocks of 8 slots that no lane
+// of the wave can touch are skipped.
+constexpr int kChainSeq = 40;      // G holds at most kMaxK + 8 entries
+constexpr int kChainSlots = kMaxK; // the row's top-k list
+constexpr int kChainThreads = 128;
 
-__global__ __launch_bounds__(kChainWaves * 64) void leaf_chain_kernel(LeafParams p) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+__global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p) {
+    __shared__ uint2 ent[kChainSeq][kChainThreads];      // (distance bits, global id) of G's entry i
+    __shared__ uint8_t order[kChainSeq][kChainThreads];  // G's entry indices in column order
+    const uint32_t tid = threadIdx.x;
     uint32_t count = *p.chain_count;
     if (count > p.chain_capacity) count = p.chain_capacity;
-    const uint32_t stride = gridDim.x * kChainWaves;
     uint64_t done = 0;
-    uint32_t w = blockIdx.x * kChainWaves + wave;
-    // software pipeline: the next row's header and pool entry load while the
-    // current row is sorted and replayed
-    uint4 hdr = w < count ? p.chain_rows[w] : make_uint4(0u, 0u, 0u, 0u);
-    uint4 e = make_uint4(__float_as_uint(kEmptyDist), 0xffffffffu, kEmptyId, 0u);
-    if (w < count && lane < (hdr.w & 0xffu)) e = p.chain_pool[hdr.z + lane];
-    while (w < count) {
-        const uint32_t wn = w + stride;
-        const uint4 hdr_n = wn < count ? p.chain_rows[wn] : make_uint4(0u, 0u, 0u, 0u);
-        const uint64_t out = (uint64_t)hdr.x | ((uint64_t)hdr.y << 32);
+    for (uint32_t base = blockIdx.x * kChainThreads; base < count; base += gridDim.x * kChainThreads) {
+        const uint32_t w = base + tid;
+        const bool live = w < count;
+        const uint4 hdr = live ? p.chain_rows[w] : make_uint4(0u, 0u, 0u, 0u);
         uint32_t m = hdr.w & 0xffu;
-        m = m < (uint32_t)kChainMax ? m : (uint32_t)kChainMax;
+        m = m < (uint32_t)kChainSeq ? m : (uint32_t)kChainSeq;
         const uint32_t keff = (hdr.w >> 8) & 0xffu;
-        uint32_t col = lane < m ? e.y : 0xffffffffu;
-        float d = lane < m ? __uint_as_float(e.x) : kEmptyDist;
-        uint32_t g = lane < m ? e.z : kEmptyId;
-        // bitonic sort of the 64 lanes by column (padding lanes sort last)
+        // keys: column << 6 | index, padding sorts last
+        uint32_t key[64];
 #pragma unroll
-        for (uint32_t kk = 2; kk <= 64; kk <<= 1) {
+        for (int i = 0; i < 64; ++i) key[i] = 0xffffffffu;
 #pragma unroll
-            for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
-                const uint32_t oc = __shfl_xor(col, j);
-                const float od = __shfl_xor(d, j);
-                const uint32_t og = __shfl_xor(g, j);
-                const bool up = (lane & kk) == 0u;
-                const bool lower = (lane & j) == 0u;
-                const bool take = (up == lower) ? (oc < col) : (oc > col);
-                col = take ? oc : col;
-                d = take ? od : d;
-                g = take ? og : g;
+        for (int i = 0; i < kChainSeq; ++i) {
+            if ((uint32_t)i < m) {
+                const uint4 e = p.chain_pool[hdr.z + i];
+                key[i] = (e.y << 6) | (uint32_t)i;
+                ent[i][tid] = make_uint2(e.x, e.z);
             }
         }
-        if (wn < count && lane < (hdr_n.w & 0xffu)) e = p.chain_pool[hdr_n.z + lane];
-        // bounded insertion over G in column order; slot j lives in lane j
-        float bd = kEmptyDist;
-        uint32_t bg = kEmptyId;
-        uint32_t len = 0;
-        for (uint32_t i = 0; i < m && keff > 0u; ++i)
-            len = wave_insert(lane_bcast(d, i), lane_bcast(g, i), bd, bg, len, keff);
-        if (lane < p.k) {
-            const bool live = lane < len;
-            p.out_ids[out + lane] = live ? bg : kEmptyId;
-            p.out_dists[out + lane] = live ? bd : kEmptyDist;
+#pragma unroll
+        for (int kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+            for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+#pragma unroll
+                for (int i = 0; i < 64; ++i) {
+                    const int l = i ^ jj;
+                    if (l > i) {
+                        const uint32_t lo = min(key[i], key[l]), hi = max(key[i], key[l]);
+                        const bool up = (i & kk) == 0;
+                        key[i] = up ? lo : hi;
+                        key[l] = up ? hi : lo;
+                    }
+                }
+            }
         }
-        done += lane == 0u ? 1u : 0u;
-        hdr = hdr_n;
-        w = wn;
+#pragma unroll
+        for (int i = 0; i < kChainSeq; ++i) order[i][tid] = (uint8_t)(key[i] & 63u);
+        // bounded insertion in column order
+        float bd[kChainSlots];
+        uint32_t bg[kChainSlots];
+#pragma unroll
+        for (int s = 0; s < kChainSlots; ++s) {
+            bd[s] = kEmptyDist;
+            bg[s] = kEmptyId;
+        }
+        uint32_t len = 0;
+        for (int t = 0; t < kChainSeq; ++t) {
+            if (!__any((uint32_t)t < m && keff > 0u)) break;
+            const bool act = (uint32_t)t < m && keff > 0u;
+            const uint2 x = ent[act ? order[t][tid] : 0u][tid];
+            const float dc = __uint_as_float(x.x);
+            const uint32_t gc = x.y;
+            const bool full = len >= keff;
+            // start: the slot the candidate takes first (the empty slot, or the
+            // last one, which it must beat to enter at all)
+            const int start = act ? (int)(full ? keff - 1u : len) : -1;
+            bool moving = false;
+#pragma unroll
+            for (int blk = kChainSlots / 8 - 1; blk >= 0; --blk) {
+                if (!__any(moving || start >= 8 * blk)) continue;
+                // beats(c, slot s) for the block's first slot; later slots carry it down
+                bool b_next = beats(dc, gc, bd[8 * blk + 7], bg[8 * blk + 7]);
+#pragma unroll
+                for (int u = 7; u >= 0; --u) {
+                    const int s = 8 * blk + u;
+                    const bool b_here = b_next;  // beats(c, slot s), before any change to slot s
+                    if (s == start) moving = full ? b_here : true;
+                    const bool b_prev = s > 0 ? beats(dc, gc, bd[s > 0 ? s - 1 : 0], bg[s > 0 ? s - 1 : 0]) : false;
+                    const bool shift = moving && b_prev;
+                    const float nd = moving ? (shift ? bd[s > 0 ? s - 1 : 0] : dc) : bd[s];
+                    const uint32_t ng = moving ? (shift ? bg[s > 0 ? s - 1 : 0] : gc) : bg[s];
+                    bd[s] = nd;
+                    bg[s] = ng;
+                    moving = shift;
+                    b_next = b_prev;
+                }
+            }
+            len += (act && !full) ? 1u : 0u;
+        }
+        if (live) {
+            const uint64_t out = (uint64_t)hdr.x | ((uint64_t)hdr.y << 32);
+#pragma unroll
+            for (int s = 0; s < kChainSlots; ++s) {
+                if ((uint32_t)s >= p.k) continue;
+                const bool keep = (uint32_t)s < len;
+                p.out_ids[out + s] = keep ? bg[s] : kEmptyId;
+                p.out_dists[out + s] = keep ? bd[s] : kEmptyDist;
+            }
+            done += 1;
+        }
     }
-    if (lane == 0) counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
+    // one atomic per wave
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) done += __shfl_xor(done, off);
+    if ((tid & 63u) == 0u) counter_add(p.counters, TESSA_C_LEAF_ROWS, done);
 }
 
 }  // namespace
 
 int launch_leaf_chain(const LeafParams &p, hipStream_t stream) {
     // grid-stride over the device-side queue count: no host round trip
-    hipLaunchKernelGGL(leaf_chain_kernel, dim3(2048), dim3(kChainWaves * 64), 0, stream, p);
+    hipLaunchKernelGGL(leaf_chain_kernel, dim3(2048), dim3(kChainThreads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -457,11 +457,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                         const int vi = 4 * q + e;
                         const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
                         bool take = __fmul_rn((float)acc[vi], csv[e]) >= tau;
-                        if (kCheck) take = take && row_ok && c < n && c != r;
-                        if (take) {
-                            if (cnt < cap) slog[cnt] = make_uint2((uint32_t)acc[vi], c);
-                            ++cnt;
-                        }
+                        if (kCheck) take = take & row_ok & (c < n) & (c != r);
+                        // one branch per candidate: the store (room left) and the count
+                        const bool store = take & (cnt < cap);
+                        if (store) slog[cnt] = make_uint2((uint32_t)acc[vi], c);
+                        cnt += take ? 1u : 0u;
                     }
                 }
             };
