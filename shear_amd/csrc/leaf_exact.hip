@@ -233,7 +233,9 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
             bool moving = false;
 #pragma unroll
             for (int blk = kChainSlots / 8 - 1; blk >= 0; --blk) {
-                if (!__any(moving || start >= 8 * blk)) continue;
+                // a lane works in this block while its candidate moves through it
+                // or enters here (start in the block)
+                if (!__any(moving || (start >= 8 * blk && start < 8 * blk + 8))) continue;
                 // beats(c, slot s) for the block's first slot; later slots carry it down
                 bool b_next = beats(dc, gc, bd[8 * blk + 7], bg[8 * blk + 7]);
 #pragma unroll

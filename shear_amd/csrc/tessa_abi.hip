@@ -118,9 +118,10 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint4), "chain pool");
     if (st.code) return st;
     // one log slot (256 threads' logs) per 128 rows of this batch, at most
-    // kLeafLogSlots; a persistent MFMA workgroup of 8 waves (256 rows) takes two
+    // kLeafLogSlots; a persistent MFMA workgroup of 8 waves (256 rows) takes
+    // two, and the grid needs one workgroup per XCD at least: 16 slots minimum
     const uint64_t blocks = (rows + 127) / 128;
-    const uint64_t slots = ((blocks < kLeafLogSlots ? blocks : kLeafLogSlots) + 7) / 8 * 8;
+    const uint64_t slots = ((blocks < kLeafLogSlots ? blocks : kLeafLogSlots) + 15) / 16 * 16;
     st = grow(&ws.survivor_log, &ws.log_entries, slots * 256 * kLeafLogCapacity, sizeof(uint2), "survivor log");
     if (st.code) return st;
     *out = &ws;

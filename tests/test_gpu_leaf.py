@@ -141,3 +141,33 @@ def test_c2_shaped_leaves_match_oracle(gpu, orc):
     assert_same(ids, d, want_ids, want_d, "C2-shaped")
     # the exact re-run is the exception, not the rule, on realistic data
     assert ctr[N.C_LEAF_FALLBACK_ROWS] < 0.05 * leaves * 1024
+
+
+_FRESH = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+from gpu_helpers import run_leaf, to_dev_sq8
+from oracle import pyoracle as orc
+from shear_amd import _native as N
+rng = np.random.default_rng(5)
+codes, scales, norms = orc.quantize(rng.standard_normal((40, 32)).astype(np.float32))
+ids, d, _ = run_leaf(to_dev_sq8(codes, scales, norms), np.arange(40), np.arange(40), [0], [40], 8, N.EXEC_MFMA)
+want_ids, want_d = orc.leaf_topk(codes, scales, norms, np.arange(40, dtype=np.uint32),
+                                 np.arange(40, dtype=np.uint32), np.array([0]), [40], 8)
+assert np.array_equal(ids, want_ids) and np.array_equal(d.view(np.uint32), want_d.view(np.uint32))
+print("fresh-process leaf ok", flush=True)
+"""
+
+
+def test_tiny_batch_in_a_fresh_process(gpu):
+    # The per-device leaf workspace grows and is kept, so in one process a
+    # tiny batch after a large one never sees a tiny workspace.  A fresh
+    # process runs the tiny case first (regression: the persistent grid had
+    # no workgroup when the survivor log held fewer than 16 slots).
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FRESH, root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "fresh-process leaf ok" in r.stdout
