@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--traffic-json", default=os.path.join(HERE, "profiles", "leaf_mfma_c2_traffic.json"),
                     help="measured HBM bytes per launch of leaf_mfma_kernel (rocprofv3 --pmc FETCH_SIZE and "
                          "WRITE_SIZE, scaled by a copy kernel; see profiles/leaf_mfma_c2_traffic.md)")
+    ap.add_argument("--subtree-rows", type=int, default=10_000_000,
+                    help="rows of the in-HBM subtree leg (C3: 10M x 768, leaves <= 2048, fanout 2, k=32)")
+    ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -210,8 +213,116 @@ def main() -> int:
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
+
+    if not args.no_subtree:
+        del out_ids, out_d, sq8, gids, lay
+        torch.cuda.empty_cache()
+        result["subtree"] = subtree_leg(args.subtree_rows, dev, check=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def subtree_leg(rows, dev, check=True, runs=2):
+    """C3-shaped resident subtree: rows x 768 unit vectors (1000-component
+    mixture, sigma 0.25, 5 % uniform outliers, random order, seed 2), one
+    tessa_session_run_subtree: level-synchronous partition (leaves <= 2048,
+    root fanout 2, max depth 16) then the leaf top-k (k = 32) on every leaf."""
+    import torch
+
+    from shear_amd import _native as N
+    from shear_amd import datagen
+    from shear_amd import subtree as S
+    from shear_amd import tessa as T
+
+    t0 = time.time()
+    x = datagen.c3_torch(rows, DIM, 1000, 0.25, 0.05, 2, device=dev)
+    sq8 = T.quantize_sq_int8_matrix(x)
+    del x
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    gids = torch.arange(rows, dtype=torch.int32, device=dev)
+    sess = S.SubtreeSession(0)
+    sess.upload_device(sq8, gids)
+    log(f"subtree: generated, quantized and uploaded {rows}x{DIM} in {time.time() - t0:.1f}s")
+    # max_depth 16: one 10M-row task needs 11 levels to reach 2048-row leaves
+    # (the reference's default of 10 assumes the host's D0 split first)
+    params = S.PiPNNSubtreeParams(leaf_knn=K, c_max=2048, fanout_second=2, psamp_fraction=0.001, max_leaders=128,
+                                  random_seed=42, max_depth=16)
+    req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(rows, np.uint32), parent_points=rows,
+                                       min_recurse_size=64)
+    out = None
+    walls, part_ms, leaf_ms = [], [], []
+    for i in range(runs + 1):
+        out = None
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        out = sess.run(req, params)
+        torch.cuda.synchronize()
+        if i > 0:
+            walls.append((time.perf_counter() - w0) * 1e3)
+            part_ms.append(out.partition_ms)
+            leaf_ms.append(out.leaf_ms)
+    c = out.counters
+    sizes = out.leaf_sizes[: out.leaf_count]
+    pairs = int((sizes * (sizes - 1)).sum().item())
+    ops = 2.0 * sq8.padded_dim * pairs
+    counted_rows = int(c[N.P_LARGE_PHYSICAL_TILES]) * 16  # COUNT passes, all attempts (16-row tiles)
+    assign_bytes = counted_rows * (sq8.padded_dim + 8)
+    pm, lm = float(np.mean(part_ms)), float(np.mean(leaf_ms))
+    res = {
+        "workload": f"C3-shaped subtree: {rows} x {DIM} SQ8 (1000-comp GMM sigma 0.25, 5% outliers, unit-norm, "
+                    f"seed 2), leaves <= 2048, root fanout 2, max depth 16, k={K}",
+        "rows": rows,
+        "leaf_rows": int(out.leaf_rows),
+        "leaves": int(out.leaf_count),
+        "levels": int(out.levels),
+        "assignment_passes": int(c[N.P_ASSIGNMENT_PASSES]),
+        "split_retries": int(c[N.P_LARGE_SPLIT_RETRIES]),
+        "partition_ms": round(pm, 3),
+        "partition_counted_rows": counted_rows,
+        "partition_gb_per_s": round(assign_bytes / (pm / 1e3) / 1e9, 1),  # rows*(padded_dim+8) per COUNT pass
+        "leaf_ms": round(lm, 3),
+        "leaf_ops": ops,
+        "leaf_tops": round(ops / (lm / 1e3) / 1e12, 1),
+        "wall_ms": round(float(np.mean(walls)), 3),
+        "leaf_overflow_flags": int(out.leaf_counters[N.C_OVERFLOW_FLAGS]),
+    }
+    log(f"subtree: {res['leaves']} leaves, {res['leaf_rows']} rows, partition {pm:.1f} ms, leaf {lm:.1f} ms")
+    if check:
+        res["parity_sample"] = subtree_parity(sq8, gids, out)
+    return res
+
+
+def subtree_parity(sq8, gids, out, leaves=64):
+    """Oracle top-k of a sample of the subtree's leaves, compared bit for bit."""
+    from oracle import pyoracle as orc
+
+    lc = out.leaf_count
+    pick = np.linspace(0, lc - 1, min(leaves, lc)).astype(np.int64)
+    starts = out.leaf_starts[: lc].cpu().numpy()[pick]
+    sizes = out.leaf_sizes[: lc].cpu().numpy()[pick]
+    rows_all = out.leaf_row_ids[: out.leaf_rows].cpu().numpy().view(np.uint32)
+    members = np.concatenate([rows_all[s: s + z] for s, z in zip(starts, sizes)])
+    uniq, local = np.unique(members, return_inverse=True)
+    codes = sq8.codes[torch_index(uniq)].cpu().numpy()
+    scales = sq8.scales[torch_index(uniq)].cpu().numpy()
+    norms = sq8.norms[torch_index(uniq)].cpu().numpy()
+    g = gids[torch_index(uniq)].cpu().numpy().view(np.uint32)
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    want_ids, want_d = orc.leaf_topk(codes, scales, norms, g, local.astype(np.uint32), offs, sizes.tolist(), out.k)
+    ids = out.topk_ids.cpu().numpy().view(np.uint32)
+    d = out.topk_dists.cpu().numpy()
+    got_ids = np.concatenate([ids[s * out.k:(s + z) * out.k] for s, z in zip(starts, sizes)])
+    got_d = np.concatenate([d[s * out.k:(s + z) * out.k] for s, z in zip(starts, sizes)])
+    mism = int(np.count_nonzero((got_ids != want_ids) | (got_d.view(np.uint32) != want_d.view(np.uint32))))
+    log(f"subtree parity: {len(pick)} leaves, {len(got_ids)} slots, mismatches {mism}")
+    return {"leaves": int(len(pick)), "slots": int(len(got_ids)), "mismatched_slots": mism, "bit_exact": mism == 0}
+
+
+def torch_index(a):
+    import torch
+
+    return torch.from_numpy(np.asarray(a, np.int64)).to("cuda:0")
 
 
 def edge_leg(gids, lay, out_ids, out_d, stream, steps, warmup):

@@ -214,7 +214,9 @@ typedef struct tessa_config {
 
 tessa_status tessa_session_create(const tessa_config *cfg, tessa_session **out);
 tessa_status tessa_session_destroy(tessa_session *session);
-/* H2D copy of a host SQ8 resident set into session-owned device buffers. */
+/* Copy of an SQ8 resident set into session-owned device buffers; the view's
+ * arrays may be host or device memory (the copy direction follows the
+ * pointers). */
 tessa_status tessa_session_upload_sq8(tessa_session *session, const tessa_sq8_view *host);
 
 /* Host-layout leaf replay: host arrays in, host arrays out; event_ms gets the

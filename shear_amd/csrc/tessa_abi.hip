@@ -590,10 +590,10 @@ static tessa_status tessa_session_upload_sq8_locked(tessa_session *s, const tess
                            "SQ8 upload of %llu rows failed overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
                            (unsigned long long)rows, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
     }
-    TESSA_HIP_TRY(hipMemcpyAsync(s->codes, host->codes, rows * host->padded_dim, hipMemcpyHostToDevice, s->stream));
-    TESSA_HIP_TRY(hipMemcpyAsync(s->scales, host->scales, rows * 4, hipMemcpyHostToDevice, s->stream));
-    TESSA_HIP_TRY(hipMemcpyAsync(s->norms, host->norms, rows * 4, hipMemcpyHostToDevice, s->stream));
-    TESSA_HIP_TRY(hipMemcpyAsync(s->gids, host->global_ids, rows * 4, hipMemcpyHostToDevice, s->stream));
+    TESSA_HIP_TRY(hipMemcpyAsync(s->codes, host->codes, rows * host->padded_dim, hipMemcpyDefault, s->stream));
+    TESSA_HIP_TRY(hipMemcpyAsync(s->scales, host->scales, rows * 4, hipMemcpyDefault, s->stream));
+    TESSA_HIP_TRY(hipMemcpyAsync(s->norms, host->norms, rows * 4, hipMemcpyDefault, s->stream));
+    TESSA_HIP_TRY(hipMemcpyAsync(s->gids, host->global_ids, rows * 4, hipMemcpyDefault, s->stream));
     TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
     s->rows = rows;
     s->dim = host->dim;

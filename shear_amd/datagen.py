@@ -8,6 +8,8 @@ component", and leaves cut from consecutive rows are spatially coherent.
 * ``gmm_numpy``  CPU, numpy PCG64 -- used by tests and small configs.
 * ``gmm_torch``  GPU, torch Philox on the device -- used for bench-size data
                  (4M x 768 does not fit a host round trip inside a bench run).
+* ``c3_torch``   GPU, the in-HBM build configuration: mixture plus uniform
+                 outliers, rows in random order (a real dataset is not sorted).
 The two generators use different RNG streams; parity tests always feed the
 same generated arrays to both sides.
 """
@@ -45,4 +47,26 @@ def gmm_torch(n: int, dim: int, components: int, sigma: float, seed: int, device
         if unit_norm:
             x = x / torch.linalg.vector_norm(x, dim=1, keepdim=True)
         out[start:end] = x
+    return out
+
+
+def c3_torch(n: int, dim: int = 768, components: int = 1000, sigma: float = 0.25, outlier_frac: float = 0.05,
+             seed: int = 2, device="cuda", chunk_rows: int = 1 << 18):
+    """Mixture rows (component centres ~N(0, I), sigma noise) with a fraction of
+    U[-1, 1]^dim outliers, unit-normalised, in random row order."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    centers = torch.randn((components, dim), generator=g, device=device, dtype=torch.float32)
+    out = torch.empty((n, dim), dtype=torch.float32, device=device)
+    for start in range(0, n, chunk_rows):
+        end = min(n, start + chunk_rows)
+        m = end - start
+        comp = torch.randint(0, components, (m,), generator=g, device=device)
+        x = centers[comp] + sigma * torch.randn((m, dim), generator=g, device=device)
+        noise = torch.rand((m,), generator=g, device=device) < outlier_frac
+        u = torch.rand((m, dim), generator=g, device=device) * 2.0 - 1.0
+        x = torch.where(noise[:, None], u, x)
+        out[start:end] = x / torch.linalg.vector_norm(x, dim=1, keepdim=True)
     return out

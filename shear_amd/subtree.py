@@ -178,6 +178,14 @@ class SubtreeSession:
         est = int(plan.max_leaf_rows) * (4 + k * 8) + int(plan.max_leaf_count) * 16
         return DeferredGpuSubtreeTopK(est, _PinnedScatter(self, int(seq.value), gids, params, owned))
 
+    def upload_device(self, sq8, global_ids: torch.Tensor):
+        """Resident set from device tensors (an Sq8Matrix and int32-viewed u32
+        global ids): a device-to-device copy into the session."""
+        view = sq8.view(global_ids)
+        N.check(self._lib.tessa_session_upload_sq8(self._h, C.byref(view)), "session upload")
+        self.rows = sq8.rows
+        self.global_ids = None
+
     def run(self, request: GpuSubtreePartitionRequest, params: PiPNNSubtreeParams,
             partition_only: bool = False) -> SubtreeDeviceOutput:
         rq, plan, k, roots = self._request(self.rows, request, params, partition_only)
