@@ -529,25 +529,60 @@ __global__ __launch_bounds__(128) void emit_kernel(PartArgs a, uint32_t cur, uin
 }
 
 // ---- child layout and per-item prefixes ----------------------------------
-__global__ __launch_bounds__(128) void node_scan_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+// 8 groups of 128 threads (one thread per leader slot) split the node's items
+// into 8 ranges; each group sums its range, the groups' sums are scanned in
+// LDS, then each group writes the exclusive prefixes of its range.  Item
+// counts are read 16 items at a time, so the loads of a batch are in flight
+// together.
+constexpr uint32_t kScanGroups = 8;
+constexpr uint32_t kScanBatch = 16;
+
+__global__ __launch_bounds__(kScanGroups * kPartMaxLeaders) void node_scan_kernel(PartArgs a, uint32_t cur,
+                                                                                 uint32_t level_nodes) {
+    __shared__ uint32_t group_sum[kScanGroups][kPartMaxLeaders];
     const uint32_t ni = blockIdx.x;
     NodeDesc *nd = a.nodes[cur] + ni;
     const uint32_t status = nd->status;
     if (status != kNodeAccepted && status != kNodeBalanced) return;
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = threadIdx.x % kPartMaxLeaders;
+    const uint32_t g = threadIdx.x / kPartMaxLeaders;
     const uint32_t nl = nd->num_leaders;
     const uint64_t cbase = (uint64_t)ni * kPartMaxLeaders;
-    if (status == kNodeAccepted && t < nl) {
+    if (status == kNodeAccepted) {
         // Stable scatter: exclusive prefix of this slot's count over the items.
+        const uint32_t items = nd->items;
+        const uint32_t per = (items + kScanGroups - 1u) / kScanGroups;
+        const uint32_t i0 = g * per < items ? g * per : items;
+        const uint32_t i1 = i0 + per < items ? i0 + per : items;
+        uint32_t *col = a.item_counts + (uint64_t)nd->item_base * kPartMaxLeaders + t;
+        uint32_t sum = 0u;
+        if (t < nl) {
+            for (uint32_t i = i0; i < i1; i += kScanBatch) {
+                uint32_t v[kScanBatch];
+#pragma unroll
+                for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
+#pragma unroll
+                for (uint32_t u = 0; u < kScanBatch; ++u) sum += v[u];
+            }
+        }
+        group_sum[g][t] = sum;
+        __syncthreads();
         uint32_t run = 0u;
-        for (uint32_t i = 0; i < nd->items; ++i) {
-            const uint64_t idx = (uint64_t)(nd->item_base + i) * kPartMaxLeaders + t;
-            const uint32_t v = a.item_counts[idx];
-            a.item_counts[idx] = run;
-            run += v;
+        for (uint32_t h = 0; h < g; ++h) run += group_sum[h][t];
+        if (t < nl) {
+            for (uint32_t i = i0; i < i1; i += kScanBatch) {
+                uint32_t v[kScanBatch];
+#pragma unroll
+                for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
+#pragma unroll
+                for (uint32_t u = 0; u < kScanBatch; ++u) {
+                    if (i + u < i1) col[(uint64_t)(i + u) * kPartMaxLeaders] = run;
+                    run += v[u];
+                }
+            }
         }
     }
-    if (t == 0) {
+    if (threadIdx.x == 0) {
         // compute_backend.rs:15666-15718: children in slot order.
         uint32_t leaf_children = 0, node_children = 0;
         uint64_t leaf_rows = 0, node_rows = 0;
@@ -1135,7 +1170,8 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
             hipLaunchKernelGGL(reset_retry_kernel, dim3(1), dim3(1), 0, s, a.hdr);
         }
         if (attempt == 16u) return -2;
-        hipLaunchKernelGGL(node_scan_kernel, dim3(level_nodes), dim3(128), 0, s, a, cur, level_nodes);
+        hipLaunchKernelGGL(node_scan_kernel, dim3(level_nodes), dim3(kScanGroups * kPartMaxLeaders), 0, s, a, cur,
+                           level_nodes);
         hipLaunchKernelGGL(pub_scan_kernel, dim3(1), dim3(1024), 0, s, a, cur, level_nodes);
         hipLaunchKernelGGL(scatter_kernel, dim3(grid), dim3(256), 0, s, a, cur, level_nodes);
         if (hipGetLastError() != hipSuccess) return -1;
