@@ -236,7 +236,13 @@ def subtree_leg(rows, dev, check=True, runs=2):
 
     t0 = time.time()
     x = datagen.c3_torch(rows, DIM, 1000, 0.25, 0.05, 2, device=dev)
+    torch.cuda.synchronize()
+    q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    q0.record()
     sq8 = T.quantize_sq_int8_matrix(x)
+    q1.record()
+    q1.synchronize()
+    quantize_ms = q0.elapsed_time(q1)
     del x
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -285,7 +291,14 @@ def subtree_leg(rows, dev, check=True, runs=2):
         "leaf_ops": ops,
         "leaf_tops": round(ops / (lm / 1e3) / 1e12, 1),
         "wall_ms": round(float(np.mean(walls)), 3),
+        # SQ8 quantizer on the same rows (once, outside the runs): algorithmic
+        # bytes 4*dim read + padded_dim + 8 written per row
+        "quantize_ms": round(quantize_ms, 3),
+        "quantize_gb_per_s": round(rows * (4 * DIM + sq8.padded_dim + 8) / (quantize_ms / 1e3) / 1e9, 1),
         "leaf_overflow_flags": int(out.leaf_counters[N.C_OVERFLOW_FLAGS]),
+        "leaf_survivors_per_row": round(float(out.leaf_counters[N.C_LEAF_SURVIVORS]) / max(1, int(out.leaf_rows)), 2),
+        "leaf_chain_rows": int(out.leaf_counters[N.C_LEAF_CHAIN_ROWS]),
+        "leaf_exact_reruns": int(out.leaf_counters[N.C_LEAF_FALLBACK_ROWS]),
     }
     log(f"subtree: {res['leaves']} leaves, {res['leaf_rows']} rows, partition {pm:.1f} ms, leaf {lm:.1f} ms")
     if check:
