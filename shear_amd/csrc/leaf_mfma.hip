@@ -42,6 +42,7 @@
 //    2e-5) is queued, with G, for the chain replay kernel; uncertified rows are
 //    queued for the exact scalar kernel.
 #include <type_traits>
+#include <utility>
 
 #include "leaf_kernels.h"
 #include "tessa_device.h"
@@ -91,10 +92,80 @@ struct Layout {
 #endif
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
-// LDS: one column tile plus the leaf's member ids, scales, norms and global
-// ids, 64 bytes of scalars and each wave's output staging (32 rows x 32 slots).
+// LDS: a region holding two column tiles and each wave's 4 KB accumulator
+// scratch during the tile stream, overlaid afterwards by each wave's output
+// staging (32 rows x 32 slots of ids and distances); then the leaf's member
+// ids, scales, norms and global ids, and 64 bytes of scalars.
+__host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes) {
+    return (2u * tile_bytes + kWaves * 16u * 64u * 4u) > (kWaves * 2u * 32u * kTop * 4u)
+               ? (2u * tile_bytes + kWaves * 16u * 64u * 4u)
+               : (kWaves * 2u * 32u * kTop * 4u);
+}
 __host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
-    return tile_bytes + cols_cap * 16u + 64u + kWaves * 2u * 32u * kTop * 4u;
+    return union_bytes(tile_bytes) + cols_cap * 16u + 64u;
+}
+
+// Compile-time loops: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, B + I>{}), ...);
+}
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (E > B) static_for_impl<B>(f, std::make_integer_sequence<int, E - B>{});
+}
+
+// One column tile's MFMAs (A = the tile row read from LDS at `arow`, B = the
+// row codes) with an epilogue spread over the k-steps: step s runs epilogue
+// units [s*kUnits/KS, (s+1)*kUnits/KS) after its MFMA.  The units belong to
+// the previous position and do not depend on these MFMAs, so they issue
+// while the matrix pipe runs.  A operands are read two steps ahead; a
+// scheduling fence after each step keeps this order (the default schedule
+// puts every LDS read first and the whole epilogue after the last MFMA).
+template <int KS, int kUnits, typename Epi>
+__device__ __forceinline__ v16i mfma_block(const int8_t *arow, const v4i (&bfrag)[KS], Epi &&epi) {
+    v16i acc = {};
+    v4i ring[3];
+    ring[0] = *reinterpret_cast<const v4i *>(arow);
+    if constexpr (KS > 1) ring[1] = *reinterpret_cast<const v4i *>(arow + 32);
+    static_for<0, KS>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        if constexpr (s + 2 < KS) ring[(s + 2) % 3] = *reinterpret_cast<const v4i *>(arow + 32 * (s + 2));
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[s % 3], bfrag[s], acc, 0, 0, 0);
+        static_for<s * kUnits / KS, (s + 1) * kUnits / KS>(epi);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    return acc;
+}
+
+// Compare-exchange number c (0..79) of the bitonic sort of 16 values: stage
+// c/8 of (k, j) = (2,1) (4,2) (4,1) (8,4) (8,2) (8,1) (16,8) (16,4) (16,2)
+// (16,1); within a stage the (c%8)-th index i with i&j == 0 pairs with i+j.
+__host__ __device__ constexpr int sort16_k(int c) {
+    return c < 8 ? 2 : c < 24 ? 4 : c < 48 ? 8 : 16;
+}
+__host__ __device__ constexpr int sort16_j(int c) {
+    return c < 8 ? 1 : c < 24 ? (2 >> ((c - 8) / 8)) : c < 48 ? (4 >> ((c - 24) / 8)) : (8 >> ((c - 48) / 8));
+}
+__host__ __device__ constexpr int ce_low(int c, int jj) {
+    return ((c % 8) / jj) * 2 * jj + (c % 8) % jj;
+}
+
+// x unchanged, but opaque to the optimizer: conditions derived from it are
+// evaluated where they are used, inside the work-item loop, instead of being
+// hoisted out of it as loop invariants (every hoisted lane mask would hold two
+// scalar registers for the kernel's lifetime and spill).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
+
+// Barrier for LDS hand-offs only: waits for this wave's LDS operations, not
+// for its global loads and stores (prefetches stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Compare-exchange on (key, payload) pairs; ascending when `up`.
@@ -259,22 +330,21 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                                                               uint32_t total_work, uint32_t per_xcd) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // Runtime layout: tile | members | scales | norms | global ids | misc | stage.
+    // Runtime layout: (tiles x2 | scratch, overlaid by stage) | members | scales | norms | global ids | misc.
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
-    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + L::kTileBytes);
+    uint32_t *stage = reinterpret_cast<uint32_t *>(smem);  // per wave: 32 rows x k output ids, then distances
+    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + union_bytes(L::kTileBytes));
     float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
     float *cn_lds = cs_lds + cols_cap;
     uint32_t *gid_lds = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);  // global id per member
     uint32_t *misc = gid_lds + cols_cap;
-    uint32_t *stage = misc + 16;  // per wave: 32 rows x k output ids, then distances
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
     const uint32_t j = lane & 31u;
     const uint32_t h = lane >> 5;
-    const uint32_t pd = p.padded_dim;
     const uint32_t cap = p.log_capacity;
         // This thread's entries are contiguous, so the final fold reads 16 of
     // them with immediate offsets from one address.
@@ -301,6 +371,8 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             continue;
         }
         const uint32_t *mem = p.members + p.member_offsets[leaf];
+        const uint32_t pd = opaque_u32(p.padded_dim);
+        const uint32_t pk = opaque_u32(p.k);
 
         __syncthreads();  // previous item's readers of the LDS arrays are done
         if (tid == 0) {
@@ -324,6 +396,12 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 lo = fminf(lo, cn);
                 hi = fmaxf(hi, cn);
             }
+            // the last column tile's columns past n: zero scale, infinite norm
+            // (their codes are zero, so their sampled distance is +inf)
+            for (uint32_t c = n + tid; c < ((n + 31u) & ~31u); c += kThreads) {
+                cs_lds[c] = 0.0f;
+                cn_lds[c] = __builtin_inff();
+            }
             // norms are sums of squares (>= 0): their bit patterns order like the values
             atomicMin(&misc[0], __float_as_uint(lo));
             atomicMax(&misc[1], __float_as_uint(hi));
@@ -336,7 +414,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const bool row_ok = r < n;
         const bool wave_rows_full = row_base + wave * 32u + 32u <= n;
         const uint32_t mr = row_ok ? mem_lds[r] : 0u;
-        const uint32_t keff = n > 1u ? ((p.k < n - 1u) ? p.k : (n - 1u)) : 0u;
+        const uint32_t keff = n > 1u ? ((pk < n - 1u) ? pk : (n - 1u)) : 0u;
 
         // Row codes for the whole K range (B operand), zero past padded_dim.
         v4i bfrag[KS];
@@ -354,121 +432,240 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const float rn = row_ok ? cn_lds[r] : 0.0f;
 
         const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
-        const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
         v4i pre[L::kChunksPerThread];
 
+        // Branch-free: every lane reads its member ids first (one LDS wait),
+        // then loads from a valid address (member 0, offset 0, when its chunk
+        // lies past the tile, the leaf or the padded row).  Such chunks are
+        // zeroed when stored to LDS, a position later, so nothing waits for
+        // the loads here.
+        uint32_t pre_ok = 0u;  // bit q: chunk q of `pre` is real data
         auto load_tile = [&](uint32_t t) {
+            uint32_t mc[L::kChunksPerThread], offs[L::kChunksPerThread];
+            pre_ok = 0u;
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
                 const uint32_t chunk = tid + q * kThreads;
-                v4i z = {0, 0, 0, 0};
-                if (chunk < (uint32_t)L::kChunks) {
-                    const uint32_t row = chunk / (KS * 2);
-                    const uint32_t off = (chunk % (KS * 2)) * 16u;
-                    const uint32_t c = t * kTileCols + row;
-                    if (c < n && off < pd)
-                        z = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mem_lds[c] * pd + off);
-                }
-                pre[q] = z;
+                const uint32_t row = chunk / (KS * 2);
+                const uint32_t off = (chunk % (KS * 2)) * 16u;
+                const uint32_t c = t * kTileCols + row;
+                const bool ok = (chunk < (uint32_t)L::kChunks) & (c < n) & (off < pd);
+                pre_ok |= ok ? (1u << q) : 0u;
+                offs[q] = ok ? off : 0u;
+                mc[q] = mem_lds[ok ? c : 0u];
             }
+#pragma unroll
+            for (int q = 0; q < L::kChunksPerThread; ++q)
+                pre[q] = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mc[q] * pd + offs[q]);
         };
-        auto store_tile = [&]() {
+        auto store_tile = [&](int8_t *dst) {
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
                 const uint32_t chunk = tid + q * kThreads;
                 if (chunk < (uint32_t)L::kChunks) {
                     const uint32_t row = chunk / (KS * 2);
                     const uint32_t off = (chunk % (KS * 2)) * 16u;
-                    *reinterpret_cast<v4i *>(tile + row * L::kTileStride + off) = pre[q];
+                    const v4i zero = {0, 0, 0, 0};
+                    *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = ((pre_ok >> q) & 1u) ? pre[q] : zero;
                 }
             }
-        };
-        auto mfma_tile = [&]() {
-            v16i acc = {};
-            const int8_t *arow = tile + j * L::kTileStride + 16u * h;
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const v4i a = *reinterpret_cast<const v4i *>(arow + 32 * s);
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
-            }
-            return acc;
         };
 
-        // ---- phase A: row threshold from every kSampleStride-th column tile ----
-        // Each lane keeps the 16 smallest exact distances it sees (values only);
-        // F is the pair's kSel-th smallest sample distance plus 3 eps, so at
-        // least kSel candidates lie at or below F.
+        // ---- the tile stream ----------------------------------------------------
+        // Stream position i < nA is phase A's sampled tile i*kSampleStride,
+        // position nA + t is phase B's tile t.  Column tiles are double
+        // buffered in LDS with one barrier per position: position i's MFMAs
+        // read buffer i&1 while the tile of position i+1 goes to the other
+        // buffer and position i+2's codes are in flight in registers.  The
+        // epilogue of position i-1 (its accumulators held over) runs in the
+        // same straight-line block as position i's MFMAs, so the VALU work
+        // overlaps the matrix pipe.
+        //  * phase A epilogue: each lane keeps the 16 smallest exact distances
+        //    it sees (values only); F is the pair's kSel-th smallest sample
+        //    distance plus 3 eps, so at least kSel candidates lie at or below F;
+        //  * phase B epilogue: a 16-bit mask of the lane's candidates meeting
+        //    cs*dot >= tau, and the raw dots parked in the wave's LDS scratch;
+        //    the next position drains the mask (set bits only) into the lane's
+        //    survivor log.  Column validity (c < n, c != r) is checked there.
         constexpr int kSample = 16;
         const int rsel = (int)(keff < (uint32_t)kSampleRank ? keff : (uint32_t)kSampleRank);
         float samp[kSample];
 #pragma unroll
         for (int i = 0; i < kSample; ++i) samp[i] = __builtin_inff();
-        for (uint32_t t = 0; t < ntiles; t += kSampleStride) {
-            load_tile(t);
-            __syncthreads();
-            store_tile();
-            __syncthreads();
-            const v16i acc = mfma_tile();
-            const uint32_t cbase = t * kTileCols;
-            float v[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int vi = 4 * q + e;
-                    const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
-                    const bool ok = row_ok && c < n && c != r;
-                    v[vi] = ok ? leaf_l2(acc[vi], rs, rn, cs_lds[c < n ? c : 0], cn_lds[c < n ? c : 0])
-                               : __builtin_inff();
-                }
-            }
-            bitonic_sort_v<16>(v);
-#pragma unroll
-            for (int i = 0; i < kSample; ++i) samp[i] = fminf(samp[i], v[kSample - 1 - i]);
-            bitonic_merge_v<kSample>(samp);
-        }
         float F = -__builtin_inff();
-        if (rsel > 0) F = __fadd_rn(pair_kth<kSample>(samp, rsel), kFilterMargin);
-        // tau: necessary condition on cs * dot for d <= F
-        const float tau = !row_ok ? __builtin_inff()
-                          : (F == -__builtin_inff() ? __builtin_inff() : filter_bound(F, rs, rn, cn_min, cn_max));
+        float tau = __builtin_inff();
+        const uint32_t nA = (ntiles + kSampleStride - 1u) / kSampleStride;
+        const uint32_t S = nA + ntiles;
+        auto tile_of = [&](uint32_t i) { return i < nA ? i * kSampleStride : i - nA; };
+        int8_t *const buf0 = tile;
+        int8_t *const buf1 = tile + L::kTileBytes;
+        int *const scr = reinterpret_cast<int *>(tile + 2 * L::kTileBytes) + wave * (16u * 64u);
 
-        // ---- phase B: every tile, survivors (cs*dot >= tau) to the log ------------
-        uint32_t cnt = 0;
-        __syncthreads();
-        load_tile(0);
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            __syncthreads();
-            store_tile();
-            __syncthreads();
-            if (t + 1 < ntiles) load_tile(t + 1);
-            const v16i acc = mfma_tile();
-            const uint32_t cbase = t * kTileCols;
-            const bool checked =
-                __builtin_amdgcn_readfirstlane((t == diag_tile || cbase + kTileCols > n || !wave_rows_full) ? 1 : 0);
-            auto epilogue = [&](auto check_tag) {
-                constexpr bool kCheck = decltype(check_tag)::value;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 cs4 = *reinterpret_cast<const float4 *>(cs_lds + cbase + 8 * q + 4 * h);
-                    const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int vi = 4 * q + e;
-                        const uint32_t c = cbase + 4u * h + (uint32_t)(8 * q + e);
-                        bool take = __fmul_rn((float)acc[vi], csv[e]) >= tau;
-                        if (kCheck) take = take & row_ok & (c < n) & (c != r);
-                        // one branch per candidate: the store (room left) and the count
-                        const bool store = take & (cnt < cap);
-                        if (store) slog[cnt] = make_uint2((uint32_t)acc[vi], c);
-                        cnt += take ? 1u : 0u;
+        // Phase A epilogue units (148): per group of 4 candidates one LDS read
+        // of their scales and norms and 4 exact distances (20), the 80
+        // compare-exchanges of a bitonic sort, 16 minima against the kept
+        // samples and the 32 of their bitonic merge.
+        constexpr int kSampleUnits = 20 + 80 + 16 + 32;
+        float4 ep_cs[4], ep_cn[4];
+        // scale and norm arrays start 16-byte aligned; each group of 4 is a float4
+        const float *cs_al = static_cast<const float *>(__builtin_assume_aligned(cs_lds, 16));
+        const float *cn_al = static_cast<const float *>(__builtin_assume_aligned(cn_lds, 16));
+        float ep_v[16];
+        const v16i *ep_acc = nullptr;
+        uint32_t ep_cbase = 0u;
+        // Columns past n carry norm +inf (distance +inf); the row's own column
+        // lies in the wave's diagonal tile only, whose epilogue variant
+        // (kDiag) excludes it.  Rows past n get samples but tau = +inf.
+        auto sample_unit_impl = [&](auto wc, auto diag_tag) {
+            constexpr int W = decltype(wc)::value;
+            constexpr bool kDiag = decltype(diag_tag)::value;
+            if constexpr (W < 20) {
+                constexpr int q = W / 5, u = W % 5;
+                if constexpr (u == 0) {
+                    ep_cs[q] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * q + 4 * h);
+                    ep_cn[q] = *reinterpret_cast<const float4 *>(cn_al + ep_cbase + 8 * q + 4 * h);
+                } else {
+                    constexpr int e = u - 1, vi = 4 * q + e;
+                    const float csv = e == 0 ? ep_cs[q].x : e == 1 ? ep_cs[q].y : e == 2 ? ep_cs[q].z : ep_cs[q].w;
+                    const float cnv = e == 0 ? ep_cn[q].x : e == 1 ? ep_cn[q].y : e == 2 ? ep_cn[q].z : ep_cn[q].w;
+                    const float d = leaf_l2((*ep_acc)[vi], rs, rn, csv, cnv);
+                    if constexpr (kDiag) {
+                        const uint32_t c = ep_cbase + 4u * h + (uint32_t)(8 * q + e);
+                        ep_v[vi] = c != r ? d : __builtin_inff();
+                    } else {
+                        ep_v[vi] = d;
                     }
                 }
-            };
-            if (checked) epilogue(std::true_type{});
-            else epilogue(std::false_type{});
+            } else if constexpr (W < 100) {
+                constexpr int c = W - 20, k = sort16_k(c), jj = sort16_j(c), lo = ce_low(c, jj);
+                if constexpr ((lo & k) == 0) cexv(ep_v[lo], ep_v[lo + jj]);
+                else cexv(ep_v[lo + jj], ep_v[lo]);
+            } else if constexpr (W < 116) {
+                constexpr int i = W - 100;
+                samp[i] = fminf(samp[i], ep_v[kSample - 1 - i]);
+            } else {
+                constexpr int c = W - 116, jj = 8 >> (c / 8), lo = ce_low(c, jj);
+                cexv(samp[lo], samp[lo + jj]);
+            }
+        };
+        auto sample_unit = [&](auto wc) { sample_unit_impl(wc, std::false_type{}); };
+        auto sample_unit_diag = [&](auto wc) { sample_unit_impl(wc, std::true_type{}); };
+        const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
+        // Phase B epilogue units (24): per group of 4 candidates one LDS read
+        // of their scales, 4 filter tests, one LDS write of the raw dots.
+        constexpr int kMaskUnits = 24;
+        uint32_t ep_m = 0u;
+        auto mask_unit = [&](auto wc) {
+            constexpr int W = decltype(wc)::value, g = W / 6, u = W % 6;
+            if constexpr (u == 0) {
+                ep_cs[g] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * g + 4 * h);
+            } else if constexpr (u < 5) {
+                constexpr int e = u - 1, vi = 4 * g + e;
+                const float csv = e == 0 ? ep_cs[g].x : e == 1 ? ep_cs[g].y : e == 2 ? ep_cs[g].z : ep_cs[g].w;
+                ep_m |= (__fmul_rn((float)(*ep_acc)[vi], csv) >= tau) ? (1u << vi) : 0u;
+            } else {
+                const v4i d = {(*ep_acc)[4 * g], (*ep_acc)[4 * g + 1], (*ep_acc)[4 * g + 2], (*ep_acc)[4 * g + 3]};
+                *reinterpret_cast<v4i *>(scr + (g * 64 + lane) * 4) = d;
+            }
+        };
+        auto no_unit = [&](auto) {};
+        const uint32_t arow_off = j * L::kTileStride + 16u * h;
+        uint32_t cnt = 0;
+        auto drain = [&](uint32_t m, uint32_t tp) {
+            const uint32_t cbase = tp * kTileCols + 4u * h;
+            while (m != 0u) {
+                const uint32_t vi = (uint32_t)__builtin_ctz(m);
+                m &= m - 1u;
+                const uint32_t c = cbase + 8u * (vi >> 2) + (vi & 3u);
+                const int dot = scr[((vi >> 2) * 64u + lane) * 4u + (vi & 3u)];
+                const bool ok = (c < n) & (c != r);
+                if (ok & (cnt < cap)) slog[cnt] = make_uint2((uint32_t)dot, c);
+                cnt += ok ? 1u : 0u;
+            }
+        };
+
+        uint32_t pend_mask = 0u, pend_tile = 0u;
+        // Start of position i: the barrier, the tile of position i+1 from
+        // registers to the free LDS buffer, the held mask's drain, then the
+        // prefetch of position i+2.  Position i reads buffer i&1.
+        auto head = [&](uint32_t i) {
+            lds_barrier();
+            if (i + 1u < S) store_tile((i & 1u) ? buf0 : buf1);
+            drain(pend_mask, pend_tile);
+            pend_mask = 0u;
+            if (i + 2u < S) load_tile(tile_of(i + 2u));
+        };
+        auto src_of = [&](uint32_t i) -> const int8_t * { return (i & 1u) ? buf1 : buf0; };
+
+        // prologue: position 0 in LDS buffer 0, position 1 in registers
+        load_tile(tile_of(0));
+        store_tile(buf0);
+        load_tile(tile_of(1));  // S >= 2: nA >= 1 and ntiles >= 1
+        // accP holds the accumulators of the latest position; each block
+        // computes position i into accQ/accP alternately while the epilogue
+        // of position i-1 runs on the other.
+        v16i accP, accQ;
+        auto sample_block = [&](uint32_t i, const v16i &prev) {
+            ep_acc = &prev;
+            const uint32_t tp = tile_of(i - 1u);
+            ep_cbase = tp * kTileCols;
+            if (tp == diag_tile) return mfma_block<KS, kSampleUnits>(src_of(i) + arow_off, bfrag, sample_unit_diag);
+            return mfma_block<KS, kSampleUnits>(src_of(i) + arow_off, bfrag, sample_unit);
+        };
+        auto mask_block = [&](uint32_t i, const v16i &prev) {
+            ep_acc = &prev;
+            ep_cbase = (i - 1u - nA) * kTileCols;
+            ep_m = 0u;
+            const v16i acc = mfma_block<KS, kMaskUnits>(src_of(i) + arow_off, bfrag, mask_unit);
+            // the mask is needed here, not only by the next position's drain: its
+            // tests stay interleaved with the MFMAs instead of sinking past them
+            asm volatile("" : "+v"(ep_m));
+            pend_mask = ep_m;
+            pend_tile = i - 1u - nA;
+            return acc;
+        };
+        head(0);
+        accP = mfma_block<KS, 0>(src_of(0) + arow_off, bfrag, no_unit);
+        uint32_t i = 1;
+        // positions 1..nA: epilogues of the sampled tiles
+        for (; i + 1u <= nA; i += 2u) {
+            head(i);
+            accQ = sample_block(i, accP);
+            head(i + 1u);
+            accP = sample_block(i + 1u, accQ);
         }
-        s_tiles += ntiles + (ntiles + kSampleStride - 1u) / kSampleStride;
+        if (i <= nA) {
+            head(i);
+            accQ = sample_block(i, accP);
+            accP = accQ;
+            ++i;
+        }
+        if (rsel > 0) F = __fadd_rn(pair_kth<kSample>(samp, rsel), kFilterMargin);
+        // tau: necessary condition on cs * dot for d <= F
+        tau = !row_ok ? __builtin_inff()
+                      : (F == -__builtin_inff() ? __builtin_inff() : filter_bound(F, rs, rn, cn_min, cn_max));
+        // positions nA+1..S-1: filter epilogues of phase B tiles
+        for (; i + 1u < S; i += 2u) {
+            head(i);
+            accQ = mask_block(i, accP);
+            head(i + 1u);
+            accP = mask_block(i + 1u, accQ);
+        }
+        if (i < S) {
+            head(i);
+            accQ = mask_block(i, accP);
+            accP = accQ;
+        }
+        // tail: drain the held mask, then the last position (phase B's last tile)
+        drain(pend_mask, pend_tile);
+        ep_acc = &accP;
+        ep_cbase = (ntiles - 1u) * kTileCols;
+        ep_m = 0u;
+        static_for<0, kMaskUnits>(mask_unit);
+        drain(ep_m, ntiles - 1u);
+        s_tiles += S;
+        // the output stage below overlays the tile buffers and scratch
+        lds_barrier();
 
         // ---- final: fold the log, merge the pair, certify, order, write -----------
         // The log entries were written by this thread's global stores above.  A
@@ -642,15 +839,15 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             float *st_d = reinterpret_cast<float *>(st_ids + 32u * kTop);
 #pragma unroll
             for (int i = 0; i < kTop; ++i) {
-                if ((i >> 4) != (int)h || (uint32_t)i >= p.k) continue;
+                if ((i >> 4) != (int)h || (uint32_t)i >= pk) continue;
                 const bool live = (uint32_t)i < keff;
-                st_ids[j * p.k + i] = live ? sc[i] : kEmptyId;
-                st_d[j * p.k + i] = live ? sd[i] : kEmptyDist;
+                st_ids[j * pk + i] = live ? sc[i] : kEmptyId;
+                st_d[j * pk + i] = live ? sd[i] : kEmptyDist;
             }
             const uint32_t wrow0 = row_base + wave * 32u;
             const uint32_t wrows = wrow0 < n ? (n - wrow0 < 32u ? n - wrow0 : 32u) : 0u;
-            const uint32_t total = wrows * p.k;
-            const uint64_t base = p.output_offsets[leaf] + (uint64_t)wrow0 * p.k;
+            const uint32_t total = wrows * pk;
+            const uint64_t base = p.output_offsets[leaf] + (uint64_t)wrow0 * pk;
             for (uint32_t e = lane; e < total; e += 64u) {
                 p.out_ids[base + e] = st_ids[e];
                 p.out_dists[base + e] = st_d[e];
@@ -674,7 +871,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                                 if ((uint32_t)i < m)
                                     p.chain_pool[off + i] = make_uint4(__float_as_uint(sd[i]), sc[i],
                                                                        gid_lds[sc[i] < n ? sc[i] : 0u], 0u);
-                            const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * p.k;
+                            const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * pk;
                             p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), off, m | (keff << 8));
                             queued = true;
                             s_ch += 1;
