@@ -6,20 +6,24 @@
 // (leaf_build.rs:887-957 with dco_sq_int8.rs:2950-2965 distances).
 //
 // Work item = (leaf, block of 256 member rows); a workgroup is 8 waves (one
-// workgroup per CU, two waves per SIMD), wave w owns 32 rows.  The wave keeps
-// its 32 rows' codes in VGPRs for the whole K range as the MFMA "B" operand
-// (N = rows); 32-candidate column tiles are staged in LDS as the "A" operand
-// (M = candidates) and shared by the 8 waves.  With v_mfma_i32_32x32x32_i8
-// output lane l holds row l%32 and candidates 8*(v/4) + 4*(l/32) + v%4 of the
-// tile: each row is served by a lane pair (l, l+32), each lane seeing half of
-// the row's candidates.  The grid is persistent; the 8 XCDs each walk a
-// contiguous range of work items, so a leaf's row blocks share one L2.
+// workgroup per CU, two waves per SIMD), wave w owns 32 rows of the block.  The wave keeps its 32 rows' codes
+// in VGPRs for the whole K range as the MFMA "B" operand (N = rows);
+// 32-candidate column tiles are staged in LDS as the "A" operand (M =
+// candidates) and shared by the 8 waves.  With v_mfma_i32_32x32x32_i8 output
+// lane l holds row l%32 and candidates 8*(v/4) + 4*(l/32) + v%4 of the tile:
+// each row is served by a lane pair (l, l+32), each lane seeing half of the
+// row's candidates.  The grid is persistent; the 8 XCDs each walk a
+// contiguous range of work items, so a leaf's items share one L2.
+//
+// The column tiles of a block form one stream (phase A's sampled tiles, then
+// every tile for phase B), double buffered in LDS with one barrier per tile;
+// each tile's epilogue runs interleaved with the next tile's MFMAs.
 //
 // Selection (exact by construction, see the certificate below):
-//  * phase A: every kSampleStride-th column tile is evaluated and each lane
-//    keeps its 16 smallest exact distances (values only); the row threshold F
-//    is the pair's kSampleRank-th smallest sampled distance plus 3*eps, so at
-//    least that many candidates lie at or below F;
+//  * phase A: every 3rd (4th for wide leaves) column tile is evaluated and
+//    each lane keeps its 16 smallest exact distances (values only); the row
+//    threshold F is the pair's 24th (18th) smallest sampled distance plus
+//    3*eps, so at least that many candidates lie at or below F;
 //  * phase B: every column tile; a candidate passes when cs*dot meets the
 //    bound tau derived from F (a necessary condition for d <= F, evaluated in
 //    double with a rounding margin) and is appended (raw dot, column) to the
@@ -51,6 +55,7 @@ namespace tessa {
 
 namespace {
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
@@ -66,15 +71,30 @@ constexpr uint32_t kMaxLeafRows = 4096;
 constexpr float kFilterMargin = 3.0f * kTieEps;
 // Phase A samples every kSampleStride-th column tile; F is the pair's
 // kSampleRank-th smallest sampled distance plus the margin.  Every third
-// tile with rank 24 leaves ~73 survivors per 1024-row leaf row (C2).
+// tile with rank 24 leaves ~72 survivors per 1024-row leaf row (C2 data).
+// Leaves of at least kSampleWideTiles column tiles sample every
+// kSampleStrideWide-th tile with rank kSampleRankWide instead (a quarter of
+// a 1024-row leaf is still 256 candidates per row): fewer sampled tiles, a
+// few more rows sent to the exact kernel (~6 in 100,000 on C2 data).
 #ifndef TESSA_LEAF_SAMPLE_STRIDE
 #define TESSA_LEAF_SAMPLE_STRIDE 3
 #endif
 #ifndef TESSA_LEAF_SAMPLE_RANK
 #define TESSA_LEAF_SAMPLE_RANK 24
 #endif
+#ifndef TESSA_LEAF_SAMPLE_WIDE_TILES
+#define TESSA_LEAF_SAMPLE_WIDE_TILES 32
+#endif
+// Survivor-log drain steps run inside each phase B MFMA block (the rest of
+// a lane's bits are drained by a loop at the next position's start).
+#ifndef TESSA_LEAF_DRAIN_STEPS
+#define TESSA_LEAF_DRAIN_STEPS 3
+#endif
 constexpr uint32_t kSampleStride = TESSA_LEAF_SAMPLE_STRIDE;
 constexpr int kSampleRank = TESSA_LEAF_SAMPLE_RANK;
+constexpr uint32_t kSampleWideTiles = TESSA_LEAF_SAMPLE_WIDE_TILES;
+constexpr uint32_t kSampleStrideWide = 4;
+constexpr int kSampleRankWide = 18;
 
 template <int KS>
 struct Layout {
@@ -350,9 +370,10 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     // them with immediate offsets from one address.
     uint2 *slog = p.survivor_log + ((uint64_t)blockIdx.x * kThreads + tid) * cap;
 
-    // Work items are (leaf, 256-row block).  Blocks are dispatched round-robin
-    // over the 8 XCDs: XCD x walks its own contiguous item range, so the row
-    // blocks of a leaf share that XCD's L2.
+    // Work items are (leaf, 256-row block).  Workgroups are dispatched
+    // round-robin over the 8 XCDs: XCD x walks its own contiguous item range,
+    // so the row blocks of a leaf run at the same time on one XCD and share
+    // its L2 for the leaf's column tiles.
     const uint32_t xcd = blockIdx.x % 8u;
     const uint32_t lane_in_xcd = blockIdx.x / 8u;
     const uint32_t wgs_per_xcd = gridDim.x / 8u;
@@ -434,29 +455,35 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
         v4i pre[L::kChunksPerThread];
 
-        // Branch-free: every lane reads its member ids first (one LDS wait),
-        // then loads from a valid address (member 0, offset 0, when its chunk
-        // lies past the tile, the leaf or the padded row).  Such chunks are
+        // Tile loads are branch-free and split in two: prep_tile reads the
+        // member ids of a tile's chunks from LDS (it runs as a unit of the
+        // previous MFMA block, so its LDS wait is hidden there), issue_tile
+        // starts the global loads.  A chunk past the tile, the leaf or the
+        // padded row loads from a valid address (member 0, offset 0) and is
         // zeroed when stored to LDS, a position later, so nothing waits for
-        // the loads here.
+        // the loads when they are issued.
         uint32_t pre_ok = 0u;  // bit q: chunk q of `pre` is real data
-        auto load_tile = [&](uint32_t t) {
-            uint32_t mc[L::kChunksPerThread], offs[L::kChunksPerThread];
-            pre_ok = 0u;
+        uint32_t nx_mc[L::kChunksPerThread];
+        uint32_t nx_ok = 0u;
+        auto chunk_off = [&](int q) { return ((tid + q * kThreads) % (KS * 2)) * 16u; };
+        auto prep_tile = [&](uint32_t t) {
+            nx_ok = 0u;
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
                 const uint32_t chunk = tid + q * kThreads;
-                const uint32_t row = chunk / (KS * 2);
-                const uint32_t off = (chunk % (KS * 2)) * 16u;
-                const uint32_t c = t * kTileCols + row;
-                const bool ok = (chunk < (uint32_t)L::kChunks) & (c < n) & (off < pd);
-                pre_ok |= ok ? (1u << q) : 0u;
-                offs[q] = ok ? off : 0u;
-                mc[q] = mem_lds[ok ? c : 0u];
+                const uint32_t c = t * kTileCols + chunk / (KS * 2);
+                const bool ok = (chunk < (uint32_t)L::kChunks) & (c < n) & (chunk_off(q) < pd);
+                nx_ok |= ok ? (1u << q) : 0u;
+                nx_mc[q] = mem_lds[ok ? c : 0u];
             }
+        };
+        auto issue_tile = [&]() {
+            pre_ok = nx_ok;
 #pragma unroll
-            for (int q = 0; q < L::kChunksPerThread; ++q)
-                pre[q] = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)mc[q] * pd + offs[q]);
+            for (int q = 0; q < L::kChunksPerThread; ++q) {
+                const uint32_t off = ((nx_ok >> q) & 1u) ? chunk_off(q) : 0u;
+                pre[q] = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)nx_mc[q] * pd + off);
+            }
         };
         auto store_tile = [&](int8_t *dst) {
 #pragma unroll
@@ -472,7 +499,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         };
 
         // ---- the tile stream ----------------------------------------------------
-        // Stream position i < nA is phase A's sampled tile i*kSampleStride,
+        // Stream position i < nA is phase A's sampled tile i*sstride,
         // position nA + t is phase B's tile t.  Column tiles are double
         // buffered in LDS with one barrier per position: position i's MFMAs
         // read buffer i&1 while the tile of position i+1 goes to the other
@@ -488,15 +515,18 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         //    the next position drains the mask (set bits only) into the lane's
         //    survivor log.  Column validity (c < n, c != r) is checked there.
         constexpr int kSample = 16;
-        const int rsel = (int)(keff < (uint32_t)kSampleRank ? keff : (uint32_t)kSampleRank);
+        const bool wide = ntiles >= kSampleWideTiles;
+        const uint32_t sstride = wide ? kSampleStrideWide : kSampleStride;
+        const uint32_t srank = wide ? (uint32_t)kSampleRankWide : (uint32_t)kSampleRank;
+        const int rsel = (int)(keff < srank ? keff : srank);
         float samp[kSample];
 #pragma unroll
         for (int i = 0; i < kSample; ++i) samp[i] = __builtin_inff();
         float F = -__builtin_inff();
         float tau = __builtin_inff();
-        const uint32_t nA = (ntiles + kSampleStride - 1u) / kSampleStride;
+        const uint32_t nA = (ntiles + sstride - 1u) / sstride;
         const uint32_t S = nA + ntiles;
-        auto tile_of = [&](uint32_t i) { return i < nA ? i * kSampleStride : i - nA; };
+        auto tile_of = [&](uint32_t i) { return i < nA ? i * sstride : i - nA; };
         int8_t *const buf0 = tile;
         int8_t *const buf1 = tile + L::kTileBytes;
         int *const scr = reinterpret_cast<int *>(tile + 2 * L::kTileBytes) + wave * (16u * 64u);
@@ -553,11 +583,44 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
         // Phase B epilogue units (24): per group of 4 candidates one LDS read
         // of their scales, 4 filter tests, one LDS write of the raw dots.
+        // The mask block adds kDrainSteps drain steps (each takes the lane's
+        // lowest set bit: an LDS read of its dot, then a store to the survivor
+        // log through a buffer store whose offset is out of range, so dropped,
+        // for lanes with nothing to store) and the next tile's prep.  Bits left
+        // after them are drained by the loop at the next position's start.
         constexpr int kMaskUnits = 24;
+        constexpr int kDrainSteps = TESSA_LEAF_DRAIN_STEPS;
+        constexpr int kMaskBlockUnits = kMaskUnits + 2 * kDrainSteps + 1;
         uint32_t ep_m = 0u;
+        uint32_t prep_t = 0u;
+        int dr_dot[kDrainSteps > 0 ? kDrainSteps : 1];
+        uint32_t dr_c[kDrainSteps > 0 ? kDrainSteps : 1];
+        uint32_t dr_has = 0u;
+        uint32_t cnt = 0;
+        // survivor log as a buffer: this thread's entries start at slog_off bytes
+        const __amdgpu_buffer_rsrc_t log_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            p.survivor_log, (short)0, (int)(p.log_slots * 256u * cap * 8u), 0x00020000);
+        const uint32_t slog_off = (uint32_t)((blockIdx.x * kThreads + tid) * cap * 8u);
         auto mask_unit = [&](auto wc) {
             constexpr int W = decltype(wc)::value, g = W / 6, u = W % 6;
-            if constexpr (u == 0) {
+            if constexpr (W >= kMaskUnits + 2 * kDrainSteps) {
+                prep_tile(prep_t);
+            } else if constexpr (W >= kMaskUnits + kDrainSteps) {
+                constexpr int d = W - kMaskUnits - kDrainSteps;
+                const bool ok = ((dr_has >> d) & 1u) & (dr_c[d] < n) & (dr_c[d] != r);
+                const uint32_t off = (ok & (cnt < cap)) ? slog_off + cnt * 8u : 0x80000000u;
+                const int2 rec = make_int2(dr_dot[d], (int)dr_c[d]);
+                __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const v2i *>(&rec), log_rsrc, off, 0, 0);
+                cnt += ok ? 1u : 0u;
+            } else if constexpr (W >= kMaskUnits) {
+                constexpr int d = W - kMaskUnits;
+                const uint32_t m = ep_m;
+                const uint32_t vi = m != 0u ? (uint32_t)__builtin_ctz(m) : 0u;
+                dr_has |= (m != 0u) ? (1u << d) : 0u;
+                ep_m = m & (m - 1u);
+                dr_c[d] = ep_cbase + 4u * h + 8u * (vi >> 2) + (vi & 3u);
+                dr_dot[d] = scr[((vi >> 2) * 64u + lane) * 4u + (vi & 3u)];
+            } else if constexpr (u == 0) {
                 ep_cs[g] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * g + 4 * h);
             } else if constexpr (u < 5) {
                 constexpr int e = u - 1, vi = 4 * g + e;
@@ -568,9 +631,16 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 *reinterpret_cast<v4i *>(scr + (g * 64 + lane) * 4) = d;
             }
         };
-        auto no_unit = [&](auto) {};
+        auto prep_unit = [&](auto) { prep_tile(prep_t); };
+        auto sample_prep_unit = [&](auto wc) {
+            if constexpr (decltype(wc)::value == kSampleUnits) prep_tile(prep_t);
+            else sample_unit(wc);
+        };
+        auto sample_prep_unit_diag = [&](auto wc) {
+            if constexpr (decltype(wc)::value == kSampleUnits) prep_tile(prep_t);
+            else sample_unit_diag(wc);
+        };
         const uint32_t arow_off = j * L::kTileStride + 16u * h;
-        uint32_t cnt = 0;
         auto drain = [&](uint32_t m, uint32_t tp) {
             const uint32_t cbase = tp * kTileCols + 4u * h;
             while (m != 0u) {
@@ -593,14 +663,20 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             if (i + 1u < S) store_tile((i & 1u) ? buf0 : buf1);
             drain(pend_mask, pend_tile);
             pend_mask = 0u;
-            if (i + 2u < S) load_tile(tile_of(i + 2u));
+            if (i + 2u < S) issue_tile();  // tile of position i+2, prepared by the previous block
         };
         auto src_of = [&](uint32_t i) -> const int8_t * { return (i & 1u) ? buf1 : buf0; };
 
-        // prologue: position 0 in LDS buffer 0, position 1 in registers
-        load_tile(tile_of(0));
+        // prologue: position 0 in LDS buffer 0, position 1 in registers, the
+        // ids of position 2 prepared (S >= 2: nA >= 1 and ntiles >= 1)
+        prep_tile(tile_of(0));
+        issue_tile();
         store_tile(buf0);
-        load_tile(tile_of(1));  // S >= 2: nA >= 1 and ntiles >= 1
+        prep_tile(tile_of(1));
+        issue_tile();
+        prep_tile(tile_of(S > 2u ? 2u : S - 1u));
+        // each block prepares the ids of the tile three positions ahead
+        auto prep_for = [&](uint32_t i) { prep_t = tile_of(i + 3u < S ? i + 3u : S - 1u); };
         // accP holds the accumulators of the latest position; each block
         // computes position i into accQ/accP alternately while the epilogue
         // of position i-1 runs on the other.
@@ -609,23 +685,28 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             ep_acc = &prev;
             const uint32_t tp = tile_of(i - 1u);
             ep_cbase = tp * kTileCols;
-            if (tp == diag_tile) return mfma_block<KS, kSampleUnits>(src_of(i) + arow_off, bfrag, sample_unit_diag);
-            return mfma_block<KS, kSampleUnits>(src_of(i) + arow_off, bfrag, sample_unit);
+            prep_for(i);
+            if (tp == diag_tile)
+                return mfma_block<KS, kSampleUnits + 1>(src_of(i) + arow_off, bfrag, sample_prep_unit_diag);
+            return mfma_block<KS, kSampleUnits + 1>(src_of(i) + arow_off, bfrag, sample_prep_unit);
         };
         auto mask_block = [&](uint32_t i, const v16i &prev) {
             ep_acc = &prev;
             ep_cbase = (i - 1u - nA) * kTileCols;
             ep_m = 0u;
-            const v16i acc = mfma_block<KS, kMaskUnits>(src_of(i) + arow_off, bfrag, mask_unit);
-            // the mask is needed here, not only by the next position's drain: its
-            // tests stay interleaved with the MFMAs instead of sinking past them
+            dr_has = 0u;
+            prep_for(i);
+            const v16i acc = mfma_block<KS, kMaskBlockUnits>(src_of(i) + arow_off, bfrag, mask_unit);
+            // the residual mask is needed here, not only by the next position's
+            // drain: its tests stay interleaved with the MFMAs instead of sinking
             asm volatile("" : "+v"(ep_m));
             pend_mask = ep_m;
             pend_tile = i - 1u - nA;
             return acc;
         };
         head(0);
-        accP = mfma_block<KS, 0>(src_of(0) + arow_off, bfrag, no_unit);
+        prep_for(0);
+        accP = mfma_block<KS, 1>(src_of(0) + arow_off, bfrag, prep_unit);
         uint32_t i = 1;
         // positions 1..nA: epilogues of the sampled tiles
         for (; i + 1u <= nA; i += 2u) {
