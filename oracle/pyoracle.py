@@ -83,6 +83,8 @@ def lib():
         _lib.orc_flush_compact_topk_into_edges.restype = C.c_longlong
         _lib.orc_flush_compact_topk_into_edges.argtypes = [P, C.c_size_t, C.c_size_t, P, P, P, C.c_size_t,
                                                            C.c_size_t, C.c_uint, P, C.c_size_t, P]
+        _lib.orc_hashprune_reduce.restype = C.c_int
+        _lib.orc_hashprune_reduce.argtypes = [C.c_size_t, C.c_size_t, P, C.c_size_t, P, P, P, P, P]
     return _lib
 
 
@@ -344,3 +346,20 @@ def flush_compact_topk_into_edges(point_ids, k: int, topk_ids, topk_dists, sketc
     if n < 0:
         raise EdgeError(int(n), bad.value)
     return out[:n]
+
+
+def hashprune_reduce(num_points: int, l_max: int, records: np.ndarray):
+    """HashPrune reservoirs after inserting `records` (EDGE_DTYPE) in order:
+    (targets [num_points, l_max] u32, hashes u16, dists f32, counts [num_points] u32),
+    each row's slots in ascending hash order, unused slots 0xFFFFFFFF / 0 / 0."""
+    rec = np.ascontiguousarray(records, EDGE_DTYPE)
+    t = np.zeros((num_points, l_max), np.uint32)
+    hs = np.zeros((num_points, l_max), np.uint16)
+    d = np.zeros((num_points, l_max), np.float32)
+    cnt = np.zeros(num_points, np.uint32)
+    bad = C.c_uint32(0)
+    rc = lib().orc_hashprune_reduce(num_points, l_max, _p(rec), len(rec), _p(t), _p(hs), _p(d), _p(cnt),
+                                    C.byref(bad))
+    if rc != 0:
+        raise ValueError(f"orc_hashprune_reduce: {rc} (record {bad.value})")
+    return t, hs, d, cnt

@@ -30,6 +30,12 @@
  *   orc_flush_compact_    with build_test_sketches :2900-2908), whose edges follow
  *   topk_into_edges       in closed form; an independent numpy restatement on random
  *                         batches; the empty-slot, non-finite and outside-leaf cases.
+ *   orc_hashprune_reduce  the reference's reservoir KATs (hash_prune.rs:4803-4875:
+ *                         exact-distance replacement inside one BF16 bucket, same-hash
+ *                         collision, 1.5e-5 band, permutation-independent epsilon
+ *                         cycle); brute force: the l_max best (dist, target, hash)
+ *                         among each hash's best candidate, listed by ascending hash;
+ *                         invariance under every shuffle of the record stream.
  */
 #ifndef TESSA_ORACLE_H
 #define TESSA_ORACLE_H
@@ -248,6 +254,16 @@ long long orc_flush_compact_topk_into_edges(const uint32_t *point_ids, size_t ro
                                             const float *sketches, size_t sketch_rows, size_t width,
                                             unsigned m_bits, orc_edge_record *out, size_t capacity,
                                             uint32_t *bad_point);
+
+/* HashPrune reservoirs of num_points points (l_max slots each) after inserting
+ * `records` in order (spill_hashprune.rs:2686-2719 with hash_prune.rs:1333-1453
+ * insert_inner, backfill and evidence off).  Per point: out_counts[p] slots, then
+ * out_targets/out_hashes/out_dists[p*l_max + s] in slot order (ascending hash),
+ * unused slots 0xFFFFFFFF / 0 / 0.  out_hashes and out_dists may be NULL.
+ * Returns 0, or -3 with *bad_record set when a record's src >= num_points. */
+int orc_hashprune_reduce(size_t num_points, size_t l_max, const orc_edge_record *records, size_t count,
+                         uint32_t *out_targets, uint16_t *out_hashes, float *out_dists, uint32_t *out_counts,
+                         uint32_t *bad_record);
 
 #ifdef __cplusplus
 }
