@@ -408,6 +408,33 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
                                      uint64_t *leaf_record_offsets, uint64_t *record_count,
                                      void *stream);
 
+/* ---- HashPrune reservoirs: the consumer of the record stream ---------------
+ * One HashPruneReservoir per point (hash_prune.rs:266-280, l_max slots, insert
+ * :1243-1246 / insert_inner :1333-1453, total order :2094-2106), fed as
+ * ExternalHashPruneReducer::reduce_spill_artifacts_ordered feeds it
+ * (spill_hashprune.rs:875-892; per edge reservoir.insert :2686-2719; emitted
+ * by copy_neighbors_and_clear :3203-3221), backfill and evidence policies off
+ * (their defaults, params.rs:3346-3350).  The reservoirs live in device
+ * memory; records are merged batch by batch, in any order (the reservoir's
+ * final state depends only on the candidates inserted).
+ *   create     reservoirs for points [0, num_points), l_max in [1, 256];
+ *   insert     device records; synchronises `stream`; a record with
+ *              src >= num_points fails the call (the reference's "edge p=...
+ *              outside shard range") after the batch's valid records are in;
+ *   neighbors  per point up to l_max slots in slot order (ascending hash):
+ *              targets / hashes / dists [num_points * l_max] (unused slots
+ *              0xFFFFFFFF / 0 / 0.0) and counts [num_points], device pointers,
+ *              each may be NULL; enqueued on `stream`;
+ *   clear      empties every reservoir (enqueued on `stream`). */
+typedef struct tessa_hashprune tessa_hashprune;
+tessa_status tessa_hashprune_create(uint32_t num_points, uint32_t l_max, tessa_hashprune **out);
+tessa_status tessa_hashprune_destroy(tessa_hashprune *hp);
+tessa_status tessa_hashprune_insert(tessa_hashprune *hp, const tessa_edge_record *records, uint64_t count,
+                                    void *stream);
+tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targets, uint16_t *hashes,
+                                       float *dists, uint32_t *counts, void *stream);
+tessa_status tessa_hashprune_clear(tessa_hashprune *hp, void *stream);
+
 /* ---- asynchronous subtree submissions ----------------------------------
  * Replaces submit_owned_quantized_subtree_l2_compact_topk
  * (compute_backend.rs:3807-3815) with its Deferred result and pinned host-slot

@@ -281,6 +281,11 @@ SIGNATURES = {
         TessaStatus,
         [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, C.POINTER(_U64), _P],
     ),
+    "tessa_hashprune_create": (TessaStatus, [_U32, _U32, C.POINTER(_P)]),
+    "tessa_hashprune_destroy": (TessaStatus, [_P]),
+    "tessa_hashprune_insert": (TessaStatus, [_P, _P, _U64, _P]),
+    "tessa_hashprune_neighbors": (TessaStatus, [_P, _P, _P, _P, _P, _P]),
+    "tessa_hashprune_clear": (TessaStatus, [_P, _P]),
 }
 
 _lib = None

@@ -1,0 +1,353 @@
+// hashprune.hip -- HashPrune reservoirs on the GPU: the reducer that consumes
+// the edge-record stream (SpillRecord16) and keeps, per source point, at most
+// l_max neighbours.
+//
+// Reference semantics (shear-core/src/algorithm/pipnn/): HashPruneReservoir
+// insert (hash_prune.rs:1333-1453) under the total order (dist by total_cmp,
+// target, hash; :2094-2106), fed edge by edge by the spill reducer
+// (spill_hashprune.rs:2686-2719) and emitted as the slot targets in slot
+// order, ascending hash (:3203-3221 emit_shard).  With the backfill and
+// evidence policies off (params.rs:3346-3350) that reservoir ends in a state
+// that depends only on the set of candidates inserted: each hash keeps its
+// best candidate (a hit keeps the better one), and of those the l_max best
+// remain (an evicted or rejected candidate is worse than l_max others of
+// distinct hashes, and those are only ever replaced by better ones).  So a
+// batch of records can be merged in any order, which is what makes it a GPU
+// reduction:
+//   1. count records per source (atomics), exclusive scan, scatter the records
+//      grouped by source (the per-source counters return to zero);
+//   2. one wave per source with new records merges its current slots with them
+//      in LDS, up to kHpMergeCap at a time: a bitonic sort by the total order
+//      (dist key, target, then hash) gives each candidate its rank; a second
+//      sort by (hash, rank) puts each hash's best first; the l_max best of
+//      those (by rank) become the new slots, in ascending hash order.
+#include "hashprune_kernels.h"
+
+namespace tessa {
+
+namespace {
+
+constexpr int kHpWaves = 4;                 // waves per workgroup of the merge kernel
+constexpr int kHpThreads = kHpWaves * 64;
+constexpr int kScanThreads = 1024;
+constexpr int kScanPerThread = 4;
+constexpr uint32_t kScanBlock = kScanThreads * kScanPerThread;
+
+__device__ __forceinline__ uint32_t total_key(float d) {
+    const uint32_t b = __float_as_uint(d);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_dist(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, uint32_t lane, uint32_t &total) {
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off);
+        if (lane >= (uint32_t)off) x += y;
+    }
+    total = __shfl(x, 63);
+    return x - v;
+}
+
+__global__ void hp_fill_u32(uint32_t *a, uint64_t n, uint32_t v) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        a[i] = v;
+}
+
+__global__ void hp_status_init(uint64_t *status) { status[0] = ~0ull; }
+
+__global__ void hp_count_kernel(const uint4 *rec, uint64_t count, uint32_t num_points, uint32_t *bucket,
+                                uint64_t *status) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t src = rec[i].x;
+        if (src >= num_points) atomicMin((unsigned long long *)status, (unsigned long long)i);
+        else atomicAdd(&bucket[src], 1u);
+    }
+}
+
+// Block sums of `bucket` over kScanBlock elements each.
+__global__ __launch_bounds__(kScanThreads) void hp_scan_reduce(const uint32_t *bucket, uint32_t n, uint32_t *sums) {
+    __shared__ uint32_t ws[kScanThreads / 64];
+    const uint32_t base = blockIdx.x * kScanBlock + threadIdx.x * kScanPerThread;
+    uint32_t v = 0;
+#pragma unroll
+    for (int e = 0; e < kScanPerThread; ++e) v += base + e < n ? bucket[base + e] : 0u;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if ((threadIdx.x & 63u) == 0) ws[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < kScanThreads / 64; ++w) t += ws[w];
+        sums[blockIdx.x] = t;
+    }
+}
+
+// Exclusive scan of the block sums in place (one workgroup); offsets[n] = total.
+__global__ __launch_bounds__(kScanThreads) void hp_scan_partials(uint32_t *sums, uint32_t nb, uint32_t *offsets,
+                                                                 uint32_t n) {
+    __shared__ uint32_t ws[kScanThreads / 64];
+    __shared__ uint32_t carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    for (uint32_t b0 = 0; b0 < nb; b0 += kScanThreads) {
+        const uint32_t i = b0 + threadIdx.x;
+        const uint32_t v = i < nb ? sums[i] : 0u;
+        uint32_t wt;
+        const uint32_t ex = wave_excl_scan(v, lane, wt);
+        if (lane == 0) ws[wave] = wt;
+        __syncthreads();
+        uint32_t before = 0, all = 0;
+        for (uint32_t w = 0; w < kScanThreads / 64; ++w) {
+            before += w < wave ? ws[w] : 0u;
+            all += ws[w];
+        }
+        if (i < nb) sums[i] = carry + before + ex;
+        __syncthreads();
+        if (threadIdx.x == 0) carry += all;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) offsets[n] = carry;
+}
+
+__global__ __launch_bounds__(kScanThreads) void hp_scan_apply(const uint32_t *bucket, uint32_t n, const uint32_t *sums,
+                                                              uint32_t *offsets) {
+    __shared__ uint32_t ws[kScanThreads / 64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t base = blockIdx.x * kScanBlock + threadIdx.x * kScanPerThread;
+    uint32_t v[kScanPerThread], t = 0;
+#pragma unroll
+    for (int e = 0; e < kScanPerThread; ++e) {
+        v[e] = base + e < n ? bucket[base + e] : 0u;
+        t += v[e];
+    }
+    uint32_t wt;
+    const uint32_t ex = wave_excl_scan(t, lane, wt);
+    if (lane == 0) ws[wave] = wt;
+    __syncthreads();
+    uint32_t before = sums[blockIdx.x];
+    for (uint32_t w = 0; w < wave; ++w) before += ws[w];
+    uint32_t run = before + ex;
+#pragma unroll
+    for (int e = 0; e < kScanPerThread; ++e) {
+        if (base + e < n) offsets[base + e] = run;
+        run += v[e];
+    }
+}
+
+// Records grouped by source; the per-source counters count back down to zero.
+__global__ void hp_scatter_kernel(const uint4 *rec, uint64_t count, uint32_t num_points, uint32_t *bucket,
+                                  const uint32_t *offsets, uint4 *grouped) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint4 r = rec[i];
+        if (r.x >= num_points) continue;
+        const uint32_t pos = offsets[r.x] + atomicSub(&bucket[r.x], 1u) - 1u;
+        grouped[pos] = r;
+    }
+}
+
+// Ascending bitonic sort of (key, payload) pairs, lexicographic, over
+// [0, P) (P a power of two >= 64), by one wave on its LDS region.  LDS
+// operations of one wave complete in order, so stages need no barrier.
+template <typename K>
+__device__ void wave_bitonic(K *key, uint32_t *val, uint32_t P, uint32_t lane) {
+    for (uint32_t k = 2; k <= P; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t c = lane; c < P / 2; c += 64) {
+                const uint32_t i = ((c & ~(j - 1u)) << 1) | (c & (j - 1u));
+                const uint32_t l = i + j;
+                const bool up = (i & k) == 0;
+                const K a = key[i], b = key[l];
+                const uint32_t va = val[i], vb = val[l];
+                const bool b_less = b < a || (b == a && vb < va);
+                const bool a_less = a < b || (a == b && va < vb);
+                if (up ? b_less : a_less) {
+                    key[i] = b;
+                    key[l] = a;
+                    val[i] = vb;
+                    val[l] = va;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+struct HpWaveLds {
+    uint64_t key[kHpMergeCap];      // candidates by total-order key
+    uint32_t val[kHpMergeCap];      // hash while sorting by key; then (hash << 16 | rank)
+    uint32_t flag[kHpMergeCap];     // kept flag by rank, then its exclusive prefix
+    uint64_t out_key[kHpMaxLMax];   // the merged reservoir
+    uint32_t out_hash[kHpMaxLMax];
+    uint32_t rank_of[kHpMergeCap];  // val sorted by (hash, rank): payload slot for the second sort
+};
+
+__global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *grouped, const uint32_t *offsets,
+                                                              uint32_t num_points, uint32_t l_max,
+                                                              uint64_t *slot_keys, uint16_t *slot_hash,
+                                                              uint32_t *slot_count) {
+    __shared__ HpWaveLds lds[kHpWaves];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    HpWaveLds &w = lds[wave];
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t src = blockIdx.x * kHpWaves + wave; src < num_points; src += waves) {
+        const uint32_t off = offsets[src];
+        const uint32_t n_new = offsets[src + 1] - off;
+        if (n_new == 0) continue;
+        uint32_t n_old = slot_count[src];
+        const uint64_t sbase = (uint64_t)src * l_max;
+        for (uint32_t e = lane; e < n_old; e += 64) {
+            w.key[e] = slot_keys[sbase + e];
+            w.val[e] = slot_hash[sbase + e];
+        }
+        uint32_t used = 0;
+        while (used < n_new) {
+            const uint32_t take = (n_new - used < kHpMergeCap - n_old) ? n_new - used : kHpMergeCap - n_old;
+            for (uint32_t e = lane; e < take; e += 64) {
+                const uint4 r = grouped[off + used + e];
+                w.key[n_old + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
+                w.val[n_old + e] = r.z & 0xffffu;
+            }
+            const uint32_t N = n_old + take;
+            uint32_t P = 64;
+            while (P < N) P <<= 1;
+            for (uint32_t e = N + lane; e < P; e += 64) {
+                w.key[e] = ~0ull;
+                w.val[e] = 0xffffu;
+            }
+            __builtin_amdgcn_wave_barrier();
+            // ranks: position in total order
+            wave_bitonic<uint64_t>(w.key, w.val, P, lane);
+            // each hash's best first: sort (hash << 16 | rank)
+            for (uint32_t e = lane; e < P; e += 64) {
+                w.rank_of[e] = e < N ? ((w.val[e] << 16) | e) : 0xffffffffu;
+                w.flag[e] = 0u;
+            }
+            __builtin_amdgcn_wave_barrier();
+            wave_bitonic<uint32_t>(w.rank_of, w.val, P, lane);
+            for (uint32_t e = lane; e < N; e += 64) {
+                const uint32_t v = w.rank_of[e];
+                const bool kept = e == 0 || (w.rank_of[e - 1] >> 16) != (v >> 16);
+                if (kept) w.flag[v & 0xffffu] = 1u;
+            }
+            __builtin_amdgcn_wave_barrier();
+            // exclusive prefix of the kept flags in rank order
+            {
+                const uint32_t E = P / 64;
+                const uint32_t b = lane * E;
+                uint32_t t = 0;
+                for (uint32_t q = 0; q < E; ++q) t += w.flag[b + q];
+                uint32_t tot;
+                uint32_t run = wave_excl_scan(t, lane, tot);
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t f = w.flag[b + q];
+                    w.flag[b + q] = f ? run : 0xffffffffu;  // prefix for kept ranks, sentinel otherwise
+                    run += f;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            // selected = kept with fewer than l_max kept before it; compact in hash order
+            {
+                const uint32_t E = P / 64;
+                const uint32_t b = lane * E;
+                uint32_t t = 0;
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t v = w.rank_of[b + q];
+                    t += (b + q < N && w.flag[v & 0xffffu] < l_max) ? 1u : 0u;
+                }
+                uint32_t tot;
+                uint32_t run = wave_excl_scan(t, lane, tot);
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t v = w.rank_of[b + q];
+                    if (b + q < N && w.flag[v & 0xffffu] < l_max) {
+                        w.out_key[run] = w.key[v & 0xffffu];
+                        w.out_hash[run] = v >> 16;
+                        ++run;
+                    }
+                }
+                n_old = tot;
+            }
+            __builtin_amdgcn_wave_barrier();
+            used += take;
+            if (used < n_new) {
+                for (uint32_t e = lane; e < n_old; e += 64) {
+                    w.key[e] = w.out_key[e];
+                    w.val[e] = w.out_hash[e];
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        for (uint32_t e = lane; e < n_old; e += 64) {
+            slot_keys[sbase + e] = w.out_key[e];
+            slot_hash[sbase + e] = (uint16_t)w.out_hash[e];
+        }
+        if (lane == 0) slot_count[src] = n_old;
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+__global__ void hp_export_kernel(const uint64_t *slot_keys, const uint16_t *slot_hash, const uint32_t *slot_count,
+                                 uint32_t num_points, uint32_t l_max, uint32_t *targets, uint16_t *hashes,
+                                 float *dists, uint32_t *counts) {
+    const uint64_t total = (uint64_t)num_points * l_max;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t p = (uint32_t)(i / l_max), s = (uint32_t)(i % l_max);
+        const uint32_t c = slot_count[p];
+        const bool live = s < c;
+        const uint64_t k = live ? slot_keys[i] : 0ull;
+        if (targets) targets[i] = live ? (uint32_t)k : 0xffffffffu;
+        if (hashes) hashes[i] = live ? slot_hash[i] : (uint16_t)0;
+        if (dists) dists[i] = live ? key_dist((uint32_t)(k >> 32)) : 0.0f;
+        if (counts && s == 0) counts[p] = c;
+    }
+}
+
+uint32_t grid_for(uint64_t n, uint32_t threads, uint32_t cap) {
+    const uint64_t g = (n + threads - 1) / threads;
+    return (uint32_t)(g < 1 ? 1 : (g > cap ? cap : g));
+}
+
+}  // namespace
+
+uint64_t hashprune_scan_blocks(uint32_t num_points) { return (num_points + kScanBlock - 1) / kScanBlock + 1; }
+
+int launch_hashprune_clear(HashPruneState &s, hipStream_t stream) {
+    hipLaunchKernelGGL(hp_fill_u32, dim3(grid_for(s.num_points, 256, 4096)), dim3(256), 0, stream, s.slot_count,
+                       (uint64_t)s.num_points, 0u);
+    hipLaunchKernelGGL(hp_fill_u32, dim3(grid_for(s.num_points, 256, 4096)), dim3(256), 0, stream, s.bucket,
+                       (uint64_t)s.num_points, 0u);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t count, hipStream_t stream) {
+    const uint32_t n = s.num_points;
+    hipLaunchKernelGGL(hp_status_init, dim3(1), dim3(1), 0, stream, s.status);
+    if (count == 0 || n == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
+    hipLaunchKernelGGL(hp_count_kernel, dim3(grid_for(count, 256, 16384)), dim3(256), 0, stream, records, count, n,
+                       s.bucket, s.status);
+    const uint32_t nb = (n + kScanBlock - 1) / kScanBlock;
+    hipLaunchKernelGGL(hp_scan_reduce, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums);
+    hipLaunchKernelGGL(hp_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, s.block_sums, nb, s.offsets, n);
+    hipLaunchKernelGGL(hp_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums, s.offsets);
+    hipLaunchKernelGGL(hp_scatter_kernel, dim3(grid_for(count, 256, 16384)), dim3(256), 0, stream, records, count, n,
+                       s.bucket, s.offsets, s.grouped);
+    hipLaunchKernelGGL(hp_merge_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream, s.grouped,
+                       s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_hashprune_export(const HashPruneState &s, uint32_t *targets, uint16_t *hashes, float *dists,
+                            uint32_t *counts, hipStream_t stream) {
+    const uint64_t total = (uint64_t)s.num_points * s.l_max;
+    if (total == 0) return 0;
+    hipLaunchKernelGGL(hp_export_kernel, dim3(grid_for(total, 256, 16384)), dim3(256), 0, stream, s.slot_keys,
+                       s.slot_hash, s.slot_count, s.num_points, s.l_max, targets, hashes, dists, counts);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace tessa

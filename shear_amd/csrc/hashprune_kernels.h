@@ -1,0 +1,40 @@
+// hashprune_kernels.h -- launch interface of the HashPrune reservoir kernels
+// (hashprune.hip), shared with the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tessa {
+
+// Largest reservoir (l_max) the reduce kernel takes: one wave merges at most
+// kHpMergeCap candidates per round, l_max of them the reservoir's own slots.
+constexpr uint32_t kHpMergeCap = 512;
+constexpr uint32_t kHpMaxLMax = 256;
+
+struct HashPruneState {
+    uint32_t num_points = 0;
+    uint32_t l_max = 0;
+    uint64_t *slot_keys = nullptr;  // num_points x l_max: total-order dist key << 32 | target
+    uint16_t *slot_hash = nullptr;  // num_points x l_max
+    uint32_t *slot_count = nullptr; // num_points
+    uint32_t *bucket = nullptr;     // num_points: records per source in the batch (zero between batches)
+    uint32_t *offsets = nullptr;    // num_points + 1: first grouped record of each source
+    uint32_t *block_sums = nullptr; // scan partials
+    uint64_t block_sums_capacity = 0;
+    uint4 *grouped = nullptr;       // the batch's records grouped by source
+    uint64_t grouped_capacity = 0;
+    uint64_t *status = nullptr;     // [0] first record with src >= num_points (UINT64_MAX: none)
+};
+
+// Groups `count` records by source and merges each source's new candidates
+// into its reservoir.  Returns 0, or -1 when a launch failed.
+int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t count, hipStream_t stream);
+// Zeroes the per-source counters (all reservoirs empty).
+int launch_hashprune_clear(HashPruneState &s, hipStream_t stream);
+// Slot targets / hashes / distances (ascending hash) and counts per point.
+int launch_hashprune_export(const HashPruneState &s, uint32_t *targets, uint16_t *hashes, float *dists,
+                            uint32_t *counts, hipStream_t stream);
+uint64_t hashprune_scan_blocks(uint32_t num_points);
+
+}  // namespace tessa

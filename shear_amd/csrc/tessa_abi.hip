@@ -20,6 +20,7 @@
 #include "../../include/tessa_hip.h"
 #include "assign_kernels.h"
 #include "edge_kernels.h"
+#include "hashprune_kernels.h"
 #include "leaf_kernels.h"
 #include "partition.h"
 #include "tessa_device.h"
@@ -1424,6 +1425,131 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge record capacity %llu below the %llu records needed",
                            (unsigned long long)p.out_capacity, (unsigned long long)w[kEdgeRecordCount]);
     *record_count = w[kEdgeRecordCount];
+    return ok_status();
+}
+
+}  // extern "C"
+
+// ---- HashPrune reservoirs --------------------------------------------------------
+
+struct tessa_hashprune {
+    int device = 0;
+    tessa::HashPruneState st;
+};
+
+namespace {
+
+void free_hashprune(tessa_hashprune *hp) {
+    auto &s = hp->st;
+    for (void *ptr : {(void *)s.slot_keys, (void *)s.slot_hash, (void *)s.slot_count, (void *)s.bucket,
+                      (void *)s.offsets, (void *)s.block_sums, (void *)s.grouped, (void *)s.status})
+        if (ptr) (void)hipFree(ptr);
+    delete hp;
+}
+
+tessa_status hp_alloc(void **ptr, uint64_t bytes, const char *what) {
+    if (hipMalloc(ptr, bytes ? bytes : 16) != hipSuccess) {
+        *ptr = nullptr;
+        return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
+                           "%s allocation of %llu bytes failed overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                           what, (unsigned long long)bytes, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+    }
+    return ok_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+tessa_status tessa_hashprune_create(uint32_t num_points, uint32_t l_max, tessa_hashprune **out) {
+    if (!out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune: null output");
+    *out = nullptr;
+    if (l_max == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "l_max must be > 0");
+    if (l_max > tessa::kHpMaxLMax)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: l_max=%u above %u", l_max, tessa::kHpMaxLMax);
+    auto *hp = new (std::nothrow) tessa_hashprune();
+    if (!hp) return make_status(TESSA_ERR_OUT_OF_MEMORY, 0, "hashprune: host allocation failed");
+    TESSA_HIP_TRY(hipGetDevice(&hp->device));
+    auto &s = hp->st;
+    s.num_points = num_points;
+    s.l_max = l_max;
+    const uint64_t slots = (uint64_t)num_points * l_max;
+    tessa_status st = hp_alloc((void **)&s.slot_keys, slots * 8, "hashprune slot keys");
+    if (!st.code) st = hp_alloc((void **)&s.slot_hash, slots * 2, "hashprune slot hashes");
+    if (!st.code) st = hp_alloc((void **)&s.slot_count, (uint64_t)num_points * 4, "hashprune slot counts");
+    if (!st.code) st = hp_alloc((void **)&s.bucket, (uint64_t)num_points * 4, "hashprune source counts");
+    if (!st.code) st = hp_alloc((void **)&s.offsets, ((uint64_t)num_points + 1) * 4, "hashprune source offsets");
+    if (!st.code) {
+        s.block_sums_capacity = tessa::hashprune_scan_blocks(num_points);
+        st = hp_alloc((void **)&s.block_sums, s.block_sums_capacity * 4, "hashprune scan partials");
+    }
+    if (!st.code) st = hp_alloc((void **)&s.status, 8 * 4, "hashprune status");
+    if (!st.code && tessa::launch_hashprune_clear(s, nullptr) != 0)
+        st = make_status(TESSA_ERR_HIP, 0, "hashprune clear launch failed");
+    if (!st.code && hipStreamSynchronize(nullptr) != hipSuccess)
+        st = make_status(TESSA_ERR_HIP, 0, "hashprune clear failed");
+    if (st.code) {
+        free_hashprune(hp);
+        return st;
+    }
+    *out = hp;
+    return ok_status();
+}
+
+tessa_status tessa_hashprune_destroy(tessa_hashprune *hp) {
+    if (!hp) return ok_status();
+    TESSA_HIP_TRY(hipSetDevice(hp->device));
+    TESSA_HIP_TRY(hipDeviceSynchronize());
+    free_hashprune(hp);
+    return ok_status();
+}
+
+tessa_status tessa_hashprune_clear(tessa_hashprune *hp, void *stream) {
+    if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
+    if (tessa::launch_hashprune_clear(hp->st, reinterpret_cast<hipStream_t>(stream)) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "hashprune clear launch failed");
+    return ok_status();
+}
+
+tessa_status tessa_hashprune_insert(tessa_hashprune *hp, const tessa_edge_record *records, uint64_t count,
+                                    void *stream) {
+    if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
+    if (count && !records) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune: null records");
+    if (count >= 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: %llu records in one batch (limit 2^32-2)",
+                           (unsigned long long)count);
+    auto &s = hp->st;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    if (count > s.grouped_capacity) {
+        TESSA_HIP_TRY(hipStreamSynchronize(hs));
+        if (s.grouped) TESSA_HIP_TRY(hipFree(s.grouped));
+        s.grouped = nullptr;
+        s.grouped_capacity = 0;
+        tessa_status st = hp_alloc((void **)&s.grouped, count * 16, "hashprune grouped records");
+        if (st.code) return st;
+        s.grouped_capacity = count;
+    }
+    if (tessa::launch_hashprune_insert(s, reinterpret_cast<const uint4 *>(records), count, hs) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "hashprune insert launch failed");
+    uint64_t bad = 0;
+    TESSA_HIP_TRY(hipMemcpyAsync(&bad, s.status, sizeof(bad), hipMemcpyDeviceToHost, hs));
+    TESSA_HIP_TRY(hipStreamSynchronize(hs));
+    if (bad != ~0ull) {
+        tessa_edge_record r{};
+        TESSA_HIP_TRY(hipMemcpy(&r, records + bad, sizeof(r), hipMemcpyDeviceToHost));
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "Spill reducer encountered edge p=%u outside shard range [0, %u) (record %llu; the "
+                           "batch's valid records were inserted)",
+                           r.src, s.num_points, (unsigned long long)bad);
+    }
+    return ok_status();
+}
+
+tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targets, uint16_t *hashes,
+                                       float *dists, uint32_t *counts, void *stream) {
+    if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
+    if (tessa::launch_hashprune_export(hp->st, targets, hashes, dists, counts, reinterpret_cast<hipStream_t>(stream)) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "hashprune export launch failed");
     return ok_status();
 }
 

@@ -1,0 +1,106 @@
+"""HashPrune reservoirs on the GPU: the consumer of the edge-record stream.
+
+Host mirror of the reference's reducer side (paths relative to
+shear-core/src/algorithm/pipnn/):
+
+* ``HashPruneReducer``                 HashPruneReservoir per point (hash_prune.rs:266-280,
+  insert :1243-1246 / :1333-1453) driven as ExternalHashPruneReducer drives it
+  (spill_hashprune.rs:853-936, per-edge insert :2686-2719, emit :3203-3221)
+* ``reduce_spill_records_ordered``     ExternalHashPruneReducer::reduce_spill_artifacts_ordered
+  (spill_hashprune.rs:875-892): one neighbour list per point, slot order
+
+Backfill and evidence policies are off (their defaults, params.rs:3346-3350).
+The reservoirs live in device memory (libtessa_hip.so, ``tessa_hashprune_*``);
+records are merged batch by batch in any order.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .edges import EDGE_RECORD_DTYPE
+from .tessa import _ptr, _stream_ptr
+
+DEFAULT_L_MAX = 64  # params.rs:3346
+
+
+class HashPruneReducer:
+    """Device-resident HashPrune reservoirs for points [0, num_points)."""
+
+    def __init__(self, num_points: int, l_max: int = DEFAULT_L_MAX, device="cuda"):
+        self.num_points = int(num_points)
+        self.l_max = int(l_max)
+        self.device = torch.device(device)
+        self._lib = N.load()
+        h = C.c_void_p()
+        with torch.cuda.device(self.device):
+            N.check(self._lib.tessa_hashprune_create(self.num_points, self.l_max, C.byref(h)), "hashprune create")
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            N.check(self._lib.tessa_hashprune_destroy(self._h), "hashprune destroy")
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def insert(self, records, count: int | None = None, stream: torch.cuda.Stream | None = None) -> None:
+        """Merge SpillRecord16 records: a device int32 [n, 4] tensor (as written
+        by ``edges.emit_edge_records``; the first ``count`` rows) or a host
+        EDGE_RECORD_DTYPE array (uploaded first).  Synchronises the stream."""
+        if isinstance(records, np.ndarray):
+            raw = np.ascontiguousarray(records, EDGE_RECORD_DTYPE).view(np.uint8).view(np.int32).reshape(-1, 4)
+            records = torch.from_numpy(raw.copy()).to(self.device)
+        if records.dtype != torch.int32 or records.dim() != 2 or records.shape[1] != 4:
+            raise ValueError("records must be an int32 [n, 4] tensor (16-byte SpillRecord16 rows)")
+        n = records.shape[0] if count is None else int(count)
+        if n > records.shape[0]:
+            raise ValueError(f"count {n} exceeds the {records.shape[0]} records given")
+        N.check(self._lib.tessa_hashprune_insert(self._h, _ptr(records), n, _stream_ptr(stream)), "hashprune insert")
+
+    def clear(self, stream: torch.cuda.Stream | None = None) -> None:
+        N.check(self._lib.tessa_hashprune_clear(self._h, _stream_ptr(stream)), "hashprune clear")
+
+    def slots(self, stream: torch.cuda.Stream | None = None):
+        """(targets int32 [num_points, l_max] (0xFFFFFFFF = unused), hashes int16,
+        dists f32, counts int32 [num_points]) in slot order (ascending hash)."""
+        t = torch.empty((self.num_points, self.l_max), dtype=torch.int32, device=self.device)
+        hs = torch.empty((self.num_points, self.l_max), dtype=torch.int16, device=self.device)
+        d = torch.empty((self.num_points, self.l_max), dtype=torch.float32, device=self.device)
+        c = torch.empty(self.num_points, dtype=torch.int32, device=self.device)
+        N.check(self._lib.tessa_hashprune_neighbors(self._h, _ptr(t), _ptr(hs), _ptr(d), _ptr(c),
+                                                    _stream_ptr(stream)), "hashprune neighbors")
+        return t, hs, d, c
+
+    def neighbors(self, stream: torch.cuda.Stream | None = None):
+        """(targets int32 [num_points, l_max], counts int32 [num_points])."""
+        t = torch.empty((self.num_points, self.l_max), dtype=torch.int32, device=self.device)
+        c = torch.empty(self.num_points, dtype=torch.int32, device=self.device)
+        N.check(self._lib.tessa_hashprune_neighbors(self._h, _ptr(t), None, None, _ptr(c), _stream_ptr(stream)),
+                "hashprune neighbors")
+        return t, c
+
+
+def reduce_spill_records_ordered(num_points: int, l_max: int, records, device="cuda") -> list[list[int]]:
+    """reduce_spill_artifacts_ordered (spill_hashprune.rs:875-892) over host or
+    device records: each point's neighbour ids in slot order."""
+    with HashPruneReducer(num_points, l_max, device) as hp:
+        hp.insert(records)
+        t, c = hp.neighbors()
+        torch.cuda.synchronize(hp.device)
+        tt = t.cpu().numpy().view(np.uint32)
+        cc = c.cpu().numpy()
+    return [tt[p, :cc[p]].tolist() for p in range(num_points)]
