@@ -52,6 +52,7 @@ def parse():
     ap.add_argument("--subtree-rows", type=int, default=10_000_000,
                     help="rows of the in-HBM subtree leg (C3: 10M x 768, leaves <= 2048, fanout 2, k=32)")
     ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
+    ap.add_argument("--no-hashprune", action="store_true", help="skip the HashPrune reservoir leg")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -209,7 +210,13 @@ def main() -> int:
     }
 
     if not args.no_edges:
-        result["record_emission"] = edge_leg(gids, lay, out_ids, out_d, stream, args.steps, args.warmup)
+        result["record_emission"], rec, rec_count = edge_leg(gids, lay, out_ids, out_d, stream, args.steps,
+                                                             args.warmup)
+        if not args.no_hashprune:
+            result["hashprune"] = hashprune_leg(rec, rec_count, gids.numel(), stream, args.steps, args.warmup,
+                                                check=not args.no_cpu_baseline)
+        del rec
+        torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
@@ -364,7 +371,7 @@ def edge_leg(gids, lay, out_ids, out_d, stream, steps, warmup):
     t = float(np.mean(ms)) / 1e3
     slots = lay.output_len
     log(f"record emission: {count} records, {np.mean(ms):.3f} ms")
-    del rec, sketches
+    del sketches
     return {
         "kernels": "edge_count_kernel + edge_scan_kernel + edge_emit_kernel",
         "records": count,
@@ -376,6 +383,66 @@ def edge_leg(gids, lay, out_ids, out_d, stream, steps, warmup):
         "hbm_bytes_algorithmic": slots * 8 + count * 16 + gids.numel() * 48,
         "hbm_gb_per_s_algorithmic": round((slots * 8 + count * 16 + gids.numel() * 48) / t / 1e9, 2),
         "peak_gb_per_s": HBM_PEAK_GBS,
+    }, rec, count
+
+
+def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_max=64, sample_points=16384):
+    """HashPrune reservoirs (l_max 64, the reference default) over the step's
+    edge records: empty reservoirs, then one batch of every record.  The
+    points [0, sample_points) are checked bit for bit against the oracle fed
+    with their records."""
+    import torch
+
+    from shear_amd import hashprune as H
+
+    ms = []
+    with H.HashPruneReducer(num_points, l_max, rec.device) as hp:
+        for i in range(warmup + steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            hp.clear(stream=stream)
+            hp.insert(rec, count, stream=stream)  # synchronises the stream (status read-back)
+            b.record(stream)
+            b.synchronize()
+            if i >= warmup:
+                ms.append(a.elapsed_time(b))
+        t, hs, d, c = hp.slots(stream=stream)
+        stream.synchronize()
+        filled = int((c == l_max).sum().item())
+        res = {}
+        if check:
+            from oracle import pyoracle as orc
+
+            r = rec[:count]
+            sel = r[:, 0].view(torch.int32) < sample_points
+            sub = r[sel].cpu().numpy().view(np.uint8).reshape(-1).view(orc.EDGE_DTYPE)
+            wt, wh, wd, wc = orc.hashprune_reduce(sample_points, l_max, sub)
+            gt = t[:sample_points].cpu().numpy().view(np.uint32)
+            gh = hs[:sample_points].cpu().numpy().view(np.uint16)
+            gd = d[:sample_points].cpu().numpy().view(np.uint32)
+            gc = c[:sample_points].cpu().numpy().view(np.uint32)
+            bad = np.nonzero((gc != wc) | np.any(gt != wt, 1) | np.any(gh != wh, 1) | np.any(gd != wd.view(np.uint32), 1))[0]
+            res = {"points": sample_points, "records": int(len(sub)), "mismatched_points": int(len(bad)),
+                   "bit_exact": len(bad) == 0}
+        del t, hs, d, c
+    tm = float(np.mean(ms)) / 1e3
+    # per record: read by the count and scatter passes, written grouped, read by
+    # the merge; per point: slots read and written (8 + 2 bytes each), 2 offsets
+    alg = count * 64 + num_points * (2 * l_max * 10 + 12)
+    log(f"hashprune: {count} records -> {num_points} reservoirs, {np.mean(ms):.3f} ms")
+    return {
+        "kernels": "hp_count + hp_scan (3) + hp_scatter + hp_merge",
+        "records": int(count),
+        "points": int(num_points),
+        "l_max": l_max,
+        "ms_mean": round(float(np.mean(ms)), 4),
+        "ms_min": round(float(np.min(ms)), 4),
+        "records_per_s": round(count / tm, 1),
+        "hbm_bytes_algorithmic": int(alg),
+        "hbm_gb_per_s_algorithmic": round(alg / tm / 1e9, 2),
+        "peak_gb_per_s": HBM_PEAK_GBS,
+        "full_reservoirs": filled,
+        "parity_sample": res,
     }
 
 

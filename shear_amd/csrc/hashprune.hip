@@ -17,10 +17,11 @@
 //   1. count records per source (atomics), exclusive scan, scatter the records
 //      grouped by source (the per-source counters return to zero);
 //   2. one wave per source with new records merges its current slots with them
-//      in LDS, up to kHpMergeCap at a time: a bitonic sort by the total order
-//      (dist key, target, then hash) gives each candidate its rank; a second
-//      sort by (hash, rank) puts each hash's best first; the l_max best of
-//      those (by rank) become the new slots, in ascending hash order.
+//      in LDS, up to kHpMergeCap at a time: a bitonic sort by (hash, total
+//      order: dist key, target) puts each hash's best first; when more than
+//      l_max hashes remain, a sort of those by the total order gives the
+//      l_max-th as a threshold; the survivors, in ascending hash order, are
+//      the new slots.
 #include "hashprune_kernels.h"
 
 namespace tessa {
@@ -59,12 +60,32 @@ __global__ void hp_fill_u32(uint32_t *a, uint64_t n, uint32_t v) {
 
 __global__ void hp_status_init(uint64_t *status) { status[0] = ~0ull; }
 
+// Lanes of a wave holding the same source as the wave's first active lane
+// share one atomic (the edge stream interleaves one row's outgoing records
+// with its reverse ones, so about half a wave has the same source).
+__device__ __forceinline__ uint64_t same_as_leader(uint32_t src, bool active, uint32_t &leader_src) {
+    const uint64_t act = __ballot(active);
+    const uint32_t leader = act ? (uint32_t)__builtin_ctzll(act) : 0u;
+    leader_src = __shfl(src, leader);
+    return __ballot(active && src == leader_src);
+}
+
 __global__ void hp_count_kernel(const uint4 *rec, uint64_t count, uint32_t num_points, uint32_t *bucket,
                                 uint64_t *status) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t src = rec[i].x;
-        if (src >= num_points) atomicMin((unsigned long long *)status, (unsigned long long)i);
-        else atomicAdd(&bucket[src], 1u);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    // uniform trip count per wave: lanes past the end stay inactive
+    for (uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63u); i0 < count; i0 += stride) {
+        const uint64_t i = i0 + lane;
+        const bool in = i < count;
+        const uint32_t src = in ? rec[i].x : 0u;
+        const bool bad = in && src >= num_points;
+        if (bad) atomicMin((unsigned long long *)status, (unsigned long long)i);
+        uint32_t lsrc;
+        const uint64_t grp = same_as_leader(src, in && !bad, lsrc);
+        const bool in_grp = (grp >> lane) & 1ull;
+        if (in_grp && lane == (uint32_t)__builtin_ctzll(grp)) atomicAdd(&bucket[lsrc], (uint32_t)__popcll(grp));
+        if (in && !bad && !in_grp) atomicAdd(&bucket[src], 1u);
     }
 }
 
@@ -142,11 +163,27 @@ __global__ __launch_bounds__(kScanThreads) void hp_scan_apply(const uint32_t *bu
 // Records grouped by source; the per-source counters count back down to zero.
 __global__ void hp_scatter_kernel(const uint4 *rec, uint64_t count, uint32_t num_points, uint32_t *bucket,
                                   const uint32_t *offsets, uint4 *grouped) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint4 r = rec[i];
-        if (r.x >= num_points) continue;
-        const uint32_t pos = offsets[r.x] + atomicSub(&bucket[r.x], 1u) - 1u;
-        grouped[pos] = r;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63u); i0 < count; i0 += stride) {
+        const uint64_t i = i0 + lane;
+        const bool in = i < count;
+        const uint4 r = in ? rec[i] : make_uint4(0u, 0u, 0u, 0u);
+        const bool ok = in && r.x < num_points;
+        uint32_t lsrc;
+        const uint64_t grp = same_as_leader(r.x, ok, lsrc);
+        const bool in_grp = (grp >> lane) & 1ull;
+        // the group takes popcount(grp) positions with one atomic; lane order inside it
+        const uint32_t first = grp ? (uint32_t)__builtin_ctzll(grp) : 0u;
+        uint32_t top = 0;
+        if (in_grp && lane == first) top = atomicSub(&bucket[lsrc], (uint32_t)__popcll(grp));
+        top = __shfl(top, first);
+        if (in_grp) {
+            const uint32_t below = (uint32_t)__popcll(grp & ((1ull << lane) - 1ull));
+            grouped[offsets[lsrc] + top - 1u - below] = r;
+        } else if (ok) {
+            grouped[offsets[r.x] + atomicSub(&bucket[r.x], 1u) - 1u] = r;
+        }
     }
 }
 
@@ -177,13 +214,35 @@ __device__ void wave_bitonic(K *key, uint32_t *val, uint32_t P, uint32_t lane) {
     }
 }
 
+// Ascending bitonic sort of (hash, key) pairs, hash first, over [0, P).
+__device__ void wave_bitonic_hk(uint32_t *hash, uint64_t *key, uint32_t P, uint32_t lane) {
+    for (uint32_t k = 2; k <= P; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t c = lane; c < P / 2; c += 64) {
+                const uint32_t i = ((c & ~(j - 1u)) << 1) | (c & (j - 1u));
+                const uint32_t l = i + j;
+                const bool up = (i & k) == 0;
+                const uint32_t ha = hash[i], hb = hash[l];
+                const uint64_t a = key[i], b = key[l];
+                const bool b_less = hb < ha || (hb == ha && b < a);
+                const bool a_less = ha < hb || (ha == hb && a < b);
+                if (up ? b_less : a_less) {
+                    hash[i] = hb;
+                    hash[l] = ha;
+                    key[i] = b;
+                    key[l] = a;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 struct HpWaveLds {
-    uint64_t key[kHpMergeCap];      // candidates by total-order key
-    uint32_t val[kHpMergeCap];      // hash while sorting by key; then (hash << 16 | rank)
-    uint32_t flag[kHpMergeCap];     // kept flag by rank, then its exclusive prefix
-    uint64_t out_key[kHpMaxLMax];   // the merged reservoir
-    uint32_t out_hash[kHpMaxLMax];
-    uint32_t rank_of[kHpMergeCap];  // val sorted by (hash, rank): payload slot for the second sort
+    uint64_t key[kHpMergeCap];      // candidates: total-order key (dist key << 32 | target)
+    uint32_t val[kHpMergeCap];      // their hashes
+    uint64_t tkey[kHpMergeCap];     // kept candidates, when more than l_max, by total order;
+    uint32_t thash[kHpMergeCap];    // then the merged reservoir (once the threshold is read)
 };
 
 __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *grouped, const uint32_t *offsets,
@@ -195,9 +254,26 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *group
     const uint32_t wave = threadIdx.x >> 6;
     HpWaveLds &w = lds[wave];
     const uint32_t waves = gridDim.x * kHpWaves;
-    for (uint32_t src = blockIdx.x * kHpWaves + wave; src < num_points; src += waves) {
-        const uint32_t off = offsets[src];
-        const uint32_t n_new = offsets[src + 1] - off;
+    // the next source's offsets and first 64 records are loaded one iteration
+    // ahead, so their latency overlaps the current merge
+    uint32_t src = blockIdx.x * kHpWaves + wave;
+    uint32_t p_off = 0, p_n = 0;
+    uint4 p_rec = make_uint4(0u, 0u, 0u, 0u);
+    if (src < num_points) {
+        p_off = offsets[src];
+        p_n = offsets[src + 1] - p_off;
+        if (lane < p_n) p_rec = grouped[p_off + lane];
+    }
+    for (; src < num_points; src += waves) {
+        const uint32_t off = p_off;
+        const uint32_t n_new = p_n;
+        const uint4 r0 = p_rec;
+        const uint32_t nsrc = src + waves;
+        if (nsrc < num_points) {
+            p_off = offsets[nsrc];
+            p_n = offsets[nsrc + 1] - p_off;
+            if (lane < p_n) p_rec = grouped[p_off + lane];
+        }
         if (n_new == 0) continue;
         uint32_t n_old = slot_count[src];
         const uint64_t sbase = (uint64_t)src * l_max;
@@ -209,7 +285,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *group
         while (used < n_new) {
             const uint32_t take = (n_new - used < kHpMergeCap - n_old) ? n_new - used : kHpMergeCap - n_old;
             for (uint32_t e = lane; e < take; e += 64) {
-                const uint4 r = grouped[off + used + e];
+                const uint4 r = (used == 0 && e == lane) ? r0 : grouped[off + used + e];
                 w.key[n_old + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
                 w.val[n_old + e] = r.z & 0xffffu;
             }
@@ -218,73 +294,88 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *group
             while (P < N) P <<= 1;
             for (uint32_t e = N + lane; e < P; e += 64) {
                 w.key[e] = ~0ull;
-                w.val[e] = 0xffffu;
+                w.val[e] = 0xffffffffu;  // after every real hash (<= 0xffff)
             }
             __builtin_amdgcn_wave_barrier();
-            // ranks: position in total order
-            wave_bitonic<uint64_t>(w.key, w.val, P, lane);
-            // each hash's best first: sort (hash << 16 | rank)
-            for (uint32_t e = lane; e < P; e += 64) {
-                w.rank_of[e] = e < N ? ((w.val[e] << 16) | e) : 0xffffffffu;
-                w.flag[e] = 0u;
+            // each hash's best first: sort by (hash, total-order key)
+            wave_bitonic_hk(w.val, w.key, P, lane);
+            const uint32_t E = P / 64;
+            const uint32_t eb = lane * E;
+            // kept = first of its hash; kpos = its place among the kept
+            uint32_t kcount = 0;
+            for (uint32_t q = 0; q < E; ++q) {
+                const uint32_t e = eb + q;
+                kcount += (e < N && (e == 0 || w.val[e - 1] != w.val[e])) ? 1u : 0u;
             }
-            __builtin_amdgcn_wave_barrier();
-            wave_bitonic<uint32_t>(w.rank_of, w.val, P, lane);
-            for (uint32_t e = lane; e < N; e += 64) {
-                const uint32_t v = w.rank_of[e];
-                const bool kept = e == 0 || (w.rank_of[e - 1] >> 16) != (v >> 16);
-                if (kept) w.flag[v & 0xffffu] = 1u;
-            }
-            __builtin_amdgcn_wave_barrier();
-            // exclusive prefix of the kept flags in rank order
-            {
-                const uint32_t E = P / 64;
-                const uint32_t b = lane * E;
-                uint32_t t = 0;
-                for (uint32_t q = 0; q < E; ++q) t += w.flag[b + q];
-                uint32_t tot;
-                uint32_t run = wave_excl_scan(t, lane, tot);
+            uint32_t n_kept;
+            const uint32_t kbase = wave_excl_scan(kcount, lane, n_kept);
+            if (n_kept <= l_max) {
+                // every hash's best stays, already in ascending hash order
+                uint32_t run = kbase;
                 for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t f = w.flag[b + q];
-                    w.flag[b + q] = f ? run : 0xffffffffu;  // prefix for kept ranks, sentinel otherwise
-                    run += f;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-            // selected = kept with fewer than l_max kept before it; compact in hash order
-            {
-                const uint32_t E = P / 64;
-                const uint32_t b = lane * E;
-                uint32_t t = 0;
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t v = w.rank_of[b + q];
-                    t += (b + q < N && w.flag[v & 0xffffu] < l_max) ? 1u : 0u;
-                }
-                uint32_t tot;
-                uint32_t run = wave_excl_scan(t, lane, tot);
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t v = w.rank_of[b + q];
-                    if (b + q < N && w.flag[v & 0xffffu] < l_max) {
-                        w.out_key[run] = w.key[v & 0xffffu];
-                        w.out_hash[run] = v >> 16;
+                    const uint32_t e = eb + q;
+                    if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
+                        w.tkey[run] = w.key[e];
+                        w.thash[run] = w.val[e];
                         ++run;
                     }
                 }
-                n_old = tot;
+                n_old = n_kept;
+            } else {
+                // the l_max best of the kept by (key, hash): threshold from a sort of the kept
+                uint32_t run = kbase;
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t e = eb + q;
+                    if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
+                        w.tkey[run] = w.key[e];
+                        w.thash[run] = w.val[e];
+                        ++run;
+                    }
+                }
+                uint32_t P2 = 64;
+                while (P2 < n_kept) P2 <<= 1;
+                for (uint32_t e = n_kept + lane; e < P2; e += 64) {
+                    w.tkey[e] = ~0ull;
+                    w.thash[e] = 0xffffffffu;
+                }
+                __builtin_amdgcn_wave_barrier();
+                wave_bitonic<uint64_t>(w.tkey, w.thash, P2, lane);
+                const uint64_t tk = w.tkey[l_max - 1];
+                const uint32_t th = w.thash[l_max - 1];
+                uint32_t scount = 0;
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t e = eb + q;
+                    const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
+                    const uint64_t k = w.key[e];
+                    scount += (kept && (k < tk || (k == tk && w.val[e] <= th))) ? 1u : 0u;
+                }
+                uint32_t n_sel;
+                uint32_t srun = wave_excl_scan(scount, lane, n_sel);
+                for (uint32_t q = 0; q < E; ++q) {
+                    const uint32_t e = eb + q;
+                    const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
+                    const uint64_t k = w.key[e];
+                    if (kept && (k < tk || (k == tk && w.val[e] <= th))) {
+                        w.tkey[srun] = k;
+                        w.thash[srun] = w.val[e];
+                        ++srun;
+                    }
+                }
+                n_old = n_sel;
             }
             __builtin_amdgcn_wave_barrier();
             used += take;
             if (used < n_new) {
                 for (uint32_t e = lane; e < n_old; e += 64) {
-                    w.key[e] = w.out_key[e];
-                    w.val[e] = w.out_hash[e];
+                    w.key[e] = w.tkey[e];
+                    w.val[e] = w.thash[e];
                 }
                 __builtin_amdgcn_wave_barrier();
             }
         }
         for (uint32_t e = lane; e < n_old; e += 64) {
-            slot_keys[sbase + e] = w.out_key[e];
-            slot_hash[sbase + e] = (uint16_t)w.out_hash[e];
+            slot_keys[sbase + e] = w.tkey[e];
+            slot_hash[sbase + e] = (uint16_t)w.thash[e];
         }
         if (lane == 0) slot_count[src] = n_old;
         __builtin_amdgcn_wave_barrier();
