@@ -17,11 +17,11 @@
 //   1. count records per source (atomics), exclusive scan, scatter the records
 //      grouped by source (the per-source counters return to zero);
 //   2. one wave per source with new records merges its current slots with them
-//      in LDS, up to kHpMergeCap at a time: a bitonic sort by (hash, total
-//      order: dist key, target) puts each hash's best first; when more than
-//      l_max hashes remain, a sort of those by the total order gives the
-//      l_max-th as a threshold; the survivors, in ascending hash order, are
-//      the new slots.
+//      (in registers up to 128 candidates, else in LDS up to kHpMergeCap at a
+//      time): a bitonic sort by (hash, total order: dist key, target) puts
+//      each hash's best first; when more than l_max hashes remain, a sort of
+//      those by the total order gives the l_max-th as a threshold; the
+//      survivors, in ascending hash order, are the new slots.
 #include "hashprune_kernels.h"
 
 namespace tessa {
@@ -238,6 +238,129 @@ __device__ void wave_bitonic_hk(uint32_t *hash, uint64_t *key, uint32_t P, uint3
     }
 }
 
+// Register bitonic sort of P = 64*E elements, element q*64 + lane in lane
+// `lane`'s slot q, by (hash, key) when kHashFirst, else by (key, hash).
+template <int E, bool kHashFirst>
+__device__ __forceinline__ void reg_bitonic(uint32_t (&h)[E], uint64_t (&k)[E], uint32_t lane) {
+    auto less = [](uint32_t ha, uint64_t ka, uint32_t hb, uint64_t kb) {
+        return kHashFirst ? (ha < hb || (ha == hb && ka < kb)) : (ka < kb || (ka == kb && ha < hb));
+    };
+#pragma unroll
+    for (uint32_t kk = 2; kk <= 64u * E; kk <<= 1) {
+#pragma unroll
+        for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
+            if (j >= 64) {
+                const uint32_t jq = j / 64;
+#pragma unroll
+                for (int q = 0; q < E; ++q) {
+                    if ((q & jq) != 0) continue;
+                    const int l = q | jq;
+                    const bool up = (((uint32_t)q * 64u + lane) & kk) == 0;
+                    const bool sw = up ? less(h[l], k[l], h[q], k[q]) : less(h[q], k[q], h[l], k[l]);
+                    const uint32_t th = h[q];
+                    const uint64_t tk = k[q];
+                    h[q] = sw ? h[l] : h[q];
+                    k[q] = sw ? k[l] : k[q];
+                    h[l] = sw ? th : h[l];
+                    k[l] = sw ? tk : k[l];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < E; ++q) {
+                    const uint32_t ph = __shfl_xor(h[q], (int)j);
+                    const uint32_t plo = __shfl_xor((uint32_t)k[q], (int)j);
+                    const uint32_t phi = __shfl_xor((uint32_t)(k[q] >> 32), (int)j);
+                    const uint64_t pk = ((uint64_t)phi << 32) | plo;
+                    const bool up = (((uint32_t)q * 64u + lane) & kk) == 0;
+                    const bool want_min = ((lane & j) == 0) == up;
+                    const bool take = want_min ? less(ph, pk, h[q], k[q]) : less(h[q], k[q], ph, pk);
+                    h[q] = take ? ph : h[q];
+                    k[q] = take ? pk : k[q];
+                }
+            }
+        }
+    }
+}
+
+// One merge of a source's n_old slots and n_new records (n_old + n_new <= 64*E)
+// entirely in registers; writes the new slots and returns their count.
+template <int E>
+__device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot_hash_in, uint32_t n_old,
+                              const uint4 *recs, uint32_t n_new, const uint4 &r0, uint32_t l_max, uint32_t lane,
+                              uint64_t *slot_keys_out, uint16_t *slot_hash_out) {
+    const uint32_t N = n_old + n_new;
+    uint32_t h[E];
+    uint64_t k[E];
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        h[q] = 0xffffffffu;
+        k[q] = ~0ull;
+        if (e < n_old) {
+            k[q] = slot_keys_in[e];
+            h[q] = slot_hash_in[e];
+        } else if (e < N) {
+            // the prefetched first 64 records line up with this slot when n_old == 64*q
+            const uint4 r = (n_old == (uint32_t)q * 64u) ? r0 : recs[e - n_old];
+            k[q] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
+            h[q] = r.z & 0xffffu;
+        }
+    }
+    reg_bitonic<E, true>(h, k, lane);
+    // kept = first of its hash (the predecessor of element 64*q is lane 63 of slot q-1)
+    bool kept[E];
+    uint32_t n_kept = 0;
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        uint32_t prev = __shfl_up(h[q], 1);
+        if (q > 0) {
+            const uint32_t last = __shfl(h[q - 1], 63);
+            prev = lane == 0 ? last : prev;
+        }
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        kept[q] = e < N && (e == 0 || prev != h[q]);
+        n_kept += (uint32_t)__popcll(__ballot(kept[q]));
+    }
+    bool sel[E];
+#pragma unroll
+    for (int q = 0; q < E; ++q) sel[q] = kept[q];
+    if (n_kept > l_max) {
+        // threshold: the l_max-th kept candidate in total order
+        uint32_t h2[E];
+        uint64_t k2[E];
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+            h2[q] = kept[q] ? h[q] : 0xffffffffu;
+            k2[q] = kept[q] ? k[q] : ~0ull;
+        }
+        reg_bitonic<E, false>(h2, k2, lane);
+        const uint32_t tq = (l_max - 1u) / 64u, tl = (l_max - 1u) % 64u;
+        uint64_t tk = k2[0];
+        uint32_t th = h2[0];
+#pragma unroll
+        for (int q = 1; q < E; ++q) {
+            tk = tq == (uint32_t)q ? k2[q] : tk;
+            th = tq == (uint32_t)q ? h2[q] : th;
+        }
+        const uint64_t tkey = ((uint64_t)__shfl((uint32_t)(tk >> 32), (int)tl) << 32) | __shfl((uint32_t)tk, (int)tl);
+        const uint32_t thash = __shfl(th, (int)tl);
+#pragma unroll
+        for (int q = 0; q < E; ++q) sel[q] = kept[q] && (k[q] < tkey || (k[q] == tkey && h[q] <= thash));
+    }
+    uint32_t base = 0;
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        const uint64_t m = __ballot(sel[q]);
+        if (sel[q]) {
+            const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+            slot_keys_out[pos] = k[q];
+            slot_hash_out[pos] = (uint16_t)h[q];
+        }
+        base += (uint32_t)__popcll(m);
+    }
+    return base;
+}
+
 struct HpWaveLds {
     uint64_t key[kHpMergeCap];      // candidates: total-order key (dist key << 32 | target)
     uint32_t val[kHpMergeCap];      // their hashes
@@ -245,18 +368,17 @@ struct HpWaveLds {
     uint32_t thash[kHpMergeCap];    // then the merged reservoir (once the threshold is read)
 };
 
-__global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *grouped, const uint32_t *offsets,
-                                                              uint32_t num_points, uint32_t l_max,
-                                                              uint64_t *slot_keys, uint16_t *slot_hash,
-                                                              uint32_t *slot_count) {
-    __shared__ HpWaveLds lds[kHpWaves];
+// Sources with at most 128 candidates (slots + new records): register merges,
+// no LDS, so occupancy is set by registers alone.
+__global__ __launch_bounds__(kHpThreads) void hp_merge_small_kernel(const uint4 *grouped, const uint32_t *offsets,
+                                                                    uint32_t num_points, uint32_t l_max,
+                                                                    uint64_t *slot_keys, uint16_t *slot_hash,
+                                                                    uint32_t *slot_count) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    HpWaveLds &w = lds[wave];
     const uint32_t waves = gridDim.x * kHpWaves;
     // the next source's offsets and first 64 records are loaded one iteration
     // ahead, so their latency overlaps the current merge
-    uint32_t src = blockIdx.x * kHpWaves + wave;
+    uint32_t src = blockIdx.x * kHpWaves + (threadIdx.x >> 6);
     uint32_t p_off = 0, p_n = 0;
     uint4 p_rec = make_uint4(0u, 0u, 0u, 0u);
     if (src < num_points) {
@@ -275,7 +397,37 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *group
             if (lane < p_n) p_rec = grouped[p_off + lane];
         }
         if (n_new == 0) continue;
+        const uint32_t n_old = slot_count[src];
+        const uint64_t sbase = (uint64_t)src * l_max;
+        uint32_t c;
+        if (n_old + n_new <= 64u)
+            c = reg_merge<1>(slot_keys + sbase, slot_hash + sbase, n_old, grouped + off, n_new, r0, l_max, lane,
+                             slot_keys + sbase, slot_hash + sbase);
+        else if (n_old + n_new <= 128u)
+            c = reg_merge<2>(slot_keys + sbase, slot_hash + sbase, n_old, grouped + off, n_new, r0, l_max, lane,
+                             slot_keys + sbase, slot_hash + sbase);
+        else
+            continue;  // hp_merge_large_kernel
+        if (lane == 0) slot_count[src] = c;
+    }
+}
+
+// Sources with more than 128 candidates: merged in LDS, kHpMergeCap at a time.
+__global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 *grouped, const uint32_t *offsets,
+                                                                    uint32_t num_points, uint32_t l_max,
+                                                                    uint64_t *slot_keys, uint16_t *slot_hash,
+                                                                    uint32_t *slot_count) {
+    __shared__ HpWaveLds lds[kHpWaves];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    HpWaveLds &w = lds[wave];
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t src = blockIdx.x * kHpWaves + wave; src < num_points; src += waves) {
+        const uint32_t off = offsets[src];
+        const uint32_t n_new = offsets[src + 1] - off;
+        if (n_new == 0) continue;
         uint32_t n_old = slot_count[src];
+        if (n_old + n_new <= 128u) continue;  // merged by hp_merge_small_kernel
         const uint64_t sbase = (uint64_t)src * l_max;
         for (uint32_t e = lane; e < n_old; e += 64) {
             w.key[e] = slot_keys[sbase + e];
@@ -285,7 +437,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_kernel(const uint4 *group
         while (used < n_new) {
             const uint32_t take = (n_new - used < kHpMergeCap - n_old) ? n_new - used : kHpMergeCap - n_old;
             for (uint32_t e = lane; e < take; e += 64) {
-                const uint4 r = (used == 0 && e == lane) ? r0 : grouped[off + used + e];
+                const uint4 r = grouped[off + used + e];
                 w.key[n_old + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
                 w.val[n_old + e] = r.z & 0xffffu;
             }
@@ -427,8 +579,14 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
     hipLaunchKernelGGL(hp_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums, s.offsets);
     hipLaunchKernelGGL(hp_scatter_kernel, dim3(grid_for(count, 256, 16384)), dim3(256), 0, stream, records, count, n,
                        s.bucket, s.offsets, s.grouped);
-    hipLaunchKernelGGL(hp_merge_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream, s.grouped,
-                       s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    // Both kernels decide from slots + new records; a merge never shrinks a
+    // reservoir, so after the large kernel every source it merged still counts
+    // more than 128 and the small kernel skips it (the reverse order could
+    // merge a source twice).
+    hipLaunchKernelGGL(hp_merge_large_kernel, dim3(grid_for(n, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
+                       s.grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    hipLaunchKernelGGL(hp_merge_small_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream,
+                       s.grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
