@@ -17,7 +17,7 @@
 //   1. count records per source (atomics), exclusive scan, scatter the records
 //      grouped by source (the per-source counters return to zero);
 //   2. one wave per source with new records merges its current slots with them
-//      (in registers up to 128 candidates, else in LDS up to kHpMergeCap at a
+//      (in registers up to 256 candidates, else in LDS up to kHpMergeCap at a
 //      time): a bitonic sort by (hash, total order: dist key, target) puts
 //      each hash's best first; when more than l_max hashes remain, a sort of
 //      those by the total order gives the l_max-th as a threshold; the
@@ -28,7 +28,8 @@ namespace tessa {
 
 namespace {
 
-constexpr int kHpWaves = 4;                 // waves per workgroup of the merge kernel
+constexpr int kHpWaves = 4;                 // waves per workgroup of the merge kernels
+constexpr uint32_t kHpRegMax = 256;         // largest merge done in registers (4 candidates per lane)
 constexpr int kHpThreads = kHpWaves * 64;
 constexpr int kScanThreads = 1024;
 constexpr int kScanPerThread = 4;
@@ -368,8 +369,8 @@ struct HpWaveLds {
     uint32_t thash[kHpMergeCap];    // then the merged reservoir (once the threshold is read)
 };
 
-// Sources with at most 128 candidates (slots + new records): register merges,
-// no LDS, so occupancy is set by registers alone.
+// Sources with at most kHpRegMax candidates (slots + new records): register
+// merges, no LDS, so occupancy is set by registers alone.
 __global__ __launch_bounds__(kHpThreads) void hp_merge_small_kernel(const uint4 *grouped, const uint32_t *offsets,
                                                                     uint32_t num_points, uint32_t l_max,
                                                                     uint64_t *slot_keys, uint16_t *slot_hash,
@@ -406,13 +407,17 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_small_kernel(const uint4 
         else if (n_old + n_new <= 128u)
             c = reg_merge<2>(slot_keys + sbase, slot_hash + sbase, n_old, grouped + off, n_new, r0, l_max, lane,
                              slot_keys + sbase, slot_hash + sbase);
+        else if (n_old + n_new <= kHpRegMax)
+            c = reg_merge<4>(slot_keys + sbase, slot_hash + sbase, n_old, grouped + off, n_new, r0, l_max, lane,
+                             slot_keys + sbase, slot_hash + sbase);
         else
             continue;  // hp_merge_large_kernel
         if (lane == 0) slot_count[src] = c;
     }
 }
 
-// Sources with more than 128 candidates: merged in LDS, kHpMergeCap at a time.
+// Sources with more than kHpRegMax candidates: merged in LDS, kHpMergeCap at a
+// time.
 __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 *grouped, const uint32_t *offsets,
                                                                     uint32_t num_points, uint32_t l_max,
                                                                     uint64_t *slot_keys, uint16_t *slot_hash,
@@ -427,7 +432,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 
         const uint32_t n_new = offsets[src + 1] - off;
         if (n_new == 0) continue;
         uint32_t n_old = slot_count[src];
-        if (n_old + n_new <= 128u) continue;  // merged by hp_merge_small_kernel
+        if (n_old + n_new <= kHpRegMax) continue;  // merged by hp_merge_small_kernel
         const uint64_t sbase = (uint64_t)src * l_max;
         for (uint32_t e = lane; e < n_old; e += 64) {
             w.key[e] = slot_keys[sbase + e];
@@ -581,8 +586,8 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
                        s.bucket, s.offsets, s.grouped);
     // Both kernels decide from slots + new records; a merge never shrinks a
     // reservoir, so after the large kernel every source it merged still counts
-    // more than 128 and the small kernel skips it (the reverse order could
-    // merge a source twice).
+    // more than kHpRegMax and the small kernel skips it (the reverse order
+    // could merge a source twice).
     hipLaunchKernelGGL(hp_merge_large_kernel, dim3(grid_for(n, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
                        s.grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
     hipLaunchKernelGGL(hp_merge_small_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream,

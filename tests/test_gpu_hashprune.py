@@ -45,6 +45,9 @@ def _same(got, want, what=""):
     (5, 1000, 60000, 64, 12, 4000),  # default l_max and m_hash_bits
     (6, 7, 9000, 256, 12, 100000),  # largest l_max
     (7, 300, 2000, 1, 1, 2),
+    (8, 20, 4000, 32, 12, 500),      # 129..256 candidates per point, in registers
+    (9, 20, 4000, 200, 12, 500),
+    (10, 60, 9000, 64, 8, 300),      # 256 hashes: many collisions at 150 candidates
 ])
 def test_random_streams_match_oracle(gpu, orc, seed, num_points, n, l_max, hash_bits, levels):
     rng = np.random.default_rng(seed)
