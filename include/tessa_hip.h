@@ -435,6 +435,20 @@ tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targ
                                        float *dists, uint32_t *counts, void *stream);
 tessa_status tessa_hashprune_clear(tessa_hashprune *hp, void *stream);
 
+/* ---- graph emission ----------------------------------------------------------
+ * The `_mem.index` byte image DirectMemGraphWriter writes
+ * (index/inmem_index/pipnn_oom_writer.rs:23-72: create, write_node per point
+ * in id order, finish rewriting the header), built on the GPU from a
+ * neighbour table: point p's row is targets[p * row_stride .. + counts[p]]
+ * (counts clipped to row_stride), e.g. the HashPrune reservoirs' slot
+ * targets.  Layout (little-endian): index_size u64 (the file size),
+ * max_degree u32, start u32, num_frozen_pts u64, then per point degree u32
+ * and its ids.  Device pointers; `out` 8-byte aligned, or NULL to get only
+ * *index_size.  Synchronises `stream` once (to read the size). */
+tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, uint32_t num_points,
+                              uint32_t row_stride, uint32_t start, uint64_t num_frozen_pts, void *out,
+                              uint64_t out_capacity, uint64_t *index_size, void *stream);
+
 /* ---- asynchronous subtree submissions ----------------------------------
  * Replaces submit_owned_quantized_subtree_l2_compact_topk
  * (compute_backend.rs:3807-3815) with its Deferred result and pinned host-slot

@@ -363,3 +363,13 @@ def hashprune_reduce(num_points: int, l_max: int, records: np.ndarray):
     if rc != 0:
         raise ValueError(f"orc_hashprune_reduce: {rc} (record {bad.value})")
     return t, hs, d, cnt
+
+
+def graph_bytes(start: int, num_frozen: int, rows) -> bytes:
+    """DirectMemGraphWriter file bytes (index/inmem_index/pipnn_oom_writer.rs:35-72):
+    header (index_size u64, max_degree u32, start u32, num_frozen_pts u64), then
+    per row its degree (u32) and ids (u32), little-endian."""
+    body = b"".join(np.uint32(len(r)).tobytes() + np.asarray(r, "<u4").tobytes() for r in rows)
+    max_degree = max((len(r) for r in rows), default=0)
+    head = np.array([(24 + len(body), max_degree, start, num_frozen)], dtype=np.dtype("<u8,<u4,<u4,<u8")).tobytes()
+    return head + body

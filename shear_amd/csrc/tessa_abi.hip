@@ -20,6 +20,7 @@
 #include "../../include/tessa_hip.h"
 #include "assign_kernels.h"
 #include "edge_kernels.h"
+#include "graph_kernels.h"
 #include "hashprune_kernels.h"
 #include "leaf_kernels.h"
 #include "partition.h"
@@ -79,6 +80,13 @@ struct DeviceWorkspace {
     uint64_t edge_base_capacity = 0;
     uint64_t *edge_status = nullptr;
     uint64_t edge_status_capacity = 0;
+    // graph packing: scan partials, row offsets, (total words, max degree)
+    uint64_t *graph_sums = nullptr;
+    uint64_t graph_sums_capacity = 0;
+    uint64_t *graph_row_off = nullptr;
+    uint64_t graph_row_off_capacity = 0;
+    uint64_t *graph_scalars = nullptr;
+    uint64_t graph_scalars_capacity = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
@@ -1550,6 +1558,58 @@ tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targ
     if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
     if (tessa::launch_hashprune_export(hp->st, targets, hashes, dists, counts, reinterpret_cast<hipStream_t>(stream)) != 0)
         return make_status(TESSA_ERR_HIP, 0, "hashprune export launch failed");
+    return ok_status();
+}
+
+}  // extern "C"
+
+// ---- graph emission ---------------------------------------------------------------
+
+extern "C" {
+
+tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, uint32_t num_points,
+                              uint32_t row_stride, uint32_t start, uint64_t num_frozen_pts, void *out,
+                              uint64_t out_capacity, uint64_t *index_size, void *stream) {
+    if (!index_size) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph pack: null index_size");
+    *index_size = 0;
+    if (num_points && (!counts || (row_stride && !targets)))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph pack: null neighbour table");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    DeviceWorkspace *ws = nullptr;
+    tessa_status st = device_workspace(&ws);
+    if (st.code) return st;
+    st = grow(&ws->graph_sums, &ws->graph_sums_capacity, tessa::graph_scan_blocks(num_points), sizeof(uint64_t),
+              "graph scan partials");
+    if (st.code) return st;
+    st = grow(&ws->graph_row_off, &ws->graph_row_off_capacity, (uint64_t)num_points + 1, sizeof(uint64_t),
+              "graph row offsets");
+    if (st.code) return st;
+    st = grow(&ws->graph_scalars, &ws->graph_scalars_capacity, 2, sizeof(uint64_t), "graph scalars");
+    if (st.code) return st;
+    tessa::GraphPackParams p{};
+    p.targets = targets;
+    p.counts = counts;
+    p.num_points = num_points;
+    p.row_stride = row_stride;
+    p.start = start;
+    p.num_frozen = num_frozen_pts;
+    p.out_words = reinterpret_cast<uint32_t *>(out);
+    p.block_sums = ws->graph_sums;
+    p.row_off = ws->graph_row_off;
+    p.total_words = ws->graph_scalars;
+    p.max_degree = reinterpret_cast<uint32_t *>(ws->graph_scalars + 1);
+    if (tessa::launch_graph_size(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph size launch failed");
+    uint64_t words = 0;
+    TESSA_HIP_TRY(hipMemcpyAsync(&words, p.total_words, sizeof(words), hipMemcpyDeviceToHost, s));
+    TESSA_HIP_TRY(hipStreamSynchronize(s));
+    *index_size = 24ull + 4ull * words;
+    if (!out) return ok_status();
+    if (out_capacity < *index_size)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph pack: output of %llu bytes below the %llu needed",
+                           (unsigned long long)out_capacity, (unsigned long long)*index_size);
+    if (reinterpret_cast<uintptr_t>(out) % 8 != 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph pack: output must be 8-byte aligned");
+    if (tessa::launch_graph_pack(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph pack launch failed");
     return ok_status();
 }
 

@@ -1,0 +1,65 @@
+"""Graph emission: the `_mem.index` file of a neighbour table, packed on the GPU.
+
+Host mirror of DirectMemGraphWriter (shear-core/src/index/inmem_index/
+pipnn_oom_writer.rs:23-72): ``write_mem_index`` writes what create +
+write_node (per point, id order) + finish write; the byte image itself is
+built by ``tessa_graph_pack`` in libtessa_hip.so.  ``read_mem_index`` parses
+the same layout back (header: index_size u64, max_degree u32, start u32,
+num_frozen_pts u64; rows: degree u32 then ids, little-endian).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .tessa import _ptr, _stream_ptr
+
+
+def pack_mem_index(targets: torch.Tensor, counts: torch.Tensor, start: int, num_frozen: int = 0,
+                   stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Device uint8 tensor holding the file image.  ``targets`` int32
+    [num_points, row_stride] (row p's ids first), ``counts`` int32 [num_points]."""
+    if targets.dim() != 2 or targets.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise ValueError("targets must be int32 [num_points, row_stride] and counts int32 [num_points]")
+    n, stride = targets.shape
+    if counts.numel() != n:
+        raise ValueError(f"counts has {counts.numel()} entries for {n} rows")
+    t = targets.contiguous()
+    size = C.c_uint64(0)
+    lib = N.load()
+    N.check(lib.tessa_graph_pack(_ptr(t), _ptr(counts), n, stride, start, num_frozen, None, 0, C.byref(size),
+                                 _stream_ptr(stream)), "graph pack")
+    out = torch.empty((size.value + 7) // 8, dtype=torch.int64, device=t.device)  # 8-byte aligned
+    N.check(lib.tessa_graph_pack(_ptr(t), _ptr(counts), n, stride, start, num_frozen, _ptr(out), out.numel() * 8,
+                                 C.byref(size), _stream_ptr(stream)), "graph pack")
+    return out.view(torch.uint8)[: size.value]
+
+
+def write_mem_index(path, targets: torch.Tensor, counts: torch.Tensor, start: int, num_frozen: int = 0) -> int:
+    """Write the `_mem.index` file; returns its size in bytes."""
+    img = pack_mem_index(targets, counts, start, num_frozen)
+    data = img.cpu().numpy()
+    Path(path).write_bytes(data.tobytes())
+    return len(data)
+
+
+def read_mem_index(src):
+    """(start, num_frozen, max_degree, rows) from a path or bytes; rows is a
+    list of uint32 arrays in point order."""
+    buf = Path(src).read_bytes() if not isinstance(src, (bytes, bytearray, memoryview)) else bytes(src)
+    size, max_degree, start, frozen = np.frombuffer(buf[:24], dtype=np.dtype("<u8,<u4,<u4,<u8"))[0]
+    if size != len(buf):
+        raise ValueError(f"index_size {size} != {len(buf)} bytes")
+    words = np.frombuffer(buf[24:], dtype="<u4")
+    rows, i = [], 0
+    while i < len(words):
+        d = int(words[i])
+        rows.append(words[i + 1: i + 1 + d].copy())
+        i += 1 + d
+    if i != len(words):
+        raise ValueError("truncated row")
+    return int(start), int(frozen), int(max_degree), rows
