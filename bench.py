@@ -53,6 +53,8 @@ def parse():
                     help="rows of the in-HBM subtree leg (C3: 10M x 768, leaves <= 2048, fanout 2, k=32)")
     ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
     ap.add_argument("--no-hashprune", action="store_true", help="skip the HashPrune reservoir leg")
+    ap.add_argument("--no-recall", action="store_true", help="skip the end-to-end graph build + recall leg")
+    ap.add_argument("--recall-rows", type=int, default=200_000, help="points of the recall leg's C1-shaped set")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -221,12 +223,155 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
 
+    if not args.no_recall:
+        result["graph_recall"] = recall_leg(args.recall_rows, dev, check=not args.no_cpu_baseline)
+        torch.cuda.empty_cache()
+
     if not args.no_subtree:
         del out_ids, out_d, sq8, gids, lay
         torch.cuda.empty_cache()
         result["subtree"] = subtree_leg(args.subtree_rows, dev, check=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 128), dim=128, components=64,
+               sigma=0.3, r_max=64, search_runs=3, unit_norm=True):
+    """C1-shaped end-to-end graph build on the GPU and its recall@10: rows x
+    128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) ->
+    SQ8 -> one subtree task (partition, leaves <= 1024, fanout 2, k = 32
+    leaf top-k) -> edge records (12-bit hashes from 12 uniform [-1, 1)
+    hyperplane sketches) -> HashPrune reservoirs (l_max = R = 64) -> the
+    `_mem.index` image; then greedy search of nq held-out queries (seed 1)
+    from the medoid at each L, recall@10 against exact f64 ground truth.
+    The first 64 queries at L = 64 are checked bit for bit against the
+    oracle's search over the same graph."""
+    import torch
+
+    from shear_amd import datagen
+    from shear_amd import edges as E
+    from shear_amd import graph as G
+    from shear_amd import hashprune as H
+    from shear_amd import subtree as S
+    from shear_amd import tessa as T
+
+    x = datagen.gmm_torch(rows, dim, components, sigma, 0, device=dev, unit_norm=unit_norm)
+    q = datagen.gmm_queries_torch(nq, dim, components, sigma, 0, 1, device=dev, unit_norm=unit_norm)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    planes = torch.rand((12, dim), generator=gen, device=dev) * 2.0 - 1.0
+    gids = torch.arange(rows, dtype=torch.int32, device=dev)
+    params = S.PiPNNSubtreeParams(leaf_knn=32, c_max=1024, fanout_second=2, psamp_fraction=0.001, max_leaders=128,
+                                  random_seed=42, max_depth=16)
+    req = S.GpuSubtreePartitionRequest(point_ids=np.arange(rows, dtype=np.uint32), parent_points=rows,
+                                       min_recurse_size=64)
+    torch.cuda.synchronize()
+    stages = {}
+    w0 = time.perf_counter()
+    sq8 = T.quantize_sq_int8_matrix(x)
+    sess = S.SubtreeSession(0)
+    sess.upload_device(sq8, gids)
+    out = sess.run(req, params)
+    sketches = x @ planes.t()
+    lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count].to(torch.int64),
+                        out.leaf_sizes[: out.leaf_count].to(torch.int32),
+                        (out.leaf_starts[: out.leaf_count] * out.k).to(torch.int64),
+                        int(out.leaf_sizes[: out.leaf_count].max().item()), out.leaf_rows * out.k)
+    torch.cuda.synchronize()
+    w1 = time.perf_counter()
+    rec, cnt = E.emit_edge_records(gids, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
+    w2 = time.perf_counter()
+    hp = H.HashPruneReducer(rows, r_max, dev)
+    hp.insert(rec, cnt)
+    targets, counts = hp.neighbors()
+    torch.cuda.synchronize()
+    w3 = time.perf_counter()
+    centroid = x.double().mean(0)
+    start = int(torch.argmin(((x.double() - centroid) ** 2).sum(1)).item())
+    image = G.pack_mem_index(targets, counts, start)
+    torch.cuda.synchronize()
+    w4 = time.perf_counter()
+    stages = {"quantize_partition_leaf_ms": round((w1 - w0) * 1e3, 2), "partition_ms": round(out.partition_ms, 2),
+              "leaf_ms": round(out.leaf_ms, 2), "edge_records_ms": round((w2 - w1) * 1e3, 2),
+              "hashprune_ms": round((w3 - w2) * 1e3, 2), "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}
+    build_s = w4 - w0
+    del rec, sess, out, lay, sketches
+    hp.close()
+    # exact ground truth in f64
+    xd, qd = x.double(), q.double()
+    dd = (qd * qd).sum(1, keepdim=True) - 2.0 * (qd @ xd.t()) + (xd * xd).sum(1)[None, :]
+    truth = torch.topk(dd, k_recall, dim=1, largest=False).indices.cpu().numpy()
+    del xd, qd, dd
+    searches = []
+    parity = {}
+    for L in search_l:
+        ms = []
+        for _ in range(search_runs + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            ids, dist, cmps = G.greedy_search(x, targets, counts, start, q, L, k_recall)
+            b.record()
+            b.synchronize()
+            ms.append(a.elapsed_time(b))
+        ms = ms[1:]
+        found = ids.cpu().numpy()
+        searches.append({"L": L, "recall_at_10": round(G.recall_at_k(found, truth, k_recall), 4),
+                         "ms": round(float(np.mean(ms)), 3), "qps": round(nq / (float(np.mean(ms)) / 1e3), 1),
+                         "mean_distance_evals": round(float(cmps.double().mean().item()) + 1.0, 1)})
+        if check and L == 64:
+            from oracle import pyoracle as orc
+
+            ns = 64
+            wi, wd, wc = orc.greedy_search(x.cpu().numpy(), targets.cpu().numpy().view(np.uint32),
+                                           counts.cpu().numpy(), start, q[:ns].cpu().numpy(), L, k_recall)
+            gi = ids[:ns].cpu().numpy().view(np.uint32)
+            gd = dist[:ns].cpu().numpy().view(np.uint32)
+            gc = cmps[:ns].cpu().numpy().view(np.uint32)
+            bad = np.nonzero(np.any(gi != wi, 1) | np.any(gd != wd.view(np.uint32), 1) | (gc != wc))[0]
+            parity = {"queries": ns, "L": L, "mismatched_queries": int(len(bad)), "bit_exact": len(bad) == 0}
+    deg = counts.double()
+    # graph diagnostics: points reachable from the start (breadth-first over
+    # the rows) and, for 2000 sample points, the share of their exact 10
+    # nearest neighbours their own row lists
+    valid = torch.arange(r_max, device=dev)[None, :] < counts[:, None]
+    seen = torch.zeros(rows, dtype=torch.bool, device=dev)
+    seen[start] = True
+    frontier = torch.tensor([start], device=dev)
+    hops = 0
+    while frontier.numel():
+        nb = targets[frontier][valid[frontier]].long()
+        nb = torch.unique(nb[~seen[nb]])
+        seen[nb] = True
+        frontier = nb
+        hops += 1
+    sample = torch.arange(0, rows, rows // 2000, device=dev)[:2000]
+    xs = x[sample].double()
+    ds = (xs * xs).sum(1, keepdim=True) - 2.0 * (xs @ x.double().t()) + (x.double() ** 2).sum(1)[None, :]
+    ds[torch.arange(len(sample), device=dev), sample] = float("inf")  # not itself
+    nn10 = torch.topk(ds, 10, dim=1, largest=False).indices
+    rows_s = torch.where(valid[sample], targets[sample].long(), -1)
+    row_recall = (nn10[:, :, None] == rows_s[:, None, :]).any(2).double().mean().item()
+    del xs, ds
+    res = {
+        "workload": f"C1-shaped build: {rows} x {dim} f32 (64-comp GMM sigma 0.3, unit-norm, seed 0), SQ8, one "
+                    f"subtree task (leaves <= 1024, fanout 2, k=32), 12-bit HashPrune l_max={r_max}; {nq} "
+                    f"held-out queries (seed 1), start = medoid",
+        "build_ms": round(build_s * 1e3, 2),
+        "points_per_s": round(rows / build_s, 1),
+        "stages": stages,
+        "graph_bytes": int(image.numel()),
+        "mean_degree": round(float(deg.mean().item()), 2),
+        "max_degree": int(counts.max().item()),
+        "start": start,
+        "reachable_from_start": int(seen.sum().item()),
+        "bfs_levels": hops,
+        "row_recall_at_10": round(row_recall, 4),
+        "search": searches,
+        "search_parity_sample": parity,
+    }
+    log(f"recall leg: build {build_s * 1e3:.1f} ms, " +
+        ", ".join(f"L={s['L']} recall@10 {s['recall_at_10']}" for s in searches))
+    return res
 
 
 def subtree_leg(rows, dev, check=True, runs=2):

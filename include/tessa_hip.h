@@ -449,6 +449,24 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
                               uint32_t row_stride, uint32_t start, uint64_t num_frozen_pts, void *out,
                               uint64_t out_capacity, uint64_t *index_size, void *stream);
 
+/* ---- greedy search: the recall harness ---------------------------------------
+ * InmemIndex::search (index/inmem_index/inmem_index.rs:523-590) over a
+ * neighbour table (row p = targets[p * row_stride .. + counts[p]], ids >=
+ * num_points skipped): greedy_search (algorithm/search/search.rs:137-233) from
+ * `start` with the capacity-L queue of neighbor_priority_queue.rs:50-85,
+ * ordered by (distance, id); per query the first K entries.  Distances are
+ * squared L2 over f32 vectors, summed in coordinate order without
+ * contraction.  Outputs, row-major [num_queries x K]: out_ids (0xFFFFFFFF
+ * past the list's end), out_dists (may be NULL); out_cmps [num_queries]
+ * distance evaluations after the start's (may be NULL).  L in [1, 256], K in
+ * [1, L] (K > L: the reference's "Set L: .. to a value of at least K: .."),
+ * start < num_points < 0xFFFFFFFF, finite data.  Device pointers; enqueued
+ * on `stream`; workspace: up to 1 GiB of visited tags. */
+tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
+                                const uint32_t *counts, uint32_t row_stride, uint32_t start, const float *queries,
+                                uint32_t num_queries, uint32_t L, uint32_t K, uint32_t *out_ids, float *out_dists,
+                                uint32_t *out_cmps, void *stream);
+
 /* ---- asynchronous subtree submissions ----------------------------------
  * Replaces submit_owned_quantized_subtree_l2_compact_topk
  * (compute_backend.rs:3807-3815) with its Deferred result and pinned host-slot

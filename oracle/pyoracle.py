@@ -85,6 +85,9 @@ def lib():
                                                            C.c_size_t, C.c_uint, P, C.c_size_t, P]
         _lib.orc_hashprune_reduce.restype = C.c_int
         _lib.orc_hashprune_reduce.argtypes = [C.c_size_t, C.c_size_t, P, C.c_size_t, P, P, P, P, P]
+        _lib.orc_greedy_search.restype = C.c_int
+        _lib.orc_greedy_search.argtypes = [P, C.c_size_t, C.c_size_t, P, P, C.c_size_t, C.c_uint32, P, C.c_size_t,
+                                           C.c_size_t, C.c_size_t, P, P, P]
     return _lib
 
 
@@ -373,3 +376,24 @@ def graph_bytes(start: int, num_frozen: int, rows) -> bytes:
     max_degree = max((len(r) for r in rows), default=0)
     head = np.array([(24 + len(body), max_degree, start, num_frozen)], dtype=np.dtype("<u8,<u4,<u4,<u8")).tobytes()
     return head + body
+
+
+def greedy_search(data: np.ndarray, targets: np.ndarray, counts: np.ndarray, start: int, queries: np.ndarray,
+                  L: int, K: int):
+    """Greedy search over the neighbour table (targets u32 [n, row_stride],
+    counts [n]) from `start` with search list L (algorithm/search/search.rs:137-233):
+    (ids u32 [q, K], squared-L2 f32 [q, K], distance evaluations u32 [q])."""
+    x = np.ascontiguousarray(data, np.float32)
+    t = np.ascontiguousarray(targets).view(np.uint32) if np.asarray(targets).dtype.itemsize == 4 else None
+    if t is None or t.ndim != 2:
+        raise ValueError("targets must be a 4-byte [n, row_stride] array")
+    c = np.ascontiguousarray(counts).astype(np.uint32)
+    q = np.ascontiguousarray(queries, np.float32).reshape(-1, x.shape[1])
+    ids = np.zeros((len(q), K), np.uint32)
+    d = np.zeros((len(q), K), np.float32)
+    cmps = np.zeros(len(q), np.uint32)
+    rc = lib().orc_greedy_search(_p(x), x.shape[0], x.shape[1], _p(t), _p(c), t.shape[1], start, _p(q), len(q), L, K,
+                                 _p(ids), _p(d), _p(cmps))
+    if rc != 0:
+        raise ValueError(f"orc_greedy_search: {rc}")
+    return ids, d, cmps

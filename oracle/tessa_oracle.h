@@ -36,6 +36,11 @@
  *                         cycle); brute force: the l_max best (dist, target, hash)
  *                         among each hash's best candidate, listed by ascending hash;
  *                         invariance under every shuffle of the record stream.
+ *   orc_greedy_search     brute force: on a complete graph (every point lists every
+ *                         other) with L >= n the search visits everything and
+ *                         returns the exact K nearest; the neighbour-queue rules
+ *                         (full-list rejection, cursor rewind on an insert in front
+ *                         of it) on hand-built graphs whose search is worked by hand.
  */
 #ifndef TESSA_ORACLE_H
 #define TESSA_ORACLE_H
@@ -264,6 +269,17 @@ long long orc_flush_compact_topk_into_edges(const uint32_t *point_ids, size_t ro
 int orc_hashprune_reduce(size_t num_points, size_t l_max, const orc_edge_record *records, size_t count,
                          uint32_t *out_targets, uint16_t *out_hashes, float *out_dists, uint32_t *out_counts,
                          uint32_t *bad_record);
+
+/* Greedy search of a [num_points x row_stride] neighbour table (row p =
+ * targets[p*row_stride .. + counts[p]]) over f32 vectors, search list L,
+ * from `start` (algorithm/search/search.rs:137-233 with the capacity-L
+ * neighbour queue, model/neighbor/neighbor_priority_queue.rs:50-85): per
+ * query the first K entries (ids, squared L2), 0xFFFFFFFF past the list, and
+ * the number of distance evaluations.  Returns 0, -1 on bad arguments. */
+int orc_greedy_search(const float *data, size_t num_points, size_t dim, const uint32_t *targets,
+                      const uint32_t *counts, size_t row_stride, uint32_t start, const float *queries,
+                      size_t num_queries, size_t L, size_t K, uint32_t *out_ids, float *out_dists,
+                      uint32_t *out_cmps);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@
 #include "hashprune_kernels.h"
 #include "leaf_kernels.h"
 #include "partition.h"
+#include "search_kernels.h"
 #include "tessa_device.h"
 
 
@@ -87,6 +88,9 @@ struct DeviceWorkspace {
     uint64_t graph_row_off_capacity = 0;
     uint64_t *graph_scalars = nullptr;
     uint64_t graph_scalars_capacity = 0;
+    // greedy search: visited tags, slots x points
+    uint32_t *search_tags = nullptr;
+    uint64_t search_tags_capacity = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
@@ -1610,6 +1614,49 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
     if (reinterpret_cast<uintptr_t>(out) % 8 != 0)
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph pack: output must be 8-byte aligned");
     if (tessa::launch_graph_pack(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph pack launch failed");
+    return ok_status();
+}
+
+tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
+                                const uint32_t *counts, uint32_t row_stride, uint32_t start, const float *queries,
+                                uint32_t num_queries, uint32_t L, uint32_t K, uint32_t *out_ids, float *out_dists,
+                                uint32_t *out_cmps, void *stream) {
+    if (K > L)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "Set L: %u to a value of at least K: %u", L, K);
+    if (L == 0 || K == 0 || L > tessa::kSearchMaxL)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: L=%u, K=%u outside 1 <= K <= L <= %u", L,
+                           K, tessa::kSearchMaxL);
+    if (num_points == 0 || num_points == 0xFFFFFFFFu || start >= num_points || dim == 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: start %u, %u points of dim %u", start,
+                           num_points, dim);
+    if (num_queries == 0) return ok_status();
+    if (!data || !counts || (row_stride && !targets) || !queries || !out_ids)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: null pointer");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    DeviceWorkspace *ws = nullptr;
+    tessa_status st = device_workspace(&ws);
+    if (st.code) return st;
+    tessa::GraphSearchParams p{};
+    p.slots = tessa::search_slots(num_points, num_queries);
+    st = grow(&ws->search_tags, &ws->search_tags_capacity, (uint64_t)p.slots * num_points, sizeof(uint32_t),
+              "search visited tags");
+    if (st.code) return st;
+    p.data = data;
+    p.num_points = num_points;
+    p.dim = dim;
+    p.targets = targets;
+    p.counts = counts;
+    p.row_stride = row_stride;
+    p.start = start;
+    p.queries = queries;
+    p.num_queries = num_queries;
+    p.L = L;
+    p.K = K;
+    p.out_ids = out_ids;
+    p.out_dists = out_dists;
+    p.out_cmps = out_cmps;
+    p.tags = ws->search_tags;
+    if (tessa::launch_graph_search(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph search launch failed");
     return ok_status();
 }
 

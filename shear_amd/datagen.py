@@ -50,6 +50,25 @@ def gmm_torch(n: int, dim: int, components: int, sigma: float, seed: int, device
     return out
 
 
+
+def gmm_queries_torch(nq: int, dim: int, components: int, sigma: float, seed: int, query_seed: int,
+                      device="cuda", unit_norm: bool = True):
+    """Held-out queries from the mixture gmm_torch(seed) draws: the same
+    component centres, components picked uniformly and noise drawn from a
+    separate generator (query_seed)."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    centers = torch.randn((components, dim), generator=g, device=device, dtype=torch.float32)
+    gq = torch.Generator(device=device)
+    gq.manual_seed(query_seed)
+    comp = torch.randint(0, components, (nq,), generator=gq, device=device)
+    q = centers[comp] + sigma * torch.randn((nq, dim), generator=gq, device=device)
+    if unit_norm:
+        q = q / torch.linalg.vector_norm(q, dim=1, keepdim=True)
+    return q
+
 def c3_torch(n: int, dim: int = 768, components: int = 1000, sigma: float = 0.25, outlier_frac: float = 0.05,
              seed: int = 2, device="cuda", chunk_rows: int = 1 << 18):
     """Mixture rows (component centres ~N(0, I), sigma noise) with a fraction of

@@ -1,4 +1,5 @@
-"""Graph emission: the `_mem.index` file of a neighbour table, packed on the GPU.
+"""Graph emission and the recall harness: the `_mem.index` file of a
+neighbour table, packed on the GPU, and greedy search over it.
 
 Host mirror of DirectMemGraphWriter (shear-core/src/index/inmem_index/
 pipnn_oom_writer.rs:23-72): ``write_mem_index`` writes what create +
@@ -6,6 +7,11 @@ write_node (per point, id order) + finish write; the byte image itself is
 built by ``tessa_graph_pack`` in libtessa_hip.so.  ``read_mem_index`` parses
 the same layout back (header: index_size u64, max_degree u32, start u32,
 num_frozen_pts u64; rows: degree u32 then ids, little-endian).
+
+``greedy_search`` is InmemIndex::search (shear-core/src/index/inmem_index/
+inmem_index.rs:523-590, greedy_search algorithm/search/search.rs:137-233) run
+by ``tessa_graph_search``, one wavefront per query; ``recall_at_k`` is the
+search app's recall (apps/search_shear_index/src/main.rs:388-413).
 """
 from __future__ import annotations
 
@@ -63,3 +69,38 @@ def read_mem_index(src):
     if i != len(words):
         raise ValueError("truncated row")
     return int(start), int(frozen), int(max_degree), rows
+
+
+def greedy_search(data: torch.Tensor, targets: torch.Tensor, counts: torch.Tensor, start: int,
+                  queries: torch.Tensor, L: int, K: int, stream: torch.cuda.Stream | None = None):
+    """(ids int32 [q, K] (-1 past the list), squared-L2 f32 [q, K], distance
+    evaluations int32 [q]) of the greedy search from ``start`` with list size L.
+    ``data`` f32 [n, dim], ``targets`` int32 [n, row_stride], ``counts`` int32 [n],
+    ``queries`` f32 [q, dim], all on the GPU."""
+    if data.dim() != 2 or data.dtype != torch.float32 or queries.dtype != torch.float32:
+        raise ValueError("data and queries must be f32 [n, dim] / [q, dim]")
+    if targets.dim() != 2 or targets.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise ValueError("targets must be int32 [num_points, row_stride] and counts int32 [num_points]")
+    n, dim = data.shape
+    q = queries.reshape(-1, dim).contiguous()
+    x, t = data.contiguous(), targets.contiguous()
+    if t.shape[0] != n or counts.numel() != n:
+        raise ValueError(f"neighbour table of {t.shape[0]} rows / {counts.numel()} counts for {n} points")
+    ids = torch.empty((q.shape[0], K), dtype=torch.int32, device=x.device)
+    d = torch.empty((q.shape[0], K), dtype=torch.float32, device=x.device)
+    cmps = torch.empty(q.shape[0], dtype=torch.int32, device=x.device)
+    N.check(N.load().tessa_graph_search(_ptr(x), n, dim, _ptr(t), _ptr(counts), t.shape[1], start, _ptr(q), q.shape[0],
+                                        L, K, _ptr(ids), _ptr(d), _ptr(cmps), _stream_ptr(stream)), "graph search")
+    return ids, d, cmps
+
+
+def recall_at_k(found: np.ndarray, truth: np.ndarray, k: int) -> float:
+    """Mean over queries of (results of the query found among the first k
+    ground-truth ids) / k (apps/search_shear_index/src/main.rs:388-411)."""
+    f = np.asarray(found)
+    g = np.asarray(truth)[:, :k]
+    total = 0.0
+    for a, b in zip(f, g):
+        gt = set(b.tolist())
+        total += sum(1 for i in a.tolist() if i in gt) / k
+    return total / len(f) if len(f) else 0.0
