@@ -224,7 +224,11 @@ def main() -> int:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
 
     if not args.no_recall:
-        result["graph_recall"] = recall_leg(args.recall_rows, dev, check=not args.no_cpu_baseline)
+        # the C1 mixture as specified (sigma 0.3: 64 well-separated clusters) and
+        # an overlapping one (sigma 2.0) on which graph connectivity is not
+        # decided by the data alone
+        result["graph_recall"] = [recall_leg(args.recall_rows, dev, check=not args.no_cpu_baseline),
+                                  recall_leg(args.recall_rows, dev, check=False, sigma=2.0)]
         torch.cuda.empty_cache()
 
     if not args.no_subtree:
@@ -236,18 +240,20 @@ def main() -> int:
 
 
 def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 128), dim=128, components=64,
-               sigma=0.3, r_max=64, search_runs=3, unit_norm=True):
+               sigma=0.3, r_max=64, search_runs=3, unit_norm=True, fanout_top=10):
     """C1-shaped end-to-end graph build on the GPU and its recall@10: rows x
-    128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) ->
-    SQ8 -> one subtree task (partition, leaves <= 1024, fanout 2, k = 32
-    leaf top-k) -> edge records (12-bit hashes from 12 uniform [-1, 1)
-    hyperplane sketches) -> HashPrune reservoirs (l_max = R = 64) -> the
-    `_mem.index` image; then greedy search of nq held-out queries (seed 1)
-    from the medoid at each L, recall@10 against exact f64 ground truth.
-    The first 64 queries at L = 64 are checked bit for bit against the
-    oracle's search over the same graph."""
+    128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) -> SQ8
+    -> global D0 assignment (rows * 0.0007 leaders, each point to its
+    fanout_top = 10 nearest) -> one subtree task per D0 child (depth 1:
+    fanout 3 at its root, leaves <= 1024, k = 32 leaf top-k) -> edge records
+    (12-bit hashes from 12 uniform [-1, 1) hyperplane sketches) -> HashPrune
+    reservoirs (l_max = R = 64) -> the `_mem.index` image; then greedy search
+    of nq held-out queries (seed 1) from the medoid at each L, recall@10
+    against exact f64 ground truth.  The first 64 queries at L = 64 are
+    checked bit for bit against the oracle's search over the same graph."""
     import torch
 
+    from shear_amd import d0 as D
     from shear_amd import datagen
     from shear_amd import edges as E
     from shear_amd import graph as G
@@ -261,28 +267,47 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     gen.manual_seed(42)
     planes = torch.rand((12, dim), generator=gen, device=dev) * 2.0 - 1.0
     gids = torch.arange(rows, dtype=torch.int32, device=dev)
-    params = S.PiPNNSubtreeParams(leaf_knn=32, c_max=1024, fanout_second=2, psamp_fraction=0.001, max_leaders=128,
+    params = S.PiPNNSubtreeParams(leaf_knn=32, c_max=1024, fanout_second=3, psamp_fraction=0.001, max_leaders=128,
                                   random_seed=42, max_depth=16)
-    req = S.GpuSubtreePartitionRequest(point_ids=np.arange(rows, dtype=np.uint32), parent_points=rows,
-                                       min_recurse_size=64)
+    nl = D.d0_leader_count(rows)
+    lrows = D.sample_leader_rows(rows, nl, 42, dev)
     torch.cuda.synchronize()
-    stages = {}
     w0 = time.perf_counter()
     sq8 = T.quantize_sq_int8_matrix(x)
-    sess = S.SubtreeSession(0)
-    sess.upload_device(sq8, gids)
-    out = sess.run(req, params)
     sketches = x @ planes.t()
-    lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count].to(torch.int64),
-                        out.leaf_sizes[: out.leaf_count].to(torch.int32),
-                        (out.leaf_starts[: out.leaf_count] * out.k).to(torch.int64),
-                        int(out.leaf_sizes[: out.leaf_count].max().item()), out.leaf_rows * out.k)
+    lead = T.Sq8Matrix(sq8.codes[lrows].contiguous(), sq8.scales[lrows].contiguous(), sq8.norms[lrows].contiguous(),
+                       sq8.dim)
+    _, _, offs, pts = D.global_d0_assign(sq8, gids, lead, gids[lrows].contiguous(), fanout_top)
+    offs_h = offs.cpu().numpy()
     torch.cuda.synchronize()
     w1 = time.perf_counter()
-    rec, cnt = E.emit_edge_records(gids, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
-    w2 = time.perf_counter()
+    sess = S.SubtreeSession(0)
     hp = H.HashPruneReducer(rows, r_max, dev)
-    hp.insert(rec, cnt)
+    part_ms = leaf_ms = 0.0
+    records = leaves = leaf_rows = 0
+    for c in range(nl):
+        a, b = int(offs_h[c]), int(offs_h[c + 1])
+        if b - a < 2:
+            continue
+        cg = pts[a:b]
+        ci = cg.long()
+        sub = T.Sq8Matrix(sq8.codes[ci].contiguous(), sq8.scales[ci].contiguous(), sq8.norms[ci].contiguous(), sq8.dim)
+        sess.upload_device(sub, cg)
+        req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
+                                           min_recurse_size=64)
+        out = sess.run(req, params)
+        part_ms += out.partition_ms
+        leaf_ms += out.leaf_ms
+        lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count].to(torch.int64),
+                            out.leaf_sizes[: out.leaf_count].to(torch.int32),
+                            (out.leaf_starts[: out.leaf_count] * out.k).to(torch.int64),
+                            int(out.leaf_sizes[: out.leaf_count].max().item()), out.leaf_rows * out.k)
+        rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
+        hp.insert(rec, cnt)
+        records += int(cnt)
+        leaves += out.leaf_count
+        leaf_rows += out.leaf_rows
+        del rec, out, lay, sub
     targets, counts = hp.neighbors()
     torch.cuda.synchronize()
     w3 = time.perf_counter()
@@ -291,11 +316,12 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
     w4 = time.perf_counter()
-    stages = {"quantize_partition_leaf_ms": round((w1 - w0) * 1e3, 2), "partition_ms": round(out.partition_ms, 2),
-              "leaf_ms": round(out.leaf_ms, 2), "edge_records_ms": round((w2 - w1) * 1e3, 2),
-              "hashprune_ms": round((w3 - w2) * 1e3, 2), "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}
+    stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": nl, "d0_fanout_top": fanout_top,
+              "children_wall_ms": round((w3 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
+              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
+              "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}
     build_s = w4 - w0
-    del rec, sess, out, lay, sketches
+    del sess, sketches, pts, offs
     hp.close()
     # exact ground truth in f64
     xd, qd = x.double(), q.double()
@@ -353,9 +379,10 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     row_recall = (nn10[:, :, None] == rows_s[:, None, :]).any(2).double().mean().item()
     del xs, ds
     res = {
-        "workload": f"C1-shaped build: {rows} x {dim} f32 (64-comp GMM sigma 0.3, unit-norm, seed 0), SQ8, one "
-                    f"subtree task (leaves <= 1024, fanout 2, k=32), 12-bit HashPrune l_max={r_max}; {nq} "
-                    f"held-out queries (seed 1), start = medoid",
+        "workload": f"C1-shaped build: {rows} x {dim} f32 (64-comp GMM sigma {sigma}, unit-norm, seed 0), SQ8, "
+                    f"global D0 ({nl} leaders, fanout_top {fanout_top}), a subtree per D0 child (root fanout 3, "
+                    f"leaves <= 1024, k=32), 12-bit HashPrune l_max={r_max}; {nq} held-out queries (seed 1), "
+                    f"start = medoid",
         "build_ms": round(build_s * 1e3, 2),
         "points_per_s": round(rows / build_s, 1),
         "stages": stages,

@@ -449,6 +449,29 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
                               uint32_t row_stride, uint32_t start, uint64_t num_frozen_pts, void *out,
                               uint64_t out_capacity, uint64_t *index_size, void *stream);
 
+/* ---- global D0 assignment: task formation above the subtrees --------------
+ * The GPU-D0 SQ8 assignment (shear-core/src/algorithm/pipnn/compute_backend.rs:
+ * sq8_global_d0_*_partial_kernel :18016-18275 + the tile merge :18446-18511;
+ * CPU statement quantize_sq8_and_assign_global_d0_reference,
+ * dco_sq_int8.rs:1929-2064): every SQ8 row to its fanout_top nearest leaders
+ * by sq_int8_approx_l2 (dco_sq_int8.rs:2950-2965), ordered by (distance,
+ * leader global id).  Outputs row-major [rows x fanout_top] fragments:
+ * out_child (leader index = D0 child), out_point (the row's global id).  With
+ * child_offsets [leader_count + 1] and child_points [rows * fanout_top] (both
+ * or neither) the fragments are also grouped by child, rows ascending within
+ * a child (the D0 children's point lists).  Leader payload: SQ8 codes /
+ * scales / norms of the leaders (same padded_dim) and their global ids.
+ * fanout_top in [1, min(32, leader_count)] (the reference's "SQ GPU-D0 staging
+ * fanout must be in 1..=min(32, leaders)"); padded_dim a multiple of 16 up to
+ * 1024; rows * fanout_top < 2^31 when grouping.  Device pointers; enqueued on
+ * `stream`. */
+tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, const float *norms,
+                                    const uint32_t *global_ids, uint64_t rows, uint32_t padded_dim,
+                                    const int8_t *leader_codes, const float *leader_scales,
+                                    const float *leader_norms, const uint32_t *leader_ids, uint32_t leader_count,
+                                    uint32_t fanout_top, uint32_t *out_child, uint32_t *out_point,
+                                    uint64_t *child_offsets, uint32_t *child_points, void *stream);
+
 /* ---- greedy search: the recall harness ---------------------------------------
  * InmemIndex::search (index/inmem_index/inmem_index.rs:523-590) over a
  * neighbour table (row p = targets[p * row_stride .. + counts[p]], ids >=

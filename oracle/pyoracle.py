@@ -85,6 +85,9 @@ def lib():
                                                            C.c_size_t, C.c_uint, P, C.c_size_t, P]
         _lib.orc_hashprune_reduce.restype = C.c_int
         _lib.orc_hashprune_reduce.argtypes = [C.c_size_t, C.c_size_t, P, C.c_size_t, P, P, P, P, P]
+        _lib.orc_d0_assign.restype = C.c_int
+        _lib.orc_d0_assign.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, C.c_size_t, C.c_size_t, P, P,
+                                       P, P]
         _lib.orc_greedy_search.restype = C.c_int
         _lib.orc_greedy_search.argtypes = [P, C.c_size_t, C.c_size_t, P, P, C.c_size_t, C.c_uint32, P, C.c_size_t,
                                            C.c_size_t, C.c_size_t, P, P, P]
@@ -397,3 +400,26 @@ def greedy_search(data: np.ndarray, targets: np.ndarray, counts: np.ndarray, sta
     if rc != 0:
         raise ValueError(f"orc_greedy_search: {rc}")
     return ids, d, cmps
+
+
+def d0_assign(codes, scales, norms, global_ids, leader_codes, leader_scales, leader_norms, leader_ids, fanout):
+    """Global D0 assignment (compute_backend.rs:18016-18511): (child u32 [rows, fanout]
+    leader indices, child_offsets u64 [leaders + 1], child_points u32 grouped by
+    child, rows ascending)."""
+    c = np.ascontiguousarray(codes, np.int8)
+    lc = np.ascontiguousarray(leader_codes, np.int8)
+    rows, pd = c.shape
+    nl = lc.shape[0]
+    s, n = np.ascontiguousarray(scales, np.float32), np.ascontiguousarray(norms, np.float32)
+    ls, ln = np.ascontiguousarray(leader_scales, np.float32), np.ascontiguousarray(leader_norms, np.float32)
+    g = np.ascontiguousarray(global_ids, np.uint32)
+    lid = np.ascontiguousarray(leader_ids, np.uint32)
+    child = np.zeros((rows, fanout), np.uint32)
+    point = np.zeros((rows, fanout), np.uint32)
+    offs = np.zeros(nl + 1, np.uint64)
+    pts = np.zeros(rows * fanout, np.uint32)
+    rc = lib().orc_d0_assign(_p(c), _p(s), _p(n), _p(g), rows, pd, _p(lc), _p(ls), _p(ln), _p(lid), nl, fanout,
+                             _p(child), _p(point), _p(offs), _p(pts))
+    if rc != 0:
+        raise ValueError(f"orc_d0_assign: {rc}")
+    return child, offs, pts

@@ -36,6 +36,10 @@
  *                         cycle); brute force: the l_max best (dist, target, hash)
  *                         among each hash's best candidate, listed by ascending hash;
  *                         invariance under every shuffle of the record stream.
+ *   orc_d0_assign         brute force in f64 on well-separated distances, a row's own
+ *                         leader first, ties by leader id on duplicated leaders,
+ *                         fanout = leader count giving the full order, the grouping
+ *                         against a sort of the fragments.
  *   orc_greedy_search     brute force: on a complete graph (every point lists every
  *                         other) with L >= n the search visits everything and
  *                         returns the exact K nearest; the neighbour-queue rules
@@ -280,6 +284,17 @@ int orc_greedy_search(const float *data, size_t num_points, size_t dim, const ui
                       const uint32_t *counts, size_t row_stride, uint32_t start, const float *queries,
                       size_t num_queries, size_t L, size_t K, uint32_t *out_ids, float *out_dists,
                       uint32_t *out_cmps);
+
+/* Global D0 assignment (GPU path, compute_backend.rs:18016-18511; distance
+ * dco_sq_int8.rs:2950-2965): each row's fanout_top (<= 32) nearest leaders
+ * by (dist, leader id) as row-major fragments (out_child = leader index,
+ * out_point = global id) and, when child_offsets is given, the fragments
+ * grouped by child (child_offsets [leader_count + 1], child_points [rows *
+ * fanout], rows ascending within a child).  Returns 0, -1 on bad fanout. */
+int orc_d0_assign(const int8_t *codes, const float *scales, const float *norms, const uint32_t *global_ids,
+                  size_t rows, size_t padded_dim, const int8_t *leader_codes, const float *leader_scales,
+                  const float *leader_norms, const uint32_t *leader_ids, size_t leader_count, size_t fanout,
+                  uint32_t *out_child, uint32_t *out_point, uint64_t *child_offsets, uint32_t *child_points);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,229 @@
+// d0_assign.hip -- global D0 assignment on gfx950 int8 MFMA: every SQ8 row
+// to its fanout_top (<= 32) nearest global D0 leaders, then the fragments
+// grouped into the D0 children.
+//
+// Reference (shear-core/src/algorithm/pipnn/compute_backend.rs): the GPU-D0
+// kernels sq8_global_d0_tiled_partial_kernel / sq8_global_d0_wmma_partial_kernel
+// (:18016-18275, per leader tile the best partial_r leaders of each row) and
+// the merge rabitq_residual_global_d0_tiled_merge_kernel (:18446-18511, the
+// best fanout_top over the tiles), both ordered by (dist, leader global id)
+// strictly, the distance sq_int8_approx_l2 (dco_sq_int8.rs:2950-2965):
+// (norm_r + norm_l) - ((2 * scale_r) * scale_l) * dot, clamped at 0.  Output
+// fragments row-major (child = leader index, point = global id, :18503-18510).
+//
+// Here one pass replaces partial + merge: a wave holds 32 rows' codes in VGPRs
+// as the MFMA B operand and streams the leaders 32 at a time as A (codes read
+// from L2: a leader tile is shared by every wave); each lane owns one row and
+// half of a tile's leaders and keeps its best F >= fanout (distance bits << 32
+// | leader rank) keys sorted in registers, inserting a candidate only when it
+// beats the current F-th.  The two halves of a row merge at the end.  A
+// leader's rank is its position in (leader id, index) order, so the key's
+// integer order is the reference's order (distances are >= 0).
+//
+// Grouping: an LSD radix sort of (child, point) pairs by child, stable, so a
+// child's points keep ascending row order; offsets from a child histogram.
+#include <hipcub/hipcub.hpp>
+
+#include "d0_kernels.h"
+#include "tessa_device.h"
+
+namespace tessa {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr uint64_t kNoKey = ~0ull;
+
+// rank of each leader in (id, index) order; O(leaders^2) compares, leaders are few
+__global__ void d0_rank_kernel(const uint32_t *ids, uint32_t n, uint32_t *rank, uint32_t *inv) {
+    const uint32_t l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= n) return;
+    const uint32_t me = ids[l];
+    uint32_t r = 0;
+    for (uint32_t o = 0; o < n; ++o) {
+        const uint32_t v = ids[o];
+        r += (v < me || (v == me && o < l)) ? 1u : 0u;
+    }
+    rank[l] = r;
+    inv[r] = l;
+}
+
+template <int F>
+__device__ __forceinline__ void insert_key(uint64_t (&best)[F], uint64_t key) {
+#pragma unroll
+    for (int s = 0; s < F; ++s) {
+        const uint64_t b = best[s];
+        const bool lt = key < b;
+        best[s] = lt ? key : b;
+        key = lt ? b : key;
+    }
+}
+
+template <int KS, int F>
+__global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t j = lane & 31u, h = lane >> 5;
+    const uint64_t row = (uint64_t)blockIdx.x * (kWaves * 32) + wave * 32u + j;
+    const bool ok = row < p.rows;
+    const uint32_t pd = p.padded_dim;
+
+    v4i bfrag[KS];
+    const int8_t *rc = p.codes + (ok ? row : 0ull) * pd;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const uint32_t off = 32u * s + 16u * h;
+        v4i z = {0, 0, 0, 0};
+        if (ok && off < pd) z = *reinterpret_cast<const v4i *>(rc + off);
+        bfrag[s] = z;
+    }
+    const float rs = ok ? p.scales[row] : 0.0f;
+    const float rn = ok ? p.norms[row] : 0.0f;
+
+    uint64_t best[F];
+#pragma unroll
+    for (int s = 0; s < F; ++s) best[s] = kNoKey;
+
+    const uint32_t ntiles = (p.leaders + 31u) / 32u;
+    for (uint32_t t = 0; t < ntiles; ++t) {
+        const uint32_t la = 32u * t + j;  // this lane's A row (leader)
+        const int8_t *lc = p.leader_codes + (uint64_t)(la < p.leaders ? la : 0u) * pd;
+        v16i acc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const uint32_t off = 32u * s + 16u * h;
+            v4i a = {0, 0, 0, 0};
+            if (la < p.leaders && off < pd) a = *reinterpret_cast<const v4i *>(lc + off);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t l = 32u * t + 8u * (v / 4) + 4u * h + (v % 4);
+            const bool live = ok && l < p.leaders;
+            const uint32_t li = live ? l : 0u;
+            const float d = assign_l2(acc[v], rs, rn, p.leader_scales[li], p.leader_norms[li]);
+            const uint64_t key = live ? (((uint64_t)__float_as_uint(d) << 32) | p.leader_rank[li]) : kNoKey;
+            if (key < best[F - 1]) insert_key<F>(best, key);
+        }
+    }
+    // merge the other half-wave's list into lanes 0..31
+#pragma unroll
+    for (int s = 0; s < F; ++s) {
+        const uint64_t o = ((uint64_t)__shfl((uint32_t)(best[s] >> 32), j + 32u) << 32) |
+                           __shfl((uint32_t)best[s], j + 32u);
+        if (h == 0u && o < best[F - 1]) insert_key<F>(best, o);
+    }
+    if (h == 0u && ok) {
+        const uint32_t g = p.global_ids[row];
+#pragma unroll
+        for (int s = 0; s < F; ++s) {
+            if ((uint32_t)s < p.fanout) {
+                const uint32_t r = (uint32_t)best[s];  // always a real leader: fanout <= leaders
+                p.out_child[row * p.fanout + s] = r < p.leaders ? p.rank_leader[r] : kEmptyId;
+                p.out_point[row * p.fanout + s] = g;
+            }
+        }
+    }
+}
+
+template <int KS>
+int launch_ks(const D0AssignParams &p, hipStream_t stream) {
+    const uint64_t blocks = (p.rows + kWaves * 32 - 1) / (kWaves * 32);
+    if (blocks > 0x7fffffffull) return -2;
+    const dim3 grid((uint32_t)blocks), block(kThreads);
+    if (p.fanout <= 4) hipLaunchKernelGGL((d0_assign_kernel<KS, 4>), grid, block, 0, stream, p);
+    else if (p.fanout <= 8) hipLaunchKernelGGL((d0_assign_kernel<KS, 8>), grid, block, 0, stream, p);
+    else if (p.fanout <= 16) hipLaunchKernelGGL((d0_assign_kernel<KS, 16>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((d0_assign_kernel<KS, 32>), grid, block, 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+__global__ void d0_hist_kernel(const uint32_t *child, uint64_t n, uint64_t *counts) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        atomicAdd(reinterpret_cast<unsigned long long *>(&counts[child[i] + 1]), 1ull);
+}
+
+__global__ void d0_fill_zero(uint64_t *a, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        a[i] = 0ull;
+}
+
+// inclusive scan of counts[1..n] in place (one workgroup; n = leaders is small)
+__global__ __launch_bounds__(1024) void d0_scan_kernel(uint64_t *counts, uint32_t n) {
+    __shared__ uint64_t part[1024];
+    __shared__ uint64_t carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (uint32_t b = 0; b < n; b += 1024) {
+        const uint32_t i = b + threadIdx.x;
+        part[threadIdx.x] = i < n ? counts[i + 1] : 0ull;
+        __syncthreads();
+        for (uint32_t off = 1; off < 1024; off <<= 1) {
+            const uint64_t v = threadIdx.x >= off ? part[threadIdx.x - off] : 0ull;
+            __syncthreads();
+            part[threadIdx.x] += v;
+            __syncthreads();
+        }
+        if (i < n) counts[i + 1] = carry + part[threadIdx.x];
+        __syncthreads();
+        if (threadIdx.x == 0) carry += part[1023];
+        __syncthreads();
+    }
+}
+
+uint32_t key_bits(uint32_t leaders) {
+    uint32_t b = 1;
+    while (b < 32 && (1ull << b) < leaders) ++b;
+    return b;
+}
+
+}  // namespace
+
+int launch_d0_assign(const D0AssignParams &p, hipStream_t stream) {
+    if (p.fanout == 0 || p.fanout > kD0MaxFanout || p.fanout > p.leaders || p.padded_dim % 16 != 0) return -3;
+    hipLaunchKernelGGL(d0_rank_kernel, dim3((p.leaders + 255) / 256), dim3(256), 0, stream, p.leader_ids, p.leaders,
+                       p.leader_rank, p.rank_leader);
+    if (hipGetLastError() != hipSuccess) return -1;
+    if (p.rows == 0) return 0;
+    const uint32_t ks = (p.padded_dim + 31) / 32;
+    if (ks <= 4) return launch_ks<4>(p, stream);
+    if (ks <= 8) return launch_ks<8>(p, stream);
+    if (ks <= 16) return launch_ks<16>(p, stream);
+    if (ks <= 24) return launch_ks<24>(p, stream);
+    if (ks <= 32) return launch_ks<32>(p, stream);
+    return -3;
+}
+
+size_t d0_group_temp_bytes(uint64_t items, uint32_t leaders) {
+    size_t sort_bytes = 0;
+    hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+                                       (const uint32_t *)nullptr, (uint32_t *)nullptr, (int)items, 0,
+                                       (int)key_bits(leaders));
+    // sorted keys, then the sort's own storage (256-byte aligned)
+    return ((items * 4 + 255) / 256) * 256 + sort_bytes;
+}
+
+int launch_d0_group(const D0AssignParams &p, uint64_t *child_offsets, uint32_t *child_points, void *temp,
+                    size_t temp_bytes, hipStream_t stream) {
+    const uint64_t items = p.rows * p.fanout;
+    hipLaunchKernelGGL(d0_fill_zero, dim3(((uint64_t)p.leaders + 256) / 256), dim3(256), 0, stream, child_offsets,
+                       (uint64_t)p.leaders + 1);
+    if (items == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
+    uint64_t hg = (items + 255) / 256;
+    hg = hg > 8192 ? 8192 : hg;
+    hipLaunchKernelGGL(d0_hist_kernel, dim3((uint32_t)hg), dim3(256), 0, stream, p.out_child, items, child_offsets);
+    hipLaunchKernelGGL(d0_scan_kernel, dim3(1), dim3(1024), 0, stream, child_offsets, p.leaders);
+    const size_t keys_bytes = ((items * 4 + 255) / 256) * 256;
+    uint32_t *keys_out = reinterpret_cast<uint32_t *>(temp);
+    size_t sort_bytes = temp_bytes - keys_bytes;
+    if (hipcub::DeviceRadixSort::SortPairs(reinterpret_cast<char *>(temp) + keys_bytes, sort_bytes, p.out_child,
+                                           keys_out, p.out_point, child_points, (int)items, 0,
+                                           (int)key_bits(p.leaders), stream) != hipSuccess)
+        return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace tessa

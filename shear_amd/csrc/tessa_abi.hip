@@ -19,6 +19,7 @@
 
 #include "../../include/tessa_hip.h"
 #include "assign_kernels.h"
+#include "d0_kernels.h"
 #include "edge_kernels.h"
 #include "graph_kernels.h"
 #include "hashprune_kernels.h"
@@ -91,6 +92,11 @@ struct DeviceWorkspace {
     // greedy search: visited tags, slots x points
     uint32_t *search_tags = nullptr;
     uint64_t search_tags_capacity = 0;
+    // D0 assignment: leader ranks and their inverse, grouping scratch
+    uint32_t *d0_rank = nullptr;
+    uint64_t d0_rank_capacity = 0;
+    uint8_t *d0_temp = nullptr;
+    uint64_t d0_temp_capacity = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
@@ -1657,6 +1663,63 @@ tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t
     p.out_cmps = out_cmps;
     p.tags = ws->search_tags;
     if (tessa::launch_graph_search(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph search launch failed");
+    return ok_status();
+}
+
+tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, const float *norms,
+                                    const uint32_t *global_ids, uint64_t rows, uint32_t padded_dim,
+                                    const int8_t *leader_codes, const float *leader_scales,
+                                    const float *leader_norms, const uint32_t *leader_ids, uint32_t leader_count,
+                                    uint32_t fanout_top, uint32_t *out_child, uint32_t *out_point,
+                                    uint64_t *child_offsets, uint32_t *child_points, void *stream) {
+    if (leader_count == 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "SQ GPU-D0 staging requires at least one global D0 leader");
+    if (fanout_top == 0 || fanout_top > leader_count || fanout_top > tessa::kD0MaxFanout)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "SQ GPU-D0 staging fanout must be in 1..=min(32, leaders), got fanout=%u leaders=%u",
+                           fanout_top, leader_count);
+    if (leader_count > tessa::kD0MaxLeaders || padded_dim == 0 || padded_dim % 16 != 0 || padded_dim > 1024)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "D0 assign: %u leaders, padded_dim %u unsupported",
+                           leader_count, padded_dim);
+    if ((child_offsets == nullptr) != (child_points == nullptr))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "D0 assign: child_offsets and child_points go together");
+    const uint64_t items = rows * fanout_top;
+    if (child_offsets && items >= 0x7fffffffull)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "D0 assign: %llu fragments exceed one grouping pass",
+                           (unsigned long long)items);
+    if ((rows && (!codes || !scales || !norms || !global_ids || !out_child || !out_point)) || !leader_codes ||
+        !leader_scales || !leader_norms || !leader_ids)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "D0 assign: null pointer");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    DeviceWorkspace *ws = nullptr;
+    tessa_status st = device_workspace(&ws);
+    if (st.code) return st;
+    st = grow(&ws->d0_rank, &ws->d0_rank_capacity, 2ull * leader_count, sizeof(uint32_t), "D0 leader ranks");
+    if (st.code) return st;
+    tessa::D0AssignParams p{};
+    p.codes = codes;
+    p.scales = scales;
+    p.norms = norms;
+    p.global_ids = global_ids;
+    p.rows = rows;
+    p.padded_dim = padded_dim;
+    p.leader_codes = leader_codes;
+    p.leader_scales = leader_scales;
+    p.leader_norms = leader_norms;
+    p.leader_ids = leader_ids;
+    p.leaders = leader_count;
+    p.fanout = fanout_top;
+    p.leader_rank = ws->d0_rank;
+    p.rank_leader = ws->d0_rank + leader_count;
+    p.out_child = out_child;
+    p.out_point = out_point;
+    if (tessa::launch_d0_assign(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "D0 assign launch failed");
+    if (!child_offsets) return ok_status();
+    const size_t temp = tessa::d0_group_temp_bytes(items, leader_count);
+    st = grow(&ws->d0_temp, &ws->d0_temp_capacity, temp, 1, "D0 grouping scratch");
+    if (st.code) return st;
+    if (tessa::launch_d0_group(p, child_offsets, child_points, ws->d0_temp, ws->d0_temp_capacity, s) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "D0 grouping launch failed");
     return ok_status();
 }
 
