@@ -355,6 +355,20 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
             gc = cmps[:ns].cpu().numpy().view(np.uint32)
             bad = np.nonzero(np.any(gi != wi, 1) | np.any(gd != wd.view(np.uint32), 1) | (gc != wc))[0]
             parity = {"queries": ns, "L": L, "mismatched_queries": int(len(bad)), "bit_exact": len(bad) == 0}
+    # the reference's optional final RobustPrune (alpha 1.2, max_occlusion 750,
+    # degree 64) over the same rows, searched the same way
+    pa, pb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pa.record()
+    ptargets, pcounts = G.robust_prune(x, targets, counts)
+    pb.record()
+    pb.synchronize()
+    pruned = {"ms": round(pa.elapsed_time(pb), 3), "mean_degree": round(float(pcounts.double().mean().item()), 2),
+              "search": []}
+    for L in search_l:
+        ids, _, cmps = G.greedy_search(x, ptargets, pcounts, start, q, L, k_recall)
+        pruned["search"].append({"L": L, "recall_at_10": round(G.recall_at_k(ids.cpu().numpy(), truth, k_recall), 4),
+                                 "mean_distance_evals": round(float(cmps.double().mean().item()) + 1.0, 1)})
+    del ptargets, pcounts
     deg = counts.double()
     # graph diagnostics: points reachable from the start (breadth-first over
     # the rows) and, for 2000 sample points, the share of their exact 10
@@ -395,6 +409,7 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
         "row_recall_at_10": round(row_recall, 4),
         "search": searches,
         "search_parity_sample": parity,
+        "final_prune": pruned,
     }
     log(f"recall leg: build {build_s * 1e3:.1f} ms, " +
         ", ".join(f"L={s['L']} recall@10 {s['recall_at_10']}" for s in searches))

@@ -472,6 +472,24 @@ tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, co
                                     uint32_t fanout_top, uint32_t *out_child, uint32_t *out_point,
                                     uint64_t *child_offsets, uint32_t *child_points, void *stream);
 
+/* ---- final RobustPrune -------------------------------------------------------
+ * final_prune_pipnn (index/inmem_index/pipnn_builder.rs:287-330) with
+ * robust_prune / occlude_list (algorithm/prune/prune.rs:17-214) over every
+ * row of a neighbour table (row p = targets[p * row_stride .. + counts[p]],
+ * ids >= num_points skipped): the pool sorted by (distance, id), cut to
+ * max_occlusion (the reference's max_occlusion_size, default 750), alpha
+ * passes 1.0, x1.2, .. <= alpha (index_write_parameter.alpha, default 1.2),
+ * at most max_degree kept (default 64); saturate != 0 fills up from the pool
+ * when alpha > 1 (saturate_graph, default off).  Distances: squared L2 of
+ * f32 rows summed in coordinate order without contraction.  Outputs
+ * out_targets [num_points x max_degree] (0xFFFFFFFF past out_counts[p]) and
+ * out_counts [num_points].  row_stride and max_degree <= 256.  Device
+ * pointers; enqueued on `stream`. */
+tessa_status tessa_robust_prune(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
+                                const uint32_t *counts, uint32_t row_stride, uint32_t max_degree,
+                                uint32_t max_occlusion, float alpha, int saturate, uint32_t *out_targets,
+                                uint32_t *out_counts, void *stream);
+
 /* ---- greedy search: the recall harness ---------------------------------------
  * InmemIndex::search (index/inmem_index/inmem_index.rs:523-590) over a
  * neighbour table (row p = targets[p * row_stride .. + counts[p]], ids >=

@@ -88,6 +88,9 @@ def lib():
         _lib.orc_d0_assign.restype = C.c_int
         _lib.orc_d0_assign.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, C.c_size_t, C.c_size_t, P, P,
                                        P, P]
+        _lib.orc_robust_prune.restype = C.c_int
+        _lib.orc_robust_prune.argtypes = [P, C.c_size_t, C.c_size_t, P, P, C.c_size_t, C.c_size_t, C.c_size_t,
+                                          C.c_float, C.c_int, P, P]
         _lib.orc_greedy_search.restype = C.c_int
         _lib.orc_greedy_search.argtypes = [P, C.c_size_t, C.c_size_t, P, P, C.c_size_t, C.c_uint32, P, C.c_size_t,
                                            C.c_size_t, C.c_size_t, P, P, P]
@@ -423,3 +426,19 @@ def d0_assign(codes, scales, norms, global_ids, leader_codes, leader_scales, lea
     if rc != 0:
         raise ValueError(f"orc_d0_assign: {rc}")
     return child, offs, pts
+
+
+def robust_prune(data: np.ndarray, targets: np.ndarray, counts: np.ndarray, max_degree: int = 64,
+                 max_occlusion: int = 750, alpha: float = 1.2, saturate: bool = False):
+    """Final RobustPrune of every row (pipnn_builder.rs:287-330, prune.rs:17-214):
+    (targets u32 [n, max_degree], counts u32 [n])."""
+    x = np.ascontiguousarray(data, np.float32)
+    t = np.ascontiguousarray(targets).view(np.uint32)
+    c = np.ascontiguousarray(counts).astype(np.uint32)
+    out = np.zeros((x.shape[0], max_degree), np.uint32)
+    cnt = np.zeros(x.shape[0], np.uint32)
+    rc = lib().orc_robust_prune(_p(x), x.shape[0], x.shape[1], _p(t), _p(c), t.shape[1], max_degree, max_occlusion,
+                                alpha, 1 if saturate else 0, _p(out), _p(cnt))
+    if rc != 0:
+        raise ValueError(f"orc_robust_prune: {rc}")
+    return out, cnt

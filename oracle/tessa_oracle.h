@@ -40,6 +40,9 @@
  *                         leader first, ties by leader id on duplicated leaders,
  *                         fanout = leader count giving the full order, the grouping
  *                         against a sort of the fragments.
+ *   orc_robust_prune      hand-worked occlusions (a point behind a kept one dropped, two
+ *                         orthogonal ones kept, one kept only in the alpha = 1.2 pass),
+ *                         the degree cap, self-loops and zero distances, saturation.
  *   orc_greedy_search     brute force: on a complete graph (every point lists every
  *                         other) with L >= n the search visits everything and
  *                         returns the exact K nearest; the neighbour-queue rules
@@ -295,6 +298,14 @@ int orc_d0_assign(const int8_t *codes, const float *scales, const float *norms, 
                   size_t rows, size_t padded_dim, const int8_t *leader_codes, const float *leader_scales,
                   const float *leader_norms, const uint32_t *leader_ids, size_t leader_count, size_t fanout,
                   uint32_t *out_child, uint32_t *out_point, uint64_t *child_offsets, uint32_t *child_points);
+
+/* Final RobustPrune of every row of a [num_points x row_stride] neighbour
+ * table (index/inmem_index/pipnn_builder.rs:287-330, algorithm/prune/
+ * prune.rs:17-214): out_targets [num_points x max_degree] (0xFFFFFFFF past
+ * out_counts).  Returns 0, -1 on bad arguments. */
+int orc_robust_prune(const float *data, size_t num_points, size_t dim, const uint32_t *targets,
+                     const uint32_t *counts, size_t row_stride, size_t max_degree, size_t max_occlusion,
+                     float alpha, int saturate, uint32_t *out_targets, uint32_t *out_counts);
 
 #ifdef __cplusplus
 }

@@ -288,6 +288,7 @@ SIGNATURES = {
     "tessa_hashprune_clear": (TessaStatus, [_P, _P]),
     "tessa_graph_pack": (TessaStatus, [_P, _P, _U32, _U32, _U32, _U64, _P, _U64, C.POINTER(_U64), _P]),
     "tessa_global_d0_assign": (TessaStatus, [_P, _P, _P, _P, _U64, _U32, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P]),
+    "tessa_robust_prune": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _U32, C.c_float, C.c_int, _P, _P, _P]),
     "tessa_graph_search": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P]),
 }
 

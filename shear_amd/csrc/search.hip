@@ -31,6 +31,7 @@
 // claimed with an atomic exchange so a point listed twice in one row enters
 // the list once.
 #include "search_kernels.h"
+#include "tessa_device.h"
 
 namespace tessa {
 
@@ -49,33 +50,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <bool kVec4>
-__device__ float l2_ordered(const float *__restrict__ x, const float *__restrict__ q, uint32_t dim) {
-#pragma clang fp contract(off)
-    float s = 0.0f;
-    if constexpr (kVec4) {
-        const float4 *xv = reinterpret_cast<const float4 *>(x);
-        const float4 *qv = reinterpret_cast<const float4 *>(q);
-        for (uint32_t i = 0; i < dim / 4; ++i) {
-            const float4 a = xv[i], b = qv[i];
-            float t = a.x - b.x;
-            s = s + t * t;
-            t = a.y - b.y;
-            s = s + t * t;
-            t = a.z - b.z;
-            s = s + t * t;
-            t = a.w - b.w;
-            s = s + t * t;
-        }
-    } else {
-        for (uint32_t i = 0; i < dim; ++i) {
-            const float t = x[i] - q[i];
-            s = s + t * t;
-        }
-    }
-    return s;
 }
 
 __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, uint32_t src) {

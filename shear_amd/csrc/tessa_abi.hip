@@ -25,6 +25,7 @@
 #include "hashprune_kernels.h"
 #include "leaf_kernels.h"
 #include "partition.h"
+#include "prune_kernels.h"
 #include "search_kernels.h"
 #include "tessa_device.h"
 
@@ -1720,6 +1721,36 @@ tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, co
     if (st.code) return st;
     if (tessa::launch_d0_group(p, child_offsets, child_points, ws->d0_temp, ws->d0_temp_capacity, s) != 0)
         return make_status(TESSA_ERR_HIP, 0, "D0 grouping launch failed");
+    return ok_status();
+}
+
+tessa_status tessa_robust_prune(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
+                                const uint32_t *counts, uint32_t row_stride, uint32_t max_degree,
+                                uint32_t max_occlusion, float alpha, int saturate, uint32_t *out_targets,
+                                uint32_t *out_counts, void *stream) {
+    if (max_degree == 0 || max_degree > tessa::kPruneMaxPool || row_stride > tessa::kPruneMaxPool)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "robust prune: max_degree %u / row_stride %u outside 1..%u",
+                           max_degree, row_stride, tessa::kPruneMaxPool);
+    if (num_points == 0) return ok_status();
+    if (num_points == 0xFFFFFFFFu || dim == 0 || !(alpha == alpha))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "robust prune: %u points of dim %u", num_points, dim);
+    if (!data || !counts || (row_stride && !targets) || !out_targets || !out_counts)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "robust prune: null pointer");
+    tessa::RobustPruneParams p{};
+    p.data = data;
+    p.num_points = num_points;
+    p.dim = dim;
+    p.targets = targets;
+    p.counts = counts;
+    p.row_stride = row_stride;
+    p.max_degree = max_degree;
+    p.max_occlusion = max_occlusion;
+    p.alpha = alpha;
+    p.saturate = saturate ? 1u : 0u;
+    p.out_targets = out_targets;
+    p.out_counts = out_counts;
+    if (tessa::launch_robust_prune(p, reinterpret_cast<hipStream_t>(stream)) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "robust prune launch failed");
     return ok_status();
 }
 

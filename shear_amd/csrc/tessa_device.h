@@ -37,6 +37,35 @@ __device__ __forceinline__ float assign_l2(int dot, float ps, float pn, float ls
     return d <= 0.0f ? 0.0f : d;
 }
 
+// Squared L2 of two f32 rows summed over the coordinates in order, each
+// product rounded before the add (the order the graph search and the final
+// prune are pinned to).  kVec4: 16-byte aligned rows, dim a multiple of 4.
+template <bool kVec4>
+__device__ float l2_ordered(const float *__restrict__ x, const float *__restrict__ q, uint32_t dim) {
+    float s = 0.0f;
+    if constexpr (kVec4) {
+        const float4 *xv = reinterpret_cast<const float4 *>(x);
+        const float4 *qv = reinterpret_cast<const float4 *>(q);
+        for (uint32_t i = 0; i < dim / 4; ++i) {
+            const float4 a = xv[i], b = qv[i];
+            float t = __fsub_rn(a.x, b.x);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+            t = __fsub_rn(a.y, b.y);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+            t = __fsub_rn(a.z, b.z);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+            t = __fsub_rn(a.w, b.w);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+        }
+    } else {
+        for (uint32_t i = 0; i < dim; ++i) {
+            const float t = __fsub_rn(x[i], q[i]);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+        }
+    }
+    return s;
+}
+
 // mod.rs:417-428 stable_distance_order(..).is_lt(): does candidate c beat s?
 __device__ __forceinline__ bool beats(float dc, uint32_t idc, float ds, uint32_t ids) {
     float delta = __fsub_rn(dc, ds);

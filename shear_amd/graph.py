@@ -8,6 +8,9 @@ built by ``tessa_graph_pack`` in libtessa_hip.so.  ``read_mem_index`` parses
 the same layout back (header: index_size u64, max_degree u32, start u32,
 num_frozen_pts u64; rows: degree u32 then ids, little-endian).
 
+``robust_prune`` is the final RobustPrune (final_prune_pipnn,
+shear-core/src/index/inmem_index/pipnn_builder.rs:287-330, with
+algorithm/prune/prune.rs:17-214) run by ``tessa_robust_prune``.
 ``greedy_search`` is InmemIndex::search (shear-core/src/index/inmem_index/
 inmem_index.rs:523-590, greedy_search algorithm/search/search.rs:137-233) run
 by ``tessa_graph_search``, one wavefront per query; ``recall_at_k`` is the
@@ -104,3 +107,25 @@ def recall_at_k(found: np.ndarray, truth: np.ndarray, k: int) -> float:
         gt = set(b.tolist())
         total += sum(1 for i in a.tolist() if i in gt) / k
     return total / len(f) if len(f) else 0.0
+
+
+def robust_prune(data: torch.Tensor, targets: torch.Tensor, counts: torch.Tensor, max_degree: int = 64,
+                 max_occlusion: int = 750, alpha: float = 1.2, saturate: bool = False,
+                 stream: torch.cuda.Stream | None = None):
+    """(targets int32 [n, max_degree] (-1 past the count), counts int32 [n]):
+    every row pruned as the reference's final prune does (defaults: the
+    reference's max_degree 64, max_occlusion_size 750, alpha 1.2, saturate off)."""
+    if data.dim() != 2 or data.dtype != torch.float32:
+        raise ValueError("data must be f32 [n, dim]")
+    if targets.dim() != 2 or targets.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise ValueError("targets must be int32 [num_points, row_stride] and counts int32 [num_points]")
+    n, dim = data.shape
+    x, t = data.contiguous(), targets.contiguous()
+    if t.shape[0] != n or counts.numel() != n:
+        raise ValueError(f"neighbour table of {t.shape[0]} rows / {counts.numel()} counts for {n} points")
+    out = torch.empty((n, max_degree), dtype=torch.int32, device=x.device)
+    cnt = torch.empty(n, dtype=torch.int32, device=x.device)
+    N.check(N.load().tessa_robust_prune(_ptr(x), n, dim, _ptr(t), _ptr(counts), t.shape[1], max_degree, max_occlusion,
+                                        alpha, 1 if saturate else 0, _ptr(out), _ptr(cnt), _stream_ptr(stream)),
+            "robust prune")
+    return out, cnt
