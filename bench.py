@@ -243,8 +243,8 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
                sigma=0.3, r_max=64, search_runs=3, unit_norm=True, fanout_top=10):
     """C1-shaped end-to-end graph build on the GPU and its recall@10: rows x
     128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) -> SQ8
-    -> global D0 assignment (rows * 0.0007 leaders, each point to its
-    fanout_top = 10 nearest) -> one subtree task per D0 child (depth 1:
+    -> global D0 assignment (leader count from the D0 capacity plan, each
+    point to its fanout_top = 10 nearest) -> one subtree task per D0 child (depth 1:
     fanout 3 at its root, leaves <= 1024, k = 32 leaf top-k) -> edge records
     (12-bit hashes from 12 uniform [-1, 1) hyperplane sketches) -> HashPrune
     reservoirs (l_max = R = 64) -> the `_mem.index` image; then greedy search
@@ -269,7 +269,16 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     gids = torch.arange(rows, dtype=torch.int32, device=dev)
     params = S.PiPNNSubtreeParams(leaf_knn=32, c_max=1024, fanout_second=3, psamp_fraction=0.001, max_leaders=128,
                                   random_seed=42, max_depth=16)
-    nl = D.d0_leader_count(rows)
+    # D0 leaders from the capacity plan (d0_capacity on by default): the largest
+    # admitted subtree under the default 512 MiB workspace budget sets c_target
+    c_gpu = D.find_max_admissible_rows(dim, params.leaf_knn, min(params.max_leaders, D.GPU_QUEUE_LEADER_STRIDE),
+                                       params.fanout_second, D.DEFAULT_GPU_WORKSPACE_BUDGET_BYTES, None,
+                                       params.c_max)
+    leader_plan = D.plan_root_leaders(rows, fanout_top, D.compute_thresholds(c_gpu))
+    # at 200k points the plan asks for its quality floor (64 leaders); children of
+    # ~34k rows then end one partition branch at max depth (OVERSIZED_TERMINAL_NODE),
+    # so the leg takes the larger of the plan and the sampling-rate count
+    nl = max(int(leader_plan["k_initial"]), D.d0_leader_count(rows))
     lrows = D.sample_leader_rows(rows, nl, 42, dev)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
@@ -316,7 +325,8 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
     w4 = time.perf_counter()
-    stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": nl, "d0_fanout_top": fanout_top,
+    stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": nl, "d0_leader_source":
+              leader_plan["root_leader_source"], "d0_c_gpu": c_gpu, "d0_fanout_top": fanout_top,
               "children_wall_ms": round((w3 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
               "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
               "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}

@@ -310,6 +310,63 @@ tessa_status tessa_plan_subtree(uint64_t resident_rows, uint32_t leaf_knn,
                                 uint64_t budget_bytes /* 0 = unlimited */, uint32_t c_max,
                                 tessa_subtree_plan *plan);
 
+/* ---- GPU-memory-aware task formation -----------------------------------------
+ * plan_gpu_persistent_subtree_resident_admission (compute_backend.rs:
+ * 1490-1522): the plan above plus the resident rows' bytes
+ * (estimate_gpu_resident_subtree_device_bytes[_for_params] :898-930: f32 rows
+ * + id + norm, the reference default; or SQ8 codes padded to 16 bytes, or
+ * packed int4, + id + scale + norm); a task whose resident + workspace bytes
+ * exceed device_budget_bytes (0 = none) is unsupported with the workspace
+ * fallback and overflow bits.  Budgets of 0 mean "none". */
+#define TESSA_RESIDENT_F32 0u
+#define TESSA_RESIDENT_SQ8 1u
+#define TESSA_RESIDENT_SQ4 2u
+typedef struct tessa_resident_admission {
+    tessa_subtree_plan plan;
+    uint64_t resident_device_bytes;
+    uint64_t device_admission_required_bytes;
+    uint64_t device_admission_budget_bytes;  /* UINT64_MAX without a budget */
+} tessa_resident_admission;
+tessa_status tessa_plan_subtree_resident_admission(uint64_t resident_rows, uint32_t dim, uint32_t leaf_knn,
+                                                   uint32_t max_leaders_per_node, uint32_t max_fanout,
+                                                   uint64_t workspace_budget_bytes, uint64_t device_budget_bytes,
+                                                   uint32_t c_max, uint32_t resident_format,
+                                                   tessa_resident_admission *out);
+/* find_max_admissible_rows (d0_capacity.rs:55-102): the largest resident row
+ * count (< 2^31 by doubling, then bisection) the admission supports; 0 when
+ * dim is 0 or one row does not fit. */
+uint64_t tessa_find_max_admissible_rows(uint32_t dim, uint32_t leaf_knn, uint32_t max_leaders_per_node,
+                                        uint32_t max_fanout, uint64_t workspace_budget_bytes,
+                                        uint64_t device_budget_bytes, uint32_t c_max, uint32_t resident_format);
+/* D0 capacity (d0_capacity.rs:201-299): thresholds from the admitted row
+ * count (ratios clamped high in [0.01, 1], target in [0.01, high], low in
+ * [0, target]; c_low lifted to min_efficient_rows, capped at c_target);
+ * root leader plan (k_capacity = ceil(points * fanout / c_target), the
+ * quality floor and the leader cap); split leader count of an oversized
+ * child; nearest-rank child size summary. */
+typedef struct tessa_d0_thresholds {
+    uint64_t c_gpu, c_high, c_target, c_low;
+} tessa_d0_thresholds;
+#define TESSA_D0_LEADERS_CAPACITY      0u  /* "capacity" */
+#define TESSA_D0_LEADERS_QUALITY_FLOOR 1u  /* "quality_floor" */
+#define TESSA_D0_LEADERS_ROOT_CAP      2u  /* "root_leader_cap" */
+typedef struct tessa_d0_leader_plan {
+    uint64_t k_capacity, k_initial, root_leader_cap;
+    uint32_t source;
+} tessa_d0_leader_plan;
+typedef struct tessa_d0_child_summary {
+    uint64_t max_rows, p50_rows, p95_rows, p99_rows;
+    uint64_t oversized_count, small_count, small_rows;
+} tessa_d0_child_summary;
+tessa_d0_thresholds tessa_d0_compute_thresholds(uint64_t c_gpu, double high_ratio, double target_ratio,
+                                                double low_ratio, uint64_t min_efficient_rows);
+tessa_d0_leader_plan tessa_d0_plan_root_leaders(uint64_t total_points, uint64_t root_fanout,
+                                                const tessa_d0_thresholds *t, uint64_t quality_min_root_leaders,
+                                                uint64_t root_leader_cap);
+uint64_t tessa_d0_split_leader_count(uint64_t rows, const tessa_d0_thresholds *t);
+tessa_d0_child_summary tessa_d0_observe_child_sizes(const uint64_t *sizes, uint64_t count,
+                                                    const tessa_d0_thresholds *t);
+
 /* gpu_queue_root_seed (compute_backend.rs:1597-1603). */
 uint64_t tessa_subtree_root_seed(uint64_t random_seed, uint64_t depth, uint64_t point_count,
                                  uint64_t parent_points, uint64_t min_recurse_size);

@@ -239,6 +239,29 @@ class SketchView(C.Structure):
     ]
 
 
+class ResidentAdmission(C.Structure):
+    _fields_ = [("plan", SubtreePlan), ("resident_device_bytes", C.c_uint64),
+                ("device_admission_required_bytes", C.c_uint64), ("device_admission_budget_bytes", C.c_uint64)]
+
+
+class D0Thresholds(C.Structure):
+    _fields_ = [("c_gpu", C.c_uint64), ("c_high", C.c_uint64), ("c_target", C.c_uint64), ("c_low", C.c_uint64)]
+
+
+class D0LeaderPlan(C.Structure):
+    _fields_ = [("k_capacity", C.c_uint64), ("k_initial", C.c_uint64), ("root_leader_cap", C.c_uint64),
+                ("source", C.c_uint32)]
+
+
+class D0ChildSummary(C.Structure):
+    _fields_ = [(f, C.c_uint64) for f in ("max_rows", "p50_rows", "p95_rows", "p99_rows", "oversized_count",
+                                          "small_count", "small_rows")]
+
+
+RESIDENT_F32, RESIDENT_SQ8, RESIDENT_SQ4 = 0, 1, 2
+D0_LEADER_SOURCES = ("capacity", "quality_floor", "root_leader_cap")
+
+
 # Every symbol include/tessa_hip.h declares, with its ctypes signature.
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -289,6 +312,13 @@ SIGNATURES = {
     "tessa_graph_pack": (TessaStatus, [_P, _P, _U32, _U32, _U32, _U64, _P, _U64, C.POINTER(_U64), _P]),
     "tessa_global_d0_assign": (TessaStatus, [_P, _P, _P, _P, _U64, _U32, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P]),
     "tessa_robust_prune": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _U32, C.c_float, C.c_int, _P, _P, _P]),
+    "tessa_plan_subtree_resident_admission": (TessaStatus, [_U64, _U32, _U32, _U32, _U32, _U64, _U64, _U32, _U32,
+                                                             C.POINTER(ResidentAdmission)]),
+    "tessa_find_max_admissible_rows": (_U64, [_U32, _U32, _U32, _U32, _U64, _U64, _U32, _U32]),
+    "tessa_d0_compute_thresholds": (D0Thresholds, [_U64, C.c_double, C.c_double, C.c_double, _U64]),
+    "tessa_d0_plan_root_leaders": (D0LeaderPlan, [_U64, _U64, C.POINTER(D0Thresholds), _U64, _U64]),
+    "tessa_d0_split_leader_count": (_U64, [_U64, C.POINTER(D0Thresholds)]),
+    "tessa_d0_observe_child_sizes": (D0ChildSummary, [_P, _U64, C.POINTER(D0Thresholds)]),
     "tessa_graph_search": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P]),
 }
 

@@ -77,3 +77,16 @@ def test_argument_errors(gpu):
     with pytest.raises(N.TessaError, match="fanout must be in 1..=min\\(32, leaders\\), got fanout=5 leaders=4"):
         D.global_d0_assign(sq8, g, lead, g[:4], 5)
     assert D.d0_leader_count(200_000) == 140 and D.d0_leader_count(50_000_000) == 1000
+
+
+def test_sidecar_round_trip_of_gpu_quantized_rows(gpu, tmp_path):
+    from shear_amd import sidecar as SC
+
+    x = torch.from_numpy(datagen.gmm_numpy(3000, 100, 8, 0.3, 9)).to(gpu)
+    sq8 = T.quantize_sq_int8_matrix(x)
+    c, s, n = _host(sq8)
+    SC.write_sidecar(tmp_path / "base", c, s, n, 100)
+    h, c2, s2, n2 = SC.read_sidecar(tmp_path / "base", rows=3000, dim=100)
+    back = T.Sq8Matrix(torch.from_numpy(c2).to(gpu), torch.from_numpy(s2).to(gpu), torch.from_numpy(n2).to(gpu), 100)
+    assert h["padded_dim"] == sq8.padded_dim == 112
+    assert torch.equal(back.codes, sq8.codes) and torch.equal(back.scales, sq8.scales) and torch.equal(back.norms, sq8.norms)
