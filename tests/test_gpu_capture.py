@@ -1,0 +1,60 @@
+"""TESSA capture from a real GPU subtree run: the sampled leaf tasks are the
+run's leaves (as global-id sets), the capture round-trips through the
+reference's fixture format, and replaying the captured tasks through the
+leaf operator matches the oracle bit for bit."""
+import numpy as np
+import pytest
+
+from gpu_helpers import assert_same, require_gpu, run_leaf, to_dev_sq8
+from shear_amd import _native as N
+from shear_amd import capture as CP
+from shear_amd import datagen
+from shear_amd import subtree as S
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    return require_gpu()
+
+
+def test_capture_and_replay_of_subtree_leaves(gpu, orc, tmp_path):
+    n, dim = 6000, 64
+    x = datagen.gmm_numpy(n, dim, 8, 0.3, 12)
+    codes, scales, norms = orc.quantize(x)
+    gids = np.random.default_rng(12).permutation(n).astype(np.uint32)
+    sess = S.SubtreeSession(0)
+    sess.upload(codes, scales, norms, gids, dim)
+    out = sess.run(S.GpuSubtreePartitionRequest(point_ids=gids, parent_points=n, min_recurse_size=64),
+                   S.PiPNNSubtreeParams(leaf_knn=16, c_max=1024, fanout_second=2, psamp_fraction=0.01, random_seed=5))
+    sampler = CP.TessaCaptureSampler(42)
+    kept = CP.observe_subtree_leaves(sampler, out, gids, codes.shape[1])
+    sel = sampler.finish()
+    assert kept > 0 and len(sel.leaf_tasks) == kept
+    rows = out.leaf_row_ids[: out.leaf_rows].cpu().numpy().view(np.uint32)
+    starts = out.leaf_starts[: out.leaf_count].cpu().numpy()
+    sizes = out.leaf_sizes[: out.leaf_count].cpu().numpy()
+    leaves = {tuple(sorted(gids[rows[s:s + c]].tolist())) for s, c in zip(starts, sizes)}
+    assert all(tuple(t.member_ids) in leaves for t in sel.leaf_tasks)
+
+    ds = {"canonical_base_path": "/data/base.fbin", "rows": n, "dimension": dim, "header_sha256": "ab" * 32}
+    prov = {"seed": 42, "git_commit": "local", "binary_sha256": "cd" * 32, "command_sha256": "ef" * 32,
+            "root_leader_hash": 1, "d0_partition_hash": 2, "d0_task_list_hash": 3}
+    CP.write_tessa_capture(tmp_path, ds, prov, sel)
+    _, loaded = CP.load_tessa_capture(tmp_path, ds)
+    assert [t.task_hash for t in loaded.leaf_tasks] == sorted(
+        (t.task_hash for t in sel.leaf_tasks),
+        key=lambda h: next((CP.leaf_size_bin(len(t.member_ids)), t.priority, t.task_hash)
+                           for t in sel.leaf_tasks if t.task_hash == h))
+
+    # replay the captured tasks: global ids -> resident rows
+    row_of = np.empty(n, np.int64)
+    row_of[gids] = np.arange(n)
+    members = np.concatenate([row_of[np.asarray(t.member_ids)] for t in loaded.leaf_tasks]).astype(np.uint32)
+    counts = np.array([len(t.member_ids) for t in loaded.leaf_tasks])
+    offs = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    k = loaded.leaf_tasks[0].k
+    want_ids, want_d = orc.leaf_topk(codes, scales, norms, gids, members, offs, counts, k)
+    ids, d, _ = run_leaf(to_dev_sq8(codes, scales, norms, dim), gids, members, offs, counts, k, N.EXEC_MFMA)
+    assert_same(ids, d, want_ids, want_d, "captured leaf tasks")
