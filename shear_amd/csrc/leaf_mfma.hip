@@ -93,8 +93,14 @@ constexpr float kFilterMargin = 3.0f * kTieEps;
 constexpr uint32_t kSampleStride = TESSA_LEAF_SAMPLE_STRIDE;
 constexpr int kSampleRank = TESSA_LEAF_SAMPLE_RANK;
 constexpr uint32_t kSampleWideTiles = TESSA_LEAF_SAMPLE_WIDE_TILES;
-constexpr uint32_t kSampleStrideWide = 4;
-constexpr int kSampleRankWide = 18;
+#ifndef TESSA_LEAF_SAMPLE_STRIDE_WIDE
+#define TESSA_LEAF_SAMPLE_STRIDE_WIDE 4
+#endif
+#ifndef TESSA_LEAF_SAMPLE_RANK_WIDE
+#define TESSA_LEAF_SAMPLE_RANK_WIDE 18
+#endif
+constexpr uint32_t kSampleStrideWide = TESSA_LEAF_SAMPLE_STRIDE_WIDE;
+constexpr int kSampleRankWide = TESSA_LEAF_SAMPLE_RANK_WIDE;
 
 template <int KS>
 struct Layout {
