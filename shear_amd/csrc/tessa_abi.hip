@@ -476,6 +476,15 @@ struct tessa_session {
         uint64_t leaf_count = 0, leaf_rows = 0;
         uint32_t k = 0, levels = 0;
         float partition_ms = 0.0f, leaf_ms = 0.0f;
+        // device outputs of this slot's job: the next job computes into the
+        // other slot's while this one's D2H runs on the copy stream
+        uint32_t *rows_d = nullptr;
+        uint64_t *starts_d = nullptr, *sizes_d = nullptr;
+        uint32_t *ids_d = nullptr;
+        float *dists_d = nullptr;
+        uint64_t rows_dcap = 0, starts_dcap = 0, sizes_dcap = 0, ids_dcap = 0, dists_dcap = 0;
+        hipEvent_t computed = nullptr, copied = nullptr;
+        bool copy_pending = false;
     };
     static constexpr int kAsyncSlots = 2;
     AsyncSlot slots[kAsyncSlots];
@@ -486,12 +495,8 @@ struct tessa_session {
     bool worker_started = false;
     bool stop = false;
     uint64_t next_seq = 1;
-    // device outputs of async jobs (one job runs at a time)
-    uint32_t *a_rows = nullptr;
-    uint64_t *a_starts = nullptr, *a_sizes = nullptr;
-    uint32_t *a_ids = nullptr;
-    float *a_dists = nullptr;
-    uint64_t a_rows_cap = 0, a_starts_cap = 0, a_sizes_cap = 0, a_ids_cap = 0, a_dists_cap = 0;
+    // side stream for the results' D2H copies (default priority)
+    hipStream_t copy_stream = nullptr;
 };
 
 namespace {
@@ -1150,20 +1155,24 @@ tessa_status run_async_job(tessa_session *s, tessa_session::AsyncSlot &slot) {
     }
     const tessa_subtree_request &rq = slot.req;
     const uint64_t k_cap = rq.partition_only ? 1 : (rq.leaf_knn ? rq.leaf_knn : 1);
-    tessa_status st = grow_device(&s->a_rows, &s->a_rows_cap, rq.max_leaf_rows);
-    if (!st.code) st = grow_device(&s->a_starts, &s->a_starts_cap, rq.max_leaf_count);
-    if (!st.code) st = grow_device(&s->a_sizes, &s->a_sizes_cap, rq.max_leaf_count);
-    if (!st.code) st = grow_device(&s->a_ids, &s->a_ids_cap, rq.max_leaf_rows * k_cap);
-    if (!st.code) st = grow_device(&s->a_dists, &s->a_dists_cap, rq.max_leaf_rows * k_cap);
+    // this slot's previous copy finished before it was released (wait syncs it)
+    tessa_status st = grow_device(&slot.rows_d, &slot.rows_dcap, rq.max_leaf_rows);
+    if (!st.code) st = grow_device(&slot.starts_d, &slot.starts_dcap, rq.max_leaf_count);
+    if (!st.code) st = grow_device(&slot.sizes_d, &slot.sizes_dcap, rq.max_leaf_count);
+    if (!st.code) st = grow_device(&slot.ids_d, &slot.ids_dcap, rq.max_leaf_rows * k_cap);
+    if (!st.code) st = grow_device(&slot.dists_d, &slot.dists_dcap, rq.max_leaf_rows * k_cap);
     if (st.code) return st;
+    if (!s->copy_stream) TESSA_HIP_TRY(hipStreamCreateWithFlags(&s->copy_stream, hipStreamNonBlocking));
+    if (!slot.computed) TESSA_HIP_TRY(hipEventCreateWithFlags(&slot.computed, hipEventDisableTiming));
+    if (!slot.copied) TESSA_HIP_TRY(hipEventCreateWithFlags(&slot.copied, hipEventDisableTiming));
     tessa_subtree_request req = rq;
     req.root_leaders = slot.roots.empty() ? nullptr : slot.roots.data();
     tessa_subtree_output out{};
-    out.leaf_row_ids = s->a_rows;
-    out.leaf_starts = s->a_starts;
-    out.leaf_sizes = s->a_sizes;
-    out.topk_ids = s->a_ids;
-    out.topk_dists = s->a_dists;
+    out.leaf_row_ids = slot.rows_d;
+    out.leaf_starts = slot.starts_d;
+    out.leaf_sizes = slot.sizes_d;
+    out.topk_ids = slot.ids_d;
+    out.topk_dists = slot.dists_d;
     out.counters = slot.counters;
     out.leaf_counters = slot.leaf_counters;
     std::memset(slot.counters, 0, sizeof(slot.counters));
@@ -1183,15 +1192,21 @@ tessa_status run_async_job(tessa_session *s, tessa_session::AsyncSlot &slot) {
     if (!st.code) st = grow_pinned(&slot.ids_h, &slot.ids_cap, nslots);
     if (!st.code) st = grow_pinned(&slot.dists_h, &slot.dists_cap, nslots);
     if (st.code) return st;
-    hipStream_t q = s->stream;
-    TESSA_HIP_TRY(hipMemcpyAsync(slot.rows_h, s->a_rows, out.leaf_rows * 4, hipMemcpyDeviceToHost, q));
-    TESSA_HIP_TRY(hipMemcpyAsync(slot.starts_h, s->a_starts, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
-    TESSA_HIP_TRY(hipMemcpyAsync(slot.sizes_h, s->a_sizes, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
+    // the D2H runs on the copy stream once the compute stream has produced the
+    // results; the worker goes on to the next job, which computes into the
+    // other slot's buffers meanwhile; wait() synchronises on `copied`
+    hipStream_t q = s->copy_stream;
+    TESSA_HIP_TRY(hipEventRecord(slot.computed, s->stream));
+    TESSA_HIP_TRY(hipStreamWaitEvent(q, slot.computed, 0));
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.rows_h, slot.rows_d, out.leaf_rows * 4, hipMemcpyDeviceToHost, q));
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.starts_h, slot.starts_d, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
+    TESSA_HIP_TRY(hipMemcpyAsync(slot.sizes_h, slot.sizes_d, out.leaf_count * 8, hipMemcpyDeviceToHost, q));
     if (nslots) {
-        TESSA_HIP_TRY(hipMemcpyAsync(slot.ids_h, s->a_ids, nslots * 4, hipMemcpyDeviceToHost, q));
-        TESSA_HIP_TRY(hipMemcpyAsync(slot.dists_h, s->a_dists, nslots * 4, hipMemcpyDeviceToHost, q));
+        TESSA_HIP_TRY(hipMemcpyAsync(slot.ids_h, slot.ids_d, nslots * 4, hipMemcpyDeviceToHost, q));
+        TESSA_HIP_TRY(hipMemcpyAsync(slot.dists_h, slot.dists_d, nslots * 4, hipMemcpyDeviceToHost, q));
     }
-    TESSA_HIP_TRY(hipStreamSynchronize(q));
+    TESSA_HIP_TRY(hipEventRecord(slot.copied, q));
+    slot.copy_pending = true;
     return ok_status();
 }
 
@@ -1229,7 +1244,15 @@ void stop_async(tessa_session *s) {
     s->q_cv.notify_all();
     if (s->worker_started && s->worker.joinable()) s->worker.join();
     s->worker_started = false;
+    if (s->copy_stream) (void)hipStreamSynchronize(s->copy_stream);
     for (auto &slot : s->slots) {
+        if (slot.rows_d) (void)hipFree(slot.rows_d);
+        if (slot.starts_d) (void)hipFree(slot.starts_d);
+        if (slot.sizes_d) (void)hipFree(slot.sizes_d);
+        if (slot.ids_d) (void)hipFree(slot.ids_d);
+        if (slot.dists_d) (void)hipFree(slot.dists_d);
+        if (slot.computed) (void)hipEventDestroy(slot.computed);
+        if (slot.copied) (void)hipEventDestroy(slot.copied);
         if (slot.rows_h) (void)hipHostFree(slot.rows_h);
         if (slot.starts_h) (void)hipHostFree(slot.starts_h);
         if (slot.sizes_h) (void)hipHostFree(slot.sizes_h);
@@ -1237,15 +1260,8 @@ void stop_async(tessa_session *s) {
         if (slot.dists_h) (void)hipHostFree(slot.dists_h);
         slot = tessa_session::AsyncSlot{};
     }
-    if (s->a_rows) (void)hipFree(s->a_rows);
-    if (s->a_starts) (void)hipFree(s->a_starts);
-    if (s->a_sizes) (void)hipFree(s->a_sizes);
-    if (s->a_ids) (void)hipFree(s->a_ids);
-    if (s->a_dists) (void)hipFree(s->a_dists);
-    s->a_rows = s->a_ids = nullptr;
-    s->a_starts = s->a_sizes = nullptr;
-    s->a_dists = nullptr;
-    s->a_rows_cap = s->a_starts_cap = s->a_sizes_cap = s->a_ids_cap = s->a_dists_cap = 0;
+    if (s->copy_stream) (void)hipStreamDestroy(s->copy_stream);
+    s->copy_stream = nullptr;
 }
 
 }  // namespace
@@ -1308,6 +1324,17 @@ tessa_status tessa_session_wait(tessa_session *s, uint64_t seq, tessa_subtree_ho
                            (unsigned long long)seq);
     tessa_session::AsyncSlot &slot = s->slots[idx];
     s->q_cv.wait(lk, [&slot] { return slot.state == 2; });
+    if (slot.copy_pending) {
+        // the D2H into the pinned slot; the lock is dropped so the worker can
+        // start the next job meanwhile (the slot stays held until release)
+        const hipEvent_t ev = slot.copied;
+        lk.unlock();
+        const hipError_t e = hipEventSynchronize(ev);
+        lk.lock();
+        slot.copy_pending = false;
+        if (e != hipSuccess && slot.status.code == 0)
+            slot.status = make_status(TESSA_ERR_HIP, 0, "result copy failed: %s", hipGetErrorString(e));
+    }
     out->leaf_row_ids = slot.rows_h;
     out->leaf_starts = slot.starts_h;
     out->leaf_sizes = slot.sizes_h;
@@ -1332,6 +1359,10 @@ tessa_status tessa_session_release(tessa_session *s, uint64_t seq) {
             if (slot.state != 2)
                 return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "submission %llu is still running: wait first",
                                    (unsigned long long)seq);
+            // released without a wait: its copy must land before the slot's
+            // buffers can be reused
+            if (slot.copy_pending) (void)hipEventSynchronize(slot.copied);
+            slot.copy_pending = false;
             slot.state = 0;
             return ok_status();
         }
