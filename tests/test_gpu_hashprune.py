@@ -48,6 +48,9 @@ def _same(got, want, what=""):
     (8, 20, 4000, 32, 12, 500),      # 129..256 candidates per point, in registers
     (9, 20, 4000, 200, 12, 500),
     (10, 60, 9000, 64, 8, 300),      # 256 hashes: many collisions at 150 candidates
+    (11, 30, 12000, 64, 12, 3000),   # 257..512 candidates per point: the LDS merge
+    (12, 25, 10000, 256, 12, 50000),  # the same band, more than l_max = 256 hashes kept
+    (13, 30, 12000, 32, 6, 100),     # the band with 64 hashes: heavy collisions and ties
 ])
 def test_random_streams_match_oracle(gpu, orc, seed, num_points, n, l_max, hash_bits, levels):
     rng = np.random.default_rng(seed)
@@ -74,6 +77,17 @@ def test_batches_in_any_split_and_order(gpu, orc):
         assert int(c.sum()) == 0 and bool(torch.all(t == -1))
         hp.insert(r[::-1].copy())  # reused after clear
         _same(_gpu_slots(hp), want, "after clear")
+
+
+def test_second_batch_lands_in_the_register_band(gpu, orc):
+    # full reservoirs (64 slots) + ~300 new records: slots + records in 257..512
+    rng = np.random.default_rng(14)
+    r = random_stream(rng, 40, 30000, 12, 4000)
+    want = orc.hashprune_reduce(40, 64, r)
+    with H.HashPruneReducer(40, 64) as hp:
+        for part in np.array_split(r, 2):
+            hp.insert(part)
+        _same(_gpu_slots(hp), want, "two batches")
 
 
 def test_hub_point_and_empty_batches(gpu, orc):
