@@ -304,23 +304,25 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     hp = H.HashPruneReducer(rows, r_max, dev)
     part_ms = leaf_ms = 0.0
     records = leaves = leaf_rows = 0
+    # every child's rows gathered once (children are contiguous runs of pts)
+    ci_all = pts.long()
+    codes_all, scales_all, norms_all = sq8.codes[ci_all], sq8.scales[ci_all], sq8.norms[ci_all]
+    leaf_max = max(256, params.c_max)  # bound on a leaf's rows (the plan's leaf_max)
     for c in range(nl):
         a, b = int(offs_h[c]), int(offs_h[c + 1])
         if b - a < 2:
             continue
         cg = pts[a:b]
-        ci = cg.long()
-        sub = T.Sq8Matrix(sq8.codes[ci].contiguous(), sq8.scales[ci].contiguous(), sq8.norms[ci].contiguous(), sq8.dim)
+        sub = T.Sq8Matrix(codes_all[a:b], scales_all[a:b], norms_all[a:b], sq8.dim)
         sess.upload_device(sub, cg)
         req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
                                            min_recurse_size=64)
         out = sess.run(req, params)
         part_ms += out.partition_ms
         leaf_ms += out.leaf_ms
-        lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count].to(torch.int64),
-                            out.leaf_sizes[: out.leaf_count].to(torch.int32),
-                            (out.leaf_starts[: out.leaf_count] * out.k).to(torch.int64),
-                            int(out.leaf_sizes[: out.leaf_count].max().item()), out.leaf_rows * out.k)
+        lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
+                            out.leaf_sizes[: out.leaf_count].to(torch.int32), out.leaf_starts[: out.leaf_count] * out.k,
+                            leaf_max, out.leaf_rows * out.k)
         rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
         hp.insert(rec, cnt)
         records += int(cnt)
@@ -341,7 +343,7 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
               "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
               "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}
     build_s = w4 - w0
-    del sess, sketches, pts, offs
+    del sess, sketches, pts, offs, codes_all, scales_all, norms_all
     hp.close()
     # exact ground truth in f64
     xd, qd = x.double(), q.double()

@@ -182,6 +182,9 @@ class SubtreeSession:
         """Resident set from device tensors (an Sq8Matrix and int32-viewed u32
         global ids): a device-to-device copy into the session."""
         view = sq8.view(global_ids)
+        # the session copies on its own stream: the tensors' producers on
+        # torch's current stream must have finished
+        torch.cuda.current_stream(sq8.codes.device).synchronize()
         N.check(self._lib.tessa_session_upload_sq8(self._h, C.byref(view)), "session upload")
         self.rows = sq8.rows
         self.global_ids = None
