@@ -240,7 +240,7 @@ def main() -> int:
 
 
 def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 128), dim=128, components=64,
-               sigma=0.3, r_max=64, search_runs=3, unit_norm=True, fanout_top=10):
+               sigma=0.3, r_max=64, search_runs=3, unit_norm=True, fanout_top=10, insert_every=16):
     """C1-shaped end-to-end graph build on the GPU and its recall@10: rows x
     128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) -> SQ8
     -> global D0 assignment (leader count from the D0 capacity plan, each
@@ -304,6 +304,7 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
     hp = H.HashPruneReducer(rows, r_max, dev)
     part_ms = leaf_ms = 0.0
     records = leaves = leaf_rows = 0
+    pending = []  # records of children not yet merged (insert_every children per HashPrune batch)
     # every child's rows gathered once (children are contiguous runs of pts)
     ci_all = pts.long()
     codes_all, scales_all, norms_all = sq8.codes[ci_all], sq8.scales[ci_all], sq8.norms[ci_all]
@@ -324,11 +325,17 @@ def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 12
                             out.leaf_sizes[: out.leaf_count].to(torch.int32), out.leaf_starts[: out.leaf_count] * out.k,
                             leaf_max, out.leaf_rows * out.k)
         rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
-        hp.insert(rec, cnt)
+        pending.append(rec[:cnt])
+        if len(pending) >= insert_every:
+            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+            pending = []
         records += int(cnt)
         leaves += out.leaf_count
         leaf_rows += out.leaf_rows
         del rec, out, lay, sub
+    if pending:
+        hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+        pending = []
     targets, counts = hp.neighbors()
     torch.cuda.synchronize()
     w3 = time.perf_counter()
