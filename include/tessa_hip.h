@@ -519,8 +519,8 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
  * a child (the D0 children's point lists).  Leader payload: SQ8 codes /
  * scales / norms of the leaders (same padded_dim) and their global ids.
  * fanout_top in [1, min(32, leader_count)] (the reference's "SQ GPU-D0 staging
- * fanout must be in 1..=min(32, leaders)"); padded_dim a multiple of 16 up to
- * 1024; rows * fanout_top < 2^31 when grouping.  Device pointers; enqueued on
+ * fanout must be in 1..=min(32, leaders)"); at most 65,536 leaders; padded_dim a
+ * multiple of 16 up to 1024; rows * fanout_top < 2^31 when grouping.  Device pointers; enqueued on
  * `stream`. */
 tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, const float *norms,
                                     const uint32_t *global_ids, uint64_t rows, uint32_t padded_dim,
