@@ -135,3 +135,20 @@ def test_l_max_limits(gpu):
         H.HashPruneReducer(4, 257)
     with pytest.raises(N.TessaError, match="l_max must be > 0"):
         H.HashPruneReducer(4, 0)
+
+
+def test_spill_round_trip_of_device_records(gpu, orc, tmp_path):
+    # device records -> spill part files + manifest -> read back -> reservoirs
+    # identical to merging the device records directly
+    from shear_amd import spill as SP
+
+    gids, sk, members, offs, sizes, lay, g, ids, d = _leaf_case(orc, [100, 257, 1024, 64], 32, 16, 4)
+    rec, n = E.emit_edge_records(g, lay, 16, ids, d, torch.from_numpy(sk).to(gpu), 12)
+    num_points = int(gids.max()) + 1
+    SP.write_spill_artifacts(tmp_path / "cand", rec, n, shard_points=max(1, num_points // 3), segment_records=700)
+    back = SP.read_spill_artifacts(tmp_path / "cand", shard_points=max(1, num_points // 3))
+    assert len(back) == n
+    with H.HashPruneReducer(num_points, 64) as a, H.HashPruneReducer(num_points, 64) as b:
+        a.insert(rec, n)
+        b.insert(back)
+        _same(_gpu_slots(b), _gpu_slots(a), "spilled records")
