@@ -506,6 +506,25 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
                               uint32_t row_stride, uint32_t start, uint64_t num_frozen_pts, void *out,
                               uint64_t out_capacity, uint64_t *index_size, void *stream);
 
+/* ---- assignment-task capture ------------------------------------------------
+ * The partition side of the TESSA capture (the in-kernel sampler
+ * gpu_tessa_capture_assignment, compute_backend.rs:5415-5546): with capture
+ * on (min_members > 0; the reference samples tasks of >= 256 members and 1..128
+ * leaders), each run_subtree records every assignment pass of a node with at
+ * least min_members rows: depth, retry (attempt), r_h (fanout), padded_dim,
+ * members and leaders as global ids, in pass order.  Nodes of a small root
+ * (one kernel, <= leaf_max rows) are not recorded.  Fetch after the run: a
+ * first call with tasks and ids NULL gives the counts.  The bottom-k
+ * selection and the fixture files are the host sampler's (tessa_capture.rs). */
+typedef struct tessa_captured_assignment {
+    uint32_t depth, retry, r_h, padded_dim, member_count, leader_count;
+    uint64_t member_offset, leader_offset;  /* into ids[] */
+} tessa_captured_assignment;
+tessa_status tessa_session_set_assignment_capture(tessa_session *s, uint32_t min_members);
+tessa_status tessa_session_captured_assignments(tessa_session *s, tessa_captured_assignment *tasks,
+                                                uint64_t task_capacity, uint32_t *ids, uint64_t id_capacity,
+                                                uint64_t *task_count, uint64_t *id_count);
+
 /* ---- global D0 assignment: task formation above the subtrees --------------
  * The GPU-D0 SQ8 assignment (shear-core/src/algorithm/pipnn/compute_backend.rs:
  * sq8_global_d0_*_partial_kernel :18016-18275 + the tile merge :18446-18511;

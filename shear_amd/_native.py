@@ -262,6 +262,12 @@ RESIDENT_F32, RESIDENT_SQ8, RESIDENT_SQ4 = 0, 1, 2
 D0_LEADER_SOURCES = ("capacity", "quality_floor", "root_leader_cap")
 
 
+class CapturedAssignment(C.Structure):
+    _fields_ = [("depth", C.c_uint32), ("retry", C.c_uint32), ("r_h", C.c_uint32), ("padded_dim", C.c_uint32),
+                ("member_count", C.c_uint32), ("leader_count", C.c_uint32), ("member_offset", C.c_uint64),
+                ("leader_offset", C.c_uint64)]
+
+
 # Every symbol include/tessa_hip.h declares, with its ctypes signature.
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -319,6 +325,8 @@ SIGNATURES = {
     "tessa_d0_plan_root_leaders": (D0LeaderPlan, [_U64, _U64, C.POINTER(D0Thresholds), _U64, _U64]),
     "tessa_d0_split_leader_count": (_U64, [_U64, C.POINTER(D0Thresholds)]),
     "tessa_d0_observe_child_sizes": (D0ChildSummary, [_P, _U64, C.POINTER(D0Thresholds)]),
+    "tessa_session_set_assignment_capture": (TessaStatus, [_P, _U32]),
+    "tessa_session_captured_assignments": (TessaStatus, [_P, _P, _U64, _P, _U64, C.POINTER(_U64), C.POINTER(_U64)]),
     "tessa_graph_search": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P]),
 }
 

@@ -21,8 +21,8 @@ finalize step of tessa_replay.rs:240-318:
 The reference samples inside its persistent kernel (compute_backend.rs:
 5415-5546); here the leaf layout of a subtree run is already in HBM, so
 ``observe_subtree_leaves`` samples it from the host after the run.
-Assignment tasks are observed when the caller has them (the partition's
-large-node passes are not exported by this build's kernels).
+Assignment tasks come from the partition's level loop
+(``SubtreeSession.set_assignment_capture``, ``observe_captured_assignments``).
 """
 from __future__ import annotations
 
@@ -265,6 +265,16 @@ def observe_subtree_leaves(sampler: TessaCaptureSampler, out, global_ids, padded
             continue
         k = min(out.k, n - 1)
         kept += sampler.observe_leaf(LeafTask(0, 0, k, padded_dim, g[rows[s:s + n]].tolist()))
+    return kept
+
+
+def observe_captured_assignments(sampler: TessaCaptureSampler, session) -> int:
+    """Observe the assignment passes a SubtreeSession recorded in its last run
+    (``set_assignment_capture``).  Returns the number kept."""
+    kept = 0
+    for t in session.captured_assignments():
+        kept += sampler.observe_assignment(AssignmentTask(0, 0, t["depth"], t["retry"], t["r_h"], t["padded_dim"],
+                                                          t["member_ids"].tolist(), t["leader_ids"].tolist()))
     return kept
 
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace tessa {
 
 constexpr uint32_t kPartMaxLeaders = 128;  // GPU_QUEUE_LEADER_STRIDE compute_backend.rs:371
@@ -108,6 +110,20 @@ struct PartResult {
     uint32_t count_launches;
 };
 
+// Assignment tasks seen by the COUNT passes (capture, host side): per task
+// depth, attempt, fanout and its member / leader resident rows.  Filled only
+// when a PartCapture is passed; tasks outside the capture bins (fewer than
+// min_members members, no leaders or more than 128) are not kept.
+struct PartCaptureTask {
+    uint32_t depth, retry, r_h, member_count, leader_count;
+    uint64_t member_offset, leader_offset;  // into rows[]
+};
+struct PartCapture {
+    uint32_t min_members = 256;
+    std::vector<PartCaptureTask> tasks;
+    std::vector<uint32_t> rows;  // members then leaders of each task, resident rows
+};
+
 // Workspace sizes for `rows` resident rows with root fanout `famp`.
 void partition_capacity(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_t *arena_cap, uint32_t *node_cap,
                         uint64_t *item_cap);
@@ -115,6 +131,7 @@ void partition_capacity(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_
 // Runs the whole partition on `stream` (host-synchronising between levels).
 // Returns 0, or -1 on a launch failure, -2 when the level loop exceeds its
 // bound, -3 when a workspace capacity is exceeded before launch.
-int run_partition(const PartArgs &a, hipStream_t stream, LevelHeader *host_hdr, PartResult *res);
+int run_partition(const PartArgs &a, hipStream_t stream, LevelHeader *host_hdr, PartResult *res,
+                  PartCapture *capture = nullptr);
 
 }  // namespace tessa

@@ -1120,7 +1120,33 @@ void partition_capacity(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_
     *item_cap = ac / kPartItemRows + nc + 1u;
 }
 
-int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res) {
+// Copy the level's counting nodes (members and leaders, resident rows) to the
+// host before a COUNT pass; every launch on `s` before it has completed.
+static int capture_level(const PartArgs &a, hipStream_t s, uint32_t cur, uint32_t level_nodes, PartCapture *cap) {
+    std::vector<NodeDesc> nodes(level_nodes);
+    if (hipMemcpyAsync(nodes.data(), a.nodes[cur], level_nodes * sizeof(NodeDesc), hipMemcpyDeviceToHost, s) !=
+            hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return -1;
+    for (uint32_t ni = 0; ni < level_nodes; ++ni) {
+        const NodeDesc &nd = nodes[ni];
+        if (nd.status != kNodeCounting || nd.n < cap->min_members || nd.num_leaders == 0 ||
+            nd.num_leaders > kPartMaxLeaders)
+            continue;
+        PartCaptureTask t{nd.depth, nd.attempt, nd.fanout, nd.n, nd.num_leaders, cap->rows.size(), 0};
+        cap->rows.resize(cap->rows.size() + nd.n + nd.num_leaders);
+        t.leader_offset = t.member_offset + nd.n;
+        if (hipMemcpyAsync(cap->rows.data() + t.member_offset, a.arena[cur] + nd.row_start, nd.n * 4ull,
+                           hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemcpyAsync(cap->rows.data() + t.leader_offset, a.leaders + (uint64_t)ni * kPartMaxLeaders,
+                           nd.num_leaders * 4ull, hipMemcpyDeviceToHost, s) != hipSuccess)
+            return -1;
+        cap->tasks.push_back(t);
+    }
+    return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
+}
+
+int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture) {
     *res = PartResult{};
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return -1;
@@ -1161,6 +1187,7 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
         if (hipGetLastError() != hipSuccess) return -1;
         uint32_t attempt = 0;
         for (; attempt < 16u; ++attempt) {
+            if (capture && capture_level(a, s, cur, level_nodes, capture)) return -1;
             if (launch_count(a, cur, level_nodes, grid, s)) return -1;
             res->count_launches += 1;
             hipLaunchKernelGGL(emit_kernel, dim3(level_nodes), dim3(128), 0, s, a, cur, level_nodes);

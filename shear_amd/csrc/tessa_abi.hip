@@ -497,6 +497,9 @@ struct tessa_session {
     uint64_t next_seq = 1;
     // side stream for the results' D2H copies (default priority)
     hipStream_t copy_stream = nullptr;
+    // assignment tasks of the last run's COUNT passes, when capture is on
+    uint32_t capture_min_members = 0;  // 0: off
+    tessa::PartCapture capture;
 };
 
 namespace {
@@ -1041,7 +1044,11 @@ static tessa_status tessa_session_run_subtree_locked(tessa_session *s, const tes
 
     TESSA_HIP_TRY(hipEventRecord(s->ev0, s->stream));
     PartResult pr{};
-    const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr);
+    s->capture.tasks.clear();
+    s->capture.rows.clear();
+    s->capture.min_members = s->capture_min_members;
+    const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr,
+                                 s->capture_min_members ? &s->capture : nullptr);
     if (rc != 0)
         return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
                            rc == -2 ? "level/attempt bound exceeded"
@@ -1349,6 +1356,46 @@ tessa_status tessa_session_wait(tessa_session *s, uint64_t seq, tessa_subtree_ho
     out->partition_ms = slot.partition_ms;
     out->leaf_ms = slot.leaf_ms;
     return slot.status;
+}
+
+tessa_status tessa_session_set_assignment_capture(tessa_session *s, uint32_t min_members) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    s->capture_min_members = min_members;
+    s->capture.tasks.clear();
+    s->capture.rows.clear();
+    return ok_status();
+}
+
+tessa_status tessa_session_captured_assignments(tessa_session *s, tessa_captured_assignment *tasks,
+                                                uint64_t task_capacity, uint32_t *ids, uint64_t id_capacity,
+                                                uint64_t *task_count, uint64_t *id_count) {
+    if (!s || !task_count || !id_count) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: null argument");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    *task_count = s->capture.tasks.size();
+    *id_count = s->capture.rows.size();
+    if (!tasks && !ids) return ok_status();
+    if (task_capacity < *task_count || id_capacity < *id_count || !tasks || !ids)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: outputs of %llu tasks / %llu ids below %llu / %llu",
+                           (unsigned long long)task_capacity, (unsigned long long)id_capacity,
+                           (unsigned long long)*task_count, (unsigned long long)*id_count);
+    // resident rows -> global ids
+    std::vector<uint32_t> gids(s->rows);
+    if (s->rows) {
+        TESSA_HIP_TRY(hipMemcpyAsync(gids.data(), s->gids, s->rows * 4ull, hipMemcpyDeviceToHost, s->stream));
+        TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+    }
+    for (uint64_t i = 0; i < *id_count; ++i) {
+        const uint32_t r = s->capture.rows[i];
+        if (r >= s->rows) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: row %u outside the resident set", r);
+        ids[i] = gids[r];
+    }
+    for (uint64_t t = 0; t < *task_count; ++t) {
+        const tessa::PartCaptureTask &c = s->capture.tasks[t];
+        tasks[t] = tessa_captured_assignment{c.depth, c.retry, c.r_h, s->padded_dim, c.member_count, c.leader_count,
+                                             c.member_offset, c.leader_offset};
+    }
+    return ok_status();
 }
 
 tessa_status tessa_session_release(tessa_session *s, uint64_t seq) {

@@ -178,6 +178,29 @@ class SubtreeSession:
         est = int(plan.max_leaf_rows) * (4 + k * 8) + int(plan.max_leaf_count) * 16
         return DeferredGpuSubtreeTopK(est, _PinnedScatter(self, int(seq.value), gids, params, owned))
 
+    def set_assignment_capture(self, min_members: int = 256) -> None:
+        """Record the assignment passes of nodes with >= min_members rows in
+        each following run (0: off); the partition side of the TESSA capture
+        (compute_backend.rs:5415-5546)."""
+        N.check(self._lib.tessa_session_set_assignment_capture(self._h, min_members), "assignment capture")
+
+    def captured_assignments(self) -> list[dict]:
+        """The last run's captured passes in pass order: depth, retry, r_h,
+        padded_dim, member_ids and leader_ids (global ids)."""
+        nt, ni = C.c_uint64(0), C.c_uint64(0)
+        N.check(self._lib.tessa_session_captured_assignments(self._h, None, 0, None, 0, C.byref(nt), C.byref(ni)),
+                "captured assignments")
+        tasks = (N.CapturedAssignment * max(nt.value, 1))()
+        ids = np.zeros(max(ni.value, 1), np.uint32)
+        N.check(self._lib.tessa_session_captured_assignments(self._h, tasks, nt.value, ids.ctypes.data, ni.value,
+                                                             C.byref(nt), C.byref(ni)), "captured assignments")
+        out = []
+        for t in tasks[: nt.value]:
+            out.append({"depth": t.depth, "retry": t.retry, "r_h": t.r_h, "padded_dim": t.padded_dim,
+                        "member_ids": ids[t.member_offset: t.member_offset + t.member_count].copy(),
+                        "leader_ids": ids[t.leader_offset: t.leader_offset + t.leader_count].copy()})
+        return out
+
     def upload_device(self, sq8, global_ids: torch.Tensor):
         """Resident set from device tensors (an Sq8Matrix and int32-viewed u32
         global ids): a device-to-device copy into the session."""

@@ -58,3 +58,63 @@ def test_capture_and_replay_of_subtree_leaves(gpu, orc, tmp_path):
     want_ids, want_d = orc.leaf_topk(codes, scales, norms, gids, members, offs, counts, k)
     ids, d, _ = run_leaf(to_dev_sq8(codes, scales, norms, dim), gids, members, offs, counts, k, N.EXEC_MFMA)
     assert_same(ids, d, want_ids, want_d, "captured leaf tasks")
+
+
+def test_assignment_capture_and_replay(gpu, orc, tmp_path):
+    # the partition's assignment passes, captured from the level loop, replayed
+    # through the assignment kernel: bit-exact vs the oracle; then sampled and
+    # written as capture fixtures
+    import torch
+
+    from shear_amd import tessa as T
+
+    n, dim = 20000, 64
+    x = datagen.gmm_numpy(n, dim, 16, 0.3, 21)
+    codes, scales, norms = orc.quantize(x)
+    gids = np.random.default_rng(21).permutation(1 << 20)[:n].astype(np.uint32)
+    sess = S.SubtreeSession(0)
+    sess.upload(codes, scales, norms, gids, dim)
+    sess.set_assignment_capture(256)
+    # four leaders per node: the root's children (~10k rows) are large nodes too,
+    # so passes at depth 1 go through the level loop as well
+    sess.run(S.GpuSubtreePartitionRequest(point_ids=gids, parent_points=n, min_recurse_size=64),
+             S.PiPNNSubtreeParams(leaf_knn=8, c_max=1024, fanout_second=2, psamp_fraction=0.01, max_leaders=4,
+                                  random_seed=9))
+    tasks = sess.captured_assignments()
+    assert tasks and tasks[0]["depth"] == 0 and tasks[0]["retry"] == 0
+    assert sorted(tasks[0]["member_ids"].tolist()) == sorted(gids.tolist())  # the root holds every row once
+    gset = set(gids.tolist())
+    for t in tasks:
+        assert len(t["member_ids"]) >= 256 and 1 <= len(t["leader_ids"]) <= 128 and 1 <= t["r_h"] <= 4
+        assert t["padded_dim"] == codes.shape[1] and set(t["leader_ids"].tolist()) <= gset
+    assert any(t["depth"] > 0 for t in tasks)
+
+    row_of = np.zeros(1 << 20, np.int64)
+    row_of[gids] = np.arange(n)
+    members, leaders, mo, mc, lo, lc, rh = [], [], [], [], [], [], []
+    for t in tasks:
+        mo.append(len(members))
+        mc.append(len(t["member_ids"]))
+        members += row_of[t["member_ids"]].tolist()
+        lo.append(len(leaders))
+        lc.append(len(t["leader_ids"]))
+        leaders += row_of[t["leader_ids"]].tolist()
+        rh.append(t["r_h"])
+    lay = T.AssignLayouts.from_host(members, leaders, mo, mc, lo, lc, rh)
+    ids, d, ctr = T.assignment_replay(to_dev_sq8(codes, scales, norms, dim),
+                                      torch.from_numpy(gids.view(np.int32)).to(gpu), lay)
+    torch.cuda.synchronize()
+    want_ids, want_d = orc.assign_replay(codes, scales, norms, gids, members, leaders, mo, mc, lo, lc, rh)
+    assert_same(ids.cpu().numpy().view(np.uint32), d.cpu().numpy(), want_ids, want_d, "captured assignment tasks")
+
+    sampler = CP.TessaCaptureSampler(42)
+    kept = CP.observe_captured_assignments(sampler, sess)
+    sel = sampler.finish()
+    # bins keep their 16 best (priority, hash): later tasks can evict earlier ones
+    assert 0 < len(sel.assignment_tasks) <= kept and sum(map(sum, sel.bin_counts.assignment_observed)) == len(tasks)
+    ds = {"canonical_base_path": "/data/base.fbin", "rows": 1 << 20, "dimension": dim, "header_sha256": "ab" * 32}
+    prov = {"seed": 42, "git_commit": "local", "binary_sha256": "cd" * 32, "command_sha256": "ef" * 32,
+            "root_leader_hash": 1, "d0_partition_hash": 2, "d0_task_list_hash": 3}
+    CP.write_tessa_capture(tmp_path, ds, prov, sel)
+    assert len(CP.load_tessa_capture(tmp_path, ds)[1].assignment_tasks) == len(sel.assignment_tasks)
+    sess.set_assignment_capture(0)
