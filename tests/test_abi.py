@@ -53,3 +53,39 @@ def test_struct_layouts_match_header_sizes():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         N.load(tmp_path / "absent.so")
+
+
+def test_struct_layouts_match_the_c_compiler(tmp_path):
+    # sizes and field offsets of the header's structs as gcc lays them out,
+    # against the ctypes mirrors
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    specs = {
+        "tessa_subtree_plan": (N.SubtreePlan, ["supported", "required_bytes", "budget_bytes"]),
+        "tessa_resident_admission": (N.ResidentAdmission, ["plan", "resident_device_bytes",
+                                                           "device_admission_budget_bytes"]),
+        "tessa_d0_thresholds": (N.D0Thresholds, ["c_gpu", "c_low"]),
+        "tessa_d0_leader_plan": (N.D0LeaderPlan, ["k_capacity", "source"]),
+        "tessa_d0_child_summary": (N.D0ChildSummary, ["max_rows", "small_rows"]),
+        "tessa_captured_assignment": (N.CapturedAssignment, ["depth", "leader_count", "member_offset",
+                                                             "leader_offset"]),
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for name, (_, fields) in specs.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for f in fields:
+            lines.append(f'printf("{name}.{f} %zu\\n", offsetof({name}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for name, (cls, fields) in specs.items():
+        assert int(got[name]) == C.sizeof(cls), name
+        for f in fields:
+            assert int(got[f"{name}.{f}"]) == getattr(cls, f).offset, f"{name}.{f}"
