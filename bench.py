@@ -184,7 +184,7 @@ def main() -> int:
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": INT8_PEAK_TOPS,
-            "unit": "TFLOP/s",
+            "unit": "TOPS",
             "frac": round(achieved / INT8_PEAK_TOPS, 4),
             "traffic": traffic,
             "traffic_source": os.path.relpath(args.traffic_json, HERE) if traffic is not None else None,

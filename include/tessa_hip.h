@@ -515,7 +515,13 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
  * members and leaders as global ids, in pass order.  Nodes of a small root
  * (one kernel, <= leaf_max rows) are not recorded.  Fetch after the run: a
  * first call with tasks and ids NULL gives the counts.  The bottom-k
- * selection and the fixture files are the host sampler's (tessa_capture.rs). */
+ * selection and the fixture files are the host sampler's (tessa_capture.rs).
+ * The session keeps the passes of its most recent subtree run only: every
+ * run (synchronous, or a submitted job when the worker starts it) replaces
+ * them, and an SQ8 upload clears them.  Ids are translated to global ids
+ * when the run ends, so they name the resident set that run used.  With
+ * submissions, fetch after tessa_session_wait of the job whose passes are
+ * wanted and before the next job is submitted. */
 typedef struct tessa_captured_assignment {
     uint32_t depth, retry, r_h, padded_dim, member_count, leader_count;
     uint64_t member_offset, leader_offset;  /* into ids[] */

@@ -115,6 +115,21 @@ class SubtreeCfg(C.Structure):
         ("max_leaf_rows", C.c_uint64),
         ("psamp_fraction", C.c_float),
         ("seed", C.c_uint64),
+        ("trace_min_members", C.c_uint32),
+        ("trace", C.c_void_p),
+    ]
+
+
+class PassTrace(C.Structure):
+    """orc_pass_trace (tessa_oracle.h)."""
+
+    _fields_ = [
+        ("passes", C.POINTER(C.c_uint32)),
+        ("pass_len", C.c_size_t),
+        ("pass_cap", C.c_size_t),
+        ("rows", C.POINTER(C.c_uint32)),
+        ("row_len", C.c_size_t),
+        ("row_cap", C.c_size_t),
     ]
 
 
@@ -292,8 +307,12 @@ def subtree_partition(codes, scales, norms, *, seed: int, root_depth: int = 0, m
                       max_leaders: int = 128, fanout_second: int = 1, leaf_min: int = 64, leaf_max: int = 256,
                       small_node_limit: int = 4096, psamp_fraction: float = 0.001, root_leaders=None,
                       large_scratch_rows: int | None = None, max_leaf_count: int | None = None,
-                      max_leaf_rows: int | None = None):
-    """-> (leaves: list of u32 arrays (resident rows, in order), counters u64[159])."""
+                      max_leaf_rows: int | None = None, trace_min_members: int = 0):
+    """-> (leaves: list of u32 arrays (resident rows, in order), counters u64[159]).
+
+    With trace_min_members > 0 a third value is returned: the COUNT passes of
+    nodes with at least that many rows, as a list of dicts (depth, attempt,
+    fanout, members, leaders; resident rows), in the oracle's walk order."""
     codes = np.ascontiguousarray(codes, np.int8)
     scales = np.ascontiguousarray(scales, np.float32)
     norms = np.ascontiguousarray(norms, np.float32)
@@ -302,10 +321,12 @@ def subtree_partition(codes, scales, norms, *, seed: int, root_depth: int = 0, m
     roots = np.zeros(0, np.uint32) if root_leaders is None else np.ascontiguousarray(root_leaders, np.uint32)
     mlr = max_leaf_rows if max_leaf_rows is not None else max(rows * famp, 1)
     mlc = max_leaf_count if max_leaf_count is not None else max(rows * famp, 1)
+    trace = PassTrace()
     cfg = SubtreeCfg(roots.ctypes.data if len(roots) else None, len(roots), root_depth, max_depth, max_leaders,
                      fanout_second, leaf_min, leaf_max, small_node_limit,
                      large_scratch_rows if large_scratch_rows is not None else max(rows, 1) * famp,
-                     mlc, mlr, np.float32(psamp_fraction).item(), seed & (2**64 - 1))
+                     mlc, mlr, np.float32(psamp_fraction).item(), seed & (2**64 - 1), trace_min_members,
+                     C.cast(C.pointer(trace), C.c_void_p) if trace_min_members > 0 else None)
     leaf_rows = np.zeros(max(mlr, 1), np.uint32)
     starts = np.zeros(max(mlc, 1), np.uint64)
     sizes = np.zeros(max(mlc, 1), np.uint64)
@@ -314,13 +335,25 @@ def subtree_partition(codes, scales, norms, *, seed: int, root_depth: int = 0, m
     lr = C.c_uint64(0)
     rc = lib().orc_subtree_partition(_p(codes), _p(scales), _p(norms), rows, pd, C.byref(cfg), _p(leaf_rows),
                                      _p(starts), _p(sizes), _p(ctr), C.byref(lc), C.byref(lr))
+    passes = None
+    if trace_min_members > 0:
+        passes = []
+        w = np.ctypeslib.as_array(trace.passes, (trace.pass_len,)).copy() if trace.pass_len else np.zeros(0, np.uint32)
+        r = np.ctypeslib.as_array(trace.rows, (trace.row_len,)).copy() if trace.row_len else np.zeros(0, np.uint32)
+        lib().orc_pass_trace_free(C.byref(trace))
+        off = 0
+        for i in range(0, len(w), 5):
+            depth, attempt, fanout, nm, nl = (int(v) for v in w[i:i + 5])
+            passes.append(dict(depth=depth, attempt=attempt, fanout=fanout, members=r[off:off + nm],
+                               leaders=r[off + nm:off + nm + nl]))
+            off += nm + nl
     if rc != 0:
         raise ValueError(f"orc_subtree_partition failed: {rc}")
     n_leaves = min(lc.value, mlc)
     if ctr[7] != 0:
-        return None, ctr
+        return (None, ctr, passes) if trace_min_members > 0 else (None, ctr)
     leaves = [leaf_rows[int(starts[i]): int(starts[i]) + int(sizes[i])].copy() for i in range(n_leaves)]
-    return leaves, ctr
+    return (leaves, ctr, passes) if trace_min_members > 0 else (leaves, ctr)
 
 
 # spill_hashprune.rs:137-145 SpillRecord16 (little-endian, 16 bytes)

@@ -210,7 +210,22 @@ typedef struct orc_subtree_cfg {
     uint64_t max_leaf_rows;
     float psamp_fraction;         /* params.psamp_fraction as f32 */
     uint64_t seed;                /* orc_subtree_root_seed(...) */
+    /* Optional trace of the COUNT passes of nodes with >= trace_min_members
+     * rows (NULL: off): the passes the reference's in-kernel sampler sees
+     * (compute_backend.rs:5415-5546), for checking a GPU capture. */
+    uint32_t trace_min_members;
+    struct orc_pass_trace *trace;
 } orc_subtree_cfg;
+
+/* Growable trace: per pass 5 words (depth, attempt, fanout, members,
+ * leaders) in `passes`; members then leaders (resident rows) in `rows`. */
+typedef struct orc_pass_trace {
+    uint32_t *passes;
+    size_t pass_len, pass_cap;
+    uint32_t *rows;
+    size_t row_len, row_cap;
+} orc_pass_trace;
+void orc_pass_trace_free(orc_pass_trace *t);
 
 /* compute_backend.rs:7044-7075, 7082-7101, 7103-7121 */
 float orc_adaptive_psamp(float base, uint32_t cluster_size, uint32_t depth);

@@ -173,6 +173,46 @@ static uint32_t rel_depth(const pctx *c, uint32_t depth) {
     return depth >= c->cfg->root_depth ? depth - c->cfg->root_depth : 0u;
 }
 
+static int grow_u32(uint32_t **v, size_t *cap, size_t need) {
+    if (need <= *cap) return 0;
+    size_t cap2 = *cap ? *cap : 1024;
+    while (cap2 < need) cap2 *= 2;
+    uint32_t *p = (uint32_t *)realloc(*v, cap2 * 4);
+    if (!p) return -1;
+    *v = p;
+    *cap = cap2;
+    return 0;
+}
+
+void orc_pass_trace_free(orc_pass_trace *t) {
+    if (!t) return;
+    free(t->passes);
+    free(t->rows);
+    memset(t, 0, sizeof(*t));
+}
+
+/* One COUNT pass into the trace (test infrastructure; no reference code). */
+static void trace_pass(pctx *c, const pnode *nd, uint32_t attempt, uint32_t fanout, const uint32_t *leaders,
+                       uint32_t nl) {
+    orc_pass_trace *t = c->cfg->trace;
+    if (!t || nd->n < c->cfg->trace_min_members) return;
+    if (grow_u32(&t->passes, &t->pass_cap, t->pass_len + 5) ||
+        grow_u32(&t->rows, &t->row_cap, t->row_len + nd->n + nl)) {
+        c->oom = 1;
+        return;
+    }
+    uint32_t *w = t->passes + t->pass_len;
+    w[0] = nd->depth;
+    w[1] = attempt;
+    w[2] = fanout;
+    w[3] = nd->n;
+    w[4] = nl;
+    t->pass_len += 5;
+    memcpy(t->rows + t->row_len, nd->rows, (size_t)nd->n * 4);
+    memcpy(t->rows + t->row_len + nd->n, leaders, (size_t)nl * 4);
+    t->row_len += (size_t)nd->n + nl;
+}
+
 /* compute_backend.rs:12456-12646 (stage) + :15047-15727 (COUNT, EMIT,
  * SCATTER, PUBLISH) for one node. */
 static void process_large(pctx *c, const pnode *nd) {
@@ -218,6 +258,7 @@ static void process_large(pctx *c, const pnode *nd) {
     int balanced = 0;
     for (;;) {
         memset(counts, 0, sizeof(counts));
+        trace_pass(c, nd, attempt, fanout, leaders, nl);
         c->ctr[ORC_P_LARGE_PHYSICAL_TILES] += (n + 15u) / 16u;
         /* rows are independent: OpenMP over rows, counted afterwards */
 #pragma omp parallel for schedule(static)

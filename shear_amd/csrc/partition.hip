@@ -1128,20 +1128,33 @@ static int capture_level(const PartArgs &a, hipStream_t s, uint32_t cur, uint32_
             hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return -1;
+    // First pass: the level's tasks and their row offsets, so the host
+    // buffer is sized once before any copy into it is queued (a resize
+    // between queued copies could move the buffer under them).
+    auto wanted = [&](const NodeDesc &nd) {
+        return nd.status == kNodeCounting && nd.n >= cap->min_members && nd.num_leaders != 0 &&
+               nd.num_leaders <= kPartMaxLeaders;
+    };
+    const size_t first_task = cap->tasks.size();
+    uint64_t total = cap->rows.size();
     for (uint32_t ni = 0; ni < level_nodes; ++ni) {
         const NodeDesc &nd = nodes[ni];
-        if (nd.status != kNodeCounting || nd.n < cap->min_members || nd.num_leaders == 0 ||
-            nd.num_leaders > kPartMaxLeaders)
-            continue;
-        PartCaptureTask t{nd.depth, nd.attempt, nd.fanout, nd.n, nd.num_leaders, cap->rows.size(), 0};
-        cap->rows.resize(cap->rows.size() + nd.n + nd.num_leaders);
-        t.leader_offset = t.member_offset + nd.n;
+        if (!wanted(nd)) continue;
+        PartCaptureTask t{nd.depth, nd.attempt, nd.fanout, nd.n, nd.num_leaders, total, total + nd.n};
+        total += (uint64_t)nd.n + nd.num_leaders;
+        cap->tasks.push_back(t);
+    }
+    cap->rows.resize(total);
+    size_t ti = first_task;
+    for (uint32_t ni = 0; ni < level_nodes; ++ni) {
+        const NodeDesc &nd = nodes[ni];
+        if (!wanted(nd)) continue;
+        const PartCaptureTask &t = cap->tasks[ti++];
         if (hipMemcpyAsync(cap->rows.data() + t.member_offset, a.arena[cur] + nd.row_start, nd.n * 4ull,
                            hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipMemcpyAsync(cap->rows.data() + t.leader_offset, a.leaders + (uint64_t)ni * kPartMaxLeaders,
                            nd.num_leaders * 4ull, hipMemcpyDeviceToHost, s) != hipSuccess)
             return -1;
-        cap->tasks.push_back(t);
     }
     return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
 }

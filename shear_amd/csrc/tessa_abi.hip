@@ -499,7 +499,8 @@ struct tessa_session {
     hipStream_t copy_stream = nullptr;
     // assignment tasks of the last run's COUNT passes, when capture is on
     uint32_t capture_min_members = 0;  // 0: off
-    tessa::PartCapture capture;
+    tessa::PartCapture capture;        // rows[] hold global ids once the run has finished
+    uint32_t capture_padded_dim = 0;
 };
 
 namespace {
@@ -609,6 +610,9 @@ static tessa_status tessa_session_upload_sq8_locked(tessa_session *s, const tess
     TESSA_HIP_TRY(hipSetDevice(s->device));
     TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
     free_sq8(s);
+    // captured passes name rows of the set being replaced
+    s->capture.tasks.clear();
+    s->capture.rows.clear();
     const uint64_t rows = host->rows;
     if (hipMalloc(&s->codes, rows * host->padded_dim) != hipSuccess ||
         hipMalloc(&s->scales, rows * 4) != hipSuccess || hipMalloc(&s->norms, rows * 4) != hipSuccess ||
@@ -1053,6 +1057,19 @@ static tessa_status tessa_session_run_subtree_locked(tessa_session *s, const tes
         return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
                            rc == -2 ? "level/attempt bound exceeded"
                                     : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+    if (s->capture_min_members && !s->capture.rows.empty()) {
+        // Resident rows -> global ids now, while the resident set is the one
+        // this run used (a later upload may replace it before the fetch).
+        std::vector<uint32_t> gids(s->rows);
+        TESSA_HIP_TRY(hipMemcpyAsync(gids.data(), s->gids, s->rows * 4ull, hipMemcpyDeviceToHost, s->stream));
+        TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+        for (uint32_t &r : s->capture.rows) {
+            if (r >= s->rows)
+                return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: row %u outside the resident set", r);
+            r = gids[r];
+        }
+    }
+    s->capture_padded_dim = s->padded_dim;
     TESSA_HIP_TRY(hipEventRecord(s->ev1, s->stream));
     uint64_t c[TESSA_SUBTREE_COUNTER_WORDS];
     TESSA_HIP_TRY(hipMemcpyAsync(c, s->part_counters, sizeof(c), hipMemcpyDeviceToHost, s->stream));
@@ -1379,21 +1396,12 @@ tessa_status tessa_session_captured_assignments(tessa_session *s, tessa_captured
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: outputs of %llu tasks / %llu ids below %llu / %llu",
                            (unsigned long long)task_capacity, (unsigned long long)id_capacity,
                            (unsigned long long)*task_count, (unsigned long long)*id_count);
-    // resident rows -> global ids
-    std::vector<uint32_t> gids(s->rows);
-    if (s->rows) {
-        TESSA_HIP_TRY(hipMemcpyAsync(gids.data(), s->gids, s->rows * 4ull, hipMemcpyDeviceToHost, s->stream));
-        TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
-    }
-    for (uint64_t i = 0; i < *id_count; ++i) {
-        const uint32_t r = s->capture.rows[i];
-        if (r >= s->rows) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "capture: row %u outside the resident set", r);
-        ids[i] = gids[r];
-    }
+    // global ids, translated when the run finished
+    std::memcpy(ids, s->capture.rows.data(), *id_count * sizeof(uint32_t));
     for (uint64_t t = 0; t < *task_count; ++t) {
         const tessa::PartCaptureTask &c = s->capture.tasks[t];
-        tasks[t] = tessa_captured_assignment{c.depth, c.retry, c.r_h, s->padded_dim, c.member_count, c.leader_count,
-                                             c.member_offset, c.leader_offset};
+        tasks[t] = tessa_captured_assignment{c.depth, c.retry, c.r_h, s->capture_padded_dim, c.member_count,
+                                             c.leader_count, c.member_offset, c.leader_offset};
     }
     return ok_status();
 }

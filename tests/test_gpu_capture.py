@@ -60,6 +60,61 @@ def test_capture_and_replay_of_subtree_leaves(gpu, orc, tmp_path):
     assert_same(ids, d, want_ids, want_d, "captured leaf tasks")
 
 
+def _oracle_passes(orc, codes, scales, norms, gids, *, seed, fan, leaf_max, psamp, max_leaders, min_members):
+    """The oracle partition's COUNT passes (resident rows mapped to global ids),
+    as sorted (depth, attempt, fanout, members, leaders) tuples."""
+    from shear_amd import subtree as S
+
+    n = len(gids)
+    plan = S.plan_subtree(n, 8, min(max_leaders, 128), fan, None, leaf_max)
+    rseed = orc.subtree_root_seed(seed, 0, n, n, 64)
+    leaves, ctr, passes = orc.subtree_partition(codes, scales, norms, seed=rseed, max_leaders=min(max_leaders, 128),
+                                                fanout_second=fan, leaf_min=plan.leaf_min, leaf_max=plan.leaf_max,
+                                                psamp_fraction=psamp, max_leaf_count=plan.max_leaf_count,
+                                                max_leaf_rows=plan.max_leaf_rows, trace_min_members=min_members)
+    assert leaves is not None, "oracle partition overflowed"
+    return sorted((p["depth"], p["attempt"], p["fanout"], tuple(gids[p["members"]].tolist()),
+                   tuple(gids[p["leaders"]].tolist())) for p in passes)
+
+
+def _gpu_passes(tasks):
+    return sorted((t["depth"], t["retry"], t["r_h"], tuple(t["member_ids"].tolist()), tuple(t["leader_ids"].tolist()))
+                  for t in tasks)
+
+
+CAPTURE_CASES = [
+    # n, dim, comps, sigma, fanout, leaf_max, psamp, max_leaders: the second forces split retries
+    (20000, 64, 16, 0.3, 2, 1024, 0.01, 4),
+    (8000, 32, 3, 0.05, 2, 512, 0.001, 2),
+]
+
+
+@pytest.mark.parametrize("case", CAPTURE_CASES, ids=["levels", "retries"])
+def test_assignment_capture_matches_oracle_passes(gpu, orc, case):
+    # every captured task is a COUNT pass the oracle's partition makes on the
+    # same rows: same depth, attempt, fanout, member set and order, leaders
+    n, dim, comps, sigma, fan, lmax, ps, ml = case
+    x = datagen.gmm_numpy(n, dim, comps, sigma, 21)
+    codes, scales, norms = orc.quantize(x)
+    gids = np.random.default_rng(21).permutation(1 << 20)[:n].astype(np.uint32)
+    sess = S.SubtreeSession(0)
+    sess.upload(codes, scales, norms, gids, dim)
+    sess.set_assignment_capture(256)
+    sess.run(S.GpuSubtreePartitionRequest(point_ids=gids, parent_points=n, min_recurse_size=64),
+             S.PiPNNSubtreeParams(leaf_knn=8, c_max=lmax, fanout_second=fan, psamp_fraction=ps, max_leaders=ml,
+                                  random_seed=9))
+    got = _gpu_passes(sess.captured_assignments())
+    want = _oracle_passes(orc, codes, scales, norms, gids, seed=9, fan=fan, leaf_max=lmax, psamp=ps,
+                          max_leaders=ml, min_members=256)
+    assert len(got) == len(want) and got == want, "captured passes differ from the oracle's COUNT passes"
+    if ml == 2:
+        assert any(p[1] > 0 for p in got), "the retry case made no retry pass"
+    # an upload clears the capture (its rows name the replaced set)
+    sess.upload(codes, scales, norms, gids, dim)
+    assert sess.captured_assignments() == []
+    sess.set_assignment_capture(0)
+
+
 def test_assignment_capture_and_replay(gpu, orc, tmp_path):
     # the partition's assignment passes, captured from the level loop, replayed
     # through the assignment kernel: bit-exact vs the oracle; then sampled and
@@ -81,6 +136,8 @@ def test_assignment_capture_and_replay(gpu, orc, tmp_path):
              S.PiPNNSubtreeParams(leaf_knn=8, c_max=1024, fanout_second=2, psamp_fraction=0.01, max_leaders=4,
                                   random_seed=9))
     tasks = sess.captured_assignments()
+    assert _gpu_passes(tasks) == _oracle_passes(orc, codes, scales, norms, gids, seed=9, fan=2, leaf_max=1024,
+                                                psamp=0.01, max_leaders=4, min_members=256)
     assert tasks and tasks[0]["depth"] == 0 and tasks[0]["retry"] == 0
     assert sorted(tasks[0]["member_ids"].tolist()) == sorted(gids.tolist())  # the root holds every row once
     gset = set(gids.tolist())
