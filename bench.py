@@ -129,7 +129,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     launch_ms = [a.elapsed_time(b) for a, b in evs]
-    ph = np.array(phases, dtype=np.float64)  # [steps, 3]: MFMA kernel, chain replay, exact re-run
+    ph = np.array(phases, dtype=np.float64)  # [steps, 4]: MFMA filter, select, chain replay, exact re-run
     T.raise_on_overflow(ctr, "leaf top-k")
     c = ctr.cpu().numpy()
     log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, launch median {np.median(launch_ms):.3f} ms")
@@ -194,8 +194,9 @@ def main() -> int:
             "kernel_ms_mean": round(float(np.mean(ph[:, 0])), 4),
             "kernel_ms_min": round(float(np.min(ph[:, 0])), 4),
             "kernel_ms_max": round(float(np.max(ph[:, 0])), 4),
-            "chain_replay_ms_mean": round(float(np.mean(ph[:, 1])), 4),
-            "exact_rerun_ms_mean": round(float(np.mean(ph[:, 2])), 4),
+            "select_ms_mean": round(float(np.mean(ph[:, 1])), 4),
+            "chain_replay_ms_mean": round(float(np.mean(ph[:, 2])), 4),
+            "exact_rerun_ms_mean": round(float(np.mean(ph[:, 3])), 4),
             "operator_ms_median": round(float(np.median(launch_ms)), 4),
         },
         "counters": {

@@ -41,20 +41,32 @@ struct LeafParams {
     uint4 *chain_pool;
     uint32_t *chain_pool_used;
     uint32_t chain_pool_capacity;
-    // MFMA kernel survivor log: one slot per persistent workgroup, holding
-    // log_capacity (raw dot, column) entries per thread.
+    // Work items are (leaf, block of kLeafBlockRows member rows); a batch is
+    // items [item_begin, item_begin + item_count) of leaf-major order, with
+    // blocks_per_leaf items per leaf.  The filter kernel writes, per block
+    // row, 2 * log_capacity survivor entries (raw dot, column) at
+    // survivor_log[((item - item_begin) * kLeafBlockRows + row) * 2 *
+    // log_capacity], entry e of the row's lane h at 2e + h, and a row_meta
+    // word set (threshold F bits, the two lanes' entry counts); the select
+    // kernel reads both.
+    uint32_t item_begin;
+    uint32_t item_count;
+    uint32_t blocks_per_leaf;
     uint2 *survivor_log;
     uint32_t log_capacity;
-    uint32_t log_slots;
+    uint4 *row_meta;
 };
 
-constexpr uint32_t kLeafLogCapacity = 128;
-constexpr uint32_t kLeafLogSlots = 2048;
+constexpr uint32_t kLeafBlockRows = 256;       // member rows per work item
+constexpr uint32_t kLeafFilterThreads = 512;   // filter workgroup: 8 waves, 32 rows each
+constexpr uint32_t kLeafLogCapacity = 128;     // survivor entries per filter thread
+constexpr uint64_t kLeafLogBytesPerItem = (uint64_t)kLeafFilterThreads * kLeafLogCapacity * 8u;
 
 // Host-side launchers (leaf_exact.hip / leaf_mfma.hip).
 int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream);
 int launch_leaf_exact_fallback(const LeafParams &p, hipStream_t stream);
 int launch_leaf_mfma(const LeafParams &p, hipStream_t stream);
+int launch_leaf_select(const LeafParams &p, hipStream_t stream);
 int launch_leaf_chain(const LeafParams &p, hipStream_t stream);
 int leaf_mfma_supported(uint32_t padded_dim, uint32_t max_leaf_rows);
 

@@ -1,25 +1,27 @@
-// leaf_mfma.hip -- SQ8 leaf all-pairs + per-row top-k on gfx950 int8 MFMA.
+// leaf_mfma.hip -- SQ8 leaf all-pairs filter on gfx950 int8 MFMA (the
+// first of the two kernels of the leaf operator; leaf_select.hip is the
+// second).
 //
 // Reference role: the WMMA leaf filter of gpu_persistent_subtree_topk_only
 // (compute_backend.rs:10389-10950 tile evaluation, :11841-12295 drain); the
-// result must equal RowTopK insertion over the columns in member order
-// (leaf_build.rs:887-957 with dco_sq_int8.rs:2950-2965 distances).
+// operator's result must equal RowTopK insertion over the columns in member
+// order (leaf_build.rs:887-957 with dco_sq_int8.rs:2950-2965 distances).
 //
 // Work item = (leaf, block of 256 member rows); a workgroup is 8 waves (one
-// workgroup per CU, two waves per SIMD), wave w owns 32 rows of the block.  The wave keeps its 32 rows' codes
-// in VGPRs for the whole K range as the MFMA "B" operand (N = rows);
-// 32-candidate column tiles are staged in LDS as the "A" operand (M =
-// candidates) and shared by the 8 waves.  With v_mfma_i32_32x32x32_i8 output
-// lane l holds row l%32 and candidates 8*(v/4) + 4*(l/32) + v%4 of the tile:
-// each row is served by a lane pair (l, l+32), each lane seeing half of the
-// row's candidates.  The grid is persistent; the 8 XCDs each walk a
-// contiguous range of work items, so a leaf's items share one L2.
+// workgroup per CU, two waves per SIMD), wave w owns 32 rows of the block.
+// The wave keeps its 32 rows' codes in VGPRs for the whole K range as the
+// MFMA "B" operand (N = rows); 32-candidate column tiles are staged in LDS
+// as the "A" operand (M = candidates) and shared by the 8 waves.  With
+// v_mfma_i32_32x32x32_i8 output lane l holds row l%32 and candidates
+// 8*(v/4) + 4*(l/32) + v%4 of the tile: each row is served by a lane pair
+// (l, l+32), each lane seeing half of the row's candidates.  The grid is
+// persistent; the 8 XCDs each walk a contiguous range of work items, so a
+// leaf's items share one L2.
 //
 // The column tiles of a block form one stream (phase A's sampled tiles, then
 // every tile for phase B), double buffered in LDS with one barrier per tile;
 // each tile's epilogue runs interleaved with the next tile's MFMAs.
 //
-// Selection (exact by construction, see the certificate below):
 //  * phase A: every 3rd (4th for wide leaves) column tile is evaluated and
 //    each lane keeps its 16 smallest exact distances (values only); the row
 //    threshold F is the pair's 24th (18th) smallest sampled distance plus
@@ -27,24 +29,12 @@
 //  * phase B: every column tile; a candidate passes when cs*dot meets the
 //    bound tau derived from F (a necessary condition for d <= F, evaluated in
 //    double with a rounding margin) and is appended (raw dot, column) to the
-//    lane's survivor log in global memory (128 entries per lane; a lane whose
-//    log overflows has its row re-run exactly);
-//  * final: the log is folded 16 entries at a time (exact distances, bitonic
-//    sort, merge into a sorted top-32 per lane); `disc` tracks the smallest
-//    distance a lane dropped; the pair's lists are merged into the sorted
-//    known sequence s_0 <= s_1 <= ...  Everything not known is > min(disc, F).
-//    Consecutive elements within 2e-5 form tie clusters.
-//    G = s_0..s_q, the prefix closed at the cluster holding s_{k-1}.  The row
-//    is certified when the next distance after s_q, known or dropped, lies
-//    more than 2e-5 above s_q, and every cluster inside G spans <= 2e-5.
-//    Then every candidate outside G is more than eps above every one inside,
-//    so the reference's bounded insertion over the whole row keeps exactly G's
-//    k best (candidates eps-separated from all kept ones can never enter in
-//    front of them or stay); and inside G the tie relation is an equivalence,
-//    so the comparator is a total order there: distance order, clusters
-//    ordered by global id.  A row whose G holds a chain (a cluster wider than
-//    2e-5) is queued, with G, for the chain replay kernel; uncertified rows are
-//    queued for the exact scalar kernel.
+//    row's survivor log in global memory (log_capacity entries per lane, the
+//    pair's entries interleaved);
+//  * end of item: F and both lanes' entry counts go to the row's row_meta
+//    words.  The select kernel folds the two logs, certifies the row and
+//    writes it, or queues it for the chain replay or the exact re-run; every
+//    candidate it does not see lies above F.
 #include <type_traits>
 #include <utility>
 
@@ -66,7 +56,6 @@ constexpr int kWaves = TESSA_LEAF_WAVES;  // waves per workgroup, 32 rows each
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerBlock = kWaves * 32;
 constexpr int kTileCols = 32;
-constexpr int kTop = 32;        // per-lane sorted list (registers)
 constexpr uint32_t kMaxLeafRows = 4096;
 constexpr float kFilterMargin = 3.0f * kTieEps;
 // Phase A samples every kSampleStride-th column tile; F is the pair's
@@ -118,17 +107,13 @@ struct Layout {
 #endif
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
-// LDS: a region holding two column tiles and each wave's 4 KB accumulator
-// scratch during the tile stream, overlaid afterwards by each wave's output
-// staging (32 rows x 32 slots of ids and distances); then the leaf's member
-// ids, scales, norms and global ids, and 64 bytes of scalars.
+// LDS: two column tiles and each wave's 4 KB accumulator scratch, then the
+// leaf's member ids, scales and norms, and 64 bytes of scalars.
 __host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes) {
-    return (2u * tile_bytes + kWaves * 16u * 64u * 4u) > (kWaves * 2u * 32u * kTop * 4u)
-               ? (2u * tile_bytes + kWaves * 16u * 64u * 4u)
-               : (kWaves * 2u * 32u * kTop * 4u);
+    return 2u * tile_bytes + kWaves * 16u * 64u * 4u;
 }
 __host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
-    return union_bytes(tile_bytes) + cols_cap * 16u + 64u;
+    return union_bytes(tile_bytes) + cols_cap * 12u + 64u;
 }
 
 // Compile-time loops: f(std::integral_constant<int, I>) for I in [B, E).
@@ -192,97 +177,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Compare-exchange on (key, payload) pairs; ascending when `up`.
-__device__ __forceinline__ void cex(float &a, uint32_t &pa, float &b, uint32_t &pb, bool up) {
-    const bool sw = up ? (b < a) : (a < b);
-    const float ta = a;
-    const uint32_t tpa = pa;
-    a = sw ? b : a;
-    pa = sw ? pb : pa;
-    b = sw ? ta : b;
-    pb = sw ? tpa : pb;
-}
-
-template <int N>
-__device__ __forceinline__ void bitonic_sort_kv(float (&v)[N], uint32_t (&p)[N]) {
-#pragma unroll
-    for (int k = 2; k <= N; k <<= 1) {
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const int l = i ^ j;
-                if (l > i) cex(v[i], p[i], v[l], p[l], (i & k) == 0);
-            }
-        }
-    }
-}
-
-template <int N>
-__device__ __forceinline__ void bitonic_merge_kv(float (&v)[N], uint32_t (&p)[N]) {
-#pragma unroll
-    for (int j = N >> 1; j > 0; j >>= 1) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const int l = i ^ j;
-            if (l > i) cex(v[i], p[i], v[l], p[l], true);
-        }
-    }
-}
-
-__device__ __forceinline__ int wave_max_i(int x) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) x = max(x, __shfl_xor(x, off));
-    return x;
-}
-
-// 32nd smallest of the union of two ascending 32-lists (own `a`, partner via
-// shuffle): min over i of max(a[i-1], b[31-i]).  Both lanes of a pair get the
-// same value.
-__device__ __forceinline__ float pair_kth32(const float (&a)[kTop]) {
-    float b[kTop];
-#pragma unroll
-    for (int m = 0; m < kTop; ++m) b[m] = __shfl_xor(a[m], 32);
-    float best = b[kTop - 1];
-#pragma unroll
-    for (int i = 1; i < kTop; ++i) best = fminf(best, fmaxf(a[i - 1], b[kTop - 1 - i]));
-    return fminf(best, a[kTop - 1]);
-}
-
-// Fold this thread's `staged` survivor-log entries (raw dot, column) into its
-// sorted top-32: exact distances are computed here, for survivors only.  The
-// loads are unconditional (entries past `staged` lie inside the thread's log
-// slot and are masked afterwards), so no per-entry branches are needed.
-__device__ __forceinline__ void fold_staged(const uint2 *stage, const float *cs, const float *cn, uint32_t ncols,
-                                            int staged, float rs, float rn, float (&topd)[kTop],
-                                            uint32_t (&topc)[kTop], float &disc) {
-    const int chunks = (wave_max_i(staged) + 15) / 16;
-    for (int ch = 0; ch < chunks; ++ch) {
-        float v[16];
-        uint32_t c[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int e = ch * 16 + i;
-            const uint2 s = stage[e];
-            const bool valid = e < staged;
-            const uint32_t col = (valid && s.y < ncols) ? s.y : 0u;
-            v[i] = valid ? leaf_l2((int)s.x, rs, rn, cs[col], cn[col]) : __builtin_inff();
-            c[i] = valid ? s.y : 0xffffu;
-        }
-        bitonic_sort_kv<16>(v, c);
-        // lower half of (top ascending) vs (chunk ascending, padded to 32, reversed)
-#pragma unroll
-        for (int i = 16; i < kTop; ++i) {
-            const float a = topd[i], b = v[kTop - 1 - i];
-            const bool sw = b < a;
-            disc = fminf(disc, sw ? a : b);  // the larger one leaves the list
-            topd[i] = sw ? b : a;
-            topc[i] = sw ? c[kTop - 1 - i] : topc[i];
-        }
-        bitonic_merge_kv<kTop>(topd, topc);
-    }
 }
 
 // Necessary condition for a candidate to pass d <= F, as a bound on cs * dot:
@@ -352,19 +246,16 @@ __device__ __forceinline__ float pair_kth(const float (&a)[N], int rsel) {
 }
 
 template <int KS>
-__global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t blocks_per_leaf,
-                                                              uint32_t total_work, uint32_t per_xcd) {
+__global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t per_xcd) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // Runtime layout: (tiles x2 | scratch, overlaid by stage) | members | scales | norms | global ids | misc.
+    // Runtime layout: tiles x2 | scratch | members | scales | norms | misc.
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
-    uint32_t *stage = reinterpret_cast<uint32_t *>(smem);  // per wave: 32 rows x k output ids, then distances
     uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + union_bytes(L::kTileBytes));
     float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
     float *cn_lds = cs_lds + cols_cap;
-    uint32_t *gid_lds = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);  // global id per member
-    uint32_t *misc = gid_lds + cols_cap;
+    uint32_t *misc = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
@@ -372,9 +263,6 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     const uint32_t j = lane & 31u;
     const uint32_t h = lane >> 5;
     const uint32_t cap = p.log_capacity;
-        // This thread's entries are contiguous, so the final fold reads 16 of
-    // them with immediate offsets from one address.
-    uint2 *slog = p.survivor_log + ((uint64_t)blockIdx.x * kThreads + tid) * cap;
 
     // Work items are (leaf, 256-row block).  Workgroups are dispatched
     // round-robin over the 8 XCDs: XCD x walks its own contiguous item range,
@@ -383,13 +271,19 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     const uint32_t xcd = blockIdx.x % 8u;
     const uint32_t lane_in_xcd = blockIdx.x / 8u;
     const uint32_t wgs_per_xcd = gridDim.x / 8u;
-    uint32_t s_surv = 0, s_fb = 0, s_done = 0, s_ch = 0, s_fc = 0, s_tiles = 0, s_ovf = 0;
+    uint32_t s_surv = 0, s_tiles = 0;
 
     for (uint32_t it = lane_in_xcd; it < per_xcd; it += wgs_per_xcd) {
-        const uint32_t work = xcd * per_xcd + it;
-        if (work >= total_work) break;
-        const uint32_t leaf = work / blocks_per_leaf;
-        const uint32_t blk = work % blocks_per_leaf;
+        const uint32_t work = xcd * per_xcd + it;  // item of the batch
+        if (work >= p.item_count) break;
+        const uint32_t item = p.item_begin + work;
+        const uint32_t leaf = item / p.blocks_per_leaf;
+        const uint32_t blk = item % p.blocks_per_leaf;
+        // The row's two lanes share one log region of 2*cap entries: lane h
+        // writes its e-th entry at 2e + h, so the select kernel reads a row's
+        // entries as one contiguous run.
+        const uint32_t brow = wave * 32u + j;  // row within the block
+        uint2 *slog = p.survivor_log + ((uint64_t)work * kRowsPerBlock + brow) * 2u * cap + h;
         const uint32_t n = p.member_counts[leaf];
         const uint32_t row_base = blk * kRowsPerBlock;
         if (row_base >= n) continue;
@@ -416,7 +310,6 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                     mc = 0u;
                 }
                 mem_lds[c] = mc;
-                gid_lds[c] = p.gids[mc];
                 const float cn = p.norms[mc];
                 cs_lds[c] = p.scales[mc];
                 cn_lds[c] = cn;
@@ -439,7 +332,6 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
 
         const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
         const bool row_ok = r < n;
-        const bool wave_rows_full = row_base + wave * 32u + 32u <= n;
         const uint32_t mr = row_ok ? mem_lds[r] : 0u;
         const uint32_t keff = n > 1u ? ((pk < n - 1u) ? pk : (n - 1u)) : 0u;
 
@@ -605,8 +497,8 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         uint32_t cnt = 0;
         // survivor log as a buffer: this thread's entries start at slog_off bytes
         const __amdgpu_buffer_rsrc_t log_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            p.survivor_log, (short)0, (int)(p.log_slots * 256u * cap * 8u), 0x00020000);
-        const uint32_t slog_off = (uint32_t)((blockIdx.x * kThreads + tid) * cap * 8u);
+            p.survivor_log, (short)0, (int)(p.item_count * (uint32_t)kThreads * cap * 8u), 0x00020000);
+        const uint32_t slog_off = ((work * (uint32_t)kRowsPerBlock + brow) * 2u * cap + h) * 8u;
         auto mask_unit = [&](auto wc) {
             constexpr int W = decltype(wc)::value, g = W / 6, u = W % 6;
             if constexpr (W >= kMaskUnits + 2 * kDrainSteps) {
@@ -614,7 +506,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             } else if constexpr (W >= kMaskUnits + kDrainSteps) {
                 constexpr int d = W - kMaskUnits - kDrainSteps;
                 const bool ok = ((dr_has >> d) & 1u) & (dr_c[d] < n) & (dr_c[d] != r);
-                const uint32_t off = (ok & (cnt < cap)) ? slog_off + cnt * 8u : 0x80000000u;
+                const uint32_t off = (ok & (cnt < cap)) ? slog_off + cnt * 16u : 0x80000000u;
                 const int2 rec = make_int2(dr_dot[d], (int)dr_c[d]);
                 __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const v2i *>(&rec), log_rsrc, off, 0, 0);
                 cnt += ok ? 1u : 0u;
@@ -655,7 +547,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 const uint32_t c = cbase + 8u * (vi >> 2) + (vi & 3u);
                 const int dot = scr[((vi >> 2) * 64u + lane) * 4u + (vi & 3u)];
                 const bool ok = (c < n) & (c != r);
-                if (ok & (cnt < cap)) slog[cnt] = make_uint2((uint32_t)dot, c);
+                if (ok & (cnt < cap)) slog[2u * cnt] = make_uint2((uint32_t)dot, c);
                 cnt += ok ? 1u : 0u;
             }
         };
@@ -751,254 +643,28 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         static_for<0, kMaskUnits>(mask_unit);
         drain(ep_m, ntiles - 1u);
         s_tiles += S;
-        // the output stage below overlays the tile buffers and scratch
-        lds_barrier();
+        s_surv += cnt < cap ? cnt : cap;
 
-        // ---- final: fold the log, merge the pair, certify, order, write -----------
-        // The log entries were written by this thread's global stores above.  A
-        // workgroup-scope fence waits for them; the workgroup's L1 serves all its
-        // waves, so no cache write-back or invalidation is needed (an agent-scope
-        // fence would write back L2 and costs more than the fold itself).
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        float topd[kTop];
-        uint32_t topc[kTop];
-#pragma unroll
-        for (int i = 0; i < kTop; ++i) {
-            topd[i] = __builtin_inff();
-            topc[i] = 0xffffu;
-        }
-        float disc = __builtin_inff();
-        const bool lane_ovf = cnt > cap;
-        const int logged = (int)(cnt < cap ? cnt : cap);
-        fold_staged(slog, cs_lds, cn_lds, n, logged, rs, rn, topd, topc, disc);
-        s_surv += logged;
-        s_ovf += lane_ovf ? 1u : 0u;
-        // pair flag through a ballot (a lane-mask value, not a shuffled register)
-        const uint64_t ovf_mask = __ballot(lane_ovf);
-        const bool pair_ovf = ((ovf_mask >> lane) & 1ull) != 0ull || ((ovf_mask >> (lane ^ 32u)) & 1ull) != 0ull;
-
-        // Known sequence: the pair's 32 smallest sorted (positions 0..31) and the
-        // 8 smallest of the rest (32..39).  Everything not known is > min(disc, F).
-        constexpr int kSeq = kTop + 8;
-        float sd[kSeq];
-        uint32_t sc[kSeq];
-        {
-            // Lower / upper halves of (own ascending) vs (partner descending):
-            // positions i and 31-i are handled together so the partner's
-            // entries are read (by shuffle) before either is overwritten.
-            float hi[kTop];
-            uint32_t phi[kTop];
-#pragma unroll
-            for (int i = 0; i < kTop / 2; ++i) {
-                const int i2 = kTop - 1 - i;
-                const float b0 = __shfl_xor(topd[i2], 32);
-                const uint32_t bc0 = __shfl_xor(topc[i2], 32);
-                const float b1 = __shfl_xor(topd[i], 32);
-                const uint32_t bc1 = __shfl_xor(topc[i], 32);
-                const float a0 = topd[i], a1 = topd[i2];
-                const uint32_t c0 = topc[i], c1 = topc[i2];
-                const bool sw0 = b0 < a0, sw1 = b1 < a1;
-                topd[i] = sw0 ? b0 : a0;
-                topc[i] = sw0 ? bc0 : c0;
-                hi[i] = sw0 ? a0 : b0;
-                phi[i] = sw0 ? c0 : bc0;
-                topd[i2] = sw1 ? b1 : a1;
-                topc[i2] = sw1 ? bc1 : c1;
-                hi[i2] = sw1 ? a1 : b1;
-                phi[i2] = sw1 ? c1 : bc1;
-            }
-            bitonic_merge_kv<kTop>(topd, topc);
-            // half-cleaners keep the lower half of a bitonic sequence: 32 -> 16 -> 8,
-            // then a bitonic merge sorts those 8
-#pragma unroll
-            for (int w = 16; w >= 8; w >>= 1) {
-#pragma unroll
-                for (int i = 0; i < w; ++i) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
-            }
-#pragma unroll
-            for (int w = 4; w >= 1; w >>= 1) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if ((i & w) == 0) cex(hi[i], phi[i], hi[i + w], phi[i + w], true);
-            }
-#pragma unroll
-            for (int i = 0; i < kTop; ++i) {
-                sd[i] = topd[i];
-                sc[i] = topc[i];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                sd[kTop + i] = hi[i];
-                sc[kTop + i] = phi[i];
-            }
-        }
-        // not known: filtered (d > F) or evicted from a lane's list (>= disc)
-        const float disc_all = fminf(fminf(disc, __shfl_xor(disc, 32)), F);
-
-        // Tie clusters over the sorted known sequence; bit i of `same` says
-        // positions i and i+1 are in one cluster (swaps below stay inside
-        // clusters, so the bits keep their meaning).
-        int q_end = (int)keff - 1;   // last index of G
-        bool extending = keff > 0u;
-        bool clique_bad = false;
-        float cstart = sd[0];
-        uint64_t same = 0ull;
-#pragma unroll
-        for (int i = 1; i < kSeq; ++i) {
-            const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
-            same |= tie ? (1ull << (i - 1)) : 0ull;
-            const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
-            cstart = tie ? cstart : sd[i];
-            if (i >= (int)keff && extending) {
-                if (tie) q_end = i;
-                else extending = false;
-            }
-            clique_bad |= span_bad && (i <= q_end || (extending && i >= (int)keff));
-        }
-        // Gap certificate: the cluster holding s_{keff-1} closes inside the known
-        // sequence and the next distance after it -- known or not -- is > eps away.
-        bool gap_ok = (keff == 0u || !extending) && !pair_ovf;
-        if (keff > 0u && gap_ok) {
-            float theta = sd[0];
-            float next = disc_all;
-#pragma unroll
-            for (int i = 1; i < kSeq; ++i) {
-                theta = (i == q_end) ? sd[i] : theta;  // static indices only: no scratch
-                next = (i == q_end + 1) ? fminf(next, sd[i]) : next;
-            }
-            gap_ok = next == __builtin_inff() || __fsub_rn(next, theta) > kTieEps;
-        }
-        // Test knob: re-run every `debug_rerun_every`-th row through the exact kernel.
-        if (p.debug_rerun_every != 0u && (r % p.debug_rerun_every) == 0u) gap_ok = false;
-        // Outcome: direct output (all clusters of G are cliques), chain queue (a
-        // cluster of G is an eps-chain: its order depends on arrival order, so G
-        // is replayed in column order by leaf_chain_kernel), or full exact re-run.
-        const bool direct = gap_ok && !clique_bad;
-        const bool chain = gap_ok && clique_bad;
-
-        // Direct rows: global ids of G's positions (then each cluster is ordered
-        // by global id).  Other rows keep the columns for the chain queue.
-#pragma unroll
-        for (int i = 0; i < kSeq; ++i)
-            sc[i] = (row_ok && direct && i <= q_end && sc[i] < n) ? gid_lds[sc[i]] : sc[i];
-        const uint64_t in_g = q_end >= 1 ? ((q_end >= 64 ? ~0ull : ((1ull << q_end) - 1ull))) : 0ull;
-        const bool need_sort = (same & in_g) != 0ull;
-        if (__any(row_ok && direct && need_sort)) {
-            // odd-even transposition sort by global id inside each cluster of G
-            // (sorted once an even and an odd phase in a row swap nothing)
-            const uint64_t mask = (row_ok && direct) ? (same & in_g) : 0ull;
-            for (int pass = 0; pass < kSeq + 2; pass += 2) {
-                bool swapped = false;
-#pragma unroll
-                for (int i = 0; i + 1 < kSeq; i += 2) {
-                    const bool sw = ((mask >> i) & 1ull) && sc[i] > sc[i + 1];
-                    const uint32_t ga = sc[i], gb = sc[i + 1];
-                    const float da = sd[i], db = sd[i + 1];
-                    sc[i] = sw ? gb : ga;
-                    sc[i + 1] = sw ? ga : gb;
-                    sd[i] = sw ? db : da;
-                    sd[i + 1] = sw ? da : db;
-                    swapped |= sw;
-                }
-#pragma unroll
-                for (int i = 1; i + 1 < kSeq; i += 2) {
-                    const bool sw = ((mask >> i) & 1ull) && sc[i] > sc[i + 1];
-                    const uint32_t ga = sc[i], gb = sc[i + 1];
-                    const float da = sd[i], db = sd[i + 1];
-                    sc[i] = sw ? gb : ga;
-                    sc[i + 1] = sw ? ga : gb;
-                    sd[i] = sw ? db : da;
-                    sd[i + 1] = sw ? da : db;
-                    swapped |= sw;
-                }
-                if (!__any(swapped)) break;
-            }
-        }
-
-        // Output: the wave's 32 rows are consecutive, so their slots form one
-        // block of rows*k records.  Lanes stage their row's slots in the
-        // wave's LDS area, then the wave writes the block with consecutive
-        // lanes on consecutive addresses.  Rows that are not direct stage
-        // placeholders: the chain and exact kernels, which run after this one,
-        // overwrite their slots.
-        {
-            uint32_t *st_ids = stage + wave * (2u * 32u * (uint32_t)kTop);
-            float *st_d = reinterpret_cast<float *>(st_ids + 32u * kTop);
-#pragma unroll
-            for (int i = 0; i < kTop; ++i) {
-                if ((i >> 4) != (int)h || (uint32_t)i >= pk) continue;
-                const bool live = (uint32_t)i < keff;
-                st_ids[j * pk + i] = live ? sc[i] : kEmptyId;
-                st_d[j * pk + i] = live ? sd[i] : kEmptyDist;
-            }
-            const uint32_t wrow0 = row_base + wave * 32u;
-            const uint32_t wrows = wrow0 < n ? (n - wrow0 < 32u ? n - wrow0 : 32u) : 0u;
-            const uint32_t total = wrows * pk;
-            const uint64_t base = p.output_offsets[leaf] + (uint64_t)wrow0 * pk;
-            for (uint32_t e = lane; e < total; e += 64u) {
-                p.out_ids[base + e] = st_ids[e];
-                p.out_dists[base + e] = st_d[e];
-            }
-        }
+        // ---- end of item: the row's threshold and each lane's entry count ----
+        // (the select kernel folds the logs, certifies and writes the rows;
+        // a count above the capacity marks a log that overflowed)
         if (row_ok) {
-            if (direct) {
-                s_done += h == 0u ? 1u : 0u;
-            } else if (h == 0u) {
-                bool queued = false;
-                const uint32_t m = (uint32_t)q_end + 1u;
-                if (chain) {
-                    const uint32_t off = atomicAdd(p.chain_pool_used, m);
-                    if (off + m <= p.chain_pool_capacity) {
-                        const uint32_t idx = atomicAdd(p.chain_count, 1u);
-                        if (idx < p.chain_capacity) {
-                            // pool entry: (distance bits, column, global id); header:
-                            // (output offset, pool offset, m | keff << 8)
-#pragma unroll
-                            for (int i = 0; i < kSeq; ++i)
-                                if ((uint32_t)i < m)
-                                    p.chain_pool[off + i] = make_uint4(__float_as_uint(sd[i]), sc[i],
-                                                                       gid_lds[sc[i] < n ? sc[i] : 0u], 0u);
-                            const uint64_t out = p.output_offsets[leaf] + (uint64_t)r * pk;
-                            p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), off, m | (keff << 8));
-                            queued = true;
-                            s_ch += 1;
-                            s_fc += m;
-                        }
-                    }
-                }
-                if (!queued) {
-                    s_fb += 1;
-                    const uint32_t idx = atomicAdd(p.fallback_count, 1u);
-                    if (idx < p.fallback_capacity) {
-                        p.fallback[2 * idx] = leaf;
-                        p.fallback[2 * idx + 1] = r;
-                    } else {
-                        flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
-                    }
-                }
+            uint32_t *rm = reinterpret_cast<uint32_t *>(p.row_meta + (uint64_t)work * kRowsPerBlock + brow);
+            if (h == 0u) {
+                rm[0] = __float_as_uint(F);
+                rm[1] = cnt;
+            } else {
+                rm[2] = cnt;
             }
         }
     }
 
     // One atomic per counter per wave.
-    uint64_t a_surv = s_surv, a_fb = s_fb, a_done = s_done, a_ch = s_ch, a_fc = s_fc, a_ovf = s_ovf;
+    uint64_t a_surv = s_surv;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        a_surv += __shfl_xor(a_surv, off);
-        a_fb += __shfl_xor(a_fb, off);
-        a_done += __shfl_xor(a_done, off);
-        a_ch += __shfl_xor(a_ch, off);
-        a_fc += __shfl_xor(a_fc, off);
-        a_ovf += __shfl_xor(a_ovf, off);
-    }
+    for (int off = 32; off > 0; off >>= 1) a_surv += __shfl_xor(a_surv, off);
     if (lane == 0) {
         counter_add(p.counters, TESSA_C_LEAF_SURVIVORS, a_surv);
-        counter_add(p.counters, TESSA_C_LEAF_FALLBACK_ROWS, a_fb);
-        counter_add(p.counters, TESSA_C_LEAF_GAP_FALLBACK_ROWS, a_fb);
-        counter_add(p.counters, TESSA_C_LEAF_CHAIN_ROWS, a_ch);
-        counter_add(p.counters, TESSA_C_LEAF_FINAL_CANDIDATES, a_fc);
-        counter_add(p.counters, TESSA_C_LEAF_ROWS, a_done);
-        counter_add(p.counters, TESSA_C_LEAF_LIST_OVERFLOW_ROWS, a_ovf);
         if (wave == 0) counter_add(p.counters, TESSA_C_LEAF_MFMA_TILES, s_tiles);
     }
 }
@@ -1016,20 +682,14 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     const uint32_t lds = lds_bytes(L::kTileBytes, cols_cap);
     if (lds > kLdsBudget) return -4;
-    const uint32_t blocks_per_leaf = (p.max_leaf_rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    const uint64_t total = (uint64_t)blocks_per_leaf * p.leaf_count;
-    if (total == 0) return 0;
-    if (total > 0x7fffff00ull) return -2;
-    const uint32_t per_xcd = (uint32_t)((total + 7) / 8);
-    // persistent grid: each workgroup owns kThreads / 256 survivor-log slots
-    // (a slot holds 256 threads' logs) for its lifetime
-    uint32_t grid = (uint32_t)((uint64_t)p.log_slots * 256u / kThreads);
-    const uint64_t need = (uint64_t)per_xcd * 8u;
-    if (need < grid) grid = (uint32_t)need;
-    grid = grid / 8u * 8u;
-    if (grid == 0) return -5;
-    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(grid), dim3(kThreads), lds, stream, p, blocks_per_leaf,
-                       (uint32_t)total, per_xcd);
+    if (p.item_count == 0) return 0;
+    if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x7fffffffull) return -2;
+    const uint32_t per_xcd = (p.item_count + 7u) / 8u;
+    // persistent grid: up to four workgroups per CU's worth of items, a
+    // multiple of the 8 XCDs; XCD x walks items [x*per_xcd, (x+1)*per_xcd)
+    uint32_t grid = 1024u;
+    if (per_xcd * 8u < grid) grid = per_xcd * 8u;
+    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

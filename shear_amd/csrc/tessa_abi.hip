@@ -74,8 +74,10 @@ struct DeviceWorkspace {
     uint64_t chain_capacity = 0;
     uint4 *chain_pool = nullptr;
     uint64_t pool_capacity = 0;
-    uint2 *survivor_log = nullptr;  // slots x 256 threads x kLeafLogCapacity entries
+    uint2 *survivor_log = nullptr;  // batch items x kLeafFilterThreads x kLeafLogCapacity entries
     uint64_t log_entries = 0;
+    uint4 *row_meta = nullptr;      // batch items x kLeafBlockRows
+    uint64_t row_meta_capacity = 0;
     // edge-record kernels: per-leaf totals, leaf record offsets, status words
     uint32_t *edge_totals = nullptr;
     uint64_t edge_totals_capacity = 0;
@@ -121,6 +123,15 @@ tessa_status grow(T **ptr, uint64_t *cap, uint64_t need, size_t elem_bytes, cons
     return ok_status();
 }
 
+// Work items per filter/select batch for `rows` member rows: the survivor
+// logs of a batch take kLeafLogBytesPerItem each, at most kLeafLogBudget in all.
+constexpr uint64_t kLeafLogBudget = 1ull << 30;
+uint64_t leaf_batch_items(uint64_t rows) {
+    const uint64_t cap = kLeafLogBudget / kLeafLogBytesPerItem;
+    const uint64_t want = (rows + kLeafBlockRows - 1) / kLeafBlockRows + 1;
+    return want < cap ? want : cap;
+}
+
 tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     int dev = 0;
     TESSA_HIP_TRY(hipGetDevice(&dev));
@@ -137,12 +148,12 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     if (st.code) return st;
     st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint4), "chain pool");
     if (st.code) return st;
-    // one log slot (256 threads' logs) per 128 rows of this batch, at most
-    // kLeafLogSlots; a persistent MFMA workgroup of 8 waves (256 rows) takes
-    // two, and the grid needs one workgroup per XCD at least: 16 slots minimum
-    const uint64_t blocks = (rows + 127) / 128;
-    const uint64_t slots = ((blocks < kLeafLogSlots ? blocks : kLeafLogSlots) + 15) / 16 * 16;
-    st = grow(&ws.survivor_log, &ws.log_entries, slots * 256 * kLeafLogCapacity, sizeof(uint2), "survivor log");
+    // survivor logs and row thresholds of one batch of work items
+    const uint64_t items = leaf_batch_items(rows);
+    st = grow(&ws.survivor_log, &ws.log_entries, items * kLeafFilterThreads * kLeafLogCapacity, sizeof(uint2),
+              "survivor log");
+    if (st.code) return st;
+    st = grow(&ws.row_meta, &ws.row_meta_capacity, items * kLeafBlockRows, sizeof(uint4), "row thresholds");
     if (st.code) return st;
     *out = &ws;
     return ok_status();
@@ -249,10 +260,11 @@ tessa_status tessa_query_caps(int32_t device, tessa_caps *out) {
 
 namespace {
 
-// Events bracketing the three leaf kernels (MFMA, chain replay, exact
-// re-run), one set per device, created on first use.
+// Events bracketing the leaf kernels: per batch the filter and the select
+// kernel (three events), then the chain replay and the exact re-run; one
+// set per device, created on first use and grown with the batch count.
 struct PhaseEvents {
-    hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+    std::vector<hipEvent_t> e;
 };
 std::mutex g_ev_mutex;
 std::vector<PhaseEvents> g_events;
@@ -262,10 +274,16 @@ tessa_status phase_events(PhaseEvents **out) {
     TESSA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_ev_mutex);
     if ((int)g_events.size() <= dev) g_events.resize(dev + 1);
-    PhaseEvents &pe = g_events[dev];
-    for (int i = 0; i < 4; ++i)
-        if (!pe.e[i]) TESSA_HIP_TRY(hipEventCreate(&pe.e[i]));
-    *out = &pe;
+    *out = &g_events[dev];
+    return ok_status();
+}
+
+tessa_status ensure_events(PhaseEvents *pe, size_t count) {
+    while (pe->e.size() < count) {
+        hipEvent_t ev = nullptr;
+        TESSA_HIP_TRY(hipEventCreate(&ev));
+        pe->e.push_back(ev);
+    }
     return ok_status();
 }
 
@@ -273,7 +291,7 @@ tessa_status phase_events(PhaseEvents **out) {
 // sizes the re-run / chain queues.  `ev` (optional) brackets the kernels.
 tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint64_t rows_bound,
                             uint32_t *out_ids, float *out_dists, uint64_t *counters, void *stream,
-                            PhaseEvents *ev) {
+                            PhaseEvents *ev, uint64_t *batches_out = nullptr) {
     tessa_status st = check_view(sq8);
     if (st.code) return st;
     if (!lb || !lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets || !out_ids ||
@@ -332,20 +350,33 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.chain_pool_capacity = clamp32(ws->pool_capacity);
     p.survivor_log = ws->survivor_log;
     p.log_capacity = kLeafLogCapacity;
-    {
-        const uint64_t slots = ws->log_entries / (256ull * kLeafLogCapacity);
-        p.log_slots = (uint32_t)(slots < kLeafLogSlots ? slots : kLeafLogSlots);
+    p.row_meta = ws->row_meta;
+    p.blocks_per_leaf = (lb->max_leaf_rows + kLeafBlockRows - 1) / kLeafBlockRows;
+    const uint64_t items = (uint64_t)p.blocks_per_leaf * lb->leaf_count;
+    if (items > 0xffffff00ull) return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaf work items");
+    const uint64_t batch = ws->log_entries / ((uint64_t)kLeafFilterThreads * kLeafLogCapacity);
+    const uint64_t nbatch = (items + batch - 1) / batch;
+    if (ev) {
+        st = ensure_events(ev, 3 * nbatch + 2);
+        if (st.code) return st;
     }
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
     hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->queue_counts, 3u, 0u);
-    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[0], s));
-    if (launch_leaf_mfma(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "MFMA leaf kernel launch failed");
-    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[1], s));
+    for (uint64_t b = 0; b < nbatch; ++b) {
+        p.item_begin = (uint32_t)(b * batch);
+        p.item_count = (uint32_t)(items - b * batch < batch ? items - b * batch : batch);
+        if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3 * b], s));
+        if (launch_leaf_mfma(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "MFMA leaf kernel launch failed");
+        if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3 * b + 1], s));
+        if (launch_leaf_select(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "leaf select kernel launch failed");
+        if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3 * b + 2], s));
+    }
     if (launch_leaf_chain(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "leaf chain kernel launch failed");
-    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[2], s));
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3 * nbatch], s));
     if (launch_leaf_exact_fallback(p, s) != 0)
         return make_status(TESSA_ERR_HIP, 0, "leaf fallback kernel launch failed");
-    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3], s));
+    if (ev) TESSA_HIP_TRY(hipEventRecord(ev->e[3 * nbatch + 1], s));
+    if (batches_out) *batches_out = nbatch;
     return ok_status();
 }
 
@@ -364,18 +395,26 @@ tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_lea
                                       float *out_dists, uint64_t *counters, void *stream, float *phase_ms) {
     if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
     if (!phase_ms) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "phase_ms is null");
+    for (int i = 0; i < 4; ++i) phase_ms[i] = 0.0f;
     PhaseEvents *ev = nullptr;
     tessa_status st = phase_events(&ev);
     if (st.code) return st;
+    uint64_t nb = 0;
     st = leaf_topk_impl(sq8, lb, (uint64_t)lb->leaf_count * lb->max_leaf_rows, out_ids, out_dists, counters, stream,
-                        ev);
-    if (st.code) return st;
-    TESSA_HIP_TRY(hipEventSynchronize(ev->e[3]));
-    for (int i = 0; i < 3; ++i) {
+                        ev, &nb);
+    if (st.code || nb == 0) return st;  // exact executor or no leaves: no MFMA phases
+    TESSA_HIP_TRY(hipEventSynchronize(ev->e[3 * nb + 1]));
+    auto span = [&](size_t a, size_t b) {
         float ms = 0.0f;
-        TESSA_HIP_TRY(hipEventElapsedTime(&ms, ev->e[i], ev->e[i + 1]));
-        phase_ms[i] = ms;
+        (void)hipEventElapsedTime(&ms, ev->e[a], ev->e[b]);
+        return ms;
+    };
+    for (uint64_t b = 0; b < nb; ++b) {
+        phase_ms[0] += span(3 * b, 3 * b + 1);
+        phase_ms[1] += span(3 * b + 1, 3 * b + 2);
     }
+    phase_ms[2] = span(3 * nb - 1, 3 * nb);
+    phase_ms[3] = span(3 * nb, 3 * nb + 1);
     return ok_status();
 }
 

@@ -157,7 +157,8 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
     """Enqueue the leaf operator; returns (ids int32 view of u32, dists f32, counters int64).
 
     With ``phase_ms`` (a list) the call synchronises and appends the hipEvent
-    times of its three kernels (MFMA, chain replay, exact re-run) in ms."""
+    times of its kernels in ms: MFMA filter, select (each summed over the
+    call's batches), chain replay, exact re-run."""
     dev = sq8.codes.device
     if out_ids is None:
         out_ids = torch.empty(layouts.output_len, dtype=torch.int32, device=dev)
@@ -173,11 +174,11 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
         N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                          _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
     else:
-        ph = (C.c_float * 3)()
+        ph = (C.c_float * 4)()
         N.check(N.load().tessa_leaf_topk_profiled(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                                   _ptr(counters), _stream_ptr(stream), ph),
                 "tessa_leaf_topk_profiled")
-        phase_ms.append([float(ph[0]), float(ph[1]), float(ph[2])])
+        phase_ms.append([float(ph[i]) for i in range(4)])
     return out_ids, out_dists, counters
 
 
