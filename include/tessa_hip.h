@@ -162,6 +162,20 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
                              uint32_t *out_ids, float *out_dists,
                              uint64_t *counters, void *stream);
 
+/* tessa_leaf_topk that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and errors as tessa_leaf_topk; all scratch (queue
+ * counters, re-run and chain queues, survivor logs) lives in one static
+ * device array of about 38 MB per GPU, held until the process ends, so a
+ * call may cover at most 65,536 member rows (leaf_count * max_leaf_rows);
+ * larger batches are rejected with TESSA_ERR_UNSUPPORTED.  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf_batch *leaves,
+                                     uint32_t *out_ids, float *out_dists,
+                                     uint64_t *counters, void *stream);
+
 /* tessa_leaf_topk with hipEvents around its kernels (the reference reports
  * the same split as persistent_kernel_event_ms / leaf DCO clocks in
  * GpuSubtreeTopKProfile, compute_backend.rs:2198-2247).  Synchronises on the

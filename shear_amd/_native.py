@@ -277,6 +277,7 @@ SIGNATURES = {
     "tessa_overflow_labels": (None, [_U64, C.c_char_p, C.c_size_t]),
     "tessa_query_caps": (TessaStatus, [C.c_int32, C.POINTER(TessaCaps)]),
     "tessa_leaf_topk": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P]),
+    "tessa_leaf_topk_noalloc": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P]),
     "tessa_leaf_topk_profiled": (
         TessaStatus,
         [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P, C.POINTER(C.c_float)],

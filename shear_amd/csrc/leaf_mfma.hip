@@ -108,7 +108,8 @@ struct Layout {
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
 // LDS: two column tiles and each wave's 4 KB accumulator scratch, then the
-// leaf's member ids, scales and norms, and 64 bytes of scalars.
+// leaf's member ids, scales and norms, and 64 bytes of scalars (each wave's
+// norm range).
 __host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes) {
     return 2u * tile_bytes + kWaves * 16u * 64u * 4u;
 }
@@ -295,26 +296,56 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const uint32_t pd = opaque_u32(p.padded_dim);
         const uint32_t pk = opaque_u32(p.k);
 
-        __syncthreads();  // previous item's readers of the LDS arrays are done
-        if (tid == 0) {
-            misc[0] = 0x7f800000u;  // +inf bits: min norm
-            misc[1] = 0u;           // max norm
-        }
-        __syncthreads();
+        // The lane's row: its member id straight from the member list, and its
+        // codes (the B operand, zero past padded_dim) requested before the
+        // staging below, so both sets of loads are in flight together.
+        const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
+        const bool row_ok = r < n;
+        uint32_t mr = row_ok ? mem[r] : 0u;
+        mr = mr < p.rows ? mr : 0u;  // the staging flags an invalid id
+        const uint32_t keff = n > 1u ? ((pk < n - 1u) ? pk : (n - 1u)) : 0u;
+        v4i bfrag[KS];
         {
+            const int8_t *rc = p.codes + (uint64_t)mr * pd;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const uint32_t off = 32u * s + 16u * h;
+                const bool ok = row_ok && off < pd;
+                const v4i z = *reinterpret_cast<const v4i *>(rc + (ok ? off : 0u));
+                const v4i zero = {0, 0, 0, 0};
+                bfrag[s] = ok ? z : zero;
+            }
+        }
+
+        __syncthreads();  // previous item's readers of the LDS arrays are done
+        {
+            // two columns per thread per step, every load of a step issued
+            // before its results are used
             float lo = __builtin_inff(), hi = 0.0f;
-            for (uint32_t c = tid; c < n; c += kThreads) {
-                uint32_t mc = mem[c];
-                if (mc >= p.rows) {
+            for (uint32_t c0 = tid; c0 < n; c0 += 2u * kThreads) {
+                const uint32_t c1 = c0 + kThreads;
+                const bool ok1 = c1 < n;
+                uint32_t m0 = mem[c0];
+                uint32_t m1 = mem[ok1 ? c1 : c0];
+                if (m0 >= p.rows || m1 >= p.rows) {
                     flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
-                    mc = 0u;
+                    m0 = m0 < p.rows ? m0 : 0u;
+                    m1 = m1 < p.rows ? m1 : 0u;
                 }
-                mem_lds[c] = mc;
-                const float cn = p.norms[mc];
-                cs_lds[c] = p.scales[mc];
-                cn_lds[c] = cn;
-                lo = fminf(lo, cn);
-                hi = fmaxf(hi, cn);
+                const float s0 = p.scales[m0], s1 = p.scales[m1];
+                const float n0 = p.norms[m0], n1 = p.norms[m1];
+                mem_lds[c0] = m0;
+                cs_lds[c0] = s0;
+                cn_lds[c0] = n0;
+                lo = fminf(lo, n0);
+                hi = fmaxf(hi, n0);
+                if (ok1) {
+                    mem_lds[c1] = m1;
+                    cs_lds[c1] = s1;
+                    cn_lds[c1] = n1;
+                    lo = fminf(lo, n1);
+                    hi = fmaxf(hi, n1);
+                }
             }
             // the last column tile's columns past n: zero scale, infinite norm
             // (their codes are zero, so their sampled distance is +inf)
@@ -322,31 +353,25 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 cs_lds[c] = 0.0f;
                 cn_lds[c] = __builtin_inff();
             }
-            // norms are sums of squares (>= 0): their bit patterns order like the values
-            atomicMin(&misc[0], __float_as_uint(lo));
-            atomicMax(&misc[1], __float_as_uint(hi));
-        }
-        __syncthreads();
-        const float cn_min = __uint_as_float(misc[0]);
-        const float cn_max = __uint_as_float(misc[1]);
-
-        const uint32_t r = row_base + wave * 32u + j;  // leaf-local row position
-        const bool row_ok = r < n;
-        const uint32_t mr = row_ok ? mem_lds[r] : 0u;
-        const uint32_t keff = n > 1u ? ((pk < n - 1u) ? pk : (n - 1u)) : 0u;
-
-        // Row codes for the whole K range (B operand), zero past padded_dim.
-        v4i bfrag[KS];
-        {
-            const int8_t *rc = p.codes + (uint64_t)mr * pd;
+            // per-wave norm range into misc; combined after the barrier
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const uint32_t off = 32u * s + 16u * h;
-                v4i z = {0, 0, 0, 0};
-                if (row_ok && off < pd) z = *reinterpret_cast<const v4i *>(rc + off);
-                bfrag[s] = z;
+            for (int off = 32; off > 0; off >>= 1) {
+                lo = fminf(lo, __shfl_xor(lo, off));
+                hi = fmaxf(hi, __shfl_xor(hi, off));
+            }
+            if (lane == 0u) {
+                misc[2u * wave] = __float_as_uint(lo);
+                misc[2u * wave + 1u] = __float_as_uint(hi);
             }
         }
+        __syncthreads();
+        float cn_min = __uint_as_float(misc[0]), cn_max = __uint_as_float(misc[1]);
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            cn_min = fminf(cn_min, __uint_as_float(misc[2 * w]));
+            cn_max = fmaxf(cn_max, __uint_as_float(misc[2 * w + 1]));
+        }
+
         const float rs = row_ok ? cs_lds[r] : 1.0f;
         const float rn = row_ok ? cn_lds[r] : 0.0f;
 

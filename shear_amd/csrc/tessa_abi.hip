@@ -287,11 +287,29 @@ tessa_status ensure_events(PhaseEvents *pe, size_t count) {
     return ok_status();
 }
 
+// Device buffers of the MFMA leaf path: queue counters (3 words), the exact
+// re-run queue, the chain queue and pool, and one batch of survivor logs and
+// row thresholds (log_items work items).
+struct LeafScratch {
+    uint32_t *queue_counts;
+    uint32_t *fallback;
+    uint64_t fallback_capacity;
+    uint4 *chain_rows;
+    uint64_t chain_capacity;
+    uint4 *chain_pool;
+    uint64_t pool_capacity;
+    uint2 *log;
+    uint64_t log_items;
+    uint4 *row_meta;
+};
+
 // Leaf top-k over device layouts; `rows_bound` bounds the member rows and
 // sizes the re-run / chain queues.  `ev` (optional) brackets the kernels.
+// `fixed` (optional) supplies the scratch buffers; else the per-device
+// workspace is grown to fit.
 tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint64_t rows_bound,
                             uint32_t *out_ids, float *out_dists, uint64_t *counters, void *stream,
-                            PhaseEvents *ev, uint64_t *batches_out = nullptr) {
+                            PhaseEvents *ev, uint64_t *batches_out = nullptr, const LeafScratch *fixed = nullptr) {
     tessa_status st = check_view(sq8);
     if (st.code) return st;
     if (!lb || !lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets || !out_ids ||
@@ -335,33 +353,42 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
         return make_status(TESSA_ERR_UNSUPPORTED, 0,
                            "MFMA leaf path needs padded_dim <= 1024 and max_leaf_rows <= 4096 (got %u, %u)",
                            sq8->padded_dim, lb->max_leaf_rows);
-    DeviceWorkspace *ws = nullptr;
-    st = get_workspace(rows_bound, &ws);
-    if (st.code) return st;
+    LeafScratch sc{};
+    if (fixed) {
+        sc = *fixed;
+    } else {
+        DeviceWorkspace *ws = nullptr;
+        st = get_workspace(rows_bound, &ws);
+        if (st.code) return st;
+        sc = LeafScratch{ws->queue_counts, ws->fallback,   ws->fallback_capacity, ws->chain_rows,
+                         ws->chain_capacity, ws->chain_pool, ws->pool_capacity,    ws->survivor_log,
+                         ws->log_entries / ((uint64_t)kLeafFilterThreads * kLeafLogCapacity), ws->row_meta};
+    }
     auto clamp32 = [](uint64_t v) { return (uint32_t)(v < 0xffffffffull ? v : 0xffffffffull); };
-    p.fallback = ws->fallback;
-    p.fallback_count = ws->queue_counts;
-    p.fallback_capacity = clamp32(ws->fallback_capacity);
-    p.chain_rows = ws->chain_rows;
-    p.chain_count = ws->queue_counts + 1;
-    p.chain_capacity = clamp32(ws->chain_capacity);
-    p.chain_pool = ws->chain_pool;
-    p.chain_pool_used = ws->queue_counts + 2;
-    p.chain_pool_capacity = clamp32(ws->pool_capacity);
-    p.survivor_log = ws->survivor_log;
+    p.fallback = sc.fallback;
+    p.fallback_count = sc.queue_counts;
+    p.fallback_capacity = clamp32(sc.fallback_capacity);
+    p.chain_rows = sc.chain_rows;
+    p.chain_count = sc.queue_counts + 1;
+    p.chain_capacity = clamp32(sc.chain_capacity);
+    p.chain_pool = sc.chain_pool;
+    p.chain_pool_used = sc.queue_counts + 2;
+    p.chain_pool_capacity = clamp32(sc.pool_capacity);
+    p.survivor_log = sc.log;
     p.log_capacity = kLeafLogCapacity;
-    p.row_meta = ws->row_meta;
+    p.row_meta = sc.row_meta;
     p.blocks_per_leaf = (lb->max_leaf_rows + kLeafBlockRows - 1) / kLeafBlockRows;
     const uint64_t items = (uint64_t)p.blocks_per_leaf * lb->leaf_count;
     if (items > 0xffffff00ull) return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaf work items");
-    const uint64_t batch = ws->log_entries / ((uint64_t)kLeafFilterThreads * kLeafLogCapacity);
+    const uint64_t batch = sc.log_items;
+    if (batch == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf workspace holds no survivor log");
     const uint64_t nbatch = (items + batch - 1) / batch;
     if (ev) {
         st = ensure_events(ev, 3 * nbatch + 2);
         if (st.code) return st;
     }
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, ws->queue_counts, 3u, 0u);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, sc.queue_counts, 3u, 0u);
     for (uint64_t b = 0; b < nbatch; ++b) {
         p.item_begin = (uint32_t)(b * batch);
         p.item_count = (uint32_t)(items - b * batch < batch ? items - b * batch : batch);
@@ -416,6 +443,74 @@ tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_lea
     phase_ms[2] = span(3 * nb - 1, 3 * nb);
     phase_ms[3] = span(3 * nb, 3 * nb + 1);
     return ok_status();
+}
+
+// ---- leaf top-k without allocation -------------------------------------------
+// All scratch of the MFMA leaf path in one static device array per GPU:
+// queue counters, re-run queue, chain queue and pool for up to
+// kNoAllocMaxRows member rows, and survivor logs for kNoAllocLogItems work
+// items per filter/select batch.
+}  // extern "C"
+namespace {
+constexpr uint64_t kNoAllocMaxRows = 65536;
+constexpr uint64_t kNoAllocLogItems = 32;
+constexpr uint64_t kNoAllocChainRows = kNoAllocMaxRows / 2 + 1;
+constexpr size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kNaOffFallback = 256;
+constexpr size_t kNaOffChainRows = kNaOffFallback + a256(kNoAllocMaxRows * 2 * sizeof(uint32_t));
+constexpr size_t kNaOffChainPool = kNaOffChainRows + a256(kNoAllocChainRows * sizeof(uint4));
+constexpr size_t kNaOffRowMeta = kNaOffChainPool + a256(kNoAllocChainRows * 40 * sizeof(uint4));
+constexpr size_t kNaOffLog = kNaOffRowMeta + a256(kNoAllocLogItems * kLeafBlockRows * sizeof(uint4));
+constexpr size_t kNoAllocBytes = kNaOffLog + a256(kNoAllocLogItems * kLeafLogBytesPerItem);
+
+__device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this GPU's `scratch` (the host-side name is only a
+// stand-in), looked up once per device with that device current.
+tessa_status scratch_for_device(unsigned char **out) {
+    int dev = 0;
+    TESSA_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "device %d beyond the no-allocation path's %d devices", dev,
+                           kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        TESSA_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[dev] = static_cast<unsigned char *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return ok_status();
+}
+}  // namespace
+extern "C" {
+
+tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf_batch *lb, uint32_t *out_ids,
+                                     float *out_dists, uint64_t *counters, void *stream) {
+    if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
+    const uint64_t rows = (uint64_t)lb->leaf_count * lb->max_leaf_rows;
+    if (rows > kNoAllocMaxRows)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0,
+                           "leaf batch of %u leaves x %u rows exceeds the no-allocation limit of %llu member rows",
+                           lb->leaf_count, lb->max_leaf_rows, (unsigned long long)kNoAllocMaxRows);
+    unsigned char *base = nullptr;
+    tessa_status st = scratch_for_device(&base);
+    if (st.code) return st;
+    const LeafScratch sc{reinterpret_cast<uint32_t *>(base),
+                         reinterpret_cast<uint32_t *>(base + kNaOffFallback),
+                         kNoAllocMaxRows,
+                         reinterpret_cast<uint4 *>(base + kNaOffChainRows),
+                         kNoAllocChainRows,
+                         reinterpret_cast<uint4 *>(base + kNaOffChainPool),
+                         kNoAllocChainRows * 40,
+                         reinterpret_cast<uint2 *>(base + kNaOffLog),
+                         kNoAllocLogItems,
+                         reinterpret_cast<uint4 *>(base + kNaOffRowMeta)};
+    return leaf_topk_impl(sq8, lb, rows, out_ids, out_dists, counters, stream, nullptr, nullptr, &sc);
 }
 
 tessa_status tessa_assign_replay(const tessa_sq8_view *sq8, const tessa_assign_batch *tb, uint32_t *out_ids,

@@ -153,12 +153,14 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
               executor: int = N.EXEC_MFMA, out_ids: torch.Tensor | None = None,
               out_dists: torch.Tensor | None = None, counters: torch.Tensor | None = None,
               stream: torch.cuda.Stream | None = None, debug_rerun_every: int = 0,
-              phase_ms: list | None = None):
+              phase_ms: list | None = None, no_alloc: bool = False):
     """Enqueue the leaf operator; returns (ids int32 view of u32, dists f32, counters int64).
 
     With ``phase_ms`` (a list) the call synchronises and appends the hipEvent
     times of its kernels in ms: MFMA filter, select (each summed over the
-    call's batches), chain replay, exact re-run."""
+    call's batches), chain replay, exact re-run.  ``no_alloc`` calls the entry
+    point that keeps its scratch in a static device array (at most 65,536
+    member rows per call; ``phase_ms`` is ignored then)."""
     dev = sq8.codes.device
     if out_ids is None:
         out_ids = torch.empty(layouts.output_len, dtype=torch.int32, device=dev)
@@ -170,7 +172,10 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
     lb = N.LeafBatch(_ptr(layouts.members), _ptr(layouts.member_offsets), _ptr(layouts.member_counts),
                      _ptr(layouts.output_offsets), layouts.leaf_count, layouts.max_leaf_rows, k, executor,
                      debug_rerun_every, 0)
-    if phase_ms is None:
+    if no_alloc:
+        N.check(N.load().tessa_leaf_topk_noalloc(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
+                                                 _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk_noalloc")
+    elif phase_ms is None:
         N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                          _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
     else:
