@@ -54,7 +54,6 @@ def parse():
     ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
     ap.add_argument("--no-hashprune", action="store_true", help="skip the HashPrune reservoir leg")
     ap.add_argument("--no-recall", action="store_true", help="skip the end-to-end graph build + recall leg")
-    ap.add_argument("--recall-rows", type=int, default=200_000, help="points of the recall leg's C1-shaped set")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -225,11 +224,8 @@ def main() -> int:
         result["cpu_baseline"], result["parity_sample"] = cpu_baseline(sq8, out_ids, out_d, args.cpu_budget_s)
 
     if not args.no_recall:
-        # the C1 mixture as specified (sigma 0.3: 64 well-separated clusters) and
-        # an overlapping one (sigma 2.0) on which graph connectivity is not
-        # decided by the data alone
-        result["graph_recall"] = [recall_leg(args.recall_rows, dev, check=not args.no_cpu_baseline),
-                                  recall_leg(args.recall_rows, dev, check=False, sigma=2.0)]
+        # BASELINE configs[0] as specified, with the CPU build beside it
+        result["graph_recall"] = recall_leg(dev, check=not args.no_cpu_baseline)
         torch.cuda.empty_cache()
 
     if not args.no_subtree:
@@ -240,209 +236,92 @@ def main() -> int:
     return 0
 
 
-def recall_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(32, 64, 128), dim=128, components=64,
-               sigma=0.3, r_max=64, search_runs=3, unit_norm=True, fanout_top=10, insert_every=16):
-    """C1-shaped end-to-end graph build on the GPU and its recall@10: rows x
-    128 mixture points (64 components, sigma 0.3, seed 0, unit-norm) -> SQ8
-    -> global D0 assignment (leader count from the D0 capacity plan, each
-    point to its fanout_top = 10 nearest) -> one subtree task per D0 child (depth 1:
-    fanout 3 at its root, leaves <= 1024, k = 32 leaf top-k) -> edge records
-    (12-bit hashes from 12 uniform [-1, 1) hyperplane sketches) -> HashPrune
-    reservoirs (l_max = R = 64) -> the `_mem.index` image; then greedy search
-    of nq held-out queries (seed 1) from the medoid at each L, recall@10
-    against exact f64 ground truth.  The first 64 queries at L = 64 are
-    checked bit for bit against the oracle's search over the same graph."""
+def recall_leg(dev, check=True, search_l=(32, 64, 128, 256), k_recall=10, search_runs=3):
+    """BASELINE configs[0] (C1) end to end on the GPU: 200,000 x 128 mixture
+    points (64 components, centres N(0, I), sigma 0.3, seed 0, not
+    normalised) -> shear_amd.pipeline.build_graph (SQ8, global D0 with
+    replication fanout 2, a subtree per D0 child with fanout 2 at its root,
+    leaves <= 1024, k = 32, 12-bit HashPrune with R = 64, `_mem.index`
+    image); 1,000 held-out queries (seed 1) searched from the build's entry
+    point, recall@10 against exact f64 ground truth.  With ``check`` the CPU
+    build (oracle/pybuild.py, every stage restated, same inputs) is timed as
+    the leg's CPU baseline and its image compared byte for byte."""
     import torch
 
-    from shear_amd import d0 as D
     from shear_amd import datagen
-    from shear_amd import edges as E
     from shear_amd import graph as G
-    from shear_amd import hashprune as H
-    from shear_amd import subtree as S
+    from shear_amd import pipeline as P
     from shear_amd import tessa as T
 
-    x = datagen.gmm_torch(rows, dim, components, sigma, 0, device=dev, unit_norm=unit_norm)
-    q = datagen.gmm_queries_torch(nq, dim, components, sigma, 0, 1, device=dev, unit_norm=unit_norm)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(42)
-    planes = torch.rand((12, dim), generator=gen, device=dev) * 2.0 - 1.0
-    gids = torch.arange(rows, dtype=torch.int32, device=dev)
-    params = S.PiPNNSubtreeParams(leaf_knn=32, c_max=1024, fanout_second=3, psamp_fraction=0.001, max_leaders=128,
-                                  random_seed=42, max_depth=16)
-    # D0 leaders from the capacity plan (d0_capacity on by default): the largest
-    # admitted subtree under the default 512 MiB workspace budget sets c_target
-    c_gpu = D.find_max_admissible_rows(dim, params.leaf_knn, min(params.max_leaders, D.GPU_QUEUE_LEADER_STRIDE),
-                                       params.fanout_second, D.DEFAULT_GPU_WORKSPACE_BUDGET_BYTES, None,
-                                       params.c_max)
-    leader_plan = D.plan_root_leaders(rows, fanout_top, D.compute_thresholds(c_gpu))
-    # at 200k points the plan asks for its quality floor (64 leaders); children of
-    # ~34k rows then end one partition branch at max depth (OVERSIZED_TERMINAL_NODE),
-    # so the leg takes the larger of the plan and the sampling-rate count
-    nl = max(int(leader_plan["k_initial"]), D.d0_leader_count(rows))
-    lrows = D.sample_leader_rows(rows, nl, 42, dev)
-    # one-time library set-up (BLAS handles, first-use kernels, workspaces) on a
-    # small slice, outside the timed build
-    wq = T.quantize_sq_int8_matrix(x[:4096])
-    _ = x[:4096] @ planes.t()
-    wl = T.Sq8Matrix(wq.codes[:64].contiguous(), wq.scales[:64].contiguous(), wq.norms[:64].contiguous(), wq.dim)
-    D.global_d0_assign(wq, gids[:4096].contiguous(), wl, gids[:64].contiguous(), fanout_top)
-    _ = torch.argmin(((x[:4096].double() - x[:4096].double().mean(0)) ** 2).sum(1)).item()
-    G.pack_mem_index(torch.zeros((4, 2), dtype=torch.int32, device=dev), torch.zeros(4, dtype=torch.int32,
-                                                                                      device=dev), 0)
-    del wq, wl
-    torch.cuda.synchronize()
-    w0 = time.perf_counter()
-    sq8 = T.quantize_sq_int8_matrix(x)
-    sketches = x @ planes.t()
-    lead = T.Sq8Matrix(sq8.codes[lrows].contiguous(), sq8.scales[lrows].contiguous(), sq8.norms[lrows].contiguous(),
-                       sq8.dim)
-    _, _, offs, pts = D.global_d0_assign(sq8, gids, lead, gids[lrows].contiguous(), fanout_top)
-    offs_h = offs.cpu().numpy()
-    torch.cuda.synchronize()
-    w1 = time.perf_counter()
-    sess = S.SubtreeSession(0)
-    hp = H.HashPruneReducer(rows, r_max, dev)
-    part_ms = leaf_ms = 0.0
-    records = leaves = leaf_rows = 0
-    pending = []  # records of children not yet merged (insert_every children per HashPrune batch)
-    # every child's rows gathered once (children are contiguous runs of pts)
-    ci_all = pts.long()
-    codes_all, scales_all, norms_all = sq8.codes[ci_all], sq8.scales[ci_all], sq8.norms[ci_all]
-    leaf_max = max(256, params.c_max)  # bound on a leaf's rows (the plan's leaf_max)
-    for c in range(nl):
-        a, b = int(offs_h[c]), int(offs_h[c + 1])
-        if b - a < 2:
-            continue
-        cg = pts[a:b]
-        sub = T.Sq8Matrix(codes_all[a:b], scales_all[a:b], norms_all[a:b], sq8.dim)
-        sess.upload_device(sub, cg)
-        req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
-                                           min_recurse_size=64)
-        out = sess.run(req, params)
-        part_ms += out.partition_ms
-        leaf_ms += out.leaf_ms
-        lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
-                            out.leaf_sizes[: out.leaf_count].to(torch.int32), out.leaf_starts[: out.leaf_count] * out.k,
-                            leaf_max, out.leaf_rows * out.k)
-        rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, 12)
-        pending.append(rec[:cnt])
-        if len(pending) >= insert_every:
-            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
-            pending = []
-        records += int(cnt)
-        leaves += out.leaf_count
-        leaf_rows += out.leaf_rows
-        del rec, out, lay, sub
-    if pending:
-        hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
-        pending = []
-    targets, counts = hp.neighbors()
-    torch.cuda.synchronize()
-    w3 = time.perf_counter()
-    centroid = x.double().mean(0)
-    start = int(torch.argmin(((x.double() - centroid) ** 2).sum(1)).item())
-    image = G.pack_mem_index(targets, counts, start)
-    torch.cuda.synchronize()
-    w4 = time.perf_counter()
-    stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": nl, "d0_leader_source":
-              leader_plan["root_leader_source"], "d0_c_gpu": c_gpu, "d0_fanout_top": fanout_top,
-              "children_wall_ms": round((w3 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
-              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
-              "medoid_and_pack_ms": round((w4 - w3) * 1e3, 2)}
-    build_s = w4 - w0
-    del sess, sketches, pts, offs, codes_all, scales_all, norms_all
-    hp.close()
-    # exact ground truth in f64
+    x_h, q_h = datagen.c1_numpy()
+    rows, dim = x_h.shape
+    p = P.GraphBuildParams()
+    lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
+    sk_h = P.sketches_of(x_h, P.sketch_planes(dim, p.m_hash_bits, 7))
+    x = torch.from_numpy(x_h).to(dev)
+    q = torch.from_numpy(q_h).to(dev)
+    sk = torch.from_numpy(sk_h).to(dev)
+    # one-time library set-up (first-use kernels, workspaces) on a slice, outside the timed build
+    P.build_graph(x[:8192].contiguous(), sk[:8192].contiguous(), lead[lead < 8192][:16], p)
+    _ = T.quantize_sq_int8_matrix(x[:64])
+    built = P.build_graph(x, sk, lead, p)
     xd, qd = x.double(), q.double()
     dd = (qd * qd).sum(1, keepdim=True) - 2.0 * (qd @ xd.t()) + (xd * xd).sum(1)[None, :]
     truth = torch.topk(dd, k_recall, dim=1, largest=False).indices.cpu().numpy()
     del xd, qd, dd
     searches = []
-    parity = {}
     for L in search_l:
         ms = []
         for _ in range(search_runs + 1):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            ids, dist, cmps = G.greedy_search(x, targets, counts, start, q, L, k_recall)
+            ids, _, cmps = G.greedy_search(x, built.targets, built.counts, built.start, q, L, k_recall)
             b.record()
             b.synchronize()
             ms.append(a.elapsed_time(b))
         ms = ms[1:]
-        found = ids.cpu().numpy()
-        searches.append({"L": L, "recall_at_10": round(G.recall_at_k(found, truth, k_recall), 4),
-                         "ms": round(float(np.mean(ms)), 3), "qps": round(nq / (float(np.mean(ms)) / 1e3), 1),
+        searches.append({"L": L, "recall_at_10": round(G.recall_at_k(ids.cpu().numpy(), truth, k_recall), 4),
+                         "qps": round(len(q_h) / (float(np.mean(ms)) / 1e3), 1),
                          "mean_distance_evals": round(float(cmps.double().mean().item()) + 1.0, 1)})
-        if check and L == 64:
-            from oracle import pyoracle as orc
-
-            ns = 64
-            wi, wd, wc = orc.greedy_search(x.cpu().numpy(), targets.cpu().numpy().view(np.uint32),
-                                           counts.cpu().numpy(), start, q[:ns].cpu().numpy(), L, k_recall)
-            gi = ids[:ns].cpu().numpy().view(np.uint32)
-            gd = dist[:ns].cpu().numpy().view(np.uint32)
-            gc = cmps[:ns].cpu().numpy().view(np.uint32)
-            bad = np.nonzero(np.any(gi != wi, 1) | np.any(gd != wd.view(np.uint32), 1) | (gc != wc))[0]
-            parity = {"queries": ns, "L": L, "mismatched_queries": int(len(bad)), "bit_exact": len(bad) == 0}
-    # the reference's optional final RobustPrune (alpha 1.2, max_occlusion 750,
-    # degree 64) over the same rows, searched the same way
-    pa, pb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    pa.record()
-    ptargets, pcounts = G.robust_prune(x, targets, counts)
-    pb.record()
-    pb.synchronize()
-    pruned = {"ms": round(pa.elapsed_time(pb), 3), "mean_degree": round(float(pcounts.double().mean().item()), 2),
-              "search": []}
-    for L in search_l:
-        ids, _, cmps = G.greedy_search(x, ptargets, pcounts, start, q, L, k_recall)
-        pruned["search"].append({"L": L, "recall_at_10": round(G.recall_at_k(ids.cpu().numpy(), truth, k_recall), 4),
-                                 "mean_distance_evals": round(float(cmps.double().mean().item()) + 1.0, 1)})
-    del ptargets, pcounts
-    deg = counts.double()
-    # graph diagnostics: points reachable from the start (breadth-first over
-    # the rows) and, for 2000 sample points, the share of their exact 10
-    # nearest neighbours their own row lists
-    valid = torch.arange(r_max, device=dev)[None, :] < counts[:, None]
+    # points reachable from the entry point (breadth-first over the rows)
+    valid = torch.arange(p.l_max, device=dev)[None, :] < built.counts[:, None]
     seen = torch.zeros(rows, dtype=torch.bool, device=dev)
-    seen[start] = True
-    frontier = torch.tensor([start], device=dev)
-    hops = 0
+    seen[built.start] = True
+    frontier = torch.tensor([built.start], device=dev)
     while frontier.numel():
-        nb = targets[frontier][valid[frontier]].long()
+        nb = built.targets[frontier][valid[frontier]].long()
         nb = torch.unique(nb[~seen[nb]])
         seen[nb] = True
         frontier = nb
-        hops += 1
-    sample = torch.arange(0, rows, rows // 2000, device=dev)[:2000]
-    xs = x[sample].double()
-    ds = (xs * xs).sum(1, keepdim=True) - 2.0 * (xs @ x.double().t()) + (x.double() ** 2).sum(1)[None, :]
-    ds[torch.arange(len(sample), device=dev), sample] = float("inf")  # not itself
-    nn10 = torch.topk(ds, 10, dim=1, largest=False).indices
-    rows_s = torch.where(valid[sample], targets[sample].long(), -1)
-    row_recall = (nn10[:, :, None] == rows_s[:, None, :]).any(2).double().mean().item()
-    del xs, ds
     res = {
-        "workload": f"C1-shaped build: {rows} x {dim} f32 (64-comp GMM sigma {sigma}, unit-norm, seed 0), SQ8, "
-                    f"global D0 ({nl} leaders, fanout_top {fanout_top}), a subtree per D0 child (root fanout 3, "
-                    f"leaves <= 1024, k=32), 12-bit HashPrune l_max={r_max}; {nq} held-out queries (seed 1), "
-                    f"start = medoid",
-        "build_ms": round(build_s * 1e3, 2),
-        "points_per_s": round(rows / build_s, 1),
-        "stages": stages,
-        "graph_bytes": int(image.numel()),
-        "mean_degree": round(float(deg.mean().item()), 2),
-        "max_degree": int(counts.max().item()),
-        "start": start,
+        "workload": f"C1: {rows} x {dim} f32 (64-comp GMM, centres N(0,I), sigma 0.3, seed 0, not normalised), SQ8, "
+                    f"global D0 ({len(lead)} leaders, fanout {p.fanout_top}), a subtree per D0 child (root fanout "
+                    f"{p.fanout_second}, leaves <= {p.c_max}, k={p.leaf_knn}), {p.m_hash_bits}-bit HashPrune "
+                    f"R={p.l_max}; {len(q_h)} held-out queries (seed 1) from the entry point",
+        "build_ms": round(built.build_s * 1e3, 2),
+        "points_per_s": round(rows / built.build_s, 1),
+        "stages": built.stages,
+        "graph_bytes": int(built.image.numel()),
+        "mean_degree": round(float(built.counts.double().mean().item()), 2),
+        "max_degree": int(built.counts.max().item()),
+        "start": built.start,
         "reachable_from_start": int(seen.sum().item()),
-        "bfs_levels": hops,
-        "row_recall_at_10": round(row_recall, 4),
         "search": searches,
-        "search_parity_sample": parity,
-        "final_prune": pruned,
+        "cpu_baseline": None,
     }
-    log(f"recall leg: build {build_s * 1e3:.1f} ms, " +
-        ", ".join(f"L={s['L']} recall@10 {s['recall_at_10']}" for s in searches))
+    if check:
+        from oracle import pybuild as PB
+
+        cpu = PB.build_graph_cpu(x_h, sk_h, lead, p)
+        img = built.image.cpu().numpy().tobytes()
+        res["cpu_baseline"] = {"value": round(rows / cpu["build_s"], 1), "unit": "points/s",
+                               "cores": os.cpu_count(), "kind": "port",
+                               "sample": f"the whole C1 build ({rows} points), every stage by the oracle",
+                               "build_s": round(cpu["build_s"], 3), "stages": cpu["stages"],
+                               "image_identical": img == cpu["image"],
+                               "recall_delta": 0.0 if img == cpu["image"] else None}
+    log(f"C1 build: {built.build_s * 1e3:.1f} ms, " +
+        ", ".join(f"L={s_['L']} recall@10 {s_['recall_at_10']}" for s_ in searches))
     return res
 
 

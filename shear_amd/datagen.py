@@ -5,7 +5,8 @@ ours (and unpinned by the reference).  Points are generated component by
 component, so rows [c*per, (c+1)*per) belong to component c: "sorted by
 component", and leaves cut from consecutive rows are spatially coherent.
 
-* ``gmm_numpy``  CPU, numpy PCG64 -- used by tests and small configs.
+* ``gmm_numpy``  CPU, numpy PCG64 -- used by tests and small configs
+                 (``gmm_queries_numpy``: held-out queries of the same mixture).
 * ``gmm_torch``  GPU, torch Philox on the device -- used for bench-size data
                  (4M x 768 does not fit a host round trip inside a bench run).
 * ``c3_torch``   GPU, the in-HBM build configuration: mixture plus uniform
@@ -28,6 +29,20 @@ def gmm_numpy(n: int, dim: int, components: int, sigma: float, seed: int,
     if unit_norm:
         x /= np.linalg.norm(x, axis=1, keepdims=True)
     return x.astype(np.float32)
+
+
+def gmm_queries_numpy(nq: int, dim: int, components: int, sigma: float, seed: int, query_seed: int,
+                      unit_norm: bool = True) -> np.ndarray:
+    """Held-out queries from the mixture gmm_numpy(seed) draws: the same
+    component centres, components picked uniformly and noise drawn from a
+    separate generator (query_seed)."""
+    centers = np.random.default_rng(seed).standard_normal((components, dim)).astype(np.float64)
+    rq = np.random.default_rng(query_seed)
+    comp = rq.integers(0, components, nq)
+    q = centers[comp] + sigma * rq.standard_normal((nq, dim))
+    if unit_norm:
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+    return q.astype(np.float32)
 
 
 def gmm_torch(n: int, dim: int, components: int, sigma: float, seed: int, device="cuda",
@@ -89,3 +104,11 @@ def c3_torch(n: int, dim: int = 768, components: int = 1000, sigma: float = 0.25
         x = torch.where(noise[:, None], u, x)
         out[start:end] = x / torch.linalg.vector_norm(x, dim=1, keepdim=True)
     return out
+
+
+def c1_numpy(rows: int = 200_000, nq: int = 1000, dim: int = 128):
+    """BASELINE configs[0] (C1): rows x dim f32 from a 64-component isotropic
+    mixture, centres ~N(0, I), sigma 0.3, seed 0, not normalised; nq held-out
+    queries of the same mixture (query seed 1)."""
+    return (gmm_numpy(rows, dim, 64, 0.3, 0, unit_norm=False),
+            gmm_queries_numpy(nq, dim, 64, 0.3, 0, 1, unit_norm=False))

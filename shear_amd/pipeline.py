@@ -1,0 +1,181 @@
+"""End-to-end PiPNN graph build with the subtree operator on the GPU.
+
+Host mirror of SHEAR's build with the CUDA subtree backend (paths relative to
+shear-core/src/algorithm/pipnn/):
+
+* ``build_graph``             build_pipnn_graph_with_store (mod.rs:3365) as it runs
+  with ``--pipnn-backend cuda``: SQ8 payload, global D0 assignment
+  (rbc_partition.rs:7174 rbc_partition_gpu_subtree_streaming), one subtree
+  task per D0 child through the operator (process_quantized_subtree_l2_compact_topk,
+  compute_backend.rs:3794-3805; child depth 1, so its root uses fanout_second),
+  candidate records -> edge records (leaf_build.rs:1679-1829) -> HashPrune
+  reservoirs (hash_prune.rs:1243-1283, l_max = R), then the `_mem.index` image
+  (pipnn_oom_writer.rs:23-72)
+* ``entry_point``             gpu_subtree_entry_point_from_sq_payloads
+  (rbc_partition.rs:4964-4985): the first point of the largest D0 child, ties
+  to the smaller point id
+* ``GraphBuildParams``        the PiPNNParams fields this path reads (params.rs:2109-2111
+  fanout_top / fanout_second, :3341-3370 defaults)
+
+Every stage runs in libtessa_hip.so; this module orders the calls.  The D0
+leader sample and the sketch hyperplanes are inputs (the reference draws both
+with rand's StdRng, which this build does not reproduce), so a CPU build fed
+the same inputs must produce the same image byte for byte.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import d0 as D
+from . import edges as E
+from . import graph as G
+from . import hashprune as H
+from . import subtree as S
+from . import tessa as T
+
+
+@dataclass
+class GraphBuildParams:
+    fanout_top: int = 2        # D0 replication: each point to its fanout_top nearest leaders
+    fanout_second: int = 2     # replication at each subtree's root (depth 1)
+    c_max: int = 1024          # leaf size bound (plan leaf_max = max(256, c_max))
+    leaf_knn: int = 32         # k of the leaf top-k
+    l_max: int = 64            # HashPrune reservoir = maximum out-degree R
+    m_hash_bits: int = 12
+    psamp_fraction: float = 0.001
+    max_leaders: int = 128
+    max_depth: int = 16
+    random_seed: int = 42
+    min_recurse_size: int = 64
+    insert_every: int = 16     # D0 children per HashPrune batch (the reservoirs do not depend on batching)
+
+    def subtree_params(self) -> S.PiPNNSubtreeParams:
+        return S.PiPNNSubtreeParams(leaf_knn=self.leaf_knn, c_max=self.c_max, fanout_second=self.fanout_second,
+                                    psamp_fraction=self.psamp_fraction, max_leaders=self.max_leaders,
+                                    random_seed=self.random_seed, max_depth=self.max_depth)
+
+
+def d0_leader_count(rows: int, dim: int, p: GraphBuildParams) -> int:
+    """D0 leaders: the capacity plan's count (largest admitted subtree under the
+    default 512 MiB workspace) or the sampling-rate count, whichever is larger
+    (the plan alone asks for its quality floor of 64 at 200k points, whose
+    ~6k-row children are fine, but the sampling rate keeps children near the
+    reference's expected size)."""
+    c_gpu = D.find_max_admissible_rows(dim, p.leaf_knn, min(p.max_leaders, D.GPU_QUEUE_LEADER_STRIDE),
+                                       p.fanout_second, D.DEFAULT_GPU_WORKSPACE_BUDGET_BYTES, None, p.c_max)
+    plan = D.plan_root_leaders(rows, p.fanout_top, D.compute_thresholds(c_gpu))
+    return min(rows, max(int(plan["k_initial"]), D.d0_leader_count(rows)))
+
+
+def d0_leader_rows(rows: int, count: int, seed: int) -> np.ndarray:
+    """``count`` distinct rows of [0, rows), ascending (int64)."""
+    return D.sample_leader_rows(rows, count, seed, "cpu").numpy()
+
+
+def sketch_planes(dim: int, m_bits: int, seed: int) -> np.ndarray:
+    """m_bits hyperplanes with coordinates uniform in [-1, 1) (f32, [m_bits, dim])."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return (torch.rand((m_bits, dim), generator=g) * 2.0 - 1.0).numpy()
+
+
+def sketches_of(x: np.ndarray, planes: np.ndarray) -> np.ndarray:
+    """Per-point sketch coordinates (f32 [rows, m_bits]): f64 dot products
+    rounded to f32, computed once on the host and handed to every build of
+    the same points (the reference's SketchAccessor rows)."""
+    return (np.asarray(x, np.float64) @ np.asarray(planes, np.float64).T).astype(np.float32)
+
+
+def entry_point(child_offsets: np.ndarray, child_points: np.ndarray) -> int:
+    """First point of the largest D0 child (ties: the smaller point id)."""
+    offs = np.asarray(child_offsets, np.int64)
+    sizes = np.diff(offs)
+    best = None
+    for c in np.nonzero(sizes > 0)[0]:
+        cand = (int(sizes[c]), -int(child_points[offs[c]]))
+        if best is None or cand > best:
+            best = cand
+    return -best[1] if best is not None else 0
+
+
+@dataclass
+class BuiltGraph:
+    targets: torch.Tensor   # int32 [rows, l_max] (row p's neighbours first, ascending hash)
+    counts: torch.Tensor    # int32 [rows]
+    start: int
+    image: torch.Tensor     # uint8 `_mem.index` image (device)
+    build_s: float
+    stages: dict = field(default_factory=dict)
+
+
+def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray,
+                p: GraphBuildParams = GraphBuildParams()) -> BuiltGraph:
+    """Build the graph of the f32 rows ``x`` (device tensor [rows, dim]).
+
+    ``sketches`` (device f32 [rows, m_bits]) and ``leader_rows`` (ascending
+    resident rows) are the build's inputs; global ids are the row numbers."""
+    dev = x.device
+    rows, dim = x.shape
+    gids = torch.arange(rows, dtype=torch.int32, device=dev)
+    lrows = torch.from_numpy(np.asarray(leader_rows, np.int64)).to(dev)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    sq8 = T.quantize_sq_int8_matrix(x)
+    lead = T.Sq8Matrix(sq8.codes[lrows].contiguous(), sq8.scales[lrows].contiguous(),
+                       sq8.norms[lrows].contiguous(), sq8.dim)
+    _, _, offs, pts = D.global_d0_assign(sq8, gids, lead, gids[lrows].contiguous(), p.fanout_top)
+    offs_h = offs.cpu().numpy()
+    pts_h = pts.cpu().numpy().view(np.uint32)
+    start = entry_point(offs_h, pts_h)
+    torch.cuda.synchronize()
+    w1 = time.perf_counter()
+    sess = S.SubtreeSession(0)
+    hp = H.HashPruneReducer(rows, p.l_max, dev)
+    sp = p.subtree_params()
+    leaf_max = max(256, p.c_max)
+    part_ms = leaf_ms = 0.0
+    records = leaves = leaf_rows = 0
+    pending = []
+    ci_all = pts.long()
+    codes_all, scales_all, norms_all = sq8.codes[ci_all], sq8.scales[ci_all], sq8.norms[ci_all]
+    for c in range(len(offs_h) - 1):
+        a, b = int(offs_h[c]), int(offs_h[c + 1])
+        if b - a < 2:
+            continue  # a one-point child has no leaf pairs
+        cg = pts[a:b]
+        sub = T.Sq8Matrix(codes_all[a:b], scales_all[a:b], norms_all[a:b], sq8.dim)
+        sess.upload_device(sub, cg)
+        req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
+                                           min_recurse_size=p.min_recurse_size)
+        out = sess.run(req, sp)
+        part_ms += out.partition_ms
+        leaf_ms += out.leaf_ms
+        lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
+                            out.leaf_sizes[: out.leaf_count].to(torch.int32),
+                            out.leaf_starts[: out.leaf_count] * out.k, leaf_max, out.leaf_rows * out.k)
+        rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, p.m_hash_bits)
+        pending.append(rec[:cnt])
+        if len(pending) >= p.insert_every:
+            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+            pending = []
+        records += int(cnt)
+        leaves += out.leaf_count
+        leaf_rows += out.leaf_rows
+        del rec, out, lay, sub
+    if pending:
+        hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+    targets, counts = hp.neighbors()
+    image = G.pack_mem_index(targets, counts, start)
+    torch.cuda.synchronize()
+    w2 = time.perf_counter()
+    hp.close()
+    del sess
+    stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": int(len(leader_rows)),
+              "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
+              "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
+              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records}
+    return BuiltGraph(targets, counts, start, image, w2 - w0, stages)
