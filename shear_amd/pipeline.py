@@ -113,21 +113,35 @@ class BuiltGraph:
 
 
 def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray,
-                p: GraphBuildParams = GraphBuildParams()) -> BuiltGraph:
+                p: GraphBuildParams = GraphBuildParams(), observer=None) -> BuiltGraph:
     """Build the graph of the f32 rows ``x`` (device tensor [rows, dim]).
 
     ``sketches`` (device f32 [rows, m_bits]) and ``leader_rows`` (ascending
     resident rows) are the build's inputs; global ids are the row numbers."""
-    dev = x.device
-    rows, dim = x.shape
-    gids = torch.arange(rows, dtype=torch.int32, device=dev)
-    lrows = torch.from_numpy(np.asarray(leader_rows, np.int64)).to(dev)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     sq8 = T.quantize_sq_int8_matrix(x)
+    return build_graph_sq8(sq8, sketches, leader_rows, p, observer, t0=w0)
+
+
+def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.ndarray,
+                    p: GraphBuildParams = GraphBuildParams(), observer=None,
+                    t0: float | None = None) -> BuiltGraph:
+    """The build from an SQ8 payload already in device memory (build time
+    counted from ``t0``, a perf_counter value, when given).  ``observer``
+    (optional) is called once per D0 child after its records are emitted, as
+    observer(child, global_ids, output, layouts, records, record_count), for
+    checks and statistics; it must not keep device tensors alive."""
+    dev = sq8.codes.device
+    rows = sq8.rows
+    gids = torch.arange(rows, dtype=torch.int32, device=dev)
+    lrows = torch.from_numpy(np.asarray(leader_rows, np.int64)).to(dev)
+    torch.cuda.synchronize()
+    w0 = t0 if t0 is not None else time.perf_counter()
     lead = T.Sq8Matrix(sq8.codes[lrows].contiguous(), sq8.scales[lrows].contiguous(),
                        sq8.norms[lrows].contiguous(), sq8.dim)
     _, _, offs, pts = D.global_d0_assign(sq8, gids, lead, gids[lrows].contiguous(), p.fanout_top)
+    del lead
     offs_h = offs.cpu().numpy()
     pts_h = pts.cpu().numpy().view(np.uint32)
     start = entry_point(offs_h, pts_h)
@@ -140,15 +154,15 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
     part_ms = leaf_ms = 0.0
     records = leaves = leaf_rows = 0
     pending = []
-    ci_all = pts.long()
-    codes_all, scales_all, norms_all = sq8.codes[ci_all], sq8.scales[ci_all], sq8.norms[ci_all]
     for c in range(len(offs_h) - 1):
         a, b = int(offs_h[c]), int(offs_h[c + 1])
         if b - a < 2:
             continue  # a one-point child has no leaf pairs
         cg = pts[a:b]
-        sub = T.Sq8Matrix(codes_all[a:b], scales_all[a:b], norms_all[a:b], sq8.dim)
+        ci = cg.long()
+        sub = T.Sq8Matrix(sq8.codes[ci], sq8.scales[ci], sq8.norms[ci], sq8.dim)
         sess.upload_device(sub, cg)
+        del sub, ci
         req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
                                            min_recurse_size=p.min_recurse_size)
         out = sess.run(req, sp)
@@ -158,6 +172,8 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
                             out.leaf_sizes[: out.leaf_count].to(torch.int32),
                             out.leaf_starts[: out.leaf_count] * out.k, leaf_max, out.leaf_rows * out.k)
         rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, p.m_hash_bits)
+        if observer is not None:
+            observer(c, cg, out, lay, rec, cnt)
         pending.append(rec[:cnt])
         if len(pending) >= p.insert_every:
             hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
@@ -165,9 +181,10 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
         records += int(cnt)
         leaves += out.leaf_count
         leaf_rows += out.leaf_rows
-        del rec, out, lay, sub
+        del rec, out, lay
     if pending:
         hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+    pending = []
     targets, counts = hp.neighbors()
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
@@ -176,6 +193,7 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
     del sess
     stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": int(len(leader_rows)),
               "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
+              "children": int(np.count_nonzero(np.diff(offs_h) >= 2)),
               "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
               "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records}
     return BuiltGraph(targets, counts, start, image, w2 - w0, stages)
