@@ -507,6 +507,76 @@ tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targ
                                        float *dists, uint32_t *counts, void *stream);
 tessa_status tessa_hashprune_clear(tessa_hashprune *hp, void *stream);
 
+/* ---- TierLift: the bounded host reducer of the record stream ---------------
+ * Replaces SpillEdgeSink + ExternalHashPruneReducer
+ * (shear-core/src/algorithm/pipnn/spill_hashprune.rs:349-651 routing, shard
+ * buffers and segment flush; :727-851 part files and manifest; :853-892
+ * shard-by-shard reduction).  Records leave the device as the leaves emit
+ * them and are held on the host, bounded by host_budget_bytes, in
+ * source-range shards (src / shard_points); past the budget the shard with
+ * the most buffered records is written to spill files as the reference
+ * writes them: segments of at most 1,000,000 records sorted by src, in
+ * `{stem}_shard{shard:05}_part{part:03}.log` next to spill_base (rolled over
+ * past 4 GiB), listed in `candidate_segments.manifest` (shard, file, offset,
+ * bytes, records, src_min, src_max, sorted=1; ordered by shard, file,
+ * offset).  With spill_base NULL or "" exceeding the budget is an error
+ * (overflow label WORKSPACE_BUDGET).
+ *   create   num_points in [1, 2^32), shard_points >= 1 (the reference's
+ *            default is 1,000,000), l_max in [1, 256], staging_records per
+ *            pinned slot (two slots), threads for host routing / spill sorting
+ *            (0: up to 16);
+ *   push     device records (count of them) produced on `stream`: enqueues
+ *            their D2H copy on the reducer's own stream after the work
+ *            already on `stream`, never making `stream` wait; blocks only
+ *            while both staging slots are still being routed; *seq_out = the
+ *            sequence number of the batch's last slot;
+ *   copied   *seq = the highest sequence number whose copy has completed (the
+ *            device records of every push up to it may be reused);
+ *   wait     blocks until batch `seq` has been copied;
+ *   finish   writes the manifest, then reduces shard by shard on the device
+ *            (spilled segments, then buffered records, through HashPrune
+ *            reservoirs as tessa_hashprune_*) into targets [num_points * l_max]
+ *            and counts [num_points] (device pointers, the layout
+ *            tessa_hashprune_neighbors writes); enqueued on and synchronises
+ *            `stream`; equal to one tessa_hashprune reduction of every record
+ *            pushed.  Once only; no push after it;
+ *   destroy  stops the worker and frees every buffer (spill files remain).
+ * A record with src >= num_points fails the push that carried it, and every
+ * later call, with "Spill reducer encountered edge p=... outside shard
+ * range". */
+typedef struct tessa_tierlift tessa_tierlift;
+typedef struct tessa_tierlift_config {
+    uint64_t num_points;
+    uint64_t shard_points;
+    uint64_t host_budget_bytes;   /* bytes of host record blocks (1,000,000 records each) */
+    uint64_t staging_records;     /* records per pinned staging slot */
+    const char *spill_base;       /* candidate path whose directory and stem name the spill files */
+    uint32_t l_max;
+    uint32_t threads;
+} tessa_tierlift_config;
+typedef struct tessa_tierlift_stats {
+    uint64_t records;             /* records pushed */
+    uint64_t pushes;              /* staging slots filled */
+    uint64_t host_peak_bytes;     /* largest host block allocation */
+    uint64_t spilled_records;
+    uint64_t spilled_bytes;
+    uint64_t segments;
+    uint64_t reread_records;      /* records read back from spill files at finish */
+    uint32_t shards;
+    uint32_t threads;
+    double route_s;               /* worker time routing records to shards */
+    double spill_s;               /* worker time sorting and writing segments */
+    double reduce_s;              /* finish: manifest, uploads, reservoir merges */
+} tessa_tierlift_stats;
+tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierlift **out);
+tessa_status tessa_tierlift_push(tessa_tierlift *t, const tessa_edge_record *records, uint64_t count, void *stream,
+                                 uint64_t *seq_out);
+tessa_status tessa_tierlift_copied(tessa_tierlift *t, uint64_t *seq);
+tessa_status tessa_tierlift_wait(tessa_tierlift *t, uint64_t seq);
+tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_t *counts, void *stream,
+                                   tessa_tierlift_stats *stats);
+tessa_status tessa_tierlift_destroy(tessa_tierlift *t);
+
 /* ---- graph emission ----------------------------------------------------------
  * The `_mem.index` byte image DirectMemGraphWriter writes
  * (index/inmem_index/pipnn_oom_writer.rs:23-72: create, write_node per point

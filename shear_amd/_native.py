@@ -268,6 +268,22 @@ class CapturedAssignment(C.Structure):
                 ("leader_offset", C.c_uint64)]
 
 
+class TierLiftConfig(C.Structure):
+    _fields_ = [("num_points", C.c_uint64), ("shard_points", C.c_uint64), ("host_budget_bytes", C.c_uint64),
+                ("staging_records", C.c_uint64), ("spill_base", C.c_char_p), ("l_max", C.c_uint32),
+                ("threads", C.c_uint32)]
+
+
+class TierLiftStats(C.Structure):
+    _fields_ = [(f, C.c_uint64) for f in ("records", "pushes", "host_peak_bytes", "spilled_records",
+                                          "spilled_bytes", "segments", "reread_records")] + [
+        ("shards", C.c_uint32), ("threads", C.c_uint32), ("route_s", C.c_double), ("spill_s", C.c_double),
+        ("reduce_s", C.c_double)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 # Every symbol include/tessa_hip.h declares, with its ctypes signature.
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -316,6 +332,12 @@ SIGNATURES = {
     "tessa_hashprune_insert": (TessaStatus, [_P, _P, _U64, _P]),
     "tessa_hashprune_neighbors": (TessaStatus, [_P, _P, _P, _P, _P, _P]),
     "tessa_hashprune_clear": (TessaStatus, [_P, _P]),
+    "tessa_tierlift_create": (TessaStatus, [C.POINTER(TierLiftConfig), C.POINTER(_P)]),
+    "tessa_tierlift_push": (TessaStatus, [_P, _P, _U64, _P, C.POINTER(_U64)]),
+    "tessa_tierlift_copied": (TessaStatus, [_P, C.POINTER(_U64)]),
+    "tessa_tierlift_wait": (TessaStatus, [_P, _U64]),
+    "tessa_tierlift_finish": (TessaStatus, [_P, _P, _P, _P, C.POINTER(TierLiftStats)]),
+    "tessa_tierlift_destroy": (TessaStatus, [_P]),
     "tessa_graph_pack": (TessaStatus, [_P, _P, _U32, _U32, _U32, _U64, _P, _U64, C.POINTER(_U64), _P]),
     "tessa_global_d0_assign": (TessaStatus, [_P, _P, _P, _P, _U64, _U32, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P]),
     "tessa_robust_prune": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _U32, C.c_float, C.c_int, _P, _P, _P]),

@@ -1,0 +1,657 @@
+// tierlift.hip -- TierLift: the bounded host reducer of the edge-record stream.
+//
+// Reference role: SpillEdgeSink feeding ExternalHashPruneReducer
+// (shear-core/src/algorithm/pipnn/spill_hashprune.rs: shard routing
+// flush_pending_edges :569-614, shard buffers and segment flush :616-658 and
+// :727-757, part files :772-830, manifest :832-851, shard-by-shard reduction
+// :853-892).
+//
+//   push     the caller's stream records an event; a side stream (default
+//            priority) waits on it and copies the batch into one of two pinned
+//            staging slots, so leaf compute goes on while a slot drains;
+//   worker   a host thread takes the slots in order and routes their records
+//            to source-range shards (src / shard_points) with several
+//            threads, into per-shard blocks of 1,000,000 records;
+//   spill    while the blocks in use exceed the host budget, the shard with
+//            the most buffered records is written out: each block becomes one
+//            segment, sorted by src (counting sort, stable), placed in the
+//            shard's part files (rolled over past 4 GiB) at offsets fixed
+//            before the parallel writes;
+//   finish   the manifest is written, then shard by shard the spilled
+//            segments and the buffered blocks go back to the device through the
+//            pinned slots, sources are rebased to the shard, the HashPrune
+//            reservoir kernels merge them, and the shard's reservoirs are
+//            exported into the caller's neighbour table.
+//
+// A reservoir's final state depends only on its record set (HashPrune with
+// backfill and evidence policies off), so the table equals one in-HBM
+// reduction of the same records, whatever was spilled.
+#include <fcntl.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <condition_variable>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "hashprune_kernels.h"
+#include "tessa_device.h"
+
+namespace {
+
+struct Rec {
+    uint32_t src, dst;
+    uint16_t hash, flags;
+    float dist;
+};
+static_assert(sizeof(Rec) == 16, "SpillRecord16");
+
+constexpr uint64_t kBlockRecords = 1000000;                   // segment cap, spill_hashprune.rs:25,:500-505
+constexpr uint64_t kBlockBytes = kBlockRecords * sizeof(Rec);
+constexpr uint64_t kPartMaxBytes = 4ull * 1024 * 1024 * 1024;  // DEFAULT_PART_MAX_BYTES :27
+constexpr uint64_t kUploadRecords = 1ull << 26;               // records per reservoir merge at finish (1 GiB)
+constexpr uint64_t kCountingSortMaxShard = 1ull << 24;        // larger shards sort by comparison
+
+struct Shard {
+    std::vector<Rec *> blocks;  // kBlockRecords each; the last one partly filled
+    uint64_t n = 0;             // buffered records
+    uint32_t part = 0;          // current part file index
+    uint64_t part_bytes = 0;    // bytes in the current part file
+    int fd = -1;
+};
+
+struct Segment {
+    uint32_t shard, file;
+    uint64_t offset, bytes, records;
+    uint32_t src_min, src_max;
+};
+
+__global__ void rebase_src_kernel(uint4 *rec, uint64_t n, uint32_t lo) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) rec[i].x -= lo;
+}
+
+tessa_status tl_status(int32_t code, const char *fmt, ...) {
+    tessa_status s{};
+    s.code = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(s.msg, sizeof(s.msg), fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+template <typename F>
+void parallel_for(uint32_t T, F &&f) {
+    if (T <= 1) {
+        f(0u);
+        return;
+    }
+    std::vector<std::thread> pool;
+    pool.reserve(T - 1);
+    for (uint32_t w = 1; w < T; ++w) pool.emplace_back(f, w);
+    f(0u);
+    for (auto &th : pool) th.join();
+}
+
+}  // namespace
+
+struct tessa_tierlift {
+    tessa_tierlift_config cfg{};
+    int device = 0;
+    uint32_t shards = 0;
+    uint32_t threads = 1;
+    std::string dir, stem;  // part files: dir/stem_shardSSSSS_partPPP.log
+    // D2H staging
+    hipStream_t copy_stream = nullptr;
+    Rec *pinned[2] = {nullptr, nullptr};
+    hipEvent_t ready[2] = {nullptr, nullptr}, copied[2] = {nullptr, nullptr};
+    uint64_t slot_n[2] = {0, 0}, slot_seq[2] = {0, 0};
+    bool slot_full[2] = {false, false};
+    int next_slot = 0;
+    uint64_t next_seq = 0, copied_seq = 0;
+    // host worker
+    std::mutex mu;
+    std::condition_variable cv;
+    std::thread worker;
+    bool stopping = false, finished = false;
+    std::string error;
+    // shard blocks, spill files
+    std::vector<Shard> shard;
+    std::vector<Rec *> free_blocks;
+    uint64_t blocks_in_use = 0, blocks_allocated = 0;
+    std::vector<Segment> segments;
+    tessa_tierlift_stats stats{};
+};
+
+namespace {
+
+std::string part_path(const tessa_tierlift *t, uint32_t shard, uint32_t part) {
+    char tail[64];
+    snprintf(tail, sizeof(tail), "_shard%05u_part%03u.log", shard, part);
+    return t->dir + "/" + t->stem + tail;
+}
+
+Rec *take_block(tessa_tierlift *t) {
+    Rec *b = nullptr;
+    if (!t->free_blocks.empty()) {
+        b = t->free_blocks.back();
+        t->free_blocks.pop_back();
+    } else {
+        b = static_cast<Rec *>(std::malloc(kBlockBytes));
+        if (!b) return nullptr;
+        t->blocks_allocated += 1;
+        t->stats.host_peak_bytes = std::max(t->stats.host_peak_bytes, t->blocks_allocated * kBlockBytes);
+    }
+    t->blocks_in_use += 1;
+    return b;
+}
+
+void give_block(tessa_tierlift *t, Rec *b) {
+    t->free_blocks.push_back(b);
+    t->blocks_in_use -= 1;
+}
+
+// Writes shard s's buffered records as segments (one per block, sorted by
+// src) to its part files, then returns the blocks to the pool.  Worker only.
+bool spill_shard(tessa_tierlift *t, uint32_t s, std::string &err) {
+    Shard &sh = t->shard[s];
+    const double t0 = now_s();
+    const uint32_t nb = (uint32_t)sh.blocks.size();
+    struct Place {
+        uint32_t file;
+        int fd;
+        uint64_t offset, records;
+    };
+    std::vector<Place> place(nb);
+    std::vector<int> to_close;  // part files rolled over here: closed after the writes
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint64_t n = std::min<uint64_t>(kBlockRecords, sh.n - (uint64_t)b * kBlockRecords);
+        const uint64_t bytes = n * sizeof(Rec);
+        if (sh.fd < 0 || sh.part_bytes + bytes > kPartMaxBytes) {
+            if (sh.fd >= 0) {
+                to_close.push_back(sh.fd);
+                sh.fd = -1;
+                sh.part += 1;
+            }
+            const std::string path = part_path(t, s, sh.part);
+            sh.fd = open(path.c_str(), O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+            sh.part_bytes = 0;
+            if (sh.fd < 0) {
+                for (int fd : to_close) close(fd);
+                err = "TierLift spill: cannot create " + path;
+                return false;
+            }
+        }
+        place[b] = Place{sh.part, sh.fd, sh.part_bytes, n};
+        sh.part_bytes += bytes;
+    }
+    const uint64_t lo = (uint64_t)s * t->cfg.shard_points;
+    const uint64_t span = std::min<uint64_t>(t->cfg.shard_points, t->cfg.num_points - lo);
+    std::vector<uint32_t> smin(nb), smax(nb);
+    const uint32_t T = std::max(1u, std::min<uint32_t>(t->threads, nb));
+    std::vector<char> failed(T, 0);
+    parallel_for(T, [&](uint32_t w) {
+        std::vector<Rec> out(kBlockRecords);
+        std::vector<uint32_t> hist(span <= kCountingSortMaxShard ? span + 1 : 0);
+        for (uint32_t b = w; b < nb; b += T) {
+            const Rec *in = sh.blocks[b];
+            const uint64_t n = place[b].records;
+            if (!hist.empty()) {
+                std::fill(hist.begin(), hist.end(), 0u);
+                for (uint64_t i = 0; i < n; ++i) hist[in[i].src - lo + 1] += 1;
+                for (uint64_t k = 1; k <= span; ++k) hist[k] += hist[k - 1];
+                for (uint64_t i = 0; i < n; ++i) out[hist[in[i].src - lo]++] = in[i];
+            } else {
+                std::copy(in, in + n, out.begin());
+                std::stable_sort(out.begin(), out.begin() + n, [](const Rec &a, const Rec &c) { return a.src < c.src; });
+            }
+            smin[b] = n ? out[0].src : 0u;
+            smax[b] = n ? out[n - 1].src : 0u;
+            const char *p = reinterpret_cast<const char *>(out.data());
+            uint64_t left = n * sizeof(Rec), off = place[b].offset;
+            while (left) {
+                const ssize_t wr = pwrite(place[b].fd, p, left, (off_t)off);
+                if (wr <= 0) {
+                    failed[w] = 1;
+                    break;
+                }
+                p += wr;
+                off += (uint64_t)wr;
+                left -= (uint64_t)wr;
+            }
+        }
+    });
+    for (int fd : to_close) close(fd);
+    for (char f : failed)
+        if (f) {
+            err = "TierLift spill: short write to a part file of shard " + std::to_string(s);
+            return false;
+        }
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint64_t bytes = place[b].records * sizeof(Rec);
+        t->segments.push_back(Segment{s, place[b].file, place[b].offset, bytes, place[b].records, smin[b], smax[b]});
+        t->stats.spilled_records += place[b].records;
+        t->stats.spilled_bytes += bytes;
+        t->stats.segments += 1;
+        give_block(t, sh.blocks[b]);
+    }
+    sh.blocks.clear();
+    sh.n = 0;
+    t->stats.spill_s += now_s() - t0;
+    return true;
+}
+
+// Routes n records to their shards' blocks: a count pass and a scatter pass
+// over T threads, each thread's records placed after the previous thread's
+// (arrival order within a shard).
+bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
+    const double t0 = now_s();
+    const uint32_t S = t->shards;
+    const uint64_t sp = t->cfg.shard_points;
+    const uint32_t T = n < (1u << 16) ? 1u : t->threads;
+    std::vector<std::vector<uint64_t>> cnt(T, std::vector<uint64_t>(S, 0));
+    std::vector<uint64_t> bad(T, ~0ull);
+    auto range = [&](uint32_t w, uint64_t &a, uint64_t &b) {
+        a = n * w / T;
+        b = n * (w + 1) / T;
+    };
+    parallel_for(T, [&](uint32_t w) {
+        uint64_t a, b;
+        range(w, a, b);
+        uint64_t *c = cnt[w].data();
+        for (uint64_t i = a; i < b; ++i) {
+            if (r[i].src >= t->cfg.num_points) {
+                bad[w] = std::min(bad[w], i);
+                continue;
+            }
+            c[r[i].src / sp] += 1;
+        }
+    });
+    for (uint32_t w = 0; w < T; ++w)
+        if (bad[w] != ~0ull) {
+            char m[200];
+            snprintf(m, sizeof(m), "Spill reducer encountered edge p=%u outside shard range [0, %llu)", r[bad[w]].src,
+                     (unsigned long long)t->cfg.num_points);
+            err = m;
+            return false;
+        }
+    std::vector<std::vector<uint64_t>> pos(T, std::vector<uint64_t>(S, 0));
+    for (uint32_t s = 0; s < S; ++s) {
+        Shard &sh = t->shard[s];
+        uint64_t at = sh.n;
+        for (uint32_t w = 0; w < T; ++w) {
+            pos[w][s] = at;
+            at += cnt[w][s];
+        }
+        while (sh.blocks.size() * kBlockRecords < at) {
+            Rec *b = take_block(t);
+            if (!b) {
+                err = "TierLift: host block allocation failed";
+                return false;
+            }
+            sh.blocks.push_back(b);
+        }
+        sh.n = at;
+    }
+    parallel_for(T, [&](uint32_t w) {
+        uint64_t a, b;
+        range(w, a, b);
+        uint64_t *p = pos[w].data();
+        for (uint64_t i = a; i < b; ++i) {
+            const uint32_t s = (uint32_t)(r[i].src / sp);
+            const uint64_t at = p[s]++;
+            t->shard[s].blocks[at / kBlockRecords][at % kBlockRecords] = r[i];
+        }
+    });
+    t->stats.records += n;
+    t->stats.route_s += now_s() - t0;
+    return true;
+}
+
+bool over_budget(const tessa_tierlift *t) { return t->blocks_in_use * kBlockBytes > t->cfg.host_budget_bytes; }
+
+void worker_main(tessa_tierlift *t) {
+    (void)hipSetDevice(t->device);
+    int slot = 0;
+    for (;;) {
+        {
+            std::unique_lock<std::mutex> lk(t->mu);
+            t->cv.wait(lk, [&] { return t->slot_full[slot] || t->stopping; });
+            if (!t->slot_full[slot]) return;
+        }
+        bool ok = hipEventSynchronize(t->copied[slot]) == hipSuccess;
+        bool clean;
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            t->copied_seq = t->slot_seq[slot];
+            if (!ok && t->error.empty()) t->error = "TierLift: D2H copy of a record batch failed";
+            clean = t->error.empty();
+        }
+        t->cv.notify_all();
+        if (clean) {
+            std::string err;
+            ok = route(t, t->pinned[slot], t->slot_n[slot], err);
+            while (ok && over_budget(t)) {
+                if (t->dir.empty()) {
+                    char m[240];
+                    snprintf(m, sizeof(m),
+                             "TierLift host budget of %llu bytes exceeded and no spill path given "
+                             "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                             (unsigned long long)t->cfg.host_budget_bytes,
+                             (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+                    err = m;
+                    ok = false;
+                    break;
+                }
+                uint32_t big = 0;
+                for (uint32_t s = 1; s < t->shards; ++s)
+                    if (t->shard[s].n > t->shard[big].n) big = s;
+                ok = spill_shard(t, big, err);
+            }
+            if (!ok) {
+                std::lock_guard<std::mutex> lk(t->mu);
+                t->error = err;
+            }
+        }
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            t->slot_full[slot] = false;
+        }
+        t->cv.notify_all();
+        slot ^= 1;
+    }
+}
+
+// Copies n records from host memory (pageable) to dev through the pinned
+// slots (alternating; a slot is refilled after its previous H2D finished),
+// the memcpy split over the worker threads.
+bool upload(tessa_tierlift *t, const Rec *src, uint64_t n, uint4 *dev, hipStream_t hs, int &slot) {
+    const uint64_t cap = t->cfg.staging_records;
+    for (uint64_t a = 0; a < n; a += cap) {
+        const uint64_t m = std::min<uint64_t>(cap, n - a);
+        if (hipEventSynchronize(t->copied[slot]) != hipSuccess) return false;
+        Rec *dst = t->pinned[slot];
+        const uint32_t T = m < (1u << 18) ? 1u : t->threads;
+        parallel_for(T, [&](uint32_t w) {
+            const uint64_t x = m * w / T, y = m * (w + 1) / T;
+            std::memcpy(dst + x, src + a + x, (y - x) * sizeof(Rec));
+        });
+        if (hipMemcpyAsync(dev + a, dst, m * sizeof(Rec), hipMemcpyHostToDevice, hs) != hipSuccess ||
+            hipEventRecord(t->copied[slot], hs) != hipSuccess)
+            return false;
+        slot ^= 1;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierlift **out) {
+    if (!cfg || !out) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: null argument");
+    *out = nullptr;
+    if (cfg->num_points == 0 || cfg->num_points > 0xffffffffull || cfg->shard_points == 0 || cfg->l_max == 0 ||
+        cfg->staging_records == 0)
+        return tl_status(TESSA_ERR_INVALID_ARGUMENT,
+                         "tierlift: num_points in [1, 2^32), shard_points, l_max and staging_records must be > 0");
+    if (cfg->l_max > tessa::kHpMaxLMax)
+        return tl_status(TESSA_ERR_UNSUPPORTED, "tierlift: l_max=%u above %u", cfg->l_max, tessa::kHpMaxLMax);
+    auto *t = new (std::nothrow) tessa_tierlift();
+    if (!t) return tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: host allocation failed");
+    t->cfg = *cfg;
+    t->cfg.spill_base = nullptr;  // copied below; the caller's string need not outlive the call
+    t->shards = (uint32_t)((cfg->num_points + cfg->shard_points - 1) / cfg->shard_points);
+    t->threads = cfg->threads ? cfg->threads : std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (cfg->spill_base && cfg->spill_base[0]) {
+        // part files sit next to the base path, named after its stem (spill_hashprune.rs:823-830)
+        const std::string base = cfg->spill_base;
+        const size_t slash = base.find_last_of('/');
+        t->dir = slash == std::string::npos ? std::string(".") : slash == 0 ? std::string("/") : base.substr(0, slash);
+        std::string name = slash == std::string::npos ? base : base.substr(slash + 1);
+        const size_t dot = name.find_last_of('.');
+        if (dot != std::string::npos && dot > 0) name = name.substr(0, dot);
+        t->stem = name.empty() ? std::string("candidate") : name;
+    }
+    t->shard.resize(t->shards);
+    bool ok = hipGetDevice(&t->device) == hipSuccess &&
+              hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; ok && i < 2; ++i)
+        ok = hipHostMalloc((void **)&t->pinned[i], cfg->staging_records * sizeof(Rec)) == hipSuccess &&
+             hipEventCreateWithFlags(&t->ready[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&t->copied[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        tessa_tierlift_destroy(t);
+        return tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: staging set-up (pinned 2 x %llu records) failed",
+                         (unsigned long long)cfg->staging_records);
+    }
+    t->stats.shards = t->shards;
+    t->stats.threads = t->threads;
+    t->worker = std::thread(worker_main, t);
+    *out = t;
+    return tessa_status{};
+}
+
+tessa_status tessa_tierlift_push(tessa_tierlift *t, const tessa_edge_record *records, uint64_t count, void *stream,
+                                 uint64_t *seq_out) {
+    if (!t) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift is null");
+    if (count && !records) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: null records");
+    if (t->finished) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: push after finish");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    uint64_t done = 0;
+    while (done < count) {
+        const uint64_t n = std::min<uint64_t>(t->cfg.staging_records, count - done);
+        const int slot = t->next_slot;
+        {
+            std::unique_lock<std::mutex> lk(t->mu);
+            t->cv.wait(lk, [&] { return !t->slot_full[slot] || !t->error.empty(); });
+            if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
+        }
+        // the copy waits for the caller's stream; the caller's stream does not wait for the copy
+        if (hipEventRecord(t->ready[slot], s) != hipSuccess ||
+            hipStreamWaitEvent(t->copy_stream, t->ready[slot], 0) != hipSuccess ||
+            hipMemcpyAsync(t->pinned[slot], records + done, n * sizeof(Rec), hipMemcpyDeviceToHost, t->copy_stream) !=
+                hipSuccess ||
+            hipEventRecord(t->copied[slot], t->copy_stream) != hipSuccess)
+            return tl_status(TESSA_ERR_HIP, "tierlift: enqueueing the D2H copy failed");
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            t->slot_n[slot] = n;
+            t->slot_seq[slot] = ++t->next_seq;
+            t->slot_full[slot] = true;
+        }
+        t->cv.notify_all();
+        t->next_slot ^= 1;
+        done += n;
+        t->stats.pushes += 1;
+    }
+    if (seq_out) *seq_out = t->next_seq;
+    return tessa_status{};
+}
+
+tessa_status tessa_tierlift_copied(tessa_tierlift *t, uint64_t *seq) {
+    if (!t || !seq) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: null argument");
+    std::lock_guard<std::mutex> lk(t->mu);
+    *seq = t->copied_seq;
+    if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
+    return tessa_status{};
+}
+
+tessa_status tessa_tierlift_wait(tessa_tierlift *t, uint64_t seq) {
+    if (!t) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift is null");
+    std::unique_lock<std::mutex> lk(t->mu);
+    t->cv.wait(lk, [&] { return t->copied_seq >= seq || !t->error.empty(); });
+    if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
+    return tessa_status{};
+}
+
+tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_t *counts, void *stream,
+                                   tessa_tierlift_stats *stats_out) {
+    if (!t || !targets || !counts) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: null argument");
+    if (t->finished) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: finish called twice");
+    {
+        std::unique_lock<std::mutex> lk(t->mu);
+        t->cv.wait(lk, [&] { return !t->slot_full[0] && !t->slot_full[1]; });
+        if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
+    }
+    t->finished = true;  // the worker is idle from here on; no push is accepted
+    const double t0 = now_s();
+    for (Shard &sh : t->shard)
+        if (sh.fd >= 0) {
+            close(sh.fd);
+            sh.fd = -1;
+        }
+    if (!t->dir.empty() && !t->segments.empty()) {
+        std::sort(t->segments.begin(), t->segments.end(), [](const Segment &a, const Segment &b) {
+            return a.shard != b.shard ? a.shard < b.shard : a.file != b.file ? a.file < b.file : a.offset < b.offset;
+        });
+        const std::string mpath = t->dir + "/candidate_segments.manifest";
+        FILE *m = fopen(mpath.c_str(), "w");
+        if (!m) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: cannot write %s", mpath.c_str());
+        for (const Segment &g : t->segments)
+            fprintf(m, "%u,%u,%llu,%llu,%llu,%u,%u,1\n", g.shard, g.file, (unsigned long long)g.offset,
+                    (unsigned long long)g.bytes, (unsigned long long)g.records, g.src_min, g.src_max);
+        if (fclose(m) != 0)
+            return tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: writing %s failed", mpath.c_str());
+    }
+    hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    const uint32_t sp = (uint32_t)std::min<uint64_t>(t->cfg.shard_points, t->cfg.num_points);
+    tessa_hashprune *hp = nullptr;
+    tessa_status st = tessa_hashprune_create(sp, t->cfg.l_max, &hp);
+    if (st.code) return st;
+    uint4 *dev = nullptr;
+    uint32_t *t_tmp = nullptr, *c_tmp = nullptr;
+    const uint64_t dev_cap = std::max<uint64_t>(kUploadRecords, t->cfg.staging_records);
+    if (hipMalloc(&dev, dev_cap * sizeof(Rec)) != hipSuccess ||
+        hipMalloc(&t_tmp, (uint64_t)sp * t->cfg.l_max * 4) != hipSuccess ||
+        hipMalloc(&c_tmp, (uint64_t)sp * 4) != hipSuccess)
+        st = tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: reduction buffers (%llu records) failed",
+                       (unsigned long long)dev_cap);
+    int slot = 0;
+    // the pinned slots' events now track H2D copies on hs
+    for (int i = 0; i < 2 && !st.code; ++i)
+        if (hipEventRecord(t->copied[i], hs) != hipSuccess) st = tl_status(TESSA_ERR_HIP, "tierlift: event failed");
+    std::vector<Rec> seg_buf;
+    size_t seg = 0;
+    for (uint32_t s = 0; s < t->shards && !st.code; ++s) {
+        const uint32_t lo = (uint32_t)((uint64_t)s * t->cfg.shard_points);
+        const uint32_t n_s = (uint32_t)std::min<uint64_t>(t->cfg.shard_points, t->cfg.num_points - lo);
+        uint64_t fill = 0;
+        auto merge = [&]() -> tessa_status {
+            if (!fill) return tessa_status{};
+            hipLaunchKernelGGL(rebase_src_kernel, dim3((uint32_t)((fill + 255) / 256)), dim3(256), 0, hs, dev, fill, lo);
+            tessa_status s2 = tessa_hashprune_insert(hp, reinterpret_cast<const tessa_edge_record *>(dev), fill, stream);
+            fill = 0;
+            return s2;
+        };
+        auto add = [&](const Rec *src, uint64_t n) -> tessa_status {
+            for (uint64_t a = 0; a < n;) {
+                const uint64_t m = std::min<uint64_t>(dev_cap - fill, n - a);
+                if (!upload(t, src + a, m, dev + fill, hs, slot))
+                    return tl_status(TESSA_ERR_HIP, "tierlift: H2D of shard %u records failed", s);
+                fill += m;
+                a += m;
+                if (fill == dev_cap) {
+                    tessa_status s2 = merge();
+                    if (s2.code) return s2;
+                }
+            }
+            return tessa_status{};
+        };
+        st = tessa_hashprune_clear(hp, stream);
+        // spilled segments of this shard (manifest order), then its buffered blocks
+        for (; !st.code && seg < t->segments.size() && t->segments[seg].shard == s; ++seg) {
+            const Segment &g = t->segments[seg];
+            const std::string path = part_path(t, g.shard, g.file);
+            const int fd = open(path.c_str(), O_RDONLY | O_CLOEXEC);
+            if (fd < 0) {
+                st = tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: cannot reopen %s", path.c_str());
+                break;
+            }
+            // seg_buf is read by in-flight H2D copies only through the pinned slots
+            seg_buf.resize(g.records);
+            char *p = reinterpret_cast<char *>(seg_buf.data());
+            uint64_t left = g.bytes, off = g.offset;
+            while (left) {
+                const ssize_t r = pread(fd, p, left, (off_t)off);
+                if (r <= 0) break;
+                p += r;
+                off += (uint64_t)r;
+                left -= (uint64_t)r;
+            }
+            close(fd);
+            if (left) {
+                st = tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: short read of a segment of %s", path.c_str());
+                break;
+            }
+            t->stats.reread_records += g.records;
+            st = add(seg_buf.data(), g.records);
+        }
+        Shard &sh = t->shard[s];
+        for (size_t b = 0; b < sh.blocks.size() && !st.code; ++b)
+            st = add(sh.blocks[b], std::min<uint64_t>(kBlockRecords, sh.n - b * kBlockRecords));
+        if (!st.code) st = merge();
+        if (!st.code) st = tessa_hashprune_neighbors(hp, t_tmp, nullptr, nullptr, c_tmp, stream);
+        if (!st.code &&
+            (hipMemcpyAsync(targets + (uint64_t)lo * t->cfg.l_max, t_tmp, (uint64_t)n_s * t->cfg.l_max * 4,
+                            hipMemcpyDeviceToDevice, hs) != hipSuccess ||
+             hipMemcpyAsync(counts + lo, c_tmp, (uint64_t)n_s * 4, hipMemcpyDeviceToDevice, hs) != hipSuccess))
+            st = tl_status(TESSA_ERR_HIP, "tierlift: shard export copy failed");
+        if (!st.code && hipStreamSynchronize(hs) != hipSuccess) st = tl_status(TESSA_ERR_HIP, "tierlift: sync failed");
+        for (Rec *b : sh.blocks) give_block(t, b);
+        sh.blocks.clear();
+        sh.n = 0;
+    }
+    (void)hipStreamSynchronize(hs);
+    if (dev) (void)hipFree(dev);
+    if (t_tmp) (void)hipFree(t_tmp);
+    if (c_tmp) (void)hipFree(c_tmp);
+    tessa_hashprune_destroy(hp);
+    for (Rec *b : t->free_blocks) std::free(b);
+    t->free_blocks.clear();
+    t->blocks_allocated = 0;
+    t->stats.reduce_s = now_s() - t0;
+    if (stats_out) *stats_out = t->stats;
+    return st;
+}
+
+tessa_status tessa_tierlift_destroy(tessa_tierlift *t) {
+    if (!t) return tessa_status{};
+    if (t->worker.joinable()) {
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            t->stopping = true;
+        }
+        t->cv.notify_all();
+        t->worker.join();
+    }
+    for (Shard &sh : t->shard) {
+        if (sh.fd >= 0) close(sh.fd);
+        for (Rec *b : sh.blocks) std::free(b);
+    }
+    for (Rec *b : t->free_blocks) std::free(b);
+    if (t->copy_stream) (void)hipStreamSynchronize(t->copy_stream);
+    for (int i = 0; i < 2; ++i) {
+        if (t->copied[i]) (void)hipEventSynchronize(t->copied[i]);
+        if (t->pinned[i]) (void)hipHostFree(t->pinned[i]);
+        if (t->ready[i]) (void)hipEventDestroy(t->ready[i]);
+        if (t->copied[i]) (void)hipEventDestroy(t->copied[i]);
+    }
+    if (t->copy_stream) (void)hipStreamDestroy(t->copy_stream);
+    delete t;
+    return tessa_status{};
+}
+
+}  // extern "C"

@@ -36,6 +36,7 @@ from . import graph as G
 from . import hashprune as H
 from . import subtree as S
 from . import tessa as T
+from . import tierlift as TL
 
 
 @dataclass
@@ -113,7 +114,8 @@ class BuiltGraph:
 
 
 def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray,
-                p: GraphBuildParams = GraphBuildParams(), observer=None) -> BuiltGraph:
+                p: GraphBuildParams = GraphBuildParams(), observer=None,
+                host_reducer: TL.TierLiftParams | None = None) -> BuiltGraph:
     """Build the graph of the f32 rows ``x`` (device tensor [rows, dim]).
 
     ``sketches`` (device f32 [rows, m_bits]) and ``leader_rows`` (ascending
@@ -121,17 +123,23 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     sq8 = T.quantize_sq_int8_matrix(x)
-    return build_graph_sq8(sq8, sketches, leader_rows, p, observer, t0=w0)
+    return build_graph_sq8(sq8, sketches, leader_rows, p, observer, t0=w0, host_reducer=host_reducer)
 
 
 def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.ndarray,
                     p: GraphBuildParams = GraphBuildParams(), observer=None,
-                    t0: float | None = None) -> BuiltGraph:
+                    t0: float | None = None, host_reducer: TL.TierLiftParams | None = None) -> BuiltGraph:
     """The build from an SQ8 payload already in device memory (build time
     counted from ``t0``, a perf_counter value, when given).  ``observer``
     (optional) is called once per D0 child after its records are emitted, as
     observer(child, global_ids, output, layouts, records, record_count), for
-    checks and statistics; it must not keep device tensors alive."""
+    checks and statistics; it must not keep device tensors alive.
+
+    ``host_reducer`` routes the records through the TierLift host reducer
+    (bounded host memory, spill files past the budget) instead of device
+    reservoirs: each child's records are queued for copy as soon as they are
+    emitted, and the copies overlap the next children's partition and leaf
+    work.  Both reducers give the same table."""
     dev = sq8.codes.device
     rows = sq8.rows
     gids = torch.arange(rows, dtype=torch.int32, device=dev)
@@ -148,7 +156,12 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     torch.cuda.synchronize()
     w1 = time.perf_counter()
     sess = S.SubtreeSession(0)
-    hp = H.HashPruneReducer(rows, p.l_max, dev)
+    hp = tl = None
+    if host_reducer is not None:
+        tl = TL.TierLiftReducer(rows, p.l_max, host_reducer, dev)
+    else:
+        hp = H.HashPruneReducer(rows, p.l_max, dev)
+    push_s = 0.0
     sp = p.subtree_params()
     leaf_max = max(256, p.c_max)
     part_ms = leaf_ms = 0.0
@@ -174,7 +187,12 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, p.m_hash_bits)
         if observer is not None:
             observer(c, cg, out, lay, rec, cnt)
-        pending.append(rec[:cnt])
+        if tl is not None:
+            q0 = time.perf_counter()
+            tl.push(rec, int(cnt))
+            push_s += time.perf_counter() - q0
+        else:
+            pending.append(rec[:cnt])
         if len(pending) >= p.insert_every:
             hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
             pending = []
@@ -185,15 +203,25 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     if pending:
         hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
     pending = []
-    targets, counts = hp.neighbors()
+    if tl is not None:
+        torch.cuda.synchronize()
+        w_emit = time.perf_counter()
+        targets, counts = tl.finish()
+        tl_stats = dict(tl.stats, push_blocked_s=round(push_s, 3), emit_done_s=round(w_emit - w1, 3))
+        tl.close()
+    else:
+        targets, counts = hp.neighbors()
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
     w2 = time.perf_counter()
-    hp.close()
+    if hp is not None:
+        hp.close()
     del sess
     stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": int(len(leader_rows)),
               "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
               "children": int(np.count_nonzero(np.diff(offs_h) >= 2)),
               "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
               "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records}
+    if tl is not None:
+        stages["tierlift"] = tl_stats
     return BuiltGraph(targets, counts, start, image, w2 - w0, stages)

@@ -1,0 +1,149 @@
+"""TierLift, the bounded host reducer: device records copied to the host
+through the pinned double buffer, routed to source-range shards, spilled past
+the host budget as the reference's part files and manifest, and reduced shard
+by shard on the GPU.
+
+  * the neighbour table equals the oracle's HashPrune reduction of the same
+    records (orc_hashprune_reduce) and the device reservoirs' (one in-HBM
+    reduction), with and without spilling, over several shards;
+  * the spill artifacts read back with the reference-format reader
+    (spill.read_spill_artifacts: segment bytes, src range, shard ids, sorted
+    flag) and hold exactly the records the reducer says it spilled, a subset
+    of those pushed;
+  * host block memory stays within the budget plus one staging slot and one
+    partial block per shard;
+  * a source outside [0, num_points) and a budget overrun without a spill
+    path are reported;
+  * a whole C1 build through TierLift (budget below the record volume, so
+    shards spill) writes the same `_mem.index` image as the in-HBM build."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import require_gpu
+from shear_amd import _native as N
+from shear_amd import datagen
+from shear_amd import edges as E
+from shear_amd import hashprune as H
+from shear_amd import pipeline as P
+from shear_amd import spill as SP
+from shear_amd import tierlift as TL
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    return require_gpu()
+
+
+def _records(n_rec, num_points, seed):
+    rng = np.random.default_rng(seed)
+    r = np.zeros(n_rec, E.EDGE_RECORD_DTYPE)
+    src = rng.integers(0, num_points, n_rec, dtype=np.uint64)
+    dst = rng.integers(0, num_points, n_rec, dtype=np.uint64)
+    r["src"] = src
+    r["dst"] = dst
+    r["hash"] = ((src * 2654435761 + dst * 40503) >> 7) & 0xFFF  # a function of the pair, as the sketches give
+    r["dist"] = rng.random(n_rec, dtype=np.float32) * 4.0
+    r["dist"][::2] = np.round(r["dist"][::2], 2)  # distance ties
+    return r
+
+
+def _dev(rec):
+    return torch.from_numpy(np.ascontiguousarray(rec).view(np.int32).reshape(-1, 4).copy()).cuda()
+
+
+def _push_all(tl, rec, batches):
+    dev = _dev(rec)
+    cuts = np.linspace(0, len(rec), batches + 1).astype(int)
+    seqs = [tl.push(dev[a:b].contiguous(), b - a) for a, b in zip(cuts[:-1], cuts[1:])]
+    return seqs
+
+
+def _table(t, c):
+    return t.cpu().numpy().view(np.uint32), c.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("budget_mb,shard_points", [(4096, 1_000_000), (48, 20_000), (16, 7_000)])
+def test_tierlift_matches_oracle(gpu, orc, tmp_path, budget_mb, shard_points):
+    num_points, l_max = 60_000, 64
+    rec = _records(6_000_000, num_points, 7)
+    base = tmp_path / "cand.log"
+    prm = TL.TierLiftParams(host_budget_bytes=budget_mb << 20, spill_base=str(base), shard_points=shard_points,
+                            staging_records=1 << 20)
+    with TL.TierLiftReducer(num_points, l_max, prm, gpu) as tl:
+        seqs = _push_all(tl, rec, 7)
+        tl.wait(seqs[-1])
+        t, c = tl.finish()
+        st = tl.stats
+    gt, gc = _table(t, c)
+    wt, _, _, wc = orc.hashprune_reduce(num_points, l_max, rec)
+    assert np.array_equal(gc, wc), "reservoir sizes differ from the oracle"
+    for p in range(num_points):
+        assert np.array_equal(gt[p, : gc[p]], wt[p, : wc[p]]), f"reservoir of point {p} differs"
+    assert st["records"] == len(rec)
+    assert st["shards"] == -(-num_points // shard_points)
+    slack = (1 << 20) * 16 + st["shards"] * 16_000_000
+    assert st["host_peak_bytes"] <= (budget_mb << 20) + slack, st
+    if budget_mb < 100:
+        assert st["spilled_records"] > 0 and st["segments"] > 0
+        back = SP.read_spill_artifacts(base, shard_points)
+        assert len(back) == st["spilled_records"] == st["reread_records"]
+        segs = SP.read_segments(base.parent / SP.MANIFEST_NAME)
+        assert all(s.sorted_by_src and s.record_count <= 1_000_000 for s in segs)
+        keys = [(s.shard_id, s.file_id, s.byte_offset) for s in segs]
+        assert keys == sorted(keys)
+        # the spilled records are pushed records (multiset inclusion)
+        view = lambda a: np.sort(np.ascontiguousarray(a).view(np.uint8).reshape(-1, 16).view("V16").ravel())
+        allr, spl = view(rec), view(back)
+        ia = np.searchsorted(allr, spl)
+        assert np.all(allr[np.minimum(ia, len(allr) - 1)] == spl)
+    else:
+        assert st["spilled_records"] == 0 and not (base.parent / SP.MANIFEST_NAME).exists()
+
+
+def test_tierlift_equals_device_reservoirs(gpu, tmp_path):
+    num_points, l_max = 250_000, 32
+    rec = _records(20_000_000, num_points, 11)
+    prm = TL.TierLiftParams(host_budget_bytes=96 << 20, spill_base=str(tmp_path / "c.log"), shard_points=100_000)
+    with TL.TierLiftReducer(num_points, l_max, prm, gpu) as tl:
+        _push_all(tl, rec, 5)
+        t1, c1 = tl.finish()
+        assert tl.stats["spilled_records"] > 0
+    with H.HashPruneReducer(num_points, l_max, gpu) as hp:
+        hp.insert(_dev(rec))
+        t2, c2 = hp.neighbors()
+    assert torch.equal(c1, c2) and torch.equal(t1, t2)
+
+
+def test_tierlift_errors(gpu, tmp_path):
+    rec = _records(100_000, 1000, 3)
+    rec["src"][77_777] = 1000  # outside [0, num_points)
+    with TL.TierLiftReducer(1000, 16, TL.TierLiftParams(host_budget_bytes=1 << 30), gpu) as tl:
+        tl.push(_dev(rec))
+        with pytest.raises(N.TessaError, match="outside shard range"):
+            t, c = tl.finish()
+    rec = _records(3_000_000, 50_000, 4)
+    with TL.TierLiftReducer(50_000, 16, TL.TierLiftParams(host_budget_bytes=8 << 20), gpu) as tl:
+        with pytest.raises(N.TessaError, match="WORKSPACE_BUDGET"):
+            tl.push(_dev(rec))
+            tl.finish()
+
+
+def test_c1_build_through_tierlift(gpu, tmp_path):
+    x, _ = datagen.c1_numpy()
+    rows, dim = x.shape
+    p = P.GraphBuildParams()
+    xd = torch.from_numpy(x).to(gpu)
+    sk = torch.from_numpy(P.sketches_of(x, P.sketch_planes(dim, p.m_hash_bits, 7))).to(gpu)
+    lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
+    ref = P.build_graph(xd, sk, lead, p)
+    prm = TL.TierLiftParams(host_budget_bytes=256 << 20, spill_base=str(tmp_path / "c1.log"), shard_points=60_000,
+                            staging_records=1 << 21)
+    got = P.build_graph(xd, sk, lead, p, host_reducer=prm)
+    st = got.stages["tierlift"]
+    assert st["records"] == ref.stages["edge_records"]
+    assert st["spilled_records"] > 0, st
+    assert torch.equal(got.image, ref.image), "TierLift build image differs from the in-HBM build"
+    print(f"C1 via TierLift: {got.build_s:.3f} s vs in-HBM {ref.build_s:.3f} s; {st}")
