@@ -14,6 +14,7 @@ Stage by stage it chains the oracle's restatements of the reference path
   HashPrune reservoirs      hash_prune.rs:1243-1283          orc_hashprune_reduce
   `_mem.index` image        pipnn_oom_writer.rs:23-72        graph_bytes
   entry point               rbc_partition.rs:4964-4985       (restated below)
+  terminal-depth retry      rbc_partition.rs:3004-3017, :15066-15115 (restated below)
 
 with the same inputs the GPU build takes (points, sketches, D0 leader rows,
 parameters), so the two images must be equal byte for byte.  The only
@@ -61,7 +62,7 @@ def build_graph_cpu(x: np.ndarray, sketches: np.ndarray, leader_rows: np.ndarray
     start = entry_point(offs, pts)
     w1 = time.perf_counter()
     parts = []
-    leaves_n = leaf_rows_n = 0
+    leaves_n = leaf_rows_n = retries = 0
     for c in range(len(offs) - 1):
         a, b = int(offs[c]), int(offs[c + 1])
         if b - a < 2:
@@ -71,11 +72,18 @@ def build_graph_cpu(x: np.ndarray, sketches: np.ndarray, leader_rows: np.ndarray
         n = b - a
         seed = orc.subtree_root_seed(p.random_seed, 1, n, rows, p.min_recurse_size)
         plan = _plan(n, p.leaf_knn, p.max_leaders, p.fanout_second, p.c_max)
-        leaves, ctr = orc.subtree_partition(cc, cs, cn, seed=seed, root_depth=1, max_depth=p.max_depth,
-                                            max_leaders=min(p.max_leaders, 128), fanout_second=p.fanout_second,
-                                            leaf_min=plan.leaf_min, leaf_max=plan.leaf_max,
-                                            psamp_fraction=p.psamp_fraction, max_leaf_count=plan.max_leaf_count,
-                                            max_leaf_rows=plan.max_leaf_rows)
+        def part(max_depth):
+            return orc.subtree_partition(cc, cs, cn, seed=seed, root_depth=1, max_depth=max_depth,
+                                         max_leaders=min(p.max_leaders, 128), fanout_second=p.fanout_second,
+                                         leaf_min=plan.leaf_min, leaf_max=plan.leaf_max,
+                                         psamp_fraction=p.psamp_fraction, max_leaf_count=plan.max_leaf_count,
+                                         max_leaf_rows=plan.max_leaf_rows)
+
+        leaves, ctr = part(p.max_depth)
+        if leaves is None and int(ctr[7]) == 1 << 10:
+            # rbc_partition.rs:3004-3017, :15066-15115: one retry with max_depth >= 1024
+            leaves, ctr = part(max(p.max_depth + 1, 1024))
+            retries += 1
         if leaves is None:
             raise RuntimeError(f"oracle partition of D0 child {c} overflowed: flags 0x{int(ctr[7]):x}")
         sizes = np.array([len(lf) for lf in leaves], np.int64)
@@ -103,5 +111,5 @@ def build_graph_cpu(x: np.ndarray, sketches: np.ndarray, leader_rows: np.ndarray
     w3 = time.perf_counter()
     stages = {"quantize_d0_s": round(w1 - w0, 3), "subtrees_and_records_s": round(w2 - w1, 3),
               "hashprune_and_image_s": round(w3 - w2, 3), "leaves": leaves_n, "leaf_rows": leaf_rows_n,
-              "edge_records": int(len(records))}
+              "edge_records": int(len(records)), "terminal_depth_retries": retries}
     return {"image": image, "start": start, "rows": nbr, "build_s": w3 - w0, "stages": stages}

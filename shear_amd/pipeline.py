@@ -25,7 +25,7 @@ the same inputs must produce the same image byte for byte.
 from __future__ import annotations
 
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 import torch
@@ -36,7 +36,15 @@ from . import graph as G
 from . import hashprune as H
 from . import subtree as S
 from . import tessa as T
+from . import _native as N
 from . import tierlift as TL
+
+# rbc_partition.rs:3004-3017: a D1+ child whose run fails with exactly
+# OVERSIZED_TERMINAL_NODE is run once more, unchanged but for max_depth =
+# max(max_depth + 1, 1024).
+OVF_OVERSIZED_TERMINAL_NODE = 1 << 10
+TERMINAL_DEPTH_RECOVERY_FLOOR = 1024
+TERMINAL_DEPTH_RETRY_LIMIT = 1
 
 
 @dataclass
@@ -53,6 +61,7 @@ class GraphBuildParams:
     random_seed: int = 42
     min_recurse_size: int = 64
     insert_every: int = 16     # D0 children per HashPrune batch (the reservoirs do not depend on batching)
+    gpu_workspace_budget_bytes: int = 0  # per subtree task (0: the default 512 MiB plan, tasks unchecked)
 
     def subtree_params(self) -> S.PiPNNSubtreeParams:
         return S.PiPNNSubtreeParams(leaf_knn=self.leaf_knn, c_max=self.c_max, fanout_second=self.fanout_second,
@@ -66,8 +75,9 @@ def d0_leader_count(rows: int, dim: int, p: GraphBuildParams) -> int:
     (the plan alone asks for its quality floor of 64 at 200k points, whose
     ~6k-row children are fine, but the sampling rate keeps children near the
     reference's expected size)."""
+    budget = p.gpu_workspace_budget_bytes or D.DEFAULT_GPU_WORKSPACE_BUDGET_BYTES
     c_gpu = D.find_max_admissible_rows(dim, p.leaf_knn, min(p.max_leaders, D.GPU_QUEUE_LEADER_STRIDE),
-                                       p.fanout_second, D.DEFAULT_GPU_WORKSPACE_BUDGET_BYTES, None, p.c_max)
+                                       p.fanout_second, budget, None, p.c_max)
     plan = D.plan_root_leaders(rows, p.fanout_top, D.compute_thresholds(c_gpu))
     return min(rows, max(int(plan["k_initial"]), D.d0_leader_count(rows)))
 
@@ -91,6 +101,34 @@ def sketches_of(x: np.ndarray, planes: np.ndarray) -> np.ndarray:
     return (np.asarray(x, np.float64) @ np.asarray(planes, np.float64).T).astype(np.float32)
 
 
+def sq8_from_chunks(chunks, rows: int, dim: int, planes: torch.Tensor):
+    """(Sq8Matrix, sketches f32 [rows, m_bits]) of a point set produced as f32
+    device chunks in row order: each chunk is quantized (SQ8 is per vector)
+    and sketched against ``planes`` (device f32 [m_bits, dim]) as it arrives,
+    so the f32 set is never resident as a whole."""
+    dev = planes.device
+    pd = T.sq_int8_padded_dim(dim)
+    codes = torch.empty((rows, pd), dtype=torch.int8, device=dev)
+    scales = torch.empty(rows, dtype=torch.float32, device=dev)
+    norms = torch.empty(rows, dtype=torch.float32, device=dev)
+    sk = torch.empty((rows, planes.shape[0]), dtype=torch.float32, device=dev)
+    at = 0
+    for x in chunks:
+        m = x.shape[0]
+        if at + m > rows or x.shape[1] != dim:
+            raise ValueError(f"chunk of shape {tuple(x.shape)} at row {at} does not fit [{rows}, {dim}]")
+        q = T.quantize_sq_int8_matrix(x)
+        codes[at:at + m] = q.codes
+        scales[at:at + m] = q.scales
+        norms[at:at + m] = q.norms
+        sk[at:at + m] = x @ planes.t()
+        at += m
+        del q, x
+    if at != rows:
+        raise ValueError(f"chunks held {at} rows, expected {rows}")
+    return T.Sq8Matrix(codes, scales, norms, dim), sk
+
+
 def entry_point(child_offsets: np.ndarray, child_points: np.ndarray) -> int:
     """First point of the largest D0 child (ties: the smaller point id)."""
     offs = np.asarray(child_offsets, np.int64)
@@ -111,6 +149,25 @@ class BuiltGraph:
     image: torch.Tensor     # uint8 `_mem.index` image (device)
     build_s: float
     stages: dict = field(default_factory=dict)
+
+
+def run_child(sess: S.SubtreeSession, req: S.GpuSubtreePartitionRequest, sp: S.PiPNNSubtreeParams):
+    """One D0 child's subtree run with the reference's terminal-depth retry
+    (rbc_partition.rs:15066-15115); the output's ``retried`` tells whether it
+    took the retry."""
+    try:
+        out = sess.run(req, sp)
+        out.retried = False
+        return out
+    except N.TessaError as e:
+        if e.overflow_flags != OVF_OVERSIZED_TERMINAL_NODE:
+            raise
+        nxt = max(sp.max_depth + 1, TERMINAL_DEPTH_RECOVERY_FLOOR)
+        if nxt == sp.max_depth:
+            raise
+    out = sess.run(req, replace(sp, max_depth=nxt))
+    out.retried = True
+    return out
 
 
 def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray,
@@ -162,6 +219,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     else:
         hp = H.HashPruneReducer(rows, p.l_max, dev)
     push_s = 0.0
+    depth_retries = 0
     sp = p.subtree_params()
     leaf_max = max(256, p.c_max)
     part_ms = leaf_ms = 0.0
@@ -177,8 +235,11 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         sess.upload_device(sub, cg)
         del sub, ci
         req = S.GpuSubtreePartitionRequest(point_ids=np.zeros(b - a, np.uint32), depth=1, parent_points=rows,
-                                           min_recurse_size=p.min_recurse_size)
-        out = sess.run(req, sp)
+                                           min_recurse_size=p.min_recurse_size,
+                                           memory_budget_bytes=p.gpu_workspace_budget_bytes or None)
+        out = run_child(sess, req, sp)
+        if out.retried:
+            depth_retries += 1
         part_ms += out.partition_ms
         leaf_ms += out.leaf_ms
         lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
@@ -221,7 +282,15 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
               "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
               "children": int(np.count_nonzero(np.diff(offs_h) >= 2)),
               "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
-              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records}
+              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
+              "terminal_depth_retries": depth_retries}
     if tl is not None:
         stages["tierlift"] = tl_stats
+    if p.gpu_workspace_budget_bytes:
+        # the largest task's workspace under the cap (a task above it fails its run)
+        big = int(np.diff(offs_h).max())
+        plan = S.plan_subtree(big, p.leaf_knn, min(p.max_leaders, D.GPU_QUEUE_LEADER_STRIDE), p.fanout_second,
+                              p.gpu_workspace_budget_bytes, p.c_max)
+        stages["largest_task_rows"] = big
+        stages["largest_task_workspace_bytes"] = int(plan.required_bytes)
     return BuiltGraph(targets, counts, start, image, w2 - w0, stages)

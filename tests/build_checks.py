@@ -1,0 +1,84 @@
+"""Checks shared by the large end-to-end build tests (C3, C4): a per-child
+observer for pipeline.build_graph_sq8 that collects what the oracle can check
+on samples, and the verification itself.
+
+  * every D0 child's leaves hold <= leaf_max rows, every point lands in at
+    least one leaf, and each child emits exactly sum 2 * rows * k_eff records;
+  * a few leaves of a few children equal the oracle's leaf top-k bit for bit
+    (ids and f32 distance bits);
+  * the reservoirs of sampled points equal the oracle's reservoirs over every
+    record those points received (HashPrune is a reduction: its state is a
+    function of the record set, so the sample is exact);
+  * degrees <= R, every point has a neighbour, and the image holds every row."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from gpu_helpers import assert_same
+from shear_amd import edges as E
+
+
+class BuildObserver:
+    def __init__(self, rows: int, device, check_children, sample_points: int = 4096, seed: int = 3):
+        self.covered = torch.zeros(rows, dtype=torch.bool, device=device)
+        rng = np.random.default_rng(seed)
+        self.sample = torch.from_numpy(np.sort(rng.choice(rows, sample_points, replace=False))).to(device)
+        self.in_sample = torch.zeros(rows, dtype=torch.bool, device=device)
+        self.in_sample[self.sample] = True
+        self.sampled_records = []
+        self.leaf_checks = []
+        self.max_leaf = 0
+        self.children = 0
+        self.check_children = set(check_children)
+
+    def __call__(self, c, cg, out, lay, rec, cnt):
+        sizes = out.leaf_sizes[: out.leaf_count]
+        self.max_leaf = max(self.max_leaf, int(sizes.max().item()))
+        self.children += 1
+        if self.children % 100 == 0:
+            print(f"  {self.children} D0 children built", flush=True)
+        local = out.leaf_row_ids[: out.leaf_rows].long()
+        self.covered[cg.long()[local]] = True
+        kk = torch.clamp(sizes - 1, max=out.k)
+        assert int(cnt) == int((2 * sizes * kk).sum().item()), f"child {c}: record count"
+        r = rec[:cnt]
+        self.sampled_records.append(r[self.in_sample[r[:, 0].long()]].clone())
+        if c in self.check_children:
+            starts = out.leaf_starts[: out.leaf_count].cpu().numpy()
+            sz = sizes.cpu().numpy()
+            g = cg.cpu().numpy().view(np.uint32)
+            li = out.leaf_row_ids[: out.leaf_rows].cpu().numpy().view(np.uint32)
+            ids = out.topk_ids[: out.leaf_rows * out.k].cpu().numpy().view(np.uint32).reshape(-1, out.k)
+            dd = out.topk_dists[: out.leaf_rows * out.k].cpu().numpy().reshape(-1, out.k)
+            for leaf in np.linspace(0, out.leaf_count - 1, 4).astype(int):
+                a, n = int(starts[leaf]), int(sz[leaf])
+                self.leaf_checks.append((g[li[a:a + n]], ids[a:a + n], dd[a:a + n]))
+
+    def verify(self, built, sq8, p, orc, leaf_max: int, what: str) -> None:
+        rows = sq8.rows
+        assert self.max_leaf <= leaf_max, f"{what}: leaf of {self.max_leaf} rows above {leaf_max}"
+        assert bool(self.covered.all()), f"{what}: a point is in no leaf"
+        assert self.leaf_checks, f"{what}: no leaf sampled"
+        counts = built.counts
+        assert int(counts.max().item()) <= p.l_max and int(counts.min().item()) >= 1
+        assert built.image.numel() == 24 + 4 * (rows + int(counts.sum().item()))
+        k = p.leaf_knn
+        for gl, ids, dd in self.leaf_checks:
+            gi = torch.from_numpy(gl.astype(np.int64)).to(sq8.codes.device)
+            want_ids, want_d = orc.leaf_topk(sq8.codes[gi].cpu().numpy(), sq8.scales[gi].cpu().numpy(),
+                                             sq8.norms[gi].cpu().numpy(), gl, np.arange(len(gl), dtype=np.uint32),
+                                             [0], [len(gl)], k)
+            assert_same(ids.reshape(-1), dd.reshape(-1), want_ids, want_d, f"{what} leaf sample")
+        rec = E.records_to_numpy(torch.cat(self.sampled_records), sum(int(r.shape[0]) for r in self.sampled_records))
+        pos = np.full(rows, -1, np.int64)
+        sample_h = self.sample.cpu().numpy()
+        pos[sample_h] = np.arange(len(sample_h))
+        rec = rec.copy()
+        rec["src"] = pos[rec["src"].astype(np.int64)].astype(np.uint32)
+        wt, _, _, wc = orc.hashprune_reduce(len(sample_h), p.l_max, rec)
+        gt = built.targets[self.sample].cpu().numpy().view(np.uint32)
+        gc = counts[self.sample].cpu().numpy()
+        assert np.array_equal(gc, wc), f"{what}: sampled reservoir sizes differ"
+        for i in range(len(sample_h)):
+            assert np.array_equal(gt[i, : gc[i]], wt[i, : wc[i]]), f"{what}: reservoir of point {sample_h[i]} differs"
