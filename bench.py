@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--no-recall", action="store_true", help="skip the end-to-end graph build + recall leg")
     ap.add_argument("--no-edges", action="store_true",
                     help="skip the record-emission leg (top-k slots -> SpillRecord16 edge records)")
+    ap.add_argument("--c5-rows", type=int, default=0,
+                    help="run only the out-of-memory build leg (BASELINE configs[4]: 150,000,000 rows as "
+                         "specified) at this many rows and print its JSON line instead")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the timed steps, run one int32 elementwise copy kernel of this many MiB "
                          "(read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE can be scaled")
@@ -87,6 +90,9 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     N.load()
+    if args.c5_rows:
+        print(json.dumps(c5_leg(dev, args.c5_rows)), flush=True)
+        return 0
     leaves = args.leaves
     rows = leaves * LEAF_ROWS
 
@@ -234,6 +240,105 @@ def main() -> int:
         result["subtree"] = subtree_leg(args.subtree_rows, dev, check=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def c5_leg(dev, rows, nq=1000, k_recall=10, search_l=(64, 128, 256)):
+    """BASELINE configs[4] (C5) on one GPU: 150,000,000 x 768 unit vectors
+    from a 16,000-component mixture (sigma uniform in [0.15, 0.4], seed 4),
+    generated, quantized and sketched chunk by chunk (the f32 set, 460 GB, is
+    never resident); the SQ8 set (115 GB) and every point's HashPrune
+    reservoir (R = 64: 96 GB) stay in HBM, D0 fanout 2, a subtree per D0
+    child (fanout 2, leaves <= 1,024, k = 32), the `_mem.index` image; then
+    recall@10 of 1,000 held-out queries against exact ground truth computed
+    by regenerating the f32 chunks, the search reading the SQ8 rows."""
+    import torch
+
+    from shear_amd import datagen
+    from shear_amd import graph as G
+    from shear_amd import pipeline as P
+
+    spec = datagen.c5_spec(rows)
+    dim = spec.dim
+    p = P.GraphBuildParams(insert_every=2)
+    planes = torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+
+    def chunks():
+        for i in range(spec.chunks):
+            if i % 16 == 0:
+                log(f"C5: chunk {i}/{spec.chunks}")
+            yield spec.chunk(i, dev)
+
+    sq8, sk = P.sq8_from_chunks(chunks(), rows, dim, planes)
+    torch.cuda.synchronize()
+    gen_s = time.perf_counter() - t0
+    torch.cuda.empty_cache()
+    log(f"C5: {rows} rows generated, quantized and sketched in {gen_s:.1f} s")
+    lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
+
+    class Progress:
+        n = 0
+
+        def __call__(self, *a):
+            self.n += 1
+            if self.n % 100 == 0:
+                log(f"C5: {self.n} D0 children built")
+
+    built = P.build_graph_sq8(sq8, sk, lead, p, observer=Progress())
+    del sk
+    torch.cuda.empty_cache()
+    log(f"C5: build {built.build_s:.1f} s, {built.stages}")
+
+    # exact ground truth: the f32 chunks regenerated, per chunk its 64 best
+    # by f32 distance re-ranked in f64, then the best k over all chunks
+    q = spec.queries(nq, 11, dev)
+    qd = q.double()
+    best_d = torch.full((nq, k_recall), float("inf"), dtype=torch.float64, device=dev)
+    best_i = torch.full((nq, k_recall), -1, dtype=torch.int64, device=dev)
+    t1 = time.perf_counter()
+    for i in range(spec.chunks):
+        x = spec.chunk(i, dev)
+        d = (x * x).sum(1)[None, :] - 2.0 * (q @ x.t())
+        ci = torch.topk(d, 64, dim=1, largest=False).indices
+        dd = ((x[ci].double() - qd[:, None, :]) ** 2).sum(2)
+        cd = torch.cat([best_d, dd], 1)
+        cid = torch.cat([best_i, ci + i * spec.chunk_rows], 1)
+        top = torch.topk(cd, k_recall, dim=1, largest=False).indices
+        best_d, best_i = torch.gather(cd, 1, top), torch.gather(cid, 1, top)
+        del x, d, ci, dd
+    truth = best_i.cpu().numpy()
+    truth_s = time.perf_counter() - t1
+    rec = {}
+    for L in search_l:
+        torch.cuda.synchronize()
+        s0 = time.perf_counter()
+        ids, _, _ = G.greedy_search_sq8(sq8, built.targets, built.counts, built.start, q, L, k_recall)
+        torch.cuda.synchronize()
+        rec[f"L{L}"] = {"recall@10": round(G.recall_at_k(ids.cpu().numpy(), truth, k_recall), 4),
+                        "qps": round(nq / (time.perf_counter() - s0), 1)}
+    counts = built.counts
+    return {
+        "metric": "build points/sec (C5 out-of-memory build); graph recall@10",
+        "value": round(rows / built.build_s, 1),
+        "unit": "points/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"C5: {rows} x {dim} unit vectors, 16,000-component mixture, sigma U[0.15, 0.4], "
+                               f"seed 4; SQ8 + reservoirs in HBM, D0 fanout 2, subtree fanout 2, leaves <= 1024, "
+                               f"k 32, R 64"},
+        "build_s": round(built.build_s, 2),
+        "generate_quantize_sketch_s": round(gen_s, 2),
+        "stages": built.stages,
+        "mean_degree": round(float(counts.float().mean().item()), 2),
+        "image_bytes": int(built.image.numel()),
+        "truth_s": round(truth_s, 2),
+        "recall": rec,
+        "search": "SQ8 rows (scale * code), the f32 set is not resident",
+        "peak_device_bytes": int(torch.cuda.max_memory_allocated()),
+    }
 
 
 def recall_leg(dev, check=True, search_l=(32, 64, 128, 256), k_recall=10, search_runs=3):

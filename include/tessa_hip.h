@@ -674,6 +674,16 @@ tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t
                                 const uint32_t *counts, uint32_t row_stride, uint32_t start, const float *queries,
                                 uint32_t num_queries, uint32_t L, uint32_t K, uint32_t *out_ids, float *out_dists,
                                 uint32_t *out_cmps, void *stream);
+/* The same search over SQ8 rows, for point sets whose f32 vectors do not
+ * stay resident (the out-of-memory configuration): row p reads as the f32
+ * products scales[p] * codes[p * padded_dim + i] (each rounded), i < dim, so
+ * the result is the search over the dequantized vectors.  It has no
+ * counterpart in the reference, whose search loads full-precision vectors;
+ * it serves the recall harness only.  padded_dim >= dim. */
+tessa_status tessa_graph_search_sq8(const int8_t *codes, const float *scales, uint32_t padded_dim, uint32_t num_points,
+                                    uint32_t dim, const uint32_t *targets, const uint32_t *counts, uint32_t row_stride,
+                                    uint32_t start, const float *queries, uint32_t num_queries, uint32_t L, uint32_t K,
+                                    uint32_t *out_ids, float *out_dists, uint32_t *out_cmps, void *stream);
 
 /* ---- asynchronous subtree submissions ----------------------------------
  * Replaces submit_owned_quantized_subtree_l2_compact_topk

@@ -351,6 +351,8 @@ SIGNATURES = {
     "tessa_session_set_assignment_capture": (TessaStatus, [_P, _U32]),
     "tessa_session_captured_assignments": (TessaStatus, [_P, _P, _U64, _P, _U64, C.POINTER(_U64), C.POINTER(_U64)]),
     "tessa_graph_search": (TessaStatus, [_P, _U32, _U32, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P]),
+    "tessa_graph_search_sq8": (TessaStatus, [_P, _P, _U32, _U32, _U32, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P,
+                                             _P, _P]),
 }
 
 _lib = None

@@ -23,7 +23,9 @@
 // Distances: squared L2 summed over the coordinates in order in f32, each
 // product rounded before the add (no contraction), one lane per candidate
 // (the harness's stated order; the reference's SIMD kernel may associate
-// differently).  Keys are (distance bits << 32 | id): for the non-negative
+// differently).  With SQ8 rows (sets too large to keep as f32) a row's
+// coordinate i is the f32 product scale * code[i], rounded, then the same sum:
+// the search over the dequantized vectors.  Keys are (distance bits << 32 | id): for the non-negative
 // distances this computes, the integer order is (distance, id).
 //
 // Visited set: a tag per (slot, point) holding query index + 1; tags are
@@ -84,7 +86,48 @@ __device__ __forceinline__ uint32_t rank_in(const uint64_t *a, uint32_t n, uint6
     return lo;
 }
 
-template <bool kVec4>
+// Squared L2 of the dequantized SQ8 row (scale * code[i], rounded) and the
+// query, coordinates in order; 16 codes per load when kVec16.
+template <bool kVec16>
+__device__ float sq8_l2_ordered(const int8_t *__restrict__ c, float sc, const float *__restrict__ q, uint32_t dim) {
+    float s = 0.0f;
+    if constexpr (kVec16) {
+        typedef int v4i_t __attribute__((ext_vector_type(4)));
+        const v4i_t *cv = reinterpret_cast<const v4i_t *>(c);
+        const float4 *qv = reinterpret_cast<const float4 *>(q);
+        for (uint32_t i = 0; i < dim / 16; ++i) {
+            const v4i_t w = cv[i];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 b = qv[4 * i + g];
+                const uint32_t word = (uint32_t)w[g];
+                const float bq[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = __fmul_rn(sc, (float)(int8_t)(word >> (8 * e)));
+                    const float t = __fsub_rn(x, bq[e]);
+                    s = __fadd_rn(s, __fmul_rn(t, t));
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = 0; i < dim; ++i) {
+            const float t = __fsub_rn(__fmul_rn(sc, (float)c[i]), q[i]);
+            s = __fadd_rn(s, __fmul_rn(t, t));
+        }
+    }
+    return s;
+}
+
+// kMode 0: f32 rows, scalar; 1: f32 rows, float4 loads; 2: SQ8 rows, scalar;
+// 3: SQ8 rows, 16 codes per load.
+template <int kMode>
+__device__ __forceinline__ float row_dist(const GraphSearchParams &p, uint32_t id, const float *q) {
+    if constexpr (kMode < 2) return l2_ordered<kMode == 1>(p.data + (uint64_t)id * p.dim, q, p.dim);
+    else return sq8_l2_ordered<kMode == 3>(p.codes + (uint64_t)id * p.padded_dim, p.scales[id], q, p.dim);
+}
+
+template <int kMode>
 __global__ __launch_bounds__(kThreads) void graph_search_kernel(GraphSearchParams p) {
     __shared__ WaveLists lists[kSearchWaves];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -98,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void graph_search_kernel(GraphSearchParam
         uint32_t buf = 0, size = 1, cur = 0, cmps = 0;
         if (lane == 0) {
             tags[p.start] = epoch;
-            const float d0 = l2_ordered<kVec4>(p.data + (uint64_t)p.start * p.dim, q, p.dim);
+            const float d0 = row_dist<kMode>(p, p.start, q);
             w.key[0][0] = ((uint64_t)__float_as_uint(d0) << 32) | p.start;
             w.visited[0][0] = 0u;
         }
@@ -118,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void graph_search_kernel(GraphSearchParam
                 if (fresh) fresh = atomicExch(&tags[id], epoch) != epoch;
                 uint64_t key = kNoKey;
                 if (fresh) {
-                    const float d = l2_ordered<kVec4>(p.data + (uint64_t)id * p.dim, q, p.dim);
+                    const float d = row_dist<kMode>(p, id, q);
                     key = ((uint64_t)__float_as_uint(d) << 32) | id;
                 }
                 const uint32_t nf = (uint32_t)__popcll(__ballot(fresh));
@@ -191,11 +234,19 @@ int launch_graph_search(const GraphSearchParams &p, hipStream_t stream) {
     uint64_t zg = (ntags + 255) / 256;
     zg = zg < 1 ? 1 : (zg > 8192 ? 8192 : zg);
     hipLaunchKernelGGL(zero_tags, dim3((uint32_t)zg), dim3(256), 0, stream, p.tags, ntags);
-    const bool vec4 = p.dim % 4 == 0 && reinterpret_cast<uintptr_t>(p.data) % 16 == 0 &&
-                      reinterpret_cast<uintptr_t>(p.queries) % 16 == 0;
     const dim3 grid(p.slots / kSearchWaves);
-    if (vec4) hipLaunchKernelGGL(graph_search_kernel<true>, grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL(graph_search_kernel<false>, grid, dim3(kThreads), 0, stream, p);
+    if (p.data) {
+        const bool vec4 = p.dim % 4 == 0 && reinterpret_cast<uintptr_t>(p.data) % 16 == 0 &&
+                          reinterpret_cast<uintptr_t>(p.queries) % 16 == 0;
+        if (vec4) hipLaunchKernelGGL(graph_search_kernel<1>, grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL(graph_search_kernel<0>, grid, dim3(kThreads), 0, stream, p);
+    } else {
+        const bool vec16 = p.dim % 16 == 0 && p.padded_dim % 16 == 0 &&
+                           reinterpret_cast<uintptr_t>(p.codes) % 16 == 0 &&
+                           reinterpret_cast<uintptr_t>(p.queries) % 16 == 0;
+        if (vec16) hipLaunchKernelGGL(graph_search_kernel<3>, grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL(graph_search_kernel<2>, grid, dim3(kThreads), 0, stream, p);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

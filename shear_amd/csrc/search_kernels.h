@@ -11,7 +11,10 @@ constexpr uint32_t kSearchMaxL = 256;   // search list capacity held in LDS
 constexpr uint32_t kSearchWaves = 4;    // waves (query slots) per workgroup
 
 struct GraphSearchParams {
-    const float *data;        // num_points x dim
+    const float *data;        // num_points x dim, or null with SQ8 rows
+    const int8_t *codes;      // SQ8 rows: num_points x padded_dim codes (when data is null)
+    const float *scales;      // SQ8 rows: num_points scales; a row reads as scale * code
+    uint32_t padded_dim;
     uint32_t num_points;
     uint32_t dim;
     const uint32_t *targets;  // num_points x row_stride neighbour ids

@@ -1844,10 +1844,12 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
     return ok_status();
 }
 
-tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
-                                const uint32_t *counts, uint32_t row_stride, uint32_t start, const float *queries,
-                                uint32_t num_queries, uint32_t L, uint32_t K, uint32_t *out_ids, float *out_dists,
-                                uint32_t *out_cmps, void *stream) {
+static tessa_status graph_search_impl(const float *data, const int8_t *codes, const float *scales,
+                                      uint32_t padded_dim, uint32_t num_points, uint32_t dim,
+                                      const uint32_t *targets, const uint32_t *counts, uint32_t row_stride,
+                                      uint32_t start, const float *queries, uint32_t num_queries, uint32_t L,
+                                      uint32_t K, uint32_t *out_ids, float *out_dists, uint32_t *out_cmps,
+                                      void *stream) {
     if (K > L)
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "Set L: %u to a value of at least K: %u", L, K);
     if (L == 0 || K == 0 || L > tessa::kSearchMaxL)
@@ -1857,8 +1859,10 @@ tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: start %u, %u points of dim %u", start,
                            num_points, dim);
     if (num_queries == 0) return ok_status();
-    if (!data || !counts || (row_stride && !targets) || !queries || !out_ids)
+    if ((!data && (!codes || !scales)) || !counts || (row_stride && !targets) || !queries || !out_ids)
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: null pointer");
+    if (!data && padded_dim < dim)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: padded_dim %u below dim %u", padded_dim, dim);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     DeviceWorkspace *ws = nullptr;
     tessa_status st = device_workspace(&ws);
@@ -1869,6 +1873,9 @@ tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t
               "search visited tags");
     if (st.code) return st;
     p.data = data;
+    p.codes = codes;
+    p.scales = scales;
+    p.padded_dim = padded_dim;
     p.num_points = num_points;
     p.dim = dim;
     p.targets = targets;
@@ -1885,6 +1892,24 @@ tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t
     p.tags = ws->search_tags;
     if (tessa::launch_graph_search(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "graph search launch failed");
     return ok_status();
+}
+
+tessa_status tessa_graph_search(const float *data, uint32_t num_points, uint32_t dim, const uint32_t *targets,
+                                const uint32_t *counts, uint32_t row_stride, uint32_t start, const float *queries,
+                                uint32_t num_queries, uint32_t L, uint32_t K, uint32_t *out_ids, float *out_dists,
+                                uint32_t *out_cmps, void *stream) {
+    if (!data) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: null pointer");
+    return graph_search_impl(data, nullptr, nullptr, 0, num_points, dim, targets, counts, row_stride, start, queries,
+                             num_queries, L, K, out_ids, out_dists, out_cmps, stream);
+}
+
+tessa_status tessa_graph_search_sq8(const int8_t *codes, const float *scales, uint32_t padded_dim, uint32_t num_points,
+                                    uint32_t dim, const uint32_t *targets, const uint32_t *counts, uint32_t row_stride,
+                                    uint32_t start, const float *queries, uint32_t num_queries, uint32_t L, uint32_t K,
+                                    uint32_t *out_ids, float *out_dists, uint32_t *out_cmps, void *stream) {
+    if (!codes || !scales) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "graph search: null pointer");
+    return graph_search_impl(nullptr, codes, scales, padded_dim, num_points, dim, targets, counts, row_stride, start,
+                             queries, num_queries, L, K, out_ids, out_dists, out_cmps, stream);
 }
 
 tessa_status tessa_global_d0_assign(const int8_t *codes, const float *scales, const float *norms,

@@ -97,6 +97,27 @@ def greedy_search(data: torch.Tensor, targets: torch.Tensor, counts: torch.Tenso
     return ids, d, cmps
 
 
+def greedy_search_sq8(sq8, targets: torch.Tensor, counts: torch.Tensor, start: int, queries: torch.Tensor, L: int,
+                      K: int, stream: torch.cuda.Stream | None = None):
+    """``greedy_search`` over SQ8 rows (a tessa.Sq8Matrix on the GPU): row p
+    reads as scales[p] * codes[p, :dim] in f32, so the result is the search
+    over the dequantized vectors (for sets whose f32 vectors are not kept)."""
+    n, dim = sq8.rows, sq8.dim
+    q = queries.reshape(-1, dim).contiguous()
+    t = targets.contiguous()
+    if t.shape[0] != n or counts.numel() != n:
+        raise ValueError(f"neighbour table of {t.shape[0]} rows / {counts.numel()} counts for {n} points")
+    if q.dtype != torch.float32 or t.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise ValueError("queries must be f32, targets and counts int32")
+    ids = torch.empty((q.shape[0], K), dtype=torch.int32, device=q.device)
+    d = torch.empty((q.shape[0], K), dtype=torch.float32, device=q.device)
+    cmps = torch.empty(q.shape[0], dtype=torch.int32, device=q.device)
+    N.check(N.load().tessa_graph_search_sq8(_ptr(sq8.codes), _ptr(sq8.scales), sq8.codes.shape[1], n, dim, _ptr(t),
+                                            _ptr(counts), t.shape[1], start, _ptr(q), q.shape[0], L, K, _ptr(ids),
+                                            _ptr(d), _ptr(cmps), _stream_ptr(stream)), "graph search sq8")
+    return ids, d, cmps
+
+
 def recall_at_k(found: np.ndarray, truth: np.ndarray, k: int) -> float:
     """Mean over queries of (results of the query found among the first k
     ground-truth ids) / k (apps/search_shear_index/src/main.rs:388-411)."""

@@ -211,6 +211,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     pts_h = pts.cpu().numpy().view(np.uint32)
     start = entry_point(offs_h, pts_h)
     torch.cuda.synchronize()
+    torch.cuda.empty_cache()  # the library allocates the reservoirs and workspaces itself, outside torch's cache
     w1 = time.perf_counter()
     sess = S.SubtreeSession(0)
     hp = tl = None
@@ -272,12 +273,12 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         tl.close()
     else:
         targets, counts = hp.neighbors()
+        torch.cuda.synchronize()
+        hp.close()  # the reservoirs go before the image is packed (at 150M points they hold 96 GB)
+    del sess
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
     w2 = time.perf_counter()
-    if hp is not None:
-        hp.close()
-    del sess
     stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": int(len(leader_rows)),
               "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
               "children": int(np.count_nonzero(np.diff(offs_h) >= 2)),

@@ -131,3 +131,27 @@ def test_argument_errors(gpu):
     torch.cuda.synchronize()
     assert ids.cpu().tolist() == [[4, -1]] * 3 and cm.cpu().tolist() == [0] * 3
 
+
+
+@pytest.mark.parametrize("seed,n,dim,stride,L,K,nq", [
+    (11, 4000, 128, 32, 64, 10, 200),   # dim a multiple of 16: 16 codes per load
+    (12, 1500, 20, 16, 40, 10, 60),     # dim 20 (padded to 32): the scalar path
+])
+def test_sq8_rows_match_oracle_on_dequantized_vectors(gpu, orc, seed, n, dim, stride, L, K, nq):
+    """tessa_graph_search_sq8 equals the oracle's search over the dequantized
+    rows scale * code (f32 products, rounded), bit for bit."""
+    from shear_amd import tessa as T
+
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    t, c = random_graph(rng, n, stride)
+    sq8 = T.quantize_sq_int8_matrix(torch.from_numpy(x).to(gpu))
+    codes = sq8.codes.cpu().numpy()[:, :dim].astype(np.float32)
+    xhat = (sq8.scales.cpu().numpy()[:, None] * codes).astype(np.float32)
+    want = orc.greedy_search(xhat, t, c, 5, q, L, K)
+    ids, d, cm = G.greedy_search_sq8(sq8, torch.from_numpy(t.view(np.int32)).to(gpu),
+                                     torch.from_numpy(c.astype(np.int32)).to(gpu), 5, torch.from_numpy(q).to(gpu), L, K)
+    torch.cuda.synchronize()
+    _same((ids.cpu().numpy().view(np.uint32), d.cpu().numpy(), cm.cpu().numpy().view(np.uint32)), want,
+          f"sq8 seed {seed}")
