@@ -59,9 +59,10 @@ def parse():
     ap.add_argument("--c5-rows", type=int, default=0,
                     help="run only the out-of-memory build leg (BASELINE configs[4]: 150,000,000 rows as "
                          "specified) at this many rows and print its JSON line instead")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="after the timed steps, run one int32 elementwise copy kernel of this many MiB "
-                         "(read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE can be scaled")
+    ap.add_argument("--copy-calibration-mib", type=str, default="",
+                    help="after the timed steps, run one int32 elementwise copy kernel per size in this "
+                         "comma-separated list of MiB (read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
+                         "can be scaled (two sizes cross-check the factor)")
     return ap.parse_args()
 
 
@@ -134,13 +135,13 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     launch_ms = [a.elapsed_time(b) for a, b in evs]
-    ph = np.array(phases, dtype=np.float64)  # [steps, 4]: MFMA filter, select, chain replay, exact re-run
+    ph = np.array(phases, dtype=np.float64)  # [steps, 5]: MFMA filter, select, chain replay, exact re-run, batches
     T.raise_on_overflow(ctr, "leaf top-k")
     c = ctr.cpu().numpy()
     log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, launch median {np.median(launch_ms):.3f} ms")
 
-    if args.copy_calibration_mib > 0:
-        n = args.copy_calibration_mib << 18
+    for mib in [int(v) for v in args.copy_calibration_mib.split(",") if v.strip()]:
+        n = mib << 18
         src = torch.ones(n, dtype=torch.int32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -152,16 +153,26 @@ def main() -> int:
     pairs = leaves * LEAF_ROWS * (LEAF_ROWS - 1)
     ops = 2.0 * DIM * pairs
     value_tops = ops * args.steps / wall / 1e12
-    # dominant kernel: leaf_mfma_kernel, timed with hipEvents on its stream
-    avg_kernel_s = float(np.mean(ph[:, 0])) / 1e3
-    achieved = ops / avg_kernel_s / 1e12
+    # dominant kernel: leaf_mfma_kernel (the MFMA filter), launched once per
+    # batch of work items, timed with hipEvents on its stream; per launch:
+    # the batch's share of the step's int8 ops over the launch's average time
+    batches = int(ph[0, 4])
+    ops_launch = ops / batches
+    avg_kernel_s = float(np.mean(ph[:, 0])) / batches / 1e3
+    achieved = ops_launch / avg_kernel_s / 1e12
     records_bytes = rows * K * 8
-    algo_bytes = rows * (DIM + 8) + records_bytes  # codes + scale/norm + (id, dist) records
+    survivors = float(c[N.C_LEAF_SURVIVORS]) / max(1, int(c[N.C_LEAF_ROWS]))
+    # the filter's algorithmic bytes: each leaf's codes, member ids, scales and
+    # norms read once; the survivor log entries (8 B each) and 16 B of row
+    # metadata written per row
+    algo_bytes = (rows * (DIM + 12) + rows * survivors * 8 + rows * 16) / batches
 
     traffic = None
     if args.traffic_json and os.path.exists(args.traffic_json) and leaves == LEAVES:
         with open(args.traffic_json) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")  # measured on this same C2 workload
+            tj = json.load(f)  # measured on this same C2 workload
+        if tj.get("launches_per_step") == batches:
+            traffic = tj.get("hbm_bytes_per_launch")
 
     result = {
         "metric": "TESSA leaf int8 TOPS (% MFMA peak)",
@@ -194,12 +205,14 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": os.path.relpath(args.traffic_json, HERE) if traffic is not None else None,
             "kernel": "leaf_mfma_kernel",
-            "ops_per_launch": ops,
-            "algorithmic_hbm_bytes_per_launch": algo_bytes,
-            "kernel_ms_mean": round(float(np.mean(ph[:, 0])), 4),
-            "kernel_ms_min": round(float(np.min(ph[:, 0])), 4),
-            "kernel_ms_max": round(float(np.max(ph[:, 0])), 4),
-            "select_ms_mean": round(float(np.mean(ph[:, 1])), 4),
+            "launches_per_step": batches,
+            "ops_per_launch": ops_launch,
+            "algorithmic_hbm_bytes_per_launch": round(algo_bytes),
+            "launch_ms_mean": round(float(np.mean(ph[:, 0])) / batches, 4),
+            "kernel_ms_per_step_mean": round(float(np.mean(ph[:, 0])), 4),
+            "kernel_ms_per_step_min": round(float(np.min(ph[:, 0])), 4),
+            "kernel_ms_per_step_max": round(float(np.max(ph[:, 0])), 4),
+            "select_ms_per_step_mean": round(float(np.mean(ph[:, 1])), 4),
             "chain_replay_ms_mean": round(float(np.mean(ph[:, 2])), 4),
             "exact_rerun_ms_mean": round(float(np.mean(ph[:, 3])), 4),
             "operator_ms_median": round(float(np.median(launch_ms)), 4),

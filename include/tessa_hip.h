@@ -180,7 +180,8 @@ tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf
  * the same split as persistent_kernel_event_ms / leaf DCO clocks in
  * GpuSubtreeTopKProfile, compute_backend.rs:2198-2247).  Synchronises on the
  * last event; phase_ms[0..3] = MFMA filter kernel and select kernel (summed
- * over the call's batches of work items), chain replay, exact re-run. */
+ * over the call's batches of work items), chain replay, exact re-run;
+ * phase_ms[4] = the number of batches (launches of each of the first two). */
 tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_leaf_batch *leaves,
                                       uint32_t *out_ids, float *out_dists,
                                       uint64_t *counters, void *stream, float *phase_ms);

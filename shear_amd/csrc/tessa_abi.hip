@@ -422,7 +422,7 @@ tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_lea
                                       float *out_dists, uint64_t *counters, void *stream, float *phase_ms) {
     if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
     if (!phase_ms) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "phase_ms is null");
-    for (int i = 0; i < 4; ++i) phase_ms[i] = 0.0f;
+    for (int i = 0; i < 5; ++i) phase_ms[i] = 0.0f;
     PhaseEvents *ev = nullptr;
     tessa_status st = phase_events(&ev);
     if (st.code) return st;
@@ -442,6 +442,7 @@ tessa_status tessa_leaf_topk_profiled(const tessa_sq8_view *sq8, const tessa_lea
     }
     phase_ms[2] = span(3 * nb - 1, 3 * nb);
     phase_ms[3] = span(3 * nb, 3 * nb + 1);
+    phase_ms[4] = (float)nb;
     return ok_status();
 }
 

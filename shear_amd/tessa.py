@@ -179,11 +179,11 @@ def leaf_topk(sq8: Sq8Matrix, global_ids: torch.Tensor, layouts: LeafLayouts, k:
         N.check(N.load().tessa_leaf_topk(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                          _ptr(counters), _stream_ptr(stream)), "tessa_leaf_topk")
     else:
-        ph = (C.c_float * 4)()
+        ph = (C.c_float * 5)()
         N.check(N.load().tessa_leaf_topk_profiled(C.byref(view), C.byref(lb), _ptr(out_ids), _ptr(out_dists),
                                                   _ptr(counters), _stream_ptr(stream), ph),
                 "tessa_leaf_topk_profiled")
-        phase_ms.append([float(ph[i]) for i in range(4)])
+        phase_ms.append([float(ph[i]) for i in range(5)])
     return out_ids, out_dists, counters
 
 
