@@ -432,6 +432,62 @@ typedef struct tessa_subtree_output {
 tessa_status tessa_session_run_subtree(tessa_session *session, const tessa_subtree_request *req,
                                        tessa_subtree_output *out);
 
+/* ---- many subtree roots in one partition run ------------------------------
+ * Replaces the build's loop over D1+ children, one
+ * process_quantized_subtree_l2_compact_topk call each (the loop
+ * rbc_partition.rs:10261-10352 run_gpu_subtree_d1plus_producer_with_context,
+ * the call at :15076-15087): every root's rows are partitioned
+ * in one level-synchronous run, all roots' nodes of a level together, with no
+ * upload of the roots' SQ8 rows (they are read in place from `sq8`, device
+ * arrays, through `rows`).  Root i owns rows[root_offsets[i] ..
+ * root_offsets[i+1]) (SQ8 row ids, ascending within a root) and starts from
+ * root_seeds[i] at depth root_depth; its leaves are exactly those a
+ * tessa_session_run_subtree call over that root's rows alone (uploaded in
+ * that order, same seed and parameters) would publish, with member rows given
+ * as SQ8 row ids.  Leaves of different roots interleave in the output.  Every
+ * root must be a large node: at least 2 rows and more than leaf_max rows or
+ * more than small_node_limit / fanout_second (smaller roots go through
+ * tessa_session_run_subtree).  Leaf outputs (device): leaf_rows
+ * [max_leaf_rows] SQ8 row ids, leaf_starts [max_leaf_count], leaf_sizes
+ * [max_leaf_count] (u32, ready as a tessa_leaf_batch's member_counts).
+ * Overflow is reported as by tessa_session_run_subtree; no leaf top-k runs. */
+typedef struct tessa_roots_request {
+    const uint32_t *rows;          /* device: the roots' SQ8 row ids, concatenated */
+    const uint64_t *root_offsets;  /* host: root_count + 1 */
+    const uint64_t *root_seeds;    /* host: root_count */
+    uint32_t root_count;
+    uint32_t root_depth;
+    uint32_t fanout_second;
+    uint32_t max_depth;
+    uint32_t max_leaders;
+    uint32_t leaf_min;
+    uint32_t leaf_max;
+    uint32_t small_node_limit;
+    float psamp_fraction;
+    uint32_t reserved;
+    uint64_t max_leaf_count;
+    uint64_t max_leaf_rows;
+} tessa_roots_request;
+
+typedef struct tessa_roots_output {
+    uint32_t *leaf_rows;           /* device, max_leaf_rows: SQ8 row ids */
+    uint64_t *leaf_starts;         /* device, max_leaf_count */
+    uint32_t *leaf_sizes;          /* device, max_leaf_count */
+    uint32_t *leaf_roots;          /* device, max_leaf_count, may be NULL: each leaf's root index */
+    uint32_t *leaf_depths;         /* device, max_leaf_count, may be NULL: each leaf's depth (a
+                                      root's leaves are one level below the deepest node split;
+                                      a run with max_depth M fails for a root iff one of its
+                                      leaves is deeper than M) */
+    uint64_t *counters;            /* host, TESSA_SUBTREE_COUNTER_WORDS, may be NULL */
+    uint64_t leaf_count;           /* out */
+    uint64_t leaf_rows_total;      /* out */
+    uint32_t levels;               /* out */
+    float partition_ms;            /* out */
+} tessa_roots_output;
+
+tessa_status tessa_session_partition_roots(tessa_session *session, const tessa_sq8_view *sq8,
+                                           const tessa_roots_request *req, tessa_roots_output *out);
+
 /* ---- candidate records -> HashPrune edge records ------------------------
  * Replaces the host conversion flush_compact_topk_batch_into_edges
  * (leaf_build.rs:1679-1829) that SHEAR runs on every CompactTopKBatch the

@@ -200,6 +200,20 @@ class SubtreeOutput(C.Structure):
     ]
 
 
+class RootsRequest(C.Structure):
+    _fields_ = [("rows", C.c_void_p), ("root_offsets", C.c_void_p), ("root_seeds", C.c_void_p),
+                ("root_count", C.c_uint32), ("root_depth", C.c_uint32), ("fanout_second", C.c_uint32),
+                ("max_depth", C.c_uint32), ("max_leaders", C.c_uint32), ("leaf_min", C.c_uint32),
+                ("leaf_max", C.c_uint32), ("small_node_limit", C.c_uint32), ("psamp_fraction", C.c_float),
+                ("reserved", C.c_uint32), ("max_leaf_count", C.c_uint64), ("max_leaf_rows", C.c_uint64)]
+
+
+class RootsOutput(C.Structure):
+    _fields_ = [("leaf_rows", C.c_void_p), ("leaf_starts", C.c_void_p), ("leaf_sizes", C.c_void_p),
+                ("leaf_roots", C.c_void_p), ("leaf_depths", C.c_void_p), ("counters", C.c_void_p), ("leaf_count", C.c_uint64), ("leaf_rows_total", C.c_uint64),
+                ("levels", C.c_uint32), ("partition_ms", C.c_float)]
+
+
 class SubtreeHostResult(C.Structure):
     _fields_ = [
         ("leaf_row_ids", C.c_void_p),
@@ -316,6 +330,10 @@ SIGNATURES = {
     "tessa_session_run_subtree": (
         TessaStatus,
         [_P, C.POINTER(SubtreeRequest), C.POINTER(SubtreeOutput)],
+    ),
+    "tessa_session_partition_roots": (
+        TessaStatus,
+        [_P, C.POINTER(Sq8View), C.POINTER(RootsRequest), C.POINTER(RootsOutput)],
     ),
     "tessa_session_submit_subtree": (
         TessaStatus,

@@ -44,6 +44,9 @@ struct NodeDesc {
     uint64_t leaf_row_base;  // absolute offset of its first leaf row
     uint64_t node_base;      // index of its first child in the next level
     uint64_t node_row_base;  // offset of that child's rows in the next arena
+    uint64_t root_base;      // resident index of its root's first row (0 for a single root)
+    uint32_t root_index;     // its root (0 for a single root)
+    uint32_t pad;
 };
 
 // Level summary, copied to the host after each level.
@@ -59,12 +62,21 @@ struct LevelHeader {
 };
 
 struct PartArgs {
-    // resident SQ8 rows (local ids 0..rows-1)
+    // resident rows 0..rows-1; row r's SQ8 row is row_map[r] (r when row_map is null)
     const int8_t *codes;
     const float *scales;
     const float *norms;
+    const uint32_t *row_map;
     uint32_t rows;
     uint32_t padded_dim;
+    // several roots in one run (root_count > 0): root i owns resident rows
+    // [root_offsets[i], root_offsets[i+1]) and starts from root_seeds[i];
+    // each root's rows are partitioned exactly as a single-root run over
+    // those rows alone would partition them (assignment tie keys use the
+    // row's index within its root)
+    const uint64_t *root_offsets;  // device
+    const uint64_t *root_seeds;    // device
+    uint32_t root_count;
     // request
     const uint32_t *root_leaders;  // device, may be null
     uint32_t root_leader_count;
@@ -87,6 +99,8 @@ struct PartArgs {
     uint64_t *leaf_sizes;
     uint32_t *leaf_sizes32;
     uint64_t *leaf_out_offsets;
+    uint32_t *leaf_root;   // optional: each leaf's root index
+    uint32_t *leaf_depth;  // optional: each leaf's depth
     uint64_t *counters;  // TESSA_SUBTREE_COUNTER_WORDS, reference layout
     LevelHeader *hdr;
     // workspace

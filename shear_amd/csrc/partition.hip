@@ -175,6 +175,23 @@ __global__ void root_kernel(PartArgs a) {
     }
 }
 
+// Several roots: resident rows 0..rows-1 in the first arena, node i = root i.
+__global__ void multi_root_kernel(PartArgs a) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.rows) a.arena[0][i] = (uint32_t)i;
+    if (i < a.root_count) {
+        NodeDesc nd{};
+        nd.row_start = a.root_offsets[i];
+        nd.root_base = a.root_offsets[i];
+        nd.root_index = (uint32_t)i;
+        nd.seed = a.root_seeds[i];
+        nd.n = (uint32_t)(a.root_offsets[i + 1] - a.root_offsets[i]);
+        nd.depth = a.root_depth;
+        nd.status = kNodeIdle;
+        a.nodes[0][i] = nd;
+    }
+}
+
 __global__ void reset_retry_kernel(LevelHeader *h) { h->retry_nodes = 0u; }
 
 // ---- stage (compute_backend.rs:12456-12646) ---------------------------------
@@ -325,25 +342,29 @@ __global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uin
     const uint32_t *node_leaders = a.leaders + (uint64_t)ni * kPartMaxLeaders;
     const uint32_t tid = threadIdx.x;
 
+    // resident row -> SQ8 row; tie keys use the row's index within its root
+    const uint32_t *rmap = a.row_map;
+    const uint32_t rb = (uint32_t)nd->root_base;
     for (uint32_t q = tid; q < (uint32_t)kPartMaxLeaders * KS * 2; q += kCountThreads) {
         const uint32_t li = q / (KS * 2);
         const uint32_t off = (q % (KS * 2)) * 16u;
         v4i z = {0, 0, 0, 0};
         if (li < nl && off < pd) {
             const uint32_t g = node_leaders[li];
-            if (g < a.rows) z = *reinterpret_cast<const v4i *>(a.codes + (uint64_t)g * pd + off);
+            if (g < a.rows) z = *reinterpret_cast<const v4i *>(a.codes + (uint64_t)(rmap ? rmap[g] : g) * pd + off);
         }
         *reinterpret_cast<v4i *>(lcodes + li * L::kStride + off) = z;
     }
     for (uint32_t li = tid; li < (uint32_t)kPartMaxLeaders; li += kCountThreads) {
-        uint32_t g = li < nl ? node_leaders[li] : 0u;
+        uint32_t g = li < nl ? node_leaders[li] : rb;
         if (li < nl && g >= a.rows) {
             pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_LEADER_ID);
-            g = 0u;
+            g = rb;
         }
-        ls[li] = li < nl ? a.scales[g] : 0.0f;
-        ln[li] = li < nl ? a.norms[g] : 0.0f;
-        lid[li] = g;
+        const uint32_t sg = rmap ? rmap[g] : g;
+        ls[li] = li < nl ? a.scales[sg] : 0.0f;
+        ln[li] = li < nl ? a.norms[sg] : 0.0f;
+        lid[li] = g - rb;
         cnt[li] = 0u;
     }
     __syncthreads();
@@ -359,14 +380,15 @@ __global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uin
         if (first + ch * kCountChunk >= n) break;  // uniform across the block
         const uint32_t m = first + ch * kCountChunk + wave * 32u + j;
         bool ok = m < n;
-        uint32_t pt = ok ? arena[row_start + m] : 0u;
+        uint32_t pt = ok ? arena[row_start + m] : rb;
         if (ok && pt >= a.rows) {
             pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_POINT_ID);
             ok = false;
-            pt = 0u;
+            pt = rb;
         }
+        const uint32_t spt = rmap ? rmap[pt] : pt;
         v4i bfrag[KS];
-        const int8_t *mc = a.codes + (uint64_t)pt * pd;
+        const int8_t *mc = a.codes + (uint64_t)spt * pd;
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             const uint32_t off = 32u * s + 16u * h;
@@ -374,8 +396,9 @@ __global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uin
             if (ok && off < pd) z = *reinterpret_cast<const v4i *>(mc + off);
             bfrag[s] = z;
         }
-        const float ps = ok ? a.scales[pt] : 0.0f;
-        const float pn = ok ? a.norms[pt] : 0.0f;
+        const float ps = ok ? a.scales[spt] : 0.0f;
+        const float pn = ok ? a.norms[spt] : 0.0f;
+        const uint32_t lpt = pt - rb;  // the row's index within its root
         // compute_backend.rs:6357-6368 reset: (FLT_MAX, empty)
         float bd[4] = {kEmptyDist, kEmptyDist, kEmptyDist, kEmptyDist};
         uint32_t bs[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
@@ -402,7 +425,7 @@ __global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uin
                     constexpr int F = decltype(fc)::value;
                     for (uint32_t li = 0; li < lim; ++li) {
                         const uint32_t slot = 32u * t + li;
-                        insert_slot<F>(wb[li * 33 + j], pt, lid[slot], slot, bd, bs, bl);
+                        insert_slot<F>(wb[li * 33 + j], lpt, lid[slot], slot, bd, bs, bl);
                     }
                 };
                 switch (fanout) {
@@ -788,6 +811,8 @@ __global__ __launch_bounds__(256) void scatter_kernel(PartArgs a, uint32_t cur, 
                 child.n = c;
                 child.depth = nd->depth + 1u;
                 child.seed = nd->seed ^ ((uint64_t)s * 0x94d049bb133111ebull) ^ (((uint64_t)c) << 23);
+                child.root_base = nd->root_base;
+                child.root_index = nd->root_index;
                 child.status = kNodeIdle;
                 a.nodes[cur ^ 1u][nd->node_base + (ci & ~kChildNodeBit)] = child;
             } else {
@@ -797,6 +822,8 @@ __global__ __launch_bounds__(256) void scatter_kernel(PartArgs a, uint32_t cur, 
                 a.leaf_sizes[li] = c;
                 a.leaf_sizes32[li] = c;
                 a.leaf_out_offsets[li] = start * a.k;
+                if (a.leaf_root) a.leaf_root[li] = nd->root_index;
+                if (a.leaf_depth) a.leaf_depth[li] = nd->depth + 1u;
                 pc_min(a.counters, TESSA_P_LEAF_SIZE_MIN, c);
                 pc_max(a.counters, TESSA_P_LEAF_SIZE_MAX, c);
                 pc_add(a.counters, TESSA_P_LEAF_SIZE_SUM, c);
@@ -1159,6 +1186,12 @@ static int capture_level(const PartArgs &a, hipStream_t s, uint32_t cur, uint32_
     return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
 }
 
+// Level bound: the terminal-depth retry runs with max_depth up to 1024, so a
+// tree may be that deep.
+constexpr uint32_t kMaxLevels = 1100u;
+static int run_levels(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
+                      uint32_t level_nodes, uint64_t level_rows);
+
 int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture) {
     *res = PartResult{};
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(256), 0, s, a);
@@ -1168,6 +1201,18 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
         return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
     };
     if (a.rows == 0) return read_header();
+    uint32_t level_nodes = 1;
+    const uint64_t level_rows = a.rows;
+    if (a.root_count > 0) {
+        // every root is a large node (more than leaf_max rows, or a fanout
+        // probe beyond the small-node scratch); the caller checked it
+        if ((uint64_t)a.rows > a.arena_cap || a.root_count > a.node_cap) return -3;
+        const uint64_t n = (uint64_t)a.rows > a.root_count ? a.rows : a.root_count;
+        hipLaunchKernelGGL(multi_root_kernel, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, s, a);
+        if (hipGetLastError() != hipSuccess) return -1;
+        level_nodes = a.root_count;
+        return run_levels(a, s, hh, res, capture, level_nodes, level_rows);
+    }
     const bool probe = a.fanout_second > 1u && a.rows > 1u;
     const bool probe_overflow = probe && (uint64_t)a.rows * a.fanout_second > (uint64_t)a.small_node_limit;
     if (a.rows <= a.leaf_max && !probe_overflow) {
@@ -1189,9 +1234,18 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
     if ((uint64_t)a.rows > a.arena_cap) return -3;
     hipLaunchKernelGGL(root_kernel, dim3((a.rows + 255u) / 256u), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return -1;
-    uint32_t level_nodes = 1, cur = 0;
-    uint64_t level_rows = a.rows;
-    for (uint32_t level = 0; level < 64u; ++level) {
+    return run_levels(a, s, hh, res, capture, level_nodes, level_rows);
+}
+
+// The level loop from the nodes of level 0 (in the first arena).
+static int run_levels(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
+                      uint32_t level_nodes, uint64_t level_rows) {
+    auto read_header = [&]() -> int {
+        if (hipMemcpyAsync(hh, a.hdr, sizeof(LevelHeader), hipMemcpyDeviceToHost, s) != hipSuccess) return -1;
+        return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
+    };
+    uint32_t cur = 0;
+    for (uint32_t level = 0; level < kMaxLevels; ++level) {
         const uint64_t items_bound = level_rows / kPartItemRows + level_nodes + 1u;
         if (items_bound > a.item_cap || items_bound > 0x7fffffffull) return -3;
         const uint32_t grid = (uint32_t)items_bound;

@@ -62,6 +62,25 @@ __global__ void fill_u32_kernel(uint32_t *p, uint32_t n, uint32_t v) {
     if (i < n) p[i] = v;
 }
 
+// out[0] = largest value of a[0, n) (out[0] starts at 0).
+__global__ void max_u32_kernel(const uint32_t *a, uint64_t n, uint32_t *out) {
+    uint32_t m = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        m = a[i] > m ? a[i] : m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = __shfl_xor(m, off);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63u) == 0u) atomicMax(out, m);
+}
+
+// x[i] = map[x[i]] for i < n (resident indices -> SQ8 rows).
+__global__ void map_rows_kernel(uint32_t *x, uint64_t n, const uint32_t *map) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        x[i] = map[x[i]];
+}
+
 // Per-device workspace of the MFMA leaf path: the exact re-run queue (pairs
 // (leaf, row)), the chain queue (headers + candidate pool) and their three
 // counters.  Grown on demand; kept until the process ends (other callers may
@@ -1257,6 +1276,180 @@ tessa_status tessa_session_run_subtree(tessa_session *s, const tessa_subtree_req
     if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
     std::lock_guard<std::mutex> lock(s->exec_mu);
     return tessa_session_run_subtree_locked(s, rq, out);
+}
+
+static tessa_status tessa_session_partition_roots_locked(tessa_session *s, const tessa_sq8_view *sq8,
+                                                         const tessa_roots_request *rq, tessa_roots_output *out) {
+    if (!sq8 || !rq || !out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: null argument");
+    out->leaf_count = out->leaf_rows_total = 0;
+    out->levels = 0;
+    out->partition_ms = 0.0f;
+    if (!sq8->codes || !sq8->scales || !sq8->norms || sq8->rows == 0 || sq8->rows > 0xffffffffull)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: SQ8 view needs device codes, scales and "
+                                                          "norms of 1..2^32-1 rows");
+    if (sq8->padded_dim == 0 || sq8->padded_dim % 16 != 0 || sq8->padded_dim > 1024)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "partition roots: padded_dim %u (multiple of 16, <= 1024)",
+                           sq8->padded_dim);
+    if (!rq->rows || !rq->root_offsets || !rq->root_seeds || rq->root_count == 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: rows, offsets and seeds of >= 1 root");
+    if (rq->fanout_second == 0 || rq->fanout_second > 4)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, TESSA_OVF_FANOUT_OVER_32,
+                           "CUDA persistent strict error: unsupported subtree fanout_second=%u (1..4) "
+                           "fallback_reason_flags=0x%x",
+                           rq->fanout_second, TESSA_PLAN_FALLBACK_UNSUPPORTED_FANOUT);
+    if (rq->max_leaders == 0 || rq->leaf_min == 0 || rq->leaf_max == 0 || rq->small_node_limit == 0 ||
+        rq->small_node_limit > kSmallNodeLimit)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "partition roots needs max_leaders, leaf_min, leaf_max >= 1 and "
+                           "small_node_limit in [1, 4096]");
+    if (!out->leaf_rows || !out->leaf_starts || !out->leaf_sizes || rq->max_leaf_count == 0 || rq->max_leaf_rows == 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: null output or zero capacity");
+    if (rq->root_offsets[0] != 0)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: root_offsets[0] must be 0");
+    for (uint32_t i = 0; i < rq->root_count; ++i) {
+        const uint64_t a = rq->root_offsets[i], b = rq->root_offsets[i + 1];
+        if (b < a + 2)
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "partition roots: root %u has %lld rows (>= 2 needed)", i,
+                               (long long)(b - a));
+        const uint64_t n = b - a;
+        const bool large = n > rq->leaf_max ||
+                           (rq->fanout_second > 1 && n * rq->fanout_second > (uint64_t)rq->small_node_limit);
+        if (!large)
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                               "partition roots: root %u of %llu rows is a small root (run it with "
+                               "tessa_session_run_subtree)",
+                               i, (unsigned long long)n);
+    }
+    const uint64_t rows = rq->root_offsets[rq->root_count];
+    const uint32_t famp = rq->fanout_second;
+    if (rows * famp > 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "partition roots: rows x fanout must stay below 2^32");
+    TESSA_HIP_TRY(hipSetDevice(s->device));
+
+    // workspace: the partition arrays, then the roots' offsets and seeds,
+    // 64-bit leaf sizes and one check word
+    const PartLayout L = part_layout(rows, famp, rq->leaf_max, rq->max_leaf_count);
+    const size_t off_roff = align256(L.bytes), off_seed = off_roff + align256((rq->root_count + 1ull) * 8),
+                 off_sz64 = off_seed + align256(rq->root_count * 8ull),
+                 off_chk = off_sz64 + align256(rq->max_leaf_count * 8ull), need = off_chk + 256;
+    if (s->part_bytes < need) {
+        TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+        if (s->part) (void)hipFree(s->part);
+        s->part = nullptr;
+        s->part_bytes = 0;
+        if (hipMalloc(&s->part, need) != hipSuccess)
+            return make_status(TESSA_ERR_OUT_OF_MEMORY, TESSA_OVF_WORKSPACE_BUDGET,
+                               "Failed to allocate CUDA GPU persistent subtree workspace (HIP, %zu bytes) "
+                               "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                               need, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+        s->part_bytes = need;
+    }
+    char *base = static_cast<char *>(s->part);
+    uint64_t *d_roff = reinterpret_cast<uint64_t *>(base + off_roff);
+    uint64_t *d_seed = reinterpret_cast<uint64_t *>(base + off_seed);
+    uint32_t *d_chk = reinterpret_cast<uint32_t *>(base + off_chk);
+    TESSA_HIP_TRY(hipMemcpyAsync(d_roff, rq->root_offsets, (rq->root_count + 1ull) * 8, hipMemcpyHostToDevice,
+                                 s->stream));
+    TESSA_HIP_TRY(hipMemcpyAsync(d_seed, rq->root_seeds, rq->root_count * 8ull, hipMemcpyHostToDevice, s->stream));
+    // every row id must be an SQ8 row (the kernels read codes through it)
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s->stream, d_chk, 1u, 0u);
+    hipLaunchKernelGGL(max_u32_kernel, dim3(1024), dim3(256), 0, s->stream, rq->rows, rows, d_chk);
+    uint32_t max_row = 0;
+    TESSA_HIP_TRY(hipMemcpyAsync(&max_row, d_chk, 4, hipMemcpyDeviceToHost, s->stream));
+    TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+    if (max_row >= sq8->rows)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, TESSA_OVF_INVALID_ASSIGN_POINT_ID,
+                           "partition roots: row id %u outside the %llu SQ8 rows overflow_flags=0x%llx "
+                           "overflow_labels=INVALID_ASSIGN_POINT_ID",
+                           max_row, (unsigned long long)sq8->rows, (unsigned long long)TESSA_OVF_INVALID_ASSIGN_POINT_ID);
+
+    PartArgs a{};
+    a.codes = sq8->codes;
+    a.scales = sq8->scales;
+    a.norms = sq8->norms;
+    a.row_map = rq->rows;
+    a.rows = (uint32_t)rows;
+    a.padded_dim = sq8->padded_dim;
+    a.root_offsets = d_roff;
+    a.root_seeds = d_seed;
+    a.root_count = rq->root_count;
+    a.root_leaders = nullptr;
+    a.root_leader_count = 0;
+    a.root_depth = rq->root_depth;
+    a.max_depth = rq->max_depth;
+    a.max_leaders = rq->max_leaders;
+    a.fanout_second = rq->fanout_second;
+    a.leaf_min = rq->leaf_min;
+    a.leaf_max = rq->leaf_max;
+    a.small_node_limit = rq->small_node_limit;
+    a.k = 0;
+    a.psamp = rq->psamp_fraction;
+    a.seed = 0;
+    a.large_scratch_rows = rows * famp;
+    a.max_leaf_count = rq->max_leaf_count;
+    a.max_leaf_rows = rq->max_leaf_rows;
+    a.leaf_row_ids = out->leaf_rows;
+    a.leaf_starts = out->leaf_starts;
+    a.leaf_sizes = reinterpret_cast<uint64_t *>(base + off_sz64);
+    a.leaf_sizes32 = out->leaf_sizes;
+    a.leaf_out_offsets = reinterpret_cast<uint64_t *>(base + L.off_outoff);
+    a.leaf_root = out->leaf_roots;
+    a.leaf_depth = out->leaf_depths;
+    a.counters = s->part_counters;
+    a.hdr = s->part_hdr;
+    for (int i = 0; i < 2; ++i) {
+        a.arena[i] = reinterpret_cast<uint32_t *>(base + L.off_arena[i]);
+        a.nodes[i] = reinterpret_cast<NodeDesc *>(base + L.off_nodes[i]);
+    }
+    a.leaders = reinterpret_cast<uint32_t *>(base + L.off_leaders);
+    a.child_counts = reinterpret_cast<uint32_t *>(base + L.off_ccount);
+    a.child_idx = reinterpret_cast<uint32_t *>(base + L.off_cidx);
+    a.child_rel = reinterpret_cast<uint32_t *>(base + L.off_crel);
+    a.slots = reinterpret_cast<uint32_t *>(base + L.off_slots);
+    a.item_counts = reinterpret_cast<uint32_t *>(base + L.off_items);
+    a.arena_cap = L.arena_cap;
+    a.item_cap = L.item_cap;
+    a.node_cap = L.node_cap;
+
+    TESSA_HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    PartResult pr{};
+    const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr, nullptr);
+    if (rc != 0)
+        return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
+                           rc == -2 ? "level/attempt bound exceeded"
+                                    : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+    uint64_t c[TESSA_SUBTREE_COUNTER_WORDS];
+    TESSA_HIP_TRY(hipMemcpyAsync(c, s->part_counters, sizeof(c), hipMemcpyDeviceToHost, s->stream));
+    TESSA_HIP_TRY(hipStreamSynchronize(s->stream));
+    if (out->counters) std::memcpy(out->counters, c, sizeof(c));
+    out->levels = pr.levels;
+    out->leaf_count = pr.leaf_count;
+    out->leaf_rows_total = pr.leaf_rows;
+    if (c[TESSA_P_OVERFLOW_FLAGS] != 0) {
+        TESSA_HIP_TRY(hipEventRecord(s->ev1, s->stream));
+        TESSA_HIP_TRY(hipEventSynchronize(s->ev1));
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, s->ev0, s->ev1);
+        out->partition_ms = ms;
+        return subtree_overflow(s, c, ms);
+    }
+    // leaf members: resident indices -> SQ8 row ids
+    if (pr.leaf_rows)
+        hipLaunchKernelGGL(map_rows_kernel, dim3((uint32_t)std::min<uint64_t>((pr.leaf_rows + 255) / 256, 8192)),
+                           dim3(256), 0, s->stream, out->leaf_rows, pr.leaf_rows, rq->rows);
+    TESSA_HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    TESSA_HIP_TRY(hipEventSynchronize(s->ev1));
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, s->ev0, s->ev1);
+    out->partition_ms = ms;
+    return ok_status();
+}
+
+tessa_status tessa_session_partition_roots(tessa_session *s, const tessa_sq8_view *sq8, const tessa_roots_request *rq,
+                                           tessa_roots_output *out) {
+    if (!s) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "session is null");
+    std::lock_guard<std::mutex> lock(s->exec_mu);
+    return tessa_session_partition_roots_locked(s, sq8, rq, out);
 }
 
 }  // extern "C"

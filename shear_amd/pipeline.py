@@ -45,6 +45,7 @@ from . import tierlift as TL
 OVF_OVERSIZED_TERMINAL_NODE = 1 << 10
 TERMINAL_DEPTH_RECOVERY_FLOOR = 1024
 TERMINAL_DEPTH_RETRY_LIMIT = 1
+SMALL_NODE_LIMIT = 4096  # the plan's small-node scratch rows (compute_backend.rs:1341)
 
 
 @dataclass
@@ -60,7 +61,11 @@ class GraphBuildParams:
     max_depth: int = 16
     random_seed: int = 42
     min_recurse_size: int = 64
-    insert_every: int = 16     # D0 children per HashPrune batch (the reservoirs do not depend on batching)
+    insert_every: int = 16     # record batches per HashPrune insert (the reservoirs do not depend on batching)
+    insert_records: int = 1 << 28  # ... or as soon as this many records are pending
+    multi_root: bool = True    # large D0 children partitioned together (tessa_session_partition_roots)
+    roots_rows_per_run: int = 1 << 26  # rows of the children partitioned by one many-root run
+    leaf_chunk_rows: int = 1 << 22     # leaf rows per leaf top-k / record batch of a many-root run
     gpu_workspace_budget_bytes: int = 0  # per subtree task (0: the default 512 MiB plan, tasks unchecked)
 
     def subtree_params(self) -> S.PiPNNSubtreeParams:
@@ -187,16 +192,29 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
                     p: GraphBuildParams = GraphBuildParams(), observer=None,
                     t0: float | None = None, host_reducer: TL.TierLiftParams | None = None) -> BuiltGraph:
     """The build from an SQ8 payload already in device memory (build time
-    counted from ``t0``, a perf_counter value, when given).  ``observer``
-    (optional) is called once per D0 child after its records are emitted, as
-    observer(child, global_ids, output, layouts, records, record_count), for
-    checks and statistics; it must not keep device tensors alive.
+    counted from ``t0``, a perf_counter value, when given).
+
+    D0 children of two or more points are the subtree tasks.  With
+    ``p.multi_root`` (the default) every large child (more than leaf_max rows,
+    or a fanout probe beyond the small-node scratch) is partitioned in one
+    many-root run per group of about ``p.roots_rows_per_run`` rows, reading
+    the SQ8 rows in place; the leaves of a group then go through the leaf
+    top-k and record emission in chunks of at most ``p.leaf_chunk_rows`` leaf
+    rows.  The remaining small children run one by one.  Each child's leaves
+    are those of its own run, so the graph is the same either way.
+
+    ``observer`` (optional) is called after each batch of records is emitted,
+    as observer(tag, global_ids, output, layouts, records, record_count):
+    ``output`` has leaf_row_ids / leaf_starts / leaf_sizes / leaf_count /
+    leaf_rows / k / topk_ids / topk_dists of the batch (starts relative to its
+    leaf_row_ids) and ``global_ids`` maps its rows to point ids (None: the
+    rows are point ids); it must not keep device tensors alive.
 
     ``host_reducer`` routes the records through the TierLift host reducer
     (bounded host memory, spill files past the budget) instead of device
-    reservoirs: each child's records are queued for copy as soon as they are
-    emitted, and the copies overlap the next children's partition and leaf
-    work.  Both reducers give the same table."""
+    reservoirs: each batch of records is queued for copy as soon as it is
+    emitted, and the copies overlap the next batches' work.  Both reducers
+    give the same table."""
     dev = sq8.codes.device
     rows = sq8.rows
     gids = torch.arange(rows, dtype=torch.int32, device=dev)
@@ -219,17 +237,45 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         tl = TL.TierLiftReducer(rows, p.l_max, host_reducer, dev)
     else:
         hp = H.HashPruneReducer(rows, p.l_max, dev)
-    push_s = 0.0
-    depth_retries = 0
+    st = {"push_s": 0.0, "part_ms": 0.0, "leaf_ms": 0.0, "records": 0, "leaves": 0, "leaf_rows": 0,
+          "retries": 0, "runs": 0}
     sp = p.subtree_params()
     leaf_max = max(256, p.c_max)
-    part_ms = leaf_ms = 0.0
-    records = leaves = leaf_rows = 0
+    famp = max(p.fanout_second, 1)
     pending = []
-    for c in range(len(offs_h) - 1):
+
+    def consume(rec, cnt):
+        nonlocal pending
+        if tl is not None:
+            q0 = time.perf_counter()
+            tl.push(rec, int(cnt))
+            st["push_s"] += time.perf_counter() - q0
+            return
+        pending.append(rec[:cnt])
+        if sum(int(r.shape[0]) for r in pending) >= p.insert_records or len(pending) >= p.insert_every:
+            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
+            pending = []
+
+    sizes = np.diff(offs_h.astype(np.int64))
+    children = [c for c in range(len(sizes)) if sizes[c] >= 2]  # a one-point child has no leaf pairs
+    if p.multi_root:
+        large = [c for c in children if sizes[c] > leaf_max or (famp > 1 and sizes[c] * famp > SMALL_NODE_LIMIT)]
+    else:
+        large = []
+    large_set = set(large)
+    small = [c for c in children if c not in large_set]
+
+    # many-root runs over groups of large children
+    group = []
+    for gi, c in enumerate(large):
+        group.append(c)
+        if gi + 1 == len(large) or sum(int(sizes[g]) for g in group) + int(sizes[large[gi + 1]]) > p.roots_rows_per_run:
+            _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, rows, sketches, p, sp, st, consume, observer)
+            group = []
+
+    # small children one by one
+    for c in small:
         a, b = int(offs_h[c]), int(offs_h[c + 1])
-        if b - a < 2:
-            continue  # a one-point child has no leaf pairs
         cg = pts[a:b]
         ci = cg.long()
         sub = T.Sq8Matrix(sq8.codes[ci], sq8.scales[ci], sq8.norms[ci], sq8.dim)
@@ -239,28 +285,20 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
                                            min_recurse_size=p.min_recurse_size,
                                            memory_budget_bytes=p.gpu_workspace_budget_bytes or None)
         out = run_child(sess, req, sp)
-        if out.retried:
-            depth_retries += 1
-        part_ms += out.partition_ms
-        leaf_ms += out.leaf_ms
+        st["retries"] += 1 if out.retried else 0
+        st["part_ms"] += out.partition_ms
+        st["leaf_ms"] += out.leaf_ms
+        st["runs"] += 1
         lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
                             out.leaf_sizes[: out.leaf_count].to(torch.int32),
                             out.leaf_starts[: out.leaf_count] * out.k, leaf_max, out.leaf_rows * out.k)
         rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, p.m_hash_bits)
         if observer is not None:
-            observer(c, cg, out, lay, rec, cnt)
-        if tl is not None:
-            q0 = time.perf_counter()
-            tl.push(rec, int(cnt))
-            push_s += time.perf_counter() - q0
-        else:
-            pending.append(rec[:cnt])
-        if len(pending) >= p.insert_every:
-            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
-            pending = []
-        records += int(cnt)
-        leaves += out.leaf_count
-        leaf_rows += out.leaf_rows
+            observer(("child", c), cg, out, lay, rec, cnt)
+        consume(rec, cnt)
+        st["records"] += int(cnt)
+        st["leaves"] += out.leaf_count
+        st["leaf_rows"] += out.leaf_rows
         del rec, out, lay
     if pending:
         hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
@@ -269,7 +307,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         torch.cuda.synchronize()
         w_emit = time.perf_counter()
         targets, counts = tl.finish()
-        tl_stats = dict(tl.stats, push_blocked_s=round(push_s, 3), emit_done_s=round(w_emit - w1, 3))
+        tl_stats = dict(tl.stats, push_blocked_s=round(st["push_s"], 3), emit_done_s=round(w_emit - w1, 3))
         tl.close()
     else:
         targets, counts = hp.neighbors()
@@ -281,17 +319,90 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     w2 = time.perf_counter()
     stages = {"quantize_d0_ms": round((w1 - w0) * 1e3, 2), "d0_leaders": int(len(leader_rows)),
               "d0_fanout_top": p.fanout_top, "subtree_fanout_second": p.fanout_second,
-              "children": int(np.count_nonzero(np.diff(offs_h) >= 2)),
-              "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(part_ms, 2),
-              "leaf_ms": round(leaf_ms, 2), "leaves": leaves, "leaf_rows": leaf_rows, "edge_records": records,
-              "terminal_depth_retries": depth_retries}
+              "children": len(children), "multi_root_children": len(large), "partition_runs": st["runs"],
+              "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(st["part_ms"], 2),
+              "leaf_ms": round(st["leaf_ms"], 2), "leaves": st["leaves"], "leaf_rows": st["leaf_rows"],
+              "edge_records": st["records"], "terminal_depth_retries": st["retries"]}
     if tl is not None:
         stages["tierlift"] = tl_stats
     if p.gpu_workspace_budget_bytes:
         # the largest task's workspace under the cap (a task above it fails its run)
-        big = int(np.diff(offs_h).max())
+        big = int(sizes.max())
         plan = S.plan_subtree(big, p.leaf_knn, min(p.max_leaders, D.GPU_QUEUE_LEADER_STRIDE), p.fanout_second,
                               p.gpu_workspace_budget_bytes, p.c_max)
         stages["largest_task_rows"] = big
         stages["largest_task_workspace_bytes"] = int(plan.required_bytes)
     return BuiltGraph(targets, counts, start, image, w2 - w0, stages)
+
+
+@dataclass
+class LeafChunk:
+    """A batch of leaves of a many-root run as the observer sees it (the
+    fields of a subtree run's output it reads)."""
+
+    leaf_row_ids: torch.Tensor
+    leaf_starts: torch.Tensor
+    leaf_sizes: torch.Tensor
+    leaf_count: int
+    leaf_rows: int
+    k: int
+    topk_ids: torch.Tensor
+    topk_dists: torch.Tensor
+
+
+def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, sketches, p, sp, st, consume,
+                    observer):
+    """One many-root partition over the D0 children in ``group``, then the
+    leaf top-k and record emission of its leaves in chunks."""
+    dev = sq8.codes.device
+    rows_t = torch.cat([pts[int(offs_h[c]):int(offs_h[c + 1])] for c in group])
+    roffs = np.zeros(len(group) + 1, np.uint64)
+    roffs[1:] = np.cumsum([int(sizes[c]) for c in group])
+    seeds = np.array([S.subtree_root_seed(p.random_seed, 1, int(sizes[c]), parent_points, p.min_recurse_size)
+                      for c in group], np.uint64)
+    # the terminal-depth retry (rbc_partition.rs:15066-15115) run up front: a
+    # root's tree under max(max_depth + 1, 1024) equals the first run's tree
+    # when that one succeeds, and is the retry's tree when it fails; a root
+    # would have failed iff one of its leaves lies deeper than max_depth
+    md = max(p.max_depth + 1, TERMINAL_DEPTH_RECOVERY_FLOOR)
+    ro = sess.partition_roots(sq8, rows_t, roffs, seeds, sp, depth=1, max_depth=md,
+                              memory_budget_bytes=p.gpu_workspace_budget_bytes or None)
+    st["runs"] += 1
+    st["part_ms"] += ro.partition_ms
+    lc = ro.leaf_count
+    if lc == 0:
+        return
+    deepest = torch.zeros(len(group), dtype=torch.int32, device=dev)
+    deepest.scatter_reduce_(0, ro.leaf_roots[:lc].long(), ro.leaf_depths[:lc], reduce="amax")
+    st["retries"] += int((deepest > p.max_depth).sum().item())
+    del rows_t, deepest
+    starts = ro.leaf_starts[:lc].cpu().numpy()
+    lsz = ro.leaf_sizes[:lc].cpu().numpy().astype(np.int64)
+    k = p.leaf_knn
+    leaf_max = max(256, p.c_max)
+    ends = starts + lsz
+    l0 = 0
+    while l0 < lc:
+        # leaves [l0, l1) with at most leaf_chunk_rows rows (at least one leaf)
+        l1 = int(np.searchsorted(ends, starts[l0] + p.leaf_chunk_rows, side="right"))
+        l1 = max(l1, l0 + 1)
+        r0, r1 = int(starts[l0]), int(ends[l1 - 1])
+        off = ro.leaf_starts[l0:l1]
+        lay = T.LeafLayouts(ro.leaf_rows, off, ro.leaf_sizes[l0:l1], (off - r0) * k, leaf_max, (r1 - r0) * k)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        ids, d, ctr = T.leaf_topk(sq8, gids, lay, k, executor=sp.executor)
+        e1.record()
+        T.raise_on_overflow(ctr, "leaf top-k")
+        st["leaf_ms"] += e0.elapsed_time(e1)
+        rec, cnt = E.emit_edge_records(gids, lay, k, ids, d, sketches, p.m_hash_bits)
+        if observer is not None:
+            chunk = LeafChunk(ro.leaf_rows[r0:r1], off - r0, ro.leaf_sizes[l0:l1], l1 - l0, r1 - r0, k, ids, d)
+            observer(("roots", st["runs"] - 1, l0), None, chunk, lay, rec, cnt)
+            del chunk
+        consume(rec, cnt)
+        st["records"] += int(cnt)
+        st["leaves"] += l1 - l0
+        st["leaf_rows"] += r1 - r0
+        del rec, ids, d, lay, off
+        l0 = l1

@@ -96,6 +96,22 @@ class SubtreeDeviceOutput:
     leaf_ms: float
 
 
+@dataclass
+class RootsDeviceOutput:
+    """Leaves of a many-root partition (device tensors; member rows are SQ8 row ids)."""
+
+    leaf_rows: torch.Tensor    # int32 view of u32 SQ8 rows, [>= leaf_rows_total]
+    leaf_starts: torch.Tensor  # int64 [>= leaf_count]
+    leaf_sizes: torch.Tensor   # int32 [>= leaf_count]
+    leaf_roots: torch.Tensor   # int32 [>= leaf_count]: root index of each leaf
+    leaf_depths: torch.Tensor  # int32 [>= leaf_count]
+    leaf_count: int
+    leaf_rows_total: int
+    levels: int
+    partition_ms: float
+    counters: np.ndarray
+
+
 class SubtreeSession:
     """One device, one stream, one uploaded resident subtree (the reference's
     CudaComputeBackend with its resident subtree workspace)."""
@@ -234,6 +250,55 @@ class SubtreeSession:
         return SubtreeDeviceOutput(out_rows, out_starts, out_sizes, out_ids, out_d, counters, leaf_counters,
                                    int(out.leaf_count), int(out.leaf_rows), int(out.k), int(out.levels),
                                    float(out.partition_ms), float(out.leaf_ms))
+
+    def partition_roots(self, sq8, rows: torch.Tensor, root_offsets: np.ndarray, root_seeds: np.ndarray,
+                        params: PiPNNSubtreeParams, depth: int = 1, max_depth: int | None = None,
+                        memory_budget_bytes: int | None = None) -> RootsDeviceOutput:
+        """Partition many subtree roots in one run (tessa_session_partition_roots):
+        root i owns the SQ8 rows rows[root_offsets[i]:root_offsets[i+1]]
+        (``rows`` a device int32 view of u32 row ids into ``sq8``, ascending per
+        root) and starts from root_seeds[i] at ``depth``.  Each root is planned
+        as a task of its own (``plan_subtree`` under ``memory_budget_bytes``);
+        every root must be a large one (more than leaf_max rows or a fanout
+        probe beyond the small-node scratch)."""
+        offs = np.ascontiguousarray(root_offsets, np.uint64)
+        seeds = np.ascontiguousarray(root_seeds, np.uint64)
+        famp = max(params.fanout_second, 1)
+        max_leaders = min(max(params.max_leaders, 1), GPU_QUEUE_LEADER_STRIDE)
+        leaf_cap = row_cap = 0
+        first = None
+        for n in np.diff(offs.astype(np.int64)).tolist():
+            plan = plan_subtree(int(n), params.leaf_knn, max_leaders, famp, memory_budget_bytes, params.c_max)
+            if not plan.supported:
+                raise N.TessaError(_status(4, plan.overflow_flags,
+                                           f"CUDA persistent strict error: unsupported subtree "
+                                           f"fallback_reason_flags=0x{plan.fallback_reason_flags:x}"), "plan")
+            key = (plan.leaf_min, plan.leaf_max, plan.small_node_limit)
+            if first is None:
+                first = key
+            elif key != first:
+                raise ValueError(f"roots planned with different leaf bounds {key} != {first}")
+            leaf_cap += int(plan.max_leaf_count)
+            row_cap += int(plan.max_leaf_rows)
+        dev = torch.device("cuda", self.device)
+        out_rows = torch.empty(max(row_cap, 1), dtype=torch.int32, device=dev)
+        out_starts = torch.empty(max(leaf_cap, 1), dtype=torch.int64, device=dev)
+        out_sizes = torch.empty(max(leaf_cap, 1), dtype=torch.int32, device=dev)
+        out_roots = torch.empty(max(leaf_cap, 1), dtype=torch.int32, device=dev)
+        out_depths = torch.empty(max(leaf_cap, 1), dtype=torch.int32, device=dev)
+        counters = np.zeros(N.SUBTREE_COUNTER_WORDS, np.uint64)
+        view = N.Sq8View(sq8.codes.data_ptr(), sq8.scales.data_ptr(), sq8.norms.data_ptr(), None, sq8.rows,
+                         sq8.dim, sq8.padded_dim)
+        rq = N.RootsRequest(rows.data_ptr(), offs.ctypes.data, seeds.ctypes.data, len(seeds), depth, famp,
+                            max_depth if max_depth is not None else params.max_depth, max_leaders, first[0],
+                            first[1], first[2], np.float32(params.psamp_fraction).item(), 0, leaf_cap, row_cap)
+        out = N.RootsOutput(out_rows.data_ptr(), out_starts.data_ptr(), out_sizes.data_ptr(), out_roots.data_ptr(),
+                            out_depths.data_ptr(), counters.ctypes.data, 0, 0, 0, 0.0)
+        torch.cuda.synchronize(dev)  # inputs and outputs come from torch's stream
+        N.check(self._lib.tessa_session_partition_roots(self._h, C.byref(view), C.byref(rq), C.byref(out)),
+                "tessa_session_partition_roots")
+        return RootsDeviceOutput(out_rows, out_starts, out_sizes, out_roots, out_depths, int(out.leaf_count),
+                                 int(out.leaf_rows_total), int(out.levels), float(out.partition_ms), counters)
 
     def process_quantized_subtree_l2_compact_topk(self, request: GpuSubtreePartitionRequest,
                                                   params: PiPNNSubtreeParams) -> GpuSubtreeTopKResult:

@@ -20,7 +20,10 @@ from shear_amd import edges as E
 
 
 class BuildObserver:
-    def __init__(self, rows: int, device, check_children, sample_points: int = 4096, seed: int = 3):
+    """Called by pipeline.build_graph_sq8 once per batch of emitted records;
+    ``check_calls`` are the call indices whose leaves are sampled."""
+
+    def __init__(self, rows: int, device, check_calls=(0, 4, 8), sample_points: int = 4096, seed: int = 3):
         self.covered = torch.zeros(rows, dtype=torch.bool, device=device)
         rng = np.random.default_rng(seed)
         self.sample = torch.from_numpy(np.sort(rng.choice(rows, sample_points, replace=False))).to(device)
@@ -29,26 +32,28 @@ class BuildObserver:
         self.sampled_records = []
         self.leaf_checks = []
         self.max_leaf = 0
-        self.children = 0
-        self.check_children = set(check_children)
+        self.calls = 0
+        self.check_calls = set(check_calls)
 
-    def __call__(self, c, cg, out, lay, rec, cnt):
-        sizes = out.leaf_sizes[: out.leaf_count]
+    def __call__(self, tag, cg, out, lay, rec, cnt):
+        sizes = out.leaf_sizes[: out.leaf_count].long()
         self.max_leaf = max(self.max_leaf, int(sizes.max().item()))
-        self.children += 1
-        if self.children % 100 == 0:
-            print(f"  {self.children} D0 children built", flush=True)
+        call = self.calls
+        self.calls += 1
+        if self.calls % 100 == 0:
+            print(f"  {self.calls} record batches built", flush=True)
         local = out.leaf_row_ids[: out.leaf_rows].long()
-        self.covered[cg.long()[local]] = True
+        self.covered[local if cg is None else cg.long()[local]] = True
         kk = torch.clamp(sizes - 1, max=out.k)
-        assert int(cnt) == int((2 * sizes * kk).sum().item()), f"child {c}: record count"
+        assert int(cnt) == int((2 * sizes * kk).sum().item()), f"{tag}: record count"
         r = rec[:cnt]
         self.sampled_records.append(r[self.in_sample[r[:, 0].long()]].clone())
-        if c in self.check_children:
+        if call in self.check_calls:
             starts = out.leaf_starts[: out.leaf_count].cpu().numpy()
             sz = sizes.cpu().numpy()
-            g = cg.cpu().numpy().view(np.uint32)
             li = out.leaf_row_ids[: out.leaf_rows].cpu().numpy().view(np.uint32)
+            g = li if cg is None else cg.cpu().numpy().view(np.uint32)[li]
+            li = np.arange(len(li))
             ids = out.topk_ids[: out.leaf_rows * out.k].cpu().numpy().view(np.uint32).reshape(-1, out.k)
             dd = out.topk_dists[: out.leaf_rows * out.k].cpu().numpy().reshape(-1, out.k)
             for leaf in np.linspace(0, out.leaf_count - 1, 4).astype(int):

@@ -51,7 +51,7 @@ def test_c4_build_through_tierlift(gpu, orc, tmp_path):
     sq8, sk = P.sq8_from_chunks(chunks(), rows, dim, planes)
     torch.cuda.empty_cache()
     lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
-    obs = BuildObserver(rows, gpu, check_children={0, 500, 990})
+    obs = BuildObserver(rows, gpu)
     base = tmp_path / "candidates.log"
     prm = TL.TierLiftParams(host_budget_bytes=HOST_BUDGET, spill_base=str(base))
     built = P.build_graph_sq8(sq8, sk, lead, p, observer=obs, host_reducer=prm)
