@@ -235,7 +235,8 @@ def main() -> int:
                                                              args.warmup)
         if not args.no_hashprune:
             result["hashprune"] = hashprune_leg(rec, rec_count, gids.numel(), stream, args.steps, args.warmup,
-                                                check=not args.no_cpu_baseline)
+                                                check=not args.no_cpu_baseline, gids=gids, lay=lay,
+                                                out_ids=out_ids, out_d=out_d)
         del rec
         torch.cuda.empty_cache()
 
@@ -272,7 +273,7 @@ def c5_leg(dev, rows, nq=1000, k_recall=10, search_l=(64, 128, 256)):
 
     spec = datagen.c5_spec(rows)
     dim = spec.dim
-    p = P.GraphBuildParams(insert_every=2)
+    p = P.GraphBuildParams()
     planes = torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -600,17 +601,43 @@ def edge_leg(gids, lay, out_ids, out_d, stream, steps, warmup):
     }, rec, count
 
 
-def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_max=64, sample_points=16384):
+def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_max=64, sample_points=16384,
+                  gids=None, lay=None, out_ids=None, out_d=None):
     """HashPrune reservoirs (l_max 64, the reference default) over the step's
-    edge records: empty reservoirs, then one batch of every record.  The
-    points [0, sample_points) are checked bit for bit against the oracle fed
-    with their records."""
+    edge records, empty reservoirs each time: (a) the build's path, the
+    records emitted in source-grouped order with one segment per row
+    (tessa_emit_edge_segments) and merged by segments in place
+    (tessa_hashprune_insert_segments); (b) the reference-order records merged
+    by tessa_hashprune_insert (records grouped by source with atomics).  The
+    points [0, sample_points) of (a) are checked bit for bit against the
+    oracle fed with their records, and (a) must equal (b) everywhere."""
     import torch
 
+    from shear_amd import edges as E
     from shear_amd import hashprune as H
 
-    ms = []
-    with H.HashPruneReducer(num_points, l_max, rec.device) as hp:
+    dev = rec.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    sketches = torch.randn((gids.numel(), 12), generator=gen, device=dev, dtype=torch.float32)
+    grec = torch.empty_like(rec)
+    segs = torch.empty((lay.output_len // K, 4), dtype=torch.int32, device=dev)
+    ms_emit, ms_seg, ms_rec = [], [], []
+    with H.HashPruneReducer(num_points, l_max, dev) as hp:
+        for i in range(warmup + steps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev[0].record(stream)
+            _, gcount, _, nseg = E.emit_edge_segments(gids, lay, K, out_ids, out_d, sketches, 12, out=grec,
+                                                      segments=segs, stream=stream)
+            ev[1].record(stream)
+            hp.clear(stream=stream)
+            hp.insert_segments(grec, segs, nseg, stream=stream)
+            ev[2].record(stream)
+            ev[2].synchronize()
+            if i >= warmup:
+                ms_emit.append(ev[0].elapsed_time(ev[1]))
+                ms_seg.append(ev[1].elapsed_time(ev[2]))
+        t, hs, d, c = hp.slots(stream=stream)
         for i in range(warmup + steps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
@@ -619,9 +646,10 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
             b.record(stream)
             b.synchronize()
             if i >= warmup:
-                ms.append(a.elapsed_time(b))
-        t, hs, d, c = hp.slots(stream=stream)
+                ms_rec.append(a.elapsed_time(b))
+        t2, hs2, d2, c2 = hp.slots(stream=stream)
         stream.synchronize()
+        same = bool(torch.equal(c, c2) and torch.equal(t, t2) and torch.equal(d, d2) and torch.equal(hs, hs2))
         filled = int((c == l_max).sum().item())
         res = {}
         if check:
@@ -638,23 +666,30 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
             bad = np.nonzero((gc != wc) | np.any(gt != wt, 1) | np.any(gh != wh, 1) | np.any(gd != wd.view(np.uint32), 1))[0]
             res = {"points": sample_points, "records": int(len(sub)), "mismatched_points": int(len(bad)),
                    "bit_exact": len(bad) == 0}
-        del t, hs, d, c
-    tm = float(np.mean(ms)) / 1e3
-    # per record: read by the count and scatter passes, written grouped, read by
-    # the merge; per point: slots read and written (8 + 2 bytes each), 2 offsets
-    alg = count * 64 + num_points * (2 * l_max * 10 + 12)
-    log(f"hashprune: {count} records -> {num_points} reservoirs, {np.mean(ms):.3f} ms")
+        del t, hs, d, c, t2, hs2, d2, c2
+    del sketches, grec, segs
+    tm = float(np.mean(ms_seg)) / 1e3
+    # algorithmic bytes: every record read once (16 B), every segment read
+    # (16 B per row), each reservoir's slots written (10 B a slot) and its
+    # count (4 B); the reservoirs start empty
+    alg = gcount * 16 + nseg * 16 + num_points * (l_max * 10 + 4)
+    log(f"hashprune: {count} records -> {num_points} reservoirs, segments {np.mean(ms_seg):.3f} ms, "
+        f"records {np.mean(ms_rec):.3f} ms, identical {same}")
     return {
-        "kernels": "hp_count + hp_scan (3) + hp_scatter + hp_merge",
+        "kernels": "hp_seg_count + hp_scan (3) + hp_seg_scatter + hp_merge_large_seg + hp_merge_small_seg",
         "records": int(count),
+        "segments": int(nseg),
         "points": int(num_points),
         "l_max": l_max,
-        "ms_mean": round(float(np.mean(ms)), 4),
-        "ms_min": round(float(np.min(ms)), 4),
+        "ms_mean": round(float(np.mean(ms_seg)), 4),
+        "ms_min": round(float(np.min(ms_seg)), 4),
         "records_per_s": round(count / tm, 1),
         "hbm_bytes_algorithmic": int(alg),
         "hbm_gb_per_s_algorithmic": round(alg / tm / 1e9, 2),
         "peak_gb_per_s": HBM_PEAK_GBS,
+        "grouped_emission_ms_mean": round(float(np.mean(ms_emit)), 4),
+        "record_path_ms_mean": round(float(np.mean(ms_rec)), 4),
+        "record_path_equal": same,
         "full_reservoirs": filled,
         "parity_sample": res,
     }

@@ -537,6 +537,30 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
                                      uint64_t *leaf_record_offsets, uint64_t *record_count,
                                      void *stream);
 
+/* The same records in source-grouped order, for the GPU reservoirs: inside
+ * each leaf the records of one source are adjacent (member row r's forward
+ * records in rank order, then the reverse records naming it), and
+ * segments[i] describes the run of the i-th member row of the batch (leaves
+ * in order, rows in order): {src, first record (low and high words), record
+ * count}.  The records are the reference's (the multiset per leaf is the one
+ * tessa_emit_edge_records writes); only their order differs, and the order of
+ * the reverse records inside a run is not fixed.  It has no counterpart in the
+ * reference: it lets tessa_hashprune_insert_segments merge without grouping
+ * records.  segment_capacity must cover every member row (rows of leaves
+ * above max_leaf_rows excluded). */
+typedef struct tessa_edge_segment {
+    uint32_t src;
+    uint32_t first_lo;
+    uint32_t first_hi;
+    uint32_t count;
+} tessa_edge_segment;
+tessa_status tessa_emit_edge_segments(const uint32_t *global_ids, uint64_t resident_rows,
+                                      const tessa_leaf_batch *leaves, const uint32_t *topk_ids,
+                                      const float *topk_dists, const tessa_sketch_view *sketches,
+                                      tessa_edge_record *out, uint64_t out_capacity, tessa_edge_segment *segments,
+                                      uint64_t segment_capacity, uint64_t *record_count, uint64_t *segment_count,
+                                      void *stream);
+
 /* ---- HashPrune reservoirs: the consumer of the record stream ---------------
  * One HashPruneReservoir per point (hash_prune.rs:266-280, l_max slots, insert
  * :1243-1246 / insert_inner :1333-1453, total order :2094-2106), fed as
@@ -563,6 +587,13 @@ tessa_status tessa_hashprune_insert(tessa_hashprune *hp, const tessa_edge_record
 tessa_status tessa_hashprune_neighbors(const tessa_hashprune *hp, uint32_t *targets, uint16_t *hashes,
                                        float *dists, uint32_t *counts, void *stream);
 tessa_status tessa_hashprune_clear(tessa_hashprune *hp, void *stream);
+/* insert for records described by segments (tessa_emit_edge_segments): each
+ * segment's records share its src; a source's segments are merged together,
+ * reading the records in place (no grouping pass over the records).  Same
+ * result as tessa_hashprune_insert of the same records; same errors. */
+tessa_status tessa_hashprune_insert_segments(tessa_hashprune *hp, const tessa_edge_record *records,
+                                             const tessa_edge_segment *segments, uint64_t segment_count,
+                                             void *stream);
 
 /* ---- TierLift: the bounded host reducer of the record stream ---------------
  * Replaces SpillEdgeSink + ExternalHashPruneReducer

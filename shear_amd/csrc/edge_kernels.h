@@ -51,6 +51,13 @@ struct EdgeParams {
     uint32_t *leaf_totals;           // workspace: valid slots per leaf
     uint64_t *leaf_base;             // leaf_count + 1: first record of each leaf, then the total
     uint64_t *status;                // kEdgeStatusWords
+    // Source-grouped order (segments != null): inside each leaf the records
+    // with the same source are adjacent, one segment per member row; segment
+    // of (leaf, row r) = {src, first record (lo, hi words), record count} at
+    // segments[leaf_seg_base[leaf] + r].
+    uint4 *segments;
+    uint64_t segment_capacity;
+    uint64_t *leaf_seg_base;         // leaf_count + 1: first segment of each leaf, then the total
 };
 
 // log2 of the LDS membership table size: >= 2 x max_leaf_rows, >= 64.

@@ -148,7 +148,10 @@ __global__ __launch_bounds__(kThreads) void edge_count_kernel(EdgeParams p) {
     }
 }
 
-__global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
+// Exclusive scan over the leaves of v(leaf) into out[0..leaf_count], the
+// total last (one 1024-thread workgroup).
+template <typename F>
+__device__ uint64_t leaf_scan(const EdgeParams &p, F v_of, uint64_t *out, uint64_t scale) {
     __shared__ uint64_t wsum[16];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
     uint64_t carry = 0;
     for (uint32_t base = 0; base < p.leaf_count; base += 1024u) {
         const uint32_t i = base + tid;
-        const uint64_t v = i < p.leaf_count ? (p.leaf_totals[i] & ~kLeafRegular) : 0ull;
+        const uint64_t v = i < p.leaf_count ? v_of(i) : 0ull;
         uint64_t x = v;
 #pragma unroll
         for (uint32_t off = 1; off < 64; off <<= 1) {
@@ -170,14 +173,25 @@ __global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
             before += w < wave ? wsum[w] : 0ull;
             total += wsum[w];
         }
-        if (i < p.leaf_count) p.leaf_base[i] = 2ull * (carry + before + x - v);  // records
+        if (i < p.leaf_count) out[i] = scale * (carry + before + x - v);
         carry += total;
         __syncthreads();
     }
-    if (tid == 0) {
-        p.leaf_base[p.leaf_count] = 2ull * carry;
-        p.status[kEdgeRecordCount] = 2ull * carry;
-    }
+    if (tid == 0) out[p.leaf_count] = scale * carry;
+    return scale * carry;
+}
+
+__global__ __launch_bounds__(1024) void edge_scan_kernel(EdgeParams p) {
+    // records: 2 per valid slot
+    const uint64_t total = leaf_scan(p, [&](uint32_t i) { return (uint64_t)(p.leaf_totals[i] & ~kLeafRegular); },
+                                     p.leaf_base, 2ull);
+    if (threadIdx.x == 0) p.status[kEdgeRecordCount] = total;
+    // segments: one per member row of a leaf within max_leaf_rows
+    if (p.segments)
+        leaf_scan(p, [&](uint32_t i) {
+            const uint32_t n = p.member_counts[i];
+            return (uint64_t)(n <= p.max_leaf_rows ? n : 0u);
+        }, p.leaf_seg_base, 1ull);
 }
 
 // compute_hash(s_i, s_j) and compute_hash(s_j, s_i) over m_bits coordinates.
@@ -223,12 +237,15 @@ enum SketchMode : int {
 
 // LDS words of the emit kernel: wave sums | row counts | member ids | table
 // keys | table values (u16) | (16-byte aligned) staged sketches.
-__host__ __device__ inline uint32_t emit_sketch_offset(uint32_t max_rows, uint32_t table_bits) {
-    const uint32_t words = kWaves + 2u * max_rows + (1u << table_bits) + (1u << table_bits) / 2u;
+// Grouped order adds two arrays of max_rows words: per row its forward record
+// count and a cursor over its reverse records.
+__host__ __device__ inline uint32_t emit_sketch_offset(uint32_t max_rows, uint32_t table_bits, bool grouped) {
+    const uint32_t words = kWaves + 2u * max_rows + (1u << table_bits) + (1u << table_bits) / 2u +
+                           (grouped ? 2u * max_rows : 0u);
     return (words + 3u) & ~3u;
 }
 
-template <int kMode>
+template <int kMode, bool kGrouped>
 __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const uint32_t tbits = p.table_bits;
@@ -238,14 +255,17 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
     uint32_t *gid = cnt + p.max_leaf_rows;
     uint32_t *tkey = gid + p.max_leaf_rows;
     uint16_t *tval = reinterpret_cast<uint16_t *>(tkey + (1u << tbits));
-    float *sk_lds = reinterpret_cast<float *>(lds + emit_sketch_offset(p.max_leaf_rows, tbits));
+    uint32_t *fwd = tkey + (1u << tbits) + (1u << tbits) / 2u;  // grouped order only
+    uint32_t *rev = fwd + p.max_leaf_rows;
+    float *sk_lds = reinterpret_cast<float *>(lds + emit_sketch_offset(p.max_leaf_rows, tbits, kGrouped));
     const uint32_t mw = (p.m_bits + 3u) & ~3u;  // staged row stride (floats)
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
     const uint32_t q = lane & 31u;
     const uint32_t h = lane >> 5;
-    if (p.leaf_base[p.leaf_count] > p.out_capacity) {
+    if (p.leaf_base[p.leaf_count] > p.out_capacity ||
+        (kGrouped && p.leaf_seg_base[p.leaf_count] > p.segment_capacity)) {
         if (blockIdx.x == 0 && tid == 0) p.status[kEdgeCapacityHit] = 1ull;
         return;  // uniform over the grid: nothing is written
     }
@@ -257,7 +277,13 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
         // Row record offsets: r * k_eff for a regular leaf (every slot valid),
         // else counted again and scanned into cnt.
         const bool regular = (p.leaf_totals[leaf] & kLeafRegular) != 0u;
-        if (regular) {
+        if (kGrouped) {
+            for (uint32_t c = tid; c < n; c += kThreads) {
+                fwd[c] = 0u;
+                rev[c] = 0u;
+            }
+            __syncthreads();
+        } else if (regular) {
             __syncthreads();
         } else {
             bool unused;
@@ -303,6 +329,72 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
         const uint64_t out0 = p.output_offsets[leaf];
         const uint64_t rec0 = p.leaf_base[leaf];
         constexpr uint32_t kStep = 2u * kWaves;
+        if (kGrouped) {
+            // Per member: its forward records (its valid slots) and its
+            // reverse records (valid slots of other rows naming it); the
+            // member's segment holds the forward ones, then the reverse ones.
+            for (uint32_t r0 = 2u * wave + h; r0 < n + h; r0 += kStep * kEmitUnroll) {
+                uint32_t j[kEmitUnroll];
+                float d[kEmitUnroll];
+#pragma unroll
+                for (int u = 0; u < kEmitUnroll; ++u) {
+                    const uint32_t r = r0 + u * kStep;
+                    j[u] = kNoKey;
+                    d[u] = 0.0f;
+                    if (r < n && q < kl) {
+                        const uint64_t sl = out0 + (uint64_t)r * p.k + q;
+                        j[u] = p.topk_ids[sl];
+                        d[u] = p.topk_dists[sl];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kEmitUnroll; ++u) {
+                    const uint32_t r = r0 + u * kStep;
+                    const bool valid = slot_valid(j[u], d[u]);
+                    const uint64_t m = __ballot(valid);
+                    if (r < n && q == 0u) fwd[r] = (uint32_t)__popc((uint32_t)(h ? (m >> 32) : m));
+                    if (valid) {
+                        for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask) {
+                            const uint32_t t = tkey[slot];
+                            if (t == j[u]) {
+                                atomicAdd(&rev[tval[slot]], 1u);
+                                break;
+                            }
+                            if (t == kNoKey) break;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            // exclusive scan of fwd + rev into cnt (segment offsets in the leaf)
+            const uint32_t per = (n + kThreads - 1) / kThreads;
+            const uint32_t b = tid * per;
+            const uint32_t e = b + per < n ? b + per : n;
+            uint32_t sum = 0;
+            for (uint32_t i = b; i < e; ++i) sum += fwd[i] + rev[i];
+            uint32_t x = sum;
+#pragma unroll
+            for (uint32_t off = 1; off < 64; off <<= 1) {
+                const uint32_t y = __shfl_up(x, off);
+                if (lane >= off) x += y;
+            }
+            if (lane == 63u) wsum[wave] = x;
+            __syncthreads();
+            uint32_t base = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) base += (uint32_t)w < wave ? wsum[w] : 0u;
+            uint32_t run = base + x - sum;
+            const uint64_t sbase = p.leaf_seg_base[leaf];
+            for (uint32_t i = b; i < e; ++i) {
+                const uint32_t c = fwd[i] + rev[i];
+                cnt[i] = run;
+                const uint64_t first = rec0 + run;
+                p.segments[sbase + i] = make_uint4(gid[i], (uint32_t)first, (uint32_t)(first >> 32), c);
+                run += c;
+                rev[i] = run - rev[i];  // cursor: the first reverse record's place
+            }
+            __syncthreads();
+        }
         for (uint32_t r0 = 2u * wave + h; r0 < n + h; r0 += kStep * kEmitUnroll) {
             uint32_t j[kEmitUnroll];
             float d[kEmitUnroll];
@@ -360,7 +452,24 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                 // row, taking the slot's values by shuffle: 16-byte stores from
                 // consecutive lanes to consecutive addresses.
                 const uint64_t ok_mask = __ballot(ok);
-                if (__ballot((half & (half + 1u)) != 0u) == 0ull) {
+                if (kGrouped) {
+                    if (ok) {
+                        // forward: its place among the row's valid slots; reverse:
+                        // the next free place of j's segment
+                        uint32_t cj = 0;
+                        for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask)
+                            if (tkey[slot] == j[u]) {
+                                cj = tval[slot];
+                                break;
+                            }
+                        const uint32_t fpos = cnt[r] + (uint32_t)__popc(half & ((1u << q) - 1u));
+                        const uint32_t rpos = atomicAdd(&rev[cj], 1u);
+                        store_record(p.out, rec0 + fpos, gi, j[u], hf, db);
+                        store_record(p.out, rec0 + rpos, j[u], gi, hr, db);
+                    }
+                    (void)ok_mask;
+                    (void)row_rec;
+                } else if (__ballot((half & (half + 1u)) != 0u) == 0ull) {
                     const uint32_t row_slots = (uint32_t)__popc(half);
                     const uint64_t base = rec0 + 2ull * row_rec;
 #pragma unroll
@@ -411,15 +520,27 @@ int launch_edge_records(const EdgeParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(edge_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
     // Stage the leaf's sketch rows in LDS when that keeps two workgroups per
     // CU; else read them from HBM (float4 loads when rows are 16-byte aligned).
-    const size_t base_lds = (size_t)emit_sketch_offset(p.max_leaf_rows, p.table_bits) * sizeof(uint32_t);
+    const bool grouped = p.segments != nullptr;
+    const size_t base_lds = (size_t)emit_sketch_offset(p.max_leaf_rows, p.table_bits, grouped) * sizeof(uint32_t);
     const size_t staged = (size_t)p.max_leaf_rows * ((p.m_bits + 3u) & ~3u) * sizeof(float);
     const bool vec4 = p.width % 4u == 0u && (reinterpret_cast<uintptr_t>(p.sketches) & 15u) == 0u;
-    if (base_lds + staged <= kEmitLdsBudget)
-        hipLaunchKernelGGL(edge_emit_kernel<kSketchLds>, dim3(grid), dim3(kThreads), base_lds + staged, stream, p);
-    else if (vec4)
-        hipLaunchKernelGGL(edge_emit_kernel<kSketchGlobalV4>, dim3(grid), dim3(kThreads), base_lds, stream, p);
-    else
-        hipLaunchKernelGGL(edge_emit_kernel<kSketchGlobal>, dim3(grid), dim3(kThreads), base_lds, stream, p);
+    const bool in_lds = base_lds + staged <= kEmitLdsBudget;
+    const size_t lds = in_lds ? base_lds + staged : base_lds;
+    if (grouped) {
+        if (in_lds)
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchLds, true>), dim3(grid), dim3(kThreads), lds, stream, p);
+        else if (vec4)
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchGlobalV4, true>), dim3(grid), dim3(kThreads), lds, stream, p);
+        else
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchGlobal, true>), dim3(grid), dim3(kThreads), lds, stream, p);
+    } else {
+        if (in_lds)
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchLds, false>), dim3(grid), dim3(kThreads), lds, stream, p);
+        else if (vec4)
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchGlobalV4, false>), dim3(grid), dim3(kThreads), lds, stream, p);
+        else
+            hipLaunchKernelGGL((edge_emit_kernel<kSketchGlobal, false>), dim3(grid), dim3(kThreads), lds, stream, p);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

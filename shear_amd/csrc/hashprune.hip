@@ -285,10 +285,11 @@ __device__ __forceinline__ void reg_bitonic(uint32_t (&h)[E], uint64_t (&k)[E], 
 
 // One merge of a source's n_old slots and n_new records (n_old + n_new <= 64*E)
 // entirely in registers; writes the new slots and returns their count.
-template <int E>
-__device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot_hash_in, uint32_t n_old,
-                              const uint4 *recs, uint32_t n_new, const uint4 &r0, uint32_t l_max, uint32_t lane,
-                              uint64_t *slot_keys_out, uint16_t *slot_hash_out) {
+// fetch(q, t) returns new record t (t < n_new) for register slot q.
+template <int E, typename Fetch>
+__device__ uint32_t reg_merge_f(const uint64_t *slot_keys_in, const uint16_t *slot_hash_in, uint32_t n_old,
+                                uint32_t n_new, Fetch &&fetch, uint32_t l_max, uint32_t lane,
+                                uint64_t *slot_keys_out, uint16_t *slot_hash_out) {
     const uint32_t N = n_old + n_new;
     uint32_t h[E];
     uint64_t k[E];
@@ -301,8 +302,7 @@ __device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot
             k[q] = slot_keys_in[e];
             h[q] = slot_hash_in[e];
         } else if (e < N) {
-            // the prefetched first 64 records line up with this slot when n_old == 64*q
-            const uint4 r = (n_old == (uint32_t)q * 64u) ? r0 : recs[e - n_old];
+            const uint4 r = fetch(q, e - n_old);
             k[q] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
             h[q] = r.z & 0xffffu;
         }
@@ -362,6 +362,17 @@ __device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot
     return base;
 }
 
+// Records contiguous at recs; the first 64 were prefetched into r0 (they line
+// up with register slot q when n_old == 64*q).
+template <int E>
+__device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot_hash_in, uint32_t n_old,
+                              const uint4 *recs, uint32_t n_new, const uint4 &r0, uint32_t l_max, uint32_t lane,
+                              uint64_t *slot_keys_out, uint16_t *slot_hash_out) {
+    auto fetch = [&](int q, uint32_t t) -> uint4 { return (n_old == (uint32_t)q * 64u) ? r0 : recs[t]; };
+    return reg_merge_f<E>(slot_keys_in, slot_hash_in, n_old, n_new, fetch, l_max, lane, slot_keys_out,
+                          slot_hash_out);
+}
+
 struct HpWaveLds {
     uint64_t key[kHpMergeCap];      // candidates: total-order key (dist key << 32 | target)
     uint32_t val[kHpMergeCap];      // their hashes
@@ -418,6 +429,89 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_small_kernel(const uint4 
 
 // Sources with more than kHpRegMax candidates: merged in LDS, kHpMergeCap at a
 // time.
+// One LDS merge round: the wave's reservoir w.key/w.val[0, n_old) and new
+// candidates w.key/w.val[n_old, N) become the merged reservoir in
+// w.tkey/w.thash[0, result); returns its size.
+__device__ uint32_t lds_merge_round(HpWaveLds &w, uint32_t n_old, uint32_t N, uint32_t l_max, uint32_t lane) {
+    uint32_t P = 64;
+    while (P < N) P <<= 1;
+    for (uint32_t e = N + lane; e < P; e += 64) {
+        w.key[e] = ~0ull;
+        w.val[e] = 0xffffffffu;  // after every real hash (<= 0xffff)
+    }
+    __builtin_amdgcn_wave_barrier();
+    // each hash's best first: sort by (hash, total-order key)
+    wave_bitonic_hk(w.val, w.key, P, lane);
+    const uint32_t E = P / 64;
+    const uint32_t eb = lane * E;
+    // kept = first of its hash; kpos = its place among the kept
+    uint32_t kcount = 0;
+    for (uint32_t q = 0; q < E; ++q) {
+        const uint32_t e = eb + q;
+        kcount += (e < N && (e == 0 || w.val[e - 1] != w.val[e])) ? 1u : 0u;
+    }
+    uint32_t n_kept;
+    const uint32_t kbase = wave_excl_scan(kcount, lane, n_kept);
+    if (n_kept <= l_max) {
+        // every hash's best stays, already in ascending hash order
+        uint32_t run = kbase;
+        for (uint32_t q = 0; q < E; ++q) {
+            const uint32_t e = eb + q;
+            if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
+                w.tkey[run] = w.key[e];
+                w.thash[run] = w.val[e];
+                ++run;
+            }
+        }
+        n_old = n_kept;
+    } else {
+        // the l_max best of the kept by (key, hash): threshold from a sort of the kept
+        uint32_t run = kbase;
+        for (uint32_t q = 0; q < E; ++q) {
+            const uint32_t e = eb + q;
+            if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
+                w.tkey[run] = w.key[e];
+                w.thash[run] = w.val[e];
+                ++run;
+            }
+        }
+        uint32_t P2 = 64;
+        while (P2 < n_kept) P2 <<= 1;
+        for (uint32_t e = n_kept + lane; e < P2; e += 64) {
+            w.tkey[e] = ~0ull;
+            w.thash[e] = 0xffffffffu;
+        }
+        __builtin_amdgcn_wave_barrier();
+        wave_bitonic<uint64_t>(w.tkey, w.thash, P2, lane);
+        const uint64_t tk = w.tkey[l_max - 1];
+        const uint32_t th = w.thash[l_max - 1];
+        uint32_t scount = 0;
+        for (uint32_t q = 0; q < E; ++q) {
+            const uint32_t e = eb + q;
+            const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
+            const uint64_t k = w.key[e];
+            scount += (kept && (k < tk || (k == tk && w.val[e] <= th))) ? 1u : 0u;
+        }
+        uint32_t n_sel;
+        uint32_t srun = wave_excl_scan(scount, lane, n_sel);
+        for (uint32_t q = 0; q < E; ++q) {
+            const uint32_t e = eb + q;
+            const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
+            const uint64_t k = w.key[e];
+            if (kept && (k < tk || (k == tk && w.val[e] <= th))) {
+                w.tkey[srun] = k;
+                w.thash[srun] = w.val[e];
+                ++srun;
+            }
+        }
+        n_old = n_sel;
+    }
+    __builtin_amdgcn_wave_barrier();
+    return n_old;
+}
+
+// Sources with more than kHpRegMax candidates: merged in LDS, kHpMergeCap at a
+// time.
 __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 *grouped, const uint32_t *offsets,
                                                                     uint32_t num_points, uint32_t l_max,
                                                                     uint64_t *slot_keys, uint16_t *slot_hash,
@@ -446,81 +540,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 
                 w.key[n_old + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
                 w.val[n_old + e] = r.z & 0xffffu;
             }
-            const uint32_t N = n_old + take;
-            uint32_t P = 64;
-            while (P < N) P <<= 1;
-            for (uint32_t e = N + lane; e < P; e += 64) {
-                w.key[e] = ~0ull;
-                w.val[e] = 0xffffffffu;  // after every real hash (<= 0xffff)
-            }
-            __builtin_amdgcn_wave_barrier();
-            // each hash's best first: sort by (hash, total-order key)
-            wave_bitonic_hk(w.val, w.key, P, lane);
-            const uint32_t E = P / 64;
-            const uint32_t eb = lane * E;
-            // kept = first of its hash; kpos = its place among the kept
-            uint32_t kcount = 0;
-            for (uint32_t q = 0; q < E; ++q) {
-                const uint32_t e = eb + q;
-                kcount += (e < N && (e == 0 || w.val[e - 1] != w.val[e])) ? 1u : 0u;
-            }
-            uint32_t n_kept;
-            const uint32_t kbase = wave_excl_scan(kcount, lane, n_kept);
-            if (n_kept <= l_max) {
-                // every hash's best stays, already in ascending hash order
-                uint32_t run = kbase;
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t e = eb + q;
-                    if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
-                        w.tkey[run] = w.key[e];
-                        w.thash[run] = w.val[e];
-                        ++run;
-                    }
-                }
-                n_old = n_kept;
-            } else {
-                // the l_max best of the kept by (key, hash): threshold from a sort of the kept
-                uint32_t run = kbase;
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t e = eb + q;
-                    if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
-                        w.tkey[run] = w.key[e];
-                        w.thash[run] = w.val[e];
-                        ++run;
-                    }
-                }
-                uint32_t P2 = 64;
-                while (P2 < n_kept) P2 <<= 1;
-                for (uint32_t e = n_kept + lane; e < P2; e += 64) {
-                    w.tkey[e] = ~0ull;
-                    w.thash[e] = 0xffffffffu;
-                }
-                __builtin_amdgcn_wave_barrier();
-                wave_bitonic<uint64_t>(w.tkey, w.thash, P2, lane);
-                const uint64_t tk = w.tkey[l_max - 1];
-                const uint32_t th = w.thash[l_max - 1];
-                uint32_t scount = 0;
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t e = eb + q;
-                    const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
-                    const uint64_t k = w.key[e];
-                    scount += (kept && (k < tk || (k == tk && w.val[e] <= th))) ? 1u : 0u;
-                }
-                uint32_t n_sel;
-                uint32_t srun = wave_excl_scan(scount, lane, n_sel);
-                for (uint32_t q = 0; q < E; ++q) {
-                    const uint32_t e = eb + q;
-                    const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
-                    const uint64_t k = w.key[e];
-                    if (kept && (k < tk || (k == tk && w.val[e] <= th))) {
-                        w.tkey[srun] = k;
-                        w.thash[srun] = w.val[e];
-                        ++srun;
-                    }
-                }
-                n_old = n_sel;
-            }
-            __builtin_amdgcn_wave_barrier();
+            n_old = lds_merge_round(w, n_old, n_old + take, l_max, lane);
             used += take;
             if (used < n_new) {
                 for (uint32_t e = lane; e < n_old; e += 64) {
@@ -529,6 +549,178 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 
                 }
                 __builtin_amdgcn_wave_barrier();
             }
+        }
+        for (uint32_t e = lane; e < n_old; e += 64) {
+            slot_keys[sbase + e] = w.tkey[e];
+            slot_hash[sbase + e] = (uint16_t)w.thash[e];
+        }
+        if (lane == 0) slot_count[src] = n_old;
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// ---- segment mode: records left where the emitter put them ------------------
+// A segment {src, first record lo/hi, count} names a run of records of one
+// source.  Segments are grouped by source (count, scan, scatter of segment
+// indices: atomics per segment, not per record), then each source's
+// segments are merged together, reading its records in place.
+
+__global__ void hp_seg_count_kernel(const uint4 *segs, uint64_t nseg, uint32_t num_points, uint32_t *bucket,
+                                    uint64_t *status) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint4 g = segs[i];
+        if (g.w == 0u) continue;
+        if (g.x >= num_points) {
+            // the first record of the segment carries the bad source
+            atomicMin((unsigned long long *)status, (unsigned long long)(((uint64_t)g.z << 32) | g.y));
+            continue;
+        }
+        atomicAdd(&bucket[g.x], 1u);
+    }
+}
+
+__global__ void hp_seg_scatter_kernel(const uint4 *segs, uint64_t nseg, uint32_t num_points, uint32_t *bucket,
+                                      const uint32_t *offsets, uint32_t *seg_grouped) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint4 g = segs[i];
+        if (g.w == 0u || g.x >= num_points) continue;
+        seg_grouped[offsets[g.x] + atomicSub(&bucket[g.x], 1u) - 1u] = (uint32_t)i;
+    }
+}
+
+// Register merge of one source's reservoir and its segments' records.  Lane
+// s < ns holds segment s (exclusive prefix `pre`, `cnt` records from
+// `first`).  The record of each register slot is located first, with every
+// lane active (the lanes' segment values are read by shuffles), then the
+// merge reads it.
+template <int E>
+__device__ uint32_t seg_merge(const uint4 *records, uint64_t *slot_keys, uint16_t *slot_hash, uint32_t n_old,
+                              uint32_t n_new, uint32_t ns, uint32_t pre, uint32_t cnt, uint64_t first, uint32_t l_max,
+                              uint32_t lane) {
+    uint64_t addr[E];
+#pragma unroll
+    for (int q = 0; q < E; ++q) addr[q] = 0;
+    for (uint32_t sg = 0; sg < ns; ++sg) {
+        const uint32_t ps = __shfl(pre, (int)sg), cs = __shfl(cnt, (int)sg);
+        const uint64_t fs = ((uint64_t)__shfl((uint32_t)(first >> 32), (int)sg) << 32) | __shfl((uint32_t)first, (int)sg);
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            if (e >= n_old && e - n_old >= ps && e - n_old < ps + cs) addr[q] = fs + (e - n_old - ps);
+        }
+    }
+    (void)n_new;
+    auto fetch = [&](int q, uint32_t) -> uint4 {
+        uint64_t a = addr[0];
+#pragma unroll
+        for (int i = 1; i < E; ++i) a = i == q ? addr[i] : a;
+        return records[a];
+    };
+    return reg_merge_f<E>(slot_keys, slot_hash, n_old, n_new, fetch, l_max, lane, slot_keys, slot_hash);
+}
+
+// Register merges of sources with at most 64 segments and kHpRegMax
+// candidates.  Lane s < nseg holds segment s; a new record t is found by its
+// segment's exclusive prefix.
+__global__ __launch_bounds__(kHpThreads) void hp_merge_small_seg_kernel(const uint4 *records, const uint4 *segs,
+                                                                        const uint32_t *seg_grouped,
+                                                                        const uint32_t *offsets, uint32_t num_points,
+                                                                        uint32_t l_max, uint64_t *slot_keys,
+                                                                        uint16_t *slot_hash, uint32_t *slot_count) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t src = blockIdx.x * kHpWaves + (threadIdx.x >> 6); src < num_points; src += waves) {
+        const uint32_t s0 = offsets[src];
+        const uint32_t ns = offsets[src + 1] - s0;
+        if (ns == 0u || ns > 64u) continue;  // none, or hp_merge_large_seg_kernel
+        uint32_t cnt = 0;
+        uint64_t first = 0;
+        if (lane < ns) {
+            const uint4 g = segs[seg_grouped[s0 + lane]];
+            cnt = g.w;
+            first = ((uint64_t)g.z << 32) | g.y;
+        }
+        uint32_t n_new;
+        const uint32_t pre = wave_excl_scan(cnt, lane, n_new);
+        const uint32_t n_old = slot_count[src];
+        if (n_old + n_new > kHpRegMax) continue;
+        const uint64_t sbase = (uint64_t)src * l_max;
+        uint32_t c;
+        if (n_old + n_new <= 64u)
+            c = seg_merge<1>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
+                             lane);
+        else if (n_old + n_new <= 128u)
+            c = seg_merge<2>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
+                             lane);
+        else
+            c = seg_merge<4>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
+                             lane);
+        if (lane == 0) slot_count[src] = c;
+    }
+}
+
+// The other sources: their segments' records staged in LDS, merged kHpMergeCap
+// candidates at a time.
+__global__ __launch_bounds__(kHpThreads) void hp_merge_large_seg_kernel(const uint4 *records, const uint4 *segs,
+                                                                        const uint32_t *seg_grouped,
+                                                                        const uint32_t *offsets, uint32_t num_points,
+                                                                        uint32_t l_max, uint64_t *slot_keys,
+                                                                        uint16_t *slot_hash, uint32_t *slot_count) {
+    __shared__ HpWaveLds lds[kHpWaves];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    HpWaveLds &w = lds[wave];
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t src = blockIdx.x * kHpWaves + wave; src < num_points; src += waves) {
+        const uint32_t s0 = offsets[src];
+        const uint32_t ns = offsets[src + 1] - s0;
+        if (ns == 0u) continue;
+        uint32_t n_old = slot_count[src];
+        if (ns <= 64u) {
+            // the small kernel's case unless it holds more than kHpRegMax candidates
+            const uint32_t cnt = lane < ns ? segs[seg_grouped[s0 + lane]].w : 0u;
+            uint32_t n_new;
+            (void)wave_excl_scan(cnt, lane, n_new);
+            if (n_old + n_new <= kHpRegMax) continue;
+        }
+        const uint64_t sbase = (uint64_t)src * l_max;
+        for (uint32_t e = lane; e < n_old; e += 64) {
+            w.key[e] = slot_keys[sbase + e];
+            w.val[e] = slot_hash[sbase + e];
+        }
+        __builtin_amdgcn_wave_barrier();
+        uint32_t fill = 0;  // candidates staged after the reservoir
+        bool merged = false;
+        for (uint32_t si = 0; si < ns; ++si) {
+            const uint4 g = segs[seg_grouped[s0 + si]];
+            const uint64_t first = ((uint64_t)g.z << 32) | g.y;
+            uint32_t used = 0;
+            while (used < g.w) {
+                const uint32_t room = kHpMergeCap - n_old - fill;
+                const uint32_t take = (g.w - used < room) ? g.w - used : room;
+                for (uint32_t e = lane; e < take; e += 64) {
+                    const uint4 r = records[first + used + e];
+                    w.key[n_old + fill + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
+                    w.val[n_old + fill + e] = r.z & 0xffffu;
+                }
+                fill += take;
+                used += take;
+                if (n_old + fill == kHpMergeCap) {
+                    __builtin_amdgcn_wave_barrier();
+                    n_old = lds_merge_round(w, n_old, n_old + fill, l_max, lane);
+                    fill = 0;
+                    for (uint32_t e = lane; e < n_old; e += 64) {
+                        w.key[e] = w.tkey[e];
+                        w.val[e] = w.thash[e];
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    merged = true;
+                }
+            }
+        }
+        if (fill > 0 || !merged) {
+            __builtin_amdgcn_wave_barrier();
+            n_old = lds_merge_round(w, n_old, n_old + fill, l_max, lane);
         }
         for (uint32_t e = lane; e < n_old; e += 64) {
             slot_keys[sbase + e] = w.tkey[e];
@@ -592,6 +784,28 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
                        s.grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
     hipLaunchKernelGGL(hp_merge_small_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream,
                        s.grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, const uint4 *segs, uint64_t nseg,
+                                     hipStream_t stream) {
+    const uint32_t n = s.num_points;
+    hipLaunchKernelGGL(hp_status_init, dim3(1), dim3(1), 0, stream, s.status);
+    if (nseg == 0 || n == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
+    hipLaunchKernelGGL(hp_seg_count_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs, nseg, n,
+                       s.bucket, s.status);
+    const uint32_t nb = (n + kScanBlock - 1) / kScanBlock;
+    hipLaunchKernelGGL(hp_scan_reduce, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums);
+    hipLaunchKernelGGL(hp_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, s.block_sums, nb, s.offsets, n);
+    hipLaunchKernelGGL(hp_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums, s.offsets);
+    hipLaunchKernelGGL(hp_seg_scatter_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs, nseg, n,
+                       s.bucket, s.offsets, s.seg_grouped);
+    // large first (a merge never shrinks a reservoir, so the small kernel then
+    // skips what the large kernel merged)
+    hipLaunchKernelGGL(hp_merge_large_seg_kernel, dim3(grid_for(n, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
+                       records, segs, s.seg_grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    hipLaunchKernelGGL(hp_merge_small_seg_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream,
+                       records, segs, s.seg_grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

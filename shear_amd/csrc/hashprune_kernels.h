@@ -25,11 +25,17 @@ struct HashPruneState {
     uint4 *grouped = nullptr;       // the batch's records grouped by source
     uint64_t grouped_capacity = 0;
     uint64_t *status = nullptr;     // [0] first record with src >= num_points (UINT64_MAX: none)
+    uint32_t *seg_grouped = nullptr; // segment mode: the batch's segment indices grouped by source
+    uint64_t seg_grouped_capacity = 0;
 };
 
 // Groups `count` records by source and merges each source's new candidates
 // into its reservoir.  Returns 0, or -1 when a launch failed.
 int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t count, hipStream_t stream);
+// The same for records described by segments {src, first lo, first hi, count}
+// (records left in place; segments grouped by source instead of records).
+int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, const uint4 *segs, uint64_t nseg,
+                                     hipStream_t stream);
 // Zeroes the per-source counters (all reservoirs empty).
 int launch_hashprune_clear(HashPruneState &s, hipStream_t stream);
 // Slot targets / hashes / distances (ascending hash) and counts per point.

@@ -102,6 +102,8 @@ struct DeviceWorkspace {
     uint64_t edge_totals_capacity = 0;
     uint64_t *edge_base = nullptr;
     uint64_t edge_base_capacity = 0;
+    uint64_t *edge_seg_base = nullptr;  // source-grouped order: first segment of each leaf
+    uint64_t edge_seg_base_capacity = 0;
     uint64_t *edge_status = nullptr;
     uint64_t edge_status_capacity = 0;
     // graph packing: scan partials, row offsets, (total words, max degree)
@@ -1758,12 +1760,17 @@ tessa_status tessa_session_release(tessa_session *s, uint64_t seq) {
 
 extern "C" {
 
-tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t resident_rows, const tessa_leaf_batch *lb,
-                                     const uint32_t *topk_ids, const float *topk_dists,
-                                     const tessa_sketch_view *sk, tessa_edge_record *out, uint64_t out_capacity,
-                                     uint64_t *leaf_record_offsets, uint64_t *record_count, void *stream) {
+static tessa_status emit_edge_records_impl(const uint32_t *global_ids, uint64_t resident_rows,
+                                           const tessa_leaf_batch *lb, const uint32_t *topk_ids,
+                                           const float *topk_dists, const tessa_sketch_view *sk,
+                                           tessa_edge_record *out, uint64_t out_capacity,
+                                           uint64_t *leaf_record_offsets, uint64_t *record_count,
+                                           tessa_edge_segment *segments, uint64_t segment_capacity,
+                                           uint64_t *segment_count, void *stream) {
     static_assert(sizeof(tessa_edge_record) == 16, "SpillRecord16 is 16 bytes");
+    static_assert(sizeof(tessa_edge_segment) == 16, "segment descriptors are 16 bytes");
     if (record_count) *record_count = 0;
+    if (segment_count) *segment_count = 0;
     if (!global_ids || !lb || !topk_ids || !topk_dists || !sk || !sk->rows || !record_count)
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge records: null argument");
     if (!lb->members || !lb->member_offsets || !lb->member_counts || !lb->output_offsets)
@@ -1792,6 +1799,11 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
         st = grow(&ws->edge_base, &ws->edge_base_capacity, leaves + 1, sizeof(uint64_t), "edge leaf offsets");
         if (st.code) return st;
     }
+    if (segments) {
+        st = grow(&ws->edge_seg_base, &ws->edge_seg_base_capacity, leaves + 1, sizeof(uint64_t),
+                  "edge segment offsets");
+        if (st.code) return st;
+    }
     EdgeParams p{};
     p.gids = global_ids;
     p.resident_rows = resident_rows;
@@ -1814,10 +1826,16 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
     p.leaf_totals = ws->edge_totals;
     p.leaf_base = leaf_record_offsets ? leaf_record_offsets : ws->edge_base;
     p.status = ws->edge_status;
+    p.segments = reinterpret_cast<uint4 *>(segments);
+    p.segment_capacity = segments ? segment_capacity : 0;
+    p.leaf_seg_base = segments ? ws->edge_seg_base : nullptr;
     if (launch_edge_records(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "edge record kernel launch failed");
     uint64_t w[kEdgeStatusWords];
     TESSA_HIP_TRY(hipMemcpyAsync(w, p.status, sizeof(w), hipMemcpyDeviceToHost, s));
+    uint64_t nseg = 0;
+    if (segments) TESSA_HIP_TRY(hipMemcpyAsync(&nseg, ws->edge_seg_base + leaves, 8, hipMemcpyDeviceToHost, s));
     TESSA_HIP_TRY(hipStreamSynchronize(s));
+    if (segment_count) *segment_count = nseg;
     if (w[kEdgeLeafTooLarge])
         return make_status(TESSA_ERR_OVERFLOW, TESSA_OVF_LEAF_ROW,
                            "edge records: a leaf of %llu rows exceeds max_leaf_rows=%u overflow_flags=0x%llx "
@@ -1854,11 +1872,34 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf %llu point %u has no sketch row (sketch rows %llu)",
                            (unsigned long long)leaf, g, (unsigned long long)sk->sketch_rows);
     }
-    if (w[kEdgeCapacityHit])
+    if (w[kEdgeCapacityHit]) {
+        if (segments && nseg > segment_capacity)
+            return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge segment capacity %llu below the %llu segments needed",
+                               (unsigned long long)segment_capacity, (unsigned long long)nseg);
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge record capacity %llu below the %llu records needed",
                            (unsigned long long)p.out_capacity, (unsigned long long)w[kEdgeRecordCount]);
+    }
     *record_count = w[kEdgeRecordCount];
     return ok_status();
+}
+
+tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t resident_rows, const tessa_leaf_batch *lb,
+                                     const uint32_t *topk_ids, const float *topk_dists,
+                                     const tessa_sketch_view *sk, tessa_edge_record *out, uint64_t out_capacity,
+                                     uint64_t *leaf_record_offsets, uint64_t *record_count, void *stream) {
+    return emit_edge_records_impl(global_ids, resident_rows, lb, topk_ids, topk_dists, sk, out, out_capacity,
+                                  leaf_record_offsets, record_count, nullptr, 0, nullptr, stream);
+}
+
+tessa_status tessa_emit_edge_segments(const uint32_t *global_ids, uint64_t resident_rows, const tessa_leaf_batch *lb,
+                                      const uint32_t *topk_ids, const float *topk_dists,
+                                      const tessa_sketch_view *sk, tessa_edge_record *out, uint64_t out_capacity,
+                                      tessa_edge_segment *segments, uint64_t segment_capacity,
+                                      uint64_t *record_count, uint64_t *segment_count, void *stream) {
+    if (!segments || !segment_count)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge segments: null segment output");
+    return emit_edge_records_impl(global_ids, resident_rows, lb, topk_ids, topk_dists, sk, out, out_capacity, nullptr,
+                                  record_count, segments, segment_capacity, segment_count, stream);
 }
 
 }  // extern "C"
@@ -1875,7 +1916,8 @@ namespace {
 void free_hashprune(tessa_hashprune *hp) {
     auto &s = hp->st;
     for (void *ptr : {(void *)s.slot_keys, (void *)s.slot_hash, (void *)s.slot_count, (void *)s.bucket,
-                      (void *)s.offsets, (void *)s.block_sums, (void *)s.grouped, (void *)s.status})
+                      (void *)s.offsets, (void *)s.block_sums, (void *)s.grouped, (void *)s.status,
+                      (void *)s.seg_grouped})
         if (ptr) (void)hipFree(ptr);
     delete hp;
 }
@@ -1973,6 +2015,43 @@ tessa_status tessa_hashprune_insert(tessa_hashprune *hp, const tessa_edge_record
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
                            "Spill reducer encountered edge p=%u outside shard range [0, %u) (record %llu; the "
                            "batch's valid records were inserted)",
+                           r.src, s.num_points, (unsigned long long)bad);
+    }
+    return ok_status();
+}
+
+tessa_status tessa_hashprune_insert_segments(tessa_hashprune *hp, const tessa_edge_record *records,
+                                             const tessa_edge_segment *segments, uint64_t segment_count,
+                                             void *stream) {
+    if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
+    if (segment_count && (!records || !segments))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune: null records or segments");
+    if (segment_count >= 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: %llu segments in one batch (limit 2^32-2)",
+                           (unsigned long long)segment_count);
+    auto &s = hp->st;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    if (segment_count > s.seg_grouped_capacity) {
+        TESSA_HIP_TRY(hipStreamSynchronize(hs));
+        if (s.seg_grouped) TESSA_HIP_TRY(hipFree(s.seg_grouped));
+        s.seg_grouped = nullptr;
+        s.seg_grouped_capacity = 0;
+        tessa_status st = hp_alloc((void **)&s.seg_grouped, segment_count * 4, "hashprune grouped segments");
+        if (st.code) return st;
+        s.seg_grouped_capacity = segment_count;
+    }
+    if (tessa::launch_hashprune_insert_segments(s, reinterpret_cast<const uint4 *>(records),
+                                                reinterpret_cast<const uint4 *>(segments), segment_count, hs) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "hashprune segment insert launch failed");
+    uint64_t bad = 0;
+    TESSA_HIP_TRY(hipMemcpyAsync(&bad, s.status, sizeof(bad), hipMemcpyDeviceToHost, hs));
+    TESSA_HIP_TRY(hipStreamSynchronize(hs));
+    if (bad != ~0ull) {
+        tessa_edge_record r{};
+        TESSA_HIP_TRY(hipMemcpy(&r, records + bad, sizeof(r), hipMemcpyDeviceToHost));
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "Spill reducer encountered edge p=%u outside shard range [0, %u) (record %llu; the "
+                           "batch's other segments were inserted)",
                            r.src, s.num_points, (unsigned long long)bad);
     }
     return ok_status();

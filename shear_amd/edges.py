@@ -63,6 +63,35 @@ def emit_edge_records(global_ids: torch.Tensor, layouts: LeafLayouts, k: int, to
     return out, int(count.value)
 
 
+def emit_edge_segments(global_ids: torch.Tensor, layouts: LeafLayouts, k: int, topk_ids: torch.Tensor,
+                       topk_dists: torch.Tensor, sketches: torch.Tensor, m_hash_bits: int = DEFAULT_M_HASH_BITS,
+                       out: torch.Tensor | None = None, segments: torch.Tensor | None = None,
+                       stream: torch.cuda.Stream | None = None):
+    """The records of ``emit_edge_records`` in source-grouped order with one
+    segment per member row (tessa_emit_edge_segments).  Returns ``(records,
+    count, segments, segment_count)``; ``segments`` is an int32 [capacity, 4]
+    tensor of {src, first record lo, hi, count}.  Synchronises the stream."""
+    dev = topk_ids.device
+    if out is None:
+        out = torch.empty((max(2 * layouts.output_len, 1), 4), dtype=torch.int32, device=dev)
+    if segments is None:
+        segments = torch.empty((max(layouts.output_len // max(k, 1), layouts.leaf_count, 1), 4), dtype=torch.int32,
+                               device=dev)
+    if out.dtype != torch.int32 or out.dim() != 2 or out.shape[1] != 4:
+        raise ValueError("out must be an int32 [capacity, 4] tensor")
+    if segments.dtype != torch.int32 or segments.dim() != 2 or segments.shape[1] != 4:
+        raise ValueError("segments must be an int32 [capacity, 4] tensor")
+    lb = N.LeafBatch(_ptr(layouts.members), _ptr(layouts.member_offsets), _ptr(layouts.member_counts),
+                     _ptr(layouts.output_offsets), layouts.leaf_count, layouts.max_leaf_rows, k, N.EXEC_MFMA, 0, 0)
+    sk = N.SketchView(_ptr(sketches), sketches.shape[0], sketches.shape[1], m_hash_bits)
+    count, nseg = C.c_uint64(0), C.c_uint64(0)
+    N.check(N.load().tessa_emit_edge_segments(_ptr(global_ids), global_ids.numel(), C.byref(lb), _ptr(topk_ids),
+                                              _ptr(topk_dists), C.byref(sk), _ptr(out), out.shape[0],
+                                              _ptr(segments), segments.shape[0], C.byref(count), C.byref(nseg),
+                                              _stream_ptr(stream)), "edge segments")
+    return out, int(count.value), segments, int(nseg.value)
+
+
 def records_to_numpy(records: torch.Tensor, count: int) -> np.ndarray:
     """First ``count`` records of an int32 [*, 4] record buffer as EDGE_RECORD_DTYPE."""
     raw = records[:count].contiguous().cpu().numpy()

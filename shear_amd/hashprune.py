@@ -71,6 +71,21 @@ class HashPruneReducer:
             raise ValueError(f"count {n} exceeds the {records.shape[0]} records given")
         N.check(self._lib.tessa_hashprune_insert(self._h, _ptr(records), n, _stream_ptr(stream)), "hashprune insert")
 
+    def insert_segments(self, records: torch.Tensor, segments: torch.Tensor, count: int | None = None,
+                        stream: torch.cuda.Stream | None = None) -> None:
+        """Merge records described by segments (``edges.emit_edge_segments``):
+        the first ``count`` rows of ``segments`` (int32 [n, 4]: src, first
+        record lo / hi, count) index into ``records`` (int32 [m, 4]).  Same
+        result as ``insert`` of the records.  Synchronises the stream."""
+        for t in (records, segments):
+            if t.dtype != torch.int32 or t.dim() != 2 or t.shape[1] != 4:
+                raise ValueError("records and segments must be int32 [n, 4] tensors")
+        n = segments.shape[0] if count is None else int(count)
+        if n > segments.shape[0]:
+            raise ValueError(f"count {n} exceeds the {segments.shape[0]} segments given")
+        N.check(self._lib.tessa_hashprune_insert_segments(self._h, _ptr(records), _ptr(segments), n,
+                                                          _stream_ptr(stream)), "hashprune insert segments")
+
     def clear(self, stream: torch.cuda.Stream | None = None) -> None:
         N.check(self._lib.tessa_hashprune_clear(self._h, _stream_ptr(stream)), "hashprune clear")
 

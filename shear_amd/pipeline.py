@@ -61,8 +61,6 @@ class GraphBuildParams:
     max_depth: int = 16
     random_seed: int = 42
     min_recurse_size: int = 64
-    insert_every: int = 16     # record batches per HashPrune insert (the reservoirs do not depend on batching)
-    insert_records: int = 1 << 28  # ... or as soon as this many records are pending
     multi_root: bool = True    # large D0 children partitioned together (tessa_session_partition_roots)
     roots_rows_per_run: int = 1 << 26  # rows of the children partitioned by one many-root run
     leaf_chunk_rows: int = 1 << 22     # leaf rows per leaf top-k / record batch of a many-root run
@@ -242,19 +240,22 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     sp = p.subtree_params()
     leaf_max = max(256, p.c_max)
     famp = max(p.fanout_second, 1)
-    pending = []
 
-    def consume(rec, cnt):
-        nonlocal pending
+    def emit(lay_gids, lay, k, ids, d):
+        # device reservoirs merge source-grouped segments in place; TierLift
+        # routes records by source, in any order
+        if tl is not None:
+            rec, cnt = E.emit_edge_records(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits)
+            return rec, cnt, None, 0
+        return E.emit_edge_segments(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits)
+
+    def consume(rec, cnt, segs, nseg):
         if tl is not None:
             q0 = time.perf_counter()
             tl.push(rec, int(cnt))
             st["push_s"] += time.perf_counter() - q0
-            return
-        pending.append(rec[:cnt])
-        if sum(int(r.shape[0]) for r in pending) >= p.insert_records or len(pending) >= p.insert_every:
-            hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
-            pending = []
+        else:
+            hp.insert_segments(rec, segs, nseg)
 
     sizes = np.diff(offs_h.astype(np.int64))
     children = [c for c in range(len(sizes)) if sizes[c] >= 2]  # a one-point child has no leaf pairs
@@ -270,7 +271,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     for gi, c in enumerate(large):
         group.append(c)
         if gi + 1 == len(large) or sum(int(sizes[g]) for g in group) + int(sizes[large[gi + 1]]) > p.roots_rows_per_run:
-            _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, rows, sketches, p, sp, st, consume, observer)
+            _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, rows, p, sp, st, emit, consume, observer)
             group = []
 
     # small children one by one
@@ -292,17 +293,14 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         lay = T.LeafLayouts(out.leaf_row_ids[: out.leaf_rows], out.leaf_starts[: out.leaf_count],
                             out.leaf_sizes[: out.leaf_count].to(torch.int32),
                             out.leaf_starts[: out.leaf_count] * out.k, leaf_max, out.leaf_rows * out.k)
-        rec, cnt = E.emit_edge_records(cg, lay, out.k, out.topk_ids, out.topk_dists, sketches, p.m_hash_bits)
+        rec, cnt, segs, nseg = emit(cg, lay, out.k, out.topk_ids, out.topk_dists)
         if observer is not None:
             observer(("child", c), cg, out, lay, rec, cnt)
-        consume(rec, cnt)
+        consume(rec, cnt, segs, nseg)
         st["records"] += int(cnt)
         st["leaves"] += out.leaf_count
         st["leaf_rows"] += out.leaf_rows
-        del rec, out, lay
-    if pending:
-        hp.insert(pending[0] if len(pending) == 1 else torch.cat(pending))
-    pending = []
+        del rec, segs, out, lay
     if tl is not None:
         torch.cuda.synchronize()
         w_emit = time.perf_counter()
@@ -350,8 +348,7 @@ class LeafChunk:
     topk_dists: torch.Tensor
 
 
-def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, sketches, p, sp, st, consume,
-                    observer):
+def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p, sp, st, emit, consume, observer):
     """One many-root partition over the D0 children in ``group``, then the
     leaf top-k and record emission of its leaves in chunks."""
     dev = sq8.codes.device
@@ -395,14 +392,14 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, s
         e1.record()
         T.raise_on_overflow(ctr, "leaf top-k")
         st["leaf_ms"] += e0.elapsed_time(e1)
-        rec, cnt = E.emit_edge_records(gids, lay, k, ids, d, sketches, p.m_hash_bits)
+        rec, cnt, segs, nseg = emit(gids, lay, k, ids, d)
         if observer is not None:
             chunk = LeafChunk(ro.leaf_rows[r0:r1], off - r0, ro.leaf_sizes[l0:l1], l1 - l0, r1 - r0, k, ids, d)
             observer(("roots", st["runs"] - 1, l0), None, chunk, lay, rec, cnt)
             del chunk
-        consume(rec, cnt)
+        consume(rec, cnt, segs, nseg)
         st["records"] += int(cnt)
         st["leaves"] += l1 - l0
         st["leaf_rows"] += r1 - r0
-        del rec, ids, d, lay, off
+        del rec, segs, ids, d, lay, off
         l0 = l1

@@ -1,0 +1,105 @@
+"""Source-grouped record emission (tessa_emit_edge_segments) and the HashPrune
+segment insert (tessa_hashprune_insert_segments).
+
+  * per leaf, the grouped records are the reference-order records
+    (tessa_emit_edge_records) as a multiset; every segment's records carry
+    its source, the segments tile the records, one per member row;
+  * the reservoirs after inserting by segments equal those after inserting
+    the records (C2-shaped leaves, and replicated points across leaves with
+    hub sources that take the LDS merge), and equal the oracle's."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import dev_u32, require_gpu, to_dev_sq8
+from shear_amd import edges as E
+from shear_amd import hashprune as H
+from shear_amd import tessa as T
+
+pytestmark = pytest.mark.gpu
+
+
+def _leaves(orc, n_points, leaf_sizes, dim, seed, replicate=0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n_points, dim)).astype(np.float32)
+    codes, scales, norms = orc.quantize(x)
+    members, offs, counts = [], [], []
+    at = 0
+    for n in leaf_sizes:
+        rows = np.sort(rng.choice(n_points, n, replace=False)).astype(np.uint32)
+        members.append(rows)
+        offs.append(at)
+        counts.append(n)
+        at += n
+    return codes, scales, norms, np.concatenate(members), np.array(offs), np.array(counts)
+
+
+def _run(orc, gpu, n_points, leaf_sizes, dim, seed, k=32, m_bits=12):
+    codes, scales, norms, members, offs, counts = _leaves(orc, n_points, leaf_sizes, dim, seed)
+    sq8 = to_dev_sq8(codes, scales, norms, dim)
+    gids = dev_u32(np.arange(n_points))
+    lay = T.LeafLayouts.from_host(members, offs, counts, k, gpu)
+    ids, d, _ = T.leaf_topk(sq8, gids, lay, k)
+    rng = np.random.default_rng(seed + 1)
+    sk = torch.from_numpy(rng.standard_normal((n_points, m_bits)).astype(np.float32)).to(gpu)
+    rec, cnt = E.emit_edge_records(gids, lay, k, ids, d, sk, m_bits)
+    grec, gcnt, segs, nseg = E.emit_edge_segments(gids, lay, k, ids, d, sk, m_bits)
+    return rec, cnt, grec, gcnt, segs, nseg, counts
+
+
+def _sorted_records(r):
+    v = np.ascontiguousarray(r).view(np.uint8).reshape(-1, 16).view("V16").ravel()
+    return np.sort(v)
+
+
+@pytest.mark.parametrize("n_points,leaf_sizes,dim", [
+    (8192, [1024] * 8, 128),                      # C2-shaped: each point in one leaf
+    (3000, [700, 2048, 33, 2, 1, 1500, 900], 64),  # ragged leaves, replicated points, a one-row leaf
+])
+def test_grouped_records_and_segments(gpu_dev, orc, n_points, leaf_sizes, dim):
+    rec, cnt, grec, gcnt, segs, nseg, counts = _run(orc, gpu_dev, n_points, leaf_sizes, dim, 5)
+    assert cnt == gcnt
+    assert nseg == int(np.sum(counts))
+    a = E.records_to_numpy(rec, cnt)
+    b = E.records_to_numpy(grec, gcnt)
+    assert np.array_equal(_sorted_records(a), _sorted_records(b)), "grouped records differ as a multiset"
+    sg = segs[:nseg].cpu().numpy().view(np.uint32)
+    first = sg[:, 1].astype(np.uint64) | (sg[:, 2].astype(np.uint64) << 32)
+    order = np.argsort(first, kind="stable")
+    covered = 0
+    for i in order:
+        src, c = int(sg[i, 0]), int(sg[i, 3])
+        f = int(first[i])
+        if c == 0:
+            continue
+        assert f == covered, "segments must tile the records"
+        assert np.all(b["src"][f:f + c] == src)
+        covered += c
+    assert covered == gcnt
+
+
+@pytest.fixture(scope="module")
+def gpu_dev():
+    return require_gpu()
+
+
+@pytest.mark.parametrize("n_points,leaf_sizes,dim,l_max", [
+    (8192, [1024] * 8, 128, 64),
+    (1500, [1400, 1400, 1300, 900, 1450, 1200], 32, 16),  # points in up to six leaves: large merges
+])
+def test_segment_insert_equals_record_insert(gpu_dev, orc, n_points, leaf_sizes, dim, l_max):
+    rec, cnt, grec, gcnt, segs, nseg, _ = _run(orc, gpu_dev, n_points, leaf_sizes, dim, 9)
+    with H.HashPruneReducer(n_points, l_max, gpu_dev) as a, H.HashPruneReducer(n_points, l_max, gpu_dev) as b:
+        a.insert(rec, cnt)
+        b.insert_segments(grec, segs, nseg)
+        # a second batch into the same reservoirs (existing slots + new segments)
+        a.insert(rec, cnt)
+        b.insert_segments(grec, segs, nseg)
+        ta, _, da, ca = a.slots()
+        tb, _, db, cb = b.slots()
+    assert torch.equal(ca, cb) and torch.equal(ta, tb) and torch.equal(da, db)
+    wt, _, _, wc = orc.hashprune_reduce(n_points, l_max, E.records_to_numpy(rec, cnt))
+    assert np.array_equal(cb.cpu().numpy().view(np.uint32), wc)
+    tbn = tb.cpu().numpy().view(np.uint32)
+    for p in range(n_points):
+        assert np.array_equal(tbn[p, : wc[p]], wt[p, : wc[p]])
