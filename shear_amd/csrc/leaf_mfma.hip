@@ -110,11 +110,11 @@ constexpr uint32_t kLdsBudget = 160u * 1024u;
 // LDS: two column tiles and each wave's 4 KB accumulator scratch, then the
 // leaf's member ids, scales and norms, and 64 bytes of scalars (each wave's
 // norm range).
-__host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes) {
-    return 2u * tile_bytes + kWaves * 16u * 64u * 4u;
+__host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes, uint32_t nbuf) {
+    return nbuf * tile_bytes + kWaves * 16u * 64u * 4u;
 }
-__host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t cols_cap) {
-    return union_bytes(tile_bytes) + cols_cap * 12u + 64u;
+__host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t nbuf, uint32_t cols_cap) {
+    return union_bytes(tile_bytes, nbuf) + cols_cap * 12u + 64u;
 }
 
 // Compile-time loops: f(std::integral_constant<int, I>) for I in [B, E).
@@ -246,14 +246,15 @@ __device__ __forceinline__ float pair_kth(const float (&a)[N], int rsel) {
     return res;
 }
 
-template <int KS>
+// NB column-tile buffers in LDS (2 or 4); a barrier every NB/2 positions.
+template <int KS, int NB>
 __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t per_xcd) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // Runtime layout: tiles x2 | scratch | members | scales | norms | misc.
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     int8_t *tile = reinterpret_cast<int8_t *>(smem);
-    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + union_bytes(L::kTileBytes));
+    uint32_t *mem_lds = reinterpret_cast<uint32_t *>(smem + union_bytes(L::kTileBytes, NB));
     float *cs_lds = reinterpret_cast<float *>(mem_lds + cols_cap);
     float *cn_lds = cs_lds + cols_cap;
     uint32_t *misc = reinterpret_cast<uint32_t *>(cn_lds + cols_cap);
@@ -450,9 +451,8 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const uint32_t nA = (ntiles + sstride - 1u) / sstride;
         const uint32_t S = nA + ntiles;
         auto tile_of = [&](uint32_t i) { return i < nA ? i * sstride : i - nA; };
-        int8_t *const buf0 = tile;
-        int8_t *const buf1 = tile + L::kTileBytes;
-        int *const scr = reinterpret_cast<int *>(tile + 2 * L::kTileBytes) + wave * (16u * 64u);
+        constexpr uint32_t kAhead = NB / 2;  // positions between a tile's store and its use
+        int *const scr = reinterpret_cast<int *>(tile + NB * L::kTileBytes) + wave * (16u * 64u);
 
         // Phase A epilogue units (148): per group of 4 candidates one LDS read
         // of their scales and norms and 4 exact distances (20), the 80
@@ -578,28 +578,35 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         };
 
         uint32_t pend_mask = 0u, pend_tile = 0u;
-        // Start of position i: the barrier, the tile of position i+1 from
-        // registers to the free LDS buffer, the held mask's drain, then the
-        // prefetch of position i+2.  Position i reads buffer i&1.
+        // Position i reads buffer i % NB.  Start of position i: a barrier
+        // when i % (NB/2) == 0, the tile of position i + NB/2 from registers
+        // to its buffer, the held mask's drain, then the prefetch of position
+        // i + NB/2 + 1.  A tile stored at position j is read at j + NB/2,
+        // after the next barrier; the buffer it overwrites was last read at
+        // j - NB/2, before the barrier every wave has passed.
+        auto bufp = [&](uint32_t i) -> int8_t * { return tile + (i % NB) * L::kTileBytes; };
         auto head = [&](uint32_t i) {
-            lds_barrier();
-            if (i + 1u < S) store_tile((i & 1u) ? buf0 : buf1);
+            if (i % kAhead == 0u) lds_barrier();
+            if (i + kAhead < S) store_tile(bufp(i + kAhead));
             drain(pend_mask, pend_tile);
             pend_mask = 0u;
-            if (i + 2u < S) issue_tile();  // tile of position i+2, prepared by the previous block
+            if (i + kAhead + 1u < S) issue_tile();  // prepared by the previous block
         };
-        auto src_of = [&](uint32_t i) -> const int8_t * { return (i & 1u) ? buf1 : buf0; };
+        auto src_of = [&](uint32_t i) -> const int8_t * { return bufp(i); };
 
-        // prologue: position 0 in LDS buffer 0, position 1 in registers, the
-        // ids of position 2 prepared (S >= 2: nA >= 1 and ntiles >= 1)
-        prep_tile(tile_of(0));
+        // prologue: positions 0 .. NB/2-1 in their LDS buffers, position
+        // NB/2 in registers, the ids of position NB/2 + 1 prepared (S >= 2:
+        // nA >= 1 and ntiles >= 1)
+        for (uint32_t t0 = 0; t0 < kAhead && t0 < S; ++t0) {
+            prep_tile(tile_of(t0));
+            issue_tile();
+            store_tile(bufp(t0));
+        }
+        prep_tile(tile_of(kAhead < S ? kAhead : S - 1u));
         issue_tile();
-        store_tile(buf0);
-        prep_tile(tile_of(1));
-        issue_tile();
-        prep_tile(tile_of(S > 2u ? 2u : S - 1u));
-        // each block prepares the ids of the tile three positions ahead
-        auto prep_for = [&](uint32_t i) { prep_t = tile_of(i + 3u < S ? i + 3u : S - 1u); };
+        prep_tile(tile_of(kAhead + 1u < S ? kAhead + 1u : S - 1u));
+        // each block prepares the ids of the tile NB/2 + 2 positions ahead
+        auto prep_for = [&](uint32_t i) { prep_t = tile_of(i + kAhead + 2u < S ? i + kAhead + 2u : S - 1u); };
         // accP holds the accumulators of the latest position; each block
         // computes position i into accQ/accP alternately while the epilogue
         // of position i-1 runs on the other.
@@ -699,13 +706,17 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     using L = Layout<KS>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kLdsBudget) != hipSuccess ||
+            hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS, 4>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)kLdsBudget) != hipSuccess)
             return -1;
         attr_set = true;
     }
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
-    const uint32_t lds = lds_bytes(L::kTileBytes, cols_cap);
+    // four tile buffers (a barrier every second position) when they fit
+    const bool four = lds_bytes(L::kTileBytes, 4, cols_cap) <= kLdsBudget;
+    const uint32_t lds = lds_bytes(L::kTileBytes, four ? 4 : 2, cols_cap);
     if (lds > kLdsBudget) return -4;
     if (p.item_count == 0) return 0;
     if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x7fffffffull) return -2;
@@ -714,7 +725,10 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     // multiple of the 8 XCDs; XCD x walks items [x*per_xcd, (x+1)*per_xcd)
     uint32_t grid = 1024u;
     if (per_xcd * 8u < grid) grid = per_xcd * 8u;
-    hipLaunchKernelGGL(leaf_mfma_kernel<KS>, dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
+    if (four)
+        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 4>), dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
+    else
+        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 2>), dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
