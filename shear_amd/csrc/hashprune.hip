@@ -22,6 +22,8 @@
 //      each hash's best first; when more than l_max hashes remain, a sort of
 //      those by the total order gives the l_max-th as a threshold; the
 //      survivors, in ascending hash order, are the new slots.
+#include <hipcub/hipcub.hpp>
+
 #include "hashprune_kernels.h"
 
 namespace tessa {
@@ -561,30 +563,35 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_kernel(const uint4 
 
 // ---- segment mode: records left where the emitter put them ------------------
 // A segment {src, first record lo/hi, count} names a run of records of one
-// source.  Segments are grouped by source (count, scan, scatter of segment
-// indices: atomics per segment, not per record), then each source's
-// segments are merged together, reading its records in place.
+// source.  The batch's segments are sorted by source (radix sort of the
+// segment indices), each run of equal sources becomes one active source, and
+// the merges walk the active sources only, reading each one's records in
+// place: the work follows the batch size, with no pass over all points and
+// no atomics per record.
 
-__global__ void hp_seg_count_kernel(const uint4 *segs, uint64_t nseg, uint32_t num_points, uint32_t *bucket,
-                                    uint64_t *status) {
+__global__ void hp_seg_keys_kernel(const uint4 *segs, uint64_t nseg, uint32_t num_points, uint32_t *keys,
+                                   uint32_t *vals, uint64_t *status) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x) {
         const uint4 g = segs[i];
-        if (g.w == 0u) continue;
-        if (g.x >= num_points) {
-            // the first record of the segment carries the bad source
-            atomicMin((unsigned long long *)status, (unsigned long long)(((uint64_t)g.z << 32) | g.y));
-            continue;
-        }
-        atomicAdd(&bucket[g.x], 1u);
+        const bool bad = g.w != 0u && g.x >= num_points;
+        // the first record of the segment carries the bad source
+        if (bad) atomicMin((unsigned long long *)status, (unsigned long long)(((uint64_t)g.z << 32) | g.y));
+        keys[i] = (g.w == 0u || bad) ? num_points : g.x;  // empty and bad segments sort last, unused
+        vals[i] = (uint32_t)i;
     }
 }
 
-__global__ void hp_seg_scatter_kernel(const uint4 *segs, uint64_t nseg, uint32_t num_points, uint32_t *bucket,
-                                      const uint32_t *offsets, uint32_t *seg_grouped) {
+// Run heads of the sorted keys -> the active sources (src, first position);
+// their order is not fixed (each source is merged independently).
+__global__ void hp_seg_runs_kernel(const uint32_t *keys, uint64_t nseg, uint32_t num_points, uint32_t *run_src,
+                                   uint32_t *run_start, uint32_t *run_count) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint4 g = segs[i];
-        if (g.w == 0u || g.x >= num_points) continue;
-        seg_grouped[offsets[g.x] + atomicSub(&bucket[g.x], 1u) - 1u] = (uint32_t)i;
+        const uint32_t k = keys[i];
+        if (k < num_points && (i == 0 || keys[i - 1] != k)) {
+            const uint32_t a = atomicAdd(run_count, 1u);
+            run_src[a] = k;
+            run_start[a] = (uint32_t)i;
+        }
     }
 }
 
@@ -609,7 +616,6 @@ __device__ uint32_t seg_merge(const uint4 *records, uint64_t *slot_keys, uint16_
             if (e >= n_old && e - n_old >= ps && e - n_old < ps + cs) addr[q] = fs + (e - n_old - ps);
         }
     }
-    (void)n_new;
     auto fetch = [&](int q, uint32_t) -> uint4 {
         uint64_t a = addr[0];
 #pragma unroll
@@ -619,24 +625,38 @@ __device__ uint32_t seg_merge(const uint4 *records, uint64_t *slot_keys, uint16_
     return reg_merge_f<E>(slot_keys, slot_hash, n_old, n_new, fetch, l_max, lane, slot_keys, slot_hash);
 }
 
-// Register merges of sources with at most 64 segments and kHpRegMax
-// candidates.  Lane s < nseg holds segment s; a new record t is found by its
-// segment's exclusive prefix.
+// The segments of active source a: sorted positions [start, start + ns);
+// lanes read the keys after `start` and count the leading run equal to src
+// (ns > 64 means "more than 64").
+__device__ __forceinline__ uint32_t run_length64(const uint32_t *keys, uint64_t nseg, uint32_t start, uint32_t src,
+                                                 uint32_t lane) {
+    const uint64_t at = (uint64_t)start + lane;
+    const bool eq = at < nseg && keys[at] == src;
+    const uint64_t m = ~__ballot(eq);
+    return m ? (uint32_t)__builtin_ctzll(m) : 65u;
+}
+
+// Register merges of active sources with at most 64 segments and kHpRegMax
+// candidates.
 __global__ __launch_bounds__(kHpThreads) void hp_merge_small_seg_kernel(const uint4 *records, const uint4 *segs,
-                                                                        const uint32_t *seg_grouped,
-                                                                        const uint32_t *offsets, uint32_t num_points,
-                                                                        uint32_t l_max, uint64_t *slot_keys,
-                                                                        uint16_t *slot_hash, uint32_t *slot_count) {
+                                                                        const uint32_t *keys, const uint32_t *vals,
+                                                                        uint64_t nseg, const uint32_t *run_src,
+                                                                        const uint32_t *run_start,
+                                                                        const uint32_t *run_count, uint32_t l_max,
+                                                                        uint64_t *slot_keys, uint16_t *slot_hash,
+                                                                        uint32_t *slot_count) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t waves = gridDim.x * kHpWaves;
-    for (uint32_t src = blockIdx.x * kHpWaves + (threadIdx.x >> 6); src < num_points; src += waves) {
-        const uint32_t s0 = offsets[src];
-        const uint32_t ns = offsets[src + 1] - s0;
-        if (ns == 0u || ns > 64u) continue;  // none, or hp_merge_large_seg_kernel
+    const uint32_t na = *run_count;
+    for (uint32_t a = blockIdx.x * kHpWaves + (threadIdx.x >> 6); a < na; a += waves) {
+        const uint32_t src = run_src[a];
+        const uint32_t s0 = run_start[a];
+        const uint32_t ns = run_length64(keys, nseg, s0, src, lane);
+        if (ns > 64u) continue;  // hp_merge_large_seg_kernel
         uint32_t cnt = 0;
         uint64_t first = 0;
         if (lane < ns) {
-            const uint4 g = segs[seg_grouped[s0 + lane]];
+            const uint4 g = segs[vals[s0 + lane]];
             cnt = g.w;
             first = ((uint64_t)g.z << 32) | g.y;
         }
@@ -659,26 +679,29 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_small_seg_kernel(const ui
     }
 }
 
-// The other sources: their segments' records staged in LDS, merged kHpMergeCap
-// candidates at a time.
+// The other active sources: their segments' records staged in LDS, merged
+// kHpMergeCap candidates at a time.
 __global__ __launch_bounds__(kHpThreads) void hp_merge_large_seg_kernel(const uint4 *records, const uint4 *segs,
-                                                                        const uint32_t *seg_grouped,
-                                                                        const uint32_t *offsets, uint32_t num_points,
-                                                                        uint32_t l_max, uint64_t *slot_keys,
-                                                                        uint16_t *slot_hash, uint32_t *slot_count) {
+                                                                        const uint32_t *keys, const uint32_t *vals,
+                                                                        uint64_t nseg, const uint32_t *run_src,
+                                                                        const uint32_t *run_start,
+                                                                        const uint32_t *run_count, uint32_t l_max,
+                                                                        uint64_t *slot_keys, uint16_t *slot_hash,
+                                                                        uint32_t *slot_count) {
     __shared__ HpWaveLds lds[kHpWaves];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     HpWaveLds &w = lds[wave];
     const uint32_t waves = gridDim.x * kHpWaves;
-    for (uint32_t src = blockIdx.x * kHpWaves + wave; src < num_points; src += waves) {
-        const uint32_t s0 = offsets[src];
-        const uint32_t ns = offsets[src + 1] - s0;
-        if (ns == 0u) continue;
+    const uint32_t na = *run_count;
+    for (uint32_t a = blockIdx.x * kHpWaves + wave; a < na; a += waves) {
+        const uint32_t src = run_src[a];
+        const uint32_t s0 = run_start[a];
+        const uint32_t ns64 = run_length64(keys, nseg, s0, src, lane);
         uint32_t n_old = slot_count[src];
-        if (ns <= 64u) {
+        if (ns64 <= 64u) {
             // the small kernel's case unless it holds more than kHpRegMax candidates
-            const uint32_t cnt = lane < ns ? segs[seg_grouped[s0 + lane]].w : 0u;
+            const uint32_t cnt = lane < ns64 ? segs[vals[s0 + lane]].w : 0u;
             uint32_t n_new;
             (void)wave_excl_scan(cnt, lane, n_new);
             if (n_old + n_new <= kHpRegMax) continue;
@@ -691,8 +714,8 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_seg_kernel(const ui
         __builtin_amdgcn_wave_barrier();
         uint32_t fill = 0;  // candidates staged after the reservoir
         bool merged = false;
-        for (uint32_t si = 0; si < ns; ++si) {
-            const uint4 g = segs[seg_grouped[s0 + si]];
+        for (uint64_t si = s0; si < nseg && keys[si] == src; ++si) {
+            const uint4 g = segs[vals[si]];
             const uint64_t first = ((uint64_t)g.z << 32) | g.y;
             uint32_t used = 0;
             while (used < g.w) {
@@ -729,6 +752,42 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_large_seg_kernel(const ui
         if (lane == 0) slot_count[src] = n_old;
         __builtin_amdgcn_wave_barrier();
     }
+}
+
+// Segment workspace layout: keys in/out, values in/out, run sources and
+// starts (nseg each, u32), the run count, then the radix sort's temporary.
+struct SegWs {
+    uint32_t *keys_in, *keys_out, *vals_in, *vals_out, *run_src, *run_start, *run_count;
+    void *temp;
+    size_t temp_bytes;
+};
+size_t seg_align(size_t x) { return (x + 255) & ~(size_t)255; }
+int key_bits(uint32_t num_points) {
+    int b = 1;
+    while (b < 32 && ((uint64_t)1 << b) <= num_points) ++b;  // keys go up to num_points (unused segments)
+    return b;
+}
+size_t seg_sort_temp(uint64_t nseg, uint32_t num_points) {
+    size_t bytes = 0;
+    hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+                                       (const uint32_t *)nullptr, (uint32_t *)nullptr, (int)nseg, 0,
+                                       key_bits(num_points));
+    return bytes;
+}
+SegWs seg_ws_layout(void *base, uint64_t nseg, uint32_t num_points) {
+    SegWs w{};
+    char *p = static_cast<char *>(base);
+    const size_t a = seg_align(nseg * 4);
+    w.keys_in = reinterpret_cast<uint32_t *>(p);
+    w.keys_out = reinterpret_cast<uint32_t *>(p + a);
+    w.vals_in = reinterpret_cast<uint32_t *>(p + 2 * a);
+    w.vals_out = reinterpret_cast<uint32_t *>(p + 3 * a);
+    w.run_src = reinterpret_cast<uint32_t *>(p + 4 * a);
+    w.run_start = reinterpret_cast<uint32_t *>(p + 5 * a);
+    w.run_count = reinterpret_cast<uint32_t *>(p + 6 * a);
+    w.temp = p + 6 * a + 256;
+    w.temp_bytes = seg_sort_temp(nseg, num_points);
+    return w;
 }
 
 __global__ void hp_export_kernel(const uint64_t *slot_keys, const uint16_t *slot_hash, const uint32_t *slot_count,
@@ -787,25 +846,34 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+uint64_t hashprune_segment_workspace_bytes(uint64_t nseg, uint32_t num_points) {
+    return 6 * seg_align((nseg ? nseg : 1) * 4) + 256 + seg_sort_temp(nseg ? nseg : 1, num_points) + 256;
+}
+
 int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, const uint4 *segs, uint64_t nseg,
                                      hipStream_t stream) {
     const uint32_t n = s.num_points;
     hipLaunchKernelGGL(hp_status_init, dim3(1), dim3(1), 0, stream, s.status);
     if (nseg == 0 || n == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
-    hipLaunchKernelGGL(hp_seg_count_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs, nseg, n,
-                       s.bucket, s.status);
-    const uint32_t nb = (n + kScanBlock - 1) / kScanBlock;
-    hipLaunchKernelGGL(hp_scan_reduce, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums);
-    hipLaunchKernelGGL(hp_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, s.block_sums, nb, s.offsets, n);
-    hipLaunchKernelGGL(hp_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums, s.offsets);
-    hipLaunchKernelGGL(hp_seg_scatter_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs, nseg, n,
-                       s.bucket, s.offsets, s.seg_grouped);
+    SegWs w = seg_ws_layout(s.seg_ws, nseg, n);
+    hipLaunchKernelGGL(hp_seg_keys_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs, nseg, n,
+                       w.keys_in, w.vals_in, s.status);
+    size_t tb = w.temp_bytes;
+    if (hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.keys_in, w.keys_out, w.vals_in, w.vals_out, (int)nseg, 0,
+                                           key_bits(n), stream) != hipSuccess)
+        return -1;
+    hipLaunchKernelGGL(hp_fill_u32, dim3(1), dim3(64), 0, stream, w.run_count, (uint64_t)1, 0u);
+    hipLaunchKernelGGL(hp_seg_runs_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, w.keys_out, nseg,
+                       n, w.run_src, w.run_start, w.run_count);
     // large first (a merge never shrinks a reservoir, so the small kernel then
     // skips what the large kernel merged)
-    hipLaunchKernelGGL(hp_merge_large_seg_kernel, dim3(grid_for(n, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
-                       records, segs, s.seg_grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
-    hipLaunchKernelGGL(hp_merge_small_seg_kernel, dim3(grid_for(n, kHpWaves, 8192)), dim3(kHpThreads), 0, stream,
-                       records, segs, s.seg_grouped, s.offsets, n, s.l_max, s.slot_keys, s.slot_hash, s.slot_count);
+    const uint32_t ga = grid_for(nseg, kHpWaves, 8192);
+    hipLaunchKernelGGL(hp_merge_large_seg_kernel, dim3(grid_for(nseg, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
+                       records, segs, w.keys_out, w.vals_out, nseg, w.run_src, w.run_start, w.run_count, s.l_max,
+                       s.slot_keys, s.slot_hash, s.slot_count);
+    hipLaunchKernelGGL(hp_merge_small_seg_kernel, dim3(ga), dim3(kHpThreads), 0, stream, records, segs, w.keys_out,
+                       w.vals_out, nseg, w.run_src, w.run_start, w.run_count, s.l_max, s.slot_keys, s.slot_hash,
+                       s.slot_count);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -25,15 +25,17 @@ struct HashPruneState {
     uint4 *grouped = nullptr;       // the batch's records grouped by source
     uint64_t grouped_capacity = 0;
     uint64_t *status = nullptr;     // [0] first record with src >= num_points (UINT64_MAX: none)
-    uint32_t *seg_grouped = nullptr; // segment mode: the batch's segment indices grouped by source
-    uint64_t seg_grouped_capacity = 0;
+    void *seg_ws = nullptr;          // segment mode workspace (hashprune_segment_workspace_bytes)
+    uint64_t seg_ws_bytes = 0;
 };
 
 // Groups `count` records by source and merges each source's new candidates
 // into its reservoir.  Returns 0, or -1 when a launch failed.
 int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t count, hipStream_t stream);
 // The same for records described by segments {src, first lo, first hi, count}
-// (records left in place; segments grouped by source instead of records).
+// (records left in place; the segments, not the records, are sorted by
+// source, so the work is proportional to the batch, not to num_points).
+uint64_t hashprune_segment_workspace_bytes(uint64_t nseg, uint32_t num_points);
 int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, const uint4 *segs, uint64_t nseg,
                                      hipStream_t stream);
 // Zeroes the per-source counters (all reservoirs empty).

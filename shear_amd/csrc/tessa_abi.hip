@@ -1917,7 +1917,7 @@ void free_hashprune(tessa_hashprune *hp) {
     auto &s = hp->st;
     for (void *ptr : {(void *)s.slot_keys, (void *)s.slot_hash, (void *)s.slot_count, (void *)s.bucket,
                       (void *)s.offsets, (void *)s.block_sums, (void *)s.grouped, (void *)s.status,
-                      (void *)s.seg_grouped})
+                      (void *)s.seg_ws})
         if (ptr) (void)hipFree(ptr);
     delete hp;
 }
@@ -2026,19 +2026,20 @@ tessa_status tessa_hashprune_insert_segments(tessa_hashprune *hp, const tessa_ed
     if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
     if (segment_count && (!records || !segments))
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune: null records or segments");
-    if (segment_count >= 0xffffffffull)
-        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: %llu segments in one batch (limit 2^32-2)",
+    if (segment_count >= 0x7fffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: %llu segments in one batch (limit 2^31-2)",
                            (unsigned long long)segment_count);
     auto &s = hp->st;
     hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-    if (segment_count > s.seg_grouped_capacity) {
+    const uint64_t need = tessa::hashprune_segment_workspace_bytes(segment_count, s.num_points);
+    if (need > s.seg_ws_bytes) {
         TESSA_HIP_TRY(hipStreamSynchronize(hs));
-        if (s.seg_grouped) TESSA_HIP_TRY(hipFree(s.seg_grouped));
-        s.seg_grouped = nullptr;
-        s.seg_grouped_capacity = 0;
-        tessa_status st = hp_alloc((void **)&s.seg_grouped, segment_count * 4, "hashprune grouped segments");
+        if (s.seg_ws) TESSA_HIP_TRY(hipFree(s.seg_ws));
+        s.seg_ws = nullptr;
+        s.seg_ws_bytes = 0;
+        tessa_status st = hp_alloc(&s.seg_ws, need, "hashprune segment workspace");
         if (st.code) return st;
-        s.seg_grouped_capacity = segment_count;
+        s.seg_ws_bytes = need;
     }
     if (tessa::launch_hashprune_insert_segments(s, reinterpret_cast<const uint4 *>(records),
                                                 reinterpret_cast<const uint4 *>(segments), segment_count, hs) != 0)

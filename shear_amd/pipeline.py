@@ -236,7 +236,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     else:
         hp = H.HashPruneReducer(rows, p.l_max, dev)
     st = {"push_s": 0.0, "part_ms": 0.0, "leaf_ms": 0.0, "records": 0, "leaves": 0, "leaf_rows": 0,
-          "retries": 0, "runs": 0}
+          "retries": 0, "runs": 0, "emit_s": 0.0, "reduce_s": 0.0}
     sp = p.subtree_params()
     leaf_max = max(256, p.c_max)
     famp = max(p.fanout_second, 1)
@@ -320,7 +320,8 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
               "children": len(children), "multi_root_children": len(large), "partition_runs": st["runs"],
               "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(st["part_ms"], 2),
               "leaf_ms": round(st["leaf_ms"], 2), "leaves": st["leaves"], "leaf_rows": st["leaf_rows"],
-              "edge_records": st["records"], "terminal_depth_retries": st["retries"]}
+              "edge_records": st["records"], "terminal_depth_retries": st["retries"],
+              "emit_ms": round(st["emit_s"] * 1e3, 2), "reduce_ms": round(st["reduce_s"] * 1e3, 2)}
     if tl is not None:
         stages["tierlift"] = tl_stats
     if p.gpu_workspace_budget_bytes:
@@ -392,12 +393,17 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p
         e1.record()
         T.raise_on_overflow(ctr, "leaf top-k")
         st["leaf_ms"] += e0.elapsed_time(e1)
+        q0 = time.perf_counter()
         rec, cnt, segs, nseg = emit(gids, lay, k, ids, d)
+        q1 = time.perf_counter()
         if observer is not None:
             chunk = LeafChunk(ro.leaf_rows[r0:r1], off - r0, ro.leaf_sizes[l0:l1], l1 - l0, r1 - r0, k, ids, d)
             observer(("roots", st["runs"] - 1, l0), None, chunk, lay, rec, cnt)
             del chunk
+        q2 = time.perf_counter()
         consume(rec, cnt, segs, nseg)
+        st["emit_s"] += q1 - q0
+        st["reduce_s"] += time.perf_counter() - q2
         st["records"] += int(cnt)
         st["leaves"] += l1 - l0
         st["leaf_rows"] += r1 - r0
