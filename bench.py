@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--subtree-rows", type=int, default=10_000_000,
                     help="rows of the in-HBM subtree leg (C3: 10M x 768, leaves <= 2048, fanout 2, k=32)")
     ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
+    ap.add_argument("--no-build", action="store_true", help="skip the C3 full-build leg")
+    ap.add_argument("--build-rows", type=int, default=10_000_000,
+                    help="rows of the C3 full-build leg (BASELINE configs[2]: 10,000,000)")
     ap.add_argument("--no-hashprune", action="store_true", help="skip the HashPrune reservoir leg")
     ap.add_argument("--no-recall", action="store_true", help="skip the end-to-end graph build + recall leg")
     ap.add_argument("--no-edges", action="store_true",
@@ -248,12 +251,126 @@ def main() -> int:
         result["graph_recall"] = recall_leg(dev, check=not args.no_cpu_baseline)
         torch.cuda.empty_cache()
 
-    if not args.no_subtree:
+    if not args.no_subtree or not args.no_build:
         del out_ids, out_d, sq8, gids, lay
         torch.cuda.empty_cache()
+    if not args.no_subtree:
         result["subtree"] = subtree_leg(args.subtree_rows, dev, check=not args.no_cpu_baseline)
+        torch.cuda.empty_cache()
+    if not args.no_build:
+        result["build_c3"] = build_leg(args.build_rows, dev, check=not args.no_cpu_baseline)
+        torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
+
+
+class _LeafSampler:
+    """Build observer of the bench's untimed first C3 build: keeps 4 leaves of
+    each of the first `calls` record batches (point ids, top-k ids and f32
+    distances) for the oracle check after the build."""
+
+    def __init__(self, calls=3):
+        self.calls, self.seen, self.leaves = calls, 0, []
+
+    def __call__(self, tag, cg, out, lay, rec, cnt):
+        import numpy as np
+
+        self.seen += 1
+        if self.seen > self.calls:
+            return
+        lc = out.leaf_count
+        starts = out.leaf_starts[:lc].cpu().numpy()
+        sz = out.leaf_sizes[:lc].cpu().numpy()
+        li = out.leaf_row_ids[: out.leaf_rows].cpu().numpy().view(np.uint32)
+        g = li if cg is None else cg.cpu().numpy().view(np.uint32)[li]
+        ids = out.topk_ids[: out.leaf_rows * out.k].cpu().numpy().view(np.uint32).reshape(-1, out.k)
+        dd = out.topk_dists[: out.leaf_rows * out.k].cpu().numpy().reshape(-1, out.k)
+        for leaf in np.linspace(0, lc - 1, 4).astype(int):
+            a, n = int(starts[leaf]), int(sz[leaf])
+            self.leaves.append((g[a:a + n].copy(), ids[a:a + n].copy(), dd[a:a + n].copy()))
+
+
+def build_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(64, 256)):
+    """BASELINE configs[2] (C3) built end to end on the GPU: rows x 768 unit
+    vectors (1,000 components, sigma 0.25, 5 % outliers, seed 2), SQ8, global
+    D0 (fanout 2), many-root subtree runs (fanout 2, leaves <= 2048, k 32),
+    source-grouped records, HashPrune (R 64), `_mem.index`.  Two builds: the
+    first (untimed for the figure: it also pays one-time set-up) samples 12
+    leaves for the oracle check, the second runs with no observer and is the
+    reported build time.  Recall@10 of 1,000 held-out queries against exact
+    ground truth on the second build's graph."""
+    import numpy as np
+    import torch
+
+    from shear_amd import datagen
+    from shear_amd import graph as G
+    from shear_amd import pipeline as P
+    from shear_amd import tessa as T
+
+    spec = datagen.c3_spec(rows)
+    x = spec.rows(dev)
+    dim = x.shape[1]
+    p = P.GraphBuildParams(c_max=2048)
+    sk = (x @ torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev).t()).contiguous()
+    lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
+    sq8 = T.quantize_sq_int8_matrix(x)
+    torch.cuda.synchronize()
+    sampler = _LeafSampler() if check else None
+    first = P.build_graph_sq8(sq8, sk, lead, p, observer=sampler)
+    first_s, first_image = first.build_s, first.image
+    del first
+    torch.cuda.empty_cache()
+    built = P.build_graph_sq8(sq8, sk, lead, p)
+    same = bool(torch.equal(first_image, built.image))
+    del first_image
+    log(f"C3 build: {built.build_s:.3f} s ({rows / built.build_s:,.0f} points/s; first build {first_s:.3f} s), "
+        f"images identical {same}")
+    res = {
+        "workload": f"C3: {rows} x {dim} unit vectors (1,000 components, sigma 0.25, 5% outliers, seed 2), SQ8, "
+                    f"D0 {len(lead)} leaders fanout 2, many-root subtrees fanout 2, leaves <= 2048, k 32, R 64",
+        "build_s": round(built.build_s, 4),
+        "first_build_s": round(first_s, 4),
+        "points_per_s": round(rows / built.build_s, 1),
+        "repeat_image_identical": same,
+        "stages": built.stages,
+        "mean_degree": round(float(built.counts.float().mean().item()), 2),
+    }
+    if check:
+        from oracle import pyoracle as orc
+
+        bad = slots = 0
+        for gl, ids, dd in sampler.leaves:
+            gi = torch.from_numpy(gl.astype(np.int64)).to(dev)
+            want_ids, want_d = orc.leaf_topk(sq8.codes[gi].cpu().numpy(), sq8.scales[gi].cpu().numpy(),
+                                             sq8.norms[gi].cpu().numpy(), gl, np.arange(len(gl), dtype=np.uint32),
+                                             [0], [len(gl)], p.leaf_knn)
+            got_i, got_d = ids.reshape(-1), dd.reshape(-1).view(np.uint32)
+            bad += int(np.count_nonzero((got_i != want_ids) | (got_d != np.asarray(want_d).view(np.uint32))))
+            slots += got_i.size
+        res["leaf_parity_sample"] = {"leaves": len(sampler.leaves), "slots": slots, "mismatched_slots": bad}
+        log(f"C3 leaf sample: {len(sampler.leaves)} leaves, {slots} slots, {bad} mismatched")
+    q = spec.queries(nq, 11, dev)
+    parts = []
+    for s0 in range(0, rows, 1 << 20):
+        xs = x[s0:s0 + (1 << 20)]
+        d = (xs * xs).sum(1)[None, :] - 2.0 * (q @ xs.t())
+        parts.append(torch.topk(d, 64, dim=1, largest=False).indices + s0)
+    cand = torch.cat(parts, 1)
+    dd = ((x[cand].double() - q.double()[:, None, :]) ** 2).sum(2)
+    truth = torch.gather(cand, 1, torch.topk(dd, k_recall, dim=1, largest=False).indices).cpu().numpy()
+    del cand, dd, parts
+    rec = []
+    for L in search_l:
+        torch.cuda.synchronize()
+        s0 = time.perf_counter()
+        ids, _, _ = G.greedy_search(x, built.targets, built.counts, built.start, q, L, k_recall)
+        torch.cuda.synchronize()
+        rec.append({"L": L, "recall_at_10": round(G.recall_at_k(ids.cpu().numpy(), truth, k_recall), 4),
+                    "qps": round(nq / (time.perf_counter() - s0), 1)})
+    res["search"] = rec
+    log(f"C3 search: {rec}")
+    del x, sq8, sk, built
+    return res
 
 
 def c5_leg(dev, rows, nq=1000, k_recall=10, search_l=(64, 128, 256)):

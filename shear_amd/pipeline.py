@@ -409,3 +409,4 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p
         st["leaf_rows"] += r1 - r0
         del rec, segs, ids, d, lay, off
         l0 = l1
+
