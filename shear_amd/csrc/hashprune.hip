@@ -13,7 +13,7 @@
 // remain (an evicted or rejected candidate is worse than l_max others of
 // distinct hashes, and those are only ever replaced by better ones).  So a
 // batch of records can be merged in any order, which is what makes it a GPU
-// reduction:
+// reduction.  Record batches:
 //   1. count records per source (atomics), exclusive scan, scatter the records
 //      grouped by source (the per-source counters return to zero);
 //   2. one wave per source with new records merges its current slots with them
@@ -21,7 +21,12 @@
 //      time): a bitonic sort by (hash, total order: dist key, target) puts
 //      each hash's best first; when more than l_max hashes remain, a sort of
 //      those by the total order gives the l_max-th as a threshold; the
-//      survivors, in ascending hash order, are the new slots.
+//      survivors are the new slots.
+// Segment batches (records left where the emitter wrote them, described by
+// per-source runs) are merged by streaming each source's records through its
+// reservoir held in registers (hp_merge_stream_kernel).  Between merges the
+// slots are kept in no particular order; the export sorts each reservoir by
+// hash, the reference's emit order.
 #include <hipcub/hipcub.hpp>
 
 #include "hashprune_kernels.h"
@@ -285,6 +290,44 @@ __device__ __forceinline__ void reg_bitonic(uint32_t (&h)[E], uint64_t (&k)[E], 
     }
 }
 
+// Of the candidates in h/k (E register slots per lane; an empty entry is
+// h = 0xffffffff, k = ~0, after every real hash <= 0xffff), keeps each hash's
+// best and, of those, the l_max best in total order; leaves them in h/k at
+// positions [0, n) (position q*64 + lane in slot q of lane), ascending in
+// total order, empty entries after them, and returns n.
+template <int E>
+__device__ uint32_t select_sorted(uint32_t (&h)[E], uint64_t (&k)[E], uint32_t l_max, uint32_t lane) {
+    reg_bitonic<E, true>(h, k, lane);
+    // kept = first of its hash (the predecessor of element 64*q is lane 63 of slot q-1)
+    uint32_t n_kept = 0;
+    bool kept[E];
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        uint32_t prev = __shfl_up(h[q], 1);
+        if (q > 0) {
+            const uint32_t last = __shfl(h[q - 1], 63);
+            prev = lane == 0 ? last : prev;
+        }
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        kept[q] = h[q] != 0xffffffffu && (e == 0 || prev != h[q]);
+        n_kept += (uint32_t)__popcll(__ballot(kept[q]));
+    }
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        h[q] = kept[q] ? h[q] : 0xffffffffu;
+        k[q] = kept[q] ? k[q] : ~0ull;
+    }
+    reg_bitonic<E, false>(h, k, lane);
+    const uint32_t n = n_kept < l_max ? n_kept : l_max;
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+        const bool live = (uint32_t)q * 64u + lane < n;
+        h[q] = live ? h[q] : 0xffffffffu;
+        k[q] = live ? k[q] : ~0ull;
+    }
+    return n;
+}
+
 // One merge of a source's n_old slots and n_new records (n_old + n_new <= 64*E)
 // entirely in registers; writes the new slots and returns their count.
 // fetch(q, t) returns new record t (t < n_new) for register slot q.
@@ -309,59 +352,16 @@ __device__ uint32_t reg_merge_f(const uint64_t *slot_keys_in, const uint16_t *sl
             h[q] = r.z & 0xffffu;
         }
     }
-    reg_bitonic<E, true>(h, k, lane);
-    // kept = first of its hash (the predecessor of element 64*q is lane 63 of slot q-1)
-    bool kept[E];
-    uint32_t n_kept = 0;
+    const uint32_t n = select_sorted<E>(h, k, l_max, lane);
 #pragma unroll
     for (int q = 0; q < E; ++q) {
-        uint32_t prev = __shfl_up(h[q], 1);
-        if (q > 0) {
-            const uint32_t last = __shfl(h[q - 1], 63);
-            prev = lane == 0 ? last : prev;
-        }
         const uint32_t e = (uint32_t)q * 64u + lane;
-        kept[q] = e < N && (e == 0 || prev != h[q]);
-        n_kept += (uint32_t)__popcll(__ballot(kept[q]));
-    }
-    bool sel[E];
-#pragma unroll
-    for (int q = 0; q < E; ++q) sel[q] = kept[q];
-    if (n_kept > l_max) {
-        // threshold: the l_max-th kept candidate in total order
-        uint32_t h2[E];
-        uint64_t k2[E];
-#pragma unroll
-        for (int q = 0; q < E; ++q) {
-            h2[q] = kept[q] ? h[q] : 0xffffffffu;
-            k2[q] = kept[q] ? k[q] : ~0ull;
+        if (e < n) {
+            slot_keys_out[e] = k[q];
+            slot_hash_out[e] = (uint16_t)h[q];
         }
-        reg_bitonic<E, false>(h2, k2, lane);
-        const uint32_t tq = (l_max - 1u) / 64u, tl = (l_max - 1u) % 64u;
-        uint64_t tk = k2[0];
-        uint32_t th = h2[0];
-#pragma unroll
-        for (int q = 1; q < E; ++q) {
-            tk = tq == (uint32_t)q ? k2[q] : tk;
-            th = tq == (uint32_t)q ? h2[q] : th;
-        }
-        const uint64_t tkey = ((uint64_t)__shfl((uint32_t)(tk >> 32), (int)tl) << 32) | __shfl((uint32_t)tk, (int)tl);
-        const uint32_t thash = __shfl(th, (int)tl);
-#pragma unroll
-        for (int q = 0; q < E; ++q) sel[q] = kept[q] && (k[q] < tkey || (k[q] == tkey && h[q] <= thash));
     }
-    uint32_t base = 0;
-#pragma unroll
-    for (int q = 0; q < E; ++q) {
-        const uint64_t m = __ballot(sel[q]);
-        if (sel[q]) {
-            const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-            slot_keys_out[pos] = k[q];
-            slot_hash_out[pos] = (uint16_t)h[q];
-        }
-        base += (uint32_t)__popcll(m);
-    }
-    return base;
+    return n;
 }
 
 // Records contiguous at recs; the first 64 were prefetched into r0 (they line
@@ -378,8 +378,8 @@ __device__ uint32_t reg_merge(const uint64_t *slot_keys_in, const uint16_t *slot
 struct HpWaveLds {
     uint64_t key[kHpMergeCap];      // candidates: total-order key (dist key << 32 | target)
     uint32_t val[kHpMergeCap];      // their hashes
-    uint64_t tkey[kHpMergeCap];     // kept candidates, when more than l_max, by total order;
-    uint32_t thash[kHpMergeCap];    // then the merged reservoir (once the threshold is read)
+    uint64_t tkey[kHpMergeCap];     // each hash's best, sorted by total order: the merged
+    uint32_t thash[kHpMergeCap];    // reservoir is their first min(count, l_max)
 };
 
 // Sources with at most kHpRegMax candidates (slots + new records): register
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_small_kernel(const uint4 
 // time.
 // One LDS merge round: the wave's reservoir w.key/w.val[0, n_old) and new
 // candidates w.key/w.val[n_old, N) become the merged reservoir in
-// w.tkey/w.thash[0, result); returns its size.
+// w.tkey/w.thash[0, result), ascending in total order; returns its size.
 __device__ uint32_t lds_merge_round(HpWaveLds &w, uint32_t n_old, uint32_t N, uint32_t l_max, uint32_t lane) {
     uint32_t P = 64;
     while (P < N) P <<= 1;
@@ -446,70 +446,33 @@ __device__ uint32_t lds_merge_round(HpWaveLds &w, uint32_t n_old, uint32_t N, ui
     wave_bitonic_hk(w.val, w.key, P, lane);
     const uint32_t E = P / 64;
     const uint32_t eb = lane * E;
-    // kept = first of its hash; kpos = its place among the kept
+    // kept = first of its hash, compacted into tkey / thash
     uint32_t kcount = 0;
     for (uint32_t q = 0; q < E; ++q) {
         const uint32_t e = eb + q;
         kcount += (e < N && (e == 0 || w.val[e - 1] != w.val[e])) ? 1u : 0u;
     }
     uint32_t n_kept;
-    const uint32_t kbase = wave_excl_scan(kcount, lane, n_kept);
-    if (n_kept <= l_max) {
-        // every hash's best stays, already in ascending hash order
-        uint32_t run = kbase;
-        for (uint32_t q = 0; q < E; ++q) {
-            const uint32_t e = eb + q;
-            if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
-                w.tkey[run] = w.key[e];
-                w.thash[run] = w.val[e];
-                ++run;
-            }
+    uint32_t run = wave_excl_scan(kcount, lane, n_kept);
+    for (uint32_t q = 0; q < E; ++q) {
+        const uint32_t e = eb + q;
+        if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
+            w.tkey[run] = w.key[e];
+            w.thash[run] = w.val[e];
+            ++run;
         }
-        n_old = n_kept;
-    } else {
-        // the l_max best of the kept by (key, hash): threshold from a sort of the kept
-        uint32_t run = kbase;
-        for (uint32_t q = 0; q < E; ++q) {
-            const uint32_t e = eb + q;
-            if (e < N && (e == 0 || w.val[e - 1] != w.val[e])) {
-                w.tkey[run] = w.key[e];
-                w.thash[run] = w.val[e];
-                ++run;
-            }
-        }
-        uint32_t P2 = 64;
-        while (P2 < n_kept) P2 <<= 1;
-        for (uint32_t e = n_kept + lane; e < P2; e += 64) {
-            w.tkey[e] = ~0ull;
-            w.thash[e] = 0xffffffffu;
-        }
-        __builtin_amdgcn_wave_barrier();
-        wave_bitonic<uint64_t>(w.tkey, w.thash, P2, lane);
-        const uint64_t tk = w.tkey[l_max - 1];
-        const uint32_t th = w.thash[l_max - 1];
-        uint32_t scount = 0;
-        for (uint32_t q = 0; q < E; ++q) {
-            const uint32_t e = eb + q;
-            const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
-            const uint64_t k = w.key[e];
-            scount += (kept && (k < tk || (k == tk && w.val[e] <= th))) ? 1u : 0u;
-        }
-        uint32_t n_sel;
-        uint32_t srun = wave_excl_scan(scount, lane, n_sel);
-        for (uint32_t q = 0; q < E; ++q) {
-            const uint32_t e = eb + q;
-            const bool kept = e < N && (e == 0 || w.val[e - 1] != w.val[e]);
-            const uint64_t k = w.key[e];
-            if (kept && (k < tk || (k == tk && w.val[e] <= th))) {
-                w.tkey[srun] = k;
-                w.thash[srun] = w.val[e];
-                ++srun;
-            }
-        }
-        n_old = n_sel;
+    }
+    // the kept by total order; the first l_max of them remain
+    uint32_t P2 = 64;
+    while (P2 < n_kept) P2 <<= 1;
+    for (uint32_t e = n_kept + lane; e < P2; e += 64) {
+        w.tkey[e] = ~0ull;
+        w.thash[e] = 0xffffffffu;
     }
     __builtin_amdgcn_wave_barrier();
-    return n_old;
+    wave_bitonic<uint64_t>(w.tkey, w.thash, P2, lane);
+    __builtin_amdgcn_wave_barrier();
+    return n_kept < l_max ? n_kept : l_max;
 }
 
 // Sources with more than kHpRegMax candidates: merged in LDS, kHpMergeCap at a
@@ -581,183 +544,296 @@ __global__ void hp_seg_keys_kernel(const uint4 *segs, uint64_t nseg, uint32_t nu
     }
 }
 
-// Run heads of the sorted keys -> the active sources (src, first position);
-// their order is not fixed (each source is merged independently).
-__global__ void hp_seg_runs_kernel(const uint32_t *keys, uint64_t nseg, uint32_t num_points, uint32_t *run_src,
-                                   uint32_t *run_start, uint32_t *run_count) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t k = keys[i];
-        if (k < num_points && (i == 0 || keys[i - 1] != k)) {
-            const uint32_t a = atomicAdd(run_count, 1u);
-            run_src[a] = k;
-            run_start[a] = (uint32_t)i;
+// The segment descriptors in sorted order (one gather, so the merge reads a
+// source's segments contiguously).
+__global__ void hp_seg_gather_kernel(const uint4 *segs, const uint32_t *order, uint64_t nseg, uint4 *sorted) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nseg; i += (uint64_t)gridDim.x * blockDim.x)
+        sorted[i] = segs[order[i]];
+}
+
+// ---- streaming merge of a source's segments ----------------------------------
+// Every merge leaves a reservoir's slots ascending in total order (the export
+// sorts them by hash, the reference's emit order).  One wave per active source
+// holds the reservoir in registers (slot position q*64 + lane in register q,
+// ER = ceil(l_max / 64) registers) and streams the source's records through
+// it 64 at a time.  A full reservoir's last slot bounds what can still enter:
+// a candidate no better than it either repeats a slot's hash with a worse (or
+// equal) key or is worse than l_max slots of distinct hashes, so it is
+// dropped by one compare.  The candidates that pass are inserted one at a time
+// (the reference's insert: a hash hit keeps the better, a new hash fills a
+// free slot or replaces the worst) by a rank ballot and a one-position shift;
+// a first chunk into an empty reservoir is sorted instead.
+
+constexpr uint32_t kBatchMin = 24;  // passing candidates of a chunk into an empty reservoir that are sorted
+
+__device__ __forceinline__ bool ent_less(uint64_t ka, uint32_t ha, uint64_t kb, uint32_t hb) {
+    return ka < kb || (ka == kb && ha < hb);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
+}
+__device__ __forceinline__ uint32_t readlane32(uint32_t v, uint32_t l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+
+template <int ER>
+struct Reservoir {
+    uint64_t k[ER];  // live positions [0, c) ascending by (k, h); the rest k = ~0, h = 0xffffffff
+    uint32_t h[ER];
+    uint32_t c;
+};
+
+// Key / hash at position pos (the same in every lane).
+template <int ER>
+__device__ __forceinline__ void res_at(const Reservoir<ER> &r, uint32_t pos, uint64_t &k, uint32_t &h) {
+    uint64_t kk = r.k[0];
+    uint32_t hh = r.h[0];
+#pragma unroll
+    for (int q = 1; q < ER; ++q) {
+        kk = pos / 64u == (uint32_t)q ? r.k[q] : kk;
+        hh = pos / 64u == (uint32_t)q ? r.h[q] : hh;
+    }
+    k = readlane64(kk, pos & 63u);
+    h = readlane32(hh, pos & 63u);
+}
+
+// Positions (p, end] take the entry before them; position p takes (bk, bh).
+template <int ER>
+__device__ __forceinline__ void res_shift_in(Reservoir<ER> &r, uint32_t p, uint32_t end, uint64_t bk, uint32_t bh,
+                                             uint32_t lane) {
+#pragma unroll
+    for (int q = ER - 1; q >= 0; --q) {
+        if ((uint32_t)q * 64u > end || (uint32_t)q * 64u + 63u < p) continue;  // register untouched
+        const uint32_t lo = __shfl_up((uint32_t)r.k[q], 1);
+        const uint32_t hi = __shfl_up((uint32_t)(r.k[q] >> 32), 1);
+        uint64_t uk = ((uint64_t)hi << 32) | lo;
+        uint32_t uh = __shfl_up(r.h[q], 1);
+        if (q > 0) {
+            const uint64_t ck = readlane64(r.k[q - 1], 63);
+            const uint32_t ch = readlane32(r.h[q - 1], 63);
+            uk = lane == 0 ? ck : uk;
+            uh = lane == 0 ? ch : uh;
         }
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        const bool mv = e > p && e <= end;
+        r.k[q] = e == p ? bk : (mv ? uk : r.k[q]);
+        r.h[q] = e == p ? bh : (mv ? uh : r.h[q]);
     }
 }
 
-// Register merge of one source's reservoir and its segments' records.  Lane
-// s < ns holds segment s (exclusive prefix `pre`, `cnt` records from
-// `first`).  The record of each register slot is located first, with every
-// lane active (the lanes' segment values are read by shuffles), then the
-// merge reads it.
-template <int E>
-__device__ uint32_t seg_merge(const uint4 *records, uint64_t *slot_keys, uint16_t *slot_hash, uint32_t n_old,
-                              uint32_t n_new, uint32_t ns, uint32_t pre, uint32_t cnt, uint64_t first, uint32_t l_max,
-                              uint32_t lane) {
-    uint64_t addr[E];
+// Inserts candidate (bk, bh), the same in every lane.
+template <int ER>
+__device__ __forceinline__ void res_insert(Reservoir<ER> &r, uint64_t bk, uint32_t bh, uint32_t l_max,
+                                           uint32_t lane) {
+    uint32_t p = 0;                // slots before the candidate in total order
+    uint32_t hit = 0xffffffffu;    // the slot of its hash
 #pragma unroll
-    for (int q = 0; q < E; ++q) addr[q] = 0;
-    for (uint32_t sg = 0; sg < ns; ++sg) {
-        const uint32_t ps = __shfl(pre, (int)sg), cs = __shfl(cnt, (int)sg);
-        const uint64_t fs = ((uint64_t)__shfl((uint32_t)(first >> 32), (int)sg) << 32) | __shfl((uint32_t)first, (int)sg);
-#pragma unroll
-        for (int q = 0; q < E; ++q) {
-            const uint32_t e = (uint32_t)q * 64u + lane;
-            if (e >= n_old && e - n_old >= ps && e - n_old < ps + cs) addr[q] = fs + (e - n_old - ps);
-        }
+    for (int q = 0; q < ER; ++q) {
+        const bool live = (uint32_t)q * 64u + lane < r.c;
+        p += (uint32_t)__popcll(__ballot(live && ent_less(r.k[q], r.h[q], bk, bh)));
+        const uint64_t m = __ballot(live && r.h[q] == bh);
+        hit = m ? (uint32_t)q * 64u + (uint32_t)__builtin_ctzll(m) : hit;
     }
-    auto fetch = [&](int q, uint32_t) -> uint4 {
-        uint64_t a = addr[0];
-#pragma unroll
-        for (int i = 1; i < E; ++i) a = i == q ? addr[i] : a;
-        return records[a];
-    };
-    return reg_merge_f<E>(slot_keys, slot_hash, n_old, n_new, fetch, l_max, lane, slot_keys, slot_hash);
+    uint32_t end;
+    if (hit != 0xffffffffu) {
+        if (hit < p) return;  // its hash holds a better candidate
+        uint64_t ek;
+        uint32_t eh;
+        res_at(r, hit, ek, eh);
+        if (ek == bk) return;  // the same candidate
+        end = hit;             // the worse candidate of its hash goes
+    } else if (r.c < l_max) {
+        end = r.c++;
+    } else {
+        if (p >= l_max) return;  // worse than every slot
+        end = l_max - 1u;        // the worst slot goes
+    }
+    res_shift_in(r, p, end, bk, bh, lane);
 }
 
-// The segments of active source a: sorted positions [start, start + ns);
-// lanes read the keys after `start` and count the leading run equal to src
-// (ns > 64 means "more than 64").
-__device__ __forceinline__ uint32_t run_length64(const uint32_t *keys, uint64_t nseg, uint32_t start, uint32_t src,
-                                                 uint32_t lane) {
-    const uint64_t at = (uint64_t)start + lane;
-    const bool eq = at < nseg && keys[at] == src;
-    const uint64_t m = ~__ballot(eq);
-    return m ? (uint32_t)__builtin_ctzll(m) : 65u;
-}
-
-// Register merges of active sources with at most 64 segments and kHpRegMax
-// candidates.
-__global__ __launch_bounds__(kHpThreads) void hp_merge_small_seg_kernel(const uint4 *records, const uint4 *segs,
-                                                                        const uint32_t *keys, const uint32_t *vals,
-                                                                        uint64_t nseg, const uint32_t *run_src,
-                                                                        const uint32_t *run_start,
-                                                                        const uint32_t *run_count, uint32_t l_max,
-                                                                        uint64_t *slot_keys, uint16_t *slot_hash,
-                                                                        uint32_t *slot_count) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t waves = gridDim.x * kHpWaves;
-    const uint32_t na = *run_count;
-    for (uint32_t a = blockIdx.x * kHpWaves + (threadIdx.x >> 6); a < na; a += waves) {
-        const uint32_t src = run_src[a];
-        const uint32_t s0 = run_start[a];
-        const uint32_t ns = run_length64(keys, nseg, s0, src, lane);
-        if (ns > 64u) continue;  // hp_merge_large_seg_kernel
-        uint32_t cnt = 0;
-        uint64_t first = 0;
-        if (lane < ns) {
-            const uint4 g = segs[vals[s0 + lane]];
-            cnt = g.w;
-            first = ((uint64_t)g.z << 32) | g.y;
-        }
-        uint32_t n_new;
-        const uint32_t pre = wave_excl_scan(cnt, lane, n_new);
-        const uint32_t n_old = slot_count[src];
-        if (n_old + n_new > kHpRegMax) continue;
-        const uint64_t sbase = (uint64_t)src * l_max;
-        uint32_t c;
-        if (n_old + n_new <= 64u)
-            c = seg_merge<1>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
-                             lane);
-        else if (n_old + n_new <= 128u)
-            c = seg_merge<2>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
-                             lane);
-        else
-            c = seg_merge<4>(records, slot_keys + sbase, slot_hash + sbase, n_old, n_new, ns, pre, cnt, first, l_max,
-                             lane);
-        if (lane == 0) slot_count[src] = c;
+// Merges one chunk (candidate (ck, ch) in each lane where v) into the reservoir.
+template <int ER>
+__device__ void res_chunk(Reservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t lane) {
+    bool pass = v;
+    if (r.c == l_max) {
+        uint64_t wk;
+        uint32_t wh;
+        res_at(r, l_max - 1u, wk, wh);
+        pass = v && ent_less(ck, ch, wk, wh);
+    }
+    uint64_t pm = __ballot(pass);
+    if (pm == 0) return;
+    if (r.c == 0 && (uint32_t)__popcll(pm) >= kBatchMin) {
+        uint32_t h[1] = {pass ? ch : 0xffffffffu};
+        uint64_t k[1] = {pass ? ck : ~0ull};
+        r.c = select_sorted<1>(h, k, l_max, lane);
+        r.k[0] = k[0];
+        r.h[0] = h[0];
+        return;
+    }
+    while (pm) {
+        const uint32_t j = (uint32_t)__builtin_ctzll(pm);
+        pm &= pm - 1ull;
+        res_insert(r, readlane64(ck, j), readlane32(ch, j), l_max, lane);
     }
 }
 
-// The other active sources: their segments' records staged in LDS, merged
-// kHpMergeCap candidates at a time.
-__global__ __launch_bounds__(kHpThreads) void hp_merge_large_seg_kernel(const uint4 *records, const uint4 *segs,
-                                                                        const uint32_t *keys, const uint32_t *vals,
-                                                                        uint64_t nseg, const uint32_t *run_src,
-                                                                        const uint32_t *run_start,
-                                                                        const uint32_t *run_count, uint32_t l_max,
-                                                                        uint64_t *slot_keys, uint16_t *slot_hash,
-                                                                        uint32_t *slot_count) {
-    __shared__ HpWaveLds lds[kHpWaves];
+// What a wave loads for one active source before merging it: its segment
+// descriptors (lane s: the run's segment s, for s < 64) and its slots.
+template <int ER>
+struct SourceLoad {
+    uint32_t src, start, len;  // run: sorted segments [start, start + len)
+    uint32_t cnt;              // lane's segment: record count and first record
+    uint64_t first;
+    uint32_t c;
+    uint64_t k[ER];
+    uint32_t h[ER];
+};
+
+template <int ER>
+__device__ __forceinline__ void load_source(SourceLoad<ER> &L, uint32_t src, uint32_t start, uint32_t len,
+                                            const uint4 *sorted, uint32_t num_points, uint32_t l_max,
+                                            const uint64_t *slot_keys, const uint16_t *slot_hash,
+                                            const uint32_t *slot_count, uint32_t lane) {
+    L.src = src;
+    L.start = start;
+    L.len = len;
+    L.cnt = 0;
+    L.first = 0;
+    L.c = 0;
+    const bool real = src < num_points;  // the run of empty / bad segments sorts last
+    if (real && lane < len) {
+        const uint4 g = sorted[(uint64_t)start + lane];
+        L.cnt = g.w;
+        L.first = ((uint64_t)g.z << 32) | g.y;
+    }
+    const uint64_t sbase = (uint64_t)(real ? src : 0u) * l_max;
+    if (real) L.c = slot_count[src];
+#pragma unroll
+    for (int q = 0; q < ER; ++q) {
+        // every slot position is read (not only the live ones), so these loads
+        // do not wait for the count
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        const bool in = real && e < l_max;
+        L.k[q] = in ? slot_keys[sbase + e] : ~0ull;
+        L.h[q] = in ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
+    }
+}
+
+// Merges the records of a group of up to 64 segments (lane s: segment s, cnt
+// records from first) 64 at a time across segment boundaries.
+template <int ER>
+__device__ __forceinline__ void merge_group(Reservoir<ER> &r, const uint4 *records, uint32_t ng, uint32_t cnt,
+                                            uint64_t first, uint32_t l_max, uint32_t lane) {
+    uint32_t total;
+    const uint32_t pre = wave_excl_scan(cnt, lane, total);
+    uint32_t sg = 0;  // first segment not yet wholly read
+    for (uint32_t c0 = 0; c0 < total; c0 += 64) {
+        const uint32_t p = c0 + lane;
+        uint64_t addr = 0;
+        for (uint32_t s = sg; s < ng; ++s) {
+            const uint32_t ps = readlane32(pre, s);
+            if (ps >= c0 + 64u) break;
+            const uint32_t cs = readlane32(cnt, s);
+            const uint64_t fs = readlane64(first, s);
+            addr = (p >= ps && p < ps + cs) ? fs + (p - ps) : addr;
+            if (ps + cs <= c0 + 64u) sg = s + 1;
+        }
+        const bool v = p < total;
+        uint64_t ck = ~0ull;
+        uint32_t ch = 0xffffffffu;
+        if (v) {
+            const uint4 rec = records[addr];
+            ck = ((uint64_t)total_key(__uint_as_float(rec.w)) << 32) | rec.y;
+            ch = rec.z & 0xffffu;
+        }
+        res_chunk(r, ck, ch, v, l_max, lane);
+    }
+}
+
+// Active sources in ascending source order (run-length encoding of the sorted
+// segment keys).  Each wave walks its sources with the next source's
+// segments and slots, and the one after's run, already in flight.
+template <int ER>
+__global__ __launch_bounds__(kHpThreads) void hp_merge_stream_kernel(const uint4 *records, const uint4 *sorted,
+                                                                     const uint32_t *run_src,
+                                                                     const uint32_t *run_start,
+                                                                     const uint32_t *run_len,
+                                                                     const uint32_t *num_runs, uint32_t num_points,
+                                                                     uint32_t l_max, uint64_t *slot_keys,
+                                                                     uint16_t *slot_hash, uint32_t *slot_count) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    HpWaveLds &w = lds[wave];
     const uint32_t waves = gridDim.x * kHpWaves;
-    const uint32_t na = *run_count;
-    for (uint32_t a = blockIdx.x * kHpWaves + wave; a < na; a += waves) {
-        const uint32_t src = run_src[a];
-        const uint32_t s0 = run_start[a];
-        const uint32_t ns64 = run_length64(keys, nseg, s0, src, lane);
-        uint32_t n_old = slot_count[src];
-        if (ns64 <= 64u) {
-            // the small kernel's case unless it holds more than kHpRegMax candidates
-            const uint32_t cnt = lane < ns64 ? segs[vals[s0 + lane]].w : 0u;
-            uint32_t n_new;
-            (void)wave_excl_scan(cnt, lane, n_new);
-            if (n_old + n_new <= kHpRegMax) continue;
+    const uint32_t na = *num_runs;
+    uint32_t a = blockIdx.x * kHpWaves + wave;
+    if (a >= na) return;
+    SourceLoad<ER> cur;
+    load_source(cur, run_src[a], run_start[a], run_len[a], sorted, num_points, l_max, slot_keys, slot_hash,
+                slot_count, lane);
+    uint32_t d_src = num_points, d_start = 0, d_len = 0;  // run of the next source
+    if (a + waves < na) {
+        d_src = run_src[a + waves];
+        d_start = run_start[a + waves];
+        d_len = run_len[a + waves];
+    }
+    for (; a < na; a += waves) {
+        SourceLoad<ER> nxt;
+        load_source(nxt, d_src, d_start, d_len, sorted, num_points, l_max, slot_keys, slot_hash, slot_count, lane);
+        const uint32_t a2 = a + 2u * waves;
+        d_src = num_points;
+        d_len = 0;
+        if (a2 < na) {
+            d_src = run_src[a2];
+            d_start = run_start[a2];
+            d_len = run_len[a2];
         }
-        const uint64_t sbase = (uint64_t)src * l_max;
-        for (uint32_t e = lane; e < n_old; e += 64) {
-            w.key[e] = slot_keys[sbase + e];
-            w.val[e] = slot_hash[sbase + e];
-        }
-        __builtin_amdgcn_wave_barrier();
-        uint32_t fill = 0;  // candidates staged after the reservoir
-        bool merged = false;
-        for (uint64_t si = s0; si < nseg && keys[si] == src; ++si) {
-            const uint4 g = segs[vals[si]];
-            const uint64_t first = ((uint64_t)g.z << 32) | g.y;
-            uint32_t used = 0;
-            while (used < g.w) {
-                const uint32_t room = kHpMergeCap - n_old - fill;
-                const uint32_t take = (g.w - used < room) ? g.w - used : room;
-                for (uint32_t e = lane; e < take; e += 64) {
-                    const uint4 r = records[first + used + e];
-                    w.key[n_old + fill + e] = ((uint64_t)total_key(__uint_as_float(r.w)) << 32) | r.y;
-                    w.val[n_old + fill + e] = r.z & 0xffffu;
+        const uint32_t src = cur.src;
+        if (src < num_points) {
+            Reservoir<ER> r;
+            r.c = cur.c;
+#pragma unroll
+            for (int q = 0; q < ER; ++q) {
+                const bool live = (uint32_t)q * 64u + lane < r.c;
+                r.k[q] = live ? cur.k[q] : ~0ull;
+                r.h[q] = live ? cur.h[q] : 0xffffffffu;
+            }
+            merge_group(r, records, cur.len < 64u ? cur.len : 64u, cur.cnt, cur.first, l_max, lane);
+            for (uint32_t g0 = 64; g0 < cur.len; g0 += 64) {
+                // a source with more than 64 segments in the batch: the rest, 64 at a time
+                const uint32_t ng = cur.len - g0 < 64u ? cur.len - g0 : 64u;
+                uint32_t cnt = 0;
+                uint64_t first = 0;
+                if (lane < ng) {
+                    const uint4 g = sorted[(uint64_t)cur.start + g0 + lane];
+                    cnt = g.w;
+                    first = ((uint64_t)g.z << 32) | g.y;
                 }
-                fill += take;
-                used += take;
-                if (n_old + fill == kHpMergeCap) {
-                    __builtin_amdgcn_wave_barrier();
-                    n_old = lds_merge_round(w, n_old, n_old + fill, l_max, lane);
-                    fill = 0;
-                    for (uint32_t e = lane; e < n_old; e += 64) {
-                        w.key[e] = w.tkey[e];
-                        w.val[e] = w.thash[e];
-                    }
-                    __builtin_amdgcn_wave_barrier();
-                    merged = true;
+                merge_group(r, records, ng, cnt, first, l_max, lane);
+            }
+            const uint64_t sbase = (uint64_t)src * l_max;
+#pragma unroll
+            for (int q = 0; q < ER; ++q) {
+                const uint32_t e = (uint32_t)q * 64u + lane;
+                if (e < r.c) {
+                    slot_keys[sbase + e] = r.k[q];
+                    slot_hash[sbase + e] = (uint16_t)r.h[q];
                 }
             }
+            if (lane == 0) slot_count[src] = r.c;
         }
-        if (fill > 0 || !merged) {
-            __builtin_amdgcn_wave_barrier();
-            n_old = lds_merge_round(w, n_old, n_old + fill, l_max, lane);
-        }
-        for (uint32_t e = lane; e < n_old; e += 64) {
-            slot_keys[sbase + e] = w.tkey[e];
-            slot_hash[sbase + e] = (uint16_t)w.thash[e];
-        }
-        if (lane == 0) slot_count[src] = n_old;
-        __builtin_amdgcn_wave_barrier();
+        cur = nxt;
     }
 }
 
-// Segment workspace layout: keys in/out, values in/out, run sources and
-// starts (nseg each, u32), the run count, then the radix sort's temporary.
+// Segment workspace layout (nseg entries each unless noted): sort keys and
+// values in / out (u32), run sources, lengths and starts (u32), the run count
+// (one u32), the segment descriptors in sorted order (uint4), then the
+// temporary of the radix sort / run-length encoding / scan.
 struct SegWs {
-    uint32_t *keys_in, *keys_out, *vals_in, *vals_out, *run_src, *run_start, *run_count;
+    uint32_t *keys_in, *keys_out, *vals_in, *vals_out, *run_src, *run_len, *run_start, *num_runs;
+    uint4 *sorted;
     void *temp;
     size_t temp_bytes;
 };
@@ -767,42 +843,60 @@ int key_bits(uint32_t num_points) {
     while (b < 32 && ((uint64_t)1 << b) <= num_points) ++b;  // keys go up to num_points (unused segments)
     return b;
 }
-size_t seg_sort_temp(uint64_t nseg, uint32_t num_points) {
-    size_t bytes = 0;
-    hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+size_t seg_temp(uint64_t nseg, uint32_t num_points) {
+    size_t sort = 0, rle = 0, scan = 0;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort, (const uint32_t *)nullptr, (uint32_t *)nullptr,
                                        (const uint32_t *)nullptr, (uint32_t *)nullptr, (int)nseg, 0,
                                        key_bits(num_points));
-    return bytes;
+    (void)hipcub::DeviceRunLengthEncode::Encode(nullptr, rle, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+                                          (uint32_t *)nullptr, (uint32_t *)nullptr, (int)nseg);
+    (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan, (const uint32_t *)nullptr, (uint32_t *)nullptr, (int)nseg);
+    return sort > rle ? (sort > scan ? sort : scan) : (rle > scan ? rle : scan);
 }
 SegWs seg_ws_layout(void *base, uint64_t nseg, uint32_t num_points) {
     SegWs w{};
     char *p = static_cast<char *>(base);
     const size_t a = seg_align(nseg * 4);
-    w.keys_in = reinterpret_cast<uint32_t *>(p);
-    w.keys_out = reinterpret_cast<uint32_t *>(p + a);
-    w.vals_in = reinterpret_cast<uint32_t *>(p + 2 * a);
-    w.vals_out = reinterpret_cast<uint32_t *>(p + 3 * a);
-    w.run_src = reinterpret_cast<uint32_t *>(p + 4 * a);
-    w.run_start = reinterpret_cast<uint32_t *>(p + 5 * a);
-    w.run_count = reinterpret_cast<uint32_t *>(p + 6 * a);
-    w.temp = p + 6 * a + 256;
-    w.temp_bytes = seg_sort_temp(nseg, num_points);
+    uint32_t **arr[7] = {&w.keys_in, &w.keys_out, &w.vals_in, &w.vals_out, &w.run_src, &w.run_len, &w.run_start};
+    for (int i = 0; i < 7; ++i) *arr[i] = reinterpret_cast<uint32_t *>(p + i * a);
+    w.num_runs = reinterpret_cast<uint32_t *>(p + 7 * a);
+    w.sorted = reinterpret_cast<uint4 *>(p + 7 * a + 256);
+    w.temp = p + 7 * a + 256 + seg_align(nseg * 16);
+    w.temp_bytes = seg_temp(nseg, num_points);
     return w;
 }
 
-__global__ void hp_export_kernel(const uint64_t *slot_keys, const uint16_t *slot_hash, const uint32_t *slot_count,
-                                 uint32_t num_points, uint32_t l_max, uint32_t *targets, uint16_t *hashes,
-                                 float *dists, uint32_t *counts) {
-    const uint64_t total = (uint64_t)num_points * l_max;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t p = (uint32_t)(i / l_max), s = (uint32_t)(i % l_max);
+// One wave per point: its slots sorted by hash (a reservoir's hashes are
+// distinct, so the order is the reference's emit order, ascending hash).
+template <int ER>
+__global__ __launch_bounds__(kHpThreads) void hp_export_kernel(const uint64_t *slot_keys, const uint16_t *slot_hash,
+                                                               const uint32_t *slot_count, uint32_t num_points,
+                                                               uint32_t l_max, uint32_t *targets, uint16_t *hashes,
+                                                               float *dists, uint32_t *counts) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t p = blockIdx.x * kHpWaves + (threadIdx.x >> 6); p < num_points; p += waves) {
         const uint32_t c = slot_count[p];
-        const bool live = s < c;
-        const uint64_t k = live ? slot_keys[i] : 0ull;
-        if (targets) targets[i] = live ? (uint32_t)k : 0xffffffffu;
-        if (hashes) hashes[i] = live ? slot_hash[i] : (uint16_t)0;
-        if (dists) dists[i] = live ? key_dist((uint32_t)(k >> 32)) : 0.0f;
-        if (counts && s == 0) counts[p] = c;
+        const uint64_t base = (uint64_t)p * l_max;
+        uint32_t h[ER];
+        uint64_t k[ER];
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            h[q] = e < c ? (uint32_t)slot_hash[base + e] : 0xffffffffu;
+            k[q] = e < c ? slot_keys[base + e] : ~0ull;
+        }
+        reg_bitonic<ER, true>(h, k, lane);
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            if (e >= l_max) continue;
+            const bool live = e < c;
+            if (targets) targets[base + e] = live ? (uint32_t)k[q] : 0xffffffffu;
+            if (hashes) hashes[base + e] = live ? (uint16_t)h[q] : (uint16_t)0;
+            if (dists) dists[base + e] = live ? key_dist((uint32_t)(k[q] >> 32)) : 0.0f;
+        }
+        if (counts && lane == 0) counts[p] = c;
     }
 }
 
@@ -847,7 +941,8 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
 }
 
 uint64_t hashprune_segment_workspace_bytes(uint64_t nseg, uint32_t num_points) {
-    return 6 * seg_align((nseg ? nseg : 1) * 4) + 256 + seg_sort_temp(nseg ? nseg : 1, num_points) + 256;
+    const uint64_t n = nseg ? nseg : 1;
+    return 7 * seg_align(n * 4) + 256 + seg_align(n * 16) + seg_temp(n, num_points) + 256;
 }
 
 int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, const uint4 *segs, uint64_t nseg,
@@ -862,27 +957,48 @@ int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, co
     if (hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.keys_in, w.keys_out, w.vals_in, w.vals_out, (int)nseg, 0,
                                            key_bits(n), stream) != hipSuccess)
         return -1;
-    hipLaunchKernelGGL(hp_fill_u32, dim3(1), dim3(64), 0, stream, w.run_count, (uint64_t)1, 0u);
-    hipLaunchKernelGGL(hp_seg_runs_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, w.keys_out, nseg,
-                       n, w.run_src, w.run_start, w.run_count);
-    // large first (a merge never shrinks a reservoir, so the small kernel then
-    // skips what the large kernel merged)
-    const uint32_t ga = grid_for(nseg, kHpWaves, 8192);
-    hipLaunchKernelGGL(hp_merge_large_seg_kernel, dim3(grid_for(nseg, kHpWaves, 2048)), dim3(kHpThreads), 0, stream,
-                       records, segs, w.keys_out, w.vals_out, nseg, w.run_src, w.run_start, w.run_count, s.l_max,
-                       s.slot_keys, s.slot_hash, s.slot_count);
-    hipLaunchKernelGGL(hp_merge_small_seg_kernel, dim3(ga), dim3(kHpThreads), 0, stream, records, segs, w.keys_out,
-                       w.vals_out, nseg, w.run_src, w.run_start, w.run_count, s.l_max, s.slot_keys, s.slot_hash,
-                       s.slot_count);
+    tb = w.temp_bytes;
+    if (hipcub::DeviceRunLengthEncode::Encode(w.temp, tb, w.keys_out, w.run_src, w.run_len, w.num_runs, (int)nseg,
+                                              stream) != hipSuccess)
+        return -1;
+    // run starts: exclusive sum of the lengths (entries past the run count
+    // are never read)
+    tb = w.temp_bytes;
+    if (hipcub::DeviceScan::ExclusiveSum(w.temp, tb, w.run_len, w.run_start, (int)nseg, stream) != hipSuccess)
+        return -1;
+    hipLaunchKernelGGL(hp_seg_gather_kernel, dim3(grid_for(nseg, 256, 16384)), dim3(256), 0, stream, segs,
+                       w.vals_out, nseg, w.sorted);
+    const uint32_t grid = grid_for(nseg, kHpWaves, 8192);
+    const uint32_t l = s.l_max;
+    if (l <= 64)
+        hipLaunchKernelGGL(hp_merge_stream_kernel<1>, dim3(grid), dim3(kHpThreads), 0, stream, records, w.sorted,
+                           w.run_src, w.run_start, w.run_len, w.num_runs, n, l, s.slot_keys, s.slot_hash,
+                           s.slot_count);
+    else if (l <= 128)
+        hipLaunchKernelGGL(hp_merge_stream_kernel<2>, dim3(grid), dim3(kHpThreads), 0, stream, records, w.sorted,
+                           w.run_src, w.run_start, w.run_len, w.num_runs, n, l, s.slot_keys, s.slot_hash,
+                           s.slot_count);
+    else
+        hipLaunchKernelGGL(hp_merge_stream_kernel<4>, dim3(grid), dim3(kHpThreads), 0, stream, records, w.sorted,
+                           w.run_src, w.run_start, w.run_len, w.num_runs, n, l, s.slot_keys, s.slot_hash,
+                           s.slot_count);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_hashprune_export(const HashPruneState &s, uint32_t *targets, uint16_t *hashes, float *dists,
                             uint32_t *counts, hipStream_t stream) {
-    const uint64_t total = (uint64_t)s.num_points * s.l_max;
-    if (total == 0) return 0;
-    hipLaunchKernelGGL(hp_export_kernel, dim3(grid_for(total, 256, 16384)), dim3(256), 0, stream, s.slot_keys,
-                       s.slot_hash, s.slot_count, s.num_points, s.l_max, targets, hashes, dists, counts);
+    const uint32_t n = s.num_points;
+    if (n == 0 || s.l_max == 0) return 0;
+    const uint32_t grid = grid_for(n, kHpWaves, 8192);
+    if (s.l_max <= 64)
+        hipLaunchKernelGGL(hp_export_kernel<1>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys, s.slot_hash,
+                           s.slot_count, n, s.l_max, targets, hashes, dists, counts);
+    else if (s.l_max <= 128)
+        hipLaunchKernelGGL(hp_export_kernel<2>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys, s.slot_hash,
+                           s.slot_count, n, s.l_max, targets, hashes, dists, counts);
+    else
+        hipLaunchKernelGGL(hp_export_kernel<4>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys, s.slot_hash,
+                           s.slot_count, n, s.l_max, targets, hashes, dists, counts);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -103,3 +103,64 @@ def test_segment_insert_equals_record_insert(gpu_dev, orc, n_points, leaf_sizes,
     tbn = tb.cpu().numpy().view(np.uint32)
     for p in range(n_points):
         assert np.array_equal(tbn[p, : wc[p]], wt[p, : wc[p]])
+
+
+def _random_segments(rng, r, max_seg):
+    """The records of stream ``r`` grouped by source and cut into segments of
+    1..max_seg records of one source, in random order."""
+    g = r[np.argsort(r["src"], kind="stable")]
+    src = g["src"].astype(np.int64)
+    cut = np.zeros(len(g) + 1, bool)
+    cut[0] = cut[-1] = True
+    cut[1:-1] = src[1:] != src[:-1]
+    pos, starts = 0, []
+    for b in np.nonzero(cut[1:])[0] + 1:  # source runs [pos, b)
+        while pos < b:
+            starts.append(pos)
+            pos += int(rng.integers(1, max_seg + 1))
+        pos = b
+    starts = np.array(starts, np.int64)
+    ends = np.append(starts[1:], len(g))
+    bounds = np.nonzero(cut)[0]
+    ends = np.minimum(ends, bounds[np.searchsorted(bounds, starts, side="right")])
+    segs = np.zeros((len(starts), 4), np.uint32)
+    segs[:, 0] = src[starts]
+    segs[:, 1] = starts & 0xFFFFFFFF
+    segs[:, 2] = starts >> 32
+    segs[:, 3] = ends - starts
+    segs = segs[rng.permutation(len(segs))]
+    return g, segs
+
+
+@pytest.mark.parametrize("seed,num_points,n,l_max,hash_bits,levels,max_seg", [
+    (1, 5, 400, 4, 3, 7, 3),           # heavy hash collisions and distance ties
+    (2, 17, 2000, 8, 5, 50, 40),
+    (3, 3, 3000, 64, 12, 1000, 2),     # ~1000 records per source in > 64 segments of 1..2
+    (4, 40, 5000, 3, 2, 3, 9),
+    (5, 1000, 60000, 64, 12, 4000, 70),  # default l_max and m_hash_bits
+    (6, 7, 9000, 256, 12, 100000, 300),  # largest l_max
+    (7, 300, 2000, 1, 1, 2, 5),
+    (8, 20, 4000, 32, 12, 500, 17),
+    (9, 20, 4000, 200, 12, 500, 64),
+    (10, 60, 9000, 64, 8, 300, 33),     # 256 hashes: many collisions
+    (11, 30, 12000, 64, 12, 3000, 128),
+    (12, 25, 10000, 256, 12, 50000, 1),  # 400 one-record segments per source
+    (13, 30, 12000, 32, 6, 100, 6),     # 64 hashes: heavy collisions and ties
+    (14, 2000, 200000, 128, 12, 100000, 40),
+    (15, 500, 100000, 100, 10, 1000, 25),
+])
+def test_random_segments_match_oracle(gpu_dev, orc, seed, num_points, n, l_max, hash_bits, levels, max_seg):
+    """Random streams (the record-path cases) through the segment insert, in
+    two batches of segments: slot for slot the oracle's reservoirs."""
+    from test_gpu_hashprune import _gpu_slots, _same
+    from test_hashprune_oracle import random_stream
+
+    rng = np.random.default_rng(seed)
+    r = random_stream(rng, num_points, n, hash_bits, levels)
+    g, segs = _random_segments(rng, r, max_seg)
+    recs = torch.from_numpy(np.ascontiguousarray(g).view(np.uint8).view(np.int32).reshape(-1, 4).copy()).to(gpu_dev)
+    half = len(segs) // 2
+    with H.HashPruneReducer(num_points, l_max, gpu_dev) as hp:
+        for part in (segs[:half], segs[half:]):
+            hp.insert_segments(recs, torch.from_numpy(part.view(np.int32).copy()).to(gpu_dev))
+        _same(_gpu_slots(hp), orc.hashprune_reduce(num_points, l_max, r), f"seed {seed}")
