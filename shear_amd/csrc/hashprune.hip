@@ -576,6 +576,7 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
 __device__ __forceinline__ uint32_t readlane32(uint32_t v, uint32_t l) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
 }
+__device__ __forceinline__ uint64_t ballot64(bool pred) { return __builtin_amdgcn_ballot_w64(pred); }
 
 template <int ER>
 struct Reservoir {
@@ -622,7 +623,8 @@ __device__ __forceinline__ void res_shift_in(Reservoir<ER> &r, uint32_t p, uint3
     }
 }
 
-// Inserts candidate (bk, bh), the same in every lane.
+// Inserts candidate (bk, bh), the same in every lane (r.c, p, hit and the
+// decision are wave-uniform, so they stay scalar).
 template <int ER>
 __device__ __forceinline__ void res_insert(Reservoir<ER> &r, uint64_t bk, uint32_t bh, uint32_t l_max,
                                            uint32_t lane) {
@@ -631,25 +633,29 @@ __device__ __forceinline__ void res_insert(Reservoir<ER> &r, uint64_t bk, uint32
 #pragma unroll
     for (int q = 0; q < ER; ++q) {
         const bool live = (uint32_t)q * 64u + lane < r.c;
-        p += (uint32_t)__popcll(__ballot(live && ent_less(r.k[q], r.h[q], bk, bh)));
-        const uint64_t m = __ballot(live && r.h[q] == bh);
+        p += (uint32_t)__popcll(ballot64(live && ent_less(r.k[q], r.h[q], bk, bh)));
+        const uint64_t m = ballot64(live && r.h[q] == bh);
         hit = m ? (uint32_t)q * 64u + (uint32_t)__builtin_ctzll(m) : hit;
     }
+    bool go;
     uint32_t end;
     if (hit != 0xffffffffu) {
-        if (hit < p) return;  // its hash holds a better candidate
+        // a hash hit: the candidate replaces the slot when it is better (a
+        // better or equal slot sorts before it, hit < p, or is the same key)
         uint64_t ek;
         uint32_t eh;
         res_at(r, hit, ek, eh);
-        if (ek == bk) return;  // the same candidate
-        end = hit;             // the worse candidate of its hash goes
+        go = hit >= p && ek != bk;
+        end = hit;
     } else if (r.c < l_max) {
-        end = r.c++;
+        go = true;  // a free slot
+        end = r.c;
+        r.c = r.c + 1u;
     } else {
-        if (p >= l_max) return;  // worse than every slot
-        end = l_max - 1u;        // the worst slot goes
+        go = p < l_max;  // the worst slot goes unless the candidate is worse than every slot
+        end = l_max - 1u;
     }
-    res_shift_in(r, p, end, bk, bh, lane);
+    if (go) res_shift_in(r, p, end, bk, bh, lane);
 }
 
 // Merges one chunk (candidate (ck, ch) in each lane where v) into the reservoir.
@@ -662,12 +668,12 @@ __device__ void res_chunk(Reservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, ui
         res_at(r, l_max - 1u, wk, wh);
         pass = v && ent_less(ck, ch, wk, wh);
     }
-    uint64_t pm = __ballot(pass);
+    uint64_t pm = ballot64(pass);
     if (pm == 0) return;
     if (r.c == 0 && (uint32_t)__popcll(pm) >= kBatchMin) {
         uint32_t h[1] = {pass ? ch : 0xffffffffu};
         uint64_t k[1] = {pass ? ck : ~0ull};
-        r.c = select_sorted<1>(h, k, l_max, lane);
+        r.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)select_sorted<1>(h, k, l_max, lane));
         r.k[0] = k[0];
         r.h[0] = h[0];
         return;
@@ -792,7 +798,7 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_stream_kernel(const uint4
         const uint32_t src = cur.src;
         if (src < num_points) {
             Reservoir<ER> r;
-            r.c = cur.c;
+            r.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)cur.c);
 #pragma unroll
             for (int q = 0; q < ER; ++q) {
                 const bool live = (uint32_t)q * 64u + lane < r.c;
