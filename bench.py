@@ -793,7 +793,7 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
     log(f"hashprune: {count} records -> {num_points} reservoirs, segments {np.mean(ms_seg):.3f} ms, "
         f"records {np.mean(ms_rec):.3f} ms, identical {same}")
     return {
-        "kernels": "hp_seg_count + hp_scan (3) + hp_seg_scatter + hp_merge_large_seg + hp_merge_small_seg",
+        "kernels": "hp_seg_keys + radix sort + run-length encode + scan + hp_seg_gather + hp_merge_stream_kernel",
         "records": int(count),
         "segments": int(nseg),
         "points": int(num_points),

@@ -420,9 +420,9 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                 const uint32_t row_rec = r < n ? (regular ? r * kl : cnt[r]) : 0u;
                 uint32_t hf = 0, hr = 0;
                 bool ok = false;
+                uint32_t cj = kNoKey;
                 if (valid) {
                     // membership of j (leaf_build.rs:1783-1801)
-                    uint32_t cj = kNoKey;
                     for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask) {
                         const uint32_t t = tkey[slot];
                         if (t == j[u]) {
@@ -456,12 +456,6 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                     if (ok) {
                         // forward: its place among the row's valid slots; reverse:
                         // the next free place of j's segment
-                        uint32_t cj = 0;
-                        for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask)
-                            if (tkey[slot] == j[u]) {
-                                cj = tval[slot];
-                                break;
-                            }
                         const uint32_t fpos = cnt[r] + (uint32_t)__popc(half & ((1u << q) - 1u));
                         const uint32_t rpos = atomicAdd(&rev[cj], 1u);
                         store_record(p.out, rec0 + fpos, gi, j[u], hf, db);
