@@ -298,25 +298,47 @@ __global__ __launch_bounds__(1024) void item_plan_kernel(PartArgs a, uint32_t cu
 // LDS as the A operand; each wave keeps 32 rows' codes in VGPRs as B.  Per
 // 32-leader tile the distances go through LDS so one lane per row can apply
 // the order-dependent insertion in leader-slot order.
-constexpr int kCountWaves = 4;
-constexpr int kCountThreads = 256;
-constexpr int kCountChunk = kCountWaves * 32;  // rows per chunk
-constexpr int kCountChunks = kPartItemRows / kCountChunk;
+// waves of a COUNT workgroup: 8 (two per SIMD) when their distance buffers
+// fit beside the leaders, else 4
+template <int KS>
+constexpr int count_waves() {
+    return (KS * 32 + 16) * 128 + 5 * 128 * 4 + 8 * 32 * 33 * 4 <= 160 * 1024 ? 8 : 4;
+}
+constexpr uint32_t kCountGrid = 512;  // persistent COUNT grid (items are taken grid-stride)
 
 template <int KS>
 struct CountLayout {
+    static constexpr int kWaves = count_waves<KS>();
+    static constexpr int kThreads = kWaves * 64;
+    static constexpr int kChunk = kWaves * 32;  // rows per chunk
+    static constexpr int kChunks = kPartItemRows / kChunk;
     static constexpr int kStride = KS * 32 + 16;
     static constexpr int kLeaderBytes = kPartMaxLeaders * kStride;
     static constexpr int kMetaOff = kLeaderBytes;  // scales, norms, ids [128] each
     static constexpr int kCntOff = kMetaOff + 3 * kPartMaxLeaders * 4;
     static constexpr int kDistOff = kCntOff + kPartMaxLeaders * 4;
-    static constexpr int kBytes = kDistOff + kCountWaves * 32 * 33 * 4;
+    static constexpr int kBytes = kDistOff + kWaves * 32 * 33 * 4;
     static_assert(kBytes <= 160 * 1024, "LDS budget");
+    static_assert(kPartItemRows % kChunk == 0, "item rows");
 };
 
+// LDS hand-off inside one wave: its lanes' LDS writes are seen by its other
+// lanes' later reads (and reads finish before later writes).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Persistent over the level's items: a workgroup takes items blockIdx.x,
+// + gridDim.x, ...; the leaders of an item's node are staged in LDS only when
+// the node differs from the previous item's (a large node's items reuse them).
+// Each wave owns 32 rows at a time and its own distance buffer, so inside an
+// item the waves only synchronise with themselves.
 template <int KS>
-__global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+__global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(PartArgs a, uint32_t cur,
+                                                                             uint32_t level_nodes) {
     using L = CountLayout<KS>;
+    constexpr uint32_t kThr = L::kThreads;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int8_t *lcodes = reinterpret_cast<int8_t *>(smem);
     float *ls = reinterpret_cast<float *>(smem + L::kMetaOff);
@@ -326,143 +348,152 @@ __global__ __launch_bounds__(kCountThreads, 1) void count_kernel(PartArgs a, uin
     float *dbuf = reinterpret_cast<float *>(smem + L::kDistOff);
     __shared__ uint32_t s_node;
 
-    const uint32_t item = blockIdx.x;
-    if (item >= a.hdr->items) return;
-    if (threadIdx.x == 0) s_node = find_item_node(a.nodes[cur], level_nodes, item);
-    __syncthreads();
-    const uint32_t ni = s_node;
-    const NodeDesc *nd = a.nodes[cur] + ni;
-    if (nd->status != kNodeCounting) return;
-    const uint32_t n = nd->n;
-    const uint32_t nl = nd->num_leaders;
-    const uint32_t fanout = nd->fanout;
-    const uint64_t row_start = nd->row_start;
-    const uint32_t first = (item - nd->item_base) * kPartItemRows;
+    const uint32_t items = a.hdr->items;
     const uint32_t pd = a.padded_dim;
-    const uint32_t *node_leaders = a.leaders + (uint64_t)ni * kPartMaxLeaders;
     const uint32_t tid = threadIdx.x;
-
-    // resident row -> SQ8 row; tie keys use the row's index within its root
-    const uint32_t *rmap = a.row_map;
-    const uint32_t rb = (uint32_t)nd->root_base;
-    for (uint32_t q = tid; q < (uint32_t)kPartMaxLeaders * KS * 2; q += kCountThreads) {
-        const uint32_t li = q / (KS * 2);
-        const uint32_t off = (q % (KS * 2)) * 16u;
-        v4i z = {0, 0, 0, 0};
-        if (li < nl && off < pd) {
-            const uint32_t g = node_leaders[li];
-            if (g < a.rows) z = *reinterpret_cast<const v4i *>(a.codes + (uint64_t)(rmap ? rmap[g] : g) * pd + off);
-        }
-        *reinterpret_cast<v4i *>(lcodes + li * L::kStride + off) = z;
-    }
-    for (uint32_t li = tid; li < (uint32_t)kPartMaxLeaders; li += kCountThreads) {
-        uint32_t g = li < nl ? node_leaders[li] : rb;
-        if (li < nl && g >= a.rows) {
-            pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_LEADER_ID);
-            g = rb;
-        }
-        const uint32_t sg = rmap ? rmap[g] : g;
-        ls[li] = li < nl ? a.scales[sg] : 0.0f;
-        ln[li] = li < nl ? a.norms[sg] : 0.0f;
-        lid[li] = g - rb;
-        cnt[li] = 0u;
-    }
-    __syncthreads();
-
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
     const uint32_t j = lane & 31u;
     const uint32_t h = lane >> 5;
-    const uint32_t ntiles = (nl + 31) / 32;
     const uint32_t *arena = a.arena[cur];
+    // resident row -> SQ8 row; tie keys use the row's index within its root
+    const uint32_t *rmap = a.row_map;
+    uint32_t staged = 0xffffffffu;  // node whose leaders are in LDS
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+        if (tid == 0) s_node = find_item_node(a.nodes[cur], level_nodes, item);
+        __syncthreads();
+        const uint32_t ni = s_node;
+        const NodeDesc *nd = a.nodes[cur] + ni;
+        if (nd->status != kNodeCounting) {
+            __syncthreads();  // s_node is rewritten by the next item
+            continue;
+        }
+        const uint32_t n = nd->n;
+        const uint32_t nl = nd->num_leaders;
+        const uint32_t fanout = nd->fanout;
+        const uint64_t row_start = nd->row_start;
+        const uint32_t first = (item - nd->item_base) * kPartItemRows;
+        const uint32_t rb = (uint32_t)nd->root_base;
+        if (ni != staged) {
+            const uint32_t *node_leaders = a.leaders + (uint64_t)ni * kPartMaxLeaders;
+            for (uint32_t q = tid; q < (uint32_t)kPartMaxLeaders * KS * 2; q += kThr) {
+                const uint32_t li = q / (KS * 2);
+                const uint32_t off = (q % (KS * 2)) * 16u;
+                v4i z = {0, 0, 0, 0};
+                if (li < nl && off < pd) {
+                    const uint32_t g = node_leaders[li];
+                    if (g < a.rows)
+                        z = *reinterpret_cast<const v4i *>(a.codes + (uint64_t)(rmap ? rmap[g] : g) * pd + off);
+                }
+                *reinterpret_cast<v4i *>(lcodes + li * L::kStride + off) = z;
+            }
+            for (uint32_t li = tid; li < (uint32_t)kPartMaxLeaders; li += kThr) {
+                uint32_t g = li < nl ? node_leaders[li] : rb;
+                if (li < nl && g >= a.rows) {
+                    pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_LEADER_ID);
+                    g = rb;
+                }
+                const uint32_t sg = rmap ? rmap[g] : g;
+                ls[li] = li < nl ? a.scales[sg] : 0.0f;
+                ln[li] = li < nl ? a.norms[sg] : 0.0f;
+                lid[li] = g - rb;
+            }
+            staged = ni;
+        }
+        for (uint32_t li = tid; li < (uint32_t)kPartMaxLeaders; li += kThr) cnt[li] = 0u;
+        __syncthreads();
 
-    for (int ch = 0; ch < kCountChunks; ++ch) {
-        if (first + ch * kCountChunk >= n) break;  // uniform across the block
-        const uint32_t m = first + ch * kCountChunk + wave * 32u + j;
-        bool ok = m < n;
-        uint32_t pt = ok ? arena[row_start + m] : rb;
-        if (ok && pt >= a.rows) {
-            pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_POINT_ID);
-            ok = false;
-            pt = rb;
-        }
-        const uint32_t spt = rmap ? rmap[pt] : pt;
-        v4i bfrag[KS];
-        const int8_t *mc = a.codes + (uint64_t)spt * pd;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const uint32_t off = 32u * s + 16u * h;
-            v4i z = {0, 0, 0, 0};
-            if (ok && off < pd) z = *reinterpret_cast<const v4i *>(mc + off);
-            bfrag[s] = z;
-        }
-        const float ps = ok ? a.scales[spt] : 0.0f;
-        const float pn = ok ? a.norms[spt] : 0.0f;
-        const uint32_t lpt = pt - rb;  // the row's index within its root
-        // compute_backend.rs:6357-6368 reset: (FLT_MAX, empty)
-        float bd[4] = {kEmptyDist, kEmptyDist, kEmptyDist, kEmptyDist};
-        uint32_t bs[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
-        uint32_t bl[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            v16i acc = {};
-            const int8_t *arow = lcodes + (32u * t + j) * L::kStride + 16u * h;
+        const uint32_t ntiles = (nl + 31) / 32;
+        float *wb = dbuf + wave * 32 * 33;
+        for (int ch = 0; ch < L::kChunks; ++ch) {
+            if (first + ch * L::kChunk >= n) break;  // uniform across the block
+            const uint32_t m = first + ch * L::kChunk + wave * 32u + j;
+            bool ok = m < n;
+            uint32_t pt = ok ? arena[row_start + m] : rb;
+            if (ok && pt >= a.rows) {
+                pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_POINT_ID);
+                ok = false;
+                pt = rb;
+            }
+            if (__ballot(ok) == 0ull) continue;  // this wave's rows are past the node's end
+            const uint32_t spt = rmap ? rmap[pt] : pt;
+            v4i bfrag[KS];
+            const int8_t *mc = a.codes + (uint64_t)spt * pd;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const v4i av = *reinterpret_cast<const v4i *>(arow + 32 * s);
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bfrag[s], acc, 0, 0, 0);
+                const uint32_t off = 32u * s + 16u * h;
+                v4i z = {0, 0, 0, 0};
+                if (ok && off < pd) z = *reinterpret_cast<const v4i *>(mc + off);
+                bfrag[s] = z;
             }
-            float *wb = dbuf + wave * 32 * 33;
+            const float ps = ok ? a.scales[spt] : 0.0f;
+            const float pn = ok ? a.norms[spt] : 0.0f;
+            const uint32_t lpt = pt - rb;  // the row's index within its root
+            // compute_backend.rs:6357-6368 reset: (FLT_MAX, empty)
+            float bd[4] = {kEmptyDist, kEmptyDist, kEmptyDist, kEmptyDist};
+            uint32_t bs[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
+            uint32_t bl[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
+            for (uint32_t t = 0; t < ntiles; ++t) {
+                v16i acc = {};
+                const int8_t *arow = lcodes + (32u * t + j) * L::kStride + 16u * h;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
-                const uint32_t gl = 32u * t + li;
-                wb[li * 33 + j] = gl < nl ? assign_l2(acc[v], ps, pn, ls[gl], ln[gl]) : kEmptyDist;
+                for (int s = 0; s < KS; ++s) {
+                    const v4i av = *reinterpret_cast<const v4i *>(arow + 32 * s);
+                    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bfrag[s], acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
+                    const uint32_t gl = 32u * t + li;
+                    wb[li * 33 + j] = gl < nl ? assign_l2(acc[v], ps, pn, ls[gl], ln[gl]) : kEmptyDist;
+                }
+                wave_lds_sync();
+                if (h == 0u && ok) {
+                    const uint32_t lim = (nl - 32u * t) < 32u ? (nl - 32u * t) : 32u;
+                    auto run = [&](auto fc) {
+                        constexpr int F = decltype(fc)::value;
+                        for (uint32_t li = 0; li < lim; ++li) {
+                            const uint32_t slot = 32u * t + li;
+                            insert_slot<F>(wb[li * 33 + j], lpt, lid[slot], slot, bd, bs, bl);
+                        }
+                    };
+                    switch (fanout) {
+                        case 1: run(std::integral_constant<int, 1>{}); break;
+                        case 2: run(std::integral_constant<int, 2>{}); break;
+                        case 3: run(std::integral_constant<int, 3>{}); break;
+                        default: run(std::integral_constant<int, 4>{}); break;
+                    }
+                }
+                wave_lds_sync();
             }
-            __syncthreads();
             if (h == 0u && ok) {
-                const uint32_t lim = (nl - 32u * t) < 32u ? (nl - 32u * t) : 32u;
-                auto run = [&](auto fc) {
-                    constexpr int F = decltype(fc)::value;
-                    for (uint32_t li = 0; li < lim; ++li) {
-                        const uint32_t slot = 32u * t + li;
-                        insert_slot<F>(wb[li * 33 + j], lpt, lid[slot], slot, bd, bs, bl);
-                    }
-                };
-                switch (fanout) {
-                    case 1: run(std::integral_constant<int, 1>{}); break;
-                    case 2: run(std::integral_constant<int, 2>{}); break;
-                    case 3: run(std::integral_constant<int, 3>{}); break;
-                    default: run(std::integral_constant<int, 4>{}); break;
-                }
-            }
-            __syncthreads();
-        }
-        if (h == 0u && ok) {
-            uint32_t packed = 0xffffffffu;
+                uint32_t packed = 0xffffffffu;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) {
-                if (k < fanout) {
-                    const uint32_t s = bs[k];
-                    if (s < nl) {
-                        packed = (packed & ~(0xffu << (8u * k))) | (s << (8u * k));
-                        atomicAdd(&cnt[s], 1u);
-                    } else {
-                        pc_flag(a.counters, TESSA_OVF_QUEUE_ROW);
+                for (uint32_t k = 0; k < 4; ++k) {
+                    if (k < fanout) {
+                        const uint32_t s = bs[k];
+                        if (s < nl) {
+                            packed = (packed & ~(0xffu << (8u * k))) | (s << (8u * k));
+                            atomicAdd(&cnt[s], 1u);
+                        } else {
+                            pc_flag(a.counters, TESSA_OVF_QUEUE_ROW);
+                        }
                     }
                 }
+                a.slots[row_start + m] = packed;
             }
-            a.slots[row_start + m] = packed;
         }
-    }
-    __syncthreads();
-    for (uint32_t s = tid; s < nl; s += kCountThreads) {
-        const uint32_t c = cnt[s];
-        a.item_counts[(uint64_t)item * kPartMaxLeaders + s] = c;
-        if (c) atomicAdd(&a.child_counts[(uint64_t)ni * kPartMaxLeaders + s], c);
-    }
-    if (tid == 0) {
-        const uint32_t rows_here = (n - first) < kPartItemRows ? (n - first) : kPartItemRows;
-        pc_add(a.counters, TESSA_P_LARGE_PHYSICAL_TILES, (rows_here + 15u) / 16u);
+        __syncthreads();
+        for (uint32_t s = tid; s < nl; s += kThr) {
+            const uint32_t c = cnt[s];
+            a.item_counts[(uint64_t)item * kPartMaxLeaders + s] = c;
+            if (c) atomicAdd(&a.child_counts[(uint64_t)ni * kPartMaxLeaders + s], c);
+        }
+        if (tid == 0) {
+            const uint32_t rows_here = (n - first) < kPartItemRows ? (n - first) : kPartItemRows;
+            pc_add(a.counters, TESSA_P_LARGE_PHYSICAL_TILES, (rows_here + 15u) / 16u);
+        }
+        __syncthreads();  // cnt and s_node are reused by the next item
     }
 }
 
@@ -1120,7 +1151,9 @@ int launch_count_ks(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint3
             return -1;
         attr = true;
     }
-    hipLaunchKernelGGL(count_kernel<KS>, dim3(grid), dim3(kCountThreads), L::kBytes, s, a, cur, level_nodes);
+    // persistent: at most two workgroups' worth of items per CU at a time
+    const uint32_t g = grid < kCountGrid ? grid : kCountGrid;
+    hipLaunchKernelGGL(count_kernel<KS>, dim3(g), dim3(L::kThreads), L::kBytes, s, a, cur, level_nodes);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
