@@ -694,7 +694,10 @@ tessa_status tessa_graph_pack(const uint32_t *targets, const uint32_t *counts, u
  * them, and an SQ8 upload clears them.  Ids are translated to global ids
  * when the run ends, so they name the resident set that run used.  With
  * submissions, fetch after tessa_session_wait of the job whose passes are
- * wanted and before the next job is submitted. */
+ * wanted and before the next job is submitted.  A run records at most 2^27 member and
+ * leader ids (512 MB of host memory); passes past that bound are not
+ * recorded (the reference's in-kernel sampler keeps a bounded set per bin;
+ * here the host sampler chooses among what was recorded). */
 typedef struct tessa_captured_assignment {
     uint32_t depth, retry, r_h, padded_dim, member_count, leader_count;
     uint64_t member_offset, leader_offset;  /* into ids[] */

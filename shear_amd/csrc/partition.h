@@ -134,6 +134,8 @@ struct PartCaptureTask {
 };
 struct PartCapture {
     uint32_t min_members = 256;
+    uint64_t max_rows = 1ull << 27;  // host bound: members + leaders kept per run (512 MB)
+    uint64_t dropped_tasks = 0;      // passes past max_rows, not recorded
     std::vector<PartCaptureTask> tasks;
     std::vector<uint32_t> rows;  // members then leaders of each task, resident rows
 };

@@ -1197,19 +1197,24 @@ static int capture_level(const PartArgs &a, hipStream_t s, uint32_t cur, uint32_
     };
     const size_t first_task = cap->tasks.size();
     uint64_t total = cap->rows.size();
+    std::vector<uint32_t> picked;  // node of each task recorded at this level
     for (uint32_t ni = 0; ni < level_nodes; ++ni) {
         const NodeDesc &nd = nodes[ni];
         if (!wanted(nd)) continue;
+        if (total + nd.n + nd.num_leaders > cap->max_rows) {
+            cap->dropped_tasks += 1;  // host memory bound reached: the pass is not recorded
+            continue;
+        }
         PartCaptureTask t{nd.depth, nd.attempt, nd.fanout, nd.n, nd.num_leaders, total, total + nd.n};
         total += (uint64_t)nd.n + nd.num_leaders;
         cap->tasks.push_back(t);
+        picked.push_back(ni);
     }
     cap->rows.resize(total);
-    size_t ti = first_task;
-    for (uint32_t ni = 0; ni < level_nodes; ++ni) {
+    for (size_t i = 0; i < picked.size(); ++i) {
+        const uint32_t ni = picked[i];
         const NodeDesc &nd = nodes[ni];
-        if (!wanted(nd)) continue;
-        const PartCaptureTask &t = cap->tasks[ti++];
+        const PartCaptureTask &t = cap->tasks[first_task + i];
         if (hipMemcpyAsync(cap->rows.data() + t.member_offset, a.arena[cur] + nd.row_start, nd.n * 4ull,
                            hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipMemcpyAsync(cap->rows.data() + t.leader_offset, a.leaders + (uint64_t)ni * kPartMaxLeaders,
