@@ -267,12 +267,13 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     small = [c for c in children if c not in large_set]
 
     # many-root runs over groups of large children
-    group = []
+    group, group_rows = [], 0
     for gi, c in enumerate(large):
         group.append(c)
-        if gi + 1 == len(large) or sum(int(sizes[g]) for g in group) + int(sizes[large[gi + 1]]) > p.roots_rows_per_run:
+        group_rows += int(sizes[c])
+        if gi + 1 == len(large) or group_rows + int(sizes[large[gi + 1]]) > p.roots_rows_per_run:
             _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, rows, p, sp, st, emit, consume, observer)
-            group = []
+            group, group_rows = [], 0
 
     # small children one by one
     for c in small:
