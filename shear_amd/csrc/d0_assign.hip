@@ -12,8 +12,11 @@
 // fragments row-major (child = leader index, point = global id, :18503-18510).
 //
 // Here one pass replaces partial + merge: a wave holds 32 rows' codes in VGPRs
-// as the MFMA B operand and streams the leaders 32 at a time as A (codes read
-// from L2: a leader tile is shared by every wave); each lane owns one row and
+// as the MFMA B operand and streams the leaders 32 at a time as A.  The eight
+// waves of a workgroup (256 rows) share each leader tile through LDS (double
+// buffered; the next tile's codes, scales, norms and ranks are loaded into
+// registers while the current one is used), so a tile crosses L2 once per
+// 256 rows instead of once per 32; each lane owns one row and
 // half of a tile's leaders and keeps its best F >= fanout (distance bits << 32
 // | leader rank) keys sorted in registers, inserting a candidate only when it
 // beats the current F-th.  The two halves of a row merge at the end.  A
@@ -34,7 +37,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;  // 256 rows per workgroup share each leader tile
 constexpr int kThreads = kWaves * 64;
 constexpr uint64_t kNoKey = ~0ull;
 
@@ -63,13 +66,26 @@ __device__ __forceinline__ void insert_key(uint64_t (&best)[F], uint64_t key) {
     }
 }
 
+template <int KS>
+struct D0Tile {
+    static constexpr int kStride = KS * 32 + 16;          // bytes per leader row (16-byte pad: no bank aliasing)
+    static constexpr int kCodeBytes = 32 * kStride;
+    static constexpr int kChunks = 32 * KS * 2;           // 16-byte chunks of the tile's codes
+    static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kBytes = kCodeBytes + 32 * 12;  // + scales, norms, ranks
+};
+
 template <int KS, int F>
 __global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    using T = D0Tile<KS>;
+    extern __shared__ __attribute__((aligned(16))) int8_t tiles[];  // 2 x T::kBytes
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t j = lane & 31u, h = lane >> 5;
     const uint64_t row = (uint64_t)blockIdx.x * (kWaves * 32) + wave * 32u + j;
     const bool ok = row < p.rows;
     const uint32_t pd = p.padded_dim;
+    const uint32_t nl = p.leaders;
 
     v4i bfrag[KS];
     const int8_t *rc = p.codes + (ok ? row : 0ull) * pd;
@@ -87,25 +103,68 @@ __global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
 #pragma unroll
     for (int s = 0; s < F; ++s) best[s] = kNoKey;
 
-    const uint32_t ntiles = (p.leaders + 31u) / 32u;
+    // the next tile in registers: this thread's code chunks and one meta word
+    v4i pre[T::kPerThread];
+    uint32_t pmeta = 0u;
+    auto issue = [&](uint32_t t) {
+#pragma unroll
+        for (int q = 0; q < T::kPerThread; ++q) {
+            const uint32_t c = tid + (uint32_t)q * kThreads;
+            const uint32_t li = c / (KS * 2), off = (c % (KS * 2)) * 16u;
+            const uint32_t l = 32u * t + li;
+            v4i z = {0, 0, 0, 0};
+            if (c < (uint32_t)T::kChunks && l < nl && off < pd)
+                z = *reinterpret_cast<const v4i *>(p.leader_codes + (uint64_t)l * pd + off);
+            pre[q] = z;
+        }
+        if (tid < 96u) {
+            const uint32_t l = 32u * t + (tid & 31u);
+            const uint32_t li = l < nl ? l : 0u;
+            pmeta = tid < 32u ? __float_as_uint(p.leader_scales[li])
+                              : tid < 64u ? __float_as_uint(p.leader_norms[li]) : p.leader_rank[li];
+        }
+    };
+    auto store = [&](int8_t *dst) {
+#pragma unroll
+        for (int q = 0; q < T::kPerThread; ++q) {
+            const uint32_t c = tid + (uint32_t)q * kThreads;
+            if (c < (uint32_t)T::kChunks) {
+                const uint32_t li = c / (KS * 2), off = (c % (KS * 2)) * 16u;
+                *reinterpret_cast<v4i *>(dst + li * T::kStride + off) = pre[q];
+            }
+        }
+        if (tid < 96u) reinterpret_cast<uint32_t *>(dst + T::kCodeBytes)[tid] = pmeta;
+    };
+
+    const uint32_t ntiles = (nl + 31u) / 32u;
+    issue(0);
+    store(tiles);
+    if (ntiles > 1u) issue(1);
     for (uint32_t t = 0; t < ntiles; ++t) {
-        const uint32_t la = 32u * t + j;  // this lane's A row (leader)
-        const int8_t *lc = p.leader_codes + (uint64_t)(la < p.leaders ? la : 0u) * pd;
+        // tile t is in buffer t & 1; the other buffer was last read at t - 1
+        __syncthreads();
+        int8_t *cur = tiles + (t & 1u) * T::kBytes;
+        if (t + 1u < ntiles) {
+            store(tiles + ((t + 1u) & 1u) * T::kBytes);
+            if (t + 2u < ntiles) issue(t + 2u);
+        }
+        const int8_t *arow = cur + j * T::kStride + 16u * h;
         v16i acc = {};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            const uint32_t off = 32u * s + 16u * h;
-            v4i a = {0, 0, 0, 0};
-            if (la < p.leaders && off < pd) a = *reinterpret_cast<const v4i *>(lc + off);
+            const v4i a = *reinterpret_cast<const v4i *>(arow + 32 * s);
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
         }
+        const float *tsc = reinterpret_cast<const float *>(cur + T::kCodeBytes);
+        const float *tno = tsc + 32;
+        const uint32_t *trk = reinterpret_cast<const uint32_t *>(tno + 32);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const uint32_t l = 32u * t + 8u * (v / 4) + 4u * h + (v % 4);
-            const bool live = ok && l < p.leaders;
-            const uint32_t li = live ? l : 0u;
-            const float d = assign_l2(acc[v], rs, rn, p.leader_scales[li], p.leader_norms[li]);
-            const uint64_t key = live ? (((uint64_t)__float_as_uint(d) << 32) | p.leader_rank[li]) : kNoKey;
+            const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
+            const uint32_t l = 32u * t + li;
+            const bool live = ok && l < nl;
+            const float d = assign_l2(acc[v], rs, rn, tsc[li], tno[li]);
+            const uint64_t key = live ? (((uint64_t)__float_as_uint(d) << 32) | trk[li]) : kNoKey;
             if (key < best[F - 1]) insert_key<F>(best, key);
         }
     }
@@ -129,16 +188,29 @@ __global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
     }
 }
 
+template <int KS, int F>
+int launch_kf(const D0AssignParams &p, dim3 grid, hipStream_t stream) {
+    constexpr int lds = 2 * D0Tile<KS>::kBytes;
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&d0_assign_kernel<KS, F>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return -1;
+        attr = true;
+    }
+    hipLaunchKernelGGL((d0_assign_kernel<KS, F>), grid, dim3(kThreads), lds, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <int KS>
 int launch_ks(const D0AssignParams &p, hipStream_t stream) {
     const uint64_t blocks = (p.rows + kWaves * 32 - 1) / (kWaves * 32);
     if (blocks > 0x7fffffffull) return -2;
-    const dim3 grid((uint32_t)blocks), block(kThreads);
-    if (p.fanout <= 4) hipLaunchKernelGGL((d0_assign_kernel<KS, 4>), grid, block, 0, stream, p);
-    else if (p.fanout <= 8) hipLaunchKernelGGL((d0_assign_kernel<KS, 8>), grid, block, 0, stream, p);
-    else if (p.fanout <= 16) hipLaunchKernelGGL((d0_assign_kernel<KS, 16>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((d0_assign_kernel<KS, 32>), grid, block, 0, stream, p);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    const dim3 grid((uint32_t)blocks);
+    if (p.fanout <= 4) return launch_kf<KS, 4>(p, grid, stream);
+    if (p.fanout <= 8) return launch_kf<KS, 8>(p, grid, stream);
+    if (p.fanout <= 16) return launch_kf<KS, 16>(p, grid, stream);
+    return launch_kf<KS, 32>(p, grid, stream);
 }
 
 __global__ void d0_hist_kernel(const uint32_t *child, uint64_t n, uint64_t *counts) {

@@ -136,9 +136,17 @@ def entry_point(child_offsets: np.ndarray, child_points: np.ndarray) -> int:
     """First point of the largest D0 child (ties: the smaller point id)."""
     offs = np.asarray(child_offsets, np.int64)
     sizes = np.diff(offs)
+    firsts = np.zeros(len(sizes), np.int64)
+    nz = np.nonzero(sizes > 0)[0]
+    firsts[nz] = np.asarray(child_points)[offs[nz]]
+    return _entry_point_of(sizes, firsts)
+
+
+def _entry_point_of(sizes: np.ndarray, firsts: np.ndarray) -> int:
+    """entry_point from the child sizes and each non-empty child's first point."""
     best = None
     for c in np.nonzero(sizes > 0)[0]:
-        cand = (int(sizes[c]), -int(child_points[offs[c]]))
+        cand = (int(sizes[c]), -int(firsts[c]))
         if best is None or cand > best:
             best = cand
     return -best[1] if best is not None else 0
@@ -224,8 +232,11 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     _, _, offs, pts = D.global_d0_assign(sq8, gids, lead, gids[lrows].contiguous(), p.fanout_top)
     del lead
     offs_h = offs.cpu().numpy()
-    pts_h = pts.cpu().numpy().view(np.uint32)
-    start = entry_point(offs_h, pts_h)
+    # the entry point needs each child's first point only (not the whole point list)
+    osz = np.diff(offs_h.astype(np.int64))
+    fidx = torch.from_numpy(np.minimum(offs_h[:-1].astype(np.int64), max(pts.numel() - 1, 0))).to(dev)
+    firsts = pts[fidx].cpu().numpy().view(np.uint32) if pts.numel() else np.zeros(len(osz), np.uint32)
+    start = _entry_point_of(osz, firsts)
     torch.cuda.synchronize()
     torch.cuda.empty_cache()  # the library allocates the reservoirs and workspaces itself, outside torch's cache
     w1 = time.perf_counter()
