@@ -155,17 +155,26 @@ __global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
             const v4i a = *reinterpret_cast<const v4i *>(arow + 32 * s);
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bfrag[s], acc, 0, 0, 0);
         }
-        const float *tsc = reinterpret_cast<const float *>(cur + T::kCodeBytes);
-        const float *tno = tsc + 32;
-        const uint32_t *trk = reinterpret_cast<const uint32_t *>(tno + 32);
+        // lane value v is leader 8*(v/4) + 4h + v%4 of the tile: four consecutive
+        // leaders per group, their scales / norms / ranks read as 16-byte vectors
+        const float4 *tsc = reinterpret_cast<const float4 *>(cur + T::kCodeBytes);
+        const float4 *tno = tsc + 8;
+        const uint4 *trk = reinterpret_cast<const uint4 *>(tno + 8);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
-            const uint32_t l = 32u * t + li;
-            const bool live = ok && l < nl;
-            const float d = assign_l2(acc[v], rs, rn, tsc[li], tno[li]);
-            const uint64_t key = live ? (((uint64_t)__float_as_uint(d) << 32) | trk[li]) : kNoKey;
-            if (key < best[F - 1]) insert_key<F>(best, key);
+        for (int g = 0; g < 4; ++g) {
+            const float4 sc4 = tsc[2 * g + h], no4 = tno[2 * g + h];
+            const uint4 rk4 = trk[2 * g + h];
+            const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w}, nov[4] = {no4.x, no4.y, no4.z, no4.w};
+            const uint32_t rkv[4] = {rk4.x, rk4.y, rk4.z, rk4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int v = 4 * g + e;
+                const uint32_t l = 32u * t + 8u * g + 4u * h + e;
+                const bool live = ok && l < nl;
+                const float d = assign_l2(acc[v], rs, rn, scv[e], nov[e]);
+                const uint64_t key = live ? (((uint64_t)__float_as_uint(d) << 32) | rkv[e]) : kNoKey;
+                if (key < best[F - 1]) insert_key<F>(best, key);
+            }
         }
     }
     // merge the other half-wave's list into lanes 0..31
