@@ -391,18 +391,37 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p
     k = p.leaf_knn
     leaf_max = max(256, p.c_max)
     ends = starts + lsz
+    chunks = []
     l0 = 0
     while l0 < lc:
         # leaves [l0, l1) with at most leaf_chunk_rows rows (at least one leaf)
         l1 = int(np.searchsorted(ends, starts[l0] + p.leaf_chunk_rows, side="right"))
         l1 = max(l1, l0 + 1)
+        chunks.append((l0, l1))
+        l0 = l1
+    # The leaf operator of chunk i + 1 is queued on its own stream before the
+    # host waits for chunk i's record emission and merge (both synchronise the
+    # caller's stream), so the GPU is not left idle while the host works.
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)  # default priority
+
+    def launch(l0, l1):
         r0, r1 = int(starts[l0]), int(ends[l1 - 1])
         off = ro.leaf_starts[l0:l1]
         lay = T.LeafLayouts(ro.leaf_rows, off, ro.leaf_sizes[l0:l1], (off - r0) * k, leaf_max, (r1 - r0) * k)
+        side.wait_stream(main)  # the layout tensors above were made on the caller's stream
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        ids, d, ctr = T.leaf_topk(sq8, gids, lay, k, executor=sp.executor)
-        e1.record()
+        with torch.cuda.stream(side):
+            e0.record(side)
+            ids, d, ctr = T.leaf_topk(sq8, gids, lay, k, executor=sp.executor, stream=side)
+            e1.record(side)
+        return l0, l1, r0, r1, off, lay, ids, d, ctr, e0, e1
+
+    def finish(job):
+        l0, l1, r0, r1, off, lay, ids, d, ctr, e0, e1 = job
+        main.wait_event(e1)
+        for t in (ids, d, ctr):
+            t.record_stream(main)  # used on the caller's stream from here on
         T.raise_on_overflow(ctr, "leaf top-k")
         st["leaf_ms"] += e0.elapsed_time(e1)
         q0 = time.perf_counter()
@@ -419,6 +438,15 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p
         st["records"] += int(cnt)
         st["leaves"] += l1 - l0
         st["leaf_rows"] += r1 - r0
-        del rec, segs, ids, d, lay, off
-        l0 = l1
+
+    pending = None
+    for l0, l1 in chunks:
+        job = launch(l0, l1)
+        if pending is not None:
+            finish(pending)
+        pending = job
+        del job
+    if pending is not None:
+        finish(pending)
+    main.wait_stream(side)
 
