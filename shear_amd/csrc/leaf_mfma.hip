@@ -150,18 +150,19 @@ __device__ __forceinline__ v16i mfma_block(const int8_t *arow, const v4i (&bfrag
     return acc;
 }
 
-// Compare-exchange number c (0..79) of the bitonic sort of 16 values: stage
-// c/8 of (k, j) = (2,1) (4,2) (4,1) (8,4) (8,2) (8,1) (16,8) (16,4) (16,2)
-// (16,1); within a stage the (c%8)-th index i with i&j == 0 pairs with i+j.
-__host__ __device__ constexpr int sort16_k(int c) {
-    return c < 8 ? 2 : c < 24 ? 4 : c < 48 ? 8 : 16;
-}
-__host__ __device__ constexpr int sort16_j(int c) {
-    return c < 8 ? 1 : c < 24 ? (2 >> ((c - 8) / 8)) : c < 48 ? (4 >> ((c - 24) / 8)) : (8 >> ((c - 48) / 8));
-}
+// Compare-exchange c of a bitonic merge stage over 16 values (8 per stage,
+// distance j): the (c%8)-th index i with i&j == 0 pairs with i+j.
 __host__ __device__ constexpr int ce_low(int c, int jj) {
     return ((c % 8) / jj) * 2 * jj + (c % 8) % jj;
 }
+// Compare-exchange number c (0..23) of the bitonic sort of 8 values: stage
+// c/4 of (k, j) = (2,1) (4,2) (4,1) (8,4) (8,2) (8,1); within a stage the
+// (c%4)-th index i with i&j == 0 pairs with i+j.
+__host__ __device__ constexpr int sort8_k(int c) { return c < 4 ? 2 : c < 12 ? 4 : 8; }
+__host__ __device__ constexpr int sort8_j(int c) {
+    return c < 4 ? 1 : c < 12 ? (2 >> ((c - 4) / 4)) : (4 >> ((c - 12) / 4));
+}
+__host__ __device__ constexpr int ce_low8(int c, int jj) { return ((c % 4) / jj) * 2 * jj + (c % 4) % jj; }
 
 // x unchanged, but opaque to the optimizer: conditions derived from it are
 // evaluated where they are used, inside the work-item loop, instead of being
@@ -431,9 +432,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         // epilogue of position i-1 (its accumulators held over) runs in the
         // same straight-line block as position i's MFMAs, so the VALU work
         // overlaps the matrix pipe.
-        //  * phase A epilogue: each lane keeps the 16 smallest exact distances
-        //    it sees (values only); F is the pair's kSel-th smallest sample
-        //    distance plus 3 eps, so at least kSel candidates lie at or below F;
+        //  * phase A epilogue: of each sampled tile a lane takes the minimum of
+        //    each adjacent pair of its 16 exact distances and keeps the 16
+        //    smallest of those minima (values only); F is the pair's kSel-th
+        //    smallest kept distance plus 3 eps, so at least kSel candidates
+        //    lie at or below F (any real distances give a valid F);
         //  * phase B epilogue: a 16-bit mask of the lane's candidates meeting
         //    cs*dot >= tau, and the raw dots parked in the wave's LDS scratch;
         //    the next position drains the mask (set bits only) into the lane's
@@ -454,11 +457,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         constexpr uint32_t kAhead = NB / 2;  // positions between a tile's store and its use
         int *const scr = reinterpret_cast<int *>(tile + NB * L::kTileBytes) + wave * (16u * 64u);
 
-        // Phase A epilogue units (148): per group of 4 candidates one LDS read
-        // of their scales and norms and 4 exact distances (20), the 80
-        // compare-exchanges of a bitonic sort, 16 minima against the kept
-        // samples and the 32 of their bitonic merge.
-        constexpr int kSampleUnits = 20 + 80 + 16 + 32;
+        // Phase A epilogue units (92): per group of 4 candidates one LDS read
+        // of their scales and norms and 4 exact distances (20), 8 pair
+        // minima, the 24 compare-exchanges of their bitonic sort, 8 minima
+        // against the kept samples and the 32 of their bitonic merge.
+        constexpr int kSampleUnits = 20 + 8 + 24 + 8 + 32;
         float4 ep_cs[4], ep_cn[4];
         // scale and norm arrays start 16-byte aligned; each group of 4 is a float4
         const float *cs_al = static_cast<const float *>(__builtin_assume_aligned(cs_lds, 16));
@@ -489,15 +492,21 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                         ep_v[vi] = d;
                     }
                 }
-            } else if constexpr (W < 100) {
-                constexpr int c = W - 20, k = sort16_k(c), jj = sort16_j(c), lo = ce_low(c, jj);
+            } else if constexpr (W < 28) {
+                constexpr int i = W - 20;  // pair minima, in place (ep_v[2i], ep_v[2i+1] are still unread)
+                ep_v[i] = fminf(ep_v[2 * i], ep_v[2 * i + 1]);
+            } else if constexpr (W < 52) {
+                constexpr int c = W - 28, k = sort8_k(c), jj = sort8_j(c), lo = ce_low8(c, jj);
                 if constexpr ((lo & k) == 0) cexv(ep_v[lo], ep_v[lo + jj]);
                 else cexv(ep_v[lo + jj], ep_v[lo]);
-            } else if constexpr (W < 116) {
-                constexpr int i = W - 100;
-                samp[i] = fminf(samp[i], ep_v[kSample - 1 - i]);
+            } else if constexpr (W < 60) {
+                // the kept 16 against the 8 sorted minima followed by 8 x +inf,
+                // reversed: the upper half takes min(samp[8+i], min[7-i]) and the
+                // whole is bitonic with the 16 smallest of both
+                constexpr int i = W - 52;
+                samp[8 + i] = fminf(samp[8 + i], ep_v[7 - i]);
             } else {
-                constexpr int c = W - 116, jj = 8 >> (c / 8), lo = ce_low(c, jj);
+                constexpr int c = W - 60, jj = 8 >> (c / 8), lo = ce_low(c, jj);
                 cexv(samp[lo], samp[lo + jj]);
             }
         };
