@@ -41,6 +41,10 @@ struct LeafParams {
     uint4 *chain_pool;
     uint32_t *chain_pool_used;
     uint32_t chain_pool_capacity;
+    // Work tickets of the filter kernel: words 0..7 one counter per XCD, word
+    // 8 the count of finished workgroups.  Zero before the first launch; the
+    // last workgroup of each launch zeroes them again.
+    uint32_t *item_tickets;
     // Work items are (leaf, block of kLeafBlockRows member rows); a batch is
     // items [item_begin, item_begin + item_count) of leaf-major order, with
     // blocks_per_leaf items per leaf.  The filter kernel writes, per block

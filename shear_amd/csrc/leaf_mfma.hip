@@ -15,17 +15,20 @@
 // v_mfma_i32_32x32x32_i8 output lane l holds row l%32 and candidates
 // 8*(v/4) + 4*(l/32) + v%4 of the tile: each row is served by a lane pair
 // (l, l+32), each lane seeing half of the row's candidates.  The grid is
-// persistent; the 8 XCDs each walk a contiguous range of work items, so a
-// leaf's items share one L2.
+// persistent (one workgroup per CU); the 8 XCDs each work through a
+// contiguous range of work items, so a leaf's items share one L2.
 //
 // The column tiles of a block form one stream (phase A's sampled tiles, then
 // every tile for phase B), double buffered in LDS with one barrier per tile;
 // each tile's epilogue runs interleaved with the next tile's MFMAs.
 //
 //  * phase A: every 3rd (4th for wide leaves) column tile is evaluated and
-//    each lane keeps its 16 smallest exact distances (values only); the row
-//    threshold F is the pair's 24th (18th) smallest sampled distance plus
-//    3*eps, so at least that many candidates lie at or below F;
+//    each lane keeps its 16 smallest of the minima of adjacent candidate
+//    pairs, ranked by cn - 2*rs*cs*dot (the distance less the row's norm, up
+//    to rounding); the row threshold F is the pair's 24th (18th) smallest
+//    kept value plus rn and 3*eps.  F only steers the filter: whatever its
+//    value, the select kernel certifies each row against it and re-runs the
+//    rows it cannot certify;
 //  * phase B: every column tile; a candidate passes when cs*dot meets the
 //    bound tau derived from F (a necessary condition for d <= F, evaluated in
 //    double with a rounding margin) and is appended (raw dot, column) to the
@@ -108,13 +111,13 @@ struct Layout {
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
 // LDS: two column tiles and each wave's 4 KB accumulator scratch, then the
-// leaf's member ids, scales and norms, and 64 bytes of scalars (each wave's
-// norm range).
+// leaf's member ids, scales and norms, and 128 bytes of scalars (each wave's
+// norm range, the workgroup's next item).
 __host__ __device__ constexpr uint32_t union_bytes(uint32_t tile_bytes, uint32_t nbuf) {
     return nbuf * tile_bytes + kWaves * 16u * 64u * 4u;
 }
 __host__ __device__ constexpr uint32_t lds_bytes(uint32_t tile_bytes, uint32_t nbuf, uint32_t cols_cap) {
-    return union_bytes(tile_bytes, nbuf) + cols_cap * 12u + 64u;
+    return union_bytes(tile_bytes, nbuf) + cols_cap * 12u + 128u;
 }
 
 // Compile-time loops: f(std::integral_constant<int, I>) for I in [B, E).
@@ -270,15 +273,24 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     // Work items are (leaf, 256-row block).  Workgroups are dispatched
     // round-robin over the 8 XCDs: XCD x walks its own contiguous item range,
     // so the row blocks of a leaf run at the same time on one XCD and share
-    // its L2 for the leaf's column tiles.
+    // its L2 for the leaf's column tiles.  The grid is one workgroup per CU;
+    // a workgroup's first item is fixed (its rank on the XCD), the rest come
+    // from the XCD's ticket counter (ragged leaves balance themselves).  The
+    // ticket for the next item is taken as an item starts and published to
+    // the workgroup through LDS at the item's second barrier, so its latency
+    // is hidden behind the item's first loads.
     const uint32_t xcd = blockIdx.x % 8u;
     const uint32_t lane_in_xcd = blockIdx.x / 8u;
     const uint32_t wgs_per_xcd = gridDim.x / 8u;
     uint32_t s_surv = 0, s_tiles = 0;
+    uint32_t *const s_next = misc + 2 * kWaves;  // the next item, from thread 0
+    uint32_t it = lane_in_xcd, it_next = per_xcd;
 
-    for (uint32_t it = lane_in_xcd; it < per_xcd; it += wgs_per_xcd) {
+    while (it < per_xcd) {
         const uint32_t work = xcd * per_xcd + it;  // item of the batch
         if (work >= p.item_count) break;
+        uint32_t ticket = 0u;
+        if (tid == 0) ticket = wgs_per_xcd + atomicAdd(p.item_tickets + xcd, 1u);
         const uint32_t item = p.item_begin + work;
         const uint32_t leaf = item / p.blocks_per_leaf;
         const uint32_t blk = item % p.blocks_per_leaf;
@@ -289,9 +301,15 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         uint2 *slog = p.survivor_log + ((uint64_t)work * kRowsPerBlock + brow) * 2u * cap + h;
         const uint32_t n = p.member_counts[leaf];
         const uint32_t row_base = blk * kRowsPerBlock;
-        if (row_base >= n) continue;
-        if (n > p.max_leaf_rows || n > kMaxLeafRows) {
-            if (tid == 0) flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+        // an item without rows (or an oversized leaf) only passes its ticket
+        // on; the first barrier orders the write after every read of the
+        // previous value
+        if (row_base >= n || n > p.max_leaf_rows || n > kMaxLeafRows) {
+            if (tid == 0 && row_base < n) flag_overflow(p.counters, TESSA_OVF_LEAF_ROW);
+            __syncthreads();
+            if (tid == 0) *s_next = ticket;
+            __syncthreads();
+            it = *s_next;
             continue;
         }
         const uint32_t *mem = p.members + p.member_offsets[leaf];
@@ -366,7 +384,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 misc[2u * wave + 1u] = __float_as_uint(hi);
             }
         }
+        if (tid == 0) *s_next = ticket;
         __syncthreads();
+        it_next = *s_next;
         float cn_min = __uint_as_float(misc[0]), cn_max = __uint_as_float(misc[1]);
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) {
@@ -376,6 +396,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
 
         const float rs = row_ok ? cs_lds[r] : 1.0f;
         const float rn = row_ok ? cn_lds[r] : 0.0f;
+        const float rs_m2 = -2.0f * rs;
 
         const uint32_t ntiles = (n + kTileCols - 1) / kTileCols;
         v4i pre[L::kChunksPerThread];
@@ -433,12 +454,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         // same straight-line block as position i's MFMAs, so the VALU work
         // overlaps the matrix pipe.
         //  * phase A epilogue: of each sampled tile a lane takes the minimum of
-        //    each adjacent pair of its 16 exact distances and keeps the 16
-        //    smallest of those minima (values only); F is the pair's kSel-th
-        //    smallest kept distance plus 3 eps, so at least kSel candidates
-        //    lie at or below F (any real distances give a valid F);
-        //  * phase B epilogue: a 16-bit mask of the lane's candidates meeting
-        //    cs*dot >= tau, and the raw dots parked in the wave's LDS scratch;
+        //    each adjacent pair of its 16 ranking values (cn - 2*rs*cs*dot)
+        //    and keeps the 16 smallest of those minima (values only); F is the
+        //    pair's kSel-th smallest kept value plus rn and 3 eps;
+        //  * phase B epilogue: a 16-bit mask of the lane's candidates with
+        //    cs*dot > tau, and the raw dots parked in the wave's LDS scratch;
         //    the next position drains the mask (set bits only) into the lane's
         //    survivor log.  Column validity (c < n, c != r) is checked there.
         constexpr int kSample = 16;
@@ -458,7 +478,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         int *const scr = reinterpret_cast<int *>(tile + NB * L::kTileBytes) + wave * (16u * 64u);
 
         // Phase A epilogue units (92): per group of 4 candidates one LDS read
-        // of their scales and norms and 4 exact distances (20), 8 pair
+        // of their scales and norms and 4 ranking values (20), 8 pair
         // minima, the 24 compare-exchanges of their bitonic sort, 8 minima
         // against the kept samples and the 32 of their bitonic merge.
         constexpr int kSampleUnits = 20 + 8 + 24 + 8 + 32;
@@ -484,7 +504,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                     constexpr int e = u - 1, vi = 4 * q + e;
                     const float csv = e == 0 ? ep_cs[q].x : e == 1 ? ep_cs[q].y : e == 2 ? ep_cs[q].z : ep_cs[q].w;
                     const float cnv = e == 0 ? ep_cn[q].x : e == 1 ? ep_cn[q].y : e == 2 ? ep_cn[q].z : ep_cn[q].w;
-                    const float d = leaf_l2((*ep_acc)[vi], rs, rn, csv, cnv);
+                    const float d = __builtin_fmaf(rs_m2, __fmul_rn(csv, (float)(*ep_acc)[vi]), cnv);
                     if constexpr (kDiag) {
                         const uint32_t c = ep_cbase + 4u * h + (uint32_t)(8 * q + e);
                         ep_v[vi] = c != r ? d : __builtin_inff();
@@ -513,8 +533,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         auto sample_unit = [&](auto wc) { sample_unit_impl(wc, std::false_type{}); };
         auto sample_unit_diag = [&](auto wc) { sample_unit_impl(wc, std::true_type{}); };
         const uint32_t diag_tile = (row_base + wave * 32u) / kTileCols;
-        // Phase B epilogue units (24): per group of 4 candidates one LDS read
-        // of their scales, 4 filter tests, one LDS write of the raw dots.
+        // Phase B epilogue units (24): per group of 4 candidates (groups
+        // taken from 3 down to 0) one LDS read of their scales, 4 filter
+        // tests, one LDS write of the raw dots.
         // The mask block adds kDrainSteps drain steps (each takes the lane's
         // lowest set bit: an LDS read of its dot, then a store to the survivor
         // log through a buffer store whose offset is out of range, so dropped,
@@ -534,7 +555,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             p.survivor_log, (short)0, (int)(p.item_count * (uint32_t)kThreads * cap * 8u), 0x00020000);
         const uint32_t slog_off = ((work * (uint32_t)kRowsPerBlock + brow) * 2u * cap + h) * 8u;
         auto mask_unit = [&](auto wc) {
-            constexpr int W = decltype(wc)::value, g = W / 6, u = W % 6;
+            constexpr int W = decltype(wc)::value, G = 3 - W / 6, u = W % 6;
             if constexpr (W >= kMaskUnits + 2 * kDrainSteps) {
                 prep_tile(prep_t);
             } else if constexpr (W >= kMaskUnits + kDrainSteps) {
@@ -553,14 +574,18 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 dr_c[d] = ep_cbase + 4u * h + 8u * (vi >> 2) + (vi & 3u);
                 dr_dot[d] = scr[((vi >> 2) * 64u + lane) * 4u + (vi & 3u)];
             } else if constexpr (u == 0) {
-                ep_cs[g] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * g + 4 * h);
+                ep_cs[G] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * G + 4 * h);
             } else if constexpr (u < 5) {
-                constexpr int e = u - 1, vi = 4 * g + e;
-                const float csv = e == 0 ? ep_cs[g].x : e == 1 ? ep_cs[g].y : e == 2 ? ep_cs[g].z : ep_cs[g].w;
-                ep_m |= (__fmul_rn((float)(*ep_acc)[vi], csv) >= tau) ? (1u << vi) : 0u;
+                // tau - cs*dot, rounded once, is negative exactly when
+                // cs*dot > tau; its sign bit is shifted into the mask, so the
+                // candidates taken from 15 down to 0 land on bits 15..0
+                constexpr int e = 4 - u, vi = 4 * G + e;
+                const float csv = e == 0 ? ep_cs[G].x : e == 1 ? ep_cs[G].y : e == 2 ? ep_cs[G].z : ep_cs[G].w;
+                const float t = __builtin_fmaf(-csv, (float)(*ep_acc)[vi], tau);
+                ep_m = __builtin_amdgcn_alignbit(ep_m, __float_as_uint(t), 31u);
             } else {
-                const v4i d = {(*ep_acc)[4 * g], (*ep_acc)[4 * g + 1], (*ep_acc)[4 * g + 2], (*ep_acc)[4 * g + 3]};
-                *reinterpret_cast<v4i *>(scr + (g * 64 + lane) * 4) = d;
+                const v4i d = {(*ep_acc)[4 * G], (*ep_acc)[4 * G + 1], (*ep_acc)[4 * G + 2], (*ep_acc)[4 * G + 3]};
+                *reinterpret_cast<v4i *>(scr + (G * 64 + lane) * 4) = d;
             }
         };
         auto prep_unit = [&](auto) { prep_tile(prep_t); };
@@ -660,7 +685,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             accP = accQ;
             ++i;
         }
-        if (rsel > 0) F = __fadd_rn(pair_kth<kSample>(samp, rsel), kFilterMargin);
+        if (rsel > 0) F = __fadd_rn(__fadd_rn(pair_kth<kSample>(samp, rsel), rn), kFilterMargin);
         // tau: necessary condition on cs * dot for d <= F
         tau = !row_ok ? __builtin_inff()
                       : (F == -__builtin_inff() ? __builtin_inff() : filter_bound(F, rs, rn, cn_min, cn_max));
@@ -698,6 +723,14 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 rm[2] = cnt;
             }
         }
+        it = it_next;
+    }
+
+    // The last workgroup to finish (every other one has taken its final
+    // ticket) resets the tickets for the next launch on the stream.
+    if (tid == 0 && atomicAdd(p.item_tickets + 8, 1u) == gridDim.x - 1u) {
+#pragma unroll
+        for (int x = 0; x < 9; ++x) atomicExch(p.item_tickets + x, 0u);
     }
 
     // One atomic per counter per wave.
@@ -708,6 +741,19 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         counter_add(p.counters, TESSA_C_LEAF_SURVIVORS, a_surv);
         if (wave == 0) counter_add(p.counters, TESSA_C_LEAF_MFMA_TILES, s_tiles);
     }
+}
+
+// CUs of the current device (cached per device).
+uint32_t cu_count() {
+    static uint32_t cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
+    if (cached[dev] == 0u) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = (uint32_t)v;
+    }
+    return cached[dev];
 }
 
 template <int KS>
@@ -730,9 +776,10 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     if (p.item_count == 0) return 0;
     if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x7fffffffull) return -2;
     const uint32_t per_xcd = (p.item_count + 7u) / 8u;
-    // persistent grid: up to four workgroups per CU's worth of items, a
-    // multiple of the 8 XCDs; XCD x walks items [x*per_xcd, (x+1)*per_xcd)
-    uint32_t grid = 1024u;
+    // persistent grid: one workgroup per CU (a multiple of the 8 XCDs); XCD x
+    // works through items [x*per_xcd, (x+1)*per_xcd)
+    uint32_t grid = cu_count() & ~7u;
+    if (grid < 8u) grid = 8u;
     if (per_xcd * 8u < grid) grid = per_xcd * 8u;
     if (four)
         hipLaunchKernelGGL((leaf_mfma_kernel<KS, 4>), dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);

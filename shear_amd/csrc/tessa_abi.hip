@@ -86,7 +86,7 @@ __global__ void map_rows_kernel(uint32_t *x, uint64_t n, const uint32_t *map) {
 // counters.  Grown on demand; kept until the process ends (other callers may
 // share the device).
 struct DeviceWorkspace {
-    uint32_t *queue_counts = nullptr;  // [0] fallback, [1] chain rows, [2] chain pool used
+    uint32_t *queue_counts = nullptr;  // [0] fallback, [1] chain rows, [2] chain pool used, [4..12] filter tickets
     uint32_t *fallback = nullptr;
     uint64_t fallback_capacity = 0;
     uint4 *chain_rows = nullptr;
@@ -394,6 +394,7 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.chain_capacity = clamp32(sc.chain_capacity);
     p.chain_pool = sc.chain_pool;
     p.chain_pool_used = sc.queue_counts + 2;
+    p.item_tickets = sc.queue_counts + 4;
     p.chain_pool_capacity = clamp32(sc.pool_capacity);
     p.survivor_log = sc.log;
     p.log_capacity = kLeafLogCapacity;
@@ -409,7 +410,7 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
         if (st.code) return st;
     }
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, sc.queue_counts, 3u, 0u);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, sc.queue_counts, 16u, 0u);
     for (uint64_t b = 0; b < nbatch; ++b) {
         p.item_begin = (uint32_t)(b * batch);
         p.item_count = (uint32_t)(items - b * batch < batch ? items - b * batch : batch);
