@@ -339,32 +339,39 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
 
         __syncthreads();  // previous item's readers of the LDS arrays are done
         {
-            // two columns per thread per step, every load of a step issued
-            // before its results are used
+            // four columns per thread per step (a 2,048-row leaf in one step),
+            // every load of a step issued before its results are used
             float lo = __builtin_inff(), hi = 0.0f;
-            for (uint32_t c0 = tid; c0 < n; c0 += 2u * kThreads) {
-                const uint32_t c1 = c0 + kThreads;
-                const bool ok1 = c1 < n;
-                uint32_t m0 = mem[c0];
-                uint32_t m1 = mem[ok1 ? c1 : c0];
-                if (m0 >= p.rows || m1 >= p.rows) {
-                    flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
-                    m0 = m0 < p.rows ? m0 : 0u;
-                    m1 = m1 < p.rows ? m1 : 0u;
+            for (uint32_t c0 = tid; c0 < n; c0 += 4u * kThreads) {
+                uint32_t m[4];
+                bool bad = false;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t c = c0 + (uint32_t)i * kThreads;
+                    m[i] = mem[c < n ? c : c0];
                 }
-                const float s0 = p.scales[m0], s1 = p.scales[m1];
-                const float n0 = p.norms[m0], n1 = p.norms[m1];
-                mem_lds[c0] = m0;
-                cs_lds[c0] = s0;
-                cn_lds[c0] = n0;
-                lo = fminf(lo, n0);
-                hi = fmaxf(hi, n0);
-                if (ok1) {
-                    mem_lds[c1] = m1;
-                    cs_lds[c1] = s1;
-                    cn_lds[c1] = n1;
-                    lo = fminf(lo, n1);
-                    hi = fmaxf(hi, n1);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bad |= m[i] >= p.rows;
+                    m[i] = m[i] < p.rows ? m[i] : 0u;
+                }
+                if (bad) flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+                float sv[4], nv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sv[i] = p.scales[m[i]];
+                    nv[i] = p.norms[m[i]];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t c = c0 + (uint32_t)i * kThreads;
+                    if (c < n) {
+                        mem_lds[c] = m[i];
+                        cs_lds[c] = sv[i];
+                        cn_lds[c] = nv[i];
+                        lo = fminf(lo, nv[i]);
+                        hi = fmaxf(hi, nv[i]);
+                    }
                 }
             }
             // the last column tile's columns past n: zero scale, infinite norm
@@ -774,7 +781,8 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     const uint32_t lds = lds_bytes(L::kTileBytes, four ? 4 : 2, cols_cap);
     if (lds > kLdsBudget) return -4;
     if (p.item_count == 0) return 0;
-    if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x7fffffffull) return -2;
+    // a batch's log offsets stay below 2^31 (the out-of-range store marker)
+    if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x80000000ull) return -2;
     const uint32_t per_xcd = (p.item_count + 7u) / 8u;
     // persistent grid: one workgroup per CU (a multiple of the 8 XCDs); XCD x
     // works through items [x*per_xcd, (x+1)*per_xcd)

@@ -148,12 +148,34 @@ __global__ __launch_bounds__(kSelThreads, 2) void leaf_select_kernel(LeafParams 
     // whole-workgroup exits only (the filter kernel flagged oversized leaves)
     if (row_base >= n || n > p.max_leaf_rows) return;
     const uint32_t *mem = p.members + p.member_offsets[leaf];
-    for (uint32_t c = tid; c < n; c += kSelThreads) {
-        uint32_t mc = mem[c];
-        mc = mc < p.rows ? mc : 0u;
-        cs_lds[c] = p.scales[mc];
-        cn_lds[c] = p.norms[mc];
-        gid_lds[c] = p.gids[mc];
+    // staged 8 columns per thread at a time: every member id of a step is
+    // requested before any of them is used, then every scale, norm and id
+    // (two memory round trips per step instead of two per column)
+    for (uint32_t c0 = tid; c0 < n; c0 += 8u * kSelThreads) {
+        uint32_t mc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = c0 + (uint32_t)i * kSelThreads;
+            mc[i] = mem[c < n ? c : c0];
+        }
+        float sv[8], nv[8];
+        uint32_t gv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t m = mc[i] < p.rows ? mc[i] : 0u;
+            sv[i] = p.scales[m];
+            nv[i] = p.norms[m];
+            gv[i] = p.gids[m];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = c0 + (uint32_t)i * kSelThreads;
+            if (c < n) {
+                cs_lds[c] = sv[i];
+                cn_lds[c] = nv[i];
+                gid_lds[c] = gv[i];
+            }
+        }
     }
     __syncthreads();
 

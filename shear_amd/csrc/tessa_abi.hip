@@ -145,8 +145,11 @@ tessa_status grow(T **ptr, uint64_t *cap, uint64_t need, size_t elem_bytes, cons
 }
 
 // Work items per filter/select batch for `rows` member rows: the survivor
-// logs of a batch take kLeafLogBytesPerItem each, at most kLeafLogBudget in all.
-constexpr uint64_t kLeafLogBudget = 1ull << 30;
+// logs of a batch take kLeafLogBytesPerItem each, at most kLeafLogBudget in
+// all (the filter addresses a batch's logs with 32-bit byte offsets below
+// 2^31, its out-of-range marker: 4,096 items of 512 KB).
+constexpr uint64_t kLeafMaxBatchItems = 4096;
+constexpr uint64_t kLeafLogBudget = kLeafMaxBatchItems * kLeafLogBytesPerItem;
 uint64_t leaf_batch_items(uint64_t rows) {
     const uint64_t cap = kLeafLogBudget / kLeafLogBytesPerItem;
     const uint64_t want = (rows + kLeafBlockRows - 1) / kLeafBlockRows + 1;
@@ -402,9 +405,11 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.blocks_per_leaf = (lb->max_leaf_rows + kLeafBlockRows - 1) / kLeafBlockRows;
     const uint64_t items = (uint64_t)p.blocks_per_leaf * lb->leaf_count;
     if (items > 0xffffff00ull) return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaf work items");
-    const uint64_t batch = sc.log_items;
-    if (batch == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf workspace holds no survivor log");
-    const uint64_t nbatch = (items + batch - 1) / batch;
+    const uint64_t batch_cap = sc.log_items < kLeafMaxBatchItems ? sc.log_items : kLeafMaxBatchItems;
+    if (batch_cap == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf workspace holds no survivor log");
+    // as few batches as the logs allow, of equal size (no short last batch)
+    const uint64_t nbatch = (items + batch_cap - 1) / batch_cap;
+    const uint64_t batch = (items + nbatch - 1) / nbatch;
     if (ev) {
         st = ensure_events(ev, 3 * nbatch + 2);
         if (st.code) return st;
