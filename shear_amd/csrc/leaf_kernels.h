@@ -45,12 +45,17 @@ struct LeafParams {
     // 8 the count of finished workgroups.  Zero before the first launch; the
     // last workgroup of each launch zeroes them again.
     uint32_t *item_tickets;
-    // Work items are (leaf, block of kLeafBlockRows member rows); a batch is
-    // items [item_begin, item_begin + item_count) of leaf-major order, with
-    // blocks_per_leaf items per leaf.  The filter kernel writes, per block
-    // row, 2 * log_capacity survivor entries (raw dot, column) at
-    // survivor_log[((item - item_begin) * kLeafBlockRows + row) * 2 *
-    // log_capacity], entry e of the row's lane h at 2e + h, and a row_meta
+    // The batch's work items, listed: entry g = (leaf, block) for g below
+    // *item_total (the leaves' non-empty blocks, a leaf's blocks in a row);
+    // batches cover list positions [item_begin, item_begin + item_count) and
+    // positions at or past *item_total are empty.
+    const uint2 *item_list;
+    const uint32_t *item_total;
+    // Work items are (leaf, block of kLeafBlockRows member rows), at most
+    // blocks_per_leaf per leaf.  The filter kernel writes, per block row of
+    // the batch's item w (list position item_begin + w), 2 * log_capacity
+    // survivor entries (raw dot, column) at survivor_log[(w * kLeafBlockRows
+    // + row) * 2 * log_capacity], entry e of the row's lane h at 2e + h, and a row_meta
     // word set (threshold F bits, the two lanes' entry counts); the select
     // kernel reads both.
     uint32_t item_begin;

@@ -252,7 +252,7 @@ __device__ __forceinline__ float pair_kth(const float (&a)[N], int rsel) {
 
 // NB column-tile buffers in LDS (2 or 4); a barrier every NB/2 positions.
 template <int KS, int NB>
-__global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p, uint32_t per_xcd) {
+__global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_kernel(LeafParams p) {
     using L = Layout<KS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // Runtime layout: tiles x2 | scratch | members | scales | norms | misc.
@@ -279,6 +279,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
     // ticket for the next item is taken as an item starts and published to
     // the workgroup through LDS at the item's second barrier, so its latency
     // is hidden behind the item's first loads.
+    const uint32_t total = *p.item_total;
+    const uint32_t items = total > p.item_begin ? (total - p.item_begin < p.item_count ? total - p.item_begin
+                                                                                      : p.item_count)
+                                                : 0u;
+    const uint32_t per_xcd = (items + 7u) / 8u;
     const uint32_t xcd = blockIdx.x % 8u;
     const uint32_t lane_in_xcd = blockIdx.x / 8u;
     const uint32_t wgs_per_xcd = gridDim.x / 8u;
@@ -288,12 +293,12 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
 
     while (it < per_xcd) {
         const uint32_t work = xcd * per_xcd + it;  // item of the batch
-        if (work >= p.item_count) break;
+        if (work >= items) break;
         uint32_t ticket = 0u;
         if (tid == 0) ticket = wgs_per_xcd + atomicAdd(p.item_tickets + xcd, 1u);
-        const uint32_t item = p.item_begin + work;
-        const uint32_t leaf = item / p.blocks_per_leaf;
-        const uint32_t blk = item % p.blocks_per_leaf;
+        const uint2 li = p.item_list[p.item_begin + work];
+        const uint32_t leaf = li.x;
+        const uint32_t blk = li.y;
         // The row's two lanes share one log region of 2*cap entries: lane h
         // writes its e-th entry at 2e + h, so the select kernel reads a row's
         // entries as one contiguous run.
@@ -783,16 +788,17 @@ int launch_ks(const LeafParams &p, hipStream_t stream) {
     if (p.item_count == 0) return 0;
     // a batch's log offsets stay below 2^31 (the out-of-range store marker)
     if ((uint64_t)p.item_count * kThreads * p.log_capacity * 8u > 0x80000000ull) return -2;
+    // persistent grid: one workgroup per CU (a multiple of the 8 XCDs); with
+    // the batch's listed items (count read on the device) split in 8 equal
+    // ranges, XCD x works through range x
     const uint32_t per_xcd = (p.item_count + 7u) / 8u;
-    // persistent grid: one workgroup per CU (a multiple of the 8 XCDs); XCD x
-    // works through items [x*per_xcd, (x+1)*per_xcd)
     uint32_t grid = cu_count() & ~7u;
     if (grid < 8u) grid = 8u;
     if (per_xcd * 8u < grid) grid = per_xcd * 8u;
     if (four)
-        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 4>), dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
+        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 4>), dim3(grid), dim3(kThreads), lds, stream, p);
     else
-        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 2>), dim3(grid), dim3(kThreads), lds, stream, p, per_xcd);
+        hipLaunchKernelGGL((leaf_mfma_kernel<KS, 2>), dim3(grid), dim3(kThreads), lds, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -140,9 +140,11 @@ __global__ __launch_bounds__(kSelThreads, 2) void leaf_select_kernel(LeafParams 
     __shared__ uint32_t stat[kSelWaves][5];
     const uint32_t tid = threadIdx.x;
     const uint32_t work = blockIdx.x;
-    const uint32_t item = p.item_begin + work;
-    const uint32_t leaf = item / p.blocks_per_leaf;
-    const uint32_t blk = item % p.blocks_per_leaf;
+    const uint32_t g = p.item_begin + work;
+    if (g >= *p.item_total) return;  // past the listed items
+    const uint2 li = p.item_list[g];
+    const uint32_t leaf = li.x;
+    const uint32_t blk = li.y;
     const uint32_t n = p.member_counts[leaf];
     const uint32_t row_base = blk * kLeafBlockRows;
     // whole-workgroup exits only (the filter kernel flagged oversized leaves)

@@ -86,7 +86,10 @@ __global__ void map_rows_kernel(uint32_t *x, uint64_t n, const uint32_t *map) {
 // counters.  Grown on demand; kept until the process ends (other callers may
 // share the device).
 struct DeviceWorkspace {
-    uint32_t *queue_counts = nullptr;  // [0] fallback, [1] chain rows, [2] chain pool used, [4..12] filter tickets
+    uint32_t *queue_counts = nullptr;  // [0] fallback, [1] chain rows, [2] chain pool used, [4..12] filter
+                                       // tickets, [13] listed work items
+    uint2 *item_list = nullptr;        // (leaf, block) work items of a call
+    uint64_t item_list_capacity = 0;
     uint32_t *fallback = nullptr;
     uint64_t fallback_capacity = 0;
     uint4 *chain_rows = nullptr;
@@ -156,7 +159,7 @@ uint64_t leaf_batch_items(uint64_t rows) {
     return want < cap ? want : cap;
 }
 
-tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
+tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out, uint64_t list_items = 0) {
     int dev = 0;
     TESSA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -179,6 +182,10 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out) {
     if (st.code) return st;
     st = grow(&ws.row_meta, &ws.row_meta_capacity, items * kLeafBlockRows, sizeof(uint4), "row thresholds");
     if (st.code) return st;
+    if (list_items) {
+        st = grow(&ws.item_list, &ws.item_list_capacity, list_items, sizeof(uint2), "work-item list");
+        if (st.code) return st;
+    }
     *out = &ws;
     return ok_status();
 }
@@ -311,9 +318,9 @@ tessa_status ensure_events(PhaseEvents *pe, size_t count) {
     return ok_status();
 }
 
-// Device buffers of the MFMA leaf path: queue counters (3 words), the exact
-// re-run queue, the chain queue and pool, and one batch of survivor logs and
-// row thresholds (log_items work items).
+// Device buffers of the MFMA leaf path: queue counters (16 words), the exact
+// re-run queue, the chain queue and pool, one batch of survivor logs and row
+// thresholds (log_items work items) and the call's work-item list.
 struct LeafScratch {
     uint32_t *queue_counts;
     uint32_t *fallback;
@@ -325,7 +332,32 @@ struct LeafScratch {
     uint2 *log;
     uint64_t log_items;
     uint4 *row_meta;
+    uint2 *item_list;
+    uint64_t item_list_capacity;
 };
+
+// The call's work items: each leaf's non-empty blocks (an oversized leaf
+// keeps its first blocks, so the filter flags it), reserved with one atomic
+// per wave; a leaf's blocks are listed in a row.
+__global__ void leaf_item_list_kernel(const uint32_t *counts, uint32_t leaf_count, uint32_t blocks_per_leaf,
+                                      uint2 *list, uint32_t *total) {
+    const uint32_t l = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n = l < leaf_count ? counts[l] : 0u;
+    uint32_t nb = (n + kLeafBlockRows - 1u) / kLeafBlockRows;
+    nb = nb < blocks_per_leaf ? nb : blocks_per_leaf;
+    uint32_t incl = nb;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d);
+        incl += lane >= (uint32_t)d ? v : 0u;
+    }
+    uint32_t base = 0u;
+    if (lane == 63u && incl) base = atomicAdd(total, incl);
+    base = __shfl(base, 63);
+    const uint32_t first = base + incl - nb;
+    for (uint32_t b = 0; b < nb; ++b) list[first + b] = make_uint2(l, b);
+}
 
 // Leaf top-k over device layouts; `rows_bound` bounds the member rows and
 // sizes the re-run / chain queues.  `ev` (optional) brackets the kernels.
@@ -377,16 +409,31 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
         return make_status(TESSA_ERR_UNSUPPORTED, 0,
                            "MFMA leaf path needs padded_dim <= 1024 and max_leaf_rows <= 4096 (got %u, %u)",
                            sq8->padded_dim, lb->max_leaf_rows);
+    const uint32_t bpl = (lb->max_leaf_rows + kLeafBlockRows - 1) / kLeafBlockRows;
+    const uint64_t items = (uint64_t)bpl * lb->leaf_count;  // bound of the listed items
+    if (items > 0xffffff00ull) return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaf work items");
     LeafScratch sc{};
     if (fixed) {
         sc = *fixed;
+        if (items > sc.item_list_capacity)
+            return make_status(TESSA_ERR_UNSUPPORTED, 0, "%llu leaf work items exceed the %llu of the fixed scratch",
+                               (unsigned long long)items, (unsigned long long)sc.item_list_capacity);
     } else {
         DeviceWorkspace *ws = nullptr;
-        st = get_workspace(rows_bound, &ws);
+        st = get_workspace(rows_bound, &ws, items);
         if (st.code) return st;
-        sc = LeafScratch{ws->queue_counts, ws->fallback,   ws->fallback_capacity, ws->chain_rows,
-                         ws->chain_capacity, ws->chain_pool, ws->pool_capacity,    ws->survivor_log,
-                         ws->log_entries / ((uint64_t)kLeafFilterThreads * kLeafLogCapacity), ws->row_meta};
+        sc = LeafScratch{ws->queue_counts,
+                         ws->fallback,
+                         ws->fallback_capacity,
+                         ws->chain_rows,
+                         ws->chain_capacity,
+                         ws->chain_pool,
+                         ws->pool_capacity,
+                         ws->survivor_log,
+                         ws->log_entries / ((uint64_t)kLeafFilterThreads * kLeafLogCapacity),
+                         ws->row_meta,
+                         ws->item_list,
+                         ws->item_list_capacity};
     }
     auto clamp32 = [](uint64_t v) { return (uint32_t)(v < 0xffffffffull ? v : 0xffffffffull); };
     p.fallback = sc.fallback;
@@ -402,9 +449,9 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.survivor_log = sc.log;
     p.log_capacity = kLeafLogCapacity;
     p.row_meta = sc.row_meta;
-    p.blocks_per_leaf = (lb->max_leaf_rows + kLeafBlockRows - 1) / kLeafBlockRows;
-    const uint64_t items = (uint64_t)p.blocks_per_leaf * lb->leaf_count;
-    if (items > 0xffffff00ull) return make_status(TESSA_ERR_UNSUPPORTED, 0, "more than 2^32 leaf work items");
+    p.blocks_per_leaf = bpl;
+    p.item_list = sc.item_list;
+    p.item_total = sc.queue_counts + 13;
     const uint64_t batch_cap = sc.log_items < kLeafMaxBatchItems ? sc.log_items : kLeafMaxBatchItems;
     if (batch_cap == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf workspace holds no survivor log");
     // as few batches as the logs allow, of equal size (no short last batch)
@@ -416,6 +463,9 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     }
     // Zero the queue counters with a kernel (capture-safe, unlike a memset node).
     hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, sc.queue_counts, 16u, 0u);
+    // the work-item list; batches past its length find no items and return
+    hipLaunchKernelGGL(leaf_item_list_kernel, dim3((lb->leaf_count + 255u) / 256u), dim3(256), 0, s,
+                       lb->member_counts, lb->leaf_count, bpl, sc.item_list, sc.queue_counts + 13);
     for (uint64_t b = 0; b < nbatch; ++b) {
         p.item_begin = (uint32_t)(b * batch);
         p.item_count = (uint32_t)(items - b * batch < batch ? items - b * batch : batch);
@@ -489,7 +539,10 @@ constexpr size_t kNaOffChainRows = kNaOffFallback + a256(kNoAllocMaxRows * 2 * s
 constexpr size_t kNaOffChainPool = kNaOffChainRows + a256(kNoAllocChainRows * sizeof(uint4));
 constexpr size_t kNaOffRowMeta = kNaOffChainPool + a256(kNoAllocChainRows * 40 * sizeof(uint4));
 constexpr size_t kNaOffLog = kNaOffRowMeta + a256(kNoAllocLogItems * kLeafBlockRows * sizeof(uint4));
-constexpr size_t kNoAllocBytes = kNaOffLog + a256(kNoAllocLogItems * kLeafLogBytesPerItem);
+// work items: leaf_count * blocks_per_leaf <= rows / kLeafBlockRows + leaf_count
+constexpr uint64_t kNoAllocListItems = kNoAllocMaxRows / kLeafBlockRows + kNoAllocMaxRows;
+constexpr size_t kNaOffItems = kNaOffLog + a256(kNoAllocLogItems * kLeafLogBytesPerItem);
+constexpr size_t kNoAllocBytes = kNaOffItems + a256(kNoAllocListItems * sizeof(uint2));
 
 __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 
@@ -537,7 +590,9 @@ tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf
                          kNoAllocChainRows * 40,
                          reinterpret_cast<uint2 *>(base + kNaOffLog),
                          kNoAllocLogItems,
-                         reinterpret_cast<uint4 *>(base + kNaOffRowMeta)};
+                         reinterpret_cast<uint4 *>(base + kNaOffRowMeta),
+                         reinterpret_cast<uint2 *>(base + kNaOffItems),
+                         kNoAllocListItems};
     return leaf_topk_impl(sq8, lb, rows, out_ids, out_dists, counters, stream, nullptr, nullptr, &sc);
 }
 
