@@ -166,8 +166,8 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
  * it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same arguments, results and errors as tessa_leaf_topk; all scratch (queue
- * counters, re-run and chain queues, survivor logs) lives in one static
- * device array of about 38 MB per GPU, held until the process ends, so a
+ * counters, re-run and chain queues, survivor logs, work-item list) lives
+ * in one static device array of about 39 MB per GPU, held until the process ends, so a
  * call may cover at most 65,536 member rows (leaf_count * max_leaf_rows);
  * larger batches are rejected with TESSA_ERR_UNSUPPORTED.  Every call on a
  * GPU shares that GPU's array: calls that overlap on one GPU (other
