@@ -421,10 +421,15 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         // zeroed when stored to LDS, a position later, so nothing waits for
         // the loads when they are issued.
         uint32_t pre_ok = 0u;  // bit q: chunk q of `pre` is real data
+        // a tile inside the leaf, rows without padding: every chunk is real
+        // data (a uniform flag, so stores of such tiles skip the selects)
+        const bool pd_full = pd == (uint32_t)(KS * 32);
+        bool nx_full = false, pre_full = false;
         uint32_t nx_mc[L::kChunksPerThread];
         uint32_t nx_ok = 0u;
         auto chunk_off = [&](int q) { return ((tid + q * kThreads) % (KS * 2)) * 16u; };
         auto prep_tile = [&](uint32_t t) {
+            nx_full = ((t + 1u) * kTileCols <= n) & pd_full;
             nx_ok = 0u;
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
@@ -436,6 +441,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             }
         };
         auto issue_tile = [&]() {
+            pre_full = nx_full;
             pre_ok = nx_ok;
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
@@ -444,6 +450,18 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             }
         };
         auto store_tile = [&](int8_t *dst) {
+            if (pre_full) {  // every chunk is real data: no selects
+#pragma unroll
+                for (int q = 0; q < L::kChunksPerThread; ++q) {
+                    const uint32_t chunk = tid + q * kThreads;
+                    if (chunk < (uint32_t)L::kChunks) {
+                        const uint32_t row = chunk / (KS * 2);
+                        const uint32_t off = (chunk % (KS * 2)) * 16u;
+                        *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = pre[q];
+                    }
+                }
+                return;
+            }
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
                 const uint32_t chunk = tid + q * kThreads;
