@@ -208,12 +208,22 @@ __global__ __launch_bounds__(kSelThreads, 2) void leaf_select_kernel(LeafParams 
 #pragma unroll
     for (int i = 0; i < kNext; ++i) nd[i] = kInfKey;
     double disc = kInfKey;
+    // 16 entries per step as 8 aligned 16-byte loads (inside the row's region:
+    // span <= 2 * cap, a multiple of 16); the next step's loads are issued
+    // before this step's entries are folded
+    uint4 qn[8];
+    if (span > 0u) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qn[i] = rlog[(uint32_t)i];
+    }
     for (uint32_t base = 0; base < span; base += 16u) {
-        // 16 entries as 8 aligned 16-byte loads (inside the row's region:
-        // span <= 2 * cap, a multiple of 16), all issued before any use
         uint4 q[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = rlog[base / 2u + (uint32_t)i];
+        for (int i = 0; i < 8; ++i) q[i] = qn[i];
+        if (base + 16u < span) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qn[i] = rlog[(base + 16u) / 2u + (uint32_t)i];
+        }
         double v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -265,24 +275,37 @@ __global__ __launch_bounds__(kSelThreads, 2) void leaf_select_kernel(LeafParams 
     const float disc_all = fminf(key_dist(disc), F);
 
     // ---- certificate -----------------------------------------------------------
-    // bit i of `same`: positions i and i+1 are in one cluster
-    int q_end = (int)keff - 1;  // last index of G
-    bool extending = keff > 0u;
-    bool clique_bad = false;
-    float cstart = sd[0];
-    uint64_t same = 0ull;
+    // bit i of `same`: positions i and i+1 are in one cluster; bit i of
+    // `bad`: position i is tied to its predecessor but lies more than eps
+    // past its cluster's first element (the cluster is not a clique).  Both
+    // are built as bit masks in one pass, so no per-position condition stays
+    // live across the passes below.
+    uint64_t same = 0ull, bad = 0ull;
+    {
+        float cstart = sd[0];
 #pragma unroll
-    for (int i = 1; i < kSeq; ++i) {
-        const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
-        same |= tie ? (1ull << (i - 1)) : 0ull;
-        const bool span_bad = tie && (__fsub_rn(sd[i], cstart) > kTieEps);
-        cstart = tie ? cstart : sd[i];
-        if (i >= (int)keff && extending) {
-            if (tie) q_end = i;
-            else extending = false;
+        for (int i = 1; i < kSeq; ++i) {
+            const bool tie = __fsub_rn(sd[i], sd[i - 1]) <= kTieEps;  // false on INF/NaN
+            same |= tie ? (1ull << (i - 1)) : 0ull;
+            bad |= (tie && (__fsub_rn(sd[i], cstart) > kTieEps)) ? (1ull << i) : 0ull;
+            cstart = tie ? cstart : sd[i];
         }
-        clique_bad |= span_bad && (i <= q_end || (extending && i >= (int)keff));
     }
+    // G = positions [0, q_end]: from keff - 1 on, every position tied to
+    // the next extends it; `extending` when the ties run to the end of the
+    // known sequence (the gap after G is then not known)
+    int q_end = (int)keff - 1;  // last index of G
+    bool extending = false;
+    if (keff > 0u) {
+        const uint32_t k0 = keff - 1u;                 // the first tie that could extend G
+        const uint32_t room = (uint32_t)kSeq - 1u - k0;  // ties that exist after it
+        const uint64_t t = ~(same >> k0);
+        const uint32_t run = t ? (uint32_t)__builtin_ctzll(t) : 64u;
+        extending = run >= room;
+        q_end = (int)(k0 + (run < room ? run : room));
+    }
+    const uint64_t in_q = q_end >= 1 ? ((2ull << q_end) - 2ull) : 0ull;  // positions 1..q_end
+    const bool clique_bad = (bad & in_q) != 0ull;
     bool gap_ok = (keff == 0u || !extending) && !log_ovf;
     if (keff > 0u && gap_ok) {
         float theta = sd[0];
