@@ -29,9 +29,9 @@
 //    kept value plus rn and 3*eps.  F only steers the filter: whatever its
 //    value, the select kernel certifies each row against it and re-runs the
 //    rows it cannot certify;
-//  * phase B: every column tile; a candidate passes when cs*dot meets the
-//    bound tau derived from F (a necessary condition for d <= F, evaluated in
-//    double with a rounding margin) and is appended (raw dot, column) to the
+//  * phase B: every column tile; a candidate passes a bound on cs*dot and its
+//    column's norm derived from F (a necessary condition for d <= F, with a
+//    rounding margin; filter_bound) and is appended (raw dot, column) to the
 //    row's survivor log in global memory (log_capacity entries per lane, the
 //    pair's entries interleaved);
 //  * end of item: F and both lanes' entry counts go to the row's row_meta
@@ -184,14 +184,37 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Necessary condition for a candidate to pass d <= F, as a bound on cs * dot:
-// d <= F implies 2*rs*cs*dot >= rn + cn - F - err >= rn + cn_min - F - err,
-// with err covering the f32 roundings of d (computed in double, lowered).
-__device__ __forceinline__ float filter_bound(float F, float rs, float rn, float cn_min, float cn_max) {
-    if (!(F < __builtin_inff())) return -__builtin_inff();
+// Necessary condition for a candidate to pass d <= F, per column: d <= F
+// implies cs*dot >= (rn - F)/(2 rs) + cn/(2 rs) - err, so the filter passes a
+// candidate when t = fma(cn, B, fma(-cs, dot, A)) < 0 with B = 1/(2 rs) and A
+// below (rn - F)/(2 rs) by a margin (1e-5 of the terms' scale) that covers
+// the f32 roundings of d, of B and of t.  F = +inf (or a row scale that is
+// not positive) passes everything; A = +inf passes nothing.
+// With the leaf's smallest norm in place of cn the bound needs no per-column
+// term: d <= F implies 2*rs*cs*dot >= rn + cn - F - err >= rn + cn_min - F -
+// err, with err covering the f32 roundings of d (computed in double, lowered),
+// so a candidate passes when fma(-cs, dot, A) < 0.  The per-column bound
+// below is tighter when the leaf's norms differ (unnormalised data).
+__device__ __forceinline__ void filter_bound_leaf(float F, float rs, float rn, float cn_min, float cn_max,
+                                                  float &A) {
+    if (!(F < __builtin_inff()) || !(rs > 0.0f)) {
+        A = -__builtin_inff();
+        return;
+    }
     const double err = 1.0e-6 * ((double)fabsf(rn) + (double)cn_max + (double)F) + 1.0e-30;
     const double tau = ((double)rn + (double)cn_min - (double)F - err) / (2.0 * (double)rs);
-    return (float)(tau - fabs(tau) * 2.0e-6 - 1.0e-30);
+    A = (float)(tau - fabs(tau) * 2.0e-6 - 1.0e-30);
+}
+__device__ __forceinline__ void filter_bound(float F, float rs, float rn, float cn_max, float &A, float &B) {
+    if (!(F < __builtin_inff()) || !(rs > 0.0f)) {
+        A = -__builtin_inff();
+        B = 0.0f;
+        return;
+    }
+    const double s2 = 2.0 * (double)rs;
+    const double scale = ((double)fabsf(rn) + (double)cn_max + fabs((double)F)) / s2;
+    A = (float)(((double)rn - (double)F) / s2 - 1.0e-5 * scale - 1.0e-30);
+    B = (float)(1.0 / s2);
 }
 
 
@@ -405,6 +428,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             cn_min = fminf(cn_min, __uint_as_float(misc[2 * w]));
             cn_max = fmaxf(cn_max, __uint_as_float(misc[2 * w + 1]));
         }
+        // the per-column test when the leaf's norms differ by more than 1 %
+        // (unnormalised data); else the cheaper leaf-wide one
+        const bool per_column = __fsub_rn(cn_max, cn_min) > 0.01f * cn_max;
 
         const float rs = row_ok ? cs_lds[r] : 1.0f;
         const float rn = row_ok ? cn_lds[r] : 0.0f;
@@ -487,8 +513,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         //    each adjacent pair of its 16 ranking values (cn - 2*rs*cs*dot)
         //    and keeps the 16 smallest of those minima (values only); F is the
         //    pair's kSel-th smallest kept value plus rn and 3 eps;
-        //  * phase B epilogue: a 16-bit mask of the lane's candidates with
-        //    cs*dot > tau, and the raw dots parked in the wave's LDS scratch;
+        //  * phase B epilogue: a 16-bit mask of the lane's candidates that
+        //    pass filter_bound's test, and the raw dots parked in the wave's
+        //    LDS scratch;
         //    the next position drains the mask (set bits only) into the lane's
         //    survivor log.  Column validity (c < n, c != r) is checked there.
         constexpr int kSample = 16;
@@ -500,7 +527,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
 #pragma unroll
         for (int i = 0; i < kSample; ++i) samp[i] = __builtin_inff();
         float F = -__builtin_inff();
-        float tau = __builtin_inff();
+        float tauA = __builtin_inff(), tauB = 0.0f;
         const uint32_t nA = (ntiles + sstride - 1u) / sstride;
         const uint32_t S = nA + ntiles;
         auto tile_of = [&](uint32_t i) { return i < nA ? i * sstride : i - nA; };
@@ -521,7 +548,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         uint32_t ep_cbase = 0u;
         // Columns past n carry norm +inf (distance +inf); the row's own column
         // lies in the wave's diagonal tile only, whose epilogue variant
-        // (kDiag) excludes it.  Rows past n get samples but tau = +inf.
+        // (kDiag) excludes it.  Rows past n get samples but pass nothing.
         auto sample_unit_impl = [&](auto wc, auto diag_tag) {
             constexpr int W = decltype(wc)::value;
             constexpr bool kDiag = decltype(diag_tag)::value;
@@ -584,8 +611,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         const __amdgpu_buffer_rsrc_t log_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             p.survivor_log, (short)0, (int)(p.item_count * (uint32_t)kThreads * cap * 8u), 0x00020000);
         const uint32_t slog_off = ((work * (uint32_t)kRowsPerBlock + brow) * 2u * cap + h) * 8u;
-        auto mask_unit = [&](auto wc) {
+        auto mask_unit_impl = [&](auto wc, auto pc_tag) {
             constexpr int W = decltype(wc)::value, G = 3 - W / 6, u = W % 6;
+            constexpr bool kPC = decltype(pc_tag)::value;
             if constexpr (W >= kMaskUnits + 2 * kDrainSteps) {
                 prep_tile(prep_t);
             } else if constexpr (W >= kMaskUnits + kDrainSteps) {
@@ -605,19 +633,27 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 dr_dot[d] = scr[((vi >> 2) * 64u + lane) * 4u + (vi & 3u)];
             } else if constexpr (u == 0) {
                 ep_cs[G] = *reinterpret_cast<const float4 *>(cs_al + ep_cbase + 8 * G + 4 * h);
+                if constexpr (kPC) ep_cn[G] = *reinterpret_cast<const float4 *>(cn_al + ep_cbase + 8 * G + 4 * h);
             } else if constexpr (u < 5) {
-                // tau - cs*dot, rounded once, is negative exactly when
-                // cs*dot > tau; its sign bit is shifted into the mask, so the
-                // candidates taken from 15 down to 0 land on bits 15..0
+                // t < 0 is the filter test (filter_bound / filter_bound_leaf),
+                // t rounded once per FMA; its sign bit is shifted into the
+                // mask, so the candidates taken from 15 down to 0 land on bits
+                // 15..0
                 constexpr int e = 4 - u, vi = 4 * G + e;
                 const float csv = e == 0 ? ep_cs[G].x : e == 1 ? ep_cs[G].y : e == 2 ? ep_cs[G].z : ep_cs[G].w;
-                const float t = __builtin_fmaf(-csv, (float)(*ep_acc)[vi], tau);
+                float t = __builtin_fmaf(-csv, (float)(*ep_acc)[vi], tauA);
+                if constexpr (kPC) {
+                    const float cnv = e == 0 ? ep_cn[G].x : e == 1 ? ep_cn[G].y : e == 2 ? ep_cn[G].z : ep_cn[G].w;
+                    t = __builtin_fmaf(cnv, tauB, t);
+                }
                 ep_m = __builtin_amdgcn_alignbit(ep_m, __float_as_uint(t), 31u);
             } else {
                 const v4i d = {(*ep_acc)[4 * G], (*ep_acc)[4 * G + 1], (*ep_acc)[4 * G + 2], (*ep_acc)[4 * G + 3]};
                 *reinterpret_cast<v4i *>(scr + (G * 64 + lane) * 4) = d;
             }
         };
+        auto mask_unit = [&](auto wc) { mask_unit_impl(wc, std::false_type{}); };
+        auto mask_unit_pc = [&](auto wc) { mask_unit_impl(wc, std::true_type{}); };
         auto prep_unit = [&](auto) { prep_tile(prep_t); };
         auto sample_prep_unit = [&](auto wc) {
             if constexpr (decltype(wc)::value == kSampleUnits) prep_tile(prep_t);
@@ -684,13 +720,13 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 return mfma_block<KS, kSampleUnits + 1>(src_of(i) + arow_off, bfrag, sample_prep_unit_diag);
             return mfma_block<KS, kSampleUnits + 1>(src_of(i) + arow_off, bfrag, sample_prep_unit);
         };
-        auto mask_block = [&](uint32_t i, const v16i &prev) {
+        auto mask_block = [&](uint32_t i, const v16i &prev, auto &unit) {
             ep_acc = &prev;
             ep_cbase = (i - 1u - nA) * kTileCols;
             ep_m = 0u;
             dr_has = 0u;
             prep_for(i);
-            const v16i acc = mfma_block<KS, kMaskBlockUnits>(src_of(i) + arow_off, bfrag, mask_unit);
+            const v16i acc = mfma_block<KS, kMaskBlockUnits>(src_of(i) + arow_off, bfrag, unit);
             // the residual mask is needed here, not only by the next position's
             // drain: its tests stay interleaved with the MFMAs instead of sinking
             asm volatile("" : "+v"(ep_m));
@@ -716,28 +752,35 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             ++i;
         }
         if (rsel > 0) F = __fadd_rn(__fadd_rn(pair_kth<kSample>(samp, rsel), rn), kFilterMargin);
-        // tau: necessary condition on cs * dot for d <= F
-        tau = !row_ok ? __builtin_inff()
-                      : (F == -__builtin_inff() ? __builtin_inff() : filter_bound(F, rs, rn, cn_min, cn_max));
-        // positions nA+1..S-1: filter epilogues of phase B tiles
-        for (; i + 1u < S; i += 2u) {
-            head(i);
-            accQ = mask_block(i, accP);
-            head(i + 1u);
-            accP = mask_block(i + 1u, accQ);
+        // the row's filter test (rows past n pass nothing)
+        if (row_ok && F != -__builtin_inff()) {
+            if (per_column) filter_bound(F, rs, rn, cn_max, tauA, tauB);
+            else filter_bound_leaf(F, rs, rn, cn_min, cn_max, tauA);
         }
-        if (i < S) {
-            head(i);
-            accQ = mask_block(i, accP);
-            accP = accQ;
-        }
-        // tail: drain the held mask, then the last position (phase B's last tile)
-        drain(pend_mask, pend_tile);
-        ep_acc = &accP;
-        ep_cbase = (ntiles - 1u) * kTileCols;
-        ep_m = 0u;
-        static_for<0, kMaskUnits>(mask_unit);
-        drain(ep_m, ntiles - 1u);
+        // positions nA+1..S-1: filter epilogues of phase B tiles, then the
+        // tail: drain the held mask, then the last position (phase B's last
+        // tile); one copy of the loop per form of the test
+        auto phase_b = [&](auto &unit) {
+            for (; i + 1u < S; i += 2u) {
+                head(i);
+                accQ = mask_block(i, accP, unit);
+                head(i + 1u);
+                accP = mask_block(i + 1u, accQ, unit);
+            }
+            if (i < S) {
+                head(i);
+                accQ = mask_block(i, accP, unit);
+                accP = accQ;
+            }
+            drain(pend_mask, pend_tile);
+            ep_acc = &accP;
+            ep_cbase = (ntiles - 1u) * kTileCols;
+            ep_m = 0u;
+            static_for<0, kMaskUnits>(unit);
+            drain(ep_m, ntiles - 1u);
+        };
+        if (per_column) phase_b(mask_unit_pc);
+        else phase_b(mask_unit);
         s_tiles += S;
         s_surv += cnt < cap ? cnt : cap;
 
