@@ -101,6 +101,24 @@ def test_subtree_matches_oracle(gpu, orc, case):
     _check_topk(orc, out, leaves, codes, scales, norms, gids)
 
 
+def test_subtree_unnormalised_rows_are_certified(gpu, orc):
+    """C1-shaped rows (128-d, centres N(0, I), sigma 0.3, not normalised):
+    their norms differ by far more than 1 %, so the filter tests each column
+    against its own norm.  With the leaf-wide smallest norm the test let
+    through so many candidates that about a third of the rows overflowed
+    their logs and took the exact re-run; the rows must now be certified (a
+    handful of re-runs at most) and still match the oracle bit for bit."""
+    x = datagen.gmm_numpy(12000, 128, 64, 0.3, 0, unit_norm=False)
+    codes, scales, norms = orc.quantize(x)
+    assert (norms.max() - norms.min()) > 0.05 * norms.max()
+    gids = np.arange(12000, dtype=np.uint32)
+    _, out, leaves, ctr, _ = _run(orc, codes, scales, norms, gids, 128, fan=2, leaf_max=1024, psamp=0.01)
+    _check_layout(out, leaves, ctr)
+    reruns = int(out.leaf_counters[N.C_LEAF_FALLBACK_ROWS])
+    assert reruns <= out.leaf_rows // 100, f"{reruns} of {out.leaf_rows} rows re-run exactly"
+    _check_topk(orc, out, leaves, codes, scales, norms, gids)
+
+
 def test_subtree_exact_executor_and_small_k(gpu, orc):
     codes, scales, norms, gids = _data(orc, 2500, 40, 8, 11)
     for executor, k in [(N.EXEC_EXACT, 32), (N.EXEC_MFMA, 5)]:
