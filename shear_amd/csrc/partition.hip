@@ -436,25 +436,51 @@ __global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(Par
             for (uint32_t t = 0; t < ntiles; ++t) {
                 v16i acc = {};
                 const int8_t *arow = lcodes + (32u * t + j) * L::kStride + 16u * h;
+                // A operands read two steps ahead of their MFMA
+                v4i ring[3];
+                ring[0] = *reinterpret_cast<const v4i *>(arow);
+                if constexpr (KS > 1) ring[1] = *reinterpret_cast<const v4i *>(arow + 32);
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
-                    const v4i av = *reinterpret_cast<const v4i *>(arow + 32 * s);
-                    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bfrag[s], acc, 0, 0, 0);
+                    if (s + 2 < KS) ring[(s + 2) % 3] = *reinterpret_cast<const v4i *>(arow + 32 * (s + 2));
+                    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[s % 3], bfrag[s], acc, 0, 0, 0);
+                }
+                // the lane's 16 leaders are 4 runs of 4 (8g + 4h + e): their
+                // scales and norms in 8 vector reads, then every distance
+                float4 lsv[4], lnv[4];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    lsv[g] = *reinterpret_cast<const float4 *>(ls + 32u * t + 8u * g + 4u * h);
+                    lnv[g] = *reinterpret_cast<const float4 *>(ln + 32u * t + 8u * g + 4u * h);
                 }
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
                     const uint32_t gl = 32u * t + li;
-                    wb[li * 33 + j] = gl < nl ? assign_l2(acc[v], ps, pn, ls[gl], ln[gl]) : kEmptyDist;
+                    const int e = v % 4, g = v / 4;
+                    const float lsc = e == 0 ? lsv[g].x : e == 1 ? lsv[g].y : e == 2 ? lsv[g].z : lsv[g].w;
+                    const float lno = e == 0 ? lnv[g].x : e == 1 ? lnv[g].y : e == 2 ? lnv[g].z : lnv[g].w;
+                    const float d = assign_l2(acc[v], ps, pn, lsc, lno);
+                    wb[li * 33 + j] = gl < nl ? d : kEmptyDist;
                 }
                 wave_lds_sync();
                 if (h == 0u && ok) {
                     const uint32_t lim = (nl - 32u * t) < 32u ? (nl - 32u * t) : 32u;
+                    // leaders in slot order, 8 at a time: the 8 distances and
+                    // leader ids of a step are read before its insertions
                     auto run = [&](auto fc) {
                         constexpr int F = decltype(fc)::value;
-                        for (uint32_t li = 0; li < lim; ++li) {
-                            const uint32_t slot = 32u * t + li;
-                            insert_slot<F>(wb[li * 33 + j], lpt, lid[slot], slot, bd, bs, bl);
+                        for (uint32_t l0 = 0; l0 < lim; l0 += 8u) {
+                            float dv[8];
+                            uint32_t idv[8];
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) {
+                                dv[q] = wb[(l0 + q) * 33 + j];
+                                idv[q] = lid[32u * t + l0 + q];
+                            }
+#pragma unroll
+                            for (int q = 0; q < 8; ++q)
+                                if (l0 + q < lim) insert_slot<F>(dv[q], lpt, idv[q], 32u * t + l0 + q, bd, bs, bl);
                         }
                     };
                     switch (fanout) {
