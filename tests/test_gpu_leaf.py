@@ -72,6 +72,22 @@ def test_random_leaves_match_oracle(gpu, orc, dim):
     assert_same(ids, d, want_ids, want_d, f"exact dim={dim}")
 
 
+def test_empty_leaves_between_real_ones(gpu, orc):
+    """Leaves without rows get no work items (the device-side item list
+    skips them); the others, including ones of 1 and 1024 rows, match the
+    oracle and every real row is counted once."""
+    sizes = [0, 5, 0, 0, 300, 0, 1024, 0, 1, 0]
+    n = sum(sizes) + 9
+    codes, scales, norms, gids = _gmm_case(orc, n, 768, seed=5)
+    members = np.random.default_rng(6).permutation(n)[: sum(sizes)].astype(np.uint32)
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]])
+    sq8 = to_dev_sq8(codes, scales, norms, 768)
+    want_ids, want_d = orc.leaf_topk(codes, scales, norms, gids, members, offs, sizes, 32)
+    ids, d, ctr = run_leaf(sq8, gids, members, offs, sizes, 32, N.EXEC_MFMA)
+    assert_same(ids, d, want_ids, want_d, "mfma with empty leaves")
+    assert ctr[N.C_LEAF_ROWS] == sum(sizes)
+
+
 def test_large_leaves_and_k_match_oracle(gpu, orc):
     sizes = [2048, 4096, 1500]
     n = sum(sizes)
