@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
 #pragma unroll
         for (int i = 0; i < kChainSeq; ++i) {
             if ((uint32_t)i < m) {
-                const uint4 e = p.chain_pool[hdr.z + i];
+                const uint4 e = p.chain_pool[(uint64_t)hdr.z + (uint64_t)i * 64u];  // 64 rows interleaved
                 key[i] = (e.y << 6) | (uint32_t)i;
                 ent[i][tid] = make_uint2(e.x, e.z);
             }

@@ -33,8 +33,9 @@ struct LeafParams {
     uint32_t debug_rerun_every;
     // Rows whose certified candidate set G holds an eps-tie chain: header
     // (output offset lo/hi, pool offset, |G| | k_eff << 8) plus |G| pool
-    // entries (f32 bits, column, global id, 0), replayed in column order by
-    // the chain kernel.
+    // entries (f32 bits, column, global id, 0) at pool offset + 64 i (the
+    // sets of 64 consecutive queue entries interleaved), replayed in column
+    // order by the chain kernel.  chain_pool_used is not used.
     uint4 *chain_rows;
     uint32_t *chain_count;
     uint32_t chain_capacity;

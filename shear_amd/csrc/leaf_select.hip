@@ -392,29 +392,30 @@ __global__ __launch_bounds__(kSelThreads, 2) void leaf_select_kernel(LeafParams 
     }
 
     // chain rows: header (output offset, pool offset, |G| | keff << 8) and
-    // |G| pool entries (distance bits, column, global id)
+    // |G| pool entries (distance bits, column, global id).  The pool keeps the
+    // candidate sets of 64 consecutive queue entries interleaved: entry i of
+    // queue index x at (x / 64 * kSeq + i) * 64 + x % 64, so the chain kernel
+    // (one lane per queue entry) reads entry i of 64 rows as one 1 KB run.
     const uint32_t m = chain ? (uint32_t)q_end + 1u : 0u;
     const uint32_t wave = tid >> 6, lane = tid & 63u;
-    // queue slots: wave prefix sums, then one atomic per workgroup and queue
-    uint32_t tot_m = 0, tot_c = 0;
-    const uint32_t pre_m = wave_excl_scan(m, &tot_m);
+    // queue slots: a wave prefix sum, then one atomic per workgroup
+    uint32_t tot_c = 0;
     const uint32_t pre_c = wave_excl_scan(chain ? 1u : 0u, &tot_c);
-    if (lane == 0u) {
-        red[wave][0] = tot_m;
-        red[wave][1] = tot_c;
-    }
+    if (lane == 0u) red[wave][0] = tot_c;
     __syncthreads();
-    if (tid == 0u) wg_reserve(red, 2, p.chain_pool_used, p.chain_count);
+    if (tid == 0u) wg_reserve(red, 1, p.chain_count, nullptr);
     __syncthreads();
-    const uint32_t off = red[kSelWaves][0] + red[wave][0] + pre_m;
-    const uint32_t idx = red[kSelWaves][1] + red[wave][1] + pre_c;
-    const bool queued = chain && (uint64_t)off + m <= p.chain_pool_capacity && idx < p.chain_capacity;
+    const uint32_t idx = red[kSelWaves][0] + red[wave][0] + pre_c;
+    const uint64_t pbase = (uint64_t)(idx >> 6) * (uint64_t)(kSeq * 64) + (idx & 63u);
+    const bool queued = chain && idx < p.chain_capacity &&
+                        ((uint64_t)(idx >> 6) + 1u) * (uint64_t)(kSeq * 64) <= p.chain_pool_capacity;
     if (queued) {
 #pragma unroll
         for (int i = 0; i < kSeq; ++i)
             if ((uint32_t)i < m)
-                p.chain_pool[off + i] = make_uint4(__float_as_uint(sd[i]), sc[i], gid_lds[sc[i] < n ? sc[i] : 0u], 0u);
-        p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), off, m | (keff << 8));
+                p.chain_pool[pbase + (uint64_t)i * 64u] =
+                    make_uint4(__float_as_uint(sd[i]), sc[i], gid_lds[sc[i] < n ? sc[i] : 0u], 0u);
+        p.chain_rows[idx] = make_uint4((uint32_t)out, (uint32_t)(out >> 32), (uint32_t)pbase, m | (keff << 8));
     }
     const bool rerun = row_ok && !direct && !queued;
     uint32_t tot_f = 0;

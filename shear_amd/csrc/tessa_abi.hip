@@ -173,7 +173,8 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out, uint64_t list_i
     // correctness.
     st = grow(&ws.chain_rows, &ws.chain_capacity, rows / 2 + 1, sizeof(uint4), "chain queue");
     if (st.code) return st;
-    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 1) * 40, sizeof(uint4), "chain pool");
+    // candidate sets of 64 queue entries interleaved: whole groups of 64 x 40
+    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 64) / 64 * 64 * 40, sizeof(uint4), "chain pool");
     if (st.code) return st;
     // survivor logs and row thresholds of one batch of work items
     const uint64_t items = leaf_batch_items(rows);
@@ -537,7 +538,8 @@ constexpr size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr size_t kNaOffFallback = 256;
 constexpr size_t kNaOffChainRows = kNaOffFallback + a256(kNoAllocMaxRows * 2 * sizeof(uint32_t));
 constexpr size_t kNaOffChainPool = kNaOffChainRows + a256(kNoAllocChainRows * sizeof(uint4));
-constexpr size_t kNaOffRowMeta = kNaOffChainPool + a256(kNoAllocChainRows * 40 * sizeof(uint4));
+constexpr uint64_t kNoAllocPoolEntries = (kNoAllocChainRows + 63) / 64 * 64 * 40;  // whole groups of 64 x 40
+constexpr size_t kNaOffRowMeta = kNaOffChainPool + a256(kNoAllocPoolEntries * sizeof(uint4));
 constexpr size_t kNaOffLog = kNaOffRowMeta + a256(kNoAllocLogItems * kLeafBlockRows * sizeof(uint4));
 // work items: leaf_count * blocks_per_leaf <= rows / kLeafBlockRows + leaf_count
 constexpr uint64_t kNoAllocListItems = kNoAllocMaxRows / kLeafBlockRows + kNoAllocMaxRows;
@@ -587,7 +589,7 @@ tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf
                          reinterpret_cast<uint4 *>(base + kNaOffChainRows),
                          kNoAllocChainRows,
                          reinterpret_cast<uint4 *>(base + kNaOffChainPool),
-                         kNoAllocChainRows * 40,
+                         kNoAllocPoolEntries,
                          reinterpret_cast<uint2 *>(base + kNaOffLog),
                          kNoAllocLogItems,
                          reinterpret_cast<uint4 *>(base + kNaOffRowMeta),
