@@ -137,12 +137,104 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_all_kernel(LeafParam
     }
 }
 
-__global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(LeafParams p) {
+// Re-run of the rows the MFMA executor could not certify: one 1,024-thread
+// workgroup per row.  The row's distances to a chunk of 1,024 member columns
+// are computed four lanes per column (a quarter of the dims each, summed over
+// the quad) into LDS; then wave 0 inserts them in member order with the rule
+// of exact_row.  Few rows (often a few hundred) are re-run per call, so the
+// latency of one row is what counts.
+constexpr int kFallbackThreads = 1024;
+constexpr uint32_t kFallbackChunk = 1024;
+
+__device__ void exact_row_wg(const LeafParams &p, uint32_t leaf, uint32_t row, float *sd, uint32_t *sg,
+                             uint8_t *sv) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t n = p.member_counts[leaf];
+    if (row >= n) return;
+    const uint32_t *mem = p.members + p.member_offsets[leaf];
+    const uint32_t keff = (p.k < n - 1u) ? p.k : (n - 1u);
+    const uint32_t self = mem[row];
+    if (self >= p.rows) {
+        if (tid == 0) flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_ROW_ID);
+        return;
+    }
+    const int4 *rc = reinterpret_cast<const int4 *>(p.codes + (uint64_t)self * p.padded_dim);
+    const float rs = p.scales[self];
+    const float rn = p.norms[self];
+    const uint32_t pieces = p.padded_dim / 16u;
+    float bd = kEmptyDist;
+    uint32_t bg = kEmptyId;
+    uint32_t len = 0;
+    for (uint32_t cb = 0; cb < n && keff > 0u; cb += kFallbackChunk) {
+        const uint32_t cn = (n - cb < kFallbackChunk) ? n - cb : kFallbackChunk;
+        __syncthreads();  // the previous chunk's insertion is done with sd/sg/sv
+        for (uint32_t j = tid >> 2; j < cn; j += kFallbackThreads / 4) {
+            const uint32_t c = cb + j, q = tid & 3u;
+            const uint32_t cj = mem[c];
+            const bool ok = c != row && cj < p.rows;
+            int acc = 0;
+            if (ok) {
+                const int4 *cc = reinterpret_cast<const int4 *>(p.codes + (uint64_t)cj * p.padded_dim);
+                for (uint32_t i = q; i < pieces; i += 4u) {
+                    const int4 x = rc[i], y = cc[i];
+                    acc = __builtin_amdgcn_sdot4(x.x, y.x, acc, false);
+                    acc = __builtin_amdgcn_sdot4(x.y, y.y, acc, false);
+                    acc = __builtin_amdgcn_sdot4(x.z, y.z, acc, false);
+                    acc = __builtin_amdgcn_sdot4(x.w, y.w, acc, false);
+                }
+            }
+            acc += __shfl_xor(acc, 1);
+            acc += __shfl_xor(acc, 2);
+            if (q == 0u) {
+                if (c != row && cj >= p.rows) flag_overflow(p.counters, TESSA_OVF_INVALID_TOPK_COL_ID);
+                sd[j] = ok ? leaf_l2(acc, rs, rn, p.scales[cj], p.norms[cj]) : kEmptyDist;
+                sg[j] = ok ? p.gids[cj] : kEmptyId;
+                sv[j] = ok ? 1u : 0u;
+            }
+        }
+        __syncthreads();
+        if (wave == 0u) {
+            for (uint32_t base = 0; base < cn; base += 64u) {
+                const uint32_t j = base + lane;
+                const bool ok = j < cn && sv[j] != 0u;
+                const float d = ok ? sd[j] : kEmptyDist;
+                const uint32_t g = ok ? sg[j] : kEmptyId;
+                uint32_t next = 0;
+                while (true) {
+                    bool cand = ok && lane >= next;
+                    if (len == keff) {
+                        const float td = lane_bcast(bd, keff - 1u);
+                        const uint32_t tg = lane_bcast(bg, keff - 1u);
+                        cand = cand && beats(d, g, td, tg);
+                    }
+                    const uint64_t m = __ballot(cand);
+                    if (m == 0ull) break;
+                    const uint32_t i = (uint32_t)(__ffsll((long long)m) - 1);
+                    len = wave_insert(lane_bcast(d, i), lane_bcast(g, i), bd, bg, len, keff);
+                    next = i + 1u;
+                }
+            }
+        }
+    }
+    if (wave == 0u) {
+        const uint64_t out = p.output_offsets[leaf] + (uint64_t)row * p.k;
+        if (lane < p.k) {
+            p.out_ids[out + lane] = lane < len ? bg : kEmptyId;
+            p.out_dists[out + lane] = lane < len ? bd : kEmptyDist;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kFallbackThreads) void leaf_exact_fallback_kernel(LeafParams p) {
+    __shared__ float sd[kFallbackChunk];
+    __shared__ uint32_t sg[kFallbackChunk];
+    __shared__ uint8_t sv[kFallbackChunk];
     uint32_t count = *p.fallback_count;
     if (count > p.fallback_capacity) count = p.fallback_capacity;
     uint64_t done = 0;
     for (uint32_t w = blockIdx.x; w < count; w += gridDim.x) {
-        exact_row(p, p.fallback[2 * w], p.fallback[2 * w + 1]);
+        exact_row_wg(p, p.fallback[2 * w], p.fallback[2 * w + 1], sd, sg, sv);
+        __syncthreads();  // the next row's first chunk overwrites sd/sg/sv
         ++done;
     }
     if (threadIdx.x == 0) {
@@ -158,17 +250,19 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_fallback_kernel(Leaf
 // neither enter in front of G's nor stay in the buffer.
 //
 // One lane per queued row (|G| <= 40).  The lane sorts (column, index) keys of
-// G in registers, keeps G's (distance, global id) in LDS for lookups by index,
-// and replays the bounded insertion of leaf_build.rs:913-951 over a 32-slot
-// list in registers: slot s is visited from the back, and a candidate moves
-// forward while it beats the slot before it.  Blocks of 8 slots that no lane
-// of the wave can touch are skipped.
+// G in registers, keeps the sorted indices in LDS, reads G's (distance, global
+// id) back from the pool in column order two steps ahead (the pool's lines are
+// still in L2), and replays the bounded insertion of leaf_build.rs:913-951 over
+// a 32-slot list in registers: slot s is visited from the back, and a
+// candidate moves forward while it beats the slot before it.  Blocks of 8
+// slots that no lane of the wave can touch are skipped.  With 5 KB of LDS per
+// workgroup the kernel runs four waves per SIMD (at most 128 VGPRs); rows
+// whose output is 16-byte aligned are written with vector stores.
 constexpr int kChainSeq = 40;      // G holds at most kMaxK + 8 entries
 constexpr int kChainSlots = kMaxK; // the row's top-k list
 constexpr int kChainThreads = 128;
 
-__global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p) {
-    __shared__ uint2 ent[kChainSeq][kChainThreads];      // (distance bits, global id) of G's entry i
+__global__ __launch_bounds__(kChainThreads) __attribute__((amdgpu_waves_per_eu(4))) void leaf_chain_kernel(LeafParams p) {
     __shared__ uint8_t order[kChainSeq][kChainThreads];  // G's entry indices in column order
     const uint32_t tid = threadIdx.x;
     uint32_t count = *p.chain_count;
@@ -190,7 +284,6 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
             if ((uint32_t)i < m) {
                 const uint4 e = p.chain_pool[(uint64_t)hdr.z + (uint64_t)i * 64u];  // 64 rows interleaved
                 key[i] = (e.y << 6) | (uint32_t)i;
-                ent[i][tid] = make_uint2(e.x, e.z);
             }
         }
 #pragma unroll
@@ -220,10 +313,23 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
             bg[s] = kEmptyId;
         }
         uint32_t len = 0;
+        // G's entries in column order, read back from the pool two steps ahead
+        const uint4 *gp = p.chain_pool + hdr.z;
+        auto fetch = [&](int t) {
+            uint2 v = make_uint2(0u, 0u);
+            if ((uint32_t)t < m && keff > 0u) {
+                const uint4 e = gp[(uint64_t)order[t][tid] * 64u];
+                v = make_uint2(e.x, e.z);
+            }
+            return v;
+        };
+        uint2 x0 = fetch(0), x1 = fetch(1);
         for (int t = 0; t < kChainSeq; ++t) {
             if (!__any((uint32_t)t < m && keff > 0u)) break;
             const bool act = (uint32_t)t < m && keff > 0u;
-            const uint2 x = ent[act ? order[t][tid] : 0u][tid];
+            const uint2 x = x0;
+            x0 = x1;
+            x1 = fetch(t + 2);
             const float dc = __uint_as_float(x.x);
             const uint32_t gc = x.y;
             const bool full = len >= keff;
@@ -257,6 +363,25 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
         }
         if (live) {
             const uint64_t out = (uint64_t)hdr.x | ((uint64_t)hdr.y << 32);
+            if (((p.k | (uint32_t)out) & 3u) == 0u) {
+#pragma unroll
+                for (int s = 0; s < kChainSlots; s += 4) {
+                    if ((uint32_t)s >= p.k) continue;
+                    uint4 vi, vd;
+                    vi.x = (uint32_t)s + 0u < len ? bg[s + 0] : kEmptyId;
+                    vi.y = (uint32_t)s + 1u < len ? bg[s + 1] : kEmptyId;
+                    vi.z = (uint32_t)s + 2u < len ? bg[s + 2] : kEmptyId;
+                    vi.w = (uint32_t)s + 3u < len ? bg[s + 3] : kEmptyId;
+                    vd.x = __float_as_uint((uint32_t)s + 0u < len ? bd[s + 0] : kEmptyDist);
+                    vd.y = __float_as_uint((uint32_t)s + 1u < len ? bd[s + 1] : kEmptyDist);
+                    vd.z = __float_as_uint((uint32_t)s + 2u < len ? bd[s + 2] : kEmptyDist);
+                    vd.w = __float_as_uint((uint32_t)s + 3u < len ? bd[s + 3] : kEmptyDist);
+                    *reinterpret_cast<uint4 *>(p.out_ids + out + s) = vi;
+                    *reinterpret_cast<uint4 *>(p.out_dists + out + s) = vd;
+                }
+                done += 1;
+                continue;
+            }
 #pragma unroll
             for (int s = 0; s < kChainSlots; ++s) {
                 if ((uint32_t)s >= p.k) continue;
@@ -277,7 +402,7 @@ __global__ __launch_bounds__(kChainThreads) void leaf_chain_kernel(LeafParams p)
 
 int launch_leaf_chain(const LeafParams &p, hipStream_t stream) {
     // grid-stride over the device-side queue count: no host round trip
-    hipLaunchKernelGGL(leaf_chain_kernel, dim3(2048), dim3(kChainThreads), 0, stream, p);
+    hipLaunchKernelGGL(leaf_chain_kernel, dim3(4096), dim3(kChainThreads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -291,7 +416,7 @@ int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream) {
 
 int launch_leaf_exact_fallback(const LeafParams &p, hipStream_t stream) {
     // Grid-stride over the device-side count: no host round trip.
-    hipLaunchKernelGGL(leaf_exact_fallback_kernel, dim3(2048), dim3(kExactThreads), 0, stream, p);
+    hipLaunchKernelGGL(leaf_exact_fallback_kernel, dim3(2048), dim3(kFallbackThreads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
