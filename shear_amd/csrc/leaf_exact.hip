@@ -251,8 +251,10 @@ __global__ __launch_bounds__(kFallbackThreads) void leaf_exact_fallback_kernel(L
 //
 // One lane per queued row (|G| <= 40).  The lane sorts (column, index) keys of
 // G in registers, keeps the sorted indices in LDS, reads G's (distance, global
-// id) back from the pool in column order two steps ahead (the pool's lines are
-// still in L2), and replays the bounded insertion of leaf_build.rs:913-951 over
+// id) back from the pool in column order two steps ahead (scattered 16-byte
+// reads: most miss L2 and fetch a whole sector from HBM, which at four waves
+// per SIMD still beats holding G in LDS at 1.5), and replays the bounded
+// insertion of leaf_build.rs:913-951 over
 // a 32-slot list in registers: slot s is visited from the back, and a
 // candidate moves forward while it beats the slot before it.  Blocks of 8
 // slots that no lane of the wave can touch are skipped.  With 5 KB of LDS per
