@@ -116,6 +116,24 @@ def test_forced_exact_rerun_path_matches_oracle(gpu, orc):
         assert ctr[N.C_LEAF_ROWS] == n
 
 
+def test_forced_exact_rerun_leaves_longer_than_one_chunk(gpu, orc):
+    # The re-run kernel computes a row's distances 1,024 columns at a time:
+    # leaves of 2,500 (three chunks) and 1,100 rows, a one-row leaf, and a k
+    # that leaves output rows unaligned to 16 bytes.
+    sizes = [2500, 1, 1100]
+    n = sum(sizes)
+    codes, scales, norms, gids = _gmm_case(orc, n, 96, seed=11, sigma=0.2, comps=4)
+    members = np.arange(n, dtype=np.uint32)
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]])
+    sq8 = to_dev_sq8(codes, scales, norms, 96)
+    for k in (32, 13):
+        want_ids, want_d = orc.leaf_topk(codes, scales, norms, gids, members, offs, sizes, k)
+        ids, d, ctr = run_leaf(sq8, gids, members, offs, sizes, k, N.EXEC_MFMA, debug_rerun_every=3)
+        assert_same(ids, d, want_ids, want_d, f"k={k}")
+        assert ctr[N.C_LEAF_FALLBACK_ROWS] > 0
+        assert ctr[N.C_LEAF_ROWS] == n
+
+
 def test_heavy_tie_data_matches_oracle(gpu, orc):
     # few distinct code patterns -> exact and eps ties everywhere
     rng = np.random.default_rng(3)
