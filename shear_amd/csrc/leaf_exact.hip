@@ -8,8 +8,10 @@
 // buffer's tail is dropped, so one ballot finds the next candidate that can
 // enter; its insertion position is one past the highest slot it does not beat
 // (the reference's scan from the tail stops there) and the slots above shift
-// up by one lane.  This kernel is the semantic baseline on the GPU and
-// re-runs the rows the MFMA kernel cannot certify.
+// up by one lane.  This kernel is the semantic baseline on the GPU; the rows
+// the MFMA executor cannot certify are re-run with the same insertion by a
+// workgroup per row (exact_row_wg), and rows with eps-tie chains are replayed
+// by the chain kernel at the end of this file.
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
