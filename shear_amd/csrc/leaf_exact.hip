@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kFallbackThreads) void leaf_exact_fallback_kernel(L
 // slots that no lane of the wave can touch are skipped.  With 5 KB of LDS per
 // workgroup the kernel runs four waves per SIMD (at most 128 VGPRs); rows
 // whose output is 16-byte aligned are written with vector stores.
-constexpr int kChainSeq = 40;      // G holds at most kMaxK + 8 entries
+constexpr int kChainSeq = (int)kLeafChainSetEntries;  // G holds at most kMaxK + 8 entries
 constexpr int kChainSlots = kMaxK; // the row's top-k list
 constexpr int kChainThreads = 128;
 

@@ -71,6 +71,17 @@ constexpr uint32_t kLeafBlockRows = 256;       // member rows per work item
 constexpr uint32_t kLeafFilterThreads = 512;   // filter workgroup: 8 waves, 32 rows each
 constexpr uint32_t kLeafLogCapacity = 128;     // survivor entries per filter thread
 constexpr uint64_t kLeafLogBytesPerItem = (uint64_t)kLeafFilterThreads * kLeafLogCapacity * 8u;
+constexpr uint32_t kLeafChainSetEntries = 40;  // chain pool entries per queued row (k + 8)
+
+// Chain rows the queue and the pool can both hold: a queued row needs its
+// header slot and its candidate set in a whole 64-row pool group.  The
+// select kernel only writes a header when both fit, and the chain kernel
+// replays every header below min(count, capacity), so the capacity passed to
+// both must not exceed what the pool holds.
+inline uint64_t leaf_chain_rows_usable(uint64_t queue_capacity, uint64_t pool_entries) {
+    const uint64_t pool_rows = pool_entries / ((uint64_t)kLeafChainSetEntries * 64u) * 64u;
+    return queue_capacity < pool_rows ? queue_capacity : pool_rows;
+}
 
 // Host-side launchers (leaf_exact.hip / leaf_mfma.hip).
 int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream);

@@ -45,6 +45,7 @@ constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kTop = 32;
 constexpr int kNext = 8;
 constexpr int kSeq = kTop + kNext;
+static_assert(kSeq == (int)kLeafChainSetEntries, "a chain row's pool set holds the 40 known positions");
 
 // Sort keys: (distance, column) as one double.  The high word holds the
 // distance's bits plus 2^20 (distances are >= 0, so their bit patterns order

@@ -174,7 +174,7 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out, uint64_t list_i
     st = grow(&ws.chain_rows, &ws.chain_capacity, rows / 2 + 1, sizeof(uint4), "chain queue");
     if (st.code) return st;
     // candidate sets of 64 queue entries interleaved: whole groups of 64 x 40
-    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 64) / 64 * 64 * 40, sizeof(uint4), "chain pool");
+    st = grow(&ws.chain_pool, &ws.pool_capacity, (rows / 2 + 64) / 64 * 64 * kLeafChainSetEntries, sizeof(uint4), "chain pool");
     if (st.code) return st;
     // survivor logs and row thresholds of one batch of work items
     const uint64_t items = leaf_batch_items(rows);
@@ -442,7 +442,7 @@ tessa_status leaf_topk_impl(const tessa_sq8_view *sq8, const tessa_leaf_batch *l
     p.fallback_capacity = clamp32(sc.fallback_capacity);
     p.chain_rows = sc.chain_rows;
     p.chain_count = sc.queue_counts + 1;
-    p.chain_capacity = clamp32(sc.chain_capacity);
+    p.chain_capacity = clamp32(leaf_chain_rows_usable(sc.chain_capacity, sc.pool_capacity));
     p.chain_pool = sc.chain_pool;
     p.chain_pool_used = sc.queue_counts + 2;
     p.item_tickets = sc.queue_counts + 4;
@@ -538,7 +538,7 @@ constexpr size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr size_t kNaOffFallback = 256;
 constexpr size_t kNaOffChainRows = kNaOffFallback + a256(kNoAllocMaxRows * 2 * sizeof(uint32_t));
 constexpr size_t kNaOffChainPool = kNaOffChainRows + a256(kNoAllocChainRows * sizeof(uint4));
-constexpr uint64_t kNoAllocPoolEntries = (kNoAllocChainRows + 63) / 64 * 64 * 40;  // whole groups of 64 x 40
+constexpr uint64_t kNoAllocPoolEntries = (kNoAllocChainRows + 63) / 64 * 64 * kLeafChainSetEntries;  // whole groups of 64 x 40
 constexpr size_t kNaOffRowMeta = kNaOffChainPool + a256(kNoAllocPoolEntries * sizeof(uint4));
 constexpr size_t kNaOffLog = kNaOffRowMeta + a256(kNoAllocLogItems * kLeafBlockRows * sizeof(uint4));
 // work items: leaf_count * blocks_per_leaf <= rows / kLeafBlockRows + leaf_count
