@@ -9,13 +9,24 @@ shear-core/src/algorithm/pipnn/):
   task per D0 child through the operator (process_quantized_subtree_l2_compact_topk,
   compute_backend.rs:3794-3805; child depth 1, so its root uses fanout_second),
   candidate records -> edge records (leaf_build.rs:1679-1829) -> HashPrune
-  reservoirs (hash_prune.rs:1243-1283, l_max = R), then the `_mem.index` image
-  (pipnn_oom_writer.rs:23-72)
+  reservoirs (hash_prune.rs:1243-1283, l_max = R), optionally the final
+  RobustPrune (pipnn_builder.rs:149, :199-225, :287-330), then the
+  `_mem.index` image (pipnn_oom_writer.rs:23-72)
 * ``entry_point``             gpu_subtree_entry_point_from_sq_payloads
   (rbc_partition.rs:4964-4985): the first point of the largest D0 child, ties
   to the smaller point id
 * ``GraphBuildParams``        the PiPNNParams fields this path reads (params.rs:2109-2111
   fanout_top / fanout_second, :3341-3370 defaults)
+
+The final RobustPrune follows the build_shear_index binary: it runs only when
+asked (``final_prune``, the binary's ``--final-prune`` flag, off unless given:
+apps/build_shear_index/src/main.rs:3752-3754, copied into PiPNNParams at
+:4006 / :4064, although PiPNNParams::default() sets it, params.rs:3491), over
+the f32 points with the binary's write parameters (alpha 1.2 and max
+occlusion 750 from the builder defaults, index_write_parameters.rs:8, :17;
+saturate on, main.rs:3004-3007).  ``final_prune_alpha`` (params.rs:2372) is
+read by nothing in the reference; the prune's alpha is the write
+parameters' alpha, ``prune_alpha`` here.
 
 Every stage runs in libtessa_hip.so; this module orders the calls.  The D0
 leader sample and the sketch hyperplanes are inputs (the reference draws both
@@ -65,6 +76,11 @@ class GraphBuildParams:
     roots_rows_per_run: int = 1 << 26  # rows of the children partitioned by one many-root run
     leaf_chunk_rows: int = 1 << 22     # leaf rows per leaf top-k / record batch of a many-root run
     gpu_workspace_budget_bytes: int = 0  # per subtree task (0: the default 512 MiB plan, tasks unchecked)
+    final_prune: bool = False      # build_shear_index --final-prune (off unless given)
+    final_prune_alpha: float = 1.2  # PiPNNParams field, unused by the reference's prune
+    prune_alpha: float = 1.2        # write parameters' alpha: what the final prune uses
+    prune_max_occlusion: int = 750
+    prune_saturate: bool = True     # build_shear_index builds its write parameters with saturate_graph(true)
 
     def subtree_params(self) -> S.PiPNNSubtreeParams:
         return S.PiPNNSubtreeParams(leaf_knn=self.leaf_knn, c_max=self.c_max, fanout_second=self.fanout_second,
@@ -191,14 +207,17 @@ def build_graph(x: torch.Tensor, sketches: torch.Tensor, leader_rows: np.ndarray
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     sq8 = T.quantize_sq_int8_matrix(x)
-    return build_graph_sq8(sq8, sketches, leader_rows, p, observer, t0=w0, host_reducer=host_reducer)
+    return build_graph_sq8(sq8, sketches, leader_rows, p, observer, t0=w0, host_reducer=host_reducer,
+                           points=x if p.final_prune else None)
 
 
 def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.ndarray,
                     p: GraphBuildParams = GraphBuildParams(), observer=None,
-                    t0: float | None = None, host_reducer: TL.TierLiftParams | None = None) -> BuiltGraph:
+                    t0: float | None = None, host_reducer: TL.TierLiftParams | None = None,
+                    points: torch.Tensor | None = None) -> BuiltGraph:
     """The build from an SQ8 payload already in device memory (build time
-    counted from ``t0``, a perf_counter value, when given).
+    counted from ``t0``, a perf_counter value, when given).  ``points`` (the
+    f32 rows on the device) is needed only for ``p.final_prune``.
 
     D0 children of two or more points are the subtree tasks.  With
     ``p.multi_root`` (the default) every large child (more than leaf_max rows,
@@ -223,6 +242,8 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     give the same table."""
     dev = sq8.codes.device
     rows = sq8.rows
+    if p.final_prune and (points is None or tuple(points.shape) != (rows, sq8.dim)):
+        raise ValueError("final_prune needs the f32 points [rows, dim] on the device")
     gids = torch.arange(rows, dtype=torch.int32, device=dev)
     lrows = torch.from_numpy(np.asarray(leader_rows, np.int64)).to(dev)
     torch.cuda.synchronize()
@@ -324,6 +345,14 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         torch.cuda.synchronize()
         hp.close()  # the reservoirs go before the image is packed (at 150M points they hold 96 GB)
     del sess
+    prune_ms = 0.0
+    if p.final_prune:
+        torch.cuda.synchronize()
+        q0 = time.perf_counter()
+        targets, counts = G.robust_prune(points, targets, counts, p.l_max, p.prune_max_occlusion, p.prune_alpha,
+                                         p.prune_saturate)
+        torch.cuda.synchronize()
+        prune_ms = (time.perf_counter() - q0) * 1e3
     image = G.pack_mem_index(targets, counts, start)
     torch.cuda.synchronize()
     w2 = time.perf_counter()
@@ -333,7 +362,8 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
               "children_and_pack_ms": round((w2 - w1) * 1e3, 2), "partition_ms": round(st["part_ms"], 2),
               "leaf_ms": round(st["leaf_ms"], 2), "leaves": st["leaves"], "leaf_rows": st["leaf_rows"],
               "edge_records": st["records"], "terminal_depth_retries": st["retries"],
-              "emit_ms": round(st["emit_s"] * 1e3, 2), "reduce_ms": round(st["reduce_s"] * 1e3, 2)}
+              "emit_ms": round(st["emit_s"] * 1e3, 2), "reduce_ms": round(st["reduce_s"] * 1e3, 2),
+              "final_prune_ms": round(prune_ms, 2)}
     if tl is not None:
         stages["tierlift"] = tl_stats
     if p.gpu_workspace_budget_bytes:

@@ -87,3 +87,68 @@ class BuildObserver:
         assert np.array_equal(gc, wc), f"{what}: sampled reservoir sizes differ"
         for i in range(len(sample_h)):
             assert np.array_equal(gt[i, : gc[i]], wt[i, : wc[i]]), f"{what}: reservoir of point {sample_h[i]} differs"
+
+
+# ---- graph quality that does not depend on navigation from one entry point --
+#
+# Recall from the single entry point mixes two things: whether each point's
+# adjacency list holds its true neighbours (the build's job) and whether
+# greedy search can travel between far-apart clusters from one start.  The
+# two checks below measure the first without the second, against brute force
+# rather than against the CPU build, so a defect shared by the GPU build and
+# its CPU restatement still shows.
+
+
+def brute_knn(chunks, queries: torch.Tensor, k: int, exclude=None) -> torch.Tensor:
+    """Exact k nearest rows (squared L2, f64 accumulation of f32 rows) of each
+    query: ``chunks`` yields (first row, f32 device rows); ``exclude`` (int64
+    per query, optional) is a row each query may not return (itself).
+    Returns int64 [q, k] on the device."""
+    q = queries.double()
+    qn = (q * q).sum(1, keepdim=True)
+    best_d = best_i = None
+    for r0, xc in chunks:
+        xd = xc.double()
+        dd = qn - 2.0 * (q @ xd.t()) + (xd * xd).sum(1)[None, :]
+        if exclude is not None:
+            rel = exclude - r0
+            hit = (rel >= 0) & (rel < xc.shape[0])
+            dd[hit.nonzero().squeeze(1), rel[hit]] = float("inf")
+        kk = min(k, xc.shape[0])
+        d, i = torch.topk(dd, kk, dim=1, largest=False)
+        i = i + r0
+        if best_d is not None:
+            d, j = torch.topk(torch.cat([best_d, d], 1), k, dim=1, largest=False)
+            i = torch.gather(torch.cat([best_i, i], 1), 1, j)
+        best_d, best_i = d, i
+    return best_i
+
+
+def knn_coverage(targets: torch.Tensor, counts: torch.Tensor, sample: torch.Tensor, truth: torch.Tensor) -> float:
+    """Mean over the sampled points of (their true nearest neighbours found in
+    their adjacency list) / k; ``truth`` int64 [s, k] excludes the point itself."""
+    t = targets[sample].long()
+    valid = torch.arange(t.shape[1], device=t.device)[None, :] < counts[sample][:, None].long()
+    t = torch.where(valid, t, torch.full_like(t, -1))
+    hit = (truth[:, :, None] == t[:, None, :]).any(2)
+    return float(hit.double().mean().item())
+
+
+def seeded_recall(search, targets: torch.Tensor, counts: torch.Tensor, queries: torch.Tensor, truth: np.ndarray,
+                  k: int = 10) -> float:
+    """recall@k of searches that each start at the first graph neighbour of
+    the query's true nearest point (or at that point when it has none):
+    ``search(start, queries)`` returns ids [q, k]; queries sharing a start
+    are searched together."""
+    from shear_amd import graph as G
+
+    nn = truth[:, 0].astype(np.int64)
+    first = targets[torch.from_numpy(nn).to(targets.device), 0].cpu().numpy()
+    cnt = counts[torch.from_numpy(nn).to(targets.device)].cpu().numpy()
+    starts = np.where(cnt > 0, first, nn).astype(np.int64)
+    found = np.zeros((len(nn), k), np.int64)
+    for s in np.unique(starts):
+        sel = np.nonzero(starts == s)[0]
+        ids = search(int(s), queries[torch.from_numpy(sel).to(queries.device)])
+        found[sel] = ids.cpu().numpy()[:, :k]
+    return G.recall_at_k(found, truth, k)

@@ -8,11 +8,25 @@ Bar: the GPU image equals the CPU build's (oracle/pybuild.py: the oracle's
 restatement of every stage, fed the same points, sketches and D0 leaders)
 byte for byte, so recall@10 of the two builds is equal (north star: within
 0.002); the GPU search is checked against the oracle's search on a query
-sample."""
+sample.
+
+Graph quality without the single-entry navigation (against brute force, not
+the CPU build, so a defect both builds share still shows): the adjacency
+lists of 2,000 sampled points hold at least 60 % of their 10 true nearest
+neighbours (measured 0.685), and searches started at the first graph
+neighbour of each query's true nearest point reach recall@10 >= 0.9 at
+L = 64 (measured 0.978).  From the entry point the same searches reach
+about 0.12: the clusters lie far apart and greedy search from one start
+rarely crosses between them.
+
+The final RobustPrune (build_shear_index --final-prune) is checked the same
+way: the GPU build with it equals the CPU build's table pruned by the
+oracle's RobustPrune, byte for byte."""
 import numpy as np
 import pytest
 import torch
 
+from build_checks import brute_knn, knn_coverage, seeded_recall
 from gpu_helpers import require_gpu
 from shear_amd import datagen
 from shear_amd import graph as G
@@ -47,7 +61,8 @@ def _reachable(targets, counts, start):
     return int(seen.sum().item())
 
 
-def test_c1_gpu_build_equals_cpu_build(gpu, orc):
+@pytest.fixture(scope="module")
+def c1(gpu):
     from oracle import pybuild as PB
 
     x, q = datagen.c1_numpy()
@@ -57,8 +72,14 @@ def test_c1_gpu_build_equals_cpu_build(gpu, orc):
     sk = P.sketches_of(x, P.sketch_planes(dim, p.m_hash_bits, 7))
     xg = torch.from_numpy(x).to(gpu)
     built = P.build_graph(xg, torch.from_numpy(sk).to(gpu), lead, p)
-    img = built.image.cpu().numpy().tobytes()
     cpu = PB.build_graph_cpu(x, sk, lead, p)
+    return dict(x=x, q=q, p=p, lead=lead, sk=sk, xg=xg, built=built, cpu=cpu)
+
+
+def test_c1_gpu_build_equals_cpu_build(gpu, orc, c1):
+    x, q, p, xg, built, cpu = c1["x"], c1["q"], c1["p"], c1["xg"], c1["built"], c1["cpu"]
+    rows = x.shape[0]
+    img = built.image.cpu().numpy().tobytes()
     assert built.start == cpu["start"]
     assert len(img) == len(cpu["image"]) and img == cpu["image"], "GPU and CPU graph images differ"
     counts = built.counts.cpu().numpy()
@@ -82,3 +103,49 @@ def test_c1_gpu_build_equals_cpu_build(gpu, orc):
     reach = _reachable(built.targets, built.counts, built.start)
     print(f"C1: recall@10 (L=64) {gpu_recall:.4f}, reachable from the entry point {reach} of {rows}, "
           f"GPU build {built.build_s * 1e3:.0f} ms, CPU build {cpu['build_s']:.1f} s")
+
+
+def test_c1_graph_local_quality(gpu, c1):
+    """Adjacency lists against brute-force neighbours, and searches seeded
+    next to each query (no single-entry navigation)."""
+    x, q, p, xg, built = c1["x"], c1["q"], c1["p"], c1["xg"], c1["built"]
+    rows = x.shape[0]
+    sample = torch.from_numpy(np.sort(np.random.default_rng(11).choice(rows, 2000, replace=False))).to(gpu)
+    truth_b = brute_knn([(0, xg)], xg[sample], 10, exclude=sample)
+    cov = knn_coverage(built.targets, built.counts, sample, truth_b)
+    qg = torch.from_numpy(q).to(gpu)
+    truth_q = brute_knn([(0, xg)], qg, 10).cpu().numpy()
+    seeded = seeded_recall(lambda s, qq: G.greedy_search(xg, built.targets, built.counts, s, qq, 64, 10)[0],
+                           built.targets, built.counts, qg, truth_q)
+    ids, _, _ = G.greedy_search(xg, built.targets, built.counts, built.start, qg, 64, 10)
+    entry = G.recall_at_k(ids.cpu().numpy(), truth_q, 10)
+    print(f"C1 graph quality: 10-NN coverage of adjacency lists {cov:.4f}, recall@10 (L=64) seeded next to "
+          f"the query {seeded:.4f}, from the entry point {entry:.4f}", flush=True)
+    assert cov >= 0.60, f"adjacency lists hold {cov:.3f} of the true 10-NN"
+    assert seeded >= 0.90, f"seeded recall@10 {seeded:.3f}"
+
+
+def test_c1_final_prune_equals_cpu(gpu, orc, c1):
+    """build_shear_index --final-prune: RobustPrune of every row over the f32
+    points (alpha 1.2, max occlusion 750, saturate on) after HashPrune."""
+    from dataclasses import replace
+
+    x, q, p, xg, cpu = c1["x"], c1["q"], c1["p"], c1["xg"], c1["cpu"]
+    rows = x.shape[0]
+    pp = replace(p, final_prune=True)
+    built = P.build_graph(xg, torch.from_numpy(c1["sk"]).to(gpu), c1["lead"], pp)
+    t = np.full((rows, p.l_max), 0xFFFFFFFF, np.uint32)
+    for i, r in enumerate(cpu["rows"]):
+        t[i, : len(r)] = r
+    cnt = np.array([len(r) for r in cpu["rows"]], np.uint32)
+    wt, wc = orc.robust_prune(x, t, cnt, pp.l_max, pp.prune_max_occlusion, pp.prune_alpha, pp.prune_saturate)
+    want = orc.graph_bytes(cpu["start"], 0, [wt[i, : wc[i]] for i in range(rows)])
+    img = built.image.cpu().numpy().tobytes()
+    assert built.start == cpu["start"]
+    assert img == want, "GPU final-prune image differs from the CPU build pruned by the oracle"
+    qg = torch.from_numpy(q).to(gpu)
+    truth = brute_knn([(0, xg)], qg, 10).cpu().numpy()
+    ids, _, _ = G.greedy_search(xg, built.targets, built.counts, built.start, qg, 64, 10)
+    print(f"C1 with final prune: recall@10 (L=64) {G.recall_at_k(ids.cpu().numpy(), truth, 10):.4f}, mean degree "
+          f"{float(built.counts.float().mean()):.1f} (without: {float(c1['built'].counts.float().mean()):.1f}), "
+          f"prune {built.stages['final_prune_ms']:.1f} ms", flush=True)
