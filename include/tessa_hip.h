@@ -264,7 +264,14 @@ tessa_status tessa_session_assign_replay(tessa_session *session, const uint32_t 
 
 /* Counter words of a subtree run, at the reference's indices
  * (compute_backend.rs:5028-5187).  Words with no counterpart in this
- * implementation (queue heads, polls, locks, clocks) stay 0. */
+ * implementation (queue heads, polls, locks, most clocks) stay 0.  The phase
+ * clocks of the persistent partition walk are in ticks of the device's
+ * 100 MHz wall clock, measured by workgroup 0 between grid barriers (the
+ * reference counts SM clock cycles): BUSY the whole walk, WAIT workgroup 0's
+ * barrier waits, COUNT_DISTANCE the COUNT passes, COUNT_COMMIT the stage,
+ * item plan and EMIT passes, SCATTER the scatter, PUBLISH the child layout
+ * and numbering scans
+ * (all 0 when the partition runs level by level for a capture). */
 #define TESSA_SUBTREE_COUNTER_WORDS 159
 enum tessa_subtree_counter {
     TESSA_P_OVERFLOW_FLAGS = 7,
@@ -287,8 +294,14 @@ enum tessa_subtree_counter {
     TESSA_P_LEAF_SIZE_SUM = 35,
     TESSA_P_LEAF_SIZE_COUNT = 36,
     TESSA_P_PARTITION_LEVEL_ROUNDS = 119,
+    TESSA_P_PARTITION_BUSY_CLOCKS = 120,
+    TESSA_P_PARTITION_WAIT_CLOCKS = 121,
     TESSA_P_LARGE_SPLIT_RETRIES = 130,
     TESSA_P_LARGE_BALANCED_FALLBACKS = 131,
+    TESSA_P_LARGE_COUNT_DISTANCE_CLOCKS = 140,
+    TESSA_P_LARGE_COUNT_COMMIT_CLOCKS = 141,
+    TESSA_P_LARGE_SCATTER_CLOCKS = 142,
+    TESSA_P_LARGE_PUBLISH_CLOCKS = 143,
     TESSA_P_LARGE_PHYSICAL_TILES = 145,
     TESSA_P_LEAF_SQ8_WMMA_TILES = 158
 };

@@ -128,6 +128,14 @@ P_LEAF_SIZE_MAX = 34
 P_LEAF_SIZE_SUM = 35
 P_LEAF_SIZE_COUNT = 36
 P_PARTITION_LEVEL_ROUNDS = 119
+# phase clocks of the persistent partition walk (ticks of the 100 MHz wall clock)
+P_PARTITION_BUSY_CLOCKS = 120
+P_PARTITION_WAIT_CLOCKS = 121
+P_LARGE_COUNT_DISTANCE_CLOCKS = 140
+P_LARGE_COUNT_COMMIT_CLOCKS = 141
+P_LARGE_SCATTER_CLOCKS = 142
+P_LARGE_PUBLISH_CLOCKS = 143
+P_CLOCK_WORDS = (120, 121, 140, 141, 142, 143)
 P_LARGE_SPLIT_RETRIES = 130
 P_LARGE_BALANCED_FALLBACKS = 131
 P_LARGE_PHYSICAL_TILES = 145

@@ -13,6 +13,7 @@
 // distances go through LDS so that one lane per member can apply the
 // order-dependent insertion in leader-slot order.  Member codes are read once
 // from HBM; leader codes come from L2 after the first workgroup of the task.
+#include "kernel_attr.h"
 #include "assign_kernels.h"
 #include "tessa_device.h"
 
@@ -207,13 +208,7 @@ __global__ __launch_bounds__(kThreads, 1) void assign_mfma_kernel(AssignParams p
 template <int KS>
 int launch_assign_ks(const AssignParams &p, hipStream_t stream) {
     using L = ALayout<KS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)assign_mfma_kernel<KS>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes) != hipSuccess)
-            return -1;
-        attr_set = true;
-    }
+    if (ensure_lds_limit(reinterpret_cast<const void *>(assign_mfma_kernel<KS>), L::kBytes)) return -1;
     const uint32_t per_block = kChunkMembers * kChunksPerBlock;
     const uint32_t blocks_per_task = (p.max_members + per_block - 1) / per_block;
     const uint64_t total = (uint64_t)blocks_per_task * p.task_count;

@@ -27,6 +27,7 @@
 // child's points keep ascending row order; offsets from a child histogram.
 #include <hipcub/hipcub.hpp>
 
+#include "kernel_attr.h"
 #include "d0_kernels.h"
 #include "tessa_device.h"
 
@@ -200,13 +201,7 @@ __global__ __launch_bounds__(kThreads) void d0_assign_kernel(D0AssignParams p) {
 template <int KS, int F>
 int launch_kf(const D0AssignParams &p, dim3 grid, hipStream_t stream) {
     constexpr int lds = 2 * D0Tile<KS>::kBytes;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&d0_assign_kernel<KS, F>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-            return -1;
-        attr = true;
-    }
+    if (ensure_lds_limit(reinterpret_cast<const void *>(&d0_assign_kernel<KS, F>), (int)lds)) return -1;
     hipLaunchKernelGGL((d0_assign_kernel<KS, F>), grid, dim3(kThreads), lds, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

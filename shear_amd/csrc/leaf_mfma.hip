@@ -41,6 +41,7 @@
 #include <type_traits>
 #include <utility>
 
+#include "kernel_attr.h"
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
@@ -832,15 +833,9 @@ uint32_t cu_count() {
 template <int KS>
 int launch_ks(const LeafParams &p, hipStream_t stream) {
     using L = Layout<KS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kLdsBudget) != hipSuccess ||
-            hipFuncSetAttribute((const void *)leaf_mfma_kernel<KS, 4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kLdsBudget) != hipSuccess)
-            return -1;
-        attr_set = true;
-    }
+    if (ensure_lds_limit(reinterpret_cast<const void *>(leaf_mfma_kernel<KS, 2>), (int)kLdsBudget) ||
+        ensure_lds_limit(reinterpret_cast<const void *>(leaf_mfma_kernel<KS, 4>), (int)kLdsBudget))
+        return -1;
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     // four tile buffers (a barrier every second position) when they fit
     const bool four = lds_bytes(L::kTileBytes, 4, cols_cap) <= kLdsBudget;

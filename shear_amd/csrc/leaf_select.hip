@@ -33,6 +33,7 @@
 //  * anything else (no gap, an overflowed log) sends the row to the exact
 //    re-run.
 // Queue slots are reserved with one atomic per wave.
+#include "kernel_attr.h"
 #include "leaf_kernels.h"
 #include "tessa_device.h"
 
@@ -466,13 +467,7 @@ int launch_leaf_select(const LeafParams &p, hipStream_t stream) {
     if (p.item_count == 0) return 0;
     const uint32_t cols_cap = (p.max_leaf_rows + 31u) & ~31u;
     const uint32_t lds = cols_cap * 12u;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)leaf_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                64 * 1024) != hipSuccess)
-            return -1;
-        attr_set = true;
-    }
+    if (ensure_lds_limit(reinterpret_cast<const void *>(leaf_select_kernel), 64 * 1024)) return -1;
     if (lds > 64u * 1024u) return -4;
     hipLaunchKernelGGL(leaf_select_kernel, dim3(p.item_count), dim3(kSelThreads), lds, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -49,7 +49,19 @@ struct NodeDesc {
     uint32_t pad;
 };
 
-// Level summary, copied to the host after each level.
+constexpr uint32_t kPartMaxAttempts = 16;  // COUNT / EMIT passes per level
+
+// Walk outcome words (LevelHeader::walk_status).
+enum WalkStatus : uint32_t {
+    kWalkOk = 0,
+    kWalkBound = 2,     // level or attempt bound exceeded
+    kWalkCapacity = 3,  // the next level's work items exceed the workspace
+    kWalkStalled = 4,   // a grid barrier outlived the watchdog (WATCHDOG_STALLED)
+};
+
+// Level summary and the walk's control words, in device memory; the host
+// reads it once the partition has finished (and, on the capture path,
+// after every level).
 struct LevelHeader {
     uint64_t leaf_count;
     uint64_t leaf_rows;
@@ -59,6 +71,13 @@ struct LevelHeader {
     uint32_t items;
     uint32_t retry_nodes;
     uint32_t pad;
+    // persistent walk: grid barrier arrivals (monotonic over the launch),
+    // EMIT retries per attempt of the current level, and the walk's result
+    uint32_t barrier;
+    uint32_t walk_status;
+    uint32_t levels;
+    uint32_t count_passes;
+    uint32_t retry[kPartMaxAttempts];
 };
 
 struct PartArgs {
@@ -112,9 +131,13 @@ struct PartArgs {
     uint32_t *child_rel;     // node_cap x 128: row offset within the node's leaf / node rows
     uint32_t *slots;         // arena_cap: 4 packed 8-bit leader slots per row
     uint32_t *item_counts;   // item_cap x 128
+    uint32_t *item_node;     // item_cap: the level's item -> node map
     uint64_t arena_cap;
     uint64_t item_cap;
     uint32_t node_cap;
+    // persistent walk: a grid barrier that waits longer than this many
+    // wall-clock ticks flags WATCHDOG_STALLED and ends the walk
+    uint64_t watchdog_ticks;
 };
 
 struct PartResult {
@@ -122,6 +145,9 @@ struct PartResult {
     uint64_t leaf_rows;
     uint32_t levels;
     uint32_t count_launches;
+    // on a -1 return: the failing HIP call's error and what it was doing
+    int hip_error;
+    const char *failed_step;
 };
 
 // Assignment tasks seen by the COUNT passes (capture, host side): per task
@@ -144,9 +170,12 @@ struct PartCapture {
 void partition_capacity(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_t *arena_cap, uint32_t *node_cap,
                         uint64_t *item_cap);
 
-// Runs the whole partition on `stream` (host-synchronising between levels).
-// Returns 0, or -1 on a launch failure, -2 when the level loop exceeds its
-// bound, -3 when a workspace capacity is exceeded before launch.
+// Runs the whole partition on `stream`: one persistent walk kernel for the
+// level loop (no host round trip between levels), or, when `capture` is
+// given, the level-by-level launches with a host copy before each COUNT
+// pass.  Returns 0, or -1 on a launch failure, -2 when the level loop
+// exceeds its bound, -3 when a workspace capacity is exceeded, -4 when the
+// walk's watchdog fired (also flagged as WATCHDOG_STALLED).
 int run_partition(const PartArgs &a, hipStream_t stream, LevelHeader *host_hdr, PartResult *res,
                   PartCapture *capture = nullptr);
 

@@ -25,6 +25,7 @@
 //   scatter    one workgroup per item: rows to leaves / next arena
 #include <type_traits>
 
+#include "kernel_attr.h"
 #include "partition.h"
 #include "tessa_device.h"
 
@@ -136,18 +137,6 @@ __device__ uint64_t block_exclusive_scan(uint64_t v, uint64_t *sh, uint64_t *tot
     return incl - v;
 }
 
-// Item -> node: the last node whose item_base <= item (nodes with no items
-// share the next node's base, so the last such node owns the item).
-__device__ uint32_t find_item_node(const NodeDesc *nodes, uint32_t level_nodes, uint32_t item) {
-    uint32_t lo = 0, hi = level_nodes - 1u;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi + 1u) >> 1;
-        if (nodes[mid].item_base <= item) lo = mid;
-        else hi = mid - 1u;
-    }
-    return lo;
-}
-
 // ---------------------------------------------------------------------------
 __global__ void init_kernel(PartArgs a) {
     for (uint32_t i = threadIdx.x; i < TESSA_SUBTREE_COUNTER_WORDS; i += blockDim.x) a.counters[i] = 0ull;
@@ -195,11 +184,13 @@ __global__ void multi_root_kernel(PartArgs a) {
 __global__ void reset_retry_kernel(LevelHeader *h) { h->retry_nodes = 0u; }
 
 // ---- stage (compute_backend.rs:12456-12646) ---------------------------------
-__global__ __launch_bounds__(128) void stage_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
-    const uint32_t ni = blockIdx.x;
+// One node per wave: lane 0 takes the node's split parameters, the lanes
+// write its 128 leader words.
+__device__ __forceinline__ void stage_node_wave(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint32_t ni) {
+    const uint32_t lane = threadIdx.x & 63u;
     NodeDesc *nd = a.nodes[cur] + ni;
-    __shared__ uint32_t s_nl, s_use_root;
-    if (threadIdx.x == 0) {
+    uint32_t s_nl = 0u, s_use_root = 0u;
+    if (lane == 0u) {
         if (ni == 0) {
             pc_add(a.counters, TESSA_P_PARTITION_POPS, level_nodes);
             pc_add(a.counters, TESSA_P_PARTITION_LEVEL_ROUNDS, 1);
@@ -245,29 +236,34 @@ __global__ __launch_bounds__(128) void stage_kernel(PartArgs a, uint32_t cur, ui
         s_nl = status == kNodeCounting ? nl : 0u;
         s_use_root = use_root;
     }
-    __syncthreads();
-    const uint32_t t = threadIdx.x;
-    const uint32_t nl = s_nl;
-    uint32_t leader = 0u;
-    if (t < nl) {
-        if (s_use_root) {
-            leader = a.root_leaders[t];
-        } else {
-            const uint32_t n = nd->n;
-            uint32_t ord = (uint32_t)(((uint64_t)t * n) / nl);
-            if (ord >= n) ord = n - 1u;
-            leader = a.arena[cur][nd->row_start + ord];
+    const uint32_t nl = __shfl(s_nl, 0);
+    const uint32_t use_root = __shfl(s_use_root, 0);
+    for (uint32_t t = lane; t < kPartMaxLeaders; t += 64u) {
+        uint32_t leader = 0u;
+        if (t < nl) {
+            if (use_root) {
+                leader = a.root_leaders[t];
+            } else {
+                const uint32_t n = nd->n;
+                uint32_t ord = (uint32_t)(((uint64_t)t * n) / nl);
+                if (ord >= n) ord = n - 1u;
+                leader = a.arena[cur][nd->row_start + ord];
+            }
         }
+        a.leaders[(uint64_t)ni * kPartMaxLeaders + t] = leader;
+        a.child_counts[(uint64_t)ni * kPartMaxLeaders + t] = 0u;
     }
-    a.leaders[(uint64_t)ni * kPartMaxLeaders + t] = leader;
-    a.child_counts[(uint64_t)ni * kPartMaxLeaders + t] = 0u;
+}
+
+__global__ __launch_bounds__(64) void stage_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+    stage_node_wave(a, cur, level_nodes, blockIdx.x);
 }
 
 // ---- item plan ---------------------------------------------------------------
-__global__ __launch_bounds__(1024) void item_plan_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
-    __shared__ uint64_t sh[1024];
+// One block of any power-of-two size; sh holds blockDim.x words.
+__device__ __forceinline__ void item_plan_block(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint64_t *sh) {
     NodeDesc *nodes = a.nodes[cur];
-    const uint32_t per = (level_nodes + 1023u) / 1024u;
+    const uint32_t per = (level_nodes + blockDim.x - 1u) / blockDim.x;
     const uint32_t b = threadIdx.x * per;
     const uint32_t e = b + per < level_nodes ? b + per : level_nodes;
     uint64_t local = 0;
@@ -290,6 +286,26 @@ __global__ __launch_bounds__(1024) void item_plan_kernel(PartArgs a, uint32_t cu
         a.hdr->items = (uint32_t)total;
         a.hdr->retry_nodes = 0u;
     }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void item_plan_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+    __shared__ uint64_t sh[1024];
+    item_plan_block(a, cur, level_nodes, sh);
+}
+
+// The level's item -> node map, one node per wave (items past the planned
+// total are never listed).
+__device__ __forceinline__ void item_map_wave(const PartArgs &a, uint32_t cur, uint32_t ni) {
+    const NodeDesc *nd = a.nodes[cur] + ni;
+    const uint32_t total = a.hdr->items;
+    const uint32_t base = nd->item_base, items = nd->items;
+    for (uint32_t it = threadIdx.x & 63u; it < items; it += 64u)
+        if (base + it < total) a.item_node[base + it] = ni;
+}
+
+__global__ __launch_bounds__(64) void item_map_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+    item_map_wave(a, cur, blockIdx.x);
 }
 
 // ---- COUNT: best leader slots per row on int8 MFMA --------------------------
@@ -334,19 +350,21 @@ __device__ __forceinline__ void wave_lds_sync() {
 // the node differs from the previous item's (a large node's items reuse them).
 // Each wave owns 32 rows at a time and its own distance buffer, so inside an
 // item the waves only synchronise with themselves.
+// One COUNT pass over the level's items first_item, + stride, ...; `smem` is
+// the CountLayout<KS> buffer and `s_node` a shared word.  The block has
+// CountLayout<KS>::kThreads threads.
 template <int KS>
-__global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(PartArgs a, uint32_t cur,
-                                                                             uint32_t level_nodes) {
+__device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint32_t first_item,
+                            uint32_t stride, unsigned char *smem, uint32_t *s_node_ptr) {
     using L = CountLayout<KS>;
     constexpr uint32_t kThr = L::kThreads;
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    uint32_t &s_node = *s_node_ptr;
     int8_t *lcodes = reinterpret_cast<int8_t *>(smem);
     float *ls = reinterpret_cast<float *>(smem + L::kMetaOff);
     float *ln = ls + kPartMaxLeaders;
     uint32_t *lid = reinterpret_cast<uint32_t *>(ln + kPartMaxLeaders);
     uint32_t *cnt = reinterpret_cast<uint32_t *>(smem + L::kCntOff);
     float *dbuf = reinterpret_cast<float *>(smem + L::kDistOff);
-    __shared__ uint32_t s_node;
 
     const uint32_t items = a.hdr->items;
     const uint32_t pd = a.padded_dim;
@@ -359,8 +377,8 @@ __global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(Par
     // resident row -> SQ8 row; tie keys use the row's index within its root
     const uint32_t *rmap = a.row_map;
     uint32_t staged = 0xffffffffu;  // node whose leaders are in LDS
-    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        if (tid == 0) s_node = find_item_node(a.nodes[cur], level_nodes, item);
+    for (uint32_t item = first_item; item < items; item += stride) {
+        if (tid == 0) s_node = a.item_node[item];
         __syncthreads();
         const uint32_t ni = s_node;
         const NodeDesc *nd = a.nodes[cur] + ni;
@@ -523,21 +541,28 @@ __global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(Par
     }
 }
 
+template <int KS>
+__global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void count_kernel(PartArgs a, uint32_t cur,
+                                                                             uint32_t level_nodes) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    __shared__ uint32_t s_node;
+    count_items<KS>(a, cur, level_nodes, blockIdx.x, gridDim.x, smem, &s_node);
+}
+
 // ---- EMIT (compute_backend.rs:15396-15555) -----------------------------------
-__global__ __launch_bounds__(128) void emit_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
-    const uint32_t ni = blockIdx.x;
+// One node per wave; a retry adds 1 to *retry_ctr.  Lane l holds slots l
+// and l + 64; lane 0 decides.
+__device__ __forceinline__ void emit_node_wave(const PartArgs &a, uint32_t cur, uint32_t ni, uint32_t *retry_ctr) {
+    const uint32_t lane = threadIdx.x & 63u;
     NodeDesc *nd = a.nodes[cur] + ni;
-    if (nd->status != kNodeCounting) return;
-    __shared__ uint64_t s_sum[2];
-    __shared__ uint32_t s_nonempty[2], s_max[2];
-    __shared__ uint32_t s_act, s_next, s_attempt;
-    const uint32_t t = threadIdx.x;
+    if (nd->status != kNodeCounting) return;  // one word, read by the whole wave
     const uint32_t nl = nd->num_leaders;
     const uint32_t n = nd->n;
     uint32_t *counts = a.child_counts + (uint64_t)ni * kPartMaxLeaders;
-    const uint32_t c = t < nl ? counts[t] : 0u;
-    uint64_t sum = c;
-    uint32_t ne = c ? 1u : 0u, mx = c;
+    const uint32_t c0 = lane < nl ? counts[lane] : 0u;
+    const uint32_t c1 = lane + 64u < nl ? counts[lane + 64u] : 0u;
+    uint64_t sum = (uint64_t)c0 + c1;
+    uint32_t ne = (c0 ? 1u : 0u) + (c1 ? 1u : 0u), mx = c0 > c1 ? c0 : c1;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         sum += __shfl_xor(sum, off);
@@ -545,17 +570,11 @@ __global__ __launch_bounds__(128) void emit_kernel(PartArgs a, uint32_t cur, uin
         const uint32_t o = __shfl_xor(mx, off);
         mx = o > mx ? o : mx;
     }
-    if ((t & 63u) == 0u) {
-        s_sum[t >> 6] = sum;
-        s_nonempty[t >> 6] = ne;
-        s_max[t >> 6] = mx;
-    }
-    __syncthreads();
-    if (t == 0) {
-        const uint64_t running = s_sum[0] + s_sum[1];
-        const uint32_t nonempty = s_nonempty[0] + s_nonempty[1];
-        const uint32_t max_child = s_max[0] > s_max[1] ? s_max[0] : s_max[1];
-        s_act = 0u;
+    uint32_t act = 0u, s_next = 0u, s_attempt = 0u;
+    if (lane == 0u) {
+        const uint64_t running = sum;
+        const uint32_t nonempty = ne;
+        const uint32_t max_child = mx;
         if (running > a.large_scratch_rows) {
             pc_flag(a.counters, TESSA_OVF_QUEUE_ROW);
             nd->status = kNodeIdle;
@@ -573,11 +592,11 @@ __global__ __launch_bounds__(128) void emit_kernel(PartArgs a, uint32_t cur, uin
             if (next > max_leaders) next = max_leaders;
             nd->num_leaders = next;
             nd->attempt += 1u;
-            s_act = 1u;
+            act = 1u;
             s_next = next;
             s_attempt = nd->attempt;
             pc_add(a.counters, TESSA_P_LARGE_SPLIT_RETRIES, 1);
-            atomicAdd(&a.hdr->retry_nodes, 1u);
+            atomicAdd(retry_ctr, 1u);
         } else {
             nd->status = kNodeBalanced;
             nd->num_leaders = 2u;
@@ -589,119 +608,212 @@ __global__ __launch_bounds__(128) void emit_kernel(PartArgs a, uint32_t cur, uin
             pc_add(a.counters, TESSA_P_REPLICATED_ROWS, n);
         }
     }
-    __syncthreads();
-    if (s_act == 1u) {
+    if (__shfl(act, 0) == 1u) {
         // compute_backend.rs:5991-6019 hash-sampled retry leaders, one per span.
-        const uint32_t next = s_next;
-        uint32_t leader = 0u;
-        if (t < next) {
-            uint32_t b = (uint32_t)(((uint64_t)t * n) / next);
-            uint32_t e = (uint32_t)(((uint64_t)(t + 1u) * n) / next);
-            if (e <= b) e = b + 1u;
-            const uint32_t span = e - b;
-            const uint64_t key = hash64(nd->seed ^ ((uint64_t)s_attempt * 0xd6e8feb86659fd93ull) ^
-                                        ((uint64_t)t * 0x9e3779b97f4a7c15ull));
-            leader = a.arena[cur][nd->row_start + b + (uint32_t)(key % span)];
+        const uint32_t next = __shfl(s_next, 0);
+        const uint32_t attempt = __shfl(s_attempt, 0);
+        const uint64_t seed = nd->seed;
+        const uint64_t row_start = nd->row_start;
+        for (uint32_t t = lane; t < kPartMaxLeaders; t += 64u) {
+            uint32_t leader = 0u;
+            if (t < next) {
+                uint32_t b = (uint32_t)(((uint64_t)t * n) / next);
+                uint32_t e = (uint32_t)(((uint64_t)(t + 1u) * n) / next);
+                if (e <= b) e = b + 1u;
+                const uint32_t span = e - b;
+                const uint64_t key = hash64(seed ^ ((uint64_t)attempt * 0xd6e8feb86659fd93ull) ^
+                                            ((uint64_t)t * 0x9e3779b97f4a7c15ull));
+                leader = a.arena[cur][row_start + b + (uint32_t)(key % span)];
+            }
+            a.leaders[(uint64_t)ni * kPartMaxLeaders + t] = leader;
+            counts[t] = 0u;
         }
-        a.leaders[(uint64_t)ni * kPartMaxLeaders + t] = leader;
-        counts[t] = 0u;
     }
 }
 
+__global__ __launch_bounds__(64) void emit_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+    emit_node_wave(a, cur, blockIdx.x, &a.hdr->retry_nodes);
+}
+
 // ---- child layout and per-item prefixes ----------------------------------
-// 8 groups of 128 threads (one thread per leader slot) split the node's items
-// into 8 ranges; each group sums its range, the groups' sums are scanned in
-// LDS, then each group writes the exclusive prefixes of its range.  Item
-// counts are read 16 items at a time, so the loads of a batch are in flight
-// together.
+// Stable scatter needs, per item and slot, the exclusive prefix of the
+// slot's count over the node's earlier items.  A node with many items is
+// scanned by a whole workgroup: groups of 128 threads (one thread per leader
+// slot) split its items into ranges, each group sums its range, the groups'
+// sums are scanned in LDS, then each group writes the prefixes of its range.
+// A node with few items is scanned by one wave (lane l owns slots l and
+// l + 64).  Item counts are read 16 items at a time, so the loads of a batch
+// are in flight together.
 constexpr uint32_t kScanGroups = 8;
 constexpr uint32_t kScanBatch = 16;
+constexpr uint32_t kWaveScanItems = 16;  // nodes with at most this many items: one wave
 
-__global__ __launch_bounds__(kScanGroups * kPartMaxLeaders) void node_scan_kernel(PartArgs a, uint32_t cur,
-                                                                                 uint32_t level_nodes) {
-    __shared__ uint32_t group_sum[kScanGroups][kPartMaxLeaders];
-    const uint32_t ni = blockIdx.x;
-    NodeDesc *nd = a.nodes[cur] + ni;
-    const uint32_t status = nd->status;
-    if (status != kNodeAccepted && status != kNodeBalanced) return;
+__device__ __forceinline__ void node_item_prefix_block(const PartArgs &a, const NodeDesc *nd, uint32_t nl,
+                                       uint32_t (*group_sum)[kPartMaxLeaders]) {
+    const uint32_t groups = blockDim.x / kPartMaxLeaders;
     const uint32_t t = threadIdx.x % kPartMaxLeaders;
     const uint32_t g = threadIdx.x / kPartMaxLeaders;
-    const uint32_t nl = nd->num_leaders;
-    const uint64_t cbase = (uint64_t)ni * kPartMaxLeaders;
-    if (status == kNodeAccepted) {
-        // Stable scatter: exclusive prefix of this slot's count over the items.
-        const uint32_t items = nd->items;
-        const uint32_t per = (items + kScanGroups - 1u) / kScanGroups;
-        const uint32_t i0 = g * per < items ? g * per : items;
-        const uint32_t i1 = i0 + per < items ? i0 + per : items;
-        uint32_t *col = a.item_counts + (uint64_t)nd->item_base * kPartMaxLeaders + t;
-        uint32_t sum = 0u;
-        if (t < nl) {
-            for (uint32_t i = i0; i < i1; i += kScanBatch) {
-                uint32_t v[kScanBatch];
+    const uint32_t items = nd->items;
+    const uint32_t per = (items + groups - 1u) / groups;
+    const uint32_t i0 = g * per < items ? g * per : items;
+    const uint32_t i1 = i0 + per < items ? i0 + per : items;
+    uint32_t *col = a.item_counts + (uint64_t)nd->item_base * kPartMaxLeaders + t;
+    uint32_t sum = 0u;
+    if (t < nl) {
+        for (uint32_t i = i0; i < i1; i += kScanBatch) {
+            uint32_t v[kScanBatch];
 #pragma unroll
-                for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
+            for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
 #pragma unroll
-                for (uint32_t u = 0; u < kScanBatch; ++u) sum += v[u];
-            }
+            for (uint32_t u = 0; u < kScanBatch; ++u) sum += v[u];
         }
-        group_sum[g][t] = sum;
-        __syncthreads();
-        uint32_t run = 0u;
-        for (uint32_t h = 0; h < g; ++h) run += group_sum[h][t];
-        if (t < nl) {
-            for (uint32_t i = i0; i < i1; i += kScanBatch) {
-                uint32_t v[kScanBatch];
+    }
+    group_sum[g][t] = sum;
+    __syncthreads();
+    uint32_t run = 0u;
+    for (uint32_t h = 0; h < g; ++h) run += group_sum[h][t];
+    if (t < nl) {
+        for (uint32_t i = i0; i < i1; i += kScanBatch) {
+            uint32_t v[kScanBatch];
 #pragma unroll
-                for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
+            for (uint32_t u = 0; u < kScanBatch; ++u) v[u] = i + u < i1 ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
 #pragma unroll
-                for (uint32_t u = 0; u < kScanBatch; ++u) {
-                    if (i + u < i1) col[(uint64_t)(i + u) * kPartMaxLeaders] = run;
-                    run += v[u];
-                }
+            for (uint32_t u = 0; u < kScanBatch; ++u) {
+                if (i + u < i1) col[(uint64_t)(i + u) * kPartMaxLeaders] = run;
+                run += v[u];
             }
         }
     }
-    if (threadIdx.x == 0) {
-        // compute_backend.rs:15666-15718: children in slot order.
-        uint32_t leaf_children = 0, node_children = 0;
-        uint64_t leaf_rows = 0, node_rows = 0;
-        bool stop = false;
-        for (uint32_t s = 0; s < kPartMaxLeaders; ++s) {
-            const uint32_t c = s < nl ? a.child_counts[cbase + s] : 0u;
-            uint32_t idx = kChildEmpty;
-            uint32_t rel = 0;
-            if (c != 0u && !stop) {
-                if (c <= a.leaf_max) {
-                    idx = leaf_children++;
-                    rel = (uint32_t)leaf_rows;
-                    leaf_rows += c;
-                } else if (nd->depth + 1u >= a.max_depth) {
-                    pc_flag(a.counters, TESSA_OVF_OVERSIZED_TERMINAL_NODE);
-                    stop = true;
-                } else {
-                    idx = kChildNodeBit | node_children++;
-                    rel = (uint32_t)node_rows;
-                    node_rows += c;
-                }
-            }
-            a.child_idx[cbase + s] = idx;
-            a.child_rel[cbase + s] = rel;
+    __syncthreads();  // group_sum is reused by the next node
+}
+
+__device__ __forceinline__ void node_item_prefix_wave(const PartArgs &a, const NodeDesc *nd, uint32_t nl) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t items = nd->items;
+    uint32_t *col = a.item_counts + (uint64_t)nd->item_base * kPartMaxLeaders + lane;
+    const bool live0 = lane < nl, live1 = lane + 64u < nl;
+    uint32_t run0 = 0u, run1 = 0u;
+    for (uint32_t i = 0; i < items; i += kScanBatch) {
+        uint32_t v0[kScanBatch], v1[kScanBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kScanBatch; ++u) {
+            const bool in = i + u < items;
+            v0[u] = (in && live0) ? col[(uint64_t)(i + u) * kPartMaxLeaders] : 0u;
+            v1[u] = (in && live1) ? col[(uint64_t)(i + u) * kPartMaxLeaders + 64u] : 0u;
         }
-        nd->leaf_children = leaf_children;
-        nd->node_children = node_children;
-        nd->leaf_rows = leaf_rows;
-        nd->node_rows = node_rows;
+#pragma unroll
+        for (uint32_t u = 0; u < kScanBatch; ++u) {
+            if (i + u < items) {
+                if (live0) col[(uint64_t)(i + u) * kPartMaxLeaders] = run0;
+                if (live1) col[(uint64_t)(i + u) * kPartMaxLeaders + 64u] = run1;
+            }
+            run0 += v0[u];
+            run1 += v1[u];
+        }
+    }
+}
+
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+        const uint64_t y = __shfl_up(v, off);
+        v += lane >= off ? y : 0ull;
+    }
+    return v;
+}
+
+// compute_backend.rs:15666-15718: children in slot order, one wave.  A child
+// of more than leaf_max rows at the depth limit flags OVERSIZED_TERMINAL_NODE
+// and, with every later slot, gets no child.  Slot s = lane + 64 h.
+__device__ __forceinline__ void node_layout_wave(const PartArgs &a, NodeDesc *nd, uint32_t ni) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t nl = nd->num_leaders;
+    const uint64_t cbase = (uint64_t)ni * kPartMaxLeaders;
+    const bool terminal = nd->depth + 1u >= a.max_depth;
+    uint32_t c[2];
+    uint32_t kind[2];  // 0 empty, 1 leaf, 2 next-level node, 3 oversized at the depth limit
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t sl = lane + 64u * h;
+        c[h] = sl < nl ? a.child_counts[cbase + sl] : 0u;
+        kind[h] = c[h] == 0u ? 0u : (c[h] <= a.leaf_max ? 1u : (terminal ? 3u : 2u));
+    }
+    const uint64_t ovf0 = __ballot(kind[0] == 3u), ovf1 = __ballot(kind[1] == 3u);
+    const uint32_t first_ovf = ovf0 ? (uint32_t)__builtin_ctzll(ovf0)
+                                    : (ovf1 ? 64u + (uint32_t)__builtin_ctzll(ovf1) : kPartMaxLeaders);
+    uint64_t leaf_base = 0ull, leaf_rows_base = 0ull, node_base = 0ull, node_rows_base = 0ull;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t sl = lane + 64u * h;
+        const bool alive = sl < first_ovf;
+        const bool leaf = alive && kind[h] == 1u;
+        const bool node = alive && kind[h] == 2u;
+        const uint64_t il = wave_incl_scan(leaf ? 1ull : 0ull);
+        const uint64_t rl = wave_incl_scan(leaf ? c[h] : 0ull);
+        const uint64_t in_ = wave_incl_scan(node ? 1ull : 0ull);
+        const uint64_t rn = wave_incl_scan(node ? c[h] : 0ull);
+        uint32_t idx = kChildEmpty, rel = 0u;
+        if (leaf) {
+            idx = (uint32_t)(leaf_base + il - 1ull);
+            rel = (uint32_t)(leaf_rows_base + rl - c[h]);
+        } else if (node) {
+            idx = kChildNodeBit | (uint32_t)(node_base + in_ - 1ull);
+            rel = (uint32_t)(node_rows_base + rn - c[h]);
+        }
+        a.child_idx[cbase + sl] = idx;
+        a.child_rel[cbase + sl] = rel;
+        leaf_base += __shfl(il, 63);
+        leaf_rows_base += __shfl(rl, 63);
+        node_base += __shfl(in_, 63);
+        node_rows_base += __shfl(rn, 63);
+    }
+    if (lane == 0u) {
+        if (first_ovf < kPartMaxLeaders) pc_flag(a.counters, TESSA_OVF_OVERSIZED_TERMINAL_NODE);
+        nd->leaf_children = (uint32_t)leaf_base;
+        nd->node_children = (uint32_t)node_base;
+        nd->leaf_rows = leaf_rows_base;
+        nd->node_rows = node_rows_base;
         pc_add(a.counters, TESSA_P_ASSIGNMENT_PASSES, 1);
         pc_add(a.counters, TESSA_P_LARGE_NODE_SPLITS, 1);
     }
 }
 
+__device__ __forceinline__ bool node_split(uint32_t status) {
+    return status == kNodeAccepted || status == kNodeBalanced;
+}
+
+// One node, a whole workgroup (a multiple of 128 threads, at most
+// kScanGroups x 128); group_sum holds kScanGroups x 128 words.
+__device__ __forceinline__ void node_scan_block(const PartArgs &a, uint32_t cur, uint32_t ni, uint32_t (*group_sum)[kPartMaxLeaders]) {
+    NodeDesc *nd = a.nodes[cur] + ni;
+    const uint32_t status = nd->status;
+    if (!node_split(status)) return;
+    if (status == kNodeAccepted) node_item_prefix_block(a, nd, nd->num_leaders, group_sum);
+    if (threadIdx.x < 64u) node_layout_wave(a, nd, ni);
+}
+
+// One node, one wave.
+__device__ __forceinline__ void node_scan_wave(const PartArgs &a, uint32_t cur, uint32_t ni) {
+    NodeDesc *nd = a.nodes[cur] + ni;
+    const uint32_t status = nd->status;
+    if (!node_split(status)) return;
+    if (status == kNodeAccepted) node_item_prefix_wave(a, nd, nd->num_leaders);
+    node_layout_wave(a, nd, ni);
+}
+
+__global__ __launch_bounds__(kScanGroups * kPartMaxLeaders) void node_scan_kernel(PartArgs a, uint32_t cur,
+                                                                                 uint32_t level_nodes) {
+    __shared__ uint32_t group_sum[kScanGroups][kPartMaxLeaders];
+    node_scan_block(a, cur, blockIdx.x, group_sum);
+}
+
 // ---- numbering of leaves and next-level nodes -------------------------------
-__global__ __launch_bounds__(1024) void pub_scan_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
-    __shared__ uint64_t sh[1024];
+// One block of any power-of-two size; sh holds blockDim.x words.
+__device__ __forceinline__ void pub_scan_block(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint64_t *sh) {
     NodeDesc *nodes = a.nodes[cur];
-    const uint32_t per = (level_nodes + 1023u) / 1024u;
+    const uint32_t per = (level_nodes + blockDim.x - 1u) / blockDim.x;
     const uint32_t b = threadIdx.x * per;
     const uint32_t e = b + per < level_nodes ? b + per : level_nodes;
     auto live = [&](uint32_t i) { return nodes[i].status == kNodeAccepted || nodes[i].status == kNodeBalanced; };
@@ -747,147 +859,171 @@ __global__ __launch_bounds__(1024) void pub_scan_kernel(PartArgs a, uint32_t cur
         a.counters[TESSA_P_OUTPUT_ROWS] = h->leaf_rows;
         h->overflow = atomicOr((unsigned long long *)&a.counters[TESSA_P_OVERFLOW_FLAGS], 0ull);
     }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void pub_scan_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
+    __shared__ uint64_t sh[1024];
+    pub_scan_block(a, cur, level_nodes, sh);
 }
 
 // ---- SCATTER + PUBLISH (compute_backend.rs:15556-15727) ---------------------
-__global__ __launch_bounds__(256) void scatter_kernel(PartArgs a, uint32_t cur, uint32_t level_nodes) {
-    __shared__ uint32_t s_node;
-    __shared__ uint32_t cidx[kPartMaxLeaders];
-    __shared__ uint32_t crel[kPartMaxLeaders];
-    __shared__ uint32_t run[kPartMaxLeaders];
-    __shared__ uint32_t wcnt[4][kPartMaxLeaders];
-    __shared__ uint32_t wpre[4][kPartMaxLeaders];
-    const uint32_t item = blockIdx.x;
-    if (item >= a.hdr->items) return;
-    if (a.counters[TESSA_P_OVERFLOW_FLAGS] != 0ull) return;
-    const uint32_t tid = threadIdx.x;
-    if (tid == 0) s_node = find_item_node(a.nodes[cur], level_nodes, item);
-    __syncthreads();
-    const uint32_t ni = s_node;
+// One item per wave.  The item's rows go to their children in row order, in
+// rounds of 64 rows.  Inside a round a row's rank among the rows bound for
+// the same child comes from a bit-sliced match: per fanout entry, one ballot
+// per bit of the 7-bit slot number, so lanes holding the same slot are found
+// with a fixed number of ballots however many slots the round touches.  The
+// wave keeps each slot's child index, child row offset and running position
+// (from the item's prefix) in its own 1.5 KB of LDS.  The node's first item
+// publishes its children.
+constexpr uint32_t kScatterWaveWords = 3 * kPartMaxLeaders;  // per-wave LDS: child idx, child rel, running position
+
+__device__ __forceinline__ void scatter_item_wave(const PartArgs &a, uint32_t cur, uint32_t item, uint32_t ni,
+                                                  uint32_t *wl) {
+    const uint32_t lane = threadIdx.x & 63u;
     const NodeDesc *nd = a.nodes[cur] + ni;
     const uint32_t status = nd->status;
-    if (status != kNodeAccepted && status != kNodeBalanced) return;
+    if (!node_split(status)) return;
     const uint64_t cbase = (uint64_t)ni * kPartMaxLeaders;
     const uint32_t nl = nd->num_leaders;
     const uint32_t fanout = nd->fanout;
     const uint32_t n = nd->n;
     const uint32_t first = (item - nd->item_base) * kPartItemRows;
     const uint32_t rows_here = (n - first) < kPartItemRows ? (n - first) : kPartItemRows;
-    const uint32_t *src = a.arena[cur] + nd->row_start;
+    const uint64_t row_start = nd->row_start;
+    const uint32_t *src = a.arena[cur] + row_start;
     uint32_t *next_arena = a.arena[cur ^ 1u];
-    if (tid < kPartMaxLeaders) {
-        cidx[tid] = a.child_idx[cbase + tid];
-        crel[tid] = a.child_rel[cbase + tid];
-        run[tid] = (status == kNodeAccepted && tid < nl) ? a.item_counts[(uint64_t)item * kPartMaxLeaders + tid] : 0u;
-    }
-    __syncthreads();
+    const uint64_t node_row_base = nd->node_row_base, leaf_row_base = nd->leaf_row_base;
+    const bool counted = status == kNodeAccepted;
+    uint32_t *w_idx = wl, *w_rel = wl + kPartMaxLeaders, *w_run = wl + 2 * kPartMaxLeaders;
+    // the lane's two slots
+    const uint32_t ci0 = a.child_idx[cbase + lane], ci1 = a.child_idx[cbase + lane + 64u];
+    const uint32_t cr0 = a.child_rel[cbase + lane], cr1 = a.child_rel[cbase + lane + 64u];
+    const uint32_t run0 = (counted && lane < nl) ? a.item_counts[(uint64_t)item * kPartMaxLeaders + lane] : 0u;
+    const uint32_t run1 =
+        (counted && lane + 64u < nl) ? a.item_counts[(uint64_t)item * kPartMaxLeaders + lane + 64u] : 0u;
+    wave_lds_sync();  // the previous item's reads of wl are done
+    w_idx[lane] = ci0;
+    w_idx[lane + 64u] = ci1;
+    w_rel[lane] = cr0;
+    w_rel[lane + 64u] = cr1;
+    w_run[lane] = run0;
+    w_run[lane + 64u] = run1;
+    wave_lds_sync();
     auto put = [&](uint32_t s, uint64_t pos, uint32_t row) {
-        const uint32_t ci = cidx[s];
+        const uint32_t ci = w_idx[s];
         if (ci == kChildEmpty) return;
-        if (ci & kChildNodeBit) next_arena[nd->node_row_base + crel[s] + pos] = row;
-        else a.leaf_row_ids[nd->leaf_row_base + crel[s] + pos] = row;
+        if (ci & kChildNodeBit) next_arena[node_row_base + w_rel[s] + pos] = row;
+        else a.leaf_row_ids[leaf_row_base + w_rel[s] + pos] = row;
     };
-    if (status == kNodeBalanced) {
-        // even rows -> child 0, odd rows -> child 1, in row order
-        for (uint32_t r = first + tid; r < first + rows_here; r += blockDim.x) put(r & 1u, r >> 1, src[r]);
+    if (!counted) {
+        // balanced: even rows -> child 0, odd rows -> child 1, in row order
+        for (uint32_t r = first + lane; r < first + rows_here; r += 64u) put(r & 1u, r >> 1, src[r]);
     } else {
-        const uint32_t wave = tid >> 6, lane = tid & 63u;
         const uint64_t lt = (1ull << lane) - 1ull;
-        for (uint32_t round = 0; round < kPartItemRows / 256u; ++round) {
-            const uint32_t r = first + round * 256u + tid;
-            const bool valid = r < first + rows_here;
-            const uint32_t packed = valid ? a.slots[nd->row_start + r] : 0xffffffffu;
+        // every round's slot word and row requested before the first round
+        constexpr uint32_t kRounds = kPartItemRows / 64u;
+        uint32_t pk[kRounds], rw[kRounds];
+#pragma unroll
+        for (uint32_t q = 0; q < kRounds; ++q) {
+            const uint32_t r = first + q * 64u + lane;
+            const bool valid = q * 64u + lane < rows_here;
+            pk[q] = valid ? a.slots[row_start + r] : 0xffffffffu;
+            rw[q] = valid ? src[r] : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kRounds; ++q) {
+            if (q * 64u >= rows_here) break;
+            const bool valid = q * 64u + lane < rows_here;
             uint32_t my[4];
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) my[k] = (valid && k < fanout) ? ((packed >> (8u * k)) & 0xffu) : 0xffu;
-            for (uint32_t s = lane; s < kPartMaxLeaders; s += 64u) wcnt[wave][s] = 0u;
-            __syncthreads();
-            // Stable rank within the wave: one pass per distinct slot value.
-            uint32_t rank[4] = {0u, 0u, 0u, 0u};
-            uint64_t pend[4];
+            for (uint32_t k = 0; k < 4; ++k) my[k] = (valid && k < fanout) ? ((pk[q] >> (8u * k)) & 0xffu) : 0xffu;
+            // bit planes of every fanout entry's slot number (a lane's slots
+            // are distinct leaders, so a lane matches a slot at most once)
+            uint64_t live[4], plane[4][7];
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) pend[k] = __ballot(my[k] != 0xffu);
-            while (true) {
-                uint32_t k0 = 4u;
-                uint64_t m0 = 0ull;
+            for (uint32_t k = 0; k < 4; ++k) {
+                live[k] = __ballot(my[k] != 0xffu);
 #pragma unroll
-                for (uint32_t k = 0; k < 4; ++k)
-                    if (k0 == 4u && pend[k] != 0ull) {
-                        k0 = k;
-                        m0 = pend[k];
-                    }
-                if (k0 == 4u) break;
-                const int lane0 = __ffsll((long long)m0) - 1;
-                uint32_t v = my[0];
+                for (uint32_t b = 0; b < 7u; ++b) plane[k][b] = __ballot((my[k] >> b) & 1u);
+            }
+            uint32_t pos[4], grow[4];
+            bool lead[4];
 #pragma unroll
-                for (uint32_t k = 1; k < 4; ++k)
-                    if (k == k0) v = my[k];
-                const uint32_t s0 = __shfl(v, lane0);
-                uint64_t any = 0ull;
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t v = my[k] == 0xffu ? 0u : my[k];
+                uint64_t same = 0ull;  // lanes holding slot v in any entry
 #pragma unroll
-                for (uint32_t k = 0; k < 4; ++k) {
-                    const uint64_t mk = __ballot(my[k] == s0);
-                    any |= mk;
-                    pend[k] &= ~mk;
+                for (uint32_t k2 = 0; k2 < 4; ++k2) {
+                    uint64_t m = live[k2];
+#pragma unroll
+                    for (uint32_t b = 0; b < 7u; ++b) m &= ((v >> b) & 1u) ? plane[k2][b] : ~plane[k2][b];
+                    same |= m;
                 }
-                const uint32_t before = (uint32_t)__popcll(any & lt);
-#pragma unroll
-                for (uint32_t k = 0; k < 4; ++k)
-                    if (my[k] == s0) rank[k] = before;
-                if ((int)lane == lane0) wcnt[wave][s0] = (uint32_t)__popcll(any);
+                const uint64_t below = same & lt;
+                const uint32_t base = my[k] != 0xffu ? w_run[v] : 0u;
+                pos[k] = base + (uint32_t)__popcll(below);
+                lead[k] = my[k] != 0xffu && below == 0ull;  // the slot's first lane advances its position
+                grow[k] = base + (uint32_t)__popcll(same);
             }
-            __syncthreads();
-            if (tid < kPartMaxLeaders) {
-                uint32_t acc = run[tid];
+            wave_lds_sync();  // every lane has read its bases
 #pragma unroll
-                for (uint32_t w = 0; w < 4; ++w) {
-                    wpre[w][tid] = acc;
-                    acc += wcnt[w][tid];
-                }
-                run[tid] = acc;
-            }
-            __syncthreads();
-            if (valid) {
-                const uint32_t row = src[r];
+            for (uint32_t k = 0; k < 4; ++k)
+                if (lead[k]) w_run[my[k]] = grow[k];
 #pragma unroll
-                for (uint32_t k = 0; k < 4; ++k)
-                    if (my[k] != 0xffu) put(my[k], (uint64_t)wpre[wave][my[k]] + rank[k], row);
-            }
-            __syncthreads();
+            for (uint32_t k = 0; k < 4; ++k)
+                if (my[k] != 0xffu) put(my[k], pos[k], rw[q]);
+            wave_lds_sync();  // the advanced positions are seen by the next round
         }
     }
     // The node's first item publishes its children (push_leaf / publish child).
-    if (item == nd->item_base && tid < nl) {
-        const uint32_t s = tid;
-        const uint32_t ci = cidx[s];
-        if (ci != kChildEmpty) {
-            const uint32_t c = a.child_counts[cbase + s];
-            if (ci & kChildNodeBit) {
-                NodeDesc child{};
-                child.row_start = nd->node_row_base + crel[s];
-                child.n = c;
-                child.depth = nd->depth + 1u;
-                child.seed = nd->seed ^ ((uint64_t)s * 0x94d049bb133111ebull) ^ (((uint64_t)c) << 23);
-                child.root_base = nd->root_base;
-                child.root_index = nd->root_index;
-                child.status = kNodeIdle;
-                a.nodes[cur ^ 1u][nd->node_base + (ci & ~kChildNodeBit)] = child;
-            } else {
-                const uint64_t li = nd->leaf_base + ci;
-                const uint64_t start = nd->leaf_row_base + crel[s];
-                a.leaf_starts[li] = start;
-                a.leaf_sizes[li] = c;
-                a.leaf_sizes32[li] = c;
-                a.leaf_out_offsets[li] = start * a.k;
-                if (a.leaf_root) a.leaf_root[li] = nd->root_index;
-                if (a.leaf_depth) a.leaf_depth[li] = nd->depth + 1u;
-                pc_min(a.counters, TESSA_P_LEAF_SIZE_MIN, c);
-                pc_max(a.counters, TESSA_P_LEAF_SIZE_MAX, c);
-                pc_add(a.counters, TESSA_P_LEAF_SIZE_SUM, c);
-                pc_add(a.counters, TESSA_P_LEAF_SIZE_COUNT, 1);
+    if (item == nd->item_base) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t sl = lane + 64u * h;
+            const uint32_t ci = h ? ci1 : ci0;
+            const uint32_t cr = h ? cr1 : cr0;
+            if (sl < nl && ci != kChildEmpty) {
+                const uint32_t c = a.child_counts[cbase + sl];
+                if (ci & kChildNodeBit) {
+                    NodeDesc child{};
+                    child.row_start = node_row_base + cr;
+                    child.n = c;
+                    child.depth = nd->depth + 1u;
+                    child.seed = nd->seed ^ ((uint64_t)sl * 0x94d049bb133111ebull) ^ (((uint64_t)c) << 23);
+                    child.root_base = nd->root_base;
+                    child.root_index = nd->root_index;
+                    child.status = kNodeIdle;
+                    a.nodes[cur ^ 1u][nd->node_base + (ci & ~kChildNodeBit)] = child;
+                } else {
+                    const uint64_t li = nd->leaf_base + ci;
+                    const uint64_t start = leaf_row_base + cr;
+                    a.leaf_starts[li] = start;
+                    a.leaf_sizes[li] = c;
+                    a.leaf_sizes32[li] = c;
+                    a.leaf_out_offsets[li] = start * a.k;
+                    if (a.leaf_root) a.leaf_root[li] = nd->root_index;
+                    if (a.leaf_depth) a.leaf_depth[li] = nd->depth + 1u;
+                    pc_min(a.counters, TESSA_P_LEAF_SIZE_MIN, c);
+                    pc_max(a.counters, TESSA_P_LEAF_SIZE_MAX, c);
+                    pc_add(a.counters, TESSA_P_LEAF_SIZE_SUM, c);
+                    pc_add(a.counters, TESSA_P_LEAF_SIZE_COUNT, 1);
+                }
             }
         }
     }
+}
+
+// Level-by-level launches: four items per 256-thread workgroup; the whole
+// scatter is skipped once an overflow is flagged.
+constexpr uint32_t kScatterWavesPerBlock = 4;
+__global__ __launch_bounds__(64 * kScatterWavesPerBlock) void scatter_kernel(PartArgs a, uint32_t cur,
+                                                                             uint32_t level_nodes) {
+    __shared__ uint32_t wl[kScatterWavesPerBlock][kScatterWaveWords];
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t item = blockIdx.x * kScatterWavesPerBlock + wave;
+    if (item >= a.hdr->items || a.counters[TESSA_P_OVERFLOW_FLAGS] != 0ull) return;  // whole waves
+    scatter_item_wave(a, cur, item, a.item_node[item], wl[wave]);
 }
 
 // ---- small root (compute_backend.rs:12648-13078) -----------------------------
@@ -1167,16 +1303,214 @@ __global__ __launch_bounds__(kSmallThreads) void small_root_kernel(PartArgs a) {
     }
 }
 
+// ---- the persistent walk ----------------------------------------------------
+// One cooperative launch runs the whole level loop (the reference's
+// persistent partition loop, compute_backend.rs:16555-17112): every phase of
+// a level (stage, item plan, COUNT / EMIT attempts, node scan, publication
+// scan, scatter) is a grid-stride loop over the level's nodes or items,
+// separated by grid barriers, and every decision the host loop used to read
+// back (retry or not, the next level's size, overflow) is read from the level
+// header by all workgroups after a barrier, so they take the same branch.
+// The schedule, and with it the leaves and counters, is the level-by-level
+// launches' schedule.
+
+// Levels: the terminal-depth retry runs with max_depth up to 1024, so a tree
+// may be that deep.
+constexpr uint32_t kMaxLevels = 1100u;
+
+__device__ __forceinline__ uint32_t load_ctl(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Grid barrier over gridDim.x co-resident workgroups: arrivals count up a
+// monotonic word, so barrier i waits for (i + 1) * gridDim.x arrivals and no
+// reset is needed.  Memory: every wave waits until its global stores are
+// acknowledged by L2 before the workgroup barrier; thread 0 then arrives with
+// an agent-scope release (the L2 written back, so the other XCDs, which have
+// L2s of their own, can see the workgroup's writes), polls with relaxed
+// loads (an acquiring load would invalidate the caches on every poll, under
+// workgroups still at work), and acquires once the count is reached (this
+// CU's L1 and its XCD's L2 invalidated) before the workgroup moves on.
+// A wait longer than watchdog_ticks of the 100 MHz wall clock flags
+// WATCHDOG_STALLED (compute_backend.rs:5883-5929 role) and returns false;
+// every workgroup then leaves the walk.
+constexpr int kWaitStores = 0x0F70;  // s_waitcnt vmcnt(0): the wave's memory operations complete
+
+__device__ __forceinline__ bool grid_barrier(const PartArgs &a, uint32_t target, uint32_t *s_ok,
+                                             uint64_t *wait_ticks = nullptr) {
+    __builtin_amdgcn_s_waitcnt(kWaitStores);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        LevelHeader *h = a.hdr;
+        uint32_t ok = 1u;
+        __hip_atomic_fetch_add(&h->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t t0 = wall_clock64();
+        if (wait_ticks) *wait_ticks -= t0;
+        while (__hip_atomic_load(&h->barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (load_ctl(&h->walk_status) == kWalkStalled) {
+                ok = 0u;
+                break;
+            }
+            if (wall_clock64() - t0 > a.watchdog_ticks) {
+                __hip_atomic_store(&h->walk_status, (uint32_t)kWalkStalled, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                pc_flag(a.counters, TESSA_OVF_WATCHDOG_STALLED);
+                ok = 0u;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        if (wait_ticks) *wait_ticks += wall_clock64();
+        *s_ok = ok;
+    }
+    __syncthreads();
+    return *s_ok != 0u;
+}
+
+template <int KS>
+__global__ __launch_bounds__(CountLayout<KS>::kThreads, 1) void walk_kernel(PartArgs a, uint32_t level_nodes,
+                                                                            uint64_t level_rows) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // CountLayout<KS>, reused per phase
+    __shared__ uint32_t s_node, s_ok;
+    static_assert(CountLayout<KS>::kThreads * 8 <= CountLayout<KS>::kBytes, "scan scratch fits the LDS");
+    static_assert(kScanGroups * kPartMaxLeaders * 4 <= CountLayout<KS>::kBytes, "node scan scratch fits the LDS");
+    static_assert(CountLayout<KS>::kWaves * kScatterWaveWords * 4 <= CountLayout<KS>::kBytes,
+                  "scatter scratch fits the LDS");
+    static_assert(CountLayout<KS>::kThreads % kPartMaxLeaders == 0 &&
+                      CountLayout<KS>::kThreads / kPartMaxLeaders <= kScanGroups,
+                  "node scan groups");
+    LevelHeader *h = a.hdr;
+    const uint32_t G = gridDim.x, b = blockIdx.x, tid = threadIdx.x;
+    // waves as workers for the per-node and per-item phases
+    const uint32_t GW = G * (blockDim.x >> 6), gw = b * (blockDim.x >> 6) + (tid >> 6);
+    uint32_t target = 0u;
+    uint32_t cur = 0u, levels = 0u, passes = 0u, status = kWalkBound;
+    // phase clocks (workgroup 0, thread 0, kept in LDS): spans between
+    // barrier exits; clk[kClkMark] is the last exit, clk[kClkStart] the start
+    enum { kClkCount, kClkEmit, kClkScatter, kClkPublish, kClkWait, kClkMark, kClkStart, kClkN };
+    __shared__ uint64_t clk[kClkN];
+    const bool timer = b == 0u && tid == 0u;
+    if (timer) {
+        for (int i = 0; i < kClkN; ++i) clk[i] = 0ull;
+        clk[kClkStart] = clk[kClkMark] = (uint64_t)wall_clock64();
+    }
+    auto barrier = [&](int phase) -> bool {
+        const bool ok = grid_barrier(a, target += G, &s_ok, timer ? &clk[kClkWait] : nullptr);
+        if (timer) {
+            const uint64_t now = wall_clock64();
+            clk[phase] += now - clk[kClkMark];
+            clk[kClkMark] = now;
+        }
+        return ok;
+    };
+    for (uint32_t level = 0; level < kMaxLevels; ++level) {
+        const uint64_t items_bound = level_rows / kPartItemRows + level_nodes + 1u;
+        if (items_bound > a.item_cap || items_bound > 0x7fffffffull) {
+            status = kWalkCapacity;
+            break;
+        }
+        if (b == 0u && tid < kPartMaxAttempts) h->retry[tid] = 0u;
+        for (uint32_t ni = gw; ni < level_nodes; ni += GW) stage_node_wave(a, cur, level_nodes, ni);
+        if (!barrier(kClkEmit)) return;
+        if (b == 0u) item_plan_block(a, cur, level_nodes, reinterpret_cast<uint64_t *>(smem));
+        if (!barrier(kClkEmit)) return;
+        for (uint32_t ni = gw; ni < level_nodes; ni += GW) item_map_wave(a, cur, ni);
+        if (!barrier(kClkEmit)) return;
+        uint32_t attempt = 0;
+        for (; attempt < kPartMaxAttempts; ++attempt) {
+            count_items<KS>(a, cur, level_nodes, b, G, smem, &s_node);
+            passes += 1u;
+            if (!barrier(kClkCount)) return;
+            for (uint32_t ni = gw; ni < level_nodes; ni += GW) emit_node_wave(a, cur, ni, &h->retry[attempt]);
+            if (!barrier(kClkEmit)) return;
+            if (load_ctl(&h->retry[attempt]) == 0u) break;
+        }
+        if (attempt == kPartMaxAttempts) {
+            status = kWalkBound;
+            break;
+        }
+        // nodes of many items: a workgroup each; the rest: a wave each
+        for (uint32_t ni = b; ni < level_nodes; ni += G)
+            if (a.nodes[cur][ni].items > kWaveScanItems)
+                node_scan_block(a, cur, ni, reinterpret_cast<uint32_t(*)[kPartMaxLeaders]>(smem));
+        for (uint32_t ni = gw; ni < level_nodes; ni += GW)
+            if (a.nodes[cur][ni].items <= kWaveScanItems) node_scan_wave(a, cur, ni);
+        if (!barrier(kClkPublish)) return;
+        if (b == 0u) pub_scan_block(a, cur, level_nodes, reinterpret_cast<uint64_t *>(smem));
+        if (!barrier(kClkPublish)) return;
+        const uint32_t items =
+            __hip_atomic_load(&a.counters[TESSA_P_OVERFLOW_FLAGS], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0ull
+                ? 0u
+                : load_ctl(&h->items);
+        uint32_t *wl = reinterpret_cast<uint32_t *>(smem) + (tid >> 6) * kScatterWaveWords;
+        for (uint32_t item = gw; item < items; item += GW) scatter_item_wave(a, cur, item, a.item_node[item], wl);
+        if (!barrier(kClkScatter)) return;
+        levels = level + 1u;
+        const uint64_t overflow = __hip_atomic_load(&h->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        level_nodes = load_ctl(&h->next_nodes);
+        level_rows = __hip_atomic_load(&h->next_rows, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        cur ^= 1u;
+        if (overflow != 0ull || level_nodes == 0u) {
+            status = kWalkOk;
+            break;
+        }
+    }
+    if (timer) {
+        h->levels = levels;
+        h->count_passes = passes;
+        if (load_ctl(&h->walk_status) != kWalkStalled) h->walk_status = status;
+        a.counters[TESSA_P_PARTITION_BUSY_CLOCKS] = (uint64_t)wall_clock64() - clk[kClkStart];
+        a.counters[TESSA_P_PARTITION_WAIT_CLOCKS] = clk[kClkWait];
+        a.counters[TESSA_P_LARGE_COUNT_DISTANCE_CLOCKS] = clk[kClkCount];
+        a.counters[TESSA_P_LARGE_COUNT_COMMIT_CLOCKS] = clk[kClkEmit];
+        a.counters[TESSA_P_LARGE_SCATTER_CLOCKS] = clk[kClkScatter];
+        a.counters[TESSA_P_LARGE_PUBLISH_CLOCKS] = clk[kClkPublish];
+    }
+}
+
+// Co-resident workgroups of the walk: the occupancy the runtime reports,
+// times the CUs.
+// A failed HIP call of the walk's launch path: records it and returns -1.
+int part_fail(PartResult *res, hipError_t e, const char *step) {
+    res->hip_error = (int)e;
+    res->failed_step = step;
+    return -1;
+}
+
+template <int KS>
+int launch_walk_ks(const PartArgs &a, uint32_t level_nodes, uint64_t level_rows, hipStream_t s, PartResult *res) {
+    using L = CountLayout<KS>;
+    const void *fn = reinterpret_cast<const void *>(walk_kernel<KS>);
+    if (ensure_lds_limit(fn, L::kBytes)) return part_fail(res, hipErrorInvalidValue, "walk LDS limit");
+    int dev = 0, cus = 0, per = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, walk_kernel<KS>, L::kThreads, L::kBytes);
+    if (e != hipSuccess) return part_fail(res, e, "walk occupancy query");
+    if (per < 1 || cus < 1) return part_fail(res, hipErrorInvalidConfiguration, "walk occupancy is zero");
+    PartArgs args = a;
+    void *params[] = {&args, &level_nodes, &level_rows};
+    e = hipLaunchCooperativeKernel(fn, dim3((uint32_t)(cus * per)), dim3(L::kThreads), params, L::kBytes, s);
+    if (e != hipSuccess) return part_fail(res, e, "walk cooperative launch");
+    return 0;
+}
+
+int launch_walk(const PartArgs &a, uint32_t level_nodes, uint64_t level_rows, hipStream_t s, PartResult *res) {
+    const uint32_t ks = (a.padded_dim + 31) / 32;
+    if (ks <= 4) return launch_walk_ks<4>(a, level_nodes, level_rows, s, res);
+    if (ks <= 8) return launch_walk_ks<8>(a, level_nodes, level_rows, s, res);
+    if (ks <= 12) return launch_walk_ks<12>(a, level_nodes, level_rows, s, res);
+    if (ks <= 16) return launch_walk_ks<16>(a, level_nodes, level_rows, s, res);
+    if (ks <= 24) return launch_walk_ks<24>(a, level_nodes, level_rows, s, res);
+    if (ks <= 32) return launch_walk_ks<32>(a, level_nodes, level_rows, s, res);
+    return -3;
+}
+
 template <int KS>
 int launch_count_ks(const PartArgs &a, uint32_t cur, uint32_t level_nodes, uint32_t grid, hipStream_t s) {
     using L = CountLayout<KS>;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)count_kernel<KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                L::kBytes) != hipSuccess)
-            return -1;
-        attr = true;
-    }
+    if (ensure_lds_limit(reinterpret_cast<const void *>(count_kernel<KS>), L::kBytes)) return -1;
     // persistent: at most two workgroups' worth of items per CU at a time
     const uint32_t g = grid < kCountGrid ? grid : kCountGrid;
     hipLaunchKernelGGL(count_kernel<KS>, dim3(g), dim3(L::kThreads), L::kBytes, s, a, cur, level_nodes);
@@ -1250,16 +1584,23 @@ static int capture_level(const PartArgs &a, hipStream_t s, uint32_t cur, uint32_
     return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
 }
 
-// Level bound: the terminal-depth retry runs with max_depth up to 1024, so a
-// tree may be that deep.
-constexpr uint32_t kMaxLevels = 1100u;
 static int run_levels(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
                       uint32_t level_nodes, uint64_t level_rows);
 
-int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture) {
+int run_partition(const PartArgs &args, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture) {
     *res = PartResult{};
+    PartArgs a = args;
+    if (a.watchdog_ticks == 0) {
+        // 10 s of the device's wall clock (its rate in kHz)
+        int dev = 0, khz = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+        if (e != hipSuccess) return part_fail(res, e, "wall clock rate query");
+        if (khz <= 0) khz = 100000;  // the gfx9 wall clock runs at 100 MHz
+        a.watchdog_ticks = (uint64_t)khz * 10000ull;
+    }
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(256), 0, s, a);
-    if (hipGetLastError() != hipSuccess) return -1;
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return part_fail(res, e, "init launch");
     auto read_header = [&]() -> int {
         if (hipMemcpyAsync(hh, a.hdr, sizeof(LevelHeader), hipMemcpyDeviceToHost, s) != hipSuccess) return -1;
         return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
@@ -1280,13 +1621,7 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
     const bool probe = a.fanout_second > 1u && a.rows > 1u;
     const bool probe_overflow = probe && (uint64_t)a.rows * a.fanout_second > (uint64_t)a.small_node_limit;
     if (a.rows <= a.leaf_max && !probe_overflow) {
-        static bool attr = false;
-        if (!attr) {
-            if (hipFuncSetAttribute((const void *)small_root_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)kSmallLdsBytes) != hipSuccess)
-                return -1;
-            attr = true;
-        }
+        if (ensure_lds_limit(reinterpret_cast<const void *>(small_root_kernel), (int)kSmallLdsBytes)) return -1;
         hipLaunchKernelGGL(small_root_kernel, dim3(1), dim3(kSmallThreads), kSmallLdsBytes, s, a);
         if (hipGetLastError() != hipSuccess) return -1;
         res->levels = 1;
@@ -1301,9 +1636,34 @@ int run_partition(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult 
     return run_levels(a, s, hh, res, capture, level_nodes, level_rows);
 }
 
-// The level loop from the nodes of level 0 (in the first arena).
+// The level loop from the nodes of level 0 (in the first arena): the
+// persistent walk, read back once it has finished; with a capture, the
+// level-by-level launches.
+static int run_levels_host(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
+                           uint32_t level_nodes, uint64_t level_rows);
+
 static int run_levels(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
                       uint32_t level_nodes, uint64_t level_rows) {
+    if (capture) return run_levels_host(a, s, hh, res, capture, level_nodes, level_rows);
+    const int rc = launch_walk(a, level_nodes, level_rows, s, res);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(hh, a.hdr, sizeof(LevelHeader), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return part_fail(res, e, "walk header read-back");
+    res->levels = hh->levels;
+    res->count_launches = hh->count_passes;
+    res->leaf_count = hh->leaf_count;
+    res->leaf_rows = hh->leaf_rows;
+    switch (hh->walk_status) {
+        case kWalkOk: return 0;
+        case kWalkCapacity: return -3;
+        case kWalkStalled: return -4;
+        default: return -2;
+    }
+}
+
+static int run_levels_host(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartResult *res, PartCapture *capture,
+                           uint32_t level_nodes, uint64_t level_rows) {
     auto read_header = [&]() -> int {
         if (hipMemcpyAsync(hh, a.hdr, sizeof(LevelHeader), hipMemcpyDeviceToHost, s) != hipSuccess) return -1;
         return hipStreamSynchronize(s) == hipSuccess ? 0 : -1;
@@ -1313,25 +1673,27 @@ static int run_levels(const PartArgs &a, hipStream_t s, LevelHeader *hh, PartRes
         const uint64_t items_bound = level_rows / kPartItemRows + level_nodes + 1u;
         if (items_bound > a.item_cap || items_bound > 0x7fffffffull) return -3;
         const uint32_t grid = (uint32_t)items_bound;
-        hipLaunchKernelGGL(stage_kernel, dim3(level_nodes), dim3(128), 0, s, a, cur, level_nodes);
+        hipLaunchKernelGGL(stage_kernel, dim3(level_nodes), dim3(64), 0, s, a, cur, level_nodes);
         hipLaunchKernelGGL(item_plan_kernel, dim3(1), dim3(1024), 0, s, a, cur, level_nodes);
+        hipLaunchKernelGGL(item_map_kernel, dim3(level_nodes), dim3(64), 0, s, a, cur, level_nodes);
         if (hipGetLastError() != hipSuccess) return -1;
         uint32_t attempt = 0;
-        for (; attempt < 16u; ++attempt) {
+        for (; attempt < kPartMaxAttempts; ++attempt) {
             if (capture && capture_level(a, s, cur, level_nodes, capture)) return -1;
             if (launch_count(a, cur, level_nodes, grid, s)) return -1;
             res->count_launches += 1;
-            hipLaunchKernelGGL(emit_kernel, dim3(level_nodes), dim3(128), 0, s, a, cur, level_nodes);
+            hipLaunchKernelGGL(emit_kernel, dim3(level_nodes), dim3(64), 0, s, a, cur, level_nodes);
             if (hipGetLastError() != hipSuccess) return -1;
             if (read_header()) return -1;
             if (hh->retry_nodes == 0u) break;
             hipLaunchKernelGGL(reset_retry_kernel, dim3(1), dim3(1), 0, s, a.hdr);
         }
-        if (attempt == 16u) return -2;
+        if (attempt == kPartMaxAttempts) return -2;
         hipLaunchKernelGGL(node_scan_kernel, dim3(level_nodes), dim3(kScanGroups * kPartMaxLeaders), 0, s, a, cur,
                            level_nodes);
         hipLaunchKernelGGL(pub_scan_kernel, dim3(1), dim3(1024), 0, s, a, cur, level_nodes);
-        hipLaunchKernelGGL(scatter_kernel, dim3(grid), dim3(256), 0, s, a, cur, level_nodes);
+        hipLaunchKernelGGL(scatter_kernel, dim3((grid + kScatterWavesPerBlock - 1) / kScatterWavesPerBlock),
+                           dim3(64 * kScatterWavesPerBlock), 0, s, a, cur, level_nodes);
         if (hipGetLastError() != hipSuccess) return -1;
         if (read_header()) return -1;
         res->levels = level + 1u;

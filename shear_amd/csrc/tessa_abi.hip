@@ -191,6 +191,21 @@ tessa_status get_workspace(uint64_t rows, DeviceWorkspace **out, uint64_t list_i
     return ok_status();
 }
 
+// The status of a failed run_partition call.
+tessa_status partition_failure(int rc, const tessa::PartResult &pr) {
+    if (rc == -1 && pr.failed_step)
+        return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code -1: %s: %s)", pr.failed_step,
+                           hipGetErrorName((hipError_t)pr.hip_error));
+    if (rc == -4)
+        return make_status(TESSA_ERR_HIP, TESSA_OVF_WATCHDOG_STALLED,
+                           "CUDA persistent subtree overflow: partition walk stalled overflow_flags=0x%llx "
+                           "overflow_labels=WATCHDOG_STALLED",
+                           (unsigned long long)TESSA_OVF_WATCHDOG_STALLED);
+    return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
+                       rc == -2 ? "level/attempt bound exceeded"
+                                : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+}
+
 tessa_status device_workspace(DeviceWorkspace **out) {
     int dev = 0;
     TESSA_HIP_TRY(hipGetDevice(&dev));
@@ -1039,7 +1054,7 @@ struct PartLayout {
     uint64_t arena_cap = 0, item_cap = 0, leaf_cap = 0;
     uint32_t node_cap = 0;
     size_t off_arena[2] = {0, 0}, off_nodes[2] = {0, 0}, off_leaders = 0, off_ccount = 0, off_cidx = 0,
-           off_crel = 0, off_slots = 0, off_items = 0, off_sizes32 = 0, off_outoff = 0, bytes = 0;
+           off_crel = 0, off_slots = 0, off_items = 0, off_item_node = 0, off_sizes32 = 0, off_outoff = 0, bytes = 0;
 };
 
 PartLayout part_layout(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_t leaf_cap) {
@@ -1063,6 +1078,7 @@ PartLayout part_layout(uint64_t rows, uint32_t famp, uint32_t leaf_max, uint64_t
     L.off_crel = take(nc * kPartMaxLeaders * 4);
     L.off_slots = take(L.arena_cap * 4);
     L.off_items = take(L.item_cap * kPartMaxLeaders * 4);
+    L.off_item_node = take(L.item_cap * 4);
     L.off_sizes32 = take(L.leaf_cap * 4);
     L.off_outoff = take(L.leaf_cap * 8);
     L.bytes = o + kLeaderStride * 4;  // root leaders
@@ -1084,7 +1100,7 @@ tessa_status subtree_overflow(const tessa_session *s, const uint64_t *c, float m
                        "CUDA persistent subtree overflow: resident_rows=%llu overflow_flags=0x%llx "
                        "overflow_labels=%s leaf_rows=%llu leaf_count=%llu partition_pops=%llu "
                        "assignment_passes=%llu max_active_points=%llu persistent_kernel_event_ms=%.3f "
-                       "partition_level_rounds=%llu (HIP gfx950 level-synchronous partition)",
+                       "partition_level_rounds=%llu (HIP gfx950 persistent partition walk)",
                        (unsigned long long)s->rows, (unsigned long long)f, labels,
                        (unsigned long long)c[TESSA_P_OUTPUT_ROWS], (unsigned long long)c[TESSA_P_OUTPUT_LEAF_COUNT],
                        (unsigned long long)c[TESSA_P_PARTITION_POPS],
@@ -1261,6 +1277,7 @@ static tessa_status tessa_session_run_subtree_locked(tessa_session *s, const tes
     a.child_rel = reinterpret_cast<uint32_t *>(base + L.off_crel);
     a.slots = reinterpret_cast<uint32_t *>(base + L.off_slots);
     a.item_counts = reinterpret_cast<uint32_t *>(base + L.off_items);
+    a.item_node = reinterpret_cast<uint32_t *>(base + L.off_item_node);
     a.arena_cap = L.arena_cap;
     a.item_cap = L.item_cap;
     a.node_cap = L.node_cap;
@@ -1273,9 +1290,7 @@ static tessa_status tessa_session_run_subtree_locked(tessa_session *s, const tes
     const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr,
                                  s->capture_min_members ? &s->capture : nullptr);
     if (rc != 0)
-        return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
-                           rc == -2 ? "level/attempt bound exceeded"
-                                    : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+        return partition_failure(rc, pr);
     if (s->capture_min_members && !s->capture.rows.empty()) {
         // Resident rows -> global ids now, while the resident set is the one
         // this run used (a later upload may replace it before the fetch).
@@ -1472,6 +1487,7 @@ static tessa_status tessa_session_partition_roots_locked(tessa_session *s, const
     a.child_rel = reinterpret_cast<uint32_t *>(base + L.off_crel);
     a.slots = reinterpret_cast<uint32_t *>(base + L.off_slots);
     a.item_counts = reinterpret_cast<uint32_t *>(base + L.off_items);
+    a.item_node = reinterpret_cast<uint32_t *>(base + L.off_item_node);
     a.arena_cap = L.arena_cap;
     a.item_cap = L.item_cap;
     a.node_cap = L.node_cap;
@@ -1480,9 +1496,7 @@ static tessa_status tessa_session_partition_roots_locked(tessa_session *s, const
     PartResult pr{};
     const int rc = run_partition(a, s->stream, s->part_hdr_host, &pr, nullptr);
     if (rc != 0)
-        return make_status(TESSA_ERR_HIP, 0, "subtree partition failed (code %d: %s)", rc,
-                           rc == -2 ? "level/attempt bound exceeded"
-                                    : rc == -3 ? "workspace capacity exceeded" : "HIP launch failure");
+        return partition_failure(rc, pr);
     uint64_t c[TESSA_SUBTREE_COUNTER_WORDS];
     TESSA_HIP_TRY(hipMemcpyAsync(c, s->part_counters, sizeof(c), hipMemcpyDeviceToHost, s->stream));
     TESSA_HIP_TRY(hipStreamSynchronize(s->stream));

@@ -14,8 +14,9 @@ from shear_amd import subtree as S
 
 pytestmark = pytest.mark.gpu
 
-# counter words the oracle does not produce (leaf MFMA tiles come from the top-k)
-SKIP_WORDS = {N.P_LEAF_SQ8_WMMA_TILES}
+# the leaf operator's tile count and the walk's phase clocks (timings) have no
+# oracle counterpart
+SKIP_WORDS = {N.P_LEAF_SQ8_WMMA_TILES, *N.P_CLOCK_WORDS}
 
 
 @pytest.fixture(scope="module")
@@ -183,3 +184,39 @@ def test_subtree_rejects_bad_root_leaders(gpu, orc):
     with pytest.raises(N.TessaError) as ei:
         sess.run(S.GpuSubtreePartitionRequest(point_ids=gids, root_leader_ids=np.array([3, 500])), params)
     assert "exceeds resident rows" in ei.value.message
+
+
+def test_walk_equals_level_by_level_launches(gpu, orc):
+    """The persistent walk (one cooperative launch for the whole level loop)
+    and the level-by-level launches the capture path uses build the same
+    leaves, top-k and counters (the walk's phase clocks aside), on a tree
+    with retries, several levels and a balanced fallback-prone leader count."""
+    codes, scales, norms, gids = _data(orc, 30000, 64, 12, 41)
+    sess = S.SubtreeSession(0)
+    sess.upload(codes, scales, norms, gids, 64)
+    params = S.PiPNNSubtreeParams(leaf_knn=16, c_max=256, psamp_fraction=0.0005, max_leaders=128, max_depth=64,
+                                  fanout_second=2, random_seed=3)
+    req = S.GpuSubtreePartitionRequest(point_ids=gids, parent_points=90000, min_recurse_size=64)
+    walk = sess.run(req, params)
+    sess.set_assignment_capture(256)  # capture runs the partition level by level
+    host = sess.run(req, params)
+    sess.set_assignment_capture(0)
+    torch.cuda.synchronize()
+    assert walk.leaf_count == host.leaf_count and walk.leaf_rows == host.leaf_rows and walk.levels == host.levels
+    lr, lc = walk.leaf_rows, walk.leaf_count
+    assert torch.equal(walk.leaf_row_ids[:lr], host.leaf_row_ids[:lr])
+    assert torch.equal(walk.leaf_starts[:lc], host.leaf_starts[:lc])
+    assert torch.equal(walk.leaf_sizes[:lc], host.leaf_sizes[:lc])
+    n = walk.leaf_rows * walk.k
+    assert torch.equal(walk.topk_ids[:n], host.topk_ids[:n]) and torch.equal(walk.topk_dists[:n], host.topk_dists[:n])
+    for w in range(N.SUBTREE_COUNTER_WORDS):
+        if w not in N.P_CLOCK_WORDS:
+            assert walk.counters[w] == host.counters[w], f"counter word {w}"
+    assert walk.counters[N.P_LARGE_SPLIT_RETRIES] > 0 and walk.levels > 3
+    # phase clocks: set by the walk, each phase inside the whole
+    busy = int(walk.counters[N.P_PARTITION_BUSY_CLOCKS])
+    assert busy > 0 and all(int(host.counters[w]) == 0 for w in N.P_CLOCK_WORDS)
+    parts = [int(walk.counters[w]) for w in (N.P_LARGE_COUNT_DISTANCE_CLOCKS, N.P_LARGE_COUNT_COMMIT_CLOCKS,
+                                              N.P_LARGE_SCATTER_CLOCKS, N.P_LARGE_PUBLISH_CLOCKS)]
+    assert all(p > 0 for p in parts) and sum(parts) <= busy
+    sess.close()
