@@ -168,8 +168,12 @@ tessa_status tessa_leaf_topk(const tessa_sq8_view *sq8, const tessa_leaf_batch *
  * Same arguments, results and errors as tessa_leaf_topk; all scratch (queue
  * counters, re-run and chain queues, survivor logs, work-item list) lives
  * in one static device array of about 39 MB per GPU, held until the process ends, so a
- * call may cover at most 65,536 member rows (leaf_count * max_leaf_rows);
- * larger batches are rejected with TESSA_ERR_UNSUPPORTED.  Every call on a
+ * call of the MFMA executor may cover at most 65,536 member rows
+ * (leaf_count * max_leaf_rows); larger batches are rejected with
+ * TESSA_ERR_UNSUPPORTED.  The exact executor uses no scratch and takes any
+ * batch.  Once a first call on a device has returned, calls may be captured
+ * into a HIP graph (the first call looks up the array's address and sets
+ * the kernels' LDS limits; later calls only launch kernels).  Every call on a
  * GPU shares that GPU's array: calls that overlap on one GPU (other
  * streams, other host threads) race and must be serialised by the caller. */
 tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf_batch *leaves,

@@ -591,6 +591,9 @@ tessa_status tessa_leaf_topk_noalloc(const tessa_sq8_view *sq8, const tessa_leaf
                                      float *out_dists, uint64_t *counters, void *stream) {
     if (!lb) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "leaf batch has a null pointer");
     const uint64_t rows = (uint64_t)lb->leaf_count * lb->max_leaf_rows;
+    // the exact executor uses no scratch: any batch size
+    if (lb->executor == TESSA_EXEC_EXACT)
+        return leaf_topk_impl(sq8, lb, rows, out_ids, out_dists, counters, stream, nullptr);
     if (rows > kNoAllocMaxRows)
         return make_status(TESSA_ERR_UNSUPPORTED, 0,
                            "leaf batch of %u leaves x %u rows exceeds the no-allocation limit of %llu member rows",

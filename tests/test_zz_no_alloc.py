@@ -73,3 +73,54 @@ def test_noalloc_rejects_batches_beyond_its_scratch(gpu, orc):
     lay.max_leaf_rows = MAX_ROWS  # 2 leaves x 65,536 rows bound: over the limit
     with pytest.raises(RuntimeError, match="no-allocation limit"):
         T.leaf_topk(sq8, dev_u32(np.arange(2048)), lay, 8, executor=N.EXEC_MFMA, no_alloc=True)
+
+
+def test_noalloc_call_captured_in_a_graph(gpu, orc):
+    """A warmed-up call captured into a HIP graph (torch.cuda.graph), replayed
+    three times with eager work and synchronisation between the replays:
+    every replay equals the eager call bit for bit."""
+    sizes = [1024, 700, 1, 300, 1024]
+    n = int(np.sum(sizes))
+    x = datagen.gmm_numpy(n, 768, 5, 0.3, 34)
+    c, s, nn = orc.quantize(x)
+    sq8 = to_dev_sq8(c, s, nn, 768)
+    gids = dev_u32(np.random.default_rng(34).permutation(1 << 24)[:n].astype(np.uint32))
+    members, offs, z = _leaves(sizes)
+    lay = T.LeafLayouts.from_host(members, offs, z, 32)
+    want_ids, want_d, _ = T.leaf_topk(sq8, gids, lay, 32, executor=N.EXEC_MFMA, no_alloc=True)  # warm-up
+    torch.cuda.synchronize()
+    want_ids, want_d = want_ids.clone(), want_d.clone()
+    out_ids = torch.empty_like(want_ids)
+    out_d = torch.empty_like(want_d)
+    ctr = torch.zeros(N.COUNTER_WORDS, dtype=torch.int64, device=gpu)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctr.zero_()
+        T.leaf_topk(sq8, gids, lay, 32, executor=N.EXEC_MFMA, out_ids=out_ids, out_dists=out_d, counters=ctr,
+                    no_alloc=True)
+    for rep in range(3):
+        out_ids.fill_(-1)
+        out_d.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        T.raise_on_overflow(ctr, "captured leaf top-k")
+        assert int(ctr[N.C_LEAF_ROWS]) == n, rep
+        assert_same(out_ids.cpu().numpy().view(np.uint32), out_d.cpu().numpy(),
+                    want_ids.cpu().numpy().view(np.uint32), want_d.cpu().numpy(), f"graph replay {rep}")
+
+
+def test_noalloc_exact_executor_takes_any_batch(gpu, orc):
+    """The exact executor needs no scratch: a batch above the MFMA limit runs
+    and matches the oracle."""
+    x = datagen.gmm_numpy(2048, 32, 4, 0.3, 35)
+    c, s, nn = orc.quantize(x)
+    sq8 = to_dev_sq8(c, s, nn, 32)
+    members, offs, sizes = _leaves([1024, 1024])
+    lay = T.LeafLayouts.from_host(members, offs, sizes, 8)
+    lay.max_leaf_rows = MAX_ROWS  # leaf_count * max_leaf_rows above the MFMA limit
+    gids = np.arange(2048, dtype=np.uint32)
+    ids, d, ctr = T.leaf_topk(sq8, dev_u32(gids), lay, 8, executor=N.EXEC_EXACT, no_alloc=True)
+    torch.cuda.synchronize()
+    want_ids, want_d = orc.leaf_topk(c, s, nn, gids, members, offs, sizes, 8)
+    assert_same(ids.cpu().numpy().view(np.uint32), d.cpu().numpy(), want_ids, want_d, "exact no-alloc")
