@@ -311,24 +311,37 @@ def build_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(64, 256)):
     x = spec.rows(dev)
     dim = x.shape[1]
     p = P.GraphBuildParams(c_max=2048)
-    sk = (x @ torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev).t()).contiguous()
+    planes_t = torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev).t().contiguous()
     lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
-    sq8 = T.quantize_sq_int8_matrix(x)
+
+    def payload():
+        # the build's inputs from the resident f32 rows: sketches and SQ8
+        return T.quantize_sq_int8_matrix(x), (x @ planes_t).contiguous()
+
+    sq8, sk = payload()
     torch.cuda.synchronize()
     sampler = _LeafSampler() if check else None
     first = P.build_graph_sq8(sq8, sk, lead, p, observer=sampler)
     first_s, first_image = first.build_s, first.image
-    del first
+    del first, sq8, sk
     torch.cuda.empty_cache()
-    built = P.build_graph_sq8(sq8, sk, lead, p)
+    # the timed build starts from the f32 rows: sketching and SQ8
+    # quantization are inside it
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    sq8, sk = payload()
+    torch.cuda.synchronize()
+    prep_s = time.perf_counter() - w0
+    built = P.build_graph_sq8(sq8, sk, lead, p, t0=w0)
     same = bool(torch.equal(first_image, built.image))
     del first_image
-    log(f"C3 build: {built.build_s:.3f} s ({rows / built.build_s:,.0f} points/s; first build {first_s:.3f} s), "
-        f"images identical {same}")
+    log(f"C3 build: {built.build_s:.3f} s ({rows / built.build_s:,.0f} points/s, sketch + SQ8 {prep_s * 1e3:.1f} ms "
+        f"included; first build {first_s:.3f} s from SQ8), images identical {same}")
     res = {
         "workload": f"C3: {rows} x {dim} unit vectors (1,000 components, sigma 0.25, 5% outliers, seed 2), SQ8, "
                     f"D0 {len(lead)} leaders fanout 2, many-root subtrees fanout 2, leaves <= 2048, k 32, R 64",
         "build_s": round(built.build_s, 4),
+        "sketch_and_sq8_ms": round(prep_s * 1e3, 2),  # inside build_s
         "first_build_s": round(first_s, 4),
         "points_per_s": round(rows / built.build_s, 1),
         "repeat_image_identical": same,
@@ -564,8 +577,11 @@ def recall_leg(dev, check=True, search_l=(32, 64, 128, 256), k_recall=10, search
 def subtree_leg(rows, dev, check=True, runs=2):
     """C3-shaped resident subtree: rows x 768 unit vectors (1000-component
     mixture, sigma 0.25, 5 % uniform outliers, random order, seed 2), one
-    tessa_session_run_subtree: level-synchronous partition (leaves <= 2048,
-    root fanout 2, max depth 16) then the leaf top-k (k = 32) on every leaf."""
+    tessa_session_run_subtree: the persistent partition walk (leaves <= 2048,
+    root fanout 2, max depth 16) then the leaf top-k (k = 32) on every leaf.
+    The walk's phase clocks (counter words 120, 121, 140-143: ticks of the
+    100 MHz wall clock, workgroup 0's spans between grid barriers) are
+    reported in ms."""
     import torch
 
     from shear_amd import _native as N
@@ -624,6 +640,10 @@ def subtree_leg(rows, dev, check=True, runs=2):
         "assignment_passes": int(c[N.P_ASSIGNMENT_PASSES]),
         "split_retries": int(c[N.P_LARGE_SPLIT_RETRIES]),
         "partition_ms": round(pm, 3),
+        "partition_phase_ms": {name: round(float(c[w]) / 1e5, 3) for name, w in (
+            ("walk", N.P_PARTITION_BUSY_CLOCKS), ("count", N.P_LARGE_COUNT_DISTANCE_CLOCKS),
+            ("stage_plan_emit", N.P_LARGE_COUNT_COMMIT_CLOCKS), ("scatter", N.P_LARGE_SCATTER_CLOCKS),
+            ("layout_and_numbering", N.P_LARGE_PUBLISH_CLOCKS), ("barrier_wait", N.P_PARTITION_WAIT_CLOCKS))},
         "partition_counted_rows": counted_rows,
         "partition_gb_per_s": round(assign_bytes / (pm / 1e3) / 1e9, 1),  # rows*(padded_dim+8) per COUNT pass
         "leaf_ms": round(lm, 3),
