@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--subtree-rows", type=int, default=10_000_000,
                     help="rows of the in-HBM subtree leg (C3: 10M x 768, leaves <= 2048, fanout 2, k=32)")
     ap.add_argument("--no-subtree", action="store_true", help="skip the subtree (partition + leaf top-k) leg")
+    ap.add_argument("--subtree-only", action="store_true",
+                    help="run only the subtree leg and print its JSON (for profiling the partition walk)")
     ap.add_argument("--no-build", action="store_true", help="skip the C3 full-build leg")
     ap.add_argument("--build-rows", type=int, default=10_000_000,
                     help="rows of the C3 full-build leg (BASELINE configs[2]: 10,000,000)")
@@ -96,6 +98,9 @@ def main() -> int:
     N.load()
     if args.c5_rows:
         print(json.dumps(c5_leg(dev, args.c5_rows)), flush=True)
+        return 0
+    if args.subtree_only:
+        print(json.dumps(subtree_leg(args.subtree_rows, dev, check=False, runs=3)), flush=True)
         return 0
     leaves = args.leaves
     rows = leaves * LEAF_ROWS
