@@ -85,6 +85,9 @@ def lib():
                                                            C.c_size_t, C.c_uint, P, C.c_size_t, P]
         _lib.orc_hashprune_reduce.restype = C.c_int
         _lib.orc_hashprune_reduce.argtypes = [C.c_size_t, C.c_size_t, P, C.c_size_t, P, P, P, P, P]
+        _lib.orc_hashprune_rhalf_reduce.restype = C.c_int
+        _lib.orc_hashprune_rhalf_reduce.argtypes = [C.c_size_t, C.c_size_t, P, C.c_size_t, C.c_int, C.c_uint,
+                                                    C.c_uint, C.c_float, P, P, P, P, P, P]
         _lib.orc_d0_assign.restype = C.c_int
         _lib.orc_d0_assign.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, P, P, P, P, C.c_size_t, C.c_size_t, P, P,
                                        P, P]
@@ -405,6 +408,32 @@ def hashprune_reduce(num_points: int, l_max: int, records: np.ndarray):
     if rc != 0:
         raise ValueError(f"orc_hashprune_reduce: {rc} (record {bad.value})")
     return t, hs, d, cnt
+
+
+RHALF_MODES = {"rhalf-hash-slot-1": 1, "rhalf-distance-first-q3": 2, "rhalf-soft-tier-q3": 3,
+               "rhalf-hard-tier-q3": 4}
+
+
+def hashprune_rhalf_reduce(num_points: int, l_max: int, records: np.ndarray, mode: str = "rhalf-soft-tier-q3",
+                           hash_quota: int = 0, row_cap: int = 0, priority_alpha: float = 0.0):
+    """HashPrune with a named R-half backfill policy (hash_prune_backfill.rs,
+    hash_prune.rs:2601-2682): (targets [num_points, l_max] u32, hashes u16,
+    dists f32, counts [num_points] u32 (primaries + shortlist), primary counts);
+    each row's primaries in ascending hash order, then its shortlist in
+    priority order.  row_cap 0 = none; priority_alpha 0 = 1.1."""
+    rec = np.ascontiguousarray(records, EDGE_DTYPE)
+    t = np.zeros((num_points, l_max), np.uint32)
+    hs = np.zeros((num_points, l_max), np.uint16)
+    d = np.zeros((num_points, l_max), np.float32)
+    cnt = np.zeros(num_points, np.uint32)
+    pcnt = np.zeros(num_points, np.uint32)
+    bad = C.c_uint32(0)
+    rc = lib().orc_hashprune_rhalf_reduce(num_points, l_max, _p(rec), len(rec), RHALF_MODES[mode], hash_quota,
+                                          row_cap, priority_alpha, _p(t), _p(hs), _p(d), _p(cnt), _p(pcnt),
+                                          C.byref(bad))
+    if rc != 0:
+        raise ValueError(f"orc_hashprune_rhalf_reduce: {rc} (record {bad.value})")
+    return t, hs, d, cnt, pcnt
 
 
 def graph_bytes(start: int, num_frozen: int, rows) -> bytes:

@@ -292,6 +292,26 @@ int orc_hashprune_reduce(size_t num_points, size_t l_max, const orc_edge_record 
                          uint32_t *out_targets, uint16_t *out_hashes, float *out_dists, uint32_t *out_counts,
                          uint32_t *bad_record);
 
+/* HashPrune with a named R-half backfill policy (hash_prune_backfill.rs,
+ * hash_prune.rs:2601-2682): the ordinary reservoirs of `records` (as
+ * orc_hashprune_reduce), then for each point with some but fewer than l_max
+ * primaries a shortlist of its primary hashes' other candidates (quota per
+ * hash, hit layers by rank) in the mode's priority order, cut to
+ * min(row_cap, floor(l_max / 2), l_max - primaries), appended after the
+ * primaries.  mode: ORC_RHALF_*; hash_quota 0 = the mode's (1 or 3);
+ * row_cap 0 = none; priority_alpha <= 0 = 1.1 (SoftTier only).
+ * out_counts = primaries + shortlist, out_primary_counts = primaries.
+ * Returns 0, -1 on bad arguments, -2 on allocation failure, -3 as
+ * orc_hashprune_reduce. */
+#define ORC_RHALF_HASH_SLOT_1 1
+#define ORC_RHALF_DISTANCE_FIRST_Q3 2
+#define ORC_RHALF_SOFT_TIER_Q3 3
+#define ORC_RHALF_HARD_TIER_Q3 4
+int orc_hashprune_rhalf_reduce(size_t num_points, size_t l_max, const orc_edge_record *records, size_t count,
+                               int mode, unsigned hash_quota, unsigned row_cap, float priority_alpha,
+                               uint32_t *out_targets, uint16_t *out_hashes, float *out_dists, uint32_t *out_counts,
+                               uint32_t *out_primary_counts, uint32_t *bad_record);
+
 /* Greedy search of a [num_points x row_stride] neighbour table (row p =
  * targets[p*row_stride .. + counts[p]]) over f32 vectors, search list L,
  * from `start` (algorithm/search/search.rs:137-233 with the capacity-L

@@ -107,20 +107,25 @@ def brute_knn(chunks, queries: torch.Tensor, k: int, exclude=None) -> torch.Tens
     q = queries.double()
     qn = (q * q).sum(1, keepdim=True)
     best_d = best_i = None
-    for r0, xc in chunks:
-        xd = xc.double()
-        dd = qn - 2.0 * (q @ xd.t()) + (xd * xd).sum(1)[None, :]
-        if exclude is not None:
-            rel = exclude - r0
-            hit = (rel >= 0) & (rel < xc.shape[0])
-            dd[hit.nonzero().squeeze(1), rel[hit]] = float("inf")
-        kk = min(k, xc.shape[0])
-        d, i = torch.topk(dd, kk, dim=1, largest=False)
-        i = i + r0
-        if best_d is not None:
-            d, j = torch.topk(torch.cat([best_d, d], 1), k, dim=1, largest=False)
-            i = torch.gather(torch.cat([best_i, i], 1), 1, j)
-        best_d, best_i = d, i
+    sub = 1 << 18  # rows per distance block (bounds the f64 temporaries)
+    for c0, xchunk in chunks:
+        for s0 in range(0, xchunk.shape[0], sub):
+            xc = xchunk[s0:s0 + sub]
+            r0 = c0 + s0
+            xd = xc.double()
+            dd = qn - 2.0 * (q @ xd.t()) + (xd * xd).sum(1)[None, :]
+            if exclude is not None:
+                rel = exclude - r0
+                hit = (rel >= 0) & (rel < xc.shape[0])
+                dd[hit.nonzero().squeeze(1), rel[hit]] = float("inf")
+            kk = min(k, xc.shape[0])
+            d, i = torch.topk(dd, kk, dim=1, largest=False)
+            i = i + r0
+            if best_d is not None:
+                d, j = torch.topk(torch.cat([best_d, d], 1), min(k, best_d.shape[1] + kk), dim=1, largest=False)
+                i = torch.gather(torch.cat([best_i, i], 1), 1, j)
+            best_d, best_i = d, i
+            del xd, dd
     return best_i
 
 
