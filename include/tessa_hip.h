@@ -612,6 +612,39 @@ tessa_status tessa_hashprune_insert_segments(tessa_hashprune *hp, const tessa_ed
                                              const tessa_edge_segment *segments, uint64_t segment_count,
                                              void *stream);
 
+/* create with a named R-half backfill policy (PiPNNParams
+ * hashprune_backfill_mode rhalf-hash-slot-1 / rhalf-distance-first-q3 /
+ * rhalf-soft-tier-q3 / rhalf-hard-tier-q3 with hashprune_rhalf_hash_quota,
+ * hashprune_rhalf_max_backfill_per_row and
+ * hashprune_soft_tier_priority_alpha: shear-core/src/algorithm/pipnn/
+ * params.rs:2070-2083, validated as :2696-2729; the build_shear_index
+ * binary's default is SoftTier-Q3, alpha 1.02, 3 per row,
+ * apps/build_shear_index/src/main.rs:2360-2374).  A row that ends with some
+ * but fewer than l_max primaries takes up to min(row cap, floor(l_max / 2),
+ * l_max - primaries) backups from each primary hash's next `quota` distinct
+ * targets, ranked by the mode's priority (hash_prune.rs:655-685,
+ * hash_prune_backfill.rs:299-386) and emitted after the primaries
+ * (hash_prune.rs:1458-1555); the result is the reference's
+ * order-independent characterization hash_prune.rs:2601-2682, so batches
+ * still merge in any order.  Zero fields take the reference's defaults
+ * (quota 1 for hash-slot-1, else 3; cap floor(l_max / 2); alpha 1.1).
+ * Extra device memory: num_points * l_max * 24 bytes.  insert,
+ * insert_segments, clear and destroy are as above; neighbors writes
+ * primaries then backups and counts them both. */
+#define TESSA_HP_BACKFILL_OFF 0u
+#define TESSA_HP_BACKFILL_RHALF_HASH_SLOT_1 1u
+#define TESSA_HP_BACKFILL_RHALF_DISTANCE_FIRST_Q3 2u
+#define TESSA_HP_BACKFILL_RHALF_SOFT_TIER_Q3 3u
+#define TESSA_HP_BACKFILL_RHALF_HARD_TIER_Q3 4u
+typedef struct tessa_hashprune_backfill {
+    uint32_t mode;                    /* TESSA_HP_BACKFILL_* */
+    uint32_t hash_quota;              /* 0 or 1..3 */
+    uint32_t max_backfill_per_row;    /* 0 or 1..floor(l_max / 2) */
+    float soft_tier_priority_alpha;   /* 0, or finite >= 1.0 (SoftTier only) */
+} tessa_hashprune_backfill;
+tessa_status tessa_hashprune_create_backfill(uint32_t num_points, uint32_t l_max,
+                                             const tessa_hashprune_backfill *policy, tessa_hashprune **out);
+
 /* ---- TierLift: the bounded host reducer of the record stream ---------------
  * Replaces SpillEdgeSink + ExternalHashPruneReducer
  * (shear-core/src/algorithm/pipnn/spill_hashprune.rs:349-651 routing, shard

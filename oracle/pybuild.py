@@ -12,6 +12,7 @@ Stage by stage it chains the oracle's restatements of the reference path
   compact batches           compute_backend.rs:32243-32339   (restated below)
   record -> edge            leaf_build.rs:1679-1829          orc_flush_compact_topk_into_edges
   HashPrune reservoirs      hash_prune.rs:1243-1283          orc_hashprune_reduce
+  (named R-half backfill)   hash_prune.rs:2601-2682          orc_hashprune_rhalf_reduce
   final RobustPrune (opt.)  pipnn_builder.rs:287-330         orc_robust_prune
   `_mem.index` image        pipnn_oom_writer.rs:23-72        graph_bytes
   entry point               rbc_partition.rs:4964-4985       (restated below)
@@ -106,7 +107,14 @@ def build_graph_cpu(x: np.ndarray, sketches: np.ndarray, leader_rows: np.ndarray
         leaf_rows_n += int(sizes.sum())
     records = np.concatenate(parts) if parts else np.zeros(0, orc.EDGE_DTYPE)
     w2 = time.perf_counter()
-    t, _, _, cnt = orc.hashprune_reduce(rows, p.l_max, records)
+    bf = getattr(p, "hashprune_backfill", None)
+    if bf is not None and bf.mode != "off":
+        t, _, _, cnt, _ = orc.hashprune_rhalf_reduce(rows, p.l_max, records, mode=bf.mode,
+                                                     hash_quota=bf.hash_quota or 0,
+                                                     row_cap=bf.max_backfill_per_row or 0,
+                                                     priority_alpha=bf.soft_tier_priority_alpha or 0.0)
+    else:
+        t, _, _, cnt = orc.hashprune_reduce(rows, p.l_max, records)
     if getattr(p, "final_prune", False):
         t, cnt = orc.robust_prune(x, t, cnt, p.l_max, p.prune_max_occlusion, p.prune_alpha, p.prune_saturate)
     nbr = [t[i, : cnt[i]] for i in range(rows)]

@@ -106,6 +106,11 @@ class TessaConfig(C.Structure):
     _fields_ = [("device", C.c_int32), ("reserved", C.c_uint32)]
 
 
+class HashPruneBackfill(C.Structure):
+    _fields_ = [("mode", C.c_uint32), ("hash_quota", C.c_uint32), ("max_backfill_per_row", C.c_uint32),
+                ("soft_tier_priority_alpha", C.c_float)]
+
+
 # Subtree counters at the reference's indices (enum tessa_subtree_counter).
 SUBTREE_COUNTER_WORDS = 159
 P_OVERFLOW_FLAGS = 7
@@ -354,6 +359,7 @@ SIGNATURES = {
         [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, C.POINTER(_U64), _P],
     ),
     "tessa_hashprune_create": (TessaStatus, [_U32, _U32, C.POINTER(_P)]),
+    "tessa_hashprune_create_backfill": (TessaStatus, [_U32, _U32, C.POINTER(HashPruneBackfill), C.POINTER(_P)]),
     "tessa_hashprune_destroy": (TessaStatus, [_P]),
     "tessa_hashprune_insert": (TessaStatus, [_P, _P, _U64, _P]),
     "tessa_hashprune_neighbors": (TessaStatus, [_P, _P, _P, _P, _P, _P]),

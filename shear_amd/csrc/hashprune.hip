@@ -727,11 +727,12 @@ __device__ __forceinline__ void load_source(SourceLoad<ER> &L, uint32_t src, uin
     }
 }
 
-// Merges the records of a group of up to 64 segments (lane s: segment s, cnt
-// records from first) 64 at a time across segment boundaries.
-template <int ER>
-__device__ __forceinline__ void merge_group(Reservoir<ER> &r, const uint4 *records, uint32_t ng, uint32_t cnt,
-                                            uint64_t first, uint32_t l_max, uint32_t lane) {
+// Streams the records of a group of up to 64 segments (lane s: segment s, cnt
+// records from first) 64 at a time across segment boundaries into
+// chunk(key, hash, valid).
+template <typename Chunk>
+__device__ __forceinline__ void stream_group(const uint4 *records, uint32_t ng, uint32_t cnt, uint64_t first,
+                                             uint32_t lane, Chunk &&chunk) {
     uint32_t total;
     const uint32_t pre = wave_excl_scan(cnt, lane, total);
     uint32_t sg = 0;  // first segment not yet wholly read
@@ -754,8 +755,15 @@ __device__ __forceinline__ void merge_group(Reservoir<ER> &r, const uint4 *recor
             ck = ((uint64_t)total_key(__uint_as_float(rec.w)) << 32) | rec.y;
             ch = rec.z & 0xffffu;
         }
-        res_chunk(r, ck, ch, v, l_max, lane);
+        chunk(ck, ch, v);
     }
+}
+
+template <int ER>
+__device__ __forceinline__ void merge_group(Reservoir<ER> &r, const uint4 *records, uint32_t ng, uint32_t cnt,
+                                            uint64_t first, uint32_t l_max, uint32_t lane) {
+    stream_group(records, ng, cnt, first, lane,
+                 [&](uint64_t ck, uint32_t ch, bool v) { res_chunk(r, ck, ch, v, l_max, lane); });
 }
 
 // Active sources in ascending source order (run-length encoding of the sorted
@@ -906,6 +914,365 @@ __global__ __launch_bounds__(kHpThreads) void hp_export_kernel(const uint64_t *s
     }
 }
 
+// ---- named R-half backfill ----------------------------------------------------
+// The reference's order-independent characterization of its R-half streaming
+// reservoir (shear-core/src/algorithm/pipnn/hash_prune.rs:2601-2682
+// reference_tiered_rhalf_slots; ranking :655-685, capacities
+// hash_prune_backfill.rs:299-336, SoftTier score :375-386): a row with some
+// but fewer than l_max primaries is completed with up to `capacity` backups,
+// chosen by the mode's priority among each primary hash's next `quota`
+// distinct targets (each at its best key, the primary's own target
+// excluded; a member's hit layer is its rank in its group).
+//
+// Each slot keeps its hash's best quota + 1 distinct targets: the slot key and
+// a group of quota keys.  That set does not depend on the order of the
+// candidates (a target dropped from it had quota + 1 better distinct targets
+// of the hash, whose keys only improve), so batches still merge in any
+// order.  A reservoir that has filled never frees a slot and a full row takes
+// no backups, so groups are kept only while a slot is free: once the
+// reservoir fills, the plain insert takes over and its groups are neither
+// read nor written again.
+
+template <int ER>
+struct GroupReservoir {
+    Reservoir<ER> b;
+    uint64_t g[ER][kRhalfGroup];  // the lane's slot's group, ascending keys, ~0 = none
+};
+
+__device__ __forceinline__ uint64_t shfl_up64(uint64_t v) {
+    const uint32_t lo = __shfl_up((uint32_t)v, 1);
+    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), 1);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// res_shift_in with each slot's group moving with it; position p takes
+// (bk, bh, bg).
+template <int ER>
+__device__ __forceinline__ void gres_shift_in(GroupReservoir<ER> &r, uint32_t p, uint32_t end, uint64_t bk,
+                                              uint32_t bh, const uint64_t (&bg)[kRhalfGroup], uint32_t lane) {
+#pragma unroll
+    for (int q = ER - 1; q >= 0; --q) {
+        if ((uint32_t)q * 64u > end || (uint32_t)q * 64u + 63u < p) continue;  // register untouched
+        const int qb = q > 0 ? q - 1 : 0;  // lane 0 takes the register below's lane 63 (q > 0)
+        uint64_t uk = shfl_up64(r.b.k[q]);
+        uint32_t uh = __shfl_up(r.b.h[q], 1);
+        uint64_t ug[kRhalfGroup];
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) ug[j] = shfl_up64(r.g[q][j]);
+        if (q > 0) {
+            const uint64_t ck = readlane64(r.b.k[qb], 63);
+            const uint32_t ch = readlane32(r.b.h[qb], 63);
+            uk = lane == 0 ? ck : uk;
+            uh = lane == 0 ? ch : uh;
+#pragma unroll
+            for (uint32_t j = 0; j < kRhalfGroup; ++j) {
+                const uint64_t cg = readlane64(r.g[qb][j], 63);
+                ug[j] = lane == 0 ? cg : ug[j];
+            }
+        }
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        const bool mv = e > p && e <= end;
+        r.b.k[q] = e == p ? bk : (mv ? uk : r.b.k[q]);
+        r.b.h[q] = e == p ? bh : (mv ? uh : r.b.h[q]);
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = e == p ? bg[j] : (mv ? ug[j] : r.g[q][j]);
+    }
+}
+
+// Inserts candidate (bk, bh) into a reservoir with a free slot.  A new hash
+// takes a free slot with an empty group; a hit updates the hash's best
+// quota + 1 distinct targets (the owner lane's copy is the slot's) and, when
+// the candidate becomes the hash's best, moves the slot as res_insert does,
+// the old slot key now heading its group.
+template <int ER>
+__device__ __forceinline__ void gres_insert(GroupReservoir<ER> &r, uint64_t bk, uint32_t bh, uint32_t quota,
+                                            uint32_t lane) {
+    uint32_t p = 0;
+    uint32_t hit = 0xffffffffu;
+#pragma unroll
+    for (int q = 0; q < ER; ++q) {
+        const bool live = (uint32_t)q * 64u + lane < r.b.c;
+        p += (uint32_t)__popcll(ballot64(live && ent_less(r.b.k[q], r.b.h[q], bk, bh)));
+        const uint64_t m = ballot64(live && r.b.h[q] == bh);
+        hit = m ? (uint32_t)q * 64u + (uint32_t)__builtin_ctzll(m) : hit;
+    }
+    if (hit == 0xffffffffu) {
+        const uint64_t none[kRhalfGroup] = {~0ull, ~0ull, ~0ull};
+        gres_shift_in(r, p, r.b.c, bk, bh, none, lane);
+        r.b.c = r.b.c + 1u;
+        return;
+    }
+    const uint32_t hq = hit >> 6, hl = hit & 63u;
+    uint64_t s[kRhalfGroup + 1];
+    s[0] = r.b.k[0];
+#pragma unroll
+    for (uint32_t j = 0; j < kRhalfGroup; ++j) s[j + 1] = r.g[0][j];
+#pragma unroll
+    for (int q = 1; q < ER; ++q) {
+        if (hq != (uint32_t)q) continue;
+        s[0] = r.b.k[q];
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) s[j + 1] = r.g[q][j];
+    }
+    const uint64_t ek = readlane64(s[0], hl);
+    // the candidate's target keeps its better key; a new target takes
+    // position quota when better than what is there (~0 when unfilled)
+    const uint32_t bt = (uint32_t)bk;
+    bool present = false;
+#pragma unroll
+    for (uint32_t j = 0; j <= kRhalfGroup; ++j) {
+        const bool m = j <= quota && s[j] != ~0ull && (uint32_t)s[j] == bt;
+        present = present || m;
+        s[j] = m && bk < s[j] ? bk : s[j];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j <= kRhalfGroup; ++j) s[j] = !present && j == quota && bk < s[j] ? bk : s[j];
+    // one key decreased: a backward pass restores the ascending order
+#pragma unroll
+    for (int j = kRhalfGroup; j >= 1; --j) {
+        const uint64_t lo = s[j] < s[j - 1] ? s[j] : s[j - 1];
+        const uint64_t hi = s[j] < s[j - 1] ? s[j - 1] : s[j];
+        s[j - 1] = lo;
+        s[j] = hi;
+    }
+    if (bk < ek) {
+        // the candidate heads its hash now: the slot moves to position p
+        uint64_t bg[kRhalfGroup];
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) bg[j] = readlane64(s[j + 1], hl);
+        gres_shift_in(r, p, hit, bk, bh, bg, lane);
+    } else {
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            if (hq != (uint32_t)q || lane != hl) continue;
+#pragma unroll
+            for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = s[j + 1];
+        }
+    }
+}
+
+template <int ER>
+__device__ void gres_chunk(GroupReservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t quota,
+                           uint32_t lane) {
+    if (r.b.c == l_max) {
+        res_chunk(r.b, ck, ch, v, l_max, lane);
+        return;
+    }
+    uint64_t pm = ballot64(v);
+    while (pm) {
+        const uint32_t j = (uint32_t)__builtin_ctzll(pm);
+        pm &= pm - 1ull;
+        const uint64_t bk = readlane64(ck, j);
+        const uint32_t bh = readlane32(ch, j);
+        if (r.b.c < l_max)
+            gres_insert(r, bk, bh, quota, lane);
+        else
+            res_insert(r.b, bk, bh, l_max, lane);
+    }
+}
+
+// One wave per source with new records: its slots (and, while a slot is free,
+// their groups) in registers, its records streamed through them.  Sources
+// come from segment runs (as hp_merge_stream_kernel) or, kGrouped, from the
+// record batch grouped by source (offsets[src] .. offsets[src + 1]).
+template <int ER, bool kGrouped>
+__global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
+    const uint4 *records, const uint4 *sorted, const uint32_t *run_src, const uint32_t *run_start,
+    const uint32_t *run_len, const uint32_t *num_runs, const uint32_t *offsets, uint32_t num_points, uint32_t l_max,
+    uint32_t quota, uint64_t *slot_keys, uint16_t *slot_hash, uint32_t *slot_count, uint64_t *grp_keys) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t waves = gridDim.x * kHpWaves;
+    const uint32_t na = kGrouped ? num_points : *num_runs;
+    for (uint32_t a = blockIdx.x * kHpWaves + (threadIdx.x >> 6); a < na; a += waves) {
+        uint32_t src, start = 0, len = 1, cnt = 0;
+        uint64_t first = 0;
+        if (kGrouped) {
+            src = a;
+            const uint32_t o0 = offsets[a], o1 = offsets[a + 1];
+            if (o1 == o0) continue;
+            cnt = lane == 0 ? o1 - o0 : 0u;
+            first = o0;
+        } else {
+            src = run_src[a];
+            if (src >= num_points) continue;  // the run of empty / bad segments
+            start = run_start[a];
+            len = run_len[a];
+            if (lane < len) {
+                const uint4 g = sorted[(uint64_t)start + lane];
+                cnt = g.w;
+                first = ((uint64_t)g.z << 32) | g.y;
+            }
+        }
+        GroupReservoir<ER> r;
+        const uint64_t sbase = (uint64_t)src * l_max;
+        r.b.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)slot_count[src]);
+        const bool groups = r.b.c < l_max;
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            const bool live = e < r.b.c;
+            r.b.k[q] = live ? slot_keys[sbase + e] : ~0ull;
+            r.b.h[q] = live ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
+#pragma unroll
+            for (uint32_t j = 0; j < kRhalfGroup; ++j)
+                r.g[q][j] = live && groups ? grp_keys[(sbase + e) * kRhalfGroup + j] : ~0ull;
+        }
+        auto chunk = [&](uint64_t ck, uint32_t ch, bool v) { gres_chunk(r, ck, ch, v, l_max, quota, lane); };
+        stream_group(records, len < 64u ? len : 64u, cnt, first, lane, chunk);
+        for (uint32_t g0 = 64; g0 < len; g0 += 64) {
+            const uint32_t ng = len - g0 < 64u ? len - g0 : 64u;
+            uint32_t c2 = 0;
+            uint64_t f2 = 0;
+            if (lane < ng) {
+                const uint4 g = sorted[(uint64_t)start + g0 + lane];
+                c2 = g.w;
+                f2 = ((uint64_t)g.z << 32) | g.y;
+            }
+            stream_group(records, ng, c2, f2, lane, chunk);
+        }
+        const bool keep_groups = r.b.c < l_max;
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            if (e < r.b.c) {
+                slot_keys[sbase + e] = r.b.k[q];
+                slot_hash[sbase + e] = (uint16_t)r.b.h[q];
+                if (keep_groups) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kRhalfGroup; ++j) grp_keys[(sbase + e) * kRhalfGroup + j] = r.g[q][j];
+                }
+            }
+        }
+        if (lane == 0) slot_count[src] = r.b.c;
+    }
+}
+
+__device__ __forceinline__ uint64_t total_key64(double d) {
+    const uint64_t b = (uint64_t)__double_as_longlong(d);
+    return (b & 0x8000000000000000ull) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// A group member's rank under the mode's priority (hash_prune.rs:655-685) as
+// a 128-bit key (hi, lo); members are distinct (hash, target) pairs, so keys
+// are distinct.  SoftTier: (score, layer, target, hash), the score the f64
+// distance times alpha^2 per layer past the first (hash_prune_backfill.rs:
+// 375-386); HardTier: (layer, distance, target, hash); the others:
+// (distance, layer, target, hash).
+__device__ __forceinline__ void member_rank(uint32_t mode, double alpha_sq, uint64_t key, uint32_t hash,
+                                            uint32_t layer, uint64_t &hi, uint64_t &lo) {
+    const uint32_t dk = (uint32_t)(key >> 32);
+    const uint64_t th = ((uint64_t)(uint32_t)key << 16) | hash;
+    if (mode == kRhalfSoftTierQ3) {
+        double s = (double)key_dist(dk);
+        if (layer >= 2) s = s * alpha_sq;
+        if (layer >= 3) s = s * alpha_sq;
+        hi = total_key64(s);
+        lo = ((uint64_t)layer << 48) | th;
+    } else if (mode == kRhalfHardTierQ3) {
+        hi = ((uint64_t)layer << 32) | dk;
+        lo = th;
+    } else {
+        hi = dk;
+        lo = ((uint64_t)layer << 48) | th;
+    }
+}
+
+// hp_export_kernel followed, for a row with some but fewer than l_max
+// primaries, by min(capacity, l_max - c) backups: the best group members by
+// the mode's priority, one wave-wide arg-min per backup, written after the
+// primaries in priority order.
+template <int ER>
+__global__ __launch_bounds__(kHpThreads) void hp_export_rhalf_kernel(
+    const uint64_t *slot_keys, const uint16_t *slot_hash, const uint32_t *slot_count, const uint64_t *grp_keys,
+    uint32_t num_points, uint32_t l_max, uint32_t mode, uint32_t quota, uint32_t capacity, double alpha_sq,
+    uint32_t *targets, uint16_t *hashes, float *dists, uint32_t *counts) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t waves = gridDim.x * kHpWaves;
+    for (uint32_t p = blockIdx.x * kHpWaves + (threadIdx.x >> 6); p < num_points; p += waves) {
+        const uint32_t c = slot_count[p];
+        const uint64_t base = (uint64_t)p * l_max;
+        uint32_t h[ER];
+        uint64_t k[ER];
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            h[q] = e < c ? (uint32_t)slot_hash[base + e] : 0xffffffffu;
+            k[q] = e < c ? slot_keys[base + e] : ~0ull;
+        }
+        uint32_t take = 0;
+        if (c > 0 && c < l_max) {
+            const uint32_t cap = capacity < l_max - c ? capacity : l_max - c;
+            uint64_t mh[ER][kRhalfGroup], ml[ER][kRhalfGroup];
+#pragma unroll
+            for (int q = 0; q < ER; ++q) {
+                const uint32_t e = (uint32_t)q * 64u + lane;
+#pragma unroll
+                for (uint32_t j = 0; j < kRhalfGroup; ++j) {
+                    const uint64_t g = e < c && j < quota ? grp_keys[(base + e) * kRhalfGroup + j] : ~0ull;
+                    mh[q][j] = ~0ull;
+                    ml[q][j] = ~0ull;
+                    if (g != ~0ull) member_rank(mode, alpha_sq, g, h[q], j + 1u, mh[q][j], ml[q][j]);
+                }
+            }
+            for (; take < cap; ++take) {
+                uint64_t bh = ~0ull, bl = ~0ull;
+                uint32_t bi = 0;
+#pragma unroll
+                for (int q = 0; q < ER; ++q) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kRhalfGroup; ++j) {
+                        const bool lt = mh[q][j] < bh || (mh[q][j] == bh && ml[q][j] < bl);
+                        bh = lt ? mh[q][j] : bh;
+                        bl = lt ? ml[q][j] : bl;
+                        bi = lt ? (uint32_t)q * kRhalfGroup + j : bi;
+                    }
+                }
+                uint64_t wh = bh, wl = bl;
+#pragma unroll
+                for (int m = 1; m < 64; m <<= 1) {
+                    const uint64_t oh = shfl_xor64(wh, m), ol = shfl_xor64(wl, m);
+                    const bool lt = oh < wh || (oh == wh && ol < wl);
+                    wh = lt ? oh : wh;
+                    wl = lt ? ol : wl;
+                }
+                if (wl == ~0ull) break;  // no member left (valid ranks never have lo = ~0)
+                if (bh == wh && bl == wl) {
+                    const uint64_t o = base + c + take;
+#pragma unroll
+                    for (int q = 0; q < ER; ++q) {
+#pragma unroll
+                        for (uint32_t j = 0; j < kRhalfGroup; ++j) {
+                            if (bi != (uint32_t)q * kRhalfGroup + j) continue;
+                            const uint64_t g = grp_keys[(base + (uint32_t)q * 64u + lane) * kRhalfGroup + j];
+                            if (targets) targets[o] = (uint32_t)g;
+                            if (hashes) hashes[o] = (uint16_t)h[q];
+                            if (dists) dists[o] = key_dist((uint32_t)(g >> 32));
+                            mh[q][j] = ~0ull;
+                            ml[q][j] = ~0ull;
+                        }
+                    }
+                }
+            }
+        }
+        reg_bitonic<ER, true>(h, k, lane);
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            const uint32_t e = (uint32_t)q * 64u + lane;
+            if (e >= l_max || (e >= c && e < c + take)) continue;  // the backups' positions
+            const bool live = e < c;
+            if (targets) targets[base + e] = live ? (uint32_t)k[q] : 0xffffffffu;
+            if (hashes) hashes[base + e] = live ? (uint16_t)h[q] : (uint16_t)0;
+            if (dists) dists[base + e] = live ? key_dist((uint32_t)(k[q] >> 32)) : 0.0f;
+        }
+        if (counts && lane == 0) counts[p] = c + take;
+    }
+}
+
 uint32_t grid_for(uint64_t n, uint32_t threads, uint32_t cap) {
     const uint64_t g = (n + threads - 1) / threads;
     return (uint32_t)(g < 1 ? 1 : (g > cap ? cap : g));
@@ -935,6 +1302,22 @@ int launch_hashprune_insert(HashPruneState &s, const uint4 *records, uint64_t co
     hipLaunchKernelGGL(hp_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, s.bucket, n, s.block_sums, s.offsets);
     hipLaunchKernelGGL(hp_scatter_kernel, dim3(grid_for(count, 256, 16384)), dim3(256), 0, stream, records, count, n,
                        s.bucket, s.offsets, s.grouped);
+    if (s.rhalf_mode) {
+        const uint32_t grid = grid_for(n, kHpWaves, 8192);
+        if (s.l_max <= 64)
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<1, true>), dim3(grid), dim3(kHpThreads), 0, stream, s.grouped,
+                               nullptr, nullptr, nullptr, nullptr, nullptr, s.offsets, n, s.l_max, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        else if (s.l_max <= 128)
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<2, true>), dim3(grid), dim3(kHpThreads), 0, stream, s.grouped,
+                               nullptr, nullptr, nullptr, nullptr, nullptr, s.offsets, n, s.l_max, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        else
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<4, true>), dim3(grid), dim3(kHpThreads), 0, stream, s.grouped,
+                               nullptr, nullptr, nullptr, nullptr, nullptr, s.offsets, n, s.l_max, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     // Both kernels decide from slots + new records; a merge never shrinks a
     // reservoir, so after the large kernel every source it merged still counts
     // more than kHpRegMax and the small kernel skips it (the reverse order
@@ -976,6 +1359,21 @@ int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, co
                        w.vals_out, nseg, w.sorted);
     const uint32_t grid = grid_for(nseg, kHpWaves, 8192);
     const uint32_t l = s.l_max;
+    if (s.rhalf_mode) {
+        if (l <= 64)
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<1, false>), dim3(grid), dim3(kHpThreads), 0, stream, records,
+                               w.sorted, w.run_src, w.run_start, w.run_len, w.num_runs, nullptr, n, l, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        else if (l <= 128)
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<2, false>), dim3(grid), dim3(kHpThreads), 0, stream, records,
+                               w.sorted, w.run_src, w.run_start, w.run_len, w.num_runs, nullptr, n, l, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        else
+            hipLaunchKernelGGL((hp_merge_rhalf_kernel<4, false>), dim3(grid), dim3(kHpThreads), 0, stream, records,
+                               w.sorted, w.run_src, w.run_start, w.run_len, w.num_runs, nullptr, n, l, s.rhalf_quota,
+                               s.slot_keys, s.slot_hash, s.slot_count, s.grp_keys);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (l <= 64)
         hipLaunchKernelGGL(hp_merge_stream_kernel<1>, dim3(grid), dim3(kHpThreads), 0, stream, records, w.sorted,
                            w.run_src, w.run_start, w.run_len, w.num_runs, n, l, s.slot_keys, s.slot_hash,
@@ -996,6 +1394,21 @@ int launch_hashprune_export(const HashPruneState &s, uint32_t *targets, uint16_t
     const uint32_t n = s.num_points;
     if (n == 0 || s.l_max == 0) return 0;
     const uint32_t grid = grid_for(n, kHpWaves, 8192);
+    if (s.rhalf_mode) {
+        if (s.l_max <= 64)
+            hipLaunchKernelGGL(hp_export_rhalf_kernel<1>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys,
+                               s.slot_hash, s.slot_count, s.grp_keys, n, s.l_max, s.rhalf_mode, s.rhalf_quota,
+                               s.rhalf_capacity, s.rhalf_alpha_sq, targets, hashes, dists, counts);
+        else if (s.l_max <= 128)
+            hipLaunchKernelGGL(hp_export_rhalf_kernel<2>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys,
+                               s.slot_hash, s.slot_count, s.grp_keys, n, s.l_max, s.rhalf_mode, s.rhalf_quota,
+                               s.rhalf_capacity, s.rhalf_alpha_sq, targets, hashes, dists, counts);
+        else
+            hipLaunchKernelGGL(hp_export_rhalf_kernel<4>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys,
+                               s.slot_hash, s.slot_count, s.grp_keys, n, s.l_max, s.rhalf_mode, s.rhalf_quota,
+                               s.rhalf_capacity, s.rhalf_alpha_sq, targets, hashes, dists, counts);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (s.l_max <= 64)
         hipLaunchKernelGGL(hp_export_kernel<1>, dim3(grid), dim3(kHpThreads), 0, stream, s.slot_keys, s.slot_hash,
                            s.slot_count, n, s.l_max, targets, hashes, dists, counts);

@@ -27,7 +27,22 @@ struct HashPruneState {
     uint64_t *status = nullptr;     // [0] first record with src >= num_points (UINT64_MAX: none)
     void *seg_ws = nullptr;          // segment mode workspace (hashprune_segment_workspace_bytes)
     uint64_t seg_ws_bytes = 0;
+    // Named R-half backfill (rhalf_mode != 0): per slot the next rhalf_quota
+    // distinct targets of its hash, ascending keys (~0: none), kept while the
+    // reservoir has a free slot; the export appends up to rhalf_capacity of
+    // them to an underfull row by the mode's priority.
+    uint32_t rhalf_mode = 0;         // kRhalf*
+    uint32_t rhalf_quota = 0;        // 1..3
+    uint32_t rhalf_capacity = 0;     // min(row cap, l_max / 2)
+    double rhalf_alpha_sq = 1.0;     // SoftTier priority alpha squared
+    uint64_t *grp_keys = nullptr;    // num_points x l_max x kRhalfGroup
 };
+
+constexpr uint32_t kRhalfHashSlot1 = 1;
+constexpr uint32_t kRhalfDistanceFirstQ3 = 2;
+constexpr uint32_t kRhalfSoftTierQ3 = 3;
+constexpr uint32_t kRhalfHardTierQ3 = 4;
+constexpr uint32_t kRhalfGroup = 3;  // group keys stored per slot (the largest quota)
 
 // Groups `count` records by source and merges each source's new candidates
 // into its reservoir.  Returns 0, or -1 when a launch failed.
@@ -40,7 +55,8 @@ int launch_hashprune_insert_segments(HashPruneState &s, const uint4 *records, co
                                      hipStream_t stream);
 // Zeroes the per-source counters (all reservoirs empty).
 int launch_hashprune_clear(HashPruneState &s, hipStream_t stream);
-// Slot targets / hashes / distances (ascending hash) and counts per point.
+// Slot targets / hashes / distances (ascending hash) and counts per point,
+// then, with a backfill policy, the row's backups in priority order.
 int launch_hashprune_export(const HashPruneState &s, uint32_t *targets, uint16_t *hashes, float *dists,
                             uint32_t *counts, hipStream_t stream);
 uint64_t hashprune_scan_blocks(uint32_t num_points);

@@ -7,6 +7,7 @@
 // by substring (rbc_partition.rs:2982-2998).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
@@ -1997,7 +1998,7 @@ void free_hashprune(tessa_hashprune *hp) {
     auto &s = hp->st;
     for (void *ptr : {(void *)s.slot_keys, (void *)s.slot_hash, (void *)s.slot_count, (void *)s.bucket,
                       (void *)s.offsets, (void *)s.block_sums, (void *)s.grouped, (void *)s.status,
-                      (void *)s.seg_ws})
+                      (void *)s.seg_ws, (void *)s.grp_keys})
         if (ptr) (void)hipFree(ptr);
     delete hp;
 }
@@ -2012,24 +2013,64 @@ tessa_status hp_alloc(void **ptr, uint64_t bytes, const char *what) {
     return ok_status();
 }
 
-}  // namespace
+// The named R-half policy's parameters, validated as PiPNNParams::validate
+// validates them (shear-core/src/algorithm/pipnn/params.rs:2696-2729) and
+// resolved as HashPruneBackfillPolicy::from_params resolves them
+// (hash_prune_backfill.rs:44-83: quota 1 for hash-slot-1 else 3, SoftTier
+// alpha 1.1 with alpha^2 exactly 1.21, capacity min(row cap, floor(l_max / 2))
+// by :299-336).
+tessa_status resolve_backfill(const tessa_hashprune_backfill *bf, uint32_t l_max, tessa::HashPruneState &s) {
+    if (!bf || bf->mode == TESSA_HP_BACKFILL_OFF) return ok_status();
+    if (bf->mode < TESSA_HP_BACKFILL_RHALF_HASH_SLOT_1 || bf->mode > TESSA_HP_BACKFILL_RHALF_HARD_TIER_Q3)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune_backfill_mode %u is not a named R-half policy",
+                           bf->mode);
+    const uint32_t budget = l_max / 2;
+    if (bf->max_backfill_per_row && bf->max_backfill_per_row > budget)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "hashprune_rhalf_max_backfill_per_row: named R-half maximum backfill per row must be in "
+                           "1..=floor(l_max/2), got cap=%u l_max=%u",
+                           bf->max_backfill_per_row, l_max);
+    if (bf->hash_quota > 3)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "hashprune_rhalf_hash_quota: named R-half hash quota must be in 1..=3");
+    const float a = bf->soft_tier_priority_alpha;
+    if (a != 0.0f && (bf->mode != TESSA_HP_BACKFILL_RHALF_SOFT_TIER_Q3 || !std::isfinite(a) || a < 1.0f))
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0,
+                           "hashprune_soft_tier_priority_alpha: SoftTier priority alpha must be finite and >= 1.0");
+    s.rhalf_mode = bf->mode;
+    s.rhalf_quota = bf->hash_quota ? bf->hash_quota : (bf->mode == TESSA_HP_BACKFILL_RHALF_HASH_SLOT_1 ? 1u : 3u);
+    s.rhalf_capacity = bf->max_backfill_per_row ? bf->max_backfill_per_row : budget;
+    if (bf->mode == TESSA_HP_BACKFILL_RHALF_SOFT_TIER_Q3) {
+        const float alpha = a != 0.0f ? a : 1.1f;
+        s.rhalf_alpha_sq = alpha == 1.1f ? 1.21 : (double)alpha * (double)alpha;
+    }
+    return ok_status();
+}
 
-extern "C" {
-
-tessa_status tessa_hashprune_create(uint32_t num_points, uint32_t l_max, tessa_hashprune **out) {
+tessa_status hashprune_make(uint32_t num_points, uint32_t l_max, const tessa_hashprune_backfill *bf,
+                            tessa_hashprune **out) {
     if (!out) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune: null output");
     *out = nullptr;
     if (l_max == 0) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "l_max must be > 0");
     if (l_max > tessa::kHpMaxLMax)
         return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: l_max=%u above %u", l_max, tessa::kHpMaxLMax);
+    tessa::HashPruneState probe;
+    tessa_status st = resolve_backfill(bf, l_max, probe);
+    if (st.code) return st;
     auto *hp = new (std::nothrow) tessa_hashprune();
     if (!hp) return make_status(TESSA_ERR_OUT_OF_MEMORY, 0, "hashprune: host allocation failed");
-    TESSA_HIP_TRY(hipGetDevice(&hp->device));
+    if (hipGetDevice(&hp->device) != hipSuccess) {
+        delete hp;
+        return make_status(TESSA_ERR_HIP, 0, "hashprune: hipGetDevice failed");
+    }
     auto &s = hp->st;
+    s = probe;
     s.num_points = num_points;
     s.l_max = l_max;
     const uint64_t slots = (uint64_t)num_points * l_max;
-    tessa_status st = hp_alloc((void **)&s.slot_keys, slots * 8, "hashprune slot keys");
+    st = hp_alloc((void **)&s.slot_keys, slots * 8, "hashprune slot keys");
+    if (!st.code && s.rhalf_mode)
+        st = hp_alloc((void **)&s.grp_keys, slots * 8 * tessa::kRhalfGroup, "hashprune backfill groups");
     if (!st.code) st = hp_alloc((void **)&s.slot_hash, slots * 2, "hashprune slot hashes");
     if (!st.code) st = hp_alloc((void **)&s.slot_count, (uint64_t)num_points * 4, "hashprune slot counts");
     if (!st.code) st = hp_alloc((void **)&s.bucket, (uint64_t)num_points * 4, "hashprune source counts");
@@ -2049,6 +2090,19 @@ tessa_status tessa_hashprune_create(uint32_t num_points, uint32_t l_max, tessa_h
     }
     *out = hp;
     return ok_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+tessa_status tessa_hashprune_create(uint32_t num_points, uint32_t l_max, tessa_hashprune **out) {
+    return hashprune_make(num_points, l_max, nullptr, out);
+}
+
+tessa_status tessa_hashprune_create_backfill(uint32_t num_points, uint32_t l_max,
+                                             const tessa_hashprune_backfill *policy, tessa_hashprune **out) {
+    return hashprune_make(num_points, l_max, policy, out);
 }
 
 tessa_status tessa_hashprune_destroy(tessa_hashprune *hp) {

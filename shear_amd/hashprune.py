@@ -9,13 +9,23 @@ shear-core/src/algorithm/pipnn/):
 * ``reduce_spill_records_ordered``     ExternalHashPruneReducer::reduce_spill_artifacts_ordered
   (spill_hashprune.rs:875-892): one neighbour list per point, slot order
 
-Backfill and evidence policies are off (their defaults, params.rs:3346-3350).
-The reservoirs live in device memory (libtessa_hip.so, ``tessa_hashprune_*``);
-records are merged batch by batch in any order.
+* ``HashPruneBackfill``                the named R-half backfill policies (PiPNNParams
+  hashprune_backfill_mode rhalf-* with hashprune_rhalf_hash_quota,
+  hashprune_rhalf_max_backfill_per_row, hashprune_soft_tier_priority_alpha:
+  params.rs:2070-2083, validated as :2696-2729); ``PRODUCTION_BACKFILL`` is
+  the build_shear_index binary's default (SoftTier-Q3, alpha 1.02, 3 per row,
+  apps/build_shear_index/src/main.rs:2360-2374)
+
+Without a policy, backfill and evidence are off (PiPNNParams' defaults,
+params.rs:3346-3350).  The reservoirs live in device memory (libtessa_hip.so,
+``tessa_hashprune_*``); records are merged batch by batch in any order, with
+or without a policy (its result is the reference's order-independent
+characterization, hash_prune.rs:2601-2682).
 """
 from __future__ import annotations
 
 import ctypes as C
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -26,18 +36,52 @@ from .tessa import _ptr, _stream_ptr
 
 DEFAULT_L_MAX = 64  # params.rs:3346
 
+# PiPNNHashPruneBackfillMode names (params.rs:1935-1966) of the named R-half
+# policies, as tessa_hashprune_backfill.mode numbers them
+BACKFILL_MODES = {"off": 0, "rhalf-hash-slot-1": 1, "rhalf-distance-first-q3": 2, "rhalf-soft-tier-q3": 3,
+                  "rhalf-hard-tier-q3": 4}
+
+
+@dataclass(frozen=True)
+class HashPruneBackfill:
+    """A named R-half policy; None fields take the reference's defaults
+    (hash_prune_backfill.rs:44-83: quota 1 for rhalf-hash-slot-1, else 3;
+    SoftTier alpha 1.1; per-row cap floor(l_max / 2))."""
+    mode: str = "off"
+    hash_quota: int | None = None
+    max_backfill_per_row: int | None = None
+    soft_tier_priority_alpha: float | None = None
+
+    def native(self) -> N.HashPruneBackfill:
+        if self.mode not in BACKFILL_MODES:
+            raise ValueError(f"unsupported hashprune_backfill_mode {self.mode!r} "
+                             f"(the named R-half policies: {', '.join(BACKFILL_MODES)})")
+        return N.HashPruneBackfill(BACKFILL_MODES[self.mode], int(self.hash_quota or 0),
+                                   int(self.max_backfill_per_row or 0), float(self.soft_tier_priority_alpha or 0.0))
+
+
+# build_shear_index's apply_production_hashprune_defaults (main.rs:2360-2374)
+PRODUCTION_BACKFILL = HashPruneBackfill("rhalf-soft-tier-q3", None, 3, 1.02)
+
 
 class HashPruneReducer:
     """Device-resident HashPrune reservoirs for points [0, num_points)."""
 
-    def __init__(self, num_points: int, l_max: int = DEFAULT_L_MAX, device="cuda"):
+    def __init__(self, num_points: int, l_max: int = DEFAULT_L_MAX, device="cuda",
+                 backfill: HashPruneBackfill | None = None):
         self.num_points = int(num_points)
         self.l_max = int(l_max)
         self.device = torch.device(device)
+        self.backfill = backfill if backfill is not None and backfill.mode != "off" else None
         self._lib = N.load()
         h = C.c_void_p()
         with torch.cuda.device(self.device):
-            N.check(self._lib.tessa_hashprune_create(self.num_points, self.l_max, C.byref(h)), "hashprune create")
+            if self.backfill is None:
+                st = self._lib.tessa_hashprune_create(self.num_points, self.l_max, C.byref(h))
+            else:
+                pol = self.backfill.native()
+                st = self._lib.tessa_hashprune_create_backfill(self.num_points, self.l_max, C.byref(pol), C.byref(h))
+            N.check(st, "hashprune create")
         self._h = h
 
     def close(self) -> None:
@@ -91,7 +135,8 @@ class HashPruneReducer:
 
     def slots(self, stream: torch.cuda.Stream | None = None):
         """(targets int32 [num_points, l_max] (0xFFFFFFFF = unused), hashes int16,
-        dists f32, counts int32 [num_points]) in slot order (ascending hash)."""
+        dists f32, counts int32 [num_points]) in slot order (ascending hash),
+        then, with a backfill policy, the row's backups in priority order."""
         t = torch.empty((self.num_points, self.l_max), dtype=torch.int32, device=self.device)
         hs = torch.empty((self.num_points, self.l_max), dtype=torch.int16, device=self.device)
         d = torch.empty((self.num_points, self.l_max), dtype=torch.float32, device=self.device)
@@ -109,10 +154,11 @@ class HashPruneReducer:
         return t, c
 
 
-def reduce_spill_records_ordered(num_points: int, l_max: int, records, device="cuda") -> list[list[int]]:
+def reduce_spill_records_ordered(num_points: int, l_max: int, records, device="cuda",
+                                 backfill: HashPruneBackfill | None = None) -> list[list[int]]:
     """reduce_spill_artifacts_ordered (spill_hashprune.rs:875-892) over host or
     device records: each point's neighbour ids in slot order."""
-    with HashPruneReducer(num_points, l_max, device) as hp:
+    with HashPruneReducer(num_points, l_max, device, backfill) as hp:
         hp.insert(records)
         t, c = hp.neighbors()
         torch.cuda.synchronize(hp.device)

@@ -16,7 +16,10 @@ shear-core/src/algorithm/pipnn/):
   (rbc_partition.rs:4964-4985): the first point of the largest D0 child, ties
   to the smaller point id
 * ``GraphBuildParams``        the PiPNNParams fields this path reads (params.rs:2109-2111
-  fanout_top / fanout_second, :3341-3370 defaults)
+  fanout_top / fanout_second, :3341-3370 defaults); ``hashprune_backfill``
+  the named R-half policy (params.rs:2070-2083), off as in PiPNNParams'
+  default, ``hashprune.PRODUCTION_BACKFILL`` for the build_shear_index
+  binary's SoftTier-Q3 cap 3 (main.rs:2360-2374)
 
 The final RobustPrune follows the build_shear_index binary: it runs only when
 asked (``final_prune``, the binary's ``--final-prune`` flag, off unless given:
@@ -81,6 +84,7 @@ class GraphBuildParams:
     prune_alpha: float = 1.2        # write parameters' alpha: what the final prune uses
     prune_max_occlusion: int = 750
     prune_saturate: bool = True     # build_shear_index builds its write parameters with saturate_graph(true)
+    hashprune_backfill: H.HashPruneBackfill | None = None  # named R-half policy (None: off)
 
     def subtree_params(self) -> S.PiPNNSubtreeParams:
         return S.PiPNNSubtreeParams(leaf_knn=self.leaf_knn, c_max=self.c_max, fanout_second=self.fanout_second,
@@ -266,7 +270,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     if host_reducer is not None:
         tl = TL.TierLiftReducer(rows, p.l_max, host_reducer, dev)
     else:
-        hp = H.HashPruneReducer(rows, p.l_max, dev)
+        hp = H.HashPruneReducer(rows, p.l_max, dev, p.hashprune_backfill)
     st = {"push_s": 0.0, "part_ms": 0.0, "leaf_ms": 0.0, "records": 0, "leaves": 0, "leaf_rows": 0,
           "retries": 0, "runs": 0, "emit_s": 0.0, "reduce_s": 0.0}
     sp = p.subtree_params()

@@ -72,6 +72,8 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         "tessa_d0_child_summary": (N.D0ChildSummary, ["max_rows", "small_rows"]),
         "tessa_captured_assignment": (N.CapturedAssignment, ["depth", "leader_count", "member_offset",
                                                              "leader_offset"]),
+        "tessa_hashprune_backfill": (N.HashPruneBackfill, ["mode", "hash_quota", "max_backfill_per_row",
+                                                           "soft_tier_priority_alpha"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for name, (_, fields) in specs.items():
@@ -89,3 +91,22 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         assert int(got[name]) == C.sizeof(cls), name
         for f in fields:
             assert int(got[f"{name}.{f}"]) == getattr(cls, f).offset, f"{name}.{f}"
+
+
+@pytest.mark.parametrize("policy,l_max,code,text", [
+    ((9, 0, 0, 0.0), 64, 4, "not a named R-half policy"),
+    ((3, 0, 33, 0.0), 64, 1, "1..=floor(l_max/2), got cap=33 l_max=64"),
+    ((1, 4, 0, 0.0), 64, 1, "hash quota must be in 1..=3"),
+    ((3, 0, 0, 0.99), 64, 1, "finite and >= 1.0"),
+    ((3, 0, 0, float("inf")), 64, 1, "finite and >= 1.0"),
+    ((2, 0, 0, 1.05), 64, 1, "SoftTier priority alpha"),  # alpha is SoftTier's only
+    ((3, 0, 1, 0.0), 1, 1, "got cap=1 l_max=1"),
+])
+def test_backfill_policy_validation_without_gpu(policy, l_max, code, text):
+    # params.rs:2696-2729: the policy is checked before any device work
+    # (codes: 1 TESSA_ERR_INVALID_ARGUMENT, 4 TESSA_ERR_UNSUPPORTED)
+    lib = N.load()
+    h = C.c_void_p()
+    st = lib.tessa_hashprune_create_backfill(16, l_max, C.byref(N.HashPruneBackfill(*policy)), C.byref(h))
+    assert st.code == code and not h.value
+    assert text in st.msg.decode()

@@ -149,3 +149,34 @@ def test_c1_final_prune_equals_cpu(gpu, orc, c1):
     print(f"C1 with final prune: recall@10 (L=64) {G.recall_at_k(ids.cpu().numpy(), truth, 10):.4f}, mean degree "
           f"{float(built.counts.float().mean()):.1f} (without: {float(c1['built'].counts.float().mean()):.1f}), "
           f"prune {built.stages['final_prune_ms']:.1f} ms", flush=True)
+
+
+def test_c1_production_backfill_equals_cpu(gpu, orc, c1):
+    """build_shear_index's default HashPrune policy (SoftTier-Q3, alpha 1.02,
+    at most 3 backups per underfull row, main.rs:2360-2374): the GPU image
+    equals the CPU build's with the same policy, byte for byte."""
+    from dataclasses import replace
+
+    from oracle import pybuild as PB
+    from shear_amd import hashprune as H
+
+    x, q, p, xg = c1["x"], c1["q"], c1["p"], c1["xg"]
+    pp = replace(p, hashprune_backfill=H.PRODUCTION_BACKFILL)
+    built = P.build_graph(xg, torch.from_numpy(c1["sk"]).to(gpu), c1["lead"], pp)
+    cpu = PB.build_graph_cpu(x, c1["sk"], c1["lead"], pp)
+    img = built.image.cpu().numpy().tobytes()
+    assert built.start == cpu["start"]
+    assert img == cpu["image"], "GPU and CPU images differ with the production backfill"
+    base = c1["built"].counts.cpu().numpy()
+    cnt = built.counts.cpu().numpy()
+    under = base < p.l_max
+    assert np.all(cnt >= base) and np.all(cnt - base <= 3) and np.all(cnt[~under] == base[~under])
+    qg = torch.from_numpy(q).to(gpu)
+    truth = brute_knn([(0, xg)], qg, 10).cpu().numpy()
+    rec = {}
+    for name, b in (("with", built), ("without", c1["built"])):
+        ids, _, _ = G.greedy_search(xg, b.targets, b.counts, b.start, qg, 64, 10)
+        rec[name] = G.recall_at_k(ids.cpu().numpy(), truth, 10)
+    print(f"C1 with the production backfill: {int((cnt > base).sum())} of {int(under.sum())} underfull rows "
+          f"took {int((cnt - base).sum())} backups; recall@10 (L=64) {rec['with']:.4f} (without: "
+          f"{rec['without']:.4f})", flush=True)
