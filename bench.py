@@ -299,7 +299,9 @@ def build_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(64, 256)):
     """BASELINE configs[2] (C3) built end to end on the GPU: rows x 768 unit
     vectors (1,000 components, sigma 0.25, 5 % outliers, seed 2), SQ8, global
     D0 (fanout 2), many-root subtree runs (fanout 2, leaves <= 2048, k 32),
-    source-grouped records, HashPrune (R 64), `_mem.index`.  Two builds: the
+    source-grouped records, HashPrune (R 64) with the build_shear_index
+    default policy (SoftTier-Q3 backfill, at most 3 backups per underfull
+    row: BASELINE's "HashPrune cap 3"), `_mem.index`.  Two builds: the
     first (untimed for the figure: it also pays one-time set-up) samples 12
     leaves for the oracle check, the second runs with no observer and is the
     reported build time.  Recall@10 of 1,000 held-out queries against exact
@@ -312,10 +314,12 @@ def build_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(64, 256)):
     from shear_amd import pipeline as P
     from shear_amd import tessa as T
 
+    from shear_amd import hashprune as H
+
     spec = datagen.c3_spec(rows)
     x = spec.rows(dev)
     dim = x.shape[1]
-    p = P.GraphBuildParams(c_max=2048)
+    p = P.GraphBuildParams(c_max=2048, hashprune_backfill=H.PRODUCTION_BACKFILL)
     planes_t = torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(dev).t().contiguous()
     lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
 
@@ -344,7 +348,8 @@ def build_leg(rows, dev, check=True, nq=1000, k_recall=10, search_l=(64, 256)):
         f"included; first build {first_s:.3f} s from SQ8), images identical {same}")
     res = {
         "workload": f"C3: {rows} x {dim} unit vectors (1,000 components, sigma 0.25, 5% outliers, seed 2), SQ8, "
-                    f"D0 {len(lead)} leaders fanout 2, many-root subtrees fanout 2, leaves <= 2048, k 32, R 64",
+                    f"D0 {len(lead)} leaders fanout 2, many-root subtrees fanout 2, leaves <= 2048, k 32, R 64, "
+                    f"HashPrune SoftTier-Q3 cap 3",
         "build_s": round(built.build_s, 4),
         "sketch_and_sq8_ms": round(prep_s * 1e3, 2),  # inside build_s
         "first_build_s": round(first_s, 4),

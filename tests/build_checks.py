@@ -7,8 +7,9 @@ on samples, and the verification itself.
   * a few leaves of a few children equal the oracle's leaf top-k bit for bit
     (ids and f32 distance bits);
   * the reservoirs of sampled points equal the oracle's reservoirs over every
-    record those points received (HashPrune is a reduction: its state is a
-    function of the record set, so the sample is exact);
+    record those points received, with the build's backfill policy if any
+    (HashPrune is a reduction: its state is a function of the record set, so
+    the sample is exact);
   * degrees <= R, every point has a neighbour, and the image holds every row."""
 from __future__ import annotations
 
@@ -81,7 +82,14 @@ class BuildObserver:
         pos[sample_h] = np.arange(len(sample_h))
         rec = rec.copy()
         rec["src"] = pos[rec["src"].astype(np.int64)].astype(np.uint32)
-        wt, _, _, wc = orc.hashprune_reduce(len(sample_h), p.l_max, rec)
+        bf = getattr(p, "hashprune_backfill", None)
+        if bf is not None and bf.mode != "off":
+            wt, _, _, wc, _ = orc.hashprune_rhalf_reduce(len(sample_h), p.l_max, rec, mode=bf.mode,
+                                                         hash_quota=bf.hash_quota or 0,
+                                                         row_cap=bf.max_backfill_per_row or 0,
+                                                         priority_alpha=bf.soft_tier_priority_alpha or 0.0)
+        else:
+            wt, _, _, wc = orc.hashprune_reduce(len(sample_h), p.l_max, rec)
         gt = built.targets[self.sample].cpu().numpy().view(np.uint32)
         gc = counts[self.sample].cpu().numpy()
         assert np.array_equal(gc, wc), f"{what}: sampled reservoir sizes differ"

@@ -2,8 +2,9 @@
 vectors (1,000-component mixture, sigma 0.25, 5 % uniform outliers, seed 2;
 inner product run as L2 on unit vectors), SQ8 resident in HBM, global D0 with
 replication fanout 2, a subtree per D0 child (fanout 2 at its root, leaves
-<= 2048, k = 32), edge records, HashPrune reservoirs (R = 64) and the
-`_mem.index` image; 1,000 held-out queries searched from the entry point
+<= 2048, k = 32), edge records, HashPrune reservoirs (R = 64) with the
+build_shear_index default policy (SoftTier-Q3 backfill, at most 3 backups per
+underfull row: "HashPrune cap 3") and the `_mem.index` image; 1,000 held-out queries searched from the entry point
 against exact ground truth.
 
 A CPU build of this size is out of reach, so parity is checked on samples
@@ -21,6 +22,7 @@ from build_checks import BuildObserver, brute_knn, knn_coverage, seeded_recall
 from gpu_helpers import require_gpu
 from shear_amd import datagen
 from shear_amd import graph as G
+from shear_amd import hashprune as H
 from shear_amd import pipeline as P
 from shear_amd import tessa as T
 
@@ -48,7 +50,7 @@ def test_c3_build(gpu, orc):
     spec = datagen.c3_spec(10_000_000)
     x = spec.rows(gpu)
     rows, dim = x.shape
-    p = P.GraphBuildParams(c_max=2048)
+    p = P.GraphBuildParams(c_max=2048, hashprune_backfill=H.PRODUCTION_BACKFILL)
     leaf_max = max(256, p.c_max)
     sk = (x @ torch.from_numpy(P.sketch_planes(dim, p.m_hash_bits, 7)).to(gpu).t()).contiguous()
     lead = P.d0_leader_rows(rows, P.d0_leader_count(rows, dim, p), p.random_seed)
