@@ -296,7 +296,7 @@ __device__ __forceinline__ void reg_bitonic(uint32_t (&h)[E], uint64_t (&k)[E], 
 // positions [0, n) (position q*64 + lane in slot q of lane), ascending in
 // total order, empty entries after them, and returns n.
 template <int E>
-__device__ uint32_t select_sorted(uint32_t (&h)[E], uint64_t (&k)[E], uint32_t l_max, uint32_t lane) {
+__device__ __forceinline__ uint32_t select_sorted(uint32_t (&h)[E], uint64_t (&k)[E], uint32_t l_max, uint32_t lane) {
     reg_bitonic<E, true>(h, k, lane);
     // kept = first of its hash (the predecessor of element 64*q is lane 63 of slot q-1)
     uint32_t n_kept = 0;
@@ -660,7 +660,7 @@ __device__ __forceinline__ void res_insert(Reservoir<ER> &r, uint64_t bk, uint32
 
 // Merges one chunk (candidate (ck, ch) in each lane where v) into the reservoir.
 template <int ER>
-__device__ void res_chunk(Reservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t lane) {
+__device__ __forceinline__ void res_chunk(Reservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t lane) {
     bool pass = v;
     if (r.c == l_max) {
         uint64_t wk;
@@ -929,9 +929,11 @@ __global__ __launch_bounds__(kHpThreads) void hp_export_kernel(const uint64_t *s
 // candidates (a target dropped from it had quota + 1 better distinct targets
 // of the hash, whose keys only improve), so batches still merge in any
 // order.  A reservoir that has filled never frees a slot and a full row takes
-// no backups, so groups are kept only while a slot is free: once the
-// reservoir fills, the plain insert takes over and its groups are neither
-// read nor written again.
+// no backups, so groups are kept only while a slot is free; nothing is
+// evicted then either, so those slots are kept unsorted (a candidate is one
+// hash ballot and an append or an in-place update).  The insert that fills
+// the reservoir sorts it in total order, the plain insert takes over, and the
+// groups are neither read nor written again.
 
 template <int ER>
 struct GroupReservoir {
@@ -939,84 +941,12 @@ struct GroupReservoir {
     uint64_t g[ER][kRhalfGroup];  // the lane's slot's group, ascending keys, ~0 = none
 };
 
-__device__ __forceinline__ uint64_t shfl_up64(uint64_t v) {
-    const uint32_t lo = __shfl_up((uint32_t)v, 1);
-    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), 1);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-// res_shift_in with each slot's group moving with it; position p takes
-// (bk, bh, bg).
-template <int ER>
-__device__ __forceinline__ void gres_shift_in(GroupReservoir<ER> &r, uint32_t p, uint32_t end, uint64_t bk,
-                                              uint32_t bh, const uint64_t (&bg)[kRhalfGroup], uint32_t lane) {
-#pragma unroll
-    for (int q = ER - 1; q >= 0; --q) {
-        if ((uint32_t)q * 64u > end || (uint32_t)q * 64u + 63u < p) continue;  // register untouched
-        const int qb = q > 0 ? q - 1 : 0;  // lane 0 takes the register below's lane 63 (q > 0)
-        uint64_t uk = shfl_up64(r.b.k[q]);
-        uint32_t uh = __shfl_up(r.b.h[q], 1);
-        uint64_t ug[kRhalfGroup];
-#pragma unroll
-        for (uint32_t j = 0; j < kRhalfGroup; ++j) ug[j] = shfl_up64(r.g[q][j]);
-        if (q > 0) {
-            const uint64_t ck = readlane64(r.b.k[qb], 63);
-            const uint32_t ch = readlane32(r.b.h[qb], 63);
-            uk = lane == 0 ? ck : uk;
-            uh = lane == 0 ? ch : uh;
-#pragma unroll
-            for (uint32_t j = 0; j < kRhalfGroup; ++j) {
-                const uint64_t cg = readlane64(r.g[qb][j], 63);
-                ug[j] = lane == 0 ? cg : ug[j];
-            }
-        }
-        const uint32_t e = (uint32_t)q * 64u + lane;
-        const bool mv = e > p && e <= end;
-        r.b.k[q] = e == p ? bk : (mv ? uk : r.b.k[q]);
-        r.b.h[q] = e == p ? bh : (mv ? uh : r.b.h[q]);
-#pragma unroll
-        for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = e == p ? bg[j] : (mv ? ug[j] : r.g[q][j]);
-    }
-}
-
-// Inserts candidate (bk, bh) into a reservoir with a free slot.  A new hash
-// takes a free slot with an empty group; a hit updates the hash's best
-// quota + 1 distinct targets (the owner lane's copy is the slot's) and, when
-// the candidate becomes the hash's best, moves the slot as res_insert does,
-// the old slot key now heading its group.
-template <int ER>
-__device__ __forceinline__ void gres_insert(GroupReservoir<ER> &r, uint64_t bk, uint32_t bh, uint32_t quota,
-                                            uint32_t lane) {
-    uint32_t p = 0;
-    uint32_t hit = 0xffffffffu;
-#pragma unroll
-    for (int q = 0; q < ER; ++q) {
-        const bool live = (uint32_t)q * 64u + lane < r.b.c;
-        p += (uint32_t)__popcll(ballot64(live && ent_less(r.b.k[q], r.b.h[q], bk, bh)));
-        const uint64_t m = ballot64(live && r.b.h[q] == bh);
-        hit = m ? (uint32_t)q * 64u + (uint32_t)__builtin_ctzll(m) : hit;
-    }
-    if (hit == 0xffffffffu) {
-        const uint64_t none[kRhalfGroup] = {~0ull, ~0ull, ~0ull};
-        gres_shift_in(r, p, r.b.c, bk, bh, none, lane);
-        r.b.c = r.b.c + 1u;
-        return;
-    }
-    const uint32_t hq = hit >> 6, hl = hit & 63u;
-    uint64_t s[kRhalfGroup + 1];
-    s[0] = r.b.k[0];
-#pragma unroll
-    for (uint32_t j = 0; j < kRhalfGroup; ++j) s[j + 1] = r.g[0][j];
-#pragma unroll
-    for (int q = 1; q < ER; ++q) {
-        if (hq != (uint32_t)q) continue;
-        s[0] = r.b.k[q];
-#pragma unroll
-        for (uint32_t j = 0; j < kRhalfGroup; ++j) s[j + 1] = r.g[q][j];
-    }
-    const uint64_t ek = readlane64(s[0], hl);
-    // the candidate's target keeps its better key; a new target takes
-    // position quota when better than what is there (~0 when unfilled)
+// The hash's best quota + 1 distinct targets (s[0] the slot key, s[1..] its
+// group, ascending, ~0 = none) with candidate bk added: its target keeps its
+// better key; a new target takes position quota when better than what is
+// there; one backward pass restores the order.
+static_assert(kRhalfGroup == 3, "a group is three keys");
+__device__ __forceinline__ void group_update(uint64_t (&s)[kRhalfGroup + 1], uint64_t bk, uint32_t quota) {
     const uint32_t bt = (uint32_t)bk;
     bool present = false;
 #pragma unroll
@@ -1027,7 +957,6 @@ __device__ __forceinline__ void gres_insert(GroupReservoir<ER> &r, uint64_t bk, 
     }
 #pragma unroll
     for (uint32_t j = 0; j <= kRhalfGroup; ++j) s[j] = !present && j == quota && bk < s[j] ? bk : s[j];
-    // one key decreased: a backward pass restores the ascending order
 #pragma unroll
     for (int j = kRhalfGroup; j >= 1; --j) {
         const uint64_t lo = s[j] < s[j - 1] ? s[j] : s[j - 1];
@@ -1035,46 +964,258 @@ __device__ __forceinline__ void gres_insert(GroupReservoir<ER> &r, uint64_t bk, 
         s[j - 1] = lo;
         s[j] = hi;
     }
-    if (bk < ek) {
-        // the candidate heads its hash now: the slot moves to position p
-        uint64_t bg[kRhalfGroup];
+}
+
+// Inserts candidate (bk, bh) into a reservoir with a free slot.  While a slot
+// is free the slots are kept in no particular order (nothing is evicted, so no
+// rank is needed): a new hash is appended with an empty group, a repeat of a
+// slot's own (target, distance) (a pair seen forward and reverse) changes
+// nothing, and any other candidate of a slot's hash updates that slot's best
+// quota + 1 distinct targets in the owner lane (the slot key is the best of
+// them, the group the rest).  The first two are selects; only the third
+// branches.
+template <int ER>
+__device__ __forceinline__ void gres_fill_insert(GroupReservoir<ER> &r, uint64_t bk, uint32_t bh, uint32_t quota,
+                                                 uint32_t lane) {
+    uint32_t hit = 0xffffffffu;
+    uint64_t ek = 0;
 #pragma unroll
-        for (uint32_t j = 0; j < kRhalfGroup; ++j) bg[j] = readlane64(s[j + 1], hl);
-        gres_shift_in(r, p, hit, bk, bh, bg, lane);
-    } else {
+    for (int q = 0; q < ER; ++q) {
+        const bool live = (uint32_t)q * 64u + lane < r.b.c;
+        const uint64_t m = ballot64(live && r.b.h[q] == bh);
+        if (m) {
+            const uint32_t l = (uint32_t)__builtin_ctzll(m);
+            hit = (uint32_t)q * 64u + l;
+            ek = readlane64(r.b.k[q], l);
+        }
+    }
+    const bool is_new = hit == 0xffffffffu;
+    const uint32_t e = r.b.c, eq = e >> 6;
 #pragma unroll
-        for (int q = 0; q < ER; ++q) {
-            if (hq != (uint32_t)q || lane != hl) continue;
+    for (int q = 0; q < ER; ++q) {
+        const bool at = is_new && eq == (uint32_t)q && lane == (e & 63u);
+        r.b.k[q] = at ? bk : r.b.k[q];
+        r.b.h[q] = at ? bh : r.b.h[q];
 #pragma unroll
-            for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = s[j + 1];
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = at ? ~0ull : r.g[q][j];
+    }
+    r.b.c = e + (is_new ? 1u : 0u);
+    if (is_new || ek == bk) return;
+    const uint32_t hq = hit >> 6, hl = hit & 63u;
+#pragma unroll
+    for (int q = 0; q < ER; ++q) {
+        if (hq != (uint32_t)q) continue;
+        uint64_t s[kRhalfGroup + 1] = {r.b.k[q], r.g[q][0], r.g[q][1], r.g[q][2]};
+        group_update(s, bk, quota);
+        const bool own = lane == hl;
+        r.b.k[q] = own ? s[0] : r.b.k[q];
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = own ? s[j + 1] : r.g[q][j];
+    }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_up64(uint64_t v) {
+    const uint32_t lo = __shfl_up((uint32_t)v, 1);
+    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), 1);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_down64(uint64_t v, uint32_t d) {
+    const uint32_t lo = __shfl_down((uint32_t)v, d);
+    const uint32_t hi = __shfl_down((uint32_t)(v >> 32), d);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t permute64(uint32_t dest, uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_permute((int)(dest * 4u), (int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_permute((int)(dest * 4u), (int)(uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Ascending bitonic sort of one (a, b) pair per lane across the wave,
+// lexicographic.
+__device__ __forceinline__ void wave_sort_pair(uint64_t &a, uint64_t &b, uint32_t lane) {
+#pragma unroll
+    for (uint32_t kk = 2; kk <= 64u; kk <<= 1) {
+#pragma unroll
+        for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
+            const uint64_t pa = shfl_xor64(a, (int)j), pb = shfl_xor64(b, (int)j);
+            const bool want_min = ((lane & j) == 0) == ((lane & kk) == 0);
+            const bool p_less = pa < a || (pa == a && pb < b);
+            const bool p_more = a < pa || (a == pa && b < pb);
+            const bool take = want_min ? p_less : p_more;
+            a = take ? pa : a;
+            b = take ? pb : b;
         }
     }
 }
 
+// A chunk (candidate (ck, ch) in each lane where v) into an empty reservoir,
+// by sorting instead of one insert per candidate: the candidates sorted by
+// (hash, target, key) drop repeats of a (hash, target); sorted by (hash,
+// key), each hash's first is its slot and the next `quota` its group.  With
+// l_max hashes or more the reservoir fills: each hash's best, the l_max best
+// of those, sorted in total order (select_sorted).  Otherwise the slots are
+// moved to positions [0, hashes) (one push permute per word).
 template <int ER>
-__device__ void gres_chunk(GroupReservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t quota,
+__device__ __forceinline__ void gres_batch_fill(GroupReservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max,
+                                uint32_t quota, uint32_t lane) {
+    uint64_t a = v ? ((uint64_t)ch << 32) | (uint32_t)ck : ~0ull;  // (hash, target)
+    uint64_t b = v ? (ck >> 32) : ~0ull;                             // distance key
+    wave_sort_pair(a, b, lane);
+    const uint64_t ap = shfl_up64(a);
+    const bool keep = a != ~0ull && (lane == 0 || ap != a);  // a target's best within its hash
+    uint64_t hs = keep ? (a >> 32) : ~0ull;
+    uint64_t k = keep ? ((b << 32) | (uint32_t)a) : ~0ull;
+    wave_sort_pair(hs, k, lane);
+    const uint32_t h = (uint32_t)hs;  // 0xffffffff for the empty entries after the real ones
+    const uint32_t hp = __shfl_up(h, 1);
+    const bool start = h != 0xffffffffu && (lane == 0 || hp != h);
+    const uint64_t S = ballot64(start);
+    const uint32_t m = (uint32_t)__popcll(S);
+    if (m >= l_max) {
+        uint32_t rh[ER];
+        uint64_t rk[ER];
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            rh[q] = q == 0 ? h : 0xffffffffu;
+            rk[q] = q == 0 ? k : ~0ull;
+        }
+        r.b.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)select_sorted<ER>(rh, rk, l_max, lane));
+#pragma unroll
+        for (int q = 0; q < ER; ++q) {
+            r.b.h[q] = rh[q];
+            r.b.k[q] = rk[q];
+        }
+        return;
+    }
+    // rank of each entry within its hash: lanes since the last start at or before it
+    const uint64_t upto = lane == 63u ? ~0ull : ((2ull << lane) - 1ull);
+    const uint32_t rank = lane - (63u - (uint32_t)__builtin_clzll(S & upto));
+    uint64_t g[kRhalfGroup];
+#pragma unroll
+    for (uint32_t j = 1; j <= kRhalfGroup; ++j) {
+        const uint64_t kd = shfl_down64(k, j);
+        const uint32_t rd = __shfl_down(rank, j);
+        const uint32_t hd = __shfl_down(h, j);
+        g[j - 1] = lane + j < 64u && j <= quota && hd == h && rd == j ? kd : ~0ull;
+    }
+    // slots to [0, m), the other entries after them
+    const uint32_t below = (uint32_t)__popcll(S & ((1ull << lane) - 1ull));
+    const uint32_t dest = start ? below : m + (lane - below);
+    const uint64_t sk = permute64(dest, k);
+    const uint32_t sh = (uint32_t)__builtin_amdgcn_ds_permute((int)(dest * 4u), (int)h);
+    uint64_t sg[kRhalfGroup];
+#pragma unroll
+    for (uint32_t j = 0; j < kRhalfGroup; ++j) sg[j] = permute64(dest, g[j]);
+    const bool live = lane < m;
+#pragma unroll
+    for (int q = 0; q < ER; ++q) {
+        r.b.k[q] = q == 0 && live ? sk : ~0ull;
+        r.b.h[q] = q == 0 && live ? sh : 0xffffffffu;
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j) r.g[q][j] = q == 0 && live ? sg[j] : ~0ull;
+    }
+    r.b.c = m;
+}
+
+// Merges one chunk.  A full reservoir takes the plain path (res_chunk: slots
+// sorted in total order, the one-compare bound); a first chunk of at least
+// kBatchMin candidates into an empty one is sorted in (gres_batch_fill).
+// Otherwise the candidates go in one at a time; the insert that fills the
+// reservoir sorts its slots in total order (the plain path's invariant) and
+// the rest of the chunk takes the plain path.
+template <int ER>
+__device__ __forceinline__ void gres_chunk(GroupReservoir<ER> &r, uint64_t ck, uint32_t ch, bool v, uint32_t l_max, uint32_t quota,
                            uint32_t lane) {
     if (r.b.c == l_max) {
         res_chunk(r.b, ck, ch, v, l_max, lane);
         return;
     }
     uint64_t pm = ballot64(v);
+    if (r.b.c == 0 && (uint32_t)__popcll(pm) >= kBatchMin) {
+        gres_batch_fill(r, ck, ch, v, l_max, quota, lane);
+        return;
+    }
     while (pm) {
         const uint32_t j = (uint32_t)__builtin_ctzll(pm);
         pm &= pm - 1ull;
-        const uint64_t bk = readlane64(ck, j);
-        const uint32_t bh = readlane32(ch, j);
-        if (r.b.c < l_max)
-            gres_insert(r, bk, bh, quota, lane);
-        else
-            res_insert(r.b, bk, bh, l_max, lane);
+        gres_fill_insert(r, readlane64(ck, j), readlane32(ch, j), quota, lane);
+        if (r.b.c == l_max) {
+            reg_bitonic<ER, false>(r.b.h, r.b.k, lane);
+            res_chunk(r.b, ck, ch, v && lane > j, l_max, lane);
+            return;
+        }
+    }
+}
+
+// A source's run as the merge needs it: source (num_points: nothing to
+// merge), its sorted segments [start, start + len), the lane's segment
+// (records cnt from first), and its slot count.
+struct RunInfo {
+    uint32_t src, start, len, cnt, c;
+    uint64_t first;
+};
+
+template <bool kGrouped>
+__device__ __forceinline__ RunInfo run_info(uint32_t a, uint32_t na, const uint4 *sorted, const uint32_t *run_src,
+                                            const uint32_t *run_start, const uint32_t *run_len,
+                                            const uint32_t *offsets, uint32_t num_points,
+                                            const uint32_t *slot_count, uint32_t lane) {
+    RunInfo ri{num_points, 0u, 1u, 0u, 0u, 0ull};
+    if (a >= na) return ri;
+    if (kGrouped) {
+        const uint32_t o0 = offsets[a], o1 = offsets[a + 1];
+        if (o1 == o0) return ri;
+        ri.src = a;
+        ri.cnt = lane == 0 ? o1 - o0 : 0u;
+        ri.first = o0;
+    } else {
+        const uint32_t src = run_src[a];
+        if (src >= num_points) return ri;  // the run of empty / bad segments
+        ri.src = src;
+        ri.start = run_start[a];
+        ri.len = run_len[a];
+        if (lane < ri.len) {
+            const uint4 g = sorted[(uint64_t)ri.start + lane];
+            ri.cnt = g.w;
+            ri.first = ((uint64_t)g.z << 32) | g.y;
+        }
+    }
+    ri.c = slot_count[ri.src];
+    return ri;
+}
+
+// A source's live slots, and their groups while a slot is free.
+template <int ER>
+__device__ __forceinline__ void load_slots(GroupReservoir<ER> &r, const RunInfo &ri, uint32_t num_points,
+                                           uint32_t l_max, const uint64_t *slot_keys, const uint16_t *slot_hash,
+                                           const uint64_t *grp_keys, uint32_t lane) {
+    const bool real = ri.src < num_points;
+    const uint32_t c = real ? ri.c : 0u;
+    const bool groups = c < l_max;
+    const uint64_t sbase = (uint64_t)(real ? ri.src : 0u) * l_max;
+#pragma unroll
+    for (int q = 0; q < ER; ++q) {
+        const uint32_t e = (uint32_t)q * 64u + lane;
+        const bool live = e < c;
+        r.b.k[q] = live ? slot_keys[sbase + e] : ~0ull;
+        r.b.h[q] = live ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
+#pragma unroll
+        for (uint32_t j = 0; j < kRhalfGroup; ++j)
+            r.g[q][j] = live && groups ? grp_keys[(sbase + e) * kRhalfGroup + j] : ~0ull;
     }
 }
 
 // One wave per source with new records: its slots (and, while a slot is free,
 // their groups) in registers, its records streamed through them.  Sources
 // come from segment runs (as hp_merge_stream_kernel) or, kGrouped, from the
-// record batch grouped by source (offsets[src] .. offsets[src + 1]).
+// record batch grouped by source (offsets[src] .. offsets[src + 1]).  Each
+// wave walks its sources with the next source's slots, and the one after's
+// run and slot count, already in flight.
 template <int ER, bool kGrouped>
 __global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
     const uint4 *records, const uint4 *sorted, const uint32_t *run_src, const uint32_t *run_start,
@@ -1083,78 +1224,65 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t waves = gridDim.x * kHpWaves;
     const uint32_t na = kGrouped ? num_points : *num_runs;
-    for (uint32_t a = blockIdx.x * kHpWaves + (threadIdx.x >> 6); a < na; a += waves) {
-        uint32_t src, start = 0, len = 1, cnt = 0;
-        uint64_t first = 0;
-        if (kGrouped) {
-            src = a;
-            const uint32_t o0 = offsets[a], o1 = offsets[a + 1];
-            if (o1 == o0) continue;
-            cnt = lane == 0 ? o1 - o0 : 0u;
-            first = o0;
-        } else {
-            src = run_src[a];
-            if (src >= num_points) continue;  // the run of empty / bad segments
-            start = run_start[a];
-            len = run_len[a];
-            if (lane < len) {
-                const uint4 g = sorted[(uint64_t)start + lane];
-                cnt = g.w;
-                first = ((uint64_t)g.z << 32) | g.y;
+    uint32_t a = blockIdx.x * kHpWaves + (threadIdx.x >> 6);
+    if (a >= na) return;
+    auto info = [&](uint32_t i) {
+        return run_info<kGrouped>(i, na, sorted, run_src, run_start, run_len, offsets, num_points, slot_count,
+                                  lane);
+    };
+    RunInfo cur_ri = info(a);
+    GroupReservoir<ER> cur;
+    load_slots(cur, cur_ri, num_points, l_max, slot_keys, slot_hash, grp_keys, lane);
+    RunInfo nxt_ri = info(a + waves);
+    for (; a < na; a += waves) {
+        GroupReservoir<ER> nxt;
+        load_slots(nxt, nxt_ri, num_points, l_max, slot_keys, slot_hash, grp_keys, lane);
+        const RunInfo far_ri = info(a + 2u * waves);
+        const uint32_t src = cur_ri.src;
+        if (src < num_points) {
+            GroupReservoir<ER> &r = cur;
+            r.b.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)cur_ri.c);
+            const uint32_t len = cur_ri.len;
+            auto chunk = [&](uint64_t ck, uint32_t ch, bool v) { gres_chunk(r, ck, ch, v, l_max, quota, lane); };
+            stream_group(records, len < 64u ? len : 64u, cur_ri.cnt, cur_ri.first, lane, chunk);
+            for (uint32_t g0 = 64; g0 < len; g0 += 64) {
+                // a source with more than 64 segments in the batch: the rest, 64 at a time
+                const uint32_t ng = len - g0 < 64u ? len - g0 : 64u;
+                uint32_t c2 = 0;
+                uint64_t f2 = 0;
+                if (lane < ng) {
+                    const uint4 g = sorted[(uint64_t)cur_ri.start + g0 + lane];
+                    c2 = g.w;
+                    f2 = ((uint64_t)g.z << 32) | g.y;
+                }
+                stream_group(records, ng, c2, f2, lane, chunk);
             }
-        }
-        GroupReservoir<ER> r;
-        const uint64_t sbase = (uint64_t)src * l_max;
-        r.b.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)slot_count[src]);
-        const bool groups = r.b.c < l_max;
+            const uint64_t sbase = (uint64_t)src * l_max;
+            const bool keep_groups = r.b.c < l_max;
 #pragma unroll
-        for (int q = 0; q < ER; ++q) {
-            const uint32_t e = (uint32_t)q * 64u + lane;
-            const bool live = e < r.b.c;
-            r.b.k[q] = live ? slot_keys[sbase + e] : ~0ull;
-            r.b.h[q] = live ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
+            for (int q = 0; q < ER; ++q) {
+                const uint32_t e = (uint32_t)q * 64u + lane;
+                if (e < r.b.c) {
+                    slot_keys[sbase + e] = r.b.k[q];
+                    slot_hash[sbase + e] = (uint16_t)r.b.h[q];
+                    if (keep_groups) {
 #pragma unroll
-            for (uint32_t j = 0; j < kRhalfGroup; ++j)
-                r.g[q][j] = live && groups ? grp_keys[(sbase + e) * kRhalfGroup + j] : ~0ull;
-        }
-        auto chunk = [&](uint64_t ck, uint32_t ch, bool v) { gres_chunk(r, ck, ch, v, l_max, quota, lane); };
-        stream_group(records, len < 64u ? len : 64u, cnt, first, lane, chunk);
-        for (uint32_t g0 = 64; g0 < len; g0 += 64) {
-            const uint32_t ng = len - g0 < 64u ? len - g0 : 64u;
-            uint32_t c2 = 0;
-            uint64_t f2 = 0;
-            if (lane < ng) {
-                const uint4 g = sorted[(uint64_t)start + g0 + lane];
-                c2 = g.w;
-                f2 = ((uint64_t)g.z << 32) | g.y;
-            }
-            stream_group(records, ng, c2, f2, lane, chunk);
-        }
-        const bool keep_groups = r.b.c < l_max;
-#pragma unroll
-        for (int q = 0; q < ER; ++q) {
-            const uint32_t e = (uint32_t)q * 64u + lane;
-            if (e < r.b.c) {
-                slot_keys[sbase + e] = r.b.k[q];
-                slot_hash[sbase + e] = (uint16_t)r.b.h[q];
-                if (keep_groups) {
-#pragma unroll
-                    for (uint32_t j = 0; j < kRhalfGroup; ++j) grp_keys[(sbase + e) * kRhalfGroup + j] = r.g[q][j];
+                        for (uint32_t j = 0; j < kRhalfGroup; ++j)
+                            grp_keys[(sbase + e) * kRhalfGroup + j] = r.g[q][j];
+                    }
                 }
             }
+            if (lane == 0) slot_count[src] = r.b.c;
         }
-        if (lane == 0) slot_count[src] = r.b.c;
+        cur = nxt;
+        cur_ri = nxt_ri;
+        nxt_ri = far_ri;
     }
 }
 
 __device__ __forceinline__ uint64_t total_key64(double d) {
     const uint64_t b = (uint64_t)__double_as_longlong(d);
     return (b & 0x8000000000000000ull) ? ~b : (b | 0x8000000000000000ull);
-}
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, m);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
-    return ((uint64_t)hi << 32) | lo;
 }
 
 // A group member's rank under the mode's priority (hash_prune.rs:655-685) as
