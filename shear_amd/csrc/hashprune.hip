@@ -1189,24 +1189,20 @@ __device__ __forceinline__ RunInfo run_info(uint32_t a, uint32_t na, const uint4
     return ri;
 }
 
-// A source's live slots, and their groups while a slot is free.
+// A source's live slots (prefetched one source ahead).
 template <int ER>
-__device__ __forceinline__ void load_slots(GroupReservoir<ER> &r, const RunInfo &ri, uint32_t num_points,
+__device__ __forceinline__ void load_slots(Reservoir<ER> &r, const RunInfo &ri, uint32_t num_points,
                                            uint32_t l_max, const uint64_t *slot_keys, const uint16_t *slot_hash,
-                                           const uint64_t *grp_keys, uint32_t lane) {
+                                           uint32_t lane) {
     const bool real = ri.src < num_points;
     const uint32_t c = real ? ri.c : 0u;
-    const bool groups = c < l_max;
     const uint64_t sbase = (uint64_t)(real ? ri.src : 0u) * l_max;
 #pragma unroll
     for (int q = 0; q < ER; ++q) {
         const uint32_t e = (uint32_t)q * 64u + lane;
         const bool live = e < c;
-        r.b.k[q] = live ? slot_keys[sbase + e] : ~0ull;
-        r.b.h[q] = live ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
-#pragma unroll
-        for (uint32_t j = 0; j < kRhalfGroup; ++j)
-            r.g[q][j] = live && groups ? grp_keys[(sbase + e) * kRhalfGroup + j] : ~0ull;
+        r.k[q] = live ? slot_keys[sbase + e] : ~0ull;
+        r.h[q] = live ? (uint32_t)slot_hash[sbase + e] : 0xffffffffu;
     }
 }
 
@@ -1215,9 +1211,11 @@ __device__ __forceinline__ void load_slots(GroupReservoir<ER> &r, const RunInfo 
 // come from segment runs (as hp_merge_stream_kernel) or, kGrouped, from the
 // record batch grouped by source (offsets[src] .. offsets[src + 1]).  Each
 // wave walks its sources with the next source's slots, and the one after's
-// run and slot count, already in flight.
+// run and slot count, already in flight.  Five waves per SIMD (a few
+// registers of the rarely taken paths spill) beat the four that fit without
+// spilling: the kernel is bound by latency more than by its instructions.
 template <int ER, bool kGrouped>
-__global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
+__global__ __launch_bounds__(kHpThreads) __attribute__((amdgpu_waves_per_eu(5))) void hp_merge_rhalf_kernel(
     const uint4 *records, const uint4 *sorted, const uint32_t *run_src, const uint32_t *run_start,
     const uint32_t *run_len, const uint32_t *num_runs, const uint32_t *offsets, uint32_t num_points, uint32_t l_max,
     uint32_t quota, uint64_t *slot_keys, uint16_t *slot_hash, uint32_t *slot_count, uint64_t *grp_keys) {
@@ -1231,17 +1229,28 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
                                   lane);
     };
     RunInfo cur_ri = info(a);
-    GroupReservoir<ER> cur;
-    load_slots(cur, cur_ri, num_points, l_max, slot_keys, slot_hash, grp_keys, lane);
+    Reservoir<ER> cur;
+    load_slots(cur, cur_ri, num_points, l_max, slot_keys, slot_hash, lane);
     RunInfo nxt_ri = info(a + waves);
     for (; a < na; a += waves) {
-        GroupReservoir<ER> nxt;
-        load_slots(nxt, nxt_ri, num_points, l_max, slot_keys, slot_hash, grp_keys, lane);
+        Reservoir<ER> nxt;
+        load_slots(nxt, nxt_ri, num_points, l_max, slot_keys, slot_hash, lane);
         const RunInfo far_ri = info(a + 2u * waves);
         const uint32_t src = cur_ri.src;
         if (src < num_points) {
-            GroupReservoir<ER> &r = cur;
+            GroupReservoir<ER> r;
+            r.b = cur;
             r.b.c = (uint32_t)__builtin_amdgcn_readfirstlane((int)cur_ri.c);
+            const uint64_t sbase = (uint64_t)src * l_max;
+            // the groups of a reservoir with a free slot (its slots' only)
+            const bool groups = r.b.c > 0u && r.b.c < l_max;
+#pragma unroll
+            for (int q = 0; q < ER; ++q) {
+                const uint32_t e = (uint32_t)q * 64u + lane;
+#pragma unroll
+                for (uint32_t j = 0; j < kRhalfGroup; ++j)
+                    r.g[q][j] = groups && e < r.b.c ? grp_keys[(sbase + e) * kRhalfGroup + j] : ~0ull;
+            }
             const uint32_t len = cur_ri.len;
             auto chunk = [&](uint64_t ck, uint32_t ch, bool v) { gres_chunk(r, ck, ch, v, l_max, quota, lane); };
             stream_group(records, len < 64u ? len : 64u, cur_ri.cnt, cur_ri.first, lane, chunk);
@@ -1257,7 +1266,6 @@ __global__ __launch_bounds__(kHpThreads) void hp_merge_rhalf_kernel(
                 }
                 stream_group(records, ng, c2, f2, lane, chunk);
             }
-            const uint64_t sbase = (uint64_t)src * l_max;
             const bool keep_groups = r.b.c < l_max;
 #pragma unroll
             for (int q = 0; q < ER; ++q) {
