@@ -366,7 +366,9 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             }
         }
 
-        __syncthreads();  // previous item's readers of the LDS arrays are done
+        // previous item's readers of the LDS arrays are done; an LDS-only
+        // barrier, so the row codes above stay in flight through the staging
+        lds_barrier();
         {
             // four columns per thread per step (a 2,048-row leaf in one step),
             // every load of a step issued before its results are used
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
             }
         }
         if (tid == 0) *s_next = ticket;
-        __syncthreads();
+        lds_barrier();
         it_next = *s_next;
         float cn_min = __uint_as_float(misc[0]), cn_max = __uint_as_float(misc[1]);
 #pragma unroll
