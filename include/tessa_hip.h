@@ -679,6 +679,13 @@ tessa_status tessa_hashprune_create_backfill(uint32_t num_points, uint32_t l_max
  *            `stream`; equal to one tessa_hashprune reduction of every record
  *            pushed.  Once only; no push after it;
  *   destroy  stops the worker and frees every buffer (spill files remain).
+ * Spilling runs on a thread of its own: past 7/8 of the budget the shard with
+ * the most buffered records is handed to it while routing goes on; pushes
+ * block only past the budget itself.  When expected_records says the stream
+ * will not fit the budget, the shards beyond those that fit are spilled from
+ * the start (whenever one has 256 MB buffered), so the disk writes overlap
+ * the whole stream; the reduction is the same either way, only which records
+ * sit in which part file differs. 
  * A record with src >= num_points fails the push that carried it, and every
  * later call, with "Spill reducer encountered edge p=... outside shard
  * range". */
@@ -691,6 +698,7 @@ typedef struct tessa_tierlift_config {
     const char *spill_base;       /* candidate path whose directory and stem name the spill files */
     uint32_t l_max;
     uint32_t threads;
+    uint64_t expected_records;    /* 0, or about how many records will be pushed (see below) */
 } tessa_tierlift_config;
 typedef struct tessa_tierlift_stats {
     uint64_t records;             /* records pushed */

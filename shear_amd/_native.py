@@ -298,7 +298,7 @@ class CapturedAssignment(C.Structure):
 class TierLiftConfig(C.Structure):
     _fields_ = [("num_points", C.c_uint64), ("shard_points", C.c_uint64), ("host_budget_bytes", C.c_uint64),
                 ("staging_records", C.c_uint64), ("spill_base", C.c_char_p), ("l_max", C.c_uint32),
-                ("threads", C.c_uint32)]
+                ("threads", C.c_uint32), ("expected_records", C.c_uint64)]
 
 
 class TierLiftStats(C.Structure):

@@ -2154,6 +2154,39 @@ tessa_status tessa_hashprune_insert(tessa_hashprune *hp, const tessa_edge_record
     return ok_status();
 }
 
+}  // extern "C"
+
+namespace tessa {
+
+// tessa_hashprune_insert without the read-back of the out-of-range check: no
+// stream synchronisation once the grouped buffer holds `count` records (it
+// grows, synchronising, on the first larger batch).  For callers whose
+// records are known to be in range (TierLift routes only those).
+tessa_status hashprune_insert_async(tessa_hashprune *hp, const tessa_edge_record *records, uint64_t count,
+                                    hipStream_t hs) {
+    if (!hp) return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "hashprune is null");
+    if (count >= 0xffffffffull)
+        return make_status(TESSA_ERR_UNSUPPORTED, 0, "hashprune: %llu records in one batch (limit 2^32-2)",
+                           (unsigned long long)count);
+    auto &s = hp->st;
+    if (count > s.grouped_capacity) {
+        TESSA_HIP_TRY(hipStreamSynchronize(hs));
+        if (s.grouped) TESSA_HIP_TRY(hipFree(s.grouped));
+        s.grouped = nullptr;
+        s.grouped_capacity = 0;
+        tessa_status st = hp_alloc((void **)&s.grouped, count * 16, "hashprune grouped records");
+        if (st.code) return st;
+        s.grouped_capacity = count;
+    }
+    if (tessa::launch_hashprune_insert(s, reinterpret_cast<const uint4 *>(records), count, hs) != 0)
+        return make_status(TESSA_ERR_HIP, 0, "hashprune insert launch failed");
+    return ok_status();
+}
+
+}  // namespace tessa
+
+extern "C" {
+
 tessa_status tessa_hashprune_insert_segments(tessa_hashprune *hp, const tessa_edge_record *records,
                                              const tessa_edge_segment *segments, uint64_t segment_count,
                                              void *stream) {

@@ -12,16 +12,19 @@
 //   worker   a host thread takes the slots in order and routes their records
 //            to source-range shards (src / shard_points) with several
 //            threads, into per-shard blocks of 1,000,000 records;
-//   spill    while the blocks in use exceed the host budget, the shard with
-//            the most buffered records is written out: each block becomes one
-//            segment, sorted by src (counting sort, stable), placed in the
-//            shard's part files (rolled over past 4 GiB) at offsets fixed
-//            before the parallel writes;
+//   spill    past 7/8 of the host budget the worker hands the shard with the
+//            most buffered records to a spill thread and goes on routing (it
+//            waits only past the budget itself): each of the shard's blocks
+//            becomes one segment, sorted by src (counting sort, stable), placed
+//            in the shard's part files (rolled over past 4 GiB) at offsets
+//            fixed before the parallel writes;
 //   finish   the manifest is written, then shard by shard the spilled
-//            segments and the buffered blocks go back to the device through the
-//            pinned slots, sources are rebased to the shard, the HashPrune
-//            reservoir kernels merge them, and the shard's reservoirs are
-//            exported into the caller's neighbour table.
+//            segments (read straight into the pinned slots) and the buffered
+//            blocks go back to the device on the copy stream into two device
+//            buffers in turn, while the caller's stream rebases sources to the
+//            shard and merges the other buffer with the HashPrune reservoir
+//            kernels; each shard's reservoirs are exported into the caller's
+//            neighbour table.
 //
 // A reservoir's final state depends only on its record set (HashPrune with
 // backfill and evidence policies off), so the table equals one in-HBM
@@ -32,6 +35,7 @@
 #include <algorithm>
 #include <chrono>
 #include <condition_variable>
+#include <deque>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -43,6 +47,11 @@
 
 #include "hashprune_kernels.h"
 #include "tessa_device.h"
+
+namespace tessa {
+tessa_status hashprune_insert_async(tessa_hashprune *hp, const tessa_edge_record *records, uint64_t count,
+                                    hipStream_t hs);
+}
 
 namespace {
 
@@ -58,6 +67,7 @@ constexpr uint64_t kBlockBytes = kBlockRecords * sizeof(Rec);
 constexpr uint64_t kPartMaxBytes = 4ull * 1024 * 1024 * 1024;  // DEFAULT_PART_MAX_BYTES :27
 constexpr uint64_t kUploadRecords = 1ull << 26;               // records per reservoir merge at finish (1 GiB)
 constexpr uint64_t kCountingSortMaxShard = 1ull << 24;        // larger shards sort by comparison
+constexpr uint64_t kEagerSpillBlocks = 16;                    // an early-spilled shard's job size (256 MB)
 
 struct Shard {
     std::vector<Rec *> blocks;  // kBlockRecords each; the last one partly filled
@@ -71,6 +81,13 @@ struct Segment {
     uint32_t shard, file;
     uint64_t offset, bytes, records;
     uint32_t src_min, src_max;
+};
+
+// A shard's buffered records handed to the spill thread.
+struct SpillJob {
+    uint32_t shard;
+    std::vector<Rec *> blocks;
+    uint64_t n;
 };
 
 __global__ void rebase_src_kernel(uint4 *rec, uint64_t n, uint32_t lo) {
@@ -121,13 +138,17 @@ struct tessa_tierlift {
     bool slot_full[2] = {false, false};
     int next_slot = 0;
     uint64_t next_seq = 0, copied_seq = 0;
-    // host worker
+    // host worker and spill thread (mu guards the slots, the block pool, the
+    // spill queue, segments and error)
     std::mutex mu;
     std::condition_variable cv;
-    std::thread worker;
+    std::thread worker, spiller;
     bool stopping = false, finished = false;
     std::string error;
-    // shard blocks, spill files
+    std::deque<SpillJob> jobs;
+    bool spilling = false;  // the spill thread holds a job
+    uint32_t keep_shards = 0;  // shards [keep_shards, shards) are spilled from the start
+    // shard blocks (routing: worker), part files (spill thread, then finish)
     std::vector<Shard> shard;
     std::vector<Rec *> free_blocks;
     uint64_t blocks_in_use = 0, blocks_allocated = 0;
@@ -143,6 +164,7 @@ std::string part_path(const tessa_tierlift *t, uint32_t shard, uint32_t part) {
     return t->dir + "/" + t->stem + tail;
 }
 
+// Block pool; the caller holds t->mu.
 Rec *take_block(tessa_tierlift *t) {
     Rec *b = nullptr;
     if (!t->free_blocks.empty()) {
@@ -163,12 +185,15 @@ void give_block(tessa_tierlift *t, Rec *b) {
     t->blocks_in_use -= 1;
 }
 
-// Writes shard s's buffered records as segments (one per block, sorted by
-// src) to its part files, then returns the blocks to the pool.  Worker only.
-bool spill_shard(tessa_tierlift *t, uint32_t s, std::string &err) {
+// Writes a job's records (a shard's detached blocks) as segments, one per
+// block, sorted by src, to the shard's part files, then returns the blocks to
+// the pool.  Spill thread only (and the part-file state is the spill
+// thread's until finish).
+bool spill_job(tessa_tierlift *t, SpillJob &job, std::string &err) {
+    const uint32_t s = job.shard;
     Shard &sh = t->shard[s];
     const double t0 = now_s();
-    const uint32_t nb = (uint32_t)sh.blocks.size();
+    const uint32_t nb = (uint32_t)job.blocks.size();
     struct Place {
         uint32_t file;
         int fd;
@@ -177,7 +202,7 @@ bool spill_shard(tessa_tierlift *t, uint32_t s, std::string &err) {
     std::vector<Place> place(nb);
     std::vector<int> to_close;  // part files rolled over here: closed after the writes
     for (uint32_t b = 0; b < nb; ++b) {
-        const uint64_t n = std::min<uint64_t>(kBlockRecords, sh.n - (uint64_t)b * kBlockRecords);
+        const uint64_t n = std::min<uint64_t>(kBlockRecords, job.n - (uint64_t)b * kBlockRecords);
         const uint64_t bytes = n * sizeof(Rec);
         if (sh.fd < 0 || sh.part_bytes + bytes > kPartMaxBytes) {
             if (sh.fd >= 0) {
@@ -206,7 +231,7 @@ bool spill_shard(tessa_tierlift *t, uint32_t s, std::string &err) {
         std::vector<Rec> out(kBlockRecords);
         std::vector<uint32_t> hist(span <= kCountingSortMaxShard ? span + 1 : 0);
         for (uint32_t b = w; b < nb; b += T) {
-            const Rec *in = sh.blocks[b];
+            const Rec *in = job.blocks[b];
             const uint64_t n = place[b].records;
             if (!hist.empty()) {
                 std::fill(hist.begin(), hist.end(), 0u);
@@ -239,18 +264,43 @@ bool spill_shard(tessa_tierlift *t, uint32_t s, std::string &err) {
             err = "TierLift spill: short write to a part file of shard " + std::to_string(s);
             return false;
         }
+    std::lock_guard<std::mutex> lk(t->mu);
     for (uint32_t b = 0; b < nb; ++b) {
         const uint64_t bytes = place[b].records * sizeof(Rec);
         t->segments.push_back(Segment{s, place[b].file, place[b].offset, bytes, place[b].records, smin[b], smax[b]});
         t->stats.spilled_records += place[b].records;
         t->stats.spilled_bytes += bytes;
         t->stats.segments += 1;
-        give_block(t, sh.blocks[b]);
+        give_block(t, job.blocks[b]);
     }
-    sh.blocks.clear();
-    sh.n = 0;
+    job.blocks.clear();
     t->stats.spill_s += now_s() - t0;
     return true;
+}
+
+void spiller_main(tessa_tierlift *t) {
+    for (;;) {
+        SpillJob job;
+        {
+            std::unique_lock<std::mutex> lk(t->mu);
+            t->cv.wait(lk, [&] { return !t->jobs.empty() || t->stopping; });
+            if (t->jobs.empty()) return;
+            job = std::move(t->jobs.front());
+            t->jobs.pop_front();
+            t->spilling = true;
+        }
+        std::string err;
+        const bool ok = spill_job(t, job, err);
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            if (!ok) {
+                if (t->error.empty()) t->error = err;
+                for (Rec *b : job.blocks) give_block(t, b);  // not written: back to the pool
+            }
+            t->spilling = false;
+        }
+        t->cv.notify_all();
+    }
 }
 
 // Routes n records to their shards' blocks: a count pass and a scatter pass
@@ -296,7 +346,11 @@ bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
             at += cnt[w][s];
         }
         while (sh.blocks.size() * kBlockRecords < at) {
-            Rec *b = take_block(t);
+            Rec *b;
+            {
+                std::lock_guard<std::mutex> lk(t->mu);
+                b = take_block(t);
+            }
             if (!b) {
                 err = "TierLift: host block allocation failed";
                 return false;
@@ -320,7 +374,58 @@ bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
     return true;
 }
 
-bool over_budget(const tessa_tierlift *t) { return t->blocks_in_use * kBlockBytes > t->cfg.host_budget_bytes; }
+// After a batch is routed: a shard past the ones the expected stream leaves
+// room for goes to the spill thread once it has kEagerSpillBlocks blocks;
+// past 7/8 of the budget the biggest shard does (one job at a time) and
+// routing goes on; past the budget itself the worker waits for the spill to
+// return blocks.
+bool keep_budget(tessa_tierlift *t, std::string &err) {
+    const uint64_t hard = t->cfg.host_budget_bytes, soft = hard - hard / 8;
+    std::unique_lock<std::mutex> lk(t->mu);
+    if (!t->dir.empty() && t->keep_shards < t->shards && t->jobs.empty() && !t->spilling) {
+        uint32_t big = t->keep_shards;
+        for (uint32_t s = big + 1; s < t->shards; ++s)
+            if (t->shard[s].n > t->shard[big].n) big = s;
+        Shard &sh = t->shard[big];
+        if (sh.n >= kEagerSpillBlocks * kBlockRecords) {
+            t->jobs.push_back(SpillJob{big, std::move(sh.blocks), sh.n});
+            sh.blocks.clear();
+            sh.n = 0;
+            t->cv.notify_all();
+        }
+    }
+    for (;;) {
+        const uint64_t used = t->blocks_in_use * kBlockBytes;
+        if (!t->error.empty()) {
+            err = t->error;
+            return false;
+        }
+        if (used <= soft) return true;
+        if (t->dir.empty()) {
+            if (used <= hard) return true;
+            char m[240];
+            snprintf(m, sizeof(m),
+                     "TierLift host budget of %llu bytes exceeded and no spill path given "
+                     "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
+                     (unsigned long long)hard, (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
+            err = m;
+            return false;
+        }
+        if (t->jobs.empty() && !t->spilling) {
+            uint32_t big = 0;
+            for (uint32_t s = 1; s < t->shards; ++s)
+                if (t->shard[s].n > t->shard[big].n) big = s;
+            Shard &sh = t->shard[big];
+            if (sh.n == 0) return true;  // everything buffered is being written
+            t->jobs.push_back(SpillJob{big, std::move(sh.blocks), sh.n});
+            sh.blocks.clear();
+            sh.n = 0;
+            t->cv.notify_all();
+        }
+        if (used <= hard) return true;
+        t->cv.wait(lk);
+    }
+}
 
 void worker_main(tessa_tierlift *t) {
     (void)hipSetDevice(t->device);
@@ -343,26 +448,10 @@ void worker_main(tessa_tierlift *t) {
         if (clean) {
             std::string err;
             ok = route(t, t->pinned[slot], t->slot_n[slot], err);
-            while (ok && over_budget(t)) {
-                if (t->dir.empty()) {
-                    char m[240];
-                    snprintf(m, sizeof(m),
-                             "TierLift host budget of %llu bytes exceeded and no spill path given "
-                             "overflow_flags=0x%llx overflow_labels=WORKSPACE_BUDGET",
-                             (unsigned long long)t->cfg.host_budget_bytes,
-                             (unsigned long long)TESSA_OVF_WORKSPACE_BUDGET);
-                    err = m;
-                    ok = false;
-                    break;
-                }
-                uint32_t big = 0;
-                for (uint32_t s = 1; s < t->shards; ++s)
-                    if (t->shard[s].n > t->shard[big].n) big = s;
-                ok = spill_shard(t, big, err);
-            }
+            if (ok) ok = keep_budget(t, err);
             if (!ok) {
                 std::lock_guard<std::mutex> lk(t->mu);
-                t->error = err;
+                if (t->error.empty()) t->error = err;
             }
         }
         {
@@ -372,28 +461,6 @@ void worker_main(tessa_tierlift *t) {
         t->cv.notify_all();
         slot ^= 1;
     }
-}
-
-// Copies n records from host memory (pageable) to dev through the pinned
-// slots (alternating; a slot is refilled after its previous H2D finished),
-// the memcpy split over the worker threads.
-bool upload(tessa_tierlift *t, const Rec *src, uint64_t n, uint4 *dev, hipStream_t hs, int &slot) {
-    const uint64_t cap = t->cfg.staging_records;
-    for (uint64_t a = 0; a < n; a += cap) {
-        const uint64_t m = std::min<uint64_t>(cap, n - a);
-        if (hipEventSynchronize(t->copied[slot]) != hipSuccess) return false;
-        Rec *dst = t->pinned[slot];
-        const uint32_t T = m < (1u << 18) ? 1u : t->threads;
-        parallel_for(T, [&](uint32_t w) {
-            const uint64_t x = m * w / T, y = m * (w + 1) / T;
-            std::memcpy(dst + x, src + a + x, (y - x) * sizeof(Rec));
-        });
-        if (hipMemcpyAsync(dev + a, dst, m * sizeof(Rec), hipMemcpyHostToDevice, hs) != hipSuccess ||
-            hipEventRecord(t->copied[slot], hs) != hipSuccess)
-            return false;
-        slot ^= 1;
-    }
-    return true;
 }
 
 }  // namespace
@@ -426,6 +493,12 @@ tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierl
         t->stem = name.empty() ? std::string("candidate") : name;
     }
     t->shard.resize(t->shards);
+    // the shards a stream of expected_records leaves room for (7/8 of the budget)
+    t->keep_shards = t->shards;
+    const uint64_t expect_bytes = cfg->expected_records * sizeof(Rec);
+    const uint64_t soft = cfg->host_budget_bytes - cfg->host_budget_bytes / 8;
+    if (expect_bytes > soft)
+        t->keep_shards = (uint32_t)((double)t->shards * (double)soft / (double)expect_bytes);
     bool ok = hipGetDevice(&t->device) == hipSuccess &&
               hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking) == hipSuccess;
     for (int i = 0; ok && i < 2; ++i)
@@ -440,6 +513,7 @@ tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierl
     t->stats.shards = t->shards;
     t->stats.threads = t->threads;
     t->worker = std::thread(worker_main, t);
+    t->spiller = std::thread(spiller_main, t);
     *out = t;
     return tessa_status{};
 }
@@ -503,7 +577,8 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
     if (t->finished) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "tierlift: finish called twice");
     {
         std::unique_lock<std::mutex> lk(t->mu);
-        t->cv.wait(lk, [&] { return !t->slot_full[0] && !t->slot_full[1]; });
+        t->cv.wait(lk, [&] { return (!t->slot_full[0] && !t->slot_full[1] && t->jobs.empty() && !t->spilling) ||
+                                    !t->error.empty(); });
         if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
     }
     t->finished = true;  // the worker is idle from here on; no push is accepted
@@ -527,40 +602,68 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
             return tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: writing %s failed", mpath.c_str());
     }
     hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    hipStream_t cs = t->copy_stream;  // idle now: the H2D side of the pipeline
     const uint32_t sp = (uint32_t)std::min<uint64_t>(t->cfg.shard_points, t->cfg.num_points);
     tessa_hashprune *hp = nullptr;
     tessa_status st = tessa_hashprune_create(sp, t->cfg.l_max, &hp);
     if (st.code) return st;
-    uint4 *dev = nullptr;
+    // two device buffers: the copy stream fills one while the caller's stream
+    // merges the other; up[b] marks buffer b filled, merged[b] merged
+    uint4 *dev[2] = {nullptr, nullptr};
+    hipEvent_t up[2] = {nullptr, nullptr}, merged[2] = {nullptr, nullptr};
     uint32_t *t_tmp = nullptr, *c_tmp = nullptr;
     const uint64_t dev_cap = std::max<uint64_t>(kUploadRecords, t->cfg.staging_records);
-    if (hipMalloc(&dev, dev_cap * sizeof(Rec)) != hipSuccess ||
-        hipMalloc(&t_tmp, (uint64_t)sp * t->cfg.l_max * 4) != hipSuccess ||
-        hipMalloc(&c_tmp, (uint64_t)sp * 4) != hipSuccess)
-        st = tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: reduction buffers (%llu records) failed",
+    bool ok = hipMalloc(&dev[0], dev_cap * sizeof(Rec)) == hipSuccess &&
+              hipMalloc(&dev[1], dev_cap * sizeof(Rec)) == hipSuccess &&
+              hipMalloc(&t_tmp, (uint64_t)sp * t->cfg.l_max * 4) == hipSuccess &&
+              hipMalloc(&c_tmp, (uint64_t)sp * 4) == hipSuccess;
+    for (int i = 0; ok && i < 2; ++i)
+        ok = hipEventCreateWithFlags(&up[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&merged[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventRecord(merged[i], hs) == hipSuccess && hipEventRecord(t->copied[i], cs) == hipSuccess;
+    if (!ok)
+        st = tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: reduction buffers (2 x %llu records) failed",
                        (unsigned long long)dev_cap);
-    int slot = 0;
-    // the pinned slots' events now track H2D copies on hs
-    for (int i = 0; i < 2 && !st.code; ++i)
-        if (hipEventRecord(t->copied[i], hs) != hipSuccess) st = tl_status(TESSA_ERR_HIP, "tierlift: event failed");
-    std::vector<Rec> seg_buf;
+    int slot = 0, cur = 0;
+    uint64_t fill = 0;
     size_t seg = 0;
+    // buffer cur may be filled once its previous merge is done
+    if (!st.code && hipStreamWaitEvent(cs, merged[cur], 0) != hipSuccess)
+        st = tl_status(TESSA_ERR_HIP, "tierlift: stream wait failed");
     for (uint32_t s = 0; s < t->shards && !st.code; ++s) {
         const uint32_t lo = (uint32_t)((uint64_t)s * t->cfg.shard_points);
         const uint32_t n_s = (uint32_t)std::min<uint64_t>(t->cfg.shard_points, t->cfg.num_points - lo);
-        uint64_t fill = 0;
+        // the filled part of buffer cur to the reservoirs (records routed to
+        // this shard are in range: no read-back of the range check)
         auto merge = [&]() -> tessa_status {
             if (!fill) return tessa_status{};
-            hipLaunchKernelGGL(rebase_src_kernel, dim3((uint32_t)((fill + 255) / 256)), dim3(256), 0, hs, dev, fill, lo);
-            tessa_status s2 = tessa_hashprune_insert(hp, reinterpret_cast<const tessa_edge_record *>(dev), fill, stream);
+            if (hipEventRecord(up[cur], cs) != hipSuccess || hipStreamWaitEvent(hs, up[cur], 0) != hipSuccess)
+                return tl_status(TESSA_ERR_HIP, "tierlift: event failed");
+            hipLaunchKernelGGL(rebase_src_kernel, dim3((uint32_t)((fill + 255) / 256)), dim3(256), 0, hs, dev[cur],
+                               fill, lo);
+            tessa_status s2 = tessa::hashprune_insert_async(hp, reinterpret_cast<const tessa_edge_record *>(dev[cur]),
+                                                            fill, hs);
+            if (s2.code) return s2;
+            if (hipEventRecord(merged[cur], hs) != hipSuccess) return tl_status(TESSA_ERR_HIP, "tierlift: event failed");
+            cur ^= 1;
             fill = 0;
-            return s2;
+            if (hipStreamWaitEvent(cs, merged[cur], 0) != hipSuccess)
+                return tl_status(TESSA_ERR_HIP, "tierlift: stream wait failed");
+            return tessa_status{};
         };
-        auto add = [&](const Rec *src, uint64_t n) -> tessa_status {
+        // m records into pinned slot `slot` by fill_slot(dst), then H2D into buffer cur
+        auto add = [&](uint64_t n, auto &&fill_slot) -> tessa_status {
             for (uint64_t a = 0; a < n;) {
-                const uint64_t m = std::min<uint64_t>(dev_cap - fill, n - a);
-                if (!upload(t, src + a, m, dev + fill, hs, slot))
+                const uint64_t m = std::min<uint64_t>({t->cfg.staging_records, dev_cap - fill, n - a});
+                if (hipEventSynchronize(t->copied[slot]) != hipSuccess)
                     return tl_status(TESSA_ERR_HIP, "tierlift: H2D of shard %u records failed", s);
+                if (!fill_slot(t->pinned[slot], a, m))
+                    return tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: short read of a segment of shard %u", s);
+                if (hipMemcpyAsync(dev[cur] + fill, t->pinned[slot], m * sizeof(Rec), hipMemcpyHostToDevice, cs) !=
+                        hipSuccess ||
+                    hipEventRecord(t->copied[slot], cs) != hipSuccess)
+                    return tl_status(TESSA_ERR_HIP, "tierlift: H2D of shard %u records failed", s);
+                slot ^= 1;
                 fill += m;
                 a += m;
                 if (fill == dev_cap) {
@@ -571,7 +674,8 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
             return tessa_status{};
         };
         st = tessa_hashprune_clear(hp, stream);
-        // spilled segments of this shard (manifest order), then its buffered blocks
+        // spilled segments of this shard (manifest order), read into the
+        // pinned slots, then its buffered blocks
         for (; !st.code && seg < t->segments.size() && t->segments[seg].shard == s; ++seg) {
             const Segment &g = t->segments[seg];
             const std::string path = part_path(t, g.shard, g.file);
@@ -580,28 +684,43 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
                 st = tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: cannot reopen %s", path.c_str());
                 break;
             }
-            // seg_buf is read by in-flight H2D copies only through the pinned slots
-            seg_buf.resize(g.records);
-            char *p = reinterpret_cast<char *>(seg_buf.data());
-            uint64_t left = g.bytes, off = g.offset;
-            while (left) {
-                const ssize_t r = pread(fd, p, left, (off_t)off);
-                if (r <= 0) break;
-                p += r;
-                off += (uint64_t)r;
-                left -= (uint64_t)r;
-            }
+            st = add(g.records, [&](Rec *dst, uint64_t a, uint64_t m) {
+                const uint32_t T = m < (1u << 16) ? 1u : t->threads;
+                std::vector<char> bad(T, 0);
+                parallel_for(T, [&](uint32_t w) {
+                    const uint64_t x = m * w / T, y = m * (w + 1) / T;
+                    char *p = reinterpret_cast<char *>(dst + x);
+                    uint64_t left = (y - x) * sizeof(Rec), off = g.offset + (a + x) * sizeof(Rec);
+                    while (left) {
+                        const ssize_t r = pread(fd, p, left, (off_t)off);
+                        if (r <= 0) {
+                            bad[w] = 1;
+                            return;
+                        }
+                        p += r;
+                        off += (uint64_t)r;
+                        left -= (uint64_t)r;
+                    }
+                });
+                for (char b : bad)
+                    if (b) return false;
+                return true;
+            });
             close(fd);
-            if (left) {
-                st = tl_status(TESSA_ERR_INVALID_ARGUMENT, "TierLift spill: short read of a segment of %s", path.c_str());
-                break;
-            }
             t->stats.reread_records += g.records;
-            st = add(seg_buf.data(), g.records);
         }
         Shard &sh = t->shard[s];
-        for (size_t b = 0; b < sh.blocks.size() && !st.code; ++b)
-            st = add(sh.blocks[b], std::min<uint64_t>(kBlockRecords, sh.n - b * kBlockRecords));
+        for (size_t b = 0; b < sh.blocks.size() && !st.code; ++b) {
+            const Rec *src = sh.blocks[b];
+            st = add(std::min<uint64_t>(kBlockRecords, sh.n - b * kBlockRecords), [&](Rec *dst, uint64_t a, uint64_t m) {
+                const uint32_t T = m < (1u << 18) ? 1u : t->threads;
+                parallel_for(T, [&](uint32_t w) {
+                    const uint64_t x = m * w / T, y = m * (w + 1) / T;
+                    std::memcpy(dst + x, src + a + x, (y - x) * sizeof(Rec));
+                });
+                return true;
+            });
+        }
         if (!st.code) st = merge();
         if (!st.code) st = tessa_hashprune_neighbors(hp, t_tmp, nullptr, nullptr, c_tmp, stream);
         if (!st.code &&
@@ -609,13 +728,22 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
                             hipMemcpyDeviceToDevice, hs) != hipSuccess ||
              hipMemcpyAsync(counts + lo, c_tmp, (uint64_t)n_s * 4, hipMemcpyDeviceToDevice, hs) != hipSuccess))
             st = tl_status(TESSA_ERR_HIP, "tierlift: shard export copy failed");
-        if (!st.code && hipStreamSynchronize(hs) != hipSuccess) st = tl_status(TESSA_ERR_HIP, "tierlift: sync failed");
-        for (Rec *b : sh.blocks) give_block(t, b);
+        // the blocks were copied into the pinned slots on the host: free now
+        {
+            std::lock_guard<std::mutex> lk(t->mu);
+            for (Rec *b : sh.blocks) give_block(t, b);
+        }
         sh.blocks.clear();
         sh.n = 0;
     }
+    if (!st.code && hipStreamSynchronize(hs) != hipSuccess) st = tl_status(TESSA_ERR_HIP, "tierlift: sync failed");
     (void)hipStreamSynchronize(hs);
-    if (dev) (void)hipFree(dev);
+    (void)hipStreamSynchronize(cs);
+    for (int i = 0; i < 2; ++i) {
+        if (dev[i]) (void)hipFree(dev[i]);
+        if (up[i]) (void)hipEventDestroy(up[i]);
+        if (merged[i]) (void)hipEventDestroy(merged[i]);
+    }
     if (t_tmp) (void)hipFree(t_tmp);
     if (c_tmp) (void)hipFree(c_tmp);
     tessa_hashprune_destroy(hp);
@@ -629,14 +757,13 @@ tessa_status tessa_tierlift_finish(tessa_tierlift *t, uint32_t *targets, uint32_
 
 tessa_status tessa_tierlift_destroy(tessa_tierlift *t) {
     if (!t) return tessa_status{};
-    if (t->worker.joinable()) {
-        {
-            std::lock_guard<std::mutex> lk(t->mu);
-            t->stopping = true;
-        }
-        t->cv.notify_all();
-        t->worker.join();
+    {
+        std::lock_guard<std::mutex> lk(t->mu);
+        t->stopping = true;
     }
+    t->cv.notify_all();
+    if (t->worker.joinable()) t->worker.join();
+    if (t->spiller.joinable()) t->spiller.join();
     for (Shard &sh : t->shard) {
         if (sh.fd >= 0) close(sh.fd);
         for (Rec *b : sh.blocks) std::free(b);

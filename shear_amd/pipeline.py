@@ -268,6 +268,10 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     sess = S.SubtreeSession(0)
     hp = tl = None
     if host_reducer is not None:
+        if not host_reducer.expected_records:
+            # each point in about fanout_top * fanout_second leaves, 2 * k records per leaf row
+            host_reducer = replace(host_reducer, expected_records=rows * 2 * p.leaf_knn * max(p.fanout_top, 1)
+                                   * max(p.fanout_second, 1))
         tl = TL.TierLiftReducer(rows, p.l_max, host_reducer, dev)
     else:
         hp = H.HashPruneReducer(rows, p.l_max, dev, p.hashprune_backfill)

@@ -33,6 +33,7 @@ class TierLiftParams:
     shard_points: int = DEFAULT_SHARD_POINTS
     staging_records: int = DEFAULT_STAGING_RECORDS
     threads: int = 0                     # host threads for routing and spill sorting (0: up to 16)
+    expected_records: int = 0            # about how many records will be pushed (0: unknown)
 
 
 class TierLiftReducer:
@@ -46,7 +47,8 @@ class TierLiftReducer:
         self._lib = N.load()
         self._base = params.spill_base.encode() if params.spill_base else None
         cfg = N.TierLiftConfig(self.num_points, int(params.shard_points), int(params.host_budget_bytes),
-                               int(params.staging_records), self._base, self.l_max, int(params.threads))
+                               int(params.staging_records), self._base, self.l_max, int(params.threads),
+                               int(params.expected_records))
         h = C.c_void_p()
         with torch.cuda.device(self.device):
             N.check(self._lib.tessa_tierlift_create(C.byref(cfg), C.byref(h)), "tierlift create")
