@@ -663,14 +663,18 @@ tessa_status tessa_hashprune_create_backfill(uint32_t num_points, uint32_t l_max
  *            default is 1,000,000), l_max in [1, 256], staging_records per
  *            pinned slot (two slots), threads for host routing / spill sorting
  *            (0: up to 16);
- *   push     device records (count of them) produced on `stream`: enqueues
- *            their D2H copy on the reducer's own stream after the work
- *            already on `stream`, never making `stream` wait; blocks only
- *            while both staging slots are still being routed; *seq_out = the
+ *   push     device records (count of them) produced on `stream`: enqueues,
+ *            on the reducer's own stream after the work already on `stream`
+ *            (never making `stream` wait), a sort of the batch by (src, dst)
+ *            that drops exact repeats of a record (the same pair seen forward
+ *            and reverse; a reservoir ignores a repeat, so the reduction is
+ *            unchanged) and the D2H copy of what is kept; blocks only while
+ *            both staging slots are still being routed; *seq_out = the
  *            sequence number of the batch's last slot;
- *   copied   *seq = the highest sequence number whose copy has completed (the
- *            device records of every push up to it may be reused);
- *   wait     blocks until batch `seq` has been copied;
+ *   copied   *seq = the highest sequence number whose batch has been read
+ *            on the device (the device records of every push up to it may be
+ *            reused);
+ *   wait     blocks until batch `seq` has been read;
  *   finish   writes the manifest, then reduces shard by shard on the device
  *            (spilled segments, then buffered records, through HashPrune
  *            reservoirs as tessa_hashprune_*) into targets [num_points * l_max]
@@ -711,8 +715,9 @@ typedef struct tessa_tierlift_stats {
     uint32_t shards;
     uint32_t threads;
     double route_s;               /* worker time routing records to shards */
-    double spill_s;               /* worker time sorting and writing segments */
+    double spill_s;               /* spill-thread time sorting and writing segments */
     double reduce_s;              /* finish: manifest, uploads, reservoir merges */
+    uint64_t unique_records;      /* records kept after dropping exact repeats within each batch */
 } tessa_tierlift_stats;
 tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierlift **out);
 tessa_status tessa_tierlift_push(tessa_tierlift *t, const tessa_edge_record *records, uint64_t count, void *stream,

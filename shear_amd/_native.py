@@ -305,7 +305,7 @@ class TierLiftStats(C.Structure):
     _fields_ = [(f, C.c_uint64) for f in ("records", "pushes", "host_peak_bytes", "spilled_records",
                                           "spilled_bytes", "segments", "reread_records")] + [
         ("shards", C.c_uint32), ("threads", C.c_uint32), ("route_s", C.c_double), ("spill_s", C.c_double),
-        ("reduce_s", C.c_double)]
+        ("reduce_s", C.c_double), ("unique_records", C.c_uint64)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}

@@ -7,11 +7,14 @@
 // :853-892).
 //
 //   push     the caller's stream records an event; a side stream (default
-//            priority) waits on it and copies the batch into one of two pinned
-//            staging slots, so leaf compute goes on while a slot drains;
-//   worker   a host thread takes the slots in order and routes their records
-//            to source-range shards (src / shard_points) with several
-//            threads, into per-shard blocks of 1,000,000 records;
+//            priority) waits on it, sorts the batch by (src, dst) on the
+//            device and drops exact repeats of a record (the same pair seen
+//            forward and reverse in one batch: a reservoir ignores a repeat),
+//            so leaf compute goes on while a slot drains;
+//   worker   a host thread takes the slots in order, copies each batch's
+//            records into its pinned staging slot and appends each shard's run
+//            (the batch is in source order, src / shard_points) to that
+//            shard's blocks of 1,000,000 records, shards in parallel;
 //   spill    past 7/8 of the host budget the worker hands the shard with the
 //            most buffered records to a spill thread and goes on routing (it
 //            waits only past the budget itself): each of the shard's blocks
@@ -30,6 +33,7 @@
 // backfill and evidence policies off), so the table equals one in-HBM
 // reduction of the same records, whatever was spilled.
 #include <fcntl.h>
+#include <sys/mman.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -44,6 +48,8 @@
 #include <string>
 #include <thread>
 #include <vector>
+
+#include <hipcub/hipcub.hpp>
 
 #include "hashprune_kernels.h"
 #include "tessa_device.h"
@@ -64,6 +70,8 @@ static_assert(sizeof(Rec) == 16, "SpillRecord16");
 
 constexpr uint64_t kBlockRecords = 1000000;                   // segment cap, spill_hashprune.rs:25,:500-505
 constexpr uint64_t kBlockBytes = kBlockRecords * sizeof(Rec);
+constexpr uint64_t kHugePage = 2ull << 20;
+constexpr uint64_t kBlockAlloc = (kBlockBytes + kHugePage - 1) / kHugePage * kHugePage;
 constexpr uint64_t kPartMaxBytes = 4ull * 1024 * 1024 * 1024;  // DEFAULT_PART_MAX_BYTES :27
 constexpr uint64_t kUploadRecords = 1ull << 26;               // records per reservoir merge at finish (1 GiB)
 constexpr uint64_t kCountingSortMaxShard = 1ull << 24;        // larger shards sort by comparison
@@ -83,12 +91,83 @@ struct Segment {
     uint32_t src_min, src_max;
 };
 
+// Per-slot device workspace of the batch sort (base 256-byte aligned).
+struct SlotWs {
+    uint64_t *keys_in, *keys_out, *vals_in, *vals_out;
+    uint4 *recs, *out;
+    uint8_t *flag;
+    unsigned long long *count;  // [0] kept records, [1] first bad record (index << 32 | src)
+    void *temp;
+};
+uint64_t ws_align(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+SlotWs slot_ws(void *base, uint64_t n) {
+    char *p = static_cast<char *>(base);
+    SlotWs w{};
+    uint64_t at = 0;
+    auto take = [&](uint64_t bytes) {
+        void *q = p + at;
+        at += ws_align(bytes);
+        return q;
+    };
+    w.keys_in = static_cast<uint64_t *>(take(n * 8));
+    w.keys_out = static_cast<uint64_t *>(take(n * 8));
+    w.vals_in = static_cast<uint64_t *>(take(n * 8));
+    w.vals_out = static_cast<uint64_t *>(take(n * 8));
+    w.recs = static_cast<uint4 *>(take(n * 16));
+    w.out = static_cast<uint4 *>(take(n * 16));
+    w.flag = static_cast<uint8_t *>(take(n));
+    w.count = static_cast<unsigned long long *>(take(16));
+    w.temp = p + at;
+    return w;
+}
+uint64_t slot_ws_fixed_bytes(uint64_t n) {
+    return 4 * ws_align(n * 8) + 2 * ws_align(n * 16) + ws_align(n) + ws_align(16);
+}
+size_t sort_temp_bytes(uint64_t n) {
+    size_t a = 0, b = 0;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, a, (const uint64_t *)nullptr, (uint64_t *)nullptr,
+                                             (const uint64_t *)nullptr, (uint64_t *)nullptr, (int)n, 0, 64);
+    (void)hipcub::DeviceSelect::Flagged(nullptr, b, (const uint4 *)nullptr, (const uint8_t *)nullptr, (uint4 *)nullptr,
+                                        (unsigned long long *)nullptr, (int)n);
+    return a > b ? a : b;
+}
+int key_bits_for(uint64_t num_points) {
+    int b = 1;
+    while (b < 32 && (1ull << b) < num_points) ++b;
+    return 32 + b;
+}
+
 // A shard's buffered records handed to the spill thread.
 struct SpillJob {
     uint32_t shard;
     std::vector<Rec *> blocks;
     uint64_t n;
 };
+
+// A batch as sort keys (src, dst) and values (hash, flags, dist).
+// A batch as sort keys (src, dst) and values (hash, flags, dist); *bad gets
+// the first record with src >= num_points as (index << 32 | src).
+__global__ void tl_keys_kernel(const uint4 *rec, uint64_t n, uint32_t num_points, uint64_t *keys, uint64_t *vals,
+                               unsigned long long *bad) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint4 r = rec[i];
+    keys[i] = ((uint64_t)r.x << 32) | r.y;
+    vals[i] = ((uint64_t)r.w << 32) | r.z;
+    if (r.x >= num_points) atomicMin(bad, (unsigned long long)((i << 32) | r.x));
+}
+
+__global__ void tl_init_kernel(unsigned long long *bad) { *bad = ~0ull; }
+
+// The sorted batch back as records; flag[i] marks a record that differs from
+// its predecessor (the first of a run of repeats).
+__global__ void tl_unkey_kernel(const uint64_t *keys, const uint64_t *vals, uint64_t n, uint4 *rec, uint8_t *flag) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i], v = vals[i];
+    rec[i] = make_uint4((uint32_t)(k >> 32), (uint32_t)k, (uint32_t)v, (uint32_t)(v >> 32));
+    flag[i] = i == 0 || keys[i - 1] != k || vals[i - 1] != v;
+}
 
 __global__ void rebase_src_kernel(uint4 *rec, uint64_t n, uint32_t lo) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -130,10 +209,15 @@ struct tessa_tierlift {
     uint32_t shards = 0;
     uint32_t threads = 1;
     std::string dir, stem;  // part files: dir/stem_shardSSSSS_partPPP.log
-    // D2H staging
-    hipStream_t copy_stream = nullptr;
+    // D2H staging: per slot the device sort buffers (keys and values in and
+    // out, the records in order, repeat flags, the kept records, their count,
+    // the sort / select temporary), the pinned host slot and its count
+    hipStream_t copy_stream = nullptr, d2h_stream = nullptr;
     Rec *pinned[2] = {nullptr, nullptr};
-    hipEvent_t ready[2] = {nullptr, nullptr}, copied[2] = {nullptr, nullptr};
+    uint64_t *pinned_count = nullptr;  // [2]
+    void *dev_ws[2] = {nullptr, nullptr};
+    size_t sort_temp_bytes = 0;
+    hipEvent_t ready[2] = {nullptr, nullptr}, counted[2] = {nullptr, nullptr}, copied[2] = {nullptr, nullptr};
     uint64_t slot_n[2] = {0, 0}, slot_seq[2] = {0, 0};
     bool slot_full[2] = {false, false};
     int next_slot = 0;
@@ -171,8 +255,12 @@ Rec *take_block(tessa_tierlift *t) {
         b = t->free_blocks.back();
         t->free_blocks.pop_back();
     } else {
-        b = static_cast<Rec *>(std::malloc(kBlockBytes));
-        if (!b) return nullptr;
+        // 2 MB aligned with huge pages: routing writes each new block once,
+        // and 4 KB first-touch faults would dominate that copy
+        void *q = nullptr;
+        if (posix_memalign(&q, kHugePage, kBlockAlloc) != 0 || !q) return nullptr;
+        (void)madvise(q, kBlockAlloc, MADV_HUGEPAGE);
+        b = static_cast<Rec *>(q);
         t->blocks_allocated += 1;
         t->stats.host_peak_bytes = std::max(t->stats.host_peak_bytes, t->blocks_allocated * kBlockBytes);
     }
@@ -303,49 +391,23 @@ void spiller_main(tessa_tierlift *t) {
     }
 }
 
-// Routes n records to their shards' blocks: a count pass and a scatter pass
-// over T threads, each thread's records placed after the previous thread's
-// (arrival order within a shard).
-bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
+// Appends a batch in source order to its shards: each shard's run (found by
+// binary search) goes after what the shard holds, shards over the threads.
+bool route_sorted(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
     const double t0 = now_s();
     const uint32_t S = t->shards;
     const uint64_t sp = t->cfg.shard_points;
-    const uint32_t T = n < (1u << 16) ? 1u : t->threads;
-    std::vector<std::vector<uint64_t>> cnt(T, std::vector<uint64_t>(S, 0));
-    std::vector<uint64_t> bad(T, ~0ull);
-    auto range = [&](uint32_t w, uint64_t &a, uint64_t &b) {
-        a = n * w / T;
-        b = n * (w + 1) / T;
-    };
-    parallel_for(T, [&](uint32_t w) {
-        uint64_t a, b;
-        range(w, a, b);
-        uint64_t *c = cnt[w].data();
-        for (uint64_t i = a; i < b; ++i) {
-            if (r[i].src >= t->cfg.num_points) {
-                bad[w] = std::min(bad[w], i);
-                continue;
-            }
-            c[r[i].src / sp] += 1;
-        }
-    });
-    for (uint32_t w = 0; w < T; ++w)
-        if (bad[w] != ~0ull) {
-            char m[200];
-            snprintf(m, sizeof(m), "Spill reducer encountered edge p=%u outside shard range [0, %llu)", r[bad[w]].src,
-                     (unsigned long long)t->cfg.num_points);
-            err = m;
-            return false;
-        }
-    std::vector<std::vector<uint64_t>> pos(T, std::vector<uint64_t>(S, 0));
+    std::vector<uint64_t> first(S + 1), at(S);
+    for (uint32_t s = 0; s < S; ++s) {
+        const uint64_t lo = (uint64_t)s * sp;
+        first[s] = (uint64_t)(std::lower_bound(r, r + n, lo, [](const Rec &a, uint64_t v) { return a.src < v; }) - r);
+    }
+    first[S] = n;
     for (uint32_t s = 0; s < S; ++s) {
         Shard &sh = t->shard[s];
-        uint64_t at = sh.n;
-        for (uint32_t w = 0; w < T; ++w) {
-            pos[w][s] = at;
-            at += cnt[w][s];
-        }
-        while (sh.blocks.size() * kBlockRecords < at) {
+        at[s] = sh.n;
+        const uint64_t need = sh.n + (first[s + 1] - first[s]);
+        while (sh.blocks.size() * kBlockRecords < need) {
             Rec *b;
             {
                 std::lock_guard<std::mutex> lk(t->mu);
@@ -357,19 +419,22 @@ bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
             }
             sh.blocks.push_back(b);
         }
-        sh.n = at;
+        sh.n = need;
     }
+    const uint32_t T = n < (1u << 16) ? 1u : std::min<uint32_t>(t->threads, S);
     parallel_for(T, [&](uint32_t w) {
-        uint64_t a, b;
-        range(w, a, b);
-        uint64_t *p = pos[w].data();
-        for (uint64_t i = a; i < b; ++i) {
-            const uint32_t s = (uint32_t)(r[i].src / sp);
-            const uint64_t at = p[s]++;
-            t->shard[s].blocks[at / kBlockRecords][at % kBlockRecords] = r[i];
+        for (uint32_t s = w; s < S; s += T) {
+            Shard &sh = t->shard[s];
+            uint64_t pos = at[s];
+            for (uint64_t i = first[s]; i < first[s + 1];) {
+                const uint64_t off = pos % kBlockRecords;
+                const uint64_t m = std::min<uint64_t>(kBlockRecords - off, first[s + 1] - i);
+                std::memcpy(sh.blocks[pos / kBlockRecords] + off, r + i, m * sizeof(Rec));
+                pos += m;
+                i += m;
+            }
         }
     });
-    t->stats.records += n;
     t->stats.route_s += now_s() - t0;
     return true;
 }
@@ -382,6 +447,13 @@ bool route(tessa_tierlift *t, const Rec *r, uint64_t n, std::string &err) {
 bool keep_budget(tessa_tierlift *t, std::string &err) {
     const uint64_t hard = t->cfg.host_budget_bytes, soft = hard - hard / 8;
     std::unique_lock<std::mutex> lk(t->mu);
+    if (t->cfg.expected_records && t->stats.records) {
+        // the expected stream as the batches so far thin it (repeats dropped)
+        const double kept = (double)t->stats.unique_records / (double)t->stats.records;
+        const double bytes = (double)t->cfg.expected_records * kept * (double)sizeof(Rec);
+        t->keep_shards =
+            bytes > (double)soft ? (uint32_t)((double)t->shards * (double)soft / bytes) : t->shards;
+    }
     if (!t->dir.empty() && t->keep_shards < t->shards && t->jobs.empty() && !t->spilling) {
         uint32_t big = t->keep_shards;
         for (uint32_t s = big + 1; s < t->shards; ++s)
@@ -427,27 +499,69 @@ bool keep_budget(tessa_tierlift *t, std::string &err) {
     }
 }
 
+// The D2H copy of slot `slot`'s kept records, once its sort is done (waits
+// for it); false (with t->error set) on a failed sort or D2H, or an
+// out-of-range record.  Worker only.
+bool start_copy(tessa_tierlift *t, int slot, uint64_t &m) {
+    bool ok = hipEventSynchronize(t->counted[slot]) == hipSuccess;
+    m = t->pinned_count[2 * slot];
+    const uint64_t bad = t->pinned_count[2 * slot + 1];
+    {
+        std::lock_guard<std::mutex> lk(t->mu);
+        t->copied_seq = t->slot_seq[slot];  // the caller's records are read
+        if (!ok && t->error.empty()) t->error = "TierLift: sorting a record batch failed";
+        if (ok && bad != ~0ull && t->error.empty()) {
+            char msg[200];
+            snprintf(msg, sizeof(msg), "Spill reducer encountered edge p=%u outside shard range [0, %llu)",
+                     (uint32_t)bad, (unsigned long long)t->cfg.num_points);
+            t->error = msg;
+        }
+        ok = t->error.empty();
+    }
+    t->cv.notify_all();
+    if (!ok) return false;
+    const SlotWs w = slot_ws(t->dev_ws[slot], t->cfg.staging_records);
+    if (hipMemcpyAsync(t->pinned[slot], w.out, m * sizeof(Rec), hipMemcpyDeviceToHost, t->d2h_stream) != hipSuccess ||
+        hipEventRecord(t->copied[slot], t->d2h_stream) != hipSuccess) {
+        std::lock_guard<std::mutex> lk(t->mu);
+        if (t->error.empty()) t->error = "TierLift: D2H copy of a record batch failed";
+        return false;
+    }
+    return true;
+}
+
 void worker_main(tessa_tierlift *t) {
     (void)hipSetDevice(t->device);
     int slot = 0;
+    bool started[2] = {false, false};
+    uint64_t kept[2] = {0, 0};
     for (;;) {
         {
             std::unique_lock<std::mutex> lk(t->mu);
             t->cv.wait(lk, [&] { return t->slot_full[slot] || t->stopping; });
             if (!t->slot_full[slot]) return;
         }
-        bool ok = hipEventSynchronize(t->copied[slot]) == hipSuccess;
-        bool clean;
+        bool ok = started[slot] || start_copy(t, slot, kept[slot]);
+        started[slot] = false;
+        // the other slot's copy goes while this one is routed, if it is
+        // filled and sorted already
+        const int other = slot ^ 1;
+        bool other_full;
         {
             std::lock_guard<std::mutex> lk(t->mu);
-            t->copied_seq = t->slot_seq[slot];
-            if (!ok && t->error.empty()) t->error = "TierLift: D2H copy of a record batch failed";
-            clean = t->error.empty();
+            other_full = t->slot_full[other];
         }
-        t->cv.notify_all();
-        if (clean) {
+        if (ok && other_full && hipEventQuery(t->counted[other]) == hipSuccess)
+            started[other] = start_copy(t, other, kept[other]);
+        if (ok) {
             std::string err;
-            ok = route(t, t->pinned[slot], t->slot_n[slot], err);
+            ok = hipEventSynchronize(t->copied[slot]) == hipSuccess;
+            if (!ok) err = "TierLift: D2H copy of a record batch failed";
+            if (ok) {
+                t->stats.records += t->slot_n[slot];
+                t->stats.unique_records += kept[slot];
+                ok = route_sorted(t, t->pinned[slot], kept[slot], err);
+            }
             if (ok) ok = keep_budget(t, err);
             if (!ok) {
                 std::lock_guard<std::mutex> lk(t->mu);
@@ -499,16 +613,28 @@ tessa_status tessa_tierlift_create(const tessa_tierlift_config *cfg, tessa_tierl
     const uint64_t soft = cfg->host_budget_bytes - cfg->host_budget_bytes / 8;
     if (expect_bytes > soft)
         t->keep_shards = (uint32_t)((double)t->shards * (double)soft / (double)expect_bytes);
+    if (cfg->staging_records >= (1ull << 31)) {
+        delete t;
+        return tl_status(TESSA_ERR_UNSUPPORTED, "tierlift: staging_records %llu (limit 2^31-1)",
+                         (unsigned long long)cfg->staging_records);
+    }
+    t->sort_temp_bytes = sort_temp_bytes(cfg->staging_records);
+    const uint64_t ws_bytes = slot_ws_fixed_bytes(cfg->staging_records) + t->sort_temp_bytes;
     bool ok = hipGetDevice(&t->device) == hipSuccess &&
-              hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking) == hipSuccess;
+              hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking) == hipSuccess &&
+              hipStreamCreateWithFlags(&t->d2h_stream, hipStreamNonBlocking) == hipSuccess &&
+              hipHostMalloc((void **)&t->pinned_count, 4 * sizeof(uint64_t)) == hipSuccess;
     for (int i = 0; ok && i < 2; ++i)
         ok = hipHostMalloc((void **)&t->pinned[i], cfg->staging_records * sizeof(Rec)) == hipSuccess &&
+             hipMalloc(&t->dev_ws[i], ws_bytes) == hipSuccess &&
              hipEventCreateWithFlags(&t->ready[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&t->counted[i], hipEventDisableTiming) == hipSuccess &&
              hipEventCreateWithFlags(&t->copied[i], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         tessa_tierlift_destroy(t);
-        return tl_status(TESSA_ERR_OUT_OF_MEMORY, "tierlift: staging set-up (pinned 2 x %llu records) failed",
-                         (unsigned long long)cfg->staging_records);
+        return tl_status(TESSA_ERR_OUT_OF_MEMORY,
+                         "tierlift: staging set-up (pinned 2 x %llu records, device 2 x %llu bytes) failed",
+                         (unsigned long long)cfg->staging_records, (unsigned long long)ws_bytes);
     }
     t->stats.shards = t->shards;
     t->stats.threads = t->threads;
@@ -533,13 +659,35 @@ tessa_status tessa_tierlift_push(tessa_tierlift *t, const tessa_edge_record *rec
             t->cv.wait(lk, [&] { return !t->slot_full[slot] || !t->error.empty(); });
             if (!t->error.empty()) return tl_status(TESSA_ERR_INVALID_ARGUMENT, "%s", t->error.c_str());
         }
-        // the copy waits for the caller's stream; the caller's stream does not wait for the copy
-        if (hipEventRecord(t->ready[slot], s) != hipSuccess ||
-            hipStreamWaitEvent(t->copy_stream, t->ready[slot], 0) != hipSuccess ||
-            hipMemcpyAsync(t->pinned[slot], records + done, n * sizeof(Rec), hipMemcpyDeviceToHost, t->copy_stream) !=
-                hipSuccess ||
-            hipEventRecord(t->copied[slot], t->copy_stream) != hipSuccess)
-            return tl_status(TESSA_ERR_HIP, "tierlift: enqueueing the D2H copy failed");
+        // the side stream waits for the caller's stream (never the other
+        // way round), sorts the batch by (src, dst), drops repeats and
+        // copies the count of kept records (and the first out-of-range
+        // record) to the host
+        const SlotWs w = slot_ws(t->dev_ws[slot], t->cfg.staging_records);
+        hipStream_t cs = t->copy_stream;
+        const uint32_t grid = (uint32_t)((n + 255) / 256);
+        size_t tb = t->sort_temp_bytes;
+        bool ok = hipEventRecord(t->ready[slot], s) == hipSuccess &&
+                  hipStreamWaitEvent(cs, t->ready[slot], 0) == hipSuccess;
+        if (ok) {
+            hipLaunchKernelGGL(tl_init_kernel, dim3(1), dim3(1), 0, cs, w.count + 1);
+            hipLaunchKernelGGL(tl_keys_kernel, dim3(grid), dim3(256), 0, cs,
+                               reinterpret_cast<const uint4 *>(records + done), n, (uint32_t)t->cfg.num_points,
+                               w.keys_in, w.vals_in, w.count + 1);
+            ok = hipGetLastError() == hipSuccess &&
+                 hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.keys_in, w.keys_out, w.vals_in, w.vals_out, (int)n,
+                                                    0, key_bits_for(t->cfg.num_points), cs) == hipSuccess;
+        }
+        if (ok) {
+            hipLaunchKernelGGL(tl_unkey_kernel, dim3(grid), dim3(256), 0, cs, w.keys_out, w.vals_out, n, w.recs,
+                               w.flag);
+            tb = t->sort_temp_bytes;
+            ok = hipGetLastError() == hipSuccess &&
+                 hipcub::DeviceSelect::Flagged(w.temp, tb, w.recs, w.flag, w.out, w.count, (int)n, cs) == hipSuccess &&
+                 hipMemcpyAsync(t->pinned_count + 2 * slot, w.count, 16, hipMemcpyDeviceToHost, cs) == hipSuccess &&
+                 hipEventRecord(t->counted[slot], cs) == hipSuccess;
+        }
+        if (!ok) return tl_status(TESSA_ERR_HIP, "tierlift: enqueueing the batch sort and D2H failed");
         {
             std::lock_guard<std::mutex> lk(t->mu);
             t->slot_n[slot] = n;
@@ -770,13 +918,17 @@ tessa_status tessa_tierlift_destroy(tessa_tierlift *t) {
     }
     for (Rec *b : t->free_blocks) std::free(b);
     if (t->copy_stream) (void)hipStreamSynchronize(t->copy_stream);
+    if (t->d2h_stream) (void)hipStreamSynchronize(t->d2h_stream);
     for (int i = 0; i < 2; ++i) {
-        if (t->copied[i]) (void)hipEventSynchronize(t->copied[i]);
         if (t->pinned[i]) (void)hipHostFree(t->pinned[i]);
+        if (t->dev_ws[i]) (void)hipFree(t->dev_ws[i]);
         if (t->ready[i]) (void)hipEventDestroy(t->ready[i]);
+        if (t->counted[i]) (void)hipEventDestroy(t->counted[i]);
         if (t->copied[i]) (void)hipEventDestroy(t->copied[i]);
     }
+    if (t->pinned_count) (void)hipHostFree(t->pinned_count);
     if (t->copy_stream) (void)hipStreamDestroy(t->copy_stream);
+    if (t->d2h_stream) (void)hipStreamDestroy(t->d2h_stream);
     delete t;
     return tessa_status{};
 }

@@ -75,6 +75,7 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         "tessa_hashprune_backfill": (N.HashPruneBackfill, ["mode", "hash_quota", "max_backfill_per_row",
                                                            "soft_tier_priority_alpha"]),
         "tessa_tierlift_config": (N.TierLiftConfig, ["spill_base", "l_max", "threads", "expected_records"]),
+        "tessa_tierlift_stats": (N.TierLiftStats, ["shards", "threads", "route_s", "reduce_s", "unique_records"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for name, (_, fields) in specs.items():
