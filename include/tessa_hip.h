@@ -689,7 +689,7 @@ tessa_status tessa_hashprune_create_backfill(uint32_t num_points, uint32_t l_max
  * will not fit the budget, the shards beyond those that fit are spilled from
  * the start (whenever one has 256 MB buffered), so the disk writes overlap
  * the whole stream; the reduction is the same either way, only which records
- * sit in which part file differs. 
+ * sit in which part file differs.
  * A record with src >= num_points fails the push that carried it, and every
  * later call, with "Spill reducer encountered edge p=... outside shard
  * range". */
