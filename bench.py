@@ -277,7 +277,7 @@ class _LeafSampler:
     def __init__(self, calls=3):
         self.calls, self.seen, self.leaves = calls, 0, []
 
-    def __call__(self, tag, cg, out, lay, rec, cnt):
+    def __call__(self, tag, cg, out, lay, rec, cnt, segs=None, nseg=0):
         import numpy as np
 
         self.seen += 1
@@ -752,12 +752,14 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
                   gids=None, lay=None, out_ids=None, out_d=None):
     """HashPrune reservoirs (l_max 64, the reference default) over the step's
     edge records, empty reservoirs each time: (a) the build's path, the
-    records emitted in source-grouped order with one segment per row
-    (tessa_emit_edge_segments) and merged by segments in place
-    (tessa_hashprune_insert_segments); (b) the reference-order records merged
-    by tessa_hashprune_insert (records grouped by source with atomics).  The
-    points [0, sample_points) of (a) are checked bit for bit against the
-    oracle fed with their records, and (a) must equal (b) everywhere."""
+    records emitted in source-grouped order with one segment per row and the
+    repeats of mutual pairs left out (tessa_emit_edge_segments_unique), merged
+    by segments in place (tessa_hashprune_insert_segments); (a') the same with
+    every record (tessa_emit_edge_segments); (b) the reference-order records
+    merged by tessa_hashprune_insert (records grouped by source with atomics).
+    The points [0, sample_points) of (a) are checked bit for bit against the
+    oracle fed with all their records, and (a), (a') and (b) must be equal
+    everywhere."""
     import torch
 
     from shear_amd import edges as E
@@ -769,22 +771,30 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
     sketches = torch.randn((gids.numel(), 12), generator=gen, device=dev, dtype=torch.float32)
     grec = torch.empty_like(rec)
     segs = torch.empty((lay.output_len // K, 4), dtype=torch.int32, device=dev)
-    ms_emit, ms_seg, ms_rec = [], [], []
+    ms = {True: ([], []), False: ([], [])}
+    ms_rec = []
+    kept = {}
     with H.HashPruneReducer(num_points, l_max, dev) as hp:
-        for i in range(warmup + steps):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-            ev[0].record(stream)
-            _, gcount, _, nseg = E.emit_edge_segments(gids, lay, K, out_ids, out_d, sketches, 12, out=grec,
-                                                      segments=segs, stream=stream)
-            ev[1].record(stream)
-            hp.clear(stream=stream)
-            hp.insert_segments(grec, segs, nseg, stream=stream)
-            ev[2].record(stream)
-            ev[2].synchronize()
-            if i >= warmup:
-                ms_emit.append(ev[0].elapsed_time(ev[1]))
-                ms_seg.append(ev[1].elapsed_time(ev[2]))
+        for unique in (False, True):  # the build's path last: its reservoirs are read below
+            ms_emit, ms_seg = ms[unique]
+            for i in range(warmup + steps):
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+                ev[0].record(stream)
+                _, gcount, _, nseg = E.emit_edge_segments(gids, lay, K, out_ids, out_d, sketches, 12, out=grec,
+                                                          segments=segs, stream=stream, unique=unique)
+                ev[1].record(stream)
+                hp.clear(stream=stream)
+                hp.insert_segments(grec, segs, nseg, stream=stream)
+                ev[2].record(stream)
+                ev[2].synchronize()
+                if i >= warmup:
+                    ms_emit.append(ev[0].elapsed_time(ev[1]))
+                    ms_seg.append(ev[1].elapsed_time(ev[2]))
+            kept[unique] = gcount
+            if not unique:
+                ta, hsa, da, ca = hp.slots(stream=stream)
         t, hs, d, c = hp.slots(stream=stream)
+        ms_emit, ms_seg = ms[True]
         for i in range(warmup + steps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
@@ -796,7 +806,8 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
                 ms_rec.append(a.elapsed_time(b))
         t2, hs2, d2, c2 = hp.slots(stream=stream)
         stream.synchronize()
-        same = bool(torch.equal(c, c2) and torch.equal(t, t2) and torch.equal(d, d2) and torch.equal(hs, hs2))
+        same = bool(torch.equal(c, c2) and torch.equal(t, t2) and torch.equal(d, d2) and torch.equal(hs, hs2)
+                    and torch.equal(c, ca) and torch.equal(t, ta) and torch.equal(d, da) and torch.equal(hs, hsa))
         filled = int((c == l_max).sum().item())
         res = {}
         if check:
@@ -813,18 +824,20 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
             bad = np.nonzero((gc != wc) | np.any(gt != wt, 1) | np.any(gh != wh, 1) | np.any(gd != wd.view(np.uint32), 1))[0]
             res = {"points": sample_points, "records": int(len(sub)), "mismatched_points": int(len(bad)),
                    "bit_exact": len(bad) == 0}
-        del t, hs, d, c, t2, hs2, d2, c2
+        del t, hs, d, c, t2, hs2, d2, c2, ta, hsa, da, ca
     del sketches, grec, segs
     tm = float(np.mean(ms_seg)) / 1e3
     # algorithmic bytes: every record read once (16 B), every segment read
     # (16 B per row), each reservoir's slots written (10 B a slot) and its
     # count (4 B); the reservoirs start empty
     alg = gcount * 16 + nseg * 16 + num_points * (l_max * 10 + 4)
-    log(f"hashprune: {count} records -> {num_points} reservoirs, segments {np.mean(ms_seg):.3f} ms, "
-        f"records {np.mean(ms_rec):.3f} ms, identical {same}")
+    log(f"hashprune: {count} records ({gcount} without mutual repeats) -> {num_points} reservoirs, segments "
+        f"{np.mean(ms_seg):.3f} ms (all records {np.mean(ms[False][1]):.3f}), records {np.mean(ms_rec):.3f} ms, "
+        f"identical {same}")
     return {
         "kernels": "hp_seg_keys + radix sort + run-length encode + scan + hp_seg_gather + hp_merge_stream_kernel",
         "records": int(count),
+        "records_without_mutual_repeats": int(kept[True]),
         "segments": int(nseg),
         "points": int(num_points),
         "l_max": l_max,
@@ -835,6 +848,8 @@ def hashprune_leg(rec, count, num_points, stream, steps, warmup, check=True, l_m
         "hbm_gb_per_s_algorithmic": round(alg / tm / 1e9, 2),
         "peak_gb_per_s": HBM_PEAK_GBS,
         "grouped_emission_ms_mean": round(float(np.mean(ms_emit)), 4),
+        "all_records_merge_ms_mean": round(float(np.mean(ms[False][1])), 4),
+        "all_records_grouped_emission_ms_mean": round(float(np.mean(ms[False][0])), 4),
         "record_path_ms_mean": round(float(np.mean(ms_rec)), 4),
         "record_path_equal": same,
         "full_reservoirs": filled,

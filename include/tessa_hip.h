@@ -577,6 +577,23 @@ tessa_status tessa_emit_edge_segments(const uint32_t *global_ids, uint64_t resid
                                       tessa_edge_record *out, uint64_t out_capacity, tessa_edge_segment *segments,
                                       uint64_t segment_capacity, uint64_t *record_count, uint64_t *segment_count,
                                       void *stream);
+/* tessa_emit_edge_segments without the repeats of mutual pairs: when leaf
+ * row r names j and row j names r at the same distance, the reverse record
+ * of r's slot, (j -> r, compute_hash(s_j, s_r), d), is bit for bit j's
+ * forward record and is left out (and likewise for j's slot).  Per leaf the
+ * records written are the reference's multiset less those repeats: every
+ * distinct record is kept, so HashPrune reservoirs (whose state depends only
+ * on the set of records inserted) end the same.  The leaves take their
+ * places in `out` in completion order, without gaps; *record_count = the
+ * records written (the sum of the segment counts).  out_capacity must still
+ * cover 2 records per valid slot.  No counterpart in the reference (whose
+ * reservoirs see both copies and ignore the second). */
+tessa_status tessa_emit_edge_segments_unique(const uint32_t *global_ids, uint64_t resident_rows,
+                                             const tessa_leaf_batch *leaves, const uint32_t *topk_ids,
+                                             const float *topk_dists, const tessa_sketch_view *sketches,
+                                             tessa_edge_record *out, uint64_t out_capacity,
+                                             tessa_edge_segment *segments, uint64_t segment_capacity,
+                                             uint64_t *record_count, uint64_t *segment_count, void *stream);
 
 /* ---- HashPrune reservoirs: the consumer of the record stream ---------------
  * One HashPruneReservoir per point (hash_prune.rs:266-280, l_max slots, insert

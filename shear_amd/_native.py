@@ -370,6 +370,11 @@ SIGNATURES = {
         [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, _U64, C.POINTER(_U64),
          C.POINTER(_U64), _P],
     ),
+    "tessa_emit_edge_segments_unique": (
+        TessaStatus,
+        [_P, _U64, C.POINTER(LeafBatch), _P, _P, C.POINTER(SketchView), _P, _U64, _P, _U64, C.POINTER(_U64),
+         C.POINTER(_U64), _P],
+    ),
     "tessa_tierlift_create": (TessaStatus, [C.POINTER(TierLiftConfig), C.POINTER(_P)]),
     "tessa_tierlift_push": (TessaStatus, [_P, _P, _U64, _P, C.POINTER(_U64)]),
     "tessa_tierlift_copied": (TessaStatus, [_P, C.POINTER(_U64)]),

@@ -17,7 +17,8 @@ enum EdgeStatusWord : uint32_t {
     kEdgeFirstError = 1,   // smallest error key, UINT64_MAX when none (see edge_error_key)
     kEdgeCapacityHit = 2,  // 1 when out_capacity was too small (nothing written)
     kEdgeLeafTooLarge = 3, // 1 + largest leaf above max_leaf_rows (such leaves emit nothing)
-    kEdgeStatusWords = 4
+    kEdgeKept = 4,         // unique grouped order: records written (the leaves' cursor)
+    kEdgeStatusWords = 5
 };
 
 // Error keys order errors as the reference meets them: leaf by leaf, the
@@ -58,6 +59,11 @@ struct EdgeParams {
     uint4 *segments;
     uint64_t segment_capacity;
     uint64_t *leaf_seg_base;         // leaf_count + 1: first segment of each leaf, then the total
+    // Grouped order only: leave out the reverse record of a slot (r -> j)
+    // whose leaf row j lists r at the same distance (j's forward record is
+    // the same record); the leaves then take their places in the output from
+    // a cursor (status[kEdgeKept]) and the output has no gaps.
+    uint32_t unique;
 };
 
 // log2 of the LDS membership table size: >= 2 x max_leaf_rows, >= 64.

@@ -235,14 +235,79 @@ enum SketchMode : int {
     kSketchLds = 2        // the leaf's sketch rows staged in LDS (float4 reads)
 };
 
-// LDS words of the emit kernel: wave sums | row counts | member ids | table
-// keys | table values (u16) | (16-byte aligned) staged sketches.
-// Grouped order adds two arrays of max_rows words: per row its forward record
-// count and a cursor over its reverse records.
+// LDS words of the emit kernel: wave sums and the leaf's record base (two
+// words) | row counts | member ids | table keys | table values (u16) |
+// (16-byte aligned) staged sketches.  Grouped order adds two arrays of
+// max_rows words: per row its record count (then a cursor over its reverse
+// records) and the mask of its slots whose reverse record is left out.
 __host__ __device__ inline uint32_t emit_sketch_offset(uint32_t max_rows, uint32_t table_bits, bool grouped) {
-    const uint32_t words = kWaves + 2u * max_rows + (1u << table_bits) + (1u << table_bits) / 2u +
+    const uint32_t words = kWaves + 2u + 2u * max_rows + (1u << table_bits) + (1u << table_bits) / 2u +
                            (grouped ? 2u * max_rows : 0u);
     return (words + 3u) & ~3u;
+}
+
+// Largest finite distance among the kl <= k <= 32 slots of a top-k list from
+// slot index `slot0`; -1 when there is none.  An entry of the list lies at or
+// below it, so a slot whose distance exceeds it cannot be repeated there.
+__device__ __forceinline__ float list_max_dist(const EdgeParams &p, uint64_t slot0, uint32_t kl) {
+    const float *ds = p.topk_dists + slot0;
+    float m = -1.0f;
+    if ((p.k & 3u) == 0u && (reinterpret_cast<uintptr_t>(ds) & 15u) == 0u) {
+        const float4 *v = reinterpret_cast<const float4 *>(ds);
+        float4 x[8];
+#pragma unroll
+        for (uint32_t c = 0; c < 8u; ++c) {
+            x[c] = make_float4(-1.0f, -1.0f, -1.0f, -1.0f);
+            if (4u * c < kl) x[c] = v[c];
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < 8u; ++c) {
+            const uint32_t t = 4u * c;
+            const float e[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i)
+                if (t + i < kl && (__float_as_uint(e[i]) & 0x7f800000u) != 0x7f800000u) m = fmaxf(m, e[i]);
+        }
+    } else {
+        for (uint32_t t = 0; t < kl; ++t)
+            if ((__float_as_uint(ds[t]) & 0x7f800000u) != 0x7f800000u) m = fmaxf(m, ds[t]);
+    }
+    return m;
+}
+
+// Whether the top-k list of a leaf row (kl <= k <= 32 slots from slot index
+// `slot0`) names target g at distance bits db.  Then that row's forward
+// record is the record (row's id -> g, compute_hash(s_row, s_g), d) -- the
+// reverse record of g's slot naming the row, bit for bit (the distance of a
+// pair is symmetric: (rn + cn) and rs * cs commute exactly).  Ids are read
+// 16 bytes at a time when the list is aligned and k is a multiple of 4 (the
+// last 16 bytes then stay inside the row's k slots); only a matching id's
+// distance is read.
+__device__ __forceinline__ bool slot_listed(const EdgeParams &p, uint64_t slot0, uint32_t kl, uint32_t g,
+                                            uint32_t db) {
+    const uint32_t *ids = p.topk_ids + slot0;
+    uint32_t pos = kNoKey;
+    if ((p.k & 3u) == 0u && (reinterpret_cast<uintptr_t>(ids) & 15u) == 0u) {
+        const uint4 *v = reinterpret_cast<const uint4 *>(ids);
+        uint4 x[8];
+#pragma unroll
+        for (uint32_t c = 0; c < 8u; ++c) {
+            x[c] = make_uint4(kNoKey, kNoKey, kNoKey, kNoKey);
+            if (4u * c < kl) x[c] = v[c];
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < 8u; ++c) {
+            const uint32_t t = 4u * c;
+            if (x[c].x == g && t < kl) pos = t;
+            if (x[c].y == g && t + 1u < kl) pos = t + 1u;
+            if (x[c].z == g && t + 2u < kl) pos = t + 2u;
+            if (x[c].w == g && t + 3u < kl) pos = t + 3u;
+        }
+    } else {
+        for (uint32_t t = 0; t < kl; ++t)
+            if (ids[t] == g) pos = t;
+    }
+    return pos != kNoKey && __float_as_uint(p.topk_dists[slot0 + pos]) == db;
 }
 
 template <int kMode, bool kGrouped>
@@ -250,13 +315,13 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const uint32_t tbits = p.table_bits;
     const uint32_t tmask = (1u << tbits) - 1u;
-    uint32_t *wsum = lds;
-    uint32_t *cnt = lds + kWaves;
+    uint32_t *wsum = lds;  // kWaves sums, then the leaf's record base (lo, hi)
+    uint32_t *cnt = lds + kWaves + 2u;
     uint32_t *gid = cnt + p.max_leaf_rows;
     uint32_t *tkey = gid + p.max_leaf_rows;
     uint16_t *tval = reinterpret_cast<uint16_t *>(tkey + (1u << tbits));
-    uint32_t *fwd = tkey + (1u << tbits) + (1u << tbits) / 2u;  // grouped order only
-    uint32_t *rev = fwd + p.max_leaf_rows;
+    uint32_t *tot = tkey + (1u << tbits) + (1u << tbits) / 2u;  // grouped order only
+    uint32_t *dup = tot + p.max_leaf_rows;
     float *sk_lds = reinterpret_cast<float *>(lds + emit_sketch_offset(p.max_leaf_rows, tbits, kGrouped));
     const uint32_t mw = (p.m_bits + 3u) & ~3u;  // staged row stride (floats)
     const uint32_t tid = threadIdx.x;
@@ -278,9 +343,12 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
         // else counted again and scanned into cnt.
         const bool regular = (p.leaf_totals[leaf] & kLeafRegular) != 0u;
         if (kGrouped) {
+            // with p.unique, cnt holds each row's largest listed distance
+            // until the segment scan below overwrites it
+            const uint64_t o0 = p.output_offsets[leaf];
             for (uint32_t c = tid; c < n; c += kThreads) {
-                fwd[c] = 0u;
-                rev[c] = 0u;
+                tot[c] = 0u;
+                if (p.unique) cnt[c] = __float_as_uint(list_max_dist(p, o0 + (uint64_t)c * p.k, kl));
             }
             __syncthreads();
         } else if (regular) {
@@ -327,12 +395,15 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
         }
         __syncthreads();
         const uint64_t out0 = p.output_offsets[leaf];
-        const uint64_t rec0 = p.leaf_base[leaf];
+        uint64_t rec0 = p.leaf_base[leaf];
         constexpr uint32_t kStep = 2u * kWaves;
         if (kGrouped) {
             // Per member: its forward records (its valid slots) and its
             // reverse records (valid slots of other rows naming it); the
             // member's segment holds the forward ones, then the reverse ones.
+            // With p.unique a slot whose reverse record another row's forward
+            // record repeats (slot_listed) gets a bit in dup[row] and its
+            // reverse record is neither counted nor written.
             for (uint32_t r0 = 2u * wave + h; r0 < n + h; r0 += kStep * kEmitUnroll) {
                 uint32_t j[kEmitUnroll];
                 float d[kEmitUnroll];
@@ -352,26 +423,37 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                     const uint32_t r = r0 + u * kStep;
                     const bool valid = slot_valid(j[u], d[u]);
                     const uint64_t m = __ballot(valid);
-                    if (r < n && q == 0u) fwd[r] = (uint32_t)__popc((uint32_t)(h ? (m >> 32) : m));
+                    uint32_t cj = kNoKey;
                     if (valid) {
                         for (uint32_t slot = table_hash(j[u], tbits);; slot = (slot + 1u) & tmask) {
                             const uint32_t t = tkey[slot];
                             if (t == j[u]) {
-                                atomicAdd(&rev[tval[slot]], 1u);
+                                cj = tval[slot];
                                 break;
                             }
                             if (t == kNoKey) break;
                         }
                     }
+                    bool same = false;
+                    if (p.unique && cj != kNoKey && d[u] <= __uint_as_float(cnt[cj])) {
+                        const uint32_t gi = gid[r];  // r < n: the slot is valid
+                        if (gi != kNoKey) same = slot_listed(p, out0 + (uint64_t)cj * p.k, kl, gi, __float_as_uint(d[u]));
+                    }
+                    if (cj != kNoKey && !same) atomicAdd(&tot[cj], 1u);
+                    const uint64_t sm = __ballot(same);
+                    if (r < n && q == 0u) {
+                        atomicAdd(&tot[r], (uint32_t)__popc((uint32_t)(h ? (m >> 32) : m)));
+                        dup[r] = (uint32_t)(h ? (sm >> 32) : sm);
+                    }
                 }
             }
             __syncthreads();
-            // exclusive scan of fwd + rev into cnt (segment offsets in the leaf)
+            // exclusive scan of tot into cnt (segment offsets in the leaf)
             const uint32_t per = (n + kThreads - 1) / kThreads;
             const uint32_t b = tid * per;
             const uint32_t e = b + per < n ? b + per : n;
             uint32_t sum = 0;
-            for (uint32_t i = b; i < e; ++i) sum += fwd[i] + rev[i];
+            for (uint32_t i = b; i < e; ++i) sum += tot[i];
             uint32_t x = sum;
 #pragma unroll
             for (uint32_t off = 1; off < 64; off <<= 1) {
@@ -380,18 +462,33 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
             }
             if (lane == 63u) wsum[wave] = x;
             __syncthreads();
-            uint32_t base = 0;
+            uint32_t base = 0, leaf_total = 0;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) base += (uint32_t)w < wave ? wsum[w] : 0u;
+            for (int w = 0; w < kWaves; ++w) {
+                base += (uint32_t)w < wave ? wsum[w] : 0u;
+                leaf_total += wsum[w];
+            }
+            if (p.unique) {
+                // the leaf's place in the output: its records once the
+                // repeats are left out, taken from the batch's cursor
+                if (tid == 0) {
+                    const uint64_t at = atomicAdd((unsigned long long *)&p.status[kEdgeKept],
+                                                  (unsigned long long)leaf_total);
+                    wsum[kWaves] = (uint32_t)at;
+                    wsum[kWaves + 1] = (uint32_t)(at >> 32);
+                }
+                __syncthreads();
+                rec0 = (uint64_t)wsum[kWaves] | ((uint64_t)wsum[kWaves + 1] << 32);
+            }
             uint32_t run = base + x - sum;
             const uint64_t sbase = p.leaf_seg_base[leaf];
             for (uint32_t i = b; i < e; ++i) {
-                const uint32_t c = fwd[i] + rev[i];
+                const uint32_t c = tot[i];
                 cnt[i] = run;
                 const uint64_t first = rec0 + run;
                 p.segments[sbase + i] = make_uint4(gid[i], (uint32_t)first, (uint32_t)(first >> 32), c);
                 run += c;
-                rev[i] = run - rev[i];  // cursor: the first reverse record's place
+                tot[i] = run;  // cursor: reverse records fill the segment from its end
             }
             __syncthreads();
         }
@@ -455,11 +552,13 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                 if (kGrouped) {
                     if (ok) {
                         // forward: its place among the row's valid slots; reverse:
-                        // the next free place of j's segment
+                        // the last free place of j's segment
                         const uint32_t fpos = cnt[r] + (uint32_t)__popc(half & ((1u << q) - 1u));
-                        const uint32_t rpos = atomicAdd(&rev[cj], 1u);
                         store_record(p.out, rec0 + fpos, gi, j[u], hf, db);
-                        store_record(p.out, rec0 + rpos, j[u], gi, hr, db);
+                        if (((dup[r] >> q) & 1u) == 0u) {
+                            const uint32_t rpos = atomicSub(&tot[cj], 1u) - 1u;
+                            store_record(p.out, rec0 + rpos, j[u], gi, hr, db);
+                        }
                     }
                     (void)ok_mask;
                     (void)row_rec;

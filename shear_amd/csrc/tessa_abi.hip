@@ -1847,7 +1847,7 @@ static tessa_status emit_edge_records_impl(const uint32_t *global_ids, uint64_t 
                                            tessa_edge_record *out, uint64_t out_capacity,
                                            uint64_t *leaf_record_offsets, uint64_t *record_count,
                                            tessa_edge_segment *segments, uint64_t segment_capacity,
-                                           uint64_t *segment_count, void *stream) {
+                                           uint64_t *segment_count, bool unique, void *stream) {
     static_assert(sizeof(tessa_edge_record) == 16, "SpillRecord16 is 16 bytes");
     static_assert(sizeof(tessa_edge_segment) == 16, "segment descriptors are 16 bytes");
     if (record_count) *record_count = 0;
@@ -1910,6 +1910,7 @@ static tessa_status emit_edge_records_impl(const uint32_t *global_ids, uint64_t 
     p.segments = reinterpret_cast<uint4 *>(segments);
     p.segment_capacity = segments ? segment_capacity : 0;
     p.leaf_seg_base = segments ? ws->edge_seg_base : nullptr;
+    p.unique = segments && unique ? 1u : 0u;
     if (launch_edge_records(p, s) != 0) return make_status(TESSA_ERR_HIP, 0, "edge record kernel launch failed");
     uint64_t w[kEdgeStatusWords];
     TESSA_HIP_TRY(hipMemcpyAsync(w, p.status, sizeof(w), hipMemcpyDeviceToHost, s));
@@ -1960,7 +1961,7 @@ static tessa_status emit_edge_records_impl(const uint32_t *global_ids, uint64_t 
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge record capacity %llu below the %llu records needed",
                            (unsigned long long)p.out_capacity, (unsigned long long)w[kEdgeRecordCount]);
     }
-    *record_count = w[kEdgeRecordCount];
+    *record_count = p.unique ? w[kEdgeKept] : w[kEdgeRecordCount];
     return ok_status();
 }
 
@@ -1969,7 +1970,7 @@ tessa_status tessa_emit_edge_records(const uint32_t *global_ids, uint64_t reside
                                      const tessa_sketch_view *sk, tessa_edge_record *out, uint64_t out_capacity,
                                      uint64_t *leaf_record_offsets, uint64_t *record_count, void *stream) {
     return emit_edge_records_impl(global_ids, resident_rows, lb, topk_ids, topk_dists, sk, out, out_capacity,
-                                  leaf_record_offsets, record_count, nullptr, 0, nullptr, stream);
+                                  leaf_record_offsets, record_count, nullptr, 0, nullptr, false, stream);
 }
 
 tessa_status tessa_emit_edge_segments(const uint32_t *global_ids, uint64_t resident_rows, const tessa_leaf_batch *lb,
@@ -1980,7 +1981,19 @@ tessa_status tessa_emit_edge_segments(const uint32_t *global_ids, uint64_t resid
     if (!segments || !segment_count)
         return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge segments: null segment output");
     return emit_edge_records_impl(global_ids, resident_rows, lb, topk_ids, topk_dists, sk, out, out_capacity, nullptr,
-                                  record_count, segments, segment_capacity, segment_count, stream);
+                                  record_count, segments, segment_capacity, segment_count, false, stream);
+}
+
+tessa_status tessa_emit_edge_segments_unique(const uint32_t *global_ids, uint64_t resident_rows,
+                                             const tessa_leaf_batch *lb, const uint32_t *topk_ids,
+                                             const float *topk_dists, const tessa_sketch_view *sk,
+                                             tessa_edge_record *out, uint64_t out_capacity,
+                                             tessa_edge_segment *segments, uint64_t segment_capacity,
+                                             uint64_t *record_count, uint64_t *segment_count, void *stream) {
+    if (!segments || !segment_count)
+        return make_status(TESSA_ERR_INVALID_ARGUMENT, 0, "edge segments: null segment output");
+    return emit_edge_records_impl(global_ids, resident_rows, lb, topk_ids, topk_dists, sk, out, out_capacity, nullptr,
+                                  record_count, segments, segment_capacity, segment_count, true, stream);
 }
 
 }  // extern "C"

@@ -66,11 +66,17 @@ def emit_edge_records(global_ids: torch.Tensor, layouts: LeafLayouts, k: int, to
 def emit_edge_segments(global_ids: torch.Tensor, layouts: LeafLayouts, k: int, topk_ids: torch.Tensor,
                        topk_dists: torch.Tensor, sketches: torch.Tensor, m_hash_bits: int = DEFAULT_M_HASH_BITS,
                        out: torch.Tensor | None = None, segments: torch.Tensor | None = None,
-                       stream: torch.cuda.Stream | None = None):
+                       stream: torch.cuda.Stream | None = None, unique: bool = False):
     """The records of ``emit_edge_records`` in source-grouped order with one
     segment per member row (tessa_emit_edge_segments).  Returns ``(records,
     count, segments, segment_count)``; ``segments`` is an int32 [capacity, 4]
-    tensor of {src, first record lo, hi, count}.  Synchronises the stream."""
+    tensor of {src, first record lo, hi, count}.  Synchronises the stream.
+
+    ``unique`` (tessa_emit_edge_segments_unique) leaves out the reverse
+    record of each slot whose target row lists the source at the same
+    distance: that row's forward record is the same record, so the set of
+    records, and any HashPrune reduction of them, is unchanged; ``count`` is
+    then the records written, with no gaps."""
     dev = topk_ids.device
     if out is None:
         out = torch.empty((max(2 * layouts.output_len, 1), 4), dtype=torch.int32, device=dev)
@@ -85,10 +91,10 @@ def emit_edge_segments(global_ids: torch.Tensor, layouts: LeafLayouts, k: int, t
                      _ptr(layouts.output_offsets), layouts.leaf_count, layouts.max_leaf_rows, k, N.EXEC_MFMA, 0, 0)
     sk = N.SketchView(_ptr(sketches), sketches.shape[0], sketches.shape[1], m_hash_bits)
     count, nseg = C.c_uint64(0), C.c_uint64(0)
-    N.check(N.load().tessa_emit_edge_segments(_ptr(global_ids), global_ids.numel(), C.byref(lb), _ptr(topk_ids),
-                                              _ptr(topk_dists), C.byref(sk), _ptr(out), out.shape[0],
-                                              _ptr(segments), segments.shape[0], C.byref(count), C.byref(nseg),
-                                              _stream_ptr(stream)), "edge segments")
+    fn = N.load().tessa_emit_edge_segments_unique if unique else N.load().tessa_emit_edge_segments
+    N.check(fn(_ptr(global_ids), global_ids.numel(), C.byref(lb), _ptr(topk_ids), _ptr(topk_dists), C.byref(sk),
+               _ptr(out), out.shape[0], _ptr(segments), segments.shape[0], C.byref(count), C.byref(nseg),
+               _stream_ptr(stream)), "edge segments")
     return out, int(count.value), segments, int(nseg.value)
 
 

@@ -233,11 +233,18 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     are those of its own run, so the graph is the same either way.
 
     ``observer`` (optional) is called after each batch of records is emitted,
-    as observer(tag, global_ids, output, layouts, records, record_count):
-    ``output`` has leaf_row_ids / leaf_starts / leaf_sizes / leaf_count /
-    leaf_rows / k / topk_ids / topk_dists of the batch (starts relative to its
-    leaf_row_ids) and ``global_ids`` maps its rows to point ids (None: the
-    rows are point ids); it must not keep device tensors alive.
+    as observer(tag, global_ids, output, layouts, records, record_count,
+    segments, segment_count): ``output`` has leaf_row_ids / leaf_starts /
+    leaf_sizes / leaf_count / leaf_rows / k / topk_ids / topk_dists of the
+    batch (starts relative to its leaf_row_ids) and ``global_ids`` maps its
+    rows to point ids (None: the rows are point ids); ``segments`` is None
+    when the records go to TierLift; it must not keep device tensors alive.
+
+    For the device reservoirs the records are emitted source-grouped without
+    the repeats of mutual pairs (edges.emit_edge_segments(unique=True): the
+    reverse record of a slot whose target lists the source at the same
+    distance is that target's forward record); the reservoirs, a function of
+    the record set, are unchanged.
 
     ``host_reducer`` routes the records through the TierLift host reducer
     (bounded host memory, spill files past the budget) instead of device
@@ -282,12 +289,13 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     famp = max(p.fanout_second, 1)
 
     def emit(lay_gids, lay, k, ids, d):
-        # device reservoirs merge source-grouped segments in place; TierLift
-        # routes records by source, in any order
+        # device reservoirs merge source-grouped segments in place (repeats
+        # of mutual pairs left out); TierLift routes records by source, in
+        # any order, and drops repeats itself
         if tl is not None:
             rec, cnt = E.emit_edge_records(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits)
             return rec, cnt, None, 0
-        return E.emit_edge_segments(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits)
+        return E.emit_edge_segments(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits, unique=True)
 
     def consume(rec, cnt, segs, nseg):
         if tl is not None:
@@ -336,7 +344,7 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
                             out.leaf_starts[: out.leaf_count] * out.k, leaf_max, out.leaf_rows * out.k)
         rec, cnt, segs, nseg = emit(cg, lay, out.k, out.topk_ids, out.topk_dists)
         if observer is not None:
-            observer(("child", c), cg, out, lay, rec, cnt)
+            observer(("child", c), cg, out, lay, rec, cnt, segs, nseg)
         consume(rec, cnt, segs, nseg)
         st["records"] += int(cnt)
         st["leaves"] += out.leaf_count
@@ -467,7 +475,7 @@ def _run_root_group(sess, sq8, gids, pts, offs_h, sizes, group, parent_points, p
         q1 = time.perf_counter()
         if observer is not None:
             chunk = LeafChunk(ro.leaf_rows[r0:r1], off - r0, ro.leaf_sizes[l0:l1], l1 - l0, r1 - r0, k, ids, d)
-            observer(("roots", st["runs"] - 1, l0), None, chunk, lay, rec, cnt)
+            observer(("roots", st["runs"] - 1, l0), None, chunk, lay, rec, cnt, segs, nseg)
             del chunk
         q2 = time.perf_counter()
         consume(rec, cnt, segs, nseg)

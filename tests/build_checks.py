@@ -3,7 +3,11 @@ observer for pipeline.build_graph_sq8 that collects what the oracle can check
 on samples, and the verification itself.
 
   * every D0 child's leaves hold <= leaf_max rows, every point lands in at
-    least one leaf, and each child emits exactly sum 2 * rows * k_eff records;
+    least one leaf, and each child emits exactly sum 2 * rows * k_eff records
+    (TierLift), or that less the repeats of mutual pairs (source-grouped
+    segments for the device reservoirs: one segment per leaf row, the
+    segments' counts summing to the records, and on sampled leaves exactly
+    2 * valid slots - mutual slots, the mutual slots found on the host);
   * a few leaves of a few children equal the oracle's leaf top-k bit for bit
     (ids and f32 distance bits);
   * the reservoirs of sampled points equal the oracle's reservoirs over every
@@ -36,7 +40,7 @@ class BuildObserver:
         self.calls = 0
         self.check_calls = set(check_calls)
 
-    def __call__(self, tag, cg, out, lay, rec, cnt):
+    def __call__(self, tag, cg, out, lay, rec, cnt, segs=None, nseg=0):
         sizes = out.leaf_sizes[: out.leaf_count].long()
         self.max_leaf = max(self.max_leaf, int(sizes.max().item()))
         call = self.calls
@@ -46,7 +50,14 @@ class BuildObserver:
         local = out.leaf_row_ids[: out.leaf_rows].long()
         self.covered[local if cg is None else cg.long()[local]] = True
         kk = torch.clamp(sizes - 1, max=out.k)
-        assert int(cnt) == int((2 * sizes * kk).sum().item()), f"{tag}: record count"
+        full = int((2 * sizes * kk).sum().item())
+        if segs is None:
+            assert int(cnt) == full, f"{tag}: record count"
+        else:
+            assert int(cnt) <= full, f"{tag}: record count"
+            assert nseg == int(sizes.sum().item()), f"{tag}: one segment per leaf row"
+            seg_counts = segs[:nseg, 3].long()
+            assert int(seg_counts.sum().item()) == int(cnt), f"{tag}: segment counts"
         r = rec[:cnt]
         self.sampled_records.append(r[self.in_sample[r[:, 0].long()]].clone())
         if call in self.check_calls:
@@ -57,9 +68,14 @@ class BuildObserver:
             li = np.arange(len(li))
             ids = out.topk_ids[: out.leaf_rows * out.k].cpu().numpy().view(np.uint32).reshape(-1, out.k)
             dd = out.topk_dists[: out.leaf_rows * out.k].cpu().numpy().reshape(-1, out.k)
+            seg0 = np.concatenate([[0], np.cumsum(sz)])
             for leaf in np.linspace(0, out.leaf_count - 1, 4).astype(int):
                 a, n = int(starts[leaf]), int(sz[leaf])
                 self.leaf_checks.append((g[li[a:a + n]], ids[a:a + n], dd[a:a + n]))
+                if segs is not None:
+                    got = int(seg_counts[int(seg0[leaf]):int(seg0[leaf]) + n].sum().item())
+                    assert got == _unique_records(g[li[a:a + n]], ids[a:a + n], dd[a:a + n], out.k), \
+                        f"{tag}: leaf {leaf} records without mutual repeats"
 
     def verify(self, built, sq8, p, orc, leaf_max: int, what: str) -> None:
         rows = sq8.rows
@@ -95,6 +111,23 @@ class BuildObserver:
         assert np.array_equal(gc, wc), f"{what}: sampled reservoir sizes differ"
         for i in range(len(sample_h)):
             assert np.array_equal(gt[i, : gc[i]], wt[i, : wc[i]]), f"{what}: reservoir of point {sample_h[i]} differs"
+
+
+def _unique_records(gl, ids, dd, k):
+    """Records of one leaf with the mutual pairs' repeats left out: 2 per
+    valid slot less one per slot (r -> j) whose row j lists gl[r] at the same
+    distance bits."""
+    n = len(gl)
+    kl = min(k, n - 1) if n > 1 else 0
+    if kl == 0:
+        return 0
+    li, lb = ids[:, :kl], dd[:, :kl].view(np.uint32)
+    valid = (li != 0xFFFFFFFF) & ((lb & 0x7F800000) != 0x7F800000)
+    order = np.argsort(gl, kind="stable")
+    pos = order[np.searchsorted(gl, li, sorter=order).clip(0, n - 1)]
+    assert np.all(~valid | (gl[pos] == li)), "a top-k id outside its leaf"
+    mutual = valid & ((li[pos] == gl[:, None, None]) & (lb[pos] == lb[:, :, None])).any(axis=2)
+    return int(2 * valid.sum() - mutual.sum())
 
 
 # ---- graph quality that does not depend on navigation from one entry point --

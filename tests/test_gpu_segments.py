@@ -6,7 +6,11 @@ segment insert (tessa_hashprune_insert_segments).
     its source, the segments tile the records, one per member row;
   * the reservoirs after inserting by segments equal those after inserting
     the records (C2-shaped leaves, and replicated points across leaves with
-    hub sources that take the LDS merge), and equal the oracle's."""
+    hub sources that take the LDS merge), and equal the oracle's;
+  * tessa_emit_edge_segments_unique writes, per leaf, the reference-order
+    multiset less exactly one copy of each mutual pair's repeated record
+    (found here from the top-k lists on the host), with no gaps, and the
+    reservoirs it feeds equal the oracle's over every record."""
 import numpy as np
 import pytest
 import torch
@@ -34,7 +38,7 @@ def _leaves(orc, n_points, leaf_sizes, dim, seed, replicate=0):
     return codes, scales, norms, np.concatenate(members), np.array(offs), np.array(counts)
 
 
-def _run(orc, gpu, n_points, leaf_sizes, dim, seed, k=32, m_bits=12):
+def _run(orc, gpu, n_points, leaf_sizes, dim, seed, k=32, m_bits=12, unique=False, full=False):
     codes, scales, norms, members, offs, counts = _leaves(orc, n_points, leaf_sizes, dim, seed)
     sq8 = to_dev_sq8(codes, scales, norms, dim)
     gids = dev_u32(np.arange(n_points))
@@ -42,8 +46,11 @@ def _run(orc, gpu, n_points, leaf_sizes, dim, seed, k=32, m_bits=12):
     ids, d, _ = T.leaf_topk(sq8, gids, lay, k)
     rng = np.random.default_rng(seed + 1)
     sk = torch.from_numpy(rng.standard_normal((n_points, m_bits)).astype(np.float32)).to(gpu)
-    rec, cnt = E.emit_edge_records(gids, lay, k, ids, d, sk, m_bits)
-    grec, gcnt, segs, nseg = E.emit_edge_segments(gids, lay, k, ids, d, sk, m_bits)
+    lro = torch.zeros(len(leaf_sizes) + 1, dtype=torch.int64, device=gpu)
+    rec, cnt = E.emit_edge_records(gids, lay, k, ids, d, sk, m_bits, leaf_record_offsets=lro)
+    grec, gcnt, segs, nseg = E.emit_edge_segments(gids, lay, k, ids, d, sk, m_bits, unique=unique)
+    if full:
+        return rec, cnt, grec, gcnt, segs, nseg, counts, members, offs, ids, d, lro
     return rec, cnt, grec, gcnt, segs, nseg, counts
 
 
@@ -78,17 +85,83 @@ def test_grouped_records_and_segments(gpu_dev, orc, n_points, leaf_sizes, dim):
     assert covered == gcnt
 
 
+def _tiles(segs, nseg, n_records, recs):
+    """Segments tile records [0, n_records) and carry their records' source."""
+    sg = segs[:nseg].cpu().numpy().view(np.uint32)
+    first = sg[:, 1].astype(np.uint64) | (sg[:, 2].astype(np.uint64) << 32)
+    covered = 0
+    for i in np.argsort(first, kind="stable"):
+        c = int(sg[i, 3])
+        if c == 0:
+            continue
+        assert int(first[i]) == covered, "segments must tile the records"
+        assert np.all(recs["src"][covered:covered + c] == sg[i, 0])
+        covered += c
+    assert covered == n_records
+    return sg, first
+
+
+@pytest.mark.parametrize("n_points,leaf_sizes,dim,k", [
+    (8192, [1024] * 8, 128, 32),                       # C2-shaped
+    (3000, [700, 2048, 33, 2, 1, 1500, 900], 64, 32),   # ragged leaves, replicated points, a one-row leaf
+    (600, [20, 300, 7, 250], 16, 10),                   # k_eff below k, k not a multiple of 4
+])
+def test_unique_segments_drop_only_mutual_repeats(gpu_dev, orc, n_points, leaf_sizes, dim, k):
+    rec, cnt, urec, ucnt, segs, nseg, counts, members, offs, ids, d, lro = _run(
+        orc, gpu_dev, n_points, leaf_sizes, dim, 5, k=k, unique=True, full=True)
+    a = E.records_to_numpy(rec, cnt)
+    u = E.records_to_numpy(urec, ucnt)
+    sg, first = _tiles(segs, nseg, ucnt, u)
+    lro = lro.cpu().numpy()
+    ids_h = ids.cpu().numpy().view(np.uint32)
+    d_h = d.cpu().numpy().view(np.uint32)
+    seg0, dropped_total = 0, 0
+    for leaf, n in enumerate(counts):
+        n = int(n)
+        m = members[offs[leaf]:offs[leaf] + n].astype(np.uint32)  # global id = row (sorted, distinct)
+        kl = min(k, n - 1) if n > 1 else 0
+        start = int(offs[leaf]) * k
+        li = ids_h[start:start + n * k].reshape(n, k)[:, :kl]
+        ld = d_h[start:start + n * k].reshape(n, k)[:, :kl]
+        want = a[lro[leaf]:lro[leaf + 1]]
+        # this leaf's kept records: its rows' segments
+        got = np.concatenate([u[int(first[i]):int(first[i]) + int(sg[i, 3])] for i in range(seg0, seg0 + n)]
+                             + [u[:0]])
+        seg0 += n
+        # the slots (r, q) whose target row lists m[r] at the same distance
+        drop = []
+        if kl:
+            c = np.searchsorted(m, li)
+            assert np.all(m[c] == li)
+            mutual = (li[c] == m[:, None, None]) & (ld[c] == ld[:, :, None])  # [r, q, slot of c's list]
+            rr, qq = np.nonzero(mutual.any(axis=2))
+            drop = [(int(li[r, q]), int(m[r]), int(ld[r, q])) for r, q in zip(rr, qq)]
+        dropped_total += len(drop)
+        # want less one copy of each repeated record equals what was kept
+        key = {}
+        for i, (s_, t_, db) in enumerate(zip(want["src"], want["dst"], want["dist"].view(np.uint32))):
+            key.setdefault((int(s_), int(t_), int(db)), []).append(i)
+        keep = np.ones(len(want), bool)
+        for dk in drop:
+            copies = key[dk]
+            assert len(copies) == 2, f"leaf {leaf}: a mutual pair's record appears {len(copies)} times"
+            keep[copies.pop()] = False
+        assert np.array_equal(_sorted_records(want[keep]), _sorted_records(got)), f"leaf {leaf}"
+    assert ucnt == cnt - dropped_total and dropped_total > 0
+
+
 @pytest.fixture(scope="module")
 def gpu_dev():
     return require_gpu()
 
 
+@pytest.mark.parametrize("unique", [False, True])
 @pytest.mark.parametrize("n_points,leaf_sizes,dim,l_max", [
     (8192, [1024] * 8, 128, 64),
     (1500, [1400, 1400, 1300, 900, 1450, 1200], 32, 16),  # points in up to six leaves: large merges
 ])
-def test_segment_insert_equals_record_insert(gpu_dev, orc, n_points, leaf_sizes, dim, l_max):
-    rec, cnt, grec, gcnt, segs, nseg, _ = _run(orc, gpu_dev, n_points, leaf_sizes, dim, 9)
+def test_segment_insert_equals_record_insert(gpu_dev, orc, n_points, leaf_sizes, dim, l_max, unique):
+    rec, cnt, grec, gcnt, segs, nseg, _ = _run(orc, gpu_dev, n_points, leaf_sizes, dim, 9, unique=unique)
     with H.HashPruneReducer(n_points, l_max, gpu_dev) as a, H.HashPruneReducer(n_points, l_max, gpu_dev) as b:
         a.insert(rec, cnt)
         b.insert_segments(grec, segs, nseg)
