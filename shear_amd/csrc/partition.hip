@@ -471,6 +471,18 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                     lsv[g] = *reinterpret_cast<const float4 *>(ls + 32u * t + 8u * g + 4u * h);
                     lnv[g] = *reinterpret_cast<const float4 *>(ln + 32u * t + 8u * g + 4u * h);
                 }
+                // The row's last live slot as the tile starts (both lanes of
+                // the row hold the same slots).  A leader whose distance lies more than
+                // the tie band above it is not assign_before it, nor before
+                // any smaller last slot, so its insertion changes nothing
+                // while the last slot stays at or below it.  Only the other
+                // leaders are visited, in slot order; if an insertion ever
+                // raises the last slot (a tie resolved by the hash key can
+                // leave a slot up to the band above the next), every later
+                // leader of the tile is visited.
+                const int fl = (fanout < 4u ? (int)fanout : 4) - 1;
+                const float last = fl == 0 ? bd[0] : fl == 1 ? bd[1] : fl == 2 ? bd[2] : bd[3];
+                uint32_t visit = 0u;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
@@ -480,25 +492,25 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                     const float lno = e == 0 ? lnv[g].x : e == 1 ? lnv[g].y : e == 2 ? lnv[g].z : lnv[g].w;
                     const float d = assign_l2(acc[v], ps, pn, lsc, lno);
                     wb[li * 33 + j] = gl < nl ? d : kEmptyDist;
+                    if (gl < nl && !(__fsub_rn(d, last) > kTieEps)) visit |= 1u << li;
                 }
+                visit |= __shfl_xor(visit, 32);  // the row's other half of the tile's leaders
                 wave_lds_sync();
-                if (h == 0u && ok) {
+                if (ok) {  // both lanes of a row insert: each keeps the row's slots
                     const uint32_t lim = (nl - 32u * t) < 32u ? (nl - 32u * t) : 32u;
-                    // leaders in slot order, 8 at a time: the 8 distances and
-                    // leader ids of a step are read before its insertions
+                    const uint32_t in_tile = lim >= 32u ? ~0u : (1u << lim) - 1u;
                     auto run = [&](auto fc) {
                         constexpr int F = decltype(fc)::value;
-                        for (uint32_t l0 = 0; l0 < lim; l0 += 8u) {
-                            float dv[8];
-                            uint32_t idv[8];
-#pragma unroll
-                            for (int q = 0; q < 8; ++q) {
-                                dv[q] = wb[(l0 + q) * 33 + j];
-                                idv[q] = lid[32u * t + l0 + q];
+                        float bound = last;
+                        uint32_t mask = visit;
+                        while (mask != 0u) {
+                            const uint32_t q = (uint32_t)__builtin_ctz(mask);
+                            mask &= mask - 1u;
+                            insert_slot<F>(wb[q * 33 + j], lpt, lid[32u * t + q], 32u * t + q, bd, bs, bl);
+                            if (bd[F - 1] > bound) {
+                                mask |= in_tile & (q >= 31u ? 0u : ~0u << (q + 1u));
+                                bound = kEmptyDist;
                             }
-#pragma unroll
-                            for (int q = 0; q < 8; ++q)
-                                if (l0 + q < lim) insert_slot<F>(dv[q], lpt, idv[q], 32u * t + l0 + q, bd, bs, bl);
                         }
                     };
                     switch (fanout) {
