@@ -39,6 +39,32 @@ def test_quantizer_matches_oracle_bits(gpu, orc, dim, bits):
     assert np.array_equal(got.norms.cpu().numpy().view(np.uint32), want[2].view(np.uint32))
 
 
+def test_quantizer_half_integer_quotients(gpu, orc):
+    """Quotients x / scale on and one ulp either side of half-integers, where
+    the kernel's multiply-by-reciprocal path hands over to the correctly
+    rounded division; plus a row whose sum of squares overflows (finite values,
+    norm +inf), rows of tiny scale and a partial last block."""
+    rng = np.random.default_rng(7)
+    rows, dim = 301, 64
+    s = rng.uniform(1e-3, 10.0, rows).astype(np.float32)
+    k = rng.integers(-126, 126, (rows, dim)).astype(np.float32)
+    x = ((k + np.float32(0.5)) * s[:, None]).astype(np.float32)
+    x[:, 0] = np.float32(127.0) * s  # max |x| fixes the scale near s
+    step = rng.integers(-1, 2, (rows, dim))
+    x = np.where(step < 0, np.nextafter(x, np.float32(-np.inf)), np.where(step > 0, np.nextafter(x, np.float32(np.inf)), x))
+    x = x.astype(np.float32)
+    x[5] = np.float32(1e20)          # norm overflows; codes are all 127
+    x[6] *= np.float32(1e-37)        # scale below the normal range: exact division only
+    x[7] = np.float32(1e-45)         # denormal values
+    want = orc.quantize(x)
+    got = T.quantize_sq_int8_matrix(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(got.codes.cpu().numpy(), want[0])
+    assert np.array_equal(got.scales.cpu().numpy().view(np.uint32), want[1].view(np.uint32))
+    assert np.array_equal(got.norms.cpu().numpy().view(np.uint32), want[2].view(np.uint32))
+    assert np.isinf(want[2][5])
+
+
 def test_quantizer_rejects_non_finite(gpu):
     x = torch.ones((10, 20), device="cuda")
     x[7, 3] = float("nan")
