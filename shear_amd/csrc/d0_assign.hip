@@ -211,10 +211,29 @@ int launch_ks(const D0AssignParams &p, hipStream_t stream) {
     const uint64_t blocks = (p.rows + kWaves * 32 - 1) / (kWaves * 32);
     if (blocks > 0x7fffffffull) return -2;
     const dim3 grid((uint32_t)blocks);
+    if (p.fanout <= 2) return launch_kf<KS, 2>(p, grid, stream);  // the builds' replication fanout
     if (p.fanout <= 4) return launch_kf<KS, 4>(p, grid, stream);
     if (p.fanout <= 8) return launch_kf<KS, 8>(p, grid, stream);
     if (p.fanout <= 16) return launch_kf<KS, 16>(p, grid, stream);
     return launch_kf<KS, 32>(p, grid, stream);
+}
+
+// Child histogram with per-workgroup counts in LDS (bins = leaders + 1 words,
+// dynamic LDS), added to the global counts once per workgroup and bin: the
+// ~1,000 global counters would otherwise take one atomic per fragment.
+__global__ __launch_bounds__(256) void d0_hist_lds_kernel(const uint32_t *child, uint64_t n, uint32_t bins,
+                                                          uint64_t *counts) {
+    extern __shared__ uint32_t hist[];
+    for (uint32_t b = threadIdx.x; b < bins; b += blockDim.x) hist[b] = 0u;
+    __syncthreads();
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t b = child[i] + 1u;
+        if (b < bins) atomicAdd(&hist[b], 1u);
+        else atomicAdd(reinterpret_cast<unsigned long long *>(&counts[b]), 1ull);  // not a leader index
+    }
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < bins; b += blockDim.x)
+        if (hist[b]) atomicAdd(reinterpret_cast<unsigned long long *>(&counts[b]), (unsigned long long)hist[b]);
 }
 
 __global__ void d0_hist_kernel(const uint32_t *child, uint64_t n, uint64_t *counts) {
@@ -289,8 +308,16 @@ int launch_d0_group(const D0AssignParams &p, uint64_t *child_offsets, uint32_t *
                        (uint64_t)p.leaders + 1);
     if (items == 0) return hipGetLastError() == hipSuccess ? 0 : -1;
     uint64_t hg = (items + 255) / 256;
-    hg = hg > 8192 ? 8192 : hg;
-    hipLaunchKernelGGL(d0_hist_kernel, dim3((uint32_t)hg), dim3(256), 0, stream, p.out_child, items, child_offsets);
+    const uint32_t bins = p.leaders + 1u;
+    if (bins <= 16384u) {
+        hg = hg > 512 ? 512 : hg;
+        hipLaunchKernelGGL(d0_hist_lds_kernel, dim3((uint32_t)hg), dim3(256), bins * 4u, stream, p.out_child, items,
+                           bins, child_offsets);
+    } else {
+        hg = hg > 8192 ? 8192 : hg;
+        hipLaunchKernelGGL(d0_hist_kernel, dim3((uint32_t)hg), dim3(256), 0, stream, p.out_child, items,
+                           child_offsets);
+    }
     hipLaunchKernelGGL(d0_scan_kernel, dim3(1), dim3(1024), 0, stream, child_offsets, p.leaders);
     const size_t keys_bytes = ((items * 4 + 255) / 256) * 256;
     uint32_t *keys_out = reinterpret_cast<uint32_t *>(temp);

@@ -57,6 +57,8 @@ def _run_case(gpu, orc, x, leader_rows, fanout, gids=None, dup=False):
     (4, 4097, 96, 1000, 3),
     (5, 700, 64, 5, 1),
     (6, 1500, 200, 64, 17),
+    (7, 6000, 768, 1000, 2),     # C3 shape: fanout_top 2 (the two-slot kernel)
+    (8, 3000, 128, 140, 2),
 ])
 def test_assignment_matches_oracle(gpu, orc, seed, rows, dim, leaders, fanout):
     x = datagen.gmm_numpy(rows, dim, 12, 0.3, seed)
@@ -68,6 +70,7 @@ def test_duplicate_leaders_and_clamped_distances(gpu, orc):
     x = datagen.gmm_numpy(1000, 32, 4, 0.05, 7)  # tight clusters: many distances clamp to 0
     lr = np.arange(0, 1000, 50, dtype=np.int64)
     _run_case(gpu, orc, x, lr, 8, dup=True)
+    _run_case(gpu, orc, x, lr, 2, dup=True)
 
 
 def test_argument_errors(gpu):
