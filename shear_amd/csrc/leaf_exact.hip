@@ -139,13 +139,24 @@ __global__ __launch_bounds__(kExactThreads) void leaf_exact_all_kernel(LeafParam
     }
 }
 
-// Re-run of the rows the MFMA executor could not certify: one 1,024-thread
+// Re-run of the rows the MFMA executor could not certify: one 512-thread
 // workgroup per row.  The row's distances to a chunk of 1,024 member columns
 // are computed four lanes per column (a quarter of the dims each, summed over
 // the quad) into LDS; then wave 0 inserts them in member order with the rule
 // of exact_row.  Few rows (often a few hundred) are re-run per call, so the
-// latency of one row is what counts.
-constexpr int kFallbackThreads = 1024;
+// latency of one row is what counts; a grid of 512 workgroups strides over
+// the device-side row count.  The workgroup size trades that latency against
+// scheduling beside other streams' kernels (the build runs the leaf operator
+// beside record emission and reservoir merges): 1,024-thread workgroups,
+// which need 16 free wave slots on one CU, took 14-62 ms per C3 build there
+// against 2-17 ms at 512 threads, and C2 alone 0.091 against 0.104 ms.
+#ifndef TESSA_FALLBACK_THREADS
+#define TESSA_FALLBACK_THREADS 512
+#endif
+#ifndef TESSA_FALLBACK_GRID
+#define TESSA_FALLBACK_GRID 512
+#endif
+constexpr int kFallbackThreads = TESSA_FALLBACK_THREADS;
 constexpr uint32_t kFallbackChunk = 1024;
 
 __device__ void exact_row_wg(const LeafParams &p, uint32_t leaf, uint32_t row, float *sd, uint32_t *sg,
@@ -420,7 +431,7 @@ int launch_leaf_exact_all(const LeafParams &p, hipStream_t stream) {
 
 int launch_leaf_exact_fallback(const LeafParams &p, hipStream_t stream) {
     // Grid-stride over the device-side count: no host round trip.
-    hipLaunchKernelGGL(leaf_exact_fallback_kernel, dim3(2048), dim3(kFallbackThreads), 0, stream, p);
+    hipLaunchKernelGGL(leaf_exact_fallback_kernel, dim3(TESSA_FALLBACK_GRID), dim3(kFallbackThreads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
