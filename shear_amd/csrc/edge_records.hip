@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include "edge_kernels.h"
+#include "kernel_attr.h"
 
 namespace tessa {
 namespace {
@@ -34,19 +35,30 @@ constexpr int kCountUnroll = 4;  // rows per half-wave in flight (count pass)
 constexpr int kEmitUnroll = 4;   // rows per half-wave in flight (emit pass)
 constexpr uint32_t kNoKey = 0xffffffffu;
 constexpr uint32_t kLeafRegular = 0x80000000u;  // leaf_totals flag: every row has k_eff valid slots
-constexpr size_t kEmitLdsBudget = 80 * 1024;  // two 512-thread workgroups per CU
+// The leaf's sketch rows are staged in LDS whenever everything fits one CU
+// (two workgroups per CU for 1,024-row leaves, one for 2,048-row leaves: the
+// hashes' reads from L2 instead made 2,048-row leaves 2.6x slower).
+constexpr size_t kEmitLdsBudget = 160 * 1024;
 
 __device__ __forceinline__ bool slot_valid(uint32_t id, float d) {
     // j != u32::MAX && d.is_finite()
     return id != 0xffffffffu && (__float_as_uint(d) & 0x7f800000u) != 0x7f800000u;
 }
 
-// Records are written once and never read back by these kernels: stream them
-// past the caches (nontemporal stores).
+// Records in the reference's order are written once, in runs from
+// consecutive lanes, and never read back by these kernels: they stream past
+// the caches (nontemporal stores).  Source-grouped records land all over the
+// leaf's range (reverse records fill their targets' segments from the end),
+// so they are written through L2, which joins a line's 16-byte pieces before
+// it goes to HBM (C2 grouped emission 7.6 -> 2.9 ms).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <bool kTemporal = false>
 __device__ __forceinline__ void store_record(uint4 *out, uint64_t i, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     u32x4 v = {a, b, c, d};
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + i));
+    if constexpr (kTemporal)
+        *reinterpret_cast<u32x4 *>(out + i) = v;
+    else
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + i));
 }
 
 __device__ __forceinline__ uint32_t table_hash(uint32_t g, uint32_t bits) { return (g * 0x9E3779B1u) >> (32 - bits); }
@@ -554,10 +566,10 @@ __global__ __launch_bounds__(kThreads) void edge_emit_kernel(EdgeParams p) {
                         // forward: its place among the row's valid slots; reverse:
                         // the last free place of j's segment
                         const uint32_t fpos = cnt[r] + (uint32_t)__popc(half & ((1u << q) - 1u));
-                        store_record(p.out, rec0 + fpos, gi, j[u], hf, db);
+                        store_record<true>(p.out, rec0 + fpos, gi, j[u], hf, db);
                         if (((dup[r] >> q) & 1u) == 0u) {
                             const uint32_t rpos = atomicSub(&tot[cj], 1u) - 1u;
-                            store_record(p.out, rec0 + rpos, j[u], gi, hr, db);
+                            store_record<true>(p.out, rec0 + rpos, j[u], gi, hr, db);
                         }
                     }
                     (void)ok_mask;
@@ -611,14 +623,21 @@ int launch_edge_records(const EdgeParams &p, hipStream_t stream) {
     const size_t count_lds = (kWaves + (size_t)p.max_leaf_rows) * sizeof(uint32_t);
     hipLaunchKernelGGL(edge_count_kernel, dim3(grid), dim3(kThreads), count_lds, stream, p);
     hipLaunchKernelGGL(edge_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
-    // Stage the leaf's sketch rows in LDS when that keeps two workgroups per
-    // CU; else read them from HBM (float4 loads when rows are 16-byte aligned).
+    // Stage the leaf's sketch rows in LDS when they fit; else read them from
+    // HBM (float4 loads when rows are 16-byte aligned).
     const bool grouped = p.segments != nullptr;
     const size_t base_lds = (size_t)emit_sketch_offset(p.max_leaf_rows, p.table_bits, grouped) * sizeof(uint32_t);
     const size_t staged = (size_t)p.max_leaf_rows * ((p.m_bits + 3u) & ~3u) * sizeof(float);
     const bool vec4 = p.width % 4u == 0u && (reinterpret_cast<uintptr_t>(p.sketches) & 15u) == 0u;
     const bool in_lds = base_lds + staged <= kEmitLdsBudget;
     const size_t lds = in_lds ? base_lds + staged : base_lds;
+    const void *emit_fn = grouped ? (in_lds ? reinterpret_cast<const void *>(edge_emit_kernel<kSketchLds, true>)
+                                            : vec4 ? reinterpret_cast<const void *>(edge_emit_kernel<kSketchGlobalV4, true>)
+                                                   : reinterpret_cast<const void *>(edge_emit_kernel<kSketchGlobal, true>))
+                                  : (in_lds ? reinterpret_cast<const void *>(edge_emit_kernel<kSketchLds, false>)
+                                            : vec4 ? reinterpret_cast<const void *>(edge_emit_kernel<kSketchGlobalV4, false>)
+                                                   : reinterpret_cast<const void *>(edge_emit_kernel<kSketchGlobal, false>));
+    if (ensure_lds_limit(emit_fn, (int)lds)) return -1;
     if (grouped) {
         if (in_lds)
             hipLaunchKernelGGL((edge_emit_kernel<kSketchLds, true>), dim3(grid), dim3(kThreads), lds, stream, p);

@@ -85,6 +85,11 @@ class GraphBuildParams:
     prune_max_occlusion: int = 750
     prune_saturate: bool = True     # build_shear_index builds its write parameters with saturate_graph(true)
     hashprune_backfill: H.HashPruneBackfill | None = None  # named R-half policy (None: off)
+    # device reservoirs: leave the repeats of mutual pairs out of the emitted
+    # records (same reservoirs; 16-17 % fewer records to merge, but the
+    # emission's list lookups cost more than the merge saves: C3 0.42-0.46 s
+    # with, 0.38-0.43 s without)
+    drop_mutual_repeats: bool = False
 
     def subtree_params(self) -> S.PiPNNSubtreeParams:
         return S.PiPNNSubtreeParams(leaf_knn=self.leaf_knn, c_max=self.c_max, fanout_second=self.fanout_second,
@@ -240,11 +245,12 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
     rows to point ids (None: the rows are point ids); ``segments`` is None
     when the records go to TierLift; it must not keep device tensors alive.
 
-    For the device reservoirs the records are emitted source-grouped without
-    the repeats of mutual pairs (edges.emit_edge_segments(unique=True): the
-    reverse record of a slot whose target lists the source at the same
-    distance is that target's forward record); the reservoirs, a function of
-    the record set, are unchanged.
+    For the device reservoirs the records are emitted source-grouped, with
+    ``p.drop_mutual_repeats`` without the repeats of mutual pairs
+    (edges.emit_edge_segments(unique=True): the reverse record of a slot whose
+    target lists the source at the same distance is that target's forward
+    record); the reservoirs, a function of the record set, are the same
+    either way.
 
     ``host_reducer`` routes the records through the TierLift host reducer
     (bounded host memory, spill files past the budget) instead of device
@@ -295,7 +301,8 @@ def build_graph_sq8(sq8: T.Sq8Matrix, sketches: torch.Tensor, leader_rows: np.nd
         if tl is not None:
             rec, cnt = E.emit_edge_records(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits)
             return rec, cnt, None, 0
-        return E.emit_edge_segments(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits, unique=True)
+        return E.emit_edge_segments(lay_gids, lay, k, ids, d, sketches, p.m_hash_bits,
+                                    unique=p.drop_mutual_repeats)
 
     def consume(rec, cnt, segs, nseg):
         if tl is not None:

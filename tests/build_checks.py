@@ -4,10 +4,11 @@ on samples, and the verification itself.
 
   * every D0 child's leaves hold <= leaf_max rows, every point lands in at
     least one leaf, and each child emits exactly sum 2 * rows * k_eff records
-    (TierLift), or that less the repeats of mutual pairs (source-grouped
-    segments for the device reservoirs: one segment per leaf row, the
-    segments' counts summing to the records, and on sampled leaves exactly
-    2 * valid slots - mutual slots, the mutual slots found on the host);
+    (TierLift, and the device reservoirs' source-grouped segments unless the
+    build leaves out the repeats of mutual pairs, when it emits that less one
+    record per mutual slot); segments: one per leaf row, their counts summing
+    to the records, and on sampled leaves exactly 2 * valid slots (less the
+    mutual slots, found on the host, when any record was left out);
   * a few leaves of a few children equal the oracle's leaf top-k bit for bit
     (ids and f32 distance bits);
   * the reservoirs of sampled points equal the oracle's reservoirs over every
@@ -74,8 +75,11 @@ class BuildObserver:
                 self.leaf_checks.append((g[li[a:a + n]], ids[a:a + n], dd[a:a + n]))
                 if segs is not None:
                     got = int(seg_counts[int(seg0[leaf]):int(seg0[leaf]) + n].sum().item())
-                    assert got == _unique_records(g[li[a:a + n]], ids[a:a + n], dd[a:a + n], out.k), \
-                        f"{tag}: leaf {leaf} records without mutual repeats"
+                    if int(cnt) == full:  # every record emitted
+                        assert got == _leaf_records(ids[a:a + n], dd[a:a + n], out.k), f"{tag}: leaf {leaf} records"
+                    else:
+                        assert got == _unique_records(g[li[a:a + n]], ids[a:a + n], dd[a:a + n], out.k), \
+                            f"{tag}: leaf {leaf} records without mutual repeats"
 
     def verify(self, built, sq8, p, orc, leaf_max: int, what: str) -> None:
         rows = sq8.rows
@@ -111,6 +115,14 @@ class BuildObserver:
         assert np.array_equal(gc, wc), f"{what}: sampled reservoir sizes differ"
         for i in range(len(sample_h)):
             assert np.array_equal(gt[i, : gc[i]], wt[i, : wc[i]]), f"{what}: reservoir of point {sample_h[i]} differs"
+
+
+def _leaf_records(ids, dd, k):
+    """Records of one leaf: 2 per valid slot (id set, distance finite)."""
+    n = ids.shape[0]
+    kl = min(k, n - 1) if n > 1 else 0
+    li, lb = ids[:, :kl], dd[:, :kl].view(np.uint32)
+    return int(2 * ((li != 0xFFFFFFFF) & ((lb & 0x7F800000) != 0x7F800000)).sum())
 
 
 def _unique_records(gl, ids, dd, k):
