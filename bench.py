@@ -64,6 +64,10 @@ def parse():
     ap.add_argument("--c5-rows", type=int, default=0,
                     help="run only the out-of-memory build leg (BASELINE configs[4]: 150,000,000 rows as "
                          "specified) at this many rows and print its JSON line instead")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only measure the sustained int8 MFMA rate of this GPU (tessa_probe_mfma_rate) and print it")
+    ap.add_argument("--no-mfma-ceiling", action="store_true",
+                    help="leave the sustained int8 MFMA rate out of the default run's line")
     ap.add_argument("--copy-calibration-mib", type=str, default="",
                     help="after the timed steps, run one int32 elementwise copy kernel per size in this "
                          "comma-separated list of MiB (read N, write N) so rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
@@ -96,6 +100,9 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     N.load()
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling()), flush=True)
+        return 0
     if args.c5_rows:
         print(json.dumps(c5_leg(dev, args.c5_rows)), flush=True)
         return 0
@@ -238,6 +245,11 @@ def main() -> int:
         "cpu_baseline": None,
     }
 
+    if not args.no_mfma_ceiling:
+        # the practical ceiling of the roofline above, measured on this GPU
+        result["mfma_ceiling"] = mfma_ceiling()
+        result["mfma_ceiling"]["filter_frac_of_sustained"] = round(achieved / result["mfma_ceiling"]["tops"], 4)
+
     if not args.no_edges:
         result["record_emission"], rec, rec_count = edge_leg(gids, lay, out_ids, out_d, stream, args.steps,
                                                              args.warmup)
@@ -267,6 +279,32 @@ def main() -> int:
         torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def mfma_ceiling(workgroups=512, chains=4, seconds=0.6):
+    """Sustained int8 MFMA rate of this GPU (tessa_probe_mfma_rate): random
+    register operands, no memory traffic, 2 waves per SIMD with 4 chains each
+    (the fastest shape measured), run long enough (about `seconds`) for the
+    clock to settle under the power limit.  The leaf filter's roofline
+    `peak` stays the published 5.0 POP/s; this is what the chip sustains."""
+    import ctypes as C
+
+    from shear_amd import _native as N
+
+    lib = N.load()
+    tops, mhz = C.c_double(0.0), C.c_double(0.0)
+    iters = 8192
+    N.check(lib.tessa_probe_mfma_rate(workgroups, chains, iters, C.byref(tops), C.byref(mhz)), "mfma probe")
+    # scale the loop to the wanted duration from the short run's rate
+    ops_per_iter = workgroups * 4 * chains * 65536.0
+    iters = max(8192, int(seconds * tops.value * 1e12 / ops_per_iter) // 8 * 8)
+    N.check(lib.tessa_probe_mfma_rate(workgroups, chains, iters, C.byref(tops), C.byref(mhz)), "mfma probe")
+    log(f"sustained int8 MFMA: {tops.value:.0f} TOPS at {mhz.value:.0f} MHz "
+        f"({100 * tops.value / INT8_PEAK_TOPS:.1f} % of {INT8_PEAK_TOPS:.0f})")
+    return {"kernel": "v_mfma_i32_32x32x32_i8 chains on random register operands (tessa_probe_mfma_rate)",
+            "workgroups": workgroups, "waves_per_simd": workgroups * 4 // 1024, "chains_per_wave": chains,
+            "iterations": iters, "tops": round(tops.value, 1), "shader_mhz": round(mhz.value, 1),
+            "frac_of_published_peak": round(tops.value / INT8_PEAK_TOPS, 4)}
 
 
 class _LeafSampler:

@@ -891,6 +891,15 @@ tessa_status tessa_session_submit_subtree(tessa_session *session, const tessa_sq
 tessa_status tessa_session_wait(tessa_session *session, uint64_t seq, tessa_subtree_host_result *out);
 tessa_status tessa_session_release(tessa_session *session, uint64_t seq);
 
+/* Diagnostic, no counterpart in the reference: the sustained int8 MFMA rate
+ * of the current GPU (v_mfma_i32_32x32x32_i8 chains on random register
+ * operands, no memory traffic; `chains` in {2, 4, 8} per wave, 256-thread
+ * workgroups) and the shader clock it ran at, the fastest of three runs.  It
+ * is the practical ceiling the leaf filter's roofline is read against; it
+ * allocates and synchronises the device. */
+tessa_status tessa_probe_mfma_rate(uint32_t workgroups, uint32_t chains, uint64_t iters, double *tops,
+                                   double *mhz);
+
 /* "QUEUE_NODE|LEAF_ROW|..." or "none" (same labels as the reference). */
 void tessa_overflow_labels(uint64_t flags, char *buf, size_t len);
 uint32_t tessa_abi_version(void);

@@ -317,6 +317,7 @@ _U32 = C.c_uint32
 _U64 = C.c_uint64
 SIGNATURES = {
     "tessa_abi_version": (_U32, []),
+    "tessa_probe_mfma_rate": (TessaStatus, [_U32, _U32, _U64, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "tessa_overflow_labels": (None, [_U64, C.c_char_p, C.c_size_t]),
     "tessa_query_caps": (TessaStatus, [C.c_int32, C.POINTER(TessaCaps)]),
     "tessa_leaf_topk": (TessaStatus, [C.POINTER(Sq8View), C.POINTER(LeafBatch), _P, _P, _P, _P]),
