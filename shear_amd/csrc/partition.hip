@@ -338,6 +338,64 @@ struct CountLayout {
     static_assert(kPartItemRows % kChunk == 0, "item rows");
 };
 
+// v[c] for a wave-uniform c, by selects (the array stays in registers)
+template <int N>
+__device__ __forceinline__ uint32_t pick(const uint32_t (&v)[N], int c) {
+    uint32_t r = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) r = c == i ? v[i] : r;
+    return r;
+}
+
+// A row's F slots are empty when its first leader tile starts, so in-order
+// insertion would visit every leader of that tile.  Let T be the row's F-th
+// smallest distance in the tile.  When no distance lies above T by at most
+// the tie band, a leader above T is after every leader at or below T under
+// assign_before, in both directions (the rounded difference only grows as
+// the smaller distance falls).  Such a leader then only ever sits behind
+// those leaders in the slots and never moves one of them, and at least F of
+// them fill the slots by the tile's end.  Inserting only the leaders at or
+// below T, in slot order, leaves the same slots.
+// `dl` holds the lane's 16 distances of the tile (kEmptyDist past the node's
+// leaders) and `all` the lane's half of the full visit mask.  Returns the
+// lane's half of the visit mask: the leaders at or below T, or `all` when a
+// distance of the row lies in the band, is NaN, or fewer than F are finite.
+// Both lanes of a row return masks of the same choice.
+template <int F>
+__device__ __forceinline__ uint32_t first_tile_visits(const float (&dl)[16], uint32_t h, uint32_t all) {
+    float s[F];  // smallest distances seen, ascending
+#pragma unroll
+    for (int k = 0; k < F; ++k) s[k] = kEmptyDist;
+    auto push = [&](float x) {
+#pragma unroll
+        for (int k = 0; k < F; ++k) {
+            const float lo = fminf(s[k], x);
+            if (k + 1 < F) x = fmaxf(s[k], x);
+            s[k] = lo;
+        }
+    };
+#pragma unroll
+    for (int v = 0; v < 16; ++v) push(dl[v]);
+    float o[F];  // the other lane's smallest, for the row's 32 leaders
+#pragma unroll
+    for (int k = 0; k < F; ++k) o[k] = __shfl_xor(s[k], 32);
+#pragma unroll
+    for (int k = 0; k < F; ++k) push(o[k]);
+    const float T = s[F - 1];
+    uint32_t near = 0u;
+    bool band = !(T < kEmptyDist);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);
+        if (dl[v] <= T) near |= 1u << li;
+        else if (!(__fsub_rn(dl[v], T) > kTieEps)) band = true;
+    }
+    // every lane takes part in the exchange (a lane left out of it hands its
+    // partner no value)
+    const int other_band = __shfl_xor(band ? 1 : 0, 32);
+    return band || other_band != 0 ? all : near;
+}
+
 // LDS hand-off inside one wave: its lanes' LDS writes are seen by its other
 // lanes' later reads (and reads finish before later writes).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -423,19 +481,34 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
 
         const uint32_t ntiles = (nl + 31) / 32;
         float *wb = dbuf + wave * 32 * 33;
-        for (int ch = 0; ch < L::kChunks; ++ch) {
-            if (first + ch * L::kChunk >= n) break;  // uniform across the block
-            const uint32_t m = first + ch * L::kChunk + wave * 32u + j;
+        // The row ids and SQ8 rows of all the item's chunks are read before
+        // its first chunk computes, and a chunk's codes, scales and norms are
+        // requested as soon as the chunk before it has issued its last MFMA:
+        // that chunk's insertion covers their latency.
+        uint32_t cpt[L::kChunks], cspt[L::kChunks];
+        uint32_t okbits = 0u;  // bit c: the lane's row of chunk c is valid
+#pragma unroll
+        for (int c = 0; c < L::kChunks; ++c) {
+            const uint32_t m = first + c * L::kChunk + wave * 32u + j;
+            cpt[c] = m < n ? arena[row_start + m] : rb;
+        }
+#pragma unroll
+        for (int c = 0; c < L::kChunks; ++c) {
+            const uint32_t m = first + c * L::kChunk + wave * 32u + j;
             bool ok = m < n;
-            uint32_t pt = ok ? arena[row_start + m] : rb;
-            if (ok && pt >= a.rows) {
+            if (ok && cpt[c] >= a.rows) {
                 pc_flag(a.counters, TESSA_OVF_INVALID_ASSIGN_POINT_ID);
                 ok = false;
-                pt = rb;
+                cpt[c] = rb;
             }
-            if (__ballot(ok) == 0ull) continue;  // this wave's rows are past the node's end
-            const uint32_t spt = rmap ? rmap[pt] : pt;
-            v4i bfrag[KS];
+            okbits |= ok ? 1u << c : 0u;
+            cspt[c] = rmap ? rmap[cpt[c]] : cpt[c];
+        }
+        v4i bfrag[KS];
+        float nps = 0.0f, npn = 0.0f;  // scale and norm of the lane's row in bfrag
+        auto load_chunk = [&](int c) {
+            const bool ok = (okbits >> c) & 1u;
+            const uint32_t spt = pick(cspt, c);
             const int8_t *mc = a.codes + (uint64_t)spt * pd;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
@@ -444,9 +517,19 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                 if (ok && off < pd) z = *reinterpret_cast<const v4i *>(mc + off);
                 bfrag[s] = z;
             }
-            const float ps = ok ? a.scales[spt] : 0.0f;
-            const float pn = ok ? a.norms[spt] : 0.0f;
-            const uint32_t lpt = pt - rb;  // the row's index within its root
+            nps = ok ? a.scales[spt] : 0.0f;
+            npn = ok ? a.norms[spt] : 0.0f;
+        };
+        int loaded = -1;  // chunk whose rows bfrag holds (wave-uniform)
+        for (int ch = 0; ch < L::kChunks; ++ch) {
+            if (first + ch * L::kChunk >= n) break;  // uniform across the block
+            const uint32_t m = first + ch * L::kChunk + wave * 32u + j;
+            const bool ok = (okbits >> ch) & 1u;
+            if (__ballot(ok) == 0ull) continue;  // this wave's rows are past the node's end
+            if (loaded != ch) load_chunk(ch);
+            const float ps = nps;
+            const float pn = npn;
+            const uint32_t lpt = pick(cpt, ch) - rb;  // the row's index within its root
             // compute_backend.rs:6357-6368 reset: (FLT_MAX, empty)
             float bd[4] = {kEmptyDist, kEmptyDist, kEmptyDist, kEmptyDist};
             uint32_t bs[4] = {kEmptyId, kEmptyId, kEmptyId, kEmptyId};
@@ -462,6 +545,10 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                 for (int s = 0; s < KS; ++s) {
                     if (s + 2 < KS) ring[(s + 2) % 3] = *reinterpret_cast<const v4i *>(arow + 32 * (s + 2));
                     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[s % 3], bfrag[s], acc, 0, 0, 0);
+                }
+                if (t + 1 == ntiles && ch + 1 < L::kChunks) {
+                    load_chunk(ch + 1);
+                    loaded = ch + 1;
                 }
                 // the lane's 16 leaders are 4 runs of 4 (8g + 4h + e): their
                 // scales and norms in 8 vector reads, then every distance
@@ -483,6 +570,7 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                 const int fl = (fanout < 4u ? (int)fanout : 4) - 1;
                 const float last = fl == 0 ? bd[0] : fl == 1 ? bd[1] : fl == 2 ? bd[2] : bd[3];
                 uint32_t visit = 0u;
+                float dl[16];
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const uint32_t li = 8u * (v / 4) + 4u * h + (v % 4);  // leader within the tile
@@ -491,8 +579,17 @@ __device__ __forceinline__ void count_items(const PartArgs &a, uint32_t cur, uin
                     const float lsc = e == 0 ? lsv[g].x : e == 1 ? lsv[g].y : e == 2 ? lsv[g].z : lsv[g].w;
                     const float lno = e == 0 ? lnv[g].x : e == 1 ? lnv[g].y : e == 2 ? lnv[g].z : lnv[g].w;
                     const float d = assign_l2(acc[v], ps, pn, lsc, lno);
-                    wb[li * 33 + j] = gl < nl ? d : kEmptyDist;
+                    dl[v] = gl < nl ? d : kEmptyDist;
+                    wb[li * 33 + j] = dl[v];
                     if (gl < nl && !(__fsub_rn(d, last) > kTieEps)) visit |= 1u << li;
+                }
+                if (t == 0u) {  // the slots are empty
+                    switch (fanout) {
+                        case 1: visit = first_tile_visits<1>(dl, h, visit); break;
+                        case 2: visit = first_tile_visits<2>(dl, h, visit); break;
+                        case 3: visit = first_tile_visits<3>(dl, h, visit); break;
+                        default: visit = first_tile_visits<4>(dl, h, visit); break;
+                    }
                 }
                 visit |= __shfl_xor(visit, 32);  // the row's other half of the tile's leaders
                 wave_lds_sync();

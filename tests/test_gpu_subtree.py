@@ -102,6 +102,24 @@ def test_subtree_matches_oracle(gpu, orc, case):
     _check_topk(orc, out, leaves, codes, scales, norms, gids)
 
 
+@pytest.mark.parametrize("fan", [1, 2, 4])
+def test_subtree_near_tied_distances_match_oracle(gpu, orc, fan):
+    """Rows on a 3-level grid, many of them repeated, each scaled by 1 + a
+    few ulps: a row's distances to the leaders fall into a handful of values
+    that differ by less than the tie band, so assignment turns on the hash
+    tie key and the first-tile visit rule mostly meets a distance inside the
+    band above its threshold (and must visit every leader)."""
+    rng = np.random.default_rng(50 + fan)
+    base = rng.integers(0, 3, (700, 16)).astype(np.float32)
+    x = base[rng.integers(0, 700, 5000)]
+    x *= (1.0 + rng.integers(0, 8, (5000, 1)) * 1e-7).astype(np.float32)
+    codes, scales, norms = orc.quantize(x.astype(np.float32))
+    gids = rng.permutation(1 << 22)[:5000].astype(np.uint32)
+    _, out, leaves, ctr, _ = _run(orc, codes, scales, norms, gids, 16, fan=fan, leaf_max=256, psamp=0.01, leaf_min=32)
+    _check_layout(out, leaves, ctr)
+    _check_topk(orc, out, leaves, codes, scales, norms, gids)
+
+
 def test_subtree_unnormalised_rows_are_certified(gpu, orc):
     """C1-shaped rows (128-d, centres N(0, I), sigma 0.3, not normalised):
     their norms differ by far more than 1 %, so the filter tests each column
