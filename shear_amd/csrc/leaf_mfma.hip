@@ -469,24 +469,27 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                 nx_mc[q] = mem_lds[ok ? c : 0u];
             }
         };
-        auto issue_tile = [&]() {
-            pre_full = nx_full;
-            pre_ok = nx_ok;
+        auto issue_to = [&](v4i (&dst)[L::kChunksPerThread]) {
 #pragma unroll
             for (int q = 0; q < L::kChunksPerThread; ++q) {
                 const uint32_t off = ((nx_ok >> q) & 1u) ? chunk_off(q) : 0u;
-                pre[q] = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)nx_mc[q] * pd + off);
+                dst[q] = *reinterpret_cast<const v4i *>(p.codes + (uint64_t)nx_mc[q] * pd + off);
             }
         };
-        auto store_tile = [&](int8_t *dst) {
-            if (pre_full) {  // every chunk is real data: no selects
+        auto issue_tile = [&]() {
+            pre_full = nx_full;
+            pre_ok = nx_ok;
+            issue_to(pre);
+        };
+        auto store_from = [&](const v4i (&src)[L::kChunksPerThread], bool full, uint32_t ok, int8_t *dst) {
+            if (full) {  // every chunk is real data: no selects
 #pragma unroll
                 for (int q = 0; q < L::kChunksPerThread; ++q) {
                     const uint32_t chunk = tid + q * kThreads;
                     if (chunk < (uint32_t)L::kChunks) {
                         const uint32_t row = chunk / (KS * 2);
                         const uint32_t off = (chunk % (KS * 2)) * 16u;
-                        *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = pre[q];
+                        *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = src[q];
                     }
                 }
                 return;
@@ -498,10 +501,11 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
                     const uint32_t row = chunk / (KS * 2);
                     const uint32_t off = (chunk % (KS * 2)) * 16u;
                     const v4i zero = {0, 0, 0, 0};
-                    *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = ((pre_ok >> q) & 1u) ? pre[q] : zero;
+                    *reinterpret_cast<v4i *>(dst + row * L::kTileStride + off) = ((ok >> q) & 1u) ? src[q] : zero;
                 }
             }
         };
+        auto store_tile = [&](int8_t *dst) { store_from(pre, pre_full, pre_ok, dst); };
 
         // ---- the tile stream ----------------------------------------------------
         // Stream position i < nA is phase A's sampled tile i*sstride,
@@ -700,10 +704,24 @@ __global__ __launch_bounds__(kThreads, TESSA_LEAF_MIN_BLOCKS) void leaf_mfma_ker
         // prologue: positions 0 .. NB/2-1 in their LDS buffers, position
         // NB/2 in registers, the ids of position NB/2 + 1 prepared (S >= 2:
         // nA >= 1 and ntiles >= 1)
-        for (uint32_t t0 = 0; t0 < kAhead && t0 < S; ++t0) {
-            prep_tile(tile_of(t0));
+        if constexpr (kAhead == 2u) {
+            // both buffered tiles' loads in flight together: one round trip
+            // before the first MFMA instead of two
+            v4i pre0[L::kChunksPerThread];
+            prep_tile(tile_of(0));
+            const bool full0 = nx_full;
+            const uint32_t ok0 = nx_ok;
+            issue_to(pre0);
+            prep_tile(tile_of(1));
             issue_tile();
-            store_tile(bufp(t0));
+            store_from(pre0, full0, ok0, bufp(0));
+            store_tile(bufp(1));
+        } else {
+            for (uint32_t t0 = 0; t0 < kAhead && t0 < S; ++t0) {
+                prep_tile(tile_of(t0));
+                issue_tile();
+                store_tile(bufp(t0));
+            }
         }
         prep_tile(tile_of(kAhead < S ? kAhead : S - 1u));
         issue_tile();
