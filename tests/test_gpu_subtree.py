@@ -102,7 +102,7 @@ def test_subtree_matches_oracle(gpu, orc, case):
     _check_topk(orc, out, leaves, codes, scales, norms, gids)
 
 
-@pytest.mark.parametrize("fan", [1, 2, 4])
+@pytest.mark.parametrize("fan", [1, 2, 3, 4])
 def test_subtree_near_tied_distances_match_oracle(gpu, orc, fan):
     """Rows on a 3-level grid, many of them repeated, each scaled by 1 + a
     few ulps: a row's distances to the leaders fall into a handful of values
